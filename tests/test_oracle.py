@@ -1,0 +1,391 @@
+"""Pins the CPU oracle (oracle/ane_oracle.c) before it is trusted as the checker.
+
+Checks, per function: the reference's own known-answer tests
+(crates/gguf/src/dequant.rs:235-270, crates/engine/src/q8_gemv.rs:257-314),
+exhaustive fp16 conversion against numpy, float64 brute force, closed forms of
+the DeltaNet recurrence and of attention, and an independent float64 numpy
+statement of each step (tests/np_ref.py).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import np_ref
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+# ---------------------------------------------------------------- fp16 ------
+
+def test_f16_to_f32_exhaustive(oracle_lib):
+    bits = np.arange(65536, dtype=np.uint16)
+    ours = oracle_lib.f16_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne(oracle_lib):
+    rng = np.random.default_rng(1)
+    # every f16 value, every midpoint between neighbours, random bit patterns
+    f16 = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    f16 = f16[np.isfinite(f16)]
+    srt = np.sort(np.unique(f16))
+    mids = ((srt[1:].astype(np.float64) + srt[:-1]) / 2).astype(np.float32)
+    rnd = rng.integers(0, 2**32, 2_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    special = np.array([0.0, -0.0, 65504, 65519.99, 65520, 65536, 1e10, -1e10, np.inf, -np.inf,
+                        2**-24, 2**-25, 2**-25 * 1.0000001, 3 * 2**-26, 2**-14, 2**-14 * 0.99999],
+                       np.float32)
+    x = np.concatenate([f16, mids, rnd, special]).astype(np.float32)
+    x = x[~np.isnan(x)]
+    ours = oracle_lib.f32_to_f16(x)
+    ref = x.astype(np.float16).view(np.uint16)
+    bad = np.nonzero(ours != ref)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first x={x[bad[:5]]} ours={ours[bad[:5]]} ref={ref[bad[:5]]}"
+    assert oracle_lib.f32_to_f16(np.array([np.nan], np.float32))[0] & 0x7C00 == 0x7C00
+
+
+# ------------------------------------------------ reference KATs ------------
+
+def _load_golden():
+    with open(os.path.join(HERE, "golden", "reference_kats.json")) as f:
+        return json.load(f)
+
+
+def test_reference_kat_q4_0_dequant(oracle_lib):
+    """dequant.rs:235-252: scale 1.0, all bytes 0x88 -> every element 0."""
+    kat = _load_golden()["q4_0_dequant_0x88"]
+    blk = np.array(kat["block"], np.uint8)
+    out = np.empty(32, np.float32)
+    oracle_lib.lib().ao_dequant_q4_0_block(blk, out)
+    assert np.all(np.abs(out - np.array(kat["expected"], np.float32)) < 0.01)
+    assert np.all(out == 0.0)
+
+
+def test_reference_kat_q8_0_dequant(oracle_lib):
+    """dequant.rs:254-270: scale 0.5, all quants 2 -> every element 1.0."""
+    kat = _load_golden()["q8_0_dequant_2s"]
+    blk = np.array(kat["block"], np.uint8)
+    out = np.empty(32, np.float32)
+    oracle_lib.lib().ao_dequant_q8_0_block(blk, out)
+    assert np.all(out == np.array(kat["expected"], np.float32))
+
+
+def test_reference_kat_q8_gemv_identity(oracle_lib):
+    """q8_gemv.rs:257-281: m=4, n=32, row r has a single 1 at column r, x=0..31 -> y=r."""
+    kat = _load_golden()["q8_gemv_identity"]
+    w = np.array(kat["w"], np.uint8)
+    x = np.array(kat["x"], np.float32)
+    for threads in (1, 0):
+        y = oracle_lib.gemv(8, w, kat["m"], kat["n"], x, threads=threads)
+        assert np.all(np.abs(y - np.array(kat["expected"], np.float32)) < 0.01)
+
+
+def _patterned_w(m=256, n=1024):
+    """q8_gemv.rs:284-298: scale 0.5, quant i of row r = ((r+i)%256) as i8."""
+    bpr = n // 32
+    blk = np.zeros((m, bpr, 34), np.uint8)
+    half = np.array([0.5], np.float16).view(np.uint16)[0]
+    blk[:, :, 0] = half & 0xFF
+    blk[:, :, 1] = half >> 8
+    r = np.arange(m)[:, None, None]
+    i = np.arange(32)[None, None, :]
+    blk[:, :, 2:] = ((r + i) % 256).astype(np.uint8)
+    return blk.reshape(-1)
+
+
+def test_reference_kat_q8_gemv_parallel_matches_scalar(oracle_lib):
+    """q8_gemv.rs:283-314: parallel GEMV within 1e-3 of scalar; also vs float64 brute force."""
+    m, n = 256, 1024
+    w = _patterned_w(m, n)
+    x = (np.arange(n) % 100).astype(np.float32)
+    y_par = oracle_lib.gemv(8, w, m, n, x, threads=0)
+    y_sc = oracle_lib.gemv(8, w, m, n, x, threads=1)
+    assert np.all(np.abs(y_par - y_sc) < 1e-3)
+    assert np.array_equal(y_par, y_sc)  # rows are independent: identical bits
+    ref = np_ref.dequant(8, w, m, n) @ x.astype(np.float64)
+    # the reference patterned case is integer-valued and exact in float32
+    assert np.array_equal(y_sc.astype(np.float64), ref)
+
+
+# ------------------------------------------------ GEMV / quantisation -------
+
+@pytest.mark.parametrize("t", [2, 8])
+@pytest.mark.parametrize("m,n", [(1, 32), (7, 64), (33, 256), (64, 2048)])
+def test_gemv_vs_float64(oracle_lib, t, m, n):
+    w = oracle_lib.gen_quant(t, 11, m * 1000 + n, m, n, std=0.02)
+    x = oracle_lib.normal(12, n, n)
+    y = oracle_lib.gemv(t, w, m, n, x, threads=1)
+    ref = np_ref.dequant(t, w, m, n) @ x.astype(np.float64)
+    assert rel_l2(y, ref) < 2e-6
+
+
+def test_q4_nibble_order(oracle_lib):
+    """Byte 0x1F at position i: element i -> (15-8)*d = +7d, element i+16 -> (1-8)*d = -7d."""
+    blk = np.zeros(18, np.uint8)
+    one = np.array([0.25], np.float16).view(np.uint16)[0]
+    blk[0], blk[1] = one & 0xFF, one >> 8
+    blk[2:] = 0x88
+    blk[2 + 5] = 0x1F
+    out = np.empty(32, np.float32)
+    oracle_lib.lib().ao_dequant_q4_0_block(blk, out)
+    exp = np.zeros(32, np.float32)
+    exp[5], exp[21] = 7 * 0.25, -7 * 0.25
+    assert np.array_equal(out, exp)
+    # GEMV: x = one-hot at 5 and 21
+    x = np.zeros(32, np.float32)
+    x[5], x[21] = 1.0, 10.0
+    y = oracle_lib.gemv(2, blk, 1, 32, x, threads=1)
+    assert y[0] == np.float32(7 * 0.25 + 10 * -7 * 0.25)
+
+
+@pytest.mark.parametrize("t,qmax", [(8, 127.0), (2, 7.0)])
+def test_quantise_round_trip_bound(oracle_lib, t, qmax):
+    m, n = 16, 512
+    w = oracle_lib.normal(5, t, m * n, std=0.02).reshape(m, n)
+    w[0, :32] = 0.0  # all-zero block -> d = 0
+    q = oracle_lib.quantize(t, w)
+    deq = np_ref.dequant(t, q, m, n)
+    blocks = np.abs(w.reshape(m, n // 32, 32)).max(axis=2)
+    d32 = blocks / qmax
+    d16 = d32.astype(np.float16).astype(np.float64)
+    lim = (d32 / 2 + qmax * np.abs(d32 - d16) + 1e-12)[:, :, None]
+    err = np.abs(deq.reshape(m, n // 32, 32) - w.reshape(m, n // 32, 32))
+    assert np.all(err <= lim * (1 + 1e-6))
+    assert np.all(deq[0, :32] == 0.0)
+    # gen_quant is the same recipe applied to the same generator stream
+    g = oracle_lib.gen_quant(t, 5, t, m, n, std=0.02)
+    bb = oracle_lib.BLOCK_BYTES[t]
+    assert np.array_equal(g[bb:], q[bb:])  # block 0 of q was zeroed above
+
+
+def test_generator_is_thread_count_independent(oracle_lib):
+    a = oracle_lib.normal(3, 4, 300_001)
+    b = oracle_lib.normal(3, 4, 300_001)
+    assert np.array_equal(a, b)
+    # a sub-range equals the start of the full stream
+    c = oracle_lib.normal(3, 4, 1000)
+    assert np.array_equal(a[:1000], c)
+    assert abs(float(a.mean())) < 0.01 and abs(float(a.std()) - 1) < 0.01
+    u = oracle_lib.uniform(3, 5, 100_000)
+    assert u.min() > 0 and u.max() < 1 and abs(u.mean() - 0.5) < 0.01
+
+
+# ------------------------------------------------ elementwise ---------------
+
+def test_rmsnorm_unit_weight_has_unit_rms(oracle_lib):
+    x = oracle_lib.normal(9, 1, 2048, std=3.0)
+    out = oracle_lib.rmsnorm(x, np.ones(2048, np.float32), 1e-6)
+    assert abs(float(np.sqrt(np.mean(out.astype(np.float64) ** 2))) - 1.0) < 1e-5
+    w = oracle_lib.normal(9, 2, 2048, mean=1.0, std=0.1)
+    assert rel_l2(oracle_lib.rmsnorm(x, w, 1e-6), np_ref.rmsnorm(x, w, 1e-6)) < 1e-6
+
+
+# ------------------------------------------------ DeltaNet core -------------
+
+H, DK = 4, 32  # small heads for closed forms
+
+
+def _dn_inputs(oracle_lib, seed, H=H, DK=DK, K=4):
+    C = 3 * H * DK
+    return dict(
+        qkv=oracle_lib.normal(seed, 1, C),
+        beta_raw=oracle_lib.normal(seed, 2, H),
+        alpha_raw=oracle_lib.normal(seed, 3, H),
+        conv_w=oracle_lib.normal(seed, 4, C * K, std=0.5).reshape(C, K),
+        ssm_a=-oracle_lib.uniform(seed, 5, H),
+        dt_bias=oracle_lib.normal(seed, 6, H),
+        conv_state=oracle_lib.normal(seed, 7, C * K).reshape(C, K),
+        S=oracle_lib.normal(seed, 8, H * DK * DK, std=0.01).reshape(H, DK, DK),
+    )
+
+
+def test_deltanet_core_vs_float64(oracle_lib):
+    inp = _dn_inputs(oracle_lib, 21)
+    cs, S = inp["conv_state"].copy(), inp["S"].copy()
+    for step in range(8):
+        qkv = oracle_lib.normal(21, 100 + step, 3 * H * DK)
+        o_ref, cs_ref, S_ref = np_ref.deltanet_core(qkv, inp["beta_raw"], inp["alpha_raw"], inp["conv_w"],
+                                                    inp["ssm_a"], inp["dt_bias"], cs, S, H, DK)
+        o = oracle_lib.deltanet_core(qkv, inp["beta_raw"], inp["alpha_raw"], inp["conv_w"], inp["ssm_a"],
+                                     inp["dt_bias"], cs, S, H, DK)
+        assert rel_l2(o, o_ref) < 1e-5
+        assert rel_l2(S, S_ref) < 1e-5
+        assert np.array_equal(cs, cs_ref.astype(np.float32))  # shift/append is exact
+
+
+def test_deltanet_exact_recall(oracle_lib):
+    """decay = 1, beta = 1, |k| = 1  =>  after the update S^T k = v."""
+    inp = _dn_inputs(oracle_lib, 22)
+    conv_w = np.zeros_like(inp["conv_w"])
+    conv_w[:, 3] = 1.0  # conv identity: conv_out = silu(current input)
+    ssm_a = np.zeros(H, np.float32)  # decay = exp(0 * softplus) = 1
+    beta_raw = np.full(H, 40.0, np.float32)  # sigmoid(40) == 1.0f
+    cs, S = inp["conv_state"].copy(), inp["S"].copy()
+    qkv = inp["qkv"]
+    oracle_lib.deltanet_core(qkv, beta_raw, inp["alpha_raw"], conv_w, ssm_a, inp["dt_bias"], cs, S, H, DK)
+    co = np_ref.silu(qkv.astype(np.float64))
+    k = co[H * DK:2 * H * DK].reshape(H, DK)
+    k = k / np.linalg.norm(k, axis=1, keepdims=True)
+    v = co[2 * H * DK:].reshape(H, DK)
+    recalled = np.einsum("hij,hi->hj", S.astype(np.float64), k)
+    assert np.max(np.abs(recalled - v)) < 1e-5 * max(1.0, np.abs(v).max())
+    # conv identity: the window now ends with the input
+    assert np.array_equal(cs[:, 3], qkv)
+
+
+def test_deltanet_zero_decay(oracle_lib):
+    """decay = 0  =>  S = beta * k v^T and out = (k . q) * beta * v."""
+    inp = _dn_inputs(oracle_lib, 23)
+    ssm_a = np.full(H, -1e30, np.float32)
+    cs, S = inp["conv_state"].copy(), inp["S"].copy()
+    o = oracle_lib.deltanet_core(inp["qkv"], inp["beta_raw"], inp["alpha_raw"], inp["conv_w"], ssm_a,
+                                 inp["dt_bias"], cs, S, H, DK)
+    co = np_ref.silu((cs.astype(np.float64) * inp["conv_w"]).sum(1))
+    q = co[:H * DK].reshape(H, DK)
+    k = co[H * DK:2 * H * DK].reshape(H, DK)
+    v = co[2 * H * DK:].reshape(H, DK)
+    q = q / np.linalg.norm(q, axis=1, keepdims=True) / np.sqrt(DK)
+    k = k / np.linalg.norm(k, axis=1, keepdims=True)
+    beta = np_ref.sigmoid(inp["beta_raw"].astype(np.float64))
+    S_exp = beta[:, None, None] * k[:, :, None] * v[:, None, :]
+    assert rel_l2(S, S_exp) < 1e-5
+    o_exp = ((k * q).sum(1) * beta)[:, None] * v
+    assert rel_l2(o, o_exp.reshape(-1)) < 1e-5
+
+
+def test_gated_rmsnorm_vs_float64(oracle_lib):
+    heads = oracle_lib.normal(30, 1, 16 * 128)
+    gate = oracle_lib.normal(30, 2, 16 * 128)
+    w = oracle_lib.normal(30, 3, 128, mean=1.0, std=0.1)
+    out = oracle_lib.gated_rmsnorm(heads, gate, w, 16, 1e-6)
+    ref = np.concatenate([np_ref.rmsnorm(heads[h * 128:(h + 1) * 128], w, 1e-6) for h in range(16)])
+    ref = ref * np_ref.silu(gate.astype(np.float64))
+    assert rel_l2(out, ref) < 1e-6
+
+
+# ------------------------------------------------ attention core ------------
+
+NH, NKV, HD = 4, 2, 64
+
+
+def _attn_inputs(oracle_lib, seed):
+    return dict(
+        q_full=oracle_lib.normal(seed, 1, NH * 2 * HD),
+        k_in=oracle_lib.normal(seed, 2, NKV * HD),
+        v_in=oracle_lib.normal(seed, 3, NKV * HD),
+        q_norm=oracle_lib.normal(seed, 4, HD, mean=1.0, std=0.1),
+        k_norm=oracle_lib.normal(seed, 5, HD, mean=1.0, std=0.1),
+    )
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_attention_core_vs_float64(oracle_lib, kv_f16):
+    max_seq, pos = 40, 17
+    dt = np.uint16 if kv_f16 else np.float32
+    kc = np.zeros((NKV, max_seq, HD), dt)
+    vc = np.zeros((NKV, max_seq, HD), dt)
+    hist_k = oracle_lib.normal(31, 10, NKV * pos * HD).reshape(NKV, pos, HD)
+    hist_v = oracle_lib.normal(31, 11, NKV * pos * HD).reshape(NKV, pos, HD)
+    if kv_f16:
+        kc[:, :pos], vc[:, :pos] = oracle_lib.f32_to_f16(hist_k), oracle_lib.f32_to_f16(hist_v)
+        hk = oracle_lib.f16_to_f32(kc[:, :pos]).astype(np.float64)
+        hv = oracle_lib.f16_to_f32(vc[:, :pos]).astype(np.float64)
+        rnd = lambda a: a.astype(np.float16).astype(np.float64)
+    else:
+        kc[:, :pos], vc[:, :pos] = hist_k, hist_v
+        hk, hv = hist_k.astype(np.float64), hist_v.astype(np.float64)
+        rnd = None
+    inp = _attn_inputs(oracle_lib, 31)
+    out = oracle_lib.attention_core(inp["q_full"], inp["k_in"], inp["v_in"], inp["q_norm"], inp["k_norm"],
+                                    kc, vc, pos, NH, NKV, HD)
+    ref, k_new, v_new = np_ref.attention_core(inp["q_full"], inp["k_in"], inp["v_in"], inp["q_norm"],
+                                              inp["k_norm"], hk, hv, pos, NH, NKV, HD, kv_round=rnd)
+    assert rel_l2(out, ref) < 1e-5
+    got_k = oracle_lib.f16_to_f32(kc[:, pos]) if kv_f16 else kc[:, pos]
+    assert rel_l2(got_k, k_new) < (1e-3 if kv_f16 else 1e-5)
+    # untouched positions stay untouched
+    assert not np.any(kc[:, pos + 1:])
+
+
+def test_attention_single_position_returns_gated_v(oracle_lib):
+    """pos = 0: softmax over one key is 1, so out = v * sigmoid(gate); RoPE at 0 is the identity."""
+    inp = _attn_inputs(oracle_lib, 32)
+    kc = np.zeros((NKV, 4, HD), np.float32)
+    vc = np.zeros((NKV, 4, HD), np.float32)
+    out = oracle_lib.attention_core(inp["q_full"], inp["k_in"], inp["v_in"], inp["q_norm"], inp["k_norm"],
+                                    kc, vc, 0, NH, NKV, HD)
+    gate = inp["q_full"].reshape(NH, 2, HD)[:, 1, :].astype(np.float64)
+    v = inp["v_in"].reshape(NKV, HD).astype(np.float64)
+    exp = np.stack([v[h // (NH // NKV)] for h in range(NH)]) * np_ref.sigmoid(gate)
+    assert rel_l2(out, exp.reshape(-1)) < 1e-6
+    # RoPE(0) identity: cached k is exactly the RMS-normed k
+    k = inp["k_in"].reshape(NKV, HD)
+    for h in range(NKV):
+        assert np.array_equal(kc[h, 0], oracle_lib.rmsnorm(k[h], inp["k_norm"], 1e-6))
+
+
+def test_attention_equal_keys_average_values(oracle_lib):
+    """All cached keys equal to the new key => uniform softmax => out = mean(v) * sigmoid(gate)."""
+    inp = _attn_inputs(oracle_lib, 33)
+    pos = 9
+    kc = np.zeros((NKV, 16, HD), np.float32)
+    vc = np.zeros((NKV, 16, HD), np.float32)
+    # first call at pos 0 writes the roped, normed key; copy it to history
+    oracle_lib.attention_core(inp["q_full"], inp["k_in"], inp["v_in"], inp["q_norm"], inp["k_norm"],
+                              kc, vc, 0, NH, NKV, HD)
+    k0 = kc[:, 0].copy()
+    # keep rope at pos 0 by evaluating at pos 0 with a history placed after it is impossible, so
+    # instead compare against the float64 statement with identical keys at every position
+    hv = oracle_lib.normal(33, 20, NKV * pos * HD).reshape(NKV, pos, HD).astype(np.float32)
+    kc2 = np.zeros((NKV, 16, HD), np.float32)
+    vc2 = np.zeros((NKV, 16, HD), np.float32)
+    inp2 = dict(inp)
+    ref, k_new, _ = np_ref.attention_core(inp["q_full"], inp["k_in"], inp["v_in"], inp["q_norm"],
+                                          inp["k_norm"], np.zeros((NKV, 0, HD)), np.zeros((NKV, 0, HD)),
+                                          pos, NH, NKV, HD)
+    kc2[:, :pos] = k_new.astype(np.float32)[:, None, :]
+    vc2[:, :pos] = hv
+    out = oracle_lib.attention_core(inp2["q_full"], inp2["k_in"], inp2["v_in"], inp2["q_norm"],
+                                    inp2["k_norm"], kc2, vc2, pos, NH, NKV, HD)
+    gate = inp["q_full"].reshape(NH, 2, HD)[:, 1, :].astype(np.float64)
+    allv = np.concatenate([hv.astype(np.float64), vc2[:, pos:pos + 1].astype(np.float64)], axis=1)
+    exp = np.stack([allv[h // (NH // NKV)].mean(0) for h in range(NH)]) * np_ref.sigmoid(gate)
+    assert rel_l2(out, exp.reshape(-1)) < 1e-5
+    assert k0.shape == (NKV, HD)
+
+
+def test_rope_preserves_pair_norms(oracle_lib):
+    inp = _attn_inputs(oracle_lib, 34)
+    kc = np.zeros((NKV, 300, HD), np.float32)
+    vc = np.zeros((NKV, 300, HD), np.float32)
+    oracle_lib.attention_core(inp["q_full"], inp["k_in"], inp["v_in"], inp["q_norm"], inp["k_norm"],
+                              kc, vc, 257, NH, NKV, HD)
+    k = inp["k_in"].reshape(NKV, HD)
+    for h in range(NKV):
+        kn = oracle_lib.rmsnorm(k[h], inp["k_norm"], 1e-6).astype(np.float64).reshape(-1, 2)
+        kr = kc[h, 257].astype(np.float64).reshape(-1, 2)
+        assert np.allclose(np.hypot(kr[:, 0], kr[:, 1]), np.hypot(kn[:, 0], kn[:, 1]), rtol=1e-6)
+        assert not np.allclose(kr, kn)
+
+
+# ------------------------------------------------ argmax --------------------
+
+def test_argmax_total_cmp_last_of_ties(oracle_lib):
+    a = np.array([1.0, 3.0, -2.0, 3.0, 0.5], np.float32)
+    assert oracle_lib.argmax(a) == 3  # max_by keeps the last maximum
+    b = np.array([-0.0, 0.0, -0.0], np.float32)
+    assert oracle_lib.argmax(b) == 1  # total_cmp: -0.0 < +0.0
+    c = np.array([1.0, np.nan, 2.0], np.float32)
+    assert oracle_lib.argmax(c) == 1  # positive NaN is the total_cmp maximum
+    d = np.array([-np.inf, -np.inf], np.float32)
+    assert oracle_lib.argmax(d) == 1
