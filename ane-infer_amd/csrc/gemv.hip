@@ -1,0 +1,268 @@
+// gemv.hip — Q8_0 / Q4_0 dequant-GEMV and small-batch GEMM for gfx950.
+//
+// Replaces the q8_gemv / q4_gemv Metal kernels (crates/engine/metal/
+// q8_gemv.metal:15-87, q4_gemv.metal:25-98) and the CPU q8_gemv
+// (crates/engine/src/q8_gemv.rs:130-148).  Same result: y[r] = sum over
+// blocks b of scale(r,b) * sum_i q(r,b,i) * x[32b+i], fp32 accumulate.
+//
+// Work decomposition (wave64, bandwidth-bound):
+//   * a "super-block" is 8 consecutive quant blocks of one row = 256 columns;
+//     for Q8_0 that is 272 bytes (17 x 16 B), for Q4_0 144 bytes (9 x 16 B),
+//     so rows of n = 256k columns start 16-byte aligned and a super-block
+//     column of a 64-row tile is exactly 17 (or 9) KiB;
+//   * a wave loads that tile with coalesced 16-byte-per-lane loads (each load
+//     instruction covers contiguous row segments), stages it through LDS and
+//     reads back one row per lane.  The activation values a lane needs are
+//     then the same for all 64 lanes: they are wave-uniform (scalar) loads,
+//     and every lane accumulates its own row with no cross-lane reduction;
+//   * 4 waves of a workgroup take interleaved super-blocks of the same 64
+//     rows and are reduced through LDS.  When there are too few row tiles to
+//     fill the chip, K is split across workgroups, which write partial sums
+//     to a workspace; a second pass adds them in fixed order, so results are
+//     deterministic and no device-wide fence is needed.
+#include "common.h"
+
+namespace anehip {
+
+namespace {
+
+constexpr int kWave = 64;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <uint32_t T> struct QTraits;
+template <> struct QTraits<ANEHIP_GGML_Q8_0> {
+    static constexpr int kBlockBytes = 34;
+    static constexpr int kSbBytes = 272;  // 8 blocks
+    static constexpr int kSbVec = 17;     // 16-byte vectors per super-block
+};
+template <> struct QTraits<ANEHIP_GGML_Q4_0> {
+    static constexpr int kBlockBytes = 18;
+    static constexpr int kSbBytes = 144;
+    static constexpr int kSbVec = 9;
+};
+
+__device__ __forceinline__ uint32_t byte_at(const uint32_t *w, int off) {
+    return (w[off >> 2] >> ((off & 3) * 8)) & 0xffu;
+}
+
+__device__ __forceinline__ float half_at(const uint32_t *w, int off) {
+    // off is even, so the two bytes never straddle a 32-bit word
+    uint32_t bits = (w[off >> 2] >> ((off & 3) * 8)) & 0xffffu;
+    return __half2float(__ushort_as_half((unsigned short)bits));
+}
+
+// Dot product of one super-block (8 blocks) held in registers with x[0..255]
+// (wave-uniform), accumulated per block then scaled, as compute_row does
+// (q8_gemv.rs:234-242): sum += block_sum * scale.
+template <uint32_t T>
+__device__ __forceinline__ float sb_dot(const uint32_t *w, const float *__restrict__ x, float acc) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int base = k * QTraits<T>::kBlockBytes;
+        const float d = half_at(w, base);
+        float bs = 0.0f;
+        if constexpr (T == ANEHIP_GGML_Q8_0) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                int q = (int)(int8_t)byte_at(w, base + 2 + i);
+                bs = fmaf((float)q, x[k * 32 + i], bs);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                uint32_t b = byte_at(w, base + 2 + i);
+                float v0 = (float)((int)(b & 15u) - 8);
+                float v1 = (float)((int)(b >> 4) - 8);
+                bs = fmaf(v0, x[k * 32 + i], bs);
+                bs = fmaf(v1, x[k * 32 + 16 + i], bs);
+            }
+        }
+        acc = fmaf(bs, d, acc);
+        // keep each block's LDS reads, converts and FMAs together: bounds the
+        // live registers to one block (the other waves hide the LDS latency)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return acc;
+}
+
+// Coalesced load of one super-block column of a 64-row tile: the tile holds
+// 64 rows x kSbBytes, i.e. kSbVec * 64 chunks of 16 bytes.  Load j of lane l
+// fetches chunk c = 64 j + l = (row c / kSbVec, part c % kSbVec), so each
+// load instruction reads whole contiguous row segments.  `off` holds the
+// lane's byte offsets of its chunks relative to the tile's first row (32-bit,
+// loop-invariant; rows past m are clamped to the last row and never stored),
+// so every load is "uniform base + 32-bit lane offset".
+template <uint32_t T>
+__device__ __forceinline__ void tile_offsets(uint32_t *off, uint32_t row_bytes, int rows_left, int lane) {
+    constexpr int V = QTraits<T>::kSbVec;
+#pragma unroll
+    for (int j = 0; j < V; j++) {
+        const int c = j * kWave + lane;
+        const int r = min(c / V, rows_left - 1);
+        off[j] = (uint32_t)r * row_bytes + (uint32_t)(c % V) * 16u;
+    }
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void load_tile(u32x4 *regs, const uint8_t *tile_base, const uint32_t *off) {
+    constexpr int V = QTraits<T>::kSbVec;
+#pragma unroll
+    for (int j = 0; j < V; j++)
+        regs[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tile_base + off[j]));
+}
+
+// Stage the tile through this wave's LDS slice (chunk c at byte 16 c, i.e.
+// row-major [64][kSbBytes]); the lane then reads its own row from LDS.  LDS
+// operations of one wave complete in issue order, so only compiler ordering
+// is needed between the writes and the reads of the same wave.
+template <uint32_t T>
+__device__ __forceinline__ void stage_tile(const u32x4 *regs, u32x4 *lds, int lane) {
+    constexpr int V = QTraits<T>::kSbVec;
+#pragma unroll
+    for (int j = 0; j < V; j++) lds[j * kWave + lane] = regs[j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int kWavesPerWg = 4;
+
+// grid = (row tiles of 64, K splits); 4 waves per workgroup.  Workgroup
+// (tile, ks) covers super-blocks [ks * sb_per_split, ...) of its 64 rows; wave
+// w takes every 4th of them.  The 4 waves are reduced through LDS.  With one
+// K split the workgroup writes y; otherwise it writes its partial row sums to
+// part[ks][batch][m], which the consumer adds in ks order.
+template <uint32_t T, int B>
+__global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_tiled(const uint8_t *__restrict__ W,
+                                                                      const float *__restrict__ x,
+                                                                      float *__restrict__ out, int m, int n,
+                                                                      int batch, int sb_per_split) {
+    constexpr int V = QTraits<T>::kSbVec;
+    __shared__ u32x4 lds[kWavesPerWg][V * kWave];
+    __shared__ float red[kWavesPerWg][B][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
+    const int tile = blockIdx.x;
+    const int ks = blockIdx.y;
+    const int nsb = n >> 8;
+    const size_t row_bytes = (size_t)nsb * QTraits<T>::kSbBytes;
+    const int row0 = tile * kWave;
+    const int sb_begin = ks * sb_per_split;
+    const int sb_end = min(nsb, sb_begin + sb_per_split);
+
+    float acc[B];
+#pragma unroll
+    for (int b = 0; b < B; b++) acc[b] = 0.0f;
+
+    // regs hold the tile in flight; after it is staged into LDS they are
+    // reused for the next tile's loads, which overlap this tile's compute.
+    u32x4 regs[V];
+    uint32_t off[V];
+    const uint32_t *wl = reinterpret_cast<const uint32_t *>(&lds[wave][lane * V]);
+    tile_offsets<T>(off, (uint32_t)row_bytes, m - row0, lane);
+    const uint8_t *tile_base = W + (size_t)row0 * row_bytes;
+    int sb = sb_begin + wave;
+    if (sb < sb_end) load_tile<T>(regs, tile_base + (size_t)sb * QTraits<T>::kSbBytes, off);
+    for (; sb < sb_end; sb += kWavesPerWg) {
+        stage_tile<T>(regs, lds[wave], lane);
+        if (sb + kWavesPerWg < sb_end)
+            load_tile<T>(regs, tile_base + (size_t)(sb + kWavesPerWg) * QTraits<T>::kSbBytes, off);
+#pragma unroll
+        for (int b = 0; b < B; b++)
+            if (b < batch) acc[b] = sb_dot<T>(wl, x + (size_t)b * n + (size_t)sb * 256, acc[b]);
+        wave_sync_lds();  // this tile's reads precede the next tile's writes
+    }
+#pragma unroll
+    for (int b = 0; b < B; b++) red[wave][b][lane] = acc[b];
+    __syncthreads();
+    if (wave != 0) return;
+    const int row = row0 + lane;
+    if (row >= m) return;
+    float *dst = out + (size_t)ks * batch * m;
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+        if (b < batch) {
+            float s = red[0][b][lane];
+#pragma unroll
+            for (int v = 1; v < kWavesPerWg; v++) s += red[v][b][lane];
+            dst[(size_t)b * m + row] = s;
+        }
+    }
+}
+
+// y[i] = sum over k of part[k][i], k ascending (deterministic).
+__global__ __launch_bounds__(256) void sum_partials(const float *__restrict__ part, float *__restrict__ y,
+                                                   size_t count, int ksplit) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= count) return;
+    float s = part[i];
+    for (int k = 1; k < ksplit; k++) s += part[(size_t)k * count + i];
+    y[i] = s;
+}
+
+// K splits: the smallest divisor of the super-block count that gives at
+// least `target` waves, with at least one super-block per wave.
+int choose_ksplit(int tiles, int nsb, int target_waves) {
+    for (int k = 1; k <= nsb; k++) {
+        if (nsb % k) continue;
+        int per = nsb / k;
+        int waves = tiles * k * min(per, kWavesPerWg);
+        if (waves >= target_waves || per <= kWavesPerWg) return k;
+    }
+    return 1;
+}
+
+template <uint32_t T, int B>
+int launch_tiled(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
+                 uint32_t batch, float *y) {
+    const int tiles = (int)((m + kWave - 1) / kWave);
+    const int nsb = (int)(n / 256);
+    const int target = 3 * (ctx->cu_count > 0 ? ctx->cu_count : 256);
+    const int ksplit = choose_ksplit(tiles, nsb, target);
+    const int per = nsb / ksplit;
+    float *out = y;
+    const size_t count = (size_t)batch * m;
+    if (ksplit > 1) {
+        int rc = ensure_workspace(ctx, (size_t)ksplit * count, 0);
+        if (rc) return rc;
+        out = ctx->ws.partial;
+    }
+    hipLaunchKernelGGL((quant_gemm_tiled<T, B>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
+                       static_cast<const uint8_t *>(w), x, out, (int)m, (int)n, (int)batch, per);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    if (ksplit > 1) {
+        hipLaunchKernelGGL(sum_partials, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream,
+                           (const float *)out, y, count, ksplit);
+        ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    }
+    return ANEHIP_OK;
+}
+
+template <uint32_t T>
+int dispatch_batch(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n,
+                   const float *x, uint32_t batch, float *y) {
+    if (batch == 1) return launch_tiled<T, 1>(ctx, stream, w, m, n, x, batch, y);
+    // small batches: groups of up to 4 rows of x per pass over W (VALU path)
+    for (uint32_t b0 = 0; b0 < batch; b0 += 4) {
+        uint32_t nb = batch - b0 < 4 ? batch - b0 : 4;
+        int rc = launch_tiled<T, 4>(ctx, stream, w, m, n, x + (size_t)b0 * n, nb, y + (size_t)b0 * m);
+        if (rc) return rc;
+    }
+    return ANEHIP_OK;
+}
+
+}  // namespace
+
+int launch_quant_gemm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
+                      uint32_t n, const float *x, uint32_t batch, float *y) {
+    if (ggml_type == ANEHIP_GGML_Q8_0) return dispatch_batch<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, x, batch, y);
+    return dispatch_batch<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, x, batch, y);
+}
+
+}  // namespace anehip

@@ -1,0 +1,210 @@
+// runtime.hip — context, errors, device memory and timing of libanehip.
+//
+// Replaces GpuContext (crates/engine/src/metal_graph.rs:49-260): one device,
+// one stream (the reference's one MTLCommandQueue), and a workspace allocated
+// once.  Unlike the reference, failures are reported as status codes with a
+// message instead of being ignored (gpu_full_decode.rs:1030-1043).
+#include "common.h"
+
+#include <cstring>
+
+namespace anehip {
+
+ErrorSlot &global_error() {
+    static thread_local ErrorSlot slot;
+    return slot;
+}
+
+int set_error(ErrorSlot &slot, int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    slot.msg = buf;
+    return code;
+}
+
+int ensure_workspace(anehip_ctx *ctx, size_t floats, size_t counters) {
+    Workspace &ws = ctx->ws;
+    if (floats > ws.partial_floats) {
+        if (ws.partial) (void)hipFree(ws.partial);
+        ws.partial = nullptr;
+        ws.partial_floats = 0;
+        size_t want = floats < (1u << 20) ? (1u << 20) : floats;
+        if (hipMalloc(&ws.partial, want * sizeof(float)) != hipSuccess)
+            return set_error(ctx->err, ANEHIP_ENOMEM, "workspace: cannot allocate %zu partials", want);
+        ws.partial_floats = want;
+    }
+    if (counters > ws.n_counters) {
+        if (ws.counters) {
+            // outstanding kernels may still use the old counters
+            ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+            (void)hipFree(ws.counters);
+        }
+        ws.counters = nullptr;
+        ws.n_counters = 0;
+        size_t want = counters < 65536 ? 65536 : counters;
+        if (hipMalloc(&ws.counters, want * sizeof(uint32_t)) != hipSuccess)
+            return set_error(ctx->err, ANEHIP_ENOMEM, "workspace: cannot allocate %zu counters", want);
+        ANEHIP_HIP_TRY(ctx->err, hipMemset(ws.counters, 0, want * sizeof(uint32_t)));
+        ws.n_counters = want;
+    }
+    return ANEHIP_OK;
+}
+
+}  // namespace anehip
+
+using namespace anehip;
+
+extern "C" {
+
+int anehip_init(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return set_error(global_error(), ANEHIP_ENODEV, "no HIP device visible");
+    for (int d = 0; d < n; d++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, d) == hipSuccess && std::strncmp(p.gcnArchName, "gfx950", 6) == 0)
+            return ANEHIP_OK;
+    }
+    return set_error(global_error(), ANEHIP_ENODEV, "no gfx950 device among %d HIP devices", n);
+}
+
+const char *anehip_last_error(const anehip_ctx *ctx) {
+    return ctx ? ctx->err.msg.c_str() : global_error().msg.c_str();
+}
+
+int anehip_model_setup(anehip_ctx *ctx, const anehip_model_desc *desc);  // decode.hip
+void anehip_model_teardown(anehip_ctx *ctx);                             // decode.hip
+
+int anehip_ctx_create(int device, const anehip_model_desc *desc, anehip_ctx **out) {
+    if (!out) return set_error(global_error(), ANEHIP_EINVAL, "ctx_create: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
+        return set_error(global_error(), ANEHIP_ENODEV, "ctx_create: device %d not present (%d visible)", device, n);
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) != hipSuccess || std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return set_error(global_error(), ANEHIP_ENODEV, "ctx_create: device %d is %s, not gfx950", device,
+                         p.gcnArchName);
+    if (hipSetDevice(device) != hipSuccess)
+        return set_error(global_error(), ANEHIP_EHIP, "ctx_create: hipSetDevice(%d) failed", device);
+    anehip_ctx *ctx = new anehip_ctx();
+    ctx->device = device;
+    ctx->cu_count = p.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&ctx->ev_start) != hipSuccess || hipEventCreate(&ctx->ev_stop) != hipSuccess) {
+        anehip_ctx_destroy(ctx);
+        return set_error(global_error(), ANEHIP_EHIP, "ctx_create: stream/event creation failed");
+    }
+    int rc = ensure_workspace(ctx, 0, 0);
+    if (rc == ANEHIP_OK && desc) rc = anehip_model_setup(ctx, desc);
+    if (rc != ANEHIP_OK) {
+        set_error(global_error(), rc, "ctx_create: %s", ctx->err.msg.c_str());
+        anehip_ctx_destroy(ctx);
+        return rc;
+    }
+    *out = ctx;
+    return ANEHIP_OK;
+}
+
+void anehip_ctx_destroy(anehip_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    anehip_model_teardown(ctx);
+    for (void *p : ctx->user_allocs) (void)hipFree(p);
+    if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
+    if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
+    if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
+    if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+int anehip_sync(anehip_ctx *ctx) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "sync: ctx is NULL");
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    return ANEHIP_OK;
+}
+
+int anehip_dev_alloc(anehip_ctx *ctx, size_t nbytes, void **dptr) {
+    if (!ctx || !dptr || nbytes == 0) return set_error(ctx ? ctx->err : global_error(), ANEHIP_EINVAL, "dev_alloc: bad argument");
+    (void)hipSetDevice(ctx->device);
+    void *p = nullptr;
+    if (hipMalloc(&p, nbytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(ctx->err, ANEHIP_ENOMEM, "dev_alloc: hipMalloc(%zu) failed", nbytes);
+    }
+    ctx->user_allocs.push_back(p);
+    *dptr = p;
+    return ANEHIP_OK;
+}
+
+int anehip_dev_free(anehip_ctx *ctx, void *dptr) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "dev_free: ctx is NULL");
+    for (size_t i = 0; i < ctx->user_allocs.size(); i++) {
+        if (ctx->user_allocs[i] == dptr) {
+            ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+            ANEHIP_HIP_TRY(ctx->err, hipFree(dptr));
+            ctx->user_allocs.erase(ctx->user_allocs.begin() + i);
+            return ANEHIP_OK;
+        }
+    }
+    return set_error(ctx->err, ANEHIP_EINVAL, "dev_free: %p was not allocated by this context", dptr);
+}
+
+int anehip_h2d(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes) {
+    if (!ctx || (!dst && nbytes) || (!src && nbytes)) return set_error(ctx ? ctx->err : global_error(), ANEHIP_EINVAL, "h2d: bad argument");
+    if (!nbytes) return ANEHIP_OK;
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, ctx->stream));
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    return ANEHIP_OK;
+}
+
+int anehip_d2h(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes) {
+    if (!ctx || (!dst && nbytes) || (!src && nbytes)) return set_error(ctx ? ctx->err : global_error(), ANEHIP_EINVAL, "d2h: bad argument");
+    if (!nbytes) return ANEHIP_OK;
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, ctx->stream));
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    return ANEHIP_OK;
+}
+
+int anehip_dev_memset(anehip_ctx *ctx, void *dst, int value, size_t nbytes) {
+    if (!ctx || (!dst && nbytes)) return set_error(ctx ? ctx->err : global_error(), ANEHIP_EINVAL, "memset: bad argument");
+    if (!nbytes) return ANEHIP_OK;
+    ANEHIP_HIP_TRY(ctx->err, hipMemsetAsync(dst, value, nbytes, ctx->stream));
+    return ANEHIP_OK;
+}
+
+int anehip_timer_start(anehip_ctx *ctx) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "timer_start: ctx is NULL");
+    ANEHIP_HIP_TRY(ctx->err, hipEventRecord(ctx->ev_start, ctx->stream));
+    return ANEHIP_OK;
+}
+
+int anehip_timer_stop(anehip_ctx *ctx, float *ms) {
+    if (!ctx || !ms) return set_error(ctx ? ctx->err : global_error(), ANEHIP_EINVAL, "timer_stop: bad argument");
+    ANEHIP_HIP_TRY(ctx->err, hipEventRecord(ctx->ev_stop, ctx->stream));
+    ANEHIP_HIP_TRY(ctx->err, hipEventSynchronize(ctx->ev_stop));
+    ANEHIP_HIP_TRY(ctx->err, hipEventElapsedTime(ms, ctx->ev_start, ctx->ev_stop));
+    return ANEHIP_OK;
+}
+
+int anehip_quant_gemm(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,
+                      const float *x, uint32_t batch, float *y) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "quant_gemm: ctx is NULL");
+    if (!w || !x || !y) return set_error(ctx->err, ANEHIP_EINVAL, "quant_gemm: null pointer");
+    if (ggml_type != ANEHIP_GGML_Q8_0 && ggml_type != ANEHIP_GGML_Q4_0)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm: ggml type %u (only Q4_0=2, Q8_0=8)", ggml_type);
+    if (m == 0 || n == 0 || n % 32 != 0)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "quant_gemm: n=%u must be a positive multiple of 32 (m=%u)", n, m);
+    if (n % 256 != 0)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm: n=%u is not a multiple of 256", n);
+    if (batch == 0 || batch > 32)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm: batch=%u outside 1..32", batch);
+    return launch_quant_gemm(ctx, ctx->stream, ggml_type, w, m, n, x, batch, y);
+}
+
+}  // extern "C"
