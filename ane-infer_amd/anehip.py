@@ -60,6 +60,29 @@ def lib():
             "anehip_timer_start": (C.c_int, [vp]),
             "anehip_timer_stop": (C.c_int, [vp, C.POINTER(f32)]),
             "anehip_quant_gemm": (C.c_int, [vp, u32, vp, u32, u32, vp, u32, vp]),
+            "anehip_rmsnorm": (C.c_int, [vp, vp, vp, vp, u32, u32, f32]),
+            "anehip_silu_mul": (C.c_int, [vp, vp, vp, sz]),
+            "anehip_residual_add": (C.c_int, [vp, vp, vp, sz]),
+            "anehip_deltanet_step": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+            "anehip_gated_rmsnorm": (C.c_int, [vp, u32, u32, vp, vp, vp, f32, vp]),
+            "anehip_attention_step": (C.c_int, [vp, u32, u32, u32, u32, vp, vp, vp, f32, vp, vp, vp, vp]),
+            "anehip_argmax": (C.c_int, [vp, vp, u32, u32, vp]),
+            "anehip_fill_random": (C.c_int, [vp, vp, sz, u32, u32, C.c_uint64, f32, f32]),
+            "anehip_quantize": (C.c_int, [vp, u32, vp, u32, u32, vp]),
+            "anehip_upload_quant": (C.c_int, [vp, i32, u32, vp, sz, u32, u32, u32]),
+            "anehip_upload_f32": (C.c_int, [vp, i32, u32, vp, sz]),
+            "anehip_tensor_ptr": (C.c_int, [vp, i32, u32, u32, C.POINTER(vp), C.POINTER(sz)]),
+            "anehip_alloc_state": (C.c_int, [vp, u32, u32]),
+            "anehip_reset_state": (C.c_int, [vp]),
+            "anehip_set_pos": (C.c_int, [vp, u32, u32]),
+            "anehip_get_pos": (C.c_int, [vp, u32, C.POINTER(u32)]),
+            "anehip_state_ptr": (C.c_int, [vp, u32, u32, C.POINTER(vp), C.POINTER(sz)]),
+            "anehip_set_graph": (C.c_int, [vp, C.c_int]),
+            "anehip_decode_step": (C.c_int, [vp, vp, u32, vp]),
+            "anehip_decode_step_async": (C.c_int, [vp, vp, u32]),
+            "anehip_logits_ptr": (C.c_int, [vp, C.POINTER(vp)]),
+            "anehip_sampled_tokens": (C.c_int, [vp, vp]),
+            "anehip_generate": (C.c_int, [vp, vp, u32, u32, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -149,8 +172,203 @@ class Context:
         self._check(lib().anehip_timer_stop(self.h, C.byref(ms)))
         return ms.value
 
+    def call(self, name, *args):
+        """Calls anehip_<name>(ctx, *args); DevBuf arguments pass their device pointer."""
+        conv = [C.c_void_p(a.ptr) if isinstance(a, DevBuf) else a for a in args]
+        self._check(getattr(lib(), "anehip_" + name)(self.h, *conv))
+
     def quant_gemm(self, ggml_type: int, w: DevBuf | int, m: int, n: int, x: DevBuf | int, batch: int,
                    y: DevBuf | int):
         ptr = lambda b: b.ptr if isinstance(b, DevBuf) else b
         self._check(lib().anehip_quant_gemm(self.h, ggml_type, C.c_void_p(ptr(w)), m, n, C.c_void_p(ptr(x)),
                                             batch, C.c_void_p(ptr(y))))
+
+
+def _p(b):
+    if b is None:
+        return None
+    return C.c_void_p(b.ptr if isinstance(b, DevBuf) else int(b))
+
+
+# tensor kinds (include/anehip.h)
+T = dict(ATTN_NORM=0, POST_ATTN_NORM=1, FFN_GATE=2, FFN_UP=3, FFN_DOWN=4, QKV=5, ATTN_GATE=6, SSM_A=7,
+         SSM_ALPHA=8, SSM_BETA=9, SSM_CONV1D=10, SSM_DT_BIAS=11, SSM_NORM=12, SSM_OUT=13, WQ=14, WK=15, WV=16,
+         WO=17, Q_NORM=18, K_NORM=19, EMBEDDING=20, FINAL_NORM=21, LM_HEAD=22)
+LAYER_DELTANET, LAYER_ATTENTION = 0, 1
+
+
+class Spec:
+    """Model shape (the fields of anehip_model_desc)."""
+
+    def __init__(self, dim=2048, hidden_dim=6144, n_layers=24, n_heads=8, n_kv_heads=2, head_dim=256,
+                 vocab_size=151936, ssm_state_size=128, ssm_conv_kernel=4, ssm_group_count=16,
+                 rope_freq_base=10000.0, rms_norm_eps=1e-6, layer_types=None, attn_interval=4):
+        self.dim, self.hidden_dim, self.n_layers = dim, hidden_dim, n_layers
+        self.n_heads, self.n_kv_heads, self.head_dim, self.vocab_size = n_heads, n_kv_heads, head_dim, vocab_size
+        self.ssm_state_size, self.ssm_conv_kernel, self.ssm_group_count = ssm_state_size, ssm_conv_kernel, ssm_group_count
+        self.rope_freq_base, self.rms_norm_eps = rope_freq_base, rms_norm_eps
+        if layer_types is None:  # full attention every `attn_interval`-th layer (l % 4 == 3)
+            layer_types = [LAYER_ATTENTION if l % attn_interval == attn_interval - 1 else LAYER_DELTANET
+                           for l in range(n_layers)]
+        self.layer_types = np.array(layer_types, np.uint8)
+
+    def desc(self) -> ModelDesc:
+        d = ModelDesc(self.dim, self.hidden_dim, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim,
+                      self.vocab_size, self.ssm_state_size, self.ssm_conv_kernel, self.ssm_group_count,
+                      self.rope_freq_base, self.rms_norm_eps,
+                      self.layer_types.ctypes.data_as(C.POINTER(C.c_uint8)))
+        d._keep = self.layer_types
+        return d
+
+    def shapes(self, layer: int):
+        """{kind: (rows, cols, is_quant)} of a layer (-1: model-level tensors)."""
+        d, F, H = self.dim, self.hidden_dim, self.ssm_group_count
+        qd, kvd = self.n_heads * self.head_dim, self.n_kv_heads * self.head_dim
+        if layer < 0:
+            return {T["EMBEDDING"]: (self.vocab_size, d, False), T["FINAL_NORM"]: (1, d, False),
+                    T["LM_HEAD"]: (self.vocab_size, d, True)}
+        out = {T["ATTN_NORM"]: (1, d, False), T["POST_ATTN_NORM"]: (1, d, False), T["FFN_GATE"]: (F, d, True),
+               T["FFN_UP"]: (F, d, True), T["FFN_DOWN"]: (d, F, True)}
+        if self.layer_types[layer] == LAYER_DELTANET:
+            out.update({T["QKV"]: (3 * d, d, True), T["ATTN_GATE"]: (d, d, True), T["SSM_A"]: (1, H, False),
+                        T["SSM_ALPHA"]: (H, d, True), T["SSM_BETA"]: (H, d, True),
+                        T["SSM_CONV1D"]: (3 * d, self.ssm_conv_kernel, False), T["SSM_DT_BIAS"]: (1, H, False),
+                        T["SSM_NORM"]: (1, self.ssm_state_size, False), T["SSM_OUT"]: (d, d, True)})
+        else:
+            out.update({T["WQ"]: (2 * qd, d, True), T["WK"]: (kvd, d, True), T["WV"]: (kvd, d, True),
+                        T["WO"]: (d, qd, True), T["Q_NORM"]: (1, self.head_dim, False),
+                        T["K_NORM"]: (1, self.head_dim, False)})
+        return out
+
+
+# Synthetic random-init recipe: (distribution, a, b) per fp32 kind; quantised
+# kinds are N(0, 0.02) weights quantised to the chosen type.
+F32_RECIPE = {
+    T["ATTN_NORM"]: (0, 1.0, 0.1), T["POST_ATTN_NORM"]: (0, 1.0, 0.1), T["FINAL_NORM"]: (0, 1.0, 0.1),
+    T["SSM_NORM"]: (0, 1.0, 0.1), T["Q_NORM"]: (0, 1.0, 0.1), T["K_NORM"]: (0, 1.0, 0.1),
+    T["SSM_A"]: (1, -1.0, 0.0),            # ssm_a = -a, a ~ U(0, 1)
+    T["SSM_DT_BIAS"]: (0, 0.0, 1.0), T["SSM_CONV1D"]: (0, 0.0, 0.3), T["EMBEDDING"]: (0, 0.0, 0.02),
+}
+WEIGHT_STD = 0.02
+
+
+def tensor_seed(seed: int, layer: int, kind: int) -> int:
+    return (seed * 1_000_003 + (layer + 1) * 64 + kind) & 0xFFFFFFFFFFFFFFFF
+
+
+class Model(Context):
+    """A context with a model description: weights, state, decode step."""
+
+    def __init__(self, spec: Spec, device: int = 0):
+        self.spec = spec
+        self._desc = spec.desc()
+        super().__init__(device, self._desc)
+
+    # -- weights --
+    def upload_quant(self, layer, kind, blocks: np.ndarray, m, n, ggml_type=Q8_0):
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        self._check(lib().anehip_upload_quant(self.h, layer, kind, blocks.ctypes.data, blocks.nbytes, m, n,
+                                              ggml_type))
+
+    def upload_f32(self, layer, kind, data: np.ndarray):
+        data = np.ascontiguousarray(data, np.float32)
+        self._check(lib().anehip_upload_f32(self.h, layer, kind, data.ctypes.data, data.size))
+
+    def tensor_ptr(self, layer, kind, ggml_type=Q8_0):
+        p, n = C.c_void_p(), C.c_size_t()
+        self._check(lib().anehip_tensor_ptr(self.h, layer, kind, ggml_type, C.byref(p), C.byref(n)))
+        return p.value, n.value
+
+    def fill_random(self, dptr, n, dist, seed, a, b, f16=False):
+        self._check(lib().anehip_fill_random(self.h, C.c_void_p(dptr), n, dist, 1 if f16 else 0, seed, a, b))
+
+    def randomize(self, seed: int = 0, ggml_type: int = Q8_0):
+        """Random-init every tensor on the device (seeded; see F32_RECIPE)."""
+        tmp = None
+        for layer in [-1] + list(range(self.spec.n_layers)):
+            for kind, (rows, cols, quant) in self.spec.shapes(layer).items():
+                s = tensor_seed(seed, layer, kind)
+                if quant:
+                    if tmp is None or tmp.nbytes < rows * cols * 4:
+                        if tmp is not None:
+                            tmp.free()
+                        tmp = self.alloc(rows * cols * 4)
+                    self.fill_random(tmp.ptr, rows * cols, 0, s, 0.0, WEIGHT_STD)
+                    dptr, _ = self.tensor_ptr(layer, kind, ggml_type)
+                    self._check(lib().anehip_quantize(self.h, ggml_type, C.c_void_p(tmp.ptr), rows, cols,
+                                                      C.c_void_p(dptr)))
+                else:
+                    dptr, _ = self.tensor_ptr(layer, kind)
+                    dist, a, b = F32_RECIPE[kind]
+                    self.fill_random(dptr, rows * cols, dist, s, a, b)
+        self.sync()
+        if tmp is not None:
+            tmp.free()
+
+    def download_tensor(self, layer, kind, ggml_type=Q8_0) -> np.ndarray:
+        rows, cols, quant = self.spec.shapes(layer)[kind]
+        dptr, nbytes = self.tensor_ptr(layer, kind, ggml_type)
+        out = np.empty(nbytes, np.uint8)
+        self._check(lib().anehip_d2h(self.h, out.ctypes.data, C.c_void_p(dptr), nbytes))
+        return out if quant else out.view(np.float32)
+
+    # -- state --
+    def alloc_state(self, batch: int, max_seq: int):
+        self._check(lib().anehip_alloc_state(self.h, batch, max_seq))
+        self.batch, self.max_seq = batch, max_seq
+
+    def reset_state(self):
+        self._check(lib().anehip_reset_state(self.h))
+
+    def set_pos(self, seq, pos):
+        self._check(lib().anehip_set_pos(self.h, seq, pos))
+
+    def get_pos(self, seq) -> int:
+        v = C.c_uint32()
+        self._check(lib().anehip_get_pos(self.h, seq, C.byref(v)))
+        return v.value
+
+    def state_ptr(self, layer, which):
+        p, n = C.c_void_p(), C.c_size_t()
+        self._check(lib().anehip_state_ptr(self.h, layer, which, C.byref(p), C.byref(n)))
+        return p.value, n.value
+
+    def get_state(self, layer, which) -> np.ndarray:
+        p, n = self.state_ptr(layer, which)
+        out = np.empty(n, np.uint8)
+        self._check(lib().anehip_d2h(self.h, out.ctypes.data, C.c_void_p(p), n))
+        return out.view(np.uint16 if which >= 2 else np.float32)
+
+    def set_state(self, layer, which, data: np.ndarray):
+        p, n = self.state_ptr(layer, which)
+        data = np.ascontiguousarray(data)
+        assert data.nbytes == n, (data.nbytes, n)
+        self._check(lib().anehip_h2d(self.h, C.c_void_p(p), data.ctypes.data, n))
+
+    def set_graph(self, enabled: bool):
+        self._check(lib().anehip_set_graph(self.h, 1 if enabled else 0))
+
+    # -- step --
+    def step(self, tokens, want_logits=True):
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        if want_logits:
+            out = np.empty((tok.size, self.spec.vocab_size), np.float32)
+            self._check(lib().anehip_decode_step(self.h, tok.ctypes.data, tok.size, out.ctypes.data))
+            return out
+        self._check(lib().anehip_decode_step(self.h, tok.ctypes.data, tok.size, None))
+        return None
+
+    def step_async(self, tokens):
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        self._check(lib().anehip_decode_step_async(self.h, tok.ctypes.data, tok.size))
+
+    def sampled(self) -> np.ndarray:
+        out = np.empty(self.batch, np.uint32)
+        self._check(lib().anehip_sampled_tokens(self.h, out.ctypes.data))
+        return out
+
+    def generate(self, first_tokens, steps: int) -> np.ndarray:
+        tok = np.ascontiguousarray(first_tokens, np.uint32)
+        out = np.empty((steps, tok.size), np.uint32)
+        self._check(lib().anehip_generate(self.h, tok.ctypes.data, tok.size, steps, out.ctypes.data))
+        return out

@@ -1,11 +1,804 @@
-// decode.hip — model weights, per-sequence state and the captured decode step.
+// decode.hip — model weights, per-sequence state and the decode step.
+//
+// Replaces upload_model_weights (crates/engine/src/gpu_decode.rs:152-283),
+// GpuLayerScratch / GpuConstantPool (gpu_full_decode.rs:18-217) and
+// encode_full_token_gpu (gpu_full_decode.rs:221-1044), whose CPU counterpart
+// is qwen35_forward_token (crates/cli/src/main.rs:953-1023).
+//
+// Differences from the reference design, all deliberate:
+//   * one hipGraph per step (captured once per state allocation) replaces the
+//     per-token command buffer with its ~506 encodes and ~150 buffer
+//     allocations; every per-step scalar (token ids, positions) is read from
+//     device memory, and a tail kernel advances the positions, so the graph
+//     is replayed unchanged;
+//   * projections that read the same input are stored stacked in one matrix
+//     ([qkv; attn_gate; ssm_beta; ssm_alpha], [wq; wk; wv], [ffn_gate;
+//     ffn_up]) so each is one streaming pass over its weights;
+//   * residual adds, the next layer's RMSNorm and SiLU-mul are fused into the
+//     kernel that also reduces the K-split GEMV partials;
+//   * state is per sequence ([batch] leading dim), so batch 1..32 decodes
+//     independent sequences (the reference is batch-1 only);
+//   * the KV cache is fp16 (RNE), [kv_head][max_seq][head_dim] per sequence;
+//   * positions are range-checked (the reference writes past the KV buffer
+//     when pos >= max_seq, gpu_full_decode.rs:805).
 #include "common.h"
+
+#include <cmath>
+#include <cstring>
 
 using namespace anehip;
 
-extern "C" int anehip_model_setup(anehip_ctx *ctx, const anehip_model_desc *desc) {
-    (void)desc;
-    return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "model decode step not built yet");
+namespace {
+
+constexpr uint32_t kDk = 128;
+constexpr uint32_t kConvK = 4;
+constexpr uint32_t kHd = 256;
+
+struct QMat {
+    void *d = nullptr;
+    uint32_t type = 0, rows = 0, cols = 0;
+};
+
+struct Layer {
+    uint32_t type = 0;
+    QMat mix_in, mix_out, ffn_gu, ffn_down;
+    float *attn_norm = nullptr, *post_attn_norm = nullptr;
+    float *ssm_a = nullptr, *conv1d = nullptr, *dt_bias = nullptr, *ssm_norm = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;
+    uint64_t have = 0;  // bit per uploaded kind
+    // state
+    float *conv_state = nullptr, *S = nullptr;
+    __half *kc = nullptr, *vc = nullptr;
+};
+
+}  // namespace
+
+struct Model {
+    anehip_model_desc desc{};
+    std::vector<uint8_t> types;
+    std::vector<Layer> layers;
+    float *embedding = nullptr, *final_norm = nullptr;
+    QMat lm_head;
+    uint64_t glob_have = 0;
+    float *inv_freq = nullptr;
+    uint32_t rows_dn = 0, rows_attn = 0;  // stacked mix_in rows
+    // state
+    uint32_t batch = 0, max_seq = 0;
+    std::vector<uint32_t> host_pos;
+    uint32_t *d_pos = nullptr, *d_tokens = nullptr, *d_sampled = nullptr;
+    uint32_t *h_tokens = nullptr;  // pinned staging
+    // scratch
+    float *x = nullptr, *xn = nullptr, *mixbuf = nullptr, *heads = nullptr, *normed = nullptr;
+    float *attn_out = nullptr, *h = nullptr, *part = nullptr, *logits = nullptr, *attn_part = nullptr;
+    void *argmax_ws = nullptr;
+    // graph
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool use_graph = true;
+};
+
+namespace {
+
+size_t qrow_bytes(uint32_t type, uint32_t cols) {
+    return (size_t)(cols / 32) * (type == ANEHIP_GGML_Q8_0 ? 34 : 18);
 }
 
-extern "C" void anehip_model_teardown(anehip_ctx *ctx) { (void)ctx; }
+void free_ptr(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+void drop_graph(Model *M) {
+    if (M->exec) (void)hipGraphExecDestroy(M->exec);
+    if (M->graph) (void)hipGraphDestroy(M->graph);
+    M->exec = nullptr;
+    M->graph = nullptr;
+}
+
+void free_state(Model *M) {
+    drop_graph(M);
+    for (Layer &L : M->layers) {
+        free_ptr(L.conv_state);
+        free_ptr(L.S);
+        free_ptr(L.kc);
+        free_ptr(L.vc);
+        L.conv_state = L.S = nullptr;
+        L.kc = L.vc = nullptr;
+    }
+    void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->x, M->xn, M->mixbuf, M->heads, M->normed,
+                    M->attn_out, M->h, M->part, M->logits, M->attn_part, M->argmax_ws};
+    for (void *p : bufs) free_ptr(p);
+    if (M->h_tokens) (void)hipHostFree(M->h_tokens);
+    M->d_pos = M->d_tokens = M->d_sampled = M->h_tokens = nullptr;
+    M->x = M->xn = M->mixbuf = M->heads = M->normed = M->attn_out = M->h = M->part = M->logits = nullptr;
+    M->attn_part = nullptr;
+    M->argmax_ws = nullptr;
+    M->batch = M->max_seq = 0;
+    M->host_pos.clear();
+}
+
+// Expected shape of a kind: {rows, cols, is_quant}; rows == 0 means the kind
+// does not belong to this layer type.
+struct KindShape {
+    uint32_t rows, cols;
+    bool quant;
+};
+
+KindShape kind_shape(const Model *M, int layer, uint32_t kind) {
+    const anehip_model_desc &D = M->desc;
+    const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
+    const uint32_t qd = D.n_heads * D.head_dim, kvd = D.n_kv_heads * D.head_dim;
+    if (layer < 0) {
+        switch (kind) {
+            case ANEHIP_T_EMBEDDING: return {D.vocab_size, d, false};
+            case ANEHIP_T_FINAL_NORM: return {1, d, false};
+            case ANEHIP_T_LM_HEAD: return {D.vocab_size, d, true};
+            default: return {0, 0, false};
+        }
+    }
+    const bool dn = M->types[layer] == ANEHIP_LAYER_DELTANET;
+    switch (kind) {
+        case ANEHIP_T_ATTN_NORM:
+        case ANEHIP_T_POST_ATTN_NORM: return {1, d, false};
+        case ANEHIP_T_FFN_GATE:
+        case ANEHIP_T_FFN_UP: return {F, d, true};
+        case ANEHIP_T_FFN_DOWN: return {d, F, true};
+        default: break;
+    }
+    if (dn) {
+        switch (kind) {
+            case ANEHIP_T_QKV: return {C, d, true};
+            case ANEHIP_T_ATTN_GATE: return {d, d, true};
+            case ANEHIP_T_SSM_A:
+            case ANEHIP_T_SSM_DT_BIAS: return {1, H, false};
+            case ANEHIP_T_SSM_ALPHA:
+            case ANEHIP_T_SSM_BETA: return {H, d, true};
+            case ANEHIP_T_SSM_CONV1D: return {C, D.ssm_conv_kernel, false};
+            case ANEHIP_T_SSM_NORM: return {1, D.ssm_state_size, false};
+            case ANEHIP_T_SSM_OUT: return {d, d, true};
+            default: return {0, 0, false};
+        }
+    }
+    switch (kind) {
+        case ANEHIP_T_WQ: return {2 * qd, d, true};
+        case ANEHIP_T_WK:
+        case ANEHIP_T_WV: return {kvd, d, true};
+        case ANEHIP_T_WO: return {d, qd, true};
+        case ANEHIP_T_Q_NORM:
+        case ANEHIP_T_K_NORM: return {1, D.head_dim, false};
+        default: return {0, 0, false};
+    }
+}
+
+uint64_t required_mask(const Model *M, int layer) {
+    uint64_t m = 0;
+    for (uint32_t k = 0; k < ANEHIP_T_COUNT; k++)
+        if (kind_shape(M, layer, k).rows) m |= 1ull << k;
+    return m;
+}
+
+const char *kind_name(uint32_t k) {
+    static const char *names[] = {"attn_norm", "post_attn_norm", "ffn_gate", "ffn_up", "ffn_down", "qkv",
+                                  "attn_gate", "ssm_a", "ssm_alpha", "ssm_beta", "ssm_conv1d", "ssm_dt_bias",
+                                  "ssm_norm", "ssm_out", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
+                                  "embedding", "final_norm", "lm_head"};
+    return k < ANEHIP_T_COUNT ? names[k] : "?";
+}
+
+// Where a quant kind lives: target matrix, its total rows, row offset.
+struct QSlot {
+    QMat *mat;
+    uint32_t total_rows, row_off;
+};
+
+QSlot quant_slot(Model *M, int layer, uint32_t kind) {
+    const anehip_model_desc &D = M->desc;
+    if (layer < 0) return {&M->lm_head, D.vocab_size, 0};
+    Layer &L = M->layers[layer];
+    const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
+    const uint32_t qd2 = 2 * D.n_heads * D.head_dim, kvd = D.n_kv_heads * D.head_dim;
+    switch (kind) {
+        case ANEHIP_T_FFN_GATE: return {&L.ffn_gu, 2 * F, 0};
+        case ANEHIP_T_FFN_UP: return {&L.ffn_gu, 2 * F, F};
+        case ANEHIP_T_FFN_DOWN: return {&L.ffn_down, d, 0};
+        case ANEHIP_T_QKV: return {&L.mix_in, M->rows_dn, 0};
+        case ANEHIP_T_ATTN_GATE: return {&L.mix_in, M->rows_dn, C};
+        case ANEHIP_T_SSM_BETA: return {&L.mix_in, M->rows_dn, C + d};
+        case ANEHIP_T_SSM_ALPHA: return {&L.mix_in, M->rows_dn, C + d + H};
+        case ANEHIP_T_SSM_OUT: return {&L.mix_out, d, 0};
+        case ANEHIP_T_WQ: return {&L.mix_in, M->rows_attn, 0};
+        case ANEHIP_T_WK: return {&L.mix_in, M->rows_attn, qd2};
+        case ANEHIP_T_WV: return {&L.mix_in, M->rows_attn, qd2 + kvd};
+        case ANEHIP_T_WO: return {&L.mix_out, d, 0};
+        default: return {nullptr, 0, 0};
+    }
+}
+
+float **f32_slot(Model *M, int layer, uint32_t kind) {
+    if (layer < 0) {
+        if (kind == ANEHIP_T_EMBEDDING) return &M->embedding;
+        if (kind == ANEHIP_T_FINAL_NORM) return &M->final_norm;
+        return nullptr;
+    }
+    Layer &L = M->layers[layer];
+    switch (kind) {
+        case ANEHIP_T_ATTN_NORM: return &L.attn_norm;
+        case ANEHIP_T_POST_ATTN_NORM: return &L.post_attn_norm;
+        case ANEHIP_T_SSM_A: return &L.ssm_a;
+        case ANEHIP_T_SSM_CONV1D: return &L.conv1d;
+        case ANEHIP_T_SSM_DT_BIAS: return &L.dt_bias;
+        case ANEHIP_T_SSM_NORM: return &L.ssm_norm;
+        case ANEHIP_T_Q_NORM: return &L.q_norm;
+        case ANEHIP_T_K_NORM: return &L.k_norm;
+        default: return nullptr;
+    }
+}
+
+__global__ void pos_advance_kernel(uint32_t *pos, int n) {
+    int i = threadIdx.x;
+    if (i < n) pos[i] += 1u;
+}
+
+int check_model(anehip_ctx *ctx, Model *M) {
+    for (uint32_t l = 0; l < M->desc.n_layers; l++) {
+        uint64_t miss = required_mask(M, (int)l) & ~M->layers[l].have;
+        if (miss) {
+            uint32_t k = (uint32_t)__builtin_ctzll(miss);
+            return set_error(ctx->err, ANEHIP_ESTATE, "layer %u: tensor %s not uploaded", l, kind_name(k));
+        }
+    }
+    uint64_t miss = required_mask(M, -1) & ~M->glob_have;
+    if (miss)
+        return set_error(ctx->err, ANEHIP_ESTATE, "model tensor %s not uploaded",
+                         kind_name((uint32_t)__builtin_ctzll(miss)));
+    if (!M->batch) return set_error(ctx->err, ANEHIP_ESTATE, "no state: call anehip_alloc_state first");
+    return ANEHIP_OK;
+}
+
+#define TRY(expr)                   \
+    do {                            \
+        int _rc = (expr);           \
+        if (_rc) return _rc;        \
+    } while (0)
+
+// Enqueues one decode step for all sequences on `s` (captured or eager).
+int enqueue_step(anehip_ctx *ctx, Model *M, hipStream_t s) {
+    const anehip_model_desc &D = M->desc;
+    const int B = (int)M->batch;
+    const int d = (int)D.dim, F = (int)D.hidden_dim, H = (int)D.ssm_group_count, C = 3 * d;
+    const float eps = D.rms_norm_eps;
+    const uint32_t nl = D.n_layers;
+    TRY(launch_embed_rmsnorm(ctx, s, B, d, M->d_tokens, M->embedding, D.vocab_size, M->x,
+                             M->layers[0].attn_norm, M->xn, eps));
+    for (uint32_t l = 0; l < nl; l++) {
+        Layer &L = M->layers[l];
+        const bool dn = L.type == ANEHIP_LAYER_DELTANET;
+        const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
+        // mixer input projections (stacked), final values in mixbuf [B][rows_in]
+        int ks = gemm_ksplit(ctx, rows_in, d);
+        if (ks == 1) {
+            TRY(launch_gemm_raw(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, M->xn, B, M->mixbuf, 1));
+        } else {
+            TRY(launch_gemm_raw(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, M->xn, B, M->part, ks));
+            TRY(launch_sum_partials(ctx, s, M->part, M->mixbuf, (size_t)B * rows_in, ks));
+        }
+        const float *mix_x;
+        uint32_t mix_cols;
+        if (dn) {
+            const float *qkv = M->mixbuf;
+            TRY(launch_deltanet_step(ctx, s, B, H, qkv, (int)rows_in, qkv + C + d, qkv + C + d + H, (int)rows_in,
+                                     L.conv1d, L.ssm_a, L.dt_bias, L.conv_state, L.S, M->heads));
+            TRY(launch_dn_finish(ctx, s, B, H, qkv, (int)rows_in, L.conv_state, M->heads, qkv + C, (int)rows_in,
+                                 L.ssm_norm, M->normed, eps));
+            mix_x = M->normed;
+            mix_cols = (uint32_t)d;
+        } else {
+            TRY(launch_attention(ctx, s, B, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, M->mixbuf,
+                                 (int)rows_in, L.q_norm, L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part,
+                                 M->attn_out));
+            mix_x = M->attn_out;
+            mix_cols = D.n_heads * D.head_dim;
+        }
+        // mixer output projection + residual + post-attention RMSNorm
+        ks = gemm_ksplit(ctx, (uint32_t)d, mix_cols);
+        TRY(launch_gemm_raw(ctx, s, L.mix_out.type, L.mix_out.d, (uint32_t)d, mix_cols, mix_x, B, M->part, ks));
+        TRY(launch_residual_rmsnorm(ctx, s, B, d, M->x, M->part, ks, L.post_attn_norm, M->xn, eps));
+        // FFN: stacked gate/up + SiLU-mul, down + residual + next RMSNorm
+        ks = gemm_ksplit(ctx, 2 * (uint32_t)F, d);
+        TRY(launch_gemm_raw(ctx, s, L.ffn_gu.type, L.ffn_gu.d, 2 * (uint32_t)F, d, M->xn, B, M->part, ks));
+        TRY(launch_silu_mul_stacked(ctx, s, B, F, M->part, ks, M->h));
+        ks = gemm_ksplit(ctx, (uint32_t)d, F);
+        TRY(launch_gemm_raw(ctx, s, L.ffn_down.type, L.ffn_down.d, (uint32_t)d, F, M->h, B, M->part, ks));
+        const float *next_norm = l + 1 < nl ? M->layers[l + 1].attn_norm : M->final_norm;
+        TRY(launch_residual_rmsnorm(ctx, s, B, d, M->x, M->part, ks, next_norm, M->xn, eps));
+    }
+    // lm_head + greedy sample + position advance
+    int ks = gemm_ksplit(ctx, D.vocab_size, d);
+    if (ks == 1) {
+        TRY(launch_gemm_raw(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, M->xn, B, M->logits, 1));
+    } else {
+        TRY(launch_gemm_raw(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, M->xn, B, M->part, ks));
+        TRY(launch_sum_partials(ctx, s, M->part, M->logits, (size_t)B * D.vocab_size, ks));
+    }
+    TRY(launch_argmax(ctx, s, B, D.vocab_size, M->logits, M->argmax_ws, M->d_sampled));
+    hipLaunchKernelGGL(pos_advance_kernel, dim3(1), dim3(64), 0, s, M->d_pos, B);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+// Largest K-split partial buffer any GEMM of the step needs.
+size_t part_floats(anehip_ctx *ctx, Model *M) {
+    const anehip_model_desc &D = M->desc;
+    const uint32_t d = D.dim, F = D.hidden_dim;
+    struct {
+        uint32_t m, n;
+    } g[] = {{M->rows_dn, d}, {M->rows_attn, d}, {d, d}, {d, D.n_heads * D.head_dim}, {2 * F, d}, {d, F},
+             {D.vocab_size, d}};
+    size_t mx = 0;
+    for (auto &e : g) {
+        if (!e.m) continue;
+        size_t need = (size_t)gemm_ksplit(ctx, e.m, e.n) * M->batch * e.m;
+        if (need > mx) mx = need;
+    }
+    return mx;
+}
+
+int launch_step(anehip_ctx *ctx, Model *M) {
+    hipStream_t s = ctx->stream;
+    if (!M->use_graph) return enqueue_step(ctx, M, s);
+    if (!M->exec) {
+        ANEHIP_HIP_TRY(ctx->err, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_step(ctx, M, s);
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(s, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess)
+            return set_error(ctx->err, ANEHIP_EHIP, "graph capture failed: %s", hipGetErrorString(e));
+        M->graph = g;
+        e = hipGraphInstantiate(&M->exec, g, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            drop_graph(M);
+            return set_error(ctx->err, ANEHIP_EHIP, "graph instantiate failed: %s", hipGetErrorString(e));
+        }
+    }
+    ANEHIP_HIP_TRY(ctx->err, hipGraphLaunch(M->exec, s));
+    return ANEHIP_OK;
+}
+
+int stage_tokens(anehip_ctx *ctx, Model *M, const uint32_t *tokens, uint32_t batch) {
+    if (!tokens) return set_error(ctx->err, ANEHIP_EINVAL, "decode_step: tokens is NULL");
+    if (batch != M->batch)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "decode_step: batch %u, state was allocated for %u", batch,
+                         M->batch);
+    for (uint32_t b = 0; b < batch; b++)
+        if (M->host_pos[b] >= M->max_seq)
+            return set_error(ctx->err, ANEHIP_ERANGE, "decode_step: sequence %u at pos %u, KV capacity %u", b,
+                             M->host_pos[b], M->max_seq);
+    // the previous step may still read the staging buffer
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    std::memcpy(M->h_tokens, tokens, batch * sizeof(uint32_t));
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(M->d_tokens, M->h_tokens, batch * sizeof(uint32_t),
+                                            hipMemcpyHostToDevice, ctx->stream));
+    return ANEHIP_OK;
+}
+
+Model *model_of(anehip_ctx *ctx, int *rc) {
+    if (!ctx) {
+        *rc = set_error(global_error(), ANEHIP_EINVAL, "ctx is NULL");
+        return nullptr;
+    }
+    if (!ctx->model) {
+        *rc = set_error(ctx->err, ANEHIP_ESTATE, "context was created without a model description");
+        return nullptr;
+    }
+    *rc = ANEHIP_OK;
+    return ctx->model;
+}
+
+}  // namespace
+
+namespace anehip {
+void rope_inv_freq(float base, int head_dim, float *out) {
+    for (int i = 0; i < head_dim; i += 2) out[i / 2] = 1.0f / powf(base, (float)i / (float)head_dim);
+}
+}  // namespace anehip
+
+extern "C" {
+
+__attribute__((visibility("hidden"))) int anehip_model_setup(anehip_ctx *ctx, const anehip_model_desc *desc) {
+    const anehip_model_desc &D = *desc;
+    if (!D.layer_types || D.n_layers == 0)
+        return set_error(ctx->err, ANEHIP_EINVAL, "model: layer_types NULL or n_layers 0");
+    for (uint32_t l = 0; l < D.n_layers; l++)
+        if (D.layer_types[l] > ANEHIP_LAYER_FULL_ATTENTION)
+            return set_error(ctx->err, ANEHIP_EINVAL, "model: layer %u has type %u", l, D.layer_types[l]);
+    if (D.dim == 0 || D.dim % 256 || D.hidden_dim == 0 || D.hidden_dim % 256 || D.vocab_size == 0)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "model: dim %u / hidden_dim %u must be multiples of 256",
+                         D.dim, D.hidden_dim);
+    if (D.ssm_state_size != kDk || D.ssm_conv_kernel != kConvK || D.ssm_group_count * kDk != D.dim)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED,
+                         "model: DeltaNet kernels need ssm_state_size 128, conv kernel 4 and "
+                         "ssm_group_count*128 == dim (got %u, %u, %u)",
+                         D.ssm_state_size, D.ssm_conv_kernel, D.ssm_group_count);
+    bool has_attn = false;
+    for (uint32_t l = 0; l < D.n_layers; l++) has_attn |= D.layer_types[l] == ANEHIP_LAYER_FULL_ATTENTION;
+    if (has_attn) {
+        if (D.head_dim != kHd || D.n_kv_heads == 0 || D.n_heads % D.n_kv_heads ||
+            (D.n_heads / D.n_kv_heads != 1 && D.n_heads / D.n_kv_heads != 2 && D.n_heads / D.n_kv_heads != 4) ||
+            (D.n_heads * D.head_dim) % 256)
+            return set_error(ctx->err, ANEHIP_EUNSUPPORTED,
+                             "model: attention kernels need head_dim 256 and 1, 2 or 4 query heads per kv head "
+                             "(got head_dim %u, %u/%u heads)",
+                             D.head_dim, D.n_heads, D.n_kv_heads);
+        if (!(D.rope_freq_base > 0.0f))
+            return set_error(ctx->err, ANEHIP_EINVAL, "model: rope_freq_base must be > 0");
+    }
+    Model *M = new Model();
+    M->desc = D;
+    M->types.assign(D.layer_types, D.layer_types + D.n_layers);
+    M->desc.layer_types = M->types.data();
+    M->layers.resize(D.n_layers);
+    for (uint32_t l = 0; l < D.n_layers; l++) M->layers[l].type = D.layer_types[l];
+    M->rows_dn = 3 * D.dim + D.dim + 2 * D.ssm_group_count;
+    M->rows_attn = has_attn ? 2 * D.n_heads * D.head_dim + 2 * D.n_kv_heads * D.head_dim : 0;
+    ctx->model = M;
+    if (has_attn) {
+        std::vector<float> f(kHd / 2);
+        rope_inv_freq(D.rope_freq_base, (int)kHd, f.data());
+        if (hipMalloc(&M->inv_freq, f.size() * sizeof(float)) != hipSuccess)
+            return set_error(ctx->err, ANEHIP_ENOMEM, "model: inv_freq allocation failed");
+        ANEHIP_HIP_TRY(ctx->err, hipMemcpy(M->inv_freq, f.data(), f.size() * sizeof(float), hipMemcpyHostToDevice));
+    }
+    return ANEHIP_OK;
+}
+
+__attribute__((visibility("hidden"))) void anehip_model_teardown(anehip_ctx *ctx) {
+    Model *M = ctx->model;
+    if (!M) return;
+    free_state(M);
+    for (Layer &L : M->layers) {
+        void *ps[] = {L.mix_in.d, L.mix_out.d, L.ffn_gu.d, L.ffn_down.d, L.attn_norm, L.post_attn_norm,
+                      L.ssm_a,    L.conv1d,    L.dt_bias,  L.ssm_norm,   L.q_norm,    L.k_norm};
+        for (void *p : ps) free_ptr(p);
+    }
+    free_ptr(M->embedding);
+    free_ptr(M->final_norm);
+    free_ptr(M->lm_head.d);
+    free_ptr(M->inv_freq);
+    delete M;
+    ctx->model = nullptr;
+}
+
+int anehip_upload_quant(anehip_ctx *ctx, int32_t layer, uint32_t kind, const uint8_t *blocks, size_t nbytes,
+                        uint32_t m, uint32_t n, uint32_t ggml_type) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!blocks) return set_error(ctx->err, ANEHIP_EINVAL, "upload_quant: blocks is NULL");
+    if (layer < -1 || layer >= (int32_t)M->desc.n_layers)
+        return set_error(ctx->err, ANEHIP_EINVAL, "upload_quant: layer %d out of range", layer);
+    if (ggml_type != ANEHIP_GGML_Q8_0 && ggml_type != ANEHIP_GGML_Q4_0)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "upload_quant: ggml type %u (Q4_0=2, Q8_0=8)", ggml_type);
+    // Q8Tensor::from_raw checks (q8_gemv.rs:41-50)
+    if (n % 32) return set_error(ctx->err, ANEHIP_ESHAPE, "upload_quant: n=%u not divisible by 32", n);
+    const size_t expected = (size_t)m * (n / 32) * (ggml_type == ANEHIP_GGML_Q8_0 ? 34 : 18);
+    if (nbytes != expected)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "upload_quant: got %zu bytes, expected %zu (m=%u, n=%u, type=%u)",
+                         nbytes, expected, m, n, ggml_type);
+    KindShape ks = kind_shape(M, layer, kind);
+    if (!ks.rows || !ks.quant)
+        return set_error(ctx->err, ANEHIP_EINVAL, "upload_quant: kind %s is not a quantised tensor of layer %d",
+                         kind_name(kind), layer);
+    if (ks.rows != m || ks.cols != n)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "upload_quant: %s of layer %d is [%u x %u], got [%u x %u]",
+                         kind_name(kind), layer, ks.rows, ks.cols, m, n);
+    QSlot slot = quant_slot(M, layer, kind);
+    QMat &Q = *slot.mat;
+    if (Q.d && Q.type != ggml_type)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED,
+                         "upload_quant: %s of layer %d is type %u but its stacked matrix holds type %u",
+                         kind_name(kind), layer, ggml_type, Q.type);
+    if (!Q.d) {
+        const size_t bytes = (size_t)slot.total_rows * qrow_bytes(ggml_type, n);
+        if (hipMalloc(&Q.d, bytes) != hipSuccess) {
+            Q.d = nullptr;
+            return set_error(ctx->err, ANEHIP_ENOMEM, "upload_quant: cannot allocate %zu bytes", bytes);
+        }
+        Q.type = ggml_type;
+        Q.rows = slot.total_rows;
+        Q.cols = n;
+    }
+    char *dst = static_cast<char *>(Q.d) + (size_t)slot.row_off * qrow_bytes(ggml_type, n);
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpy(dst, blocks, nbytes, hipMemcpyHostToDevice));
+    if (layer < 0) M->glob_have |= 1ull << kind;
+    else M->layers[layer].have |= 1ull << kind;
+    return ANEHIP_OK;
+}
+
+int anehip_upload_f32(anehip_ctx *ctx, int32_t layer, uint32_t kind, const float *data, size_t n) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!data) return set_error(ctx->err, ANEHIP_EINVAL, "upload_f32: data is NULL");
+    if (layer < -1 || layer >= (int32_t)M->desc.n_layers)
+        return set_error(ctx->err, ANEHIP_EINVAL, "upload_f32: layer %d out of range", layer);
+    KindShape ks = kind_shape(M, layer, kind);
+    if (!ks.rows || ks.quant)
+        return set_error(ctx->err, ANEHIP_EINVAL, "upload_f32: kind %s is not an f32 tensor of layer %d",
+                         kind_name(kind), layer);
+    const size_t want = (size_t)ks.rows * ks.cols;
+    if (n != want)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "upload_f32: %s of layer %d has %zu values, got %zu",
+                         kind_name(kind), layer, want, n);
+    float **slot = f32_slot(M, layer, kind);
+    if (!*slot && hipMalloc((void **)slot, want * sizeof(float)) != hipSuccess) {
+        *slot = nullptr;
+        return set_error(ctx->err, ANEHIP_ENOMEM, "upload_f32: cannot allocate %zu floats", want);
+    }
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpy(*slot, data, want * sizeof(float), hipMemcpyHostToDevice));
+    if (layer < 0) M->glob_have |= 1ull << kind;
+    else M->layers[layer].have |= 1ull << kind;
+    return ANEHIP_OK;
+}
+
+int anehip_tensor_ptr(anehip_ctx *ctx, int32_t layer, uint32_t kind, uint32_t ggml_type, void **dptr,
+                      size_t *nbytes) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!dptr || !nbytes || layer < -1 || layer >= (int32_t)M->desc.n_layers)
+        return set_error(ctx->err, ANEHIP_EINVAL, "tensor_ptr: bad argument");
+    KindShape ks = kind_shape(M, layer, kind);
+    if (!ks.rows) return set_error(ctx->err, ANEHIP_EINVAL, "tensor_ptr: layer %d has no %s", layer, kind_name(kind));
+    if (ks.quant) {
+        if (ggml_type != ANEHIP_GGML_Q8_0 && ggml_type != ANEHIP_GGML_Q4_0)
+            return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "tensor_ptr: ggml type %u", ggml_type);
+        QSlot slot = quant_slot(M, layer, kind);
+        QMat &Q = *slot.mat;
+        if (Q.d && Q.type != ggml_type)
+            return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "tensor_ptr: stacked matrix of %s holds type %u",
+                             kind_name(kind), Q.type);
+        if (!Q.d) {
+            const size_t bytes = (size_t)slot.total_rows * qrow_bytes(ggml_type, ks.cols);
+            if (hipMalloc(&Q.d, bytes) != hipSuccess) {
+                Q.d = nullptr;
+                return set_error(ctx->err, ANEHIP_ENOMEM, "tensor_ptr: cannot allocate %zu bytes", bytes);
+            }
+            Q.type = ggml_type;
+            Q.rows = slot.total_rows;
+            Q.cols = ks.cols;
+        }
+        *dptr = static_cast<char *>(Q.d) + (size_t)slot.row_off * qrow_bytes(ggml_type, ks.cols);
+        *nbytes = (size_t)ks.rows * qrow_bytes(ggml_type, ks.cols);
+    } else {
+        float **slot = f32_slot(M, layer, kind);
+        const size_t want = (size_t)ks.rows * ks.cols;
+        if (!*slot && hipMalloc((void **)slot, want * sizeof(float)) != hipSuccess) {
+            *slot = nullptr;
+            return set_error(ctx->err, ANEHIP_ENOMEM, "tensor_ptr: cannot allocate %zu floats", want);
+        }
+        *dptr = *slot;
+        *nbytes = want * sizeof(float);
+    }
+    if (layer < 0) M->glob_have |= 1ull << kind;
+    else M->layers[layer].have |= 1ull << kind;
+    return ANEHIP_OK;
+}
+
+int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (batch == 0 || batch > 32) return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "alloc_state: batch %u outside 1..32", batch);
+    if (max_seq == 0) return set_error(ctx->err, ANEHIP_EINVAL, "alloc_state: max_seq is 0");
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    free_state(M);
+    const anehip_model_desc &D = M->desc;
+    const size_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
+    const size_t kvd = (size_t)D.n_kv_heads * D.head_dim;
+    auto alloc = [&](void **p, size_t bytes) -> int {
+        if (hipMalloc(p, bytes) != hipSuccess) {
+            *p = nullptr;
+            (void)hipGetLastError();
+            return set_error(ctx->err, ANEHIP_ENOMEM, "alloc_state: cannot allocate %zu bytes", bytes);
+        }
+        if (hipMemset(*p, 0, bytes) != hipSuccess)
+            return set_error(ctx->err, ANEHIP_EHIP, "alloc_state: memset failed");
+        return ANEHIP_OK;
+    };
+    M->batch = batch;
+    M->max_seq = max_seq;
+    int r = ANEHIP_OK;
+    for (Layer &L : M->layers) {
+        if (L.type == ANEHIP_LAYER_DELTANET) {
+            r = r ? r : alloc((void **)&L.conv_state, batch * C * kConvK * sizeof(float));
+            r = r ? r : alloc((void **)&L.S, batch * H * kDk * kDk * sizeof(float));
+        } else {
+            r = r ? r : alloc((void **)&L.kc, batch * kvd * max_seq * sizeof(__half));
+            r = r ? r : alloc((void **)&L.vc, batch * kvd * max_seq * sizeof(__half));
+        }
+    }
+    const size_t rows_in = M->rows_dn > M->rows_attn ? M->rows_dn : M->rows_attn;
+    const size_t qd = (size_t)D.n_heads * D.head_dim;
+    r = r ? r : alloc((void **)&M->d_pos, 64 * sizeof(uint32_t));
+    r = r ? r : alloc((void **)&M->d_tokens, 64 * sizeof(uint32_t));
+    r = r ? r : alloc((void **)&M->d_sampled, 64 * sizeof(uint32_t));
+    r = r ? r : alloc((void **)&M->x, batch * d * sizeof(float));
+    r = r ? r : alloc((void **)&M->xn, batch * d * sizeof(float));
+    r = r ? r : alloc((void **)&M->mixbuf, batch * rows_in * sizeof(float));
+    r = r ? r : alloc((void **)&M->heads, batch * d * sizeof(float));
+    r = r ? r : alloc((void **)&M->normed, batch * d * sizeof(float));
+    r = r ? r : alloc((void **)&M->attn_out, batch * (qd ? qd : 1) * sizeof(float));
+    r = r ? r : alloc((void **)&M->h, batch * F * sizeof(float));
+    r = r ? r : alloc((void **)&M->part, part_floats(ctx, M) * sizeof(float));
+    r = r ? r : alloc((void **)&M->logits, batch * (size_t)D.vocab_size * sizeof(float));
+    r = r ? r : alloc(&M->argmax_ws, argmax_workspace_bytes((int)batch));
+    if (M->rows_attn) {
+        const int G = (int)(D.n_heads / D.n_kv_heads);
+        r = r ? r : alloc((void **)&M->attn_part, attn_partial_floats((int)batch, (int)D.n_kv_heads, (int)max_seq, G) * sizeof(float));
+    }
+    if (!r && hipHostMalloc((void **)&M->h_tokens, 64 * sizeof(uint32_t), 0) != hipSuccess) {
+        M->h_tokens = nullptr;
+        r = set_error(ctx->err, ANEHIP_ENOMEM, "alloc_state: pinned staging allocation failed");
+    }
+    if (r) {
+        free_state(M);
+        return r;
+    }
+    M->host_pos.assign(batch, 0);
+    return ANEHIP_OK;
+}
+
+int anehip_reset_state(anehip_ctx *ctx) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!M->batch) return set_error(ctx->err, ANEHIP_ESTATE, "reset_state: no state allocated");
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    const anehip_model_desc &D = M->desc;
+    const size_t C = 3 * (size_t)D.dim, kvd = (size_t)D.n_kv_heads * D.head_dim;
+    for (Layer &L : M->layers) {
+        if (L.type == ANEHIP_LAYER_DELTANET) {
+            ANEHIP_HIP_TRY(ctx->err, hipMemset(L.conv_state, 0, M->batch * C * kConvK * sizeof(float)));
+            ANEHIP_HIP_TRY(ctx->err, hipMemset(L.S, 0, M->batch * (size_t)D.ssm_group_count * kDk * kDk * sizeof(float)));
+        } else {
+            ANEHIP_HIP_TRY(ctx->err, hipMemset(L.kc, 0, M->batch * kvd * M->max_seq * sizeof(__half)));
+            ANEHIP_HIP_TRY(ctx->err, hipMemset(L.vc, 0, M->batch * kvd * M->max_seq * sizeof(__half)));
+        }
+    }
+    ANEHIP_HIP_TRY(ctx->err, hipMemset(M->d_pos, 0, 64 * sizeof(uint32_t)));
+    M->host_pos.assign(M->batch, 0);
+    return ANEHIP_OK;
+}
+
+int anehip_set_pos(anehip_ctx *ctx, uint32_t seq, uint32_t pos) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (seq >= M->batch) return set_error(ctx->err, ANEHIP_EINVAL, "set_pos: sequence %u of %u", seq, M->batch);
+    if (pos >= M->max_seq) return set_error(ctx->err, ANEHIP_ERANGE, "set_pos: pos %u >= capacity %u", pos, M->max_seq);
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpy(M->d_pos + seq, &pos, sizeof(uint32_t), hipMemcpyHostToDevice));
+    M->host_pos[seq] = pos;
+    return ANEHIP_OK;
+}
+
+int anehip_get_pos(anehip_ctx *ctx, uint32_t seq, uint32_t *pos) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!pos || seq >= M->batch) return set_error(ctx->err, ANEHIP_EINVAL, "get_pos: bad argument");
+    *pos = M->host_pos[seq];
+    return ANEHIP_OK;
+}
+
+int anehip_state_ptr(anehip_ctx *ctx, uint32_t layer, uint32_t which, void **dptr, size_t *nbytes) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!dptr || !nbytes || layer >= M->desc.n_layers || which > 3)
+        return set_error(ctx->err, ANEHIP_EINVAL, "state_ptr: bad argument");
+    if (!M->batch) return set_error(ctx->err, ANEHIP_ESTATE, "state_ptr: no state allocated");
+    Layer &L = M->layers[layer];
+    const anehip_model_desc &D = M->desc;
+    const bool dn = L.type == ANEHIP_LAYER_DELTANET;
+    if (dn != (which < 2))
+        return set_error(ctx->err, ANEHIP_EINVAL, "state_ptr: layer %u has no state kind %u", layer, which);
+    switch (which) {
+        case 0: *dptr = L.conv_state; *nbytes = M->batch * 3 * (size_t)D.dim * kConvK * sizeof(float); break;
+        case 1: *dptr = L.S; *nbytes = M->batch * (size_t)D.ssm_group_count * kDk * kDk * sizeof(float); break;
+        case 2: *dptr = L.kc; *nbytes = M->batch * (size_t)D.n_kv_heads * D.head_dim * M->max_seq * sizeof(__half); break;
+        default: *dptr = L.vc; *nbytes = M->batch * (size_t)D.n_kv_heads * D.head_dim * M->max_seq * sizeof(__half); break;
+    }
+    return ANEHIP_OK;
+}
+
+int anehip_set_graph(anehip_ctx *ctx, int enabled) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    drop_graph(M);
+    M->use_graph = enabled != 0;
+    return ANEHIP_OK;
+}
+
+int anehip_decode_step_async(anehip_ctx *ctx, const uint32_t *tokens, uint32_t batch) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if ((rc = check_model(ctx, M))) return rc;
+    if ((rc = stage_tokens(ctx, M, tokens, batch))) return rc;
+    if ((rc = launch_step(ctx, M))) return rc;
+    for (uint32_t b = 0; b < batch; b++) M->host_pos[b]++;
+    return ANEHIP_OK;
+}
+
+int anehip_decode_step(anehip_ctx *ctx, const uint32_t *tokens, uint32_t batch, float *logits_out) {
+    int rc = anehip_decode_step_async(ctx, tokens, batch);
+    if (rc) return rc;
+    Model *M = ctx->model;
+    if (logits_out)
+        ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(logits_out, M->logits, (size_t)batch * M->desc.vocab_size * sizeof(float),
+                                                hipMemcpyDeviceToHost, ctx->stream));
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    return ANEHIP_OK;
+}
+
+int anehip_logits_ptr(anehip_ctx *ctx, const float **dptr) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!dptr || !M->batch) return set_error(ctx->err, ANEHIP_ESTATE, "logits_ptr: no state");
+    *dptr = M->logits;
+    return ANEHIP_OK;
+}
+
+int anehip_sampled_tokens(anehip_ctx *ctx, uint32_t *out) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!out || !M->batch) return set_error(ctx->err, ANEHIP_ESTATE, "sampled_tokens: no state");
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(out, M->d_sampled, M->batch * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                            ctx->stream));
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    return ANEHIP_OK;
+}
+
+int anehip_generate(anehip_ctx *ctx, const uint32_t *first_tokens, uint32_t batch, uint32_t steps,
+                    uint32_t *out_tokens) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if (!out_tokens || steps == 0) return set_error(ctx->err, ANEHIP_EINVAL, "generate: bad argument");
+    if ((rc = check_model(ctx, M))) return rc;
+    for (uint32_t b = 0; b < M->batch && b < batch; b++)
+        if ((uint64_t)M->host_pos[b] + steps > M->max_seq)
+            return set_error(ctx->err, ANEHIP_ERANGE, "generate: sequence %u at pos %u + %u steps > capacity %u", b,
+                             M->host_pos[b], steps, M->max_seq);
+    if ((rc = stage_tokens(ctx, M, first_tokens, batch))) return rc;
+    uint32_t *d_out = nullptr;
+    ANEHIP_HIP_TRY(ctx->err, hipMallocAsync((void **)&d_out, (size_t)steps * batch * sizeof(uint32_t), ctx->stream));
+    for (uint32_t i = 0; i < steps; i++) {
+        if ((rc = launch_step(ctx, M))) break;
+        // greedy feedback: the sampled tokens are the next step's input, on device
+        if (hipMemcpyAsync(M->d_tokens, M->d_sampled, batch * sizeof(uint32_t), hipMemcpyDeviceToDevice,
+                           ctx->stream) != hipSuccess ||
+            hipMemcpyAsync(d_out + (size_t)i * batch, M->d_sampled, batch * sizeof(uint32_t),
+                           hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess) {
+            rc = set_error(ctx->err, ANEHIP_EHIP, "generate: device copy failed");
+            break;
+        }
+        for (uint32_t b = 0; b < batch; b++) M->host_pos[b]++;
+    }
+    if (!rc && hipMemcpyAsync(out_tokens, d_out, (size_t)steps * batch * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                              ctx->stream) != hipSuccess)
+        rc = set_error(ctx->err, ANEHIP_EHIP, "generate: copy-out failed");
+    (void)hipFreeAsync(d_out, ctx->stream);
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,218 @@
+// deltanet.hip — fused Gated DeltaNet decode step for gfx950.
+//
+// Replaces conv1d_silu, the q/k gpu_memcpy split, l2_normalize_scale,
+// compute_beta_decay and deltanet_recurrence (crates/engine/metal/
+// deltanet.metal:16-156, dispatched at gpu_full_decode.rs:350-456) and the CPU
+// core of deltanet_decode_step (crates/engine/src/deltanet.rs:444-512), and
+// rmsnorm_gated in its DeltaNet use (deltanet.metal:184-220,
+// deltanet.rs:517-533).
+//
+// One workgroup (256 threads) per (sequence, head, 32-column slice of the
+// value dim).  Every workgroup of a head recomputes the head's conv + SiLU +
+// L2 norm of q and k (256 channels, cheap) from the old conv window; each
+// slice writes back the window of its own 32 v channels.  The q/k windows are
+// read by all 4 slices of a head, so they are committed (shift + append) by
+// the next kernel, dn_finish_kernel, after every slice has read them.
+// The state slice S[h][0:128][c0:c0+32] is read once and written once:
+//   S' = decay * S;  sk = S'^T k;  delta = beta (v - sk);
+//   S'' = S' + k delta^T;  o = S''^T q
+// which is the reference's per-head order (decay, recall, delta, rank-1
+// update, query) with the three global passes of the Metal kernel fused into
+// one read and one write of the 64 KiB head state.
+#include "common.h"
+
+namespace anehip {
+
+namespace {
+
+constexpr int kDk = 128;     // key dim == value dim (ssm_state_size)
+constexpr int kCols = 32;    // value columns per workgroup
+constexpr int kThreads = 256;
+constexpr int kKsize = 4;    // conv width (ssm_conv_kernel)
+
+__device__ __forceinline__ float silu_ref(float x) { return x / (1.0f + expf(-x)); }
+
+// conv_shift_and_append + conv_apply (deltanet_cache.rs:34-54) for one channel;
+// returns the conv output before SiLU, updates the window if `write`.
+__device__ __forceinline__ float conv_channel(float *__restrict__ state, const float *__restrict__ w, float x,
+                                              bool write) {
+    float4 s = *reinterpret_cast<const float4 *>(state);
+    float4 k = *reinterpret_cast<const float4 *>(w);
+    float4 ns = make_float4(s.y, s.z, s.w, x);
+    float sum = 0.0f;
+    sum += ns.x * k.x;
+    sum += ns.y * k.y;
+    sum += ns.z * k.z;
+    sum += ns.w * k.w;
+    if (write) *reinterpret_cast<float4 *>(state) = ns;
+    return sum;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// grid = (dv / 32, n_heads, batch).  qkv_stride / ba_stride are the row
+// strides (floats) of the per-sequence inputs.
+__global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
+    const float *__restrict__ qkv, int qkv_stride, const float *__restrict__ beta_raw,
+    const float *__restrict__ alpha_raw, int ba_stride, const float *__restrict__ conv_w,
+    const float *__restrict__ ssm_a, const float *__restrict__ dt_bias, float *__restrict__ conv_state,
+    float *__restrict__ S, float *__restrict__ out, int n_heads) {
+    __shared__ float qn[kDk], kn[kDk], vv[kCols];
+    __shared__ float red[1][4];
+    __shared__ float part[32][kCols];
+    __shared__ float misc[2];  // beta, decay
+
+    const int t = threadIdx.x;
+    const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int chunk = n_heads * kDk;  // = dim
+    const int C = 3 * chunk;
+    const int c0 = slice * kCols;
+    const float *xin = qkv + (size_t)b * qkv_stride;
+    float *cs = conv_state + (size_t)b * C * kKsize;
+
+    // 1. conv + SiLU of the head's q (t < 128) and k (t >= 128) channels
+    {
+        const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + (t - kDk);
+        float y = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, xin[ch], false));
+        // sum of squares per half (waves 0-1: q, waves 2-3: k)
+        float sq = wave_sum(y * y);
+        if ((t & 63) == 0) red[0][t >> 6] = sq;
+        if (t < kDk) qn[t] = y;
+        else kn[t - kDk] = y;
+    }
+    if (t < kCols) {
+        const int ch = 2 * chunk + h * kDk + c0 + t;
+        vv[t] = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, xin[ch], true));
+    }
+    if (t == 0) {
+        // deltanet.rs:474-480
+        const float br = beta_raw[(size_t)b * ba_stride + h];
+        const float ar = alpha_raw[(size_t)b * ba_stride + h];
+        misc[0] = 1.0f / (1.0f + expf(-br));
+        const float g = ssm_a[h] * logf(1.0f + expf(ar + dt_bias[h]));
+        misc[1] = expf(g);
+    }
+    __syncthreads();
+    // 2. L2 normalise (deltanet.rs:25-31, 461-467): x *= 1/sqrt(sum x^2 + 1e-12); q *= 1/sqrt(dk)
+    if (t < kDk) {
+        const float inv = 1.0f / sqrtf((red[0][0] + red[0][1]) + 1e-12f);
+        const float scale = 1.0f / sqrtf((float)kDk);
+        qn[t] = (qn[t] * inv) * scale;
+    } else {
+        const float inv = 1.0f / sqrtf((red[0][2] + red[0][3]) + 1e-12f);
+        kn[t - kDk] = kn[t - kDk] * inv;
+    }
+    __syncthreads();
+
+    // 3. state slice: thread -> 4 columns (cq) x 4 rows (rg)
+    const int cq = t & 7;          // column quad: columns c0 + 4cq .. +3
+    const int rg = t >> 3;         // row group: rows 4rg .. 4rg+3
+    const float beta = misc[0], decay = misc[1];
+    float *Sh = S + (((size_t)b * n_heads + h) * kDk) * kDk + c0 + 4 * cq;
+    float4 s[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(4 * rg + r) * kDk);
+    // S' = decay * S, partial recall sum_i S'_ij k_i over this thread's rows
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float ki = kn[4 * rg + r];
+        s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
+        sk.x += s[r].x * ki; sk.y += s[r].y * ki; sk.z += s[r].z * ki; sk.w += s[r].w * ki;
+    }
+    *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = sk;
+    __syncthreads();
+    // delta_j = beta (v_j - sk_j), every thread for its 4 columns (fixed order)
+    float4 delta;
+    {
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int g = 0; g < 32; g++) {
+            float4 p = *reinterpret_cast<const float4 *>(&part[g][4 * cq]);
+            a[0] += p.x; a[1] += p.y; a[2] += p.z; a[3] += p.w;
+        }
+        delta.x = beta * (vv[4 * cq + 0] - a[0]);
+        delta.y = beta * (vv[4 * cq + 1] - a[1]);
+        delta.z = beta * (vv[4 * cq + 2] - a[2]);
+        delta.w = beta * (vv[4 * cq + 3] - a[3]);
+    }
+    __syncthreads();  // part[] is reused below
+    // S'' = S' + k delta^T (written back), partial query sum_i S''_ij q_i
+    float4 so = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float ki = kn[4 * rg + r], qi = qn[4 * rg + r];
+        s[r].x += ki * delta.x; s[r].y += ki * delta.y; s[r].z += ki * delta.z; s[r].w += ki * delta.w;
+        *reinterpret_cast<float4 *>(Sh + (size_t)(4 * rg + r) * kDk) = s[r];
+        so.x += s[r].x * qi; so.y += s[r].y * qi; so.z += s[r].z * qi; so.w += s[r].w * qi;
+    }
+    *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = so;
+    __syncthreads();
+    if (t < kCols) {
+        float o = 0.f;
+        for (int g = 0; g < 32; g++) o += part[g][t];
+        out[(size_t)b * chunk + h * kDk + c0 + t] = o;
+    }
+}
+
+// Runs after deltanet_step_kernel.  If `conv_state` is not null, commits the
+// q/k conv windows of head h (shift left, append the new input:
+// deltanet_cache.rs:34-42); if `heads` is not null, applies the per-head RMSNorm with ssm_norm and the
+// SiLU(gate) product (deltanet.rs:517-533).  grid = (n_heads, batch), 128
+// threads (one per element of the head).
+__global__ __launch_bounds__(kDk) void dn_finish_kernel(const float *__restrict__ qkv, int qkv_stride,
+                                                        float *__restrict__ conv_state,
+                                                        const float *__restrict__ heads,
+                                                        const float *__restrict__ gate, int gate_stride,
+                                                        const float *__restrict__ norm_w,
+                                                        float *__restrict__ out, int n_heads, float eps) {
+    __shared__ float red[2];
+    const int t = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
+    const int chunk = n_heads * kDk;
+    if (conv_state) {
+        const float *xin = qkv + (size_t)b * qkv_stride;
+        float *cs = conv_state + (size_t)b * 3 * chunk * kKsize;
+        const int cq = h * kDk + t, ck = chunk + h * kDk + t;
+        float4 a = *reinterpret_cast<const float4 *>(cs + (size_t)cq * kKsize);
+        float4 c = *reinterpret_cast<const float4 *>(cs + (size_t)ck * kKsize);
+        *reinterpret_cast<float4 *>(cs + (size_t)cq * kKsize) = make_float4(a.y, a.z, a.w, xin[cq]);
+        *reinterpret_cast<float4 *>(cs + (size_t)ck * kKsize) = make_float4(c.y, c.z, c.w, xin[ck]);
+    }
+    if (!heads) return;
+    const float x = heads[(size_t)b * chunk + h * kDk + t];
+    float ss = wave_sum(x * x);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float ms = (red[0] + red[1]) / (float)kDk;
+    const float inv_rms = 1.0f / sqrtf(ms + eps);
+    const float g = gate[(size_t)b * gate_stride + h * kDk + t];
+    out[(size_t)b * chunk + h * kDk + t] = ((x * inv_rms) * norm_w[t]) * (g / (1.0f + expf(-g)));
+}
+
+}  // namespace
+
+int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const float *qkv,
+                         int qkv_stride, const float *beta_raw, const float *alpha_raw, int ba_stride,
+                         const float *conv_w, const float *ssm_a, const float *dt_bias, float *conv_state, float *S,
+                         float *out) {
+    hipLaunchKernelGGL(deltanet_step_kernel, dim3(kDk / kCols, n_heads, batch), dim3(kThreads), 0, stream, qkv,
+                       qkv_stride, beta_raw, alpha_raw, ba_stride, conv_w, ssm_a, dt_bias, conv_state, S, out,
+                       n_heads);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+// heads == nullptr: only commit the q/k conv windows.
+int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const float *qkv, int qkv_stride,
+                     float *conv_state, const float *heads, const float *gate, int gate_stride, const float *norm_w,
+                     float *out, float eps) {
+    hipLaunchKernelGGL(dn_finish_kernel, dim3(n_heads, batch), dim3(kDk), 0, stream, qkv, qkv_stride, conv_state,
+                       heads, gate, gate_stride, norm_w, out, n_heads, eps);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+}  // namespace anehip

@@ -1,0 +1,258 @@
+// elementwise.hip — row-wise norms, residuals, SiLU-mul, embedding gather and
+// greedy argmax for gfx950.
+//
+// Replaces rmsnorm_simple, residual_add and silu_mul (crates/engine/metal/
+// deltanet.metal:227-272, q8_gemv.metal:89-97) and their CPU forms
+// (main.rs:983-992, 1106-1135; scratch.rs:174-186), plus the host-side
+// embedding copy (gpu_full_decode.rs:273-278) and greedy_sample
+// (main.rs:1767-1785), which move on-device.  GEMV outputs may arrive as
+// K-split partial sums ([ksplit][rows][n]); the kernels here add them in split
+// order, then apply the element-wise step, so a GEMV and its epilogue cost
+// one extra launch at most.
+#include "common.h"
+
+namespace anehip {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Sum over a 256-thread block; every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return s;
+}
+
+// out[b] = x[b] * (1/sqrt(mean(x[b]^2) + eps)) * w     (main.rs:1106-1113)
+__device__ __forceinline__ void rmsnorm_row(const float *x, const float *__restrict__ w, float *out, int n,
+                                            float eps, float *red) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kThreads) ss += x[i] * x[i];
+    ss = block_sum(ss, red);
+    const float inv_rms = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += kThreads) out[i] = (x[i] * inv_rms) * w[i];
+}
+
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                           float *__restrict__ out, int n, float eps) {
+    __shared__ float red[4];
+    const size_t b = blockIdx.x;
+    rmsnorm_row(x + b * n, w, out + b * n, n, eps, red);
+}
+
+// x[b] = embedding[token[b]] (zeros if token >= vocab, main.rs:960-963);
+// xn[b] = rmsnorm(x[b], w).
+__global__ __launch_bounds__(kThreads) void embed_rmsnorm_kernel(const uint32_t *__restrict__ tokens,
+                                                                 const float *__restrict__ emb, uint32_t vocab,
+                                                                 float *__restrict__ x, const float *__restrict__ w,
+                                                                 float *__restrict__ xn, int n, float eps) {
+    __shared__ float red[4];
+    const size_t b = blockIdx.x;
+    const uint32_t tok = tokens[b];
+    float *xb = x + b * n;
+    for (int i = threadIdx.x; i < n; i += kThreads) xb[i] = tok < vocab ? emb[(size_t)tok * n + i] : 0.0f;
+    __syncthreads();
+    rmsnorm_row(xb, w, xn + b * n, n, eps, red);
+}
+
+// x[b] += sum_k part[k][b]; if w: xn[b] = rmsnorm(x[b], w).   part stride between
+// splits = rows * n.
+__global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(float *__restrict__ x,
+                                                                    const float *__restrict__ part, int ksplit,
+                                                                    int rows, const float *__restrict__ w,
+                                                                    float *__restrict__ xn, int n, float eps) {
+    __shared__ float red[4];
+    const size_t b = blockIdx.x;
+    float *xb = x + b * n;
+    const size_t split = (size_t)rows * n;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        float s = part[b * n + i];
+        for (int k = 1; k < ksplit; k++) s += part[k * split + b * n + i];
+        xb[i] = xb[i] + s;
+    }
+    if (!w) return;
+    __syncthreads();
+    rmsnorm_row(xb, w, xn + b * n, n, eps, red);
+}
+
+// Stacked [gate; up] GEMV output gu[k][b][2F]: h[b][r] = SiLU(gate) * up
+// (scratch.rs:181-186: a = (a / (1 + exp(-a))) * b).
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restrict__ gu, int ksplit, int rows,
+                                                            float *__restrict__ h, int F) {
+    const size_t b = blockIdx.y;
+    const int r = blockIdx.x * kThreads + threadIdx.x;
+    if (r >= F) return;
+    const size_t split = (size_t)rows * 2 * F;
+    float g = gu[b * 2 * F + r], u = gu[b * 2 * F + F + r];
+    for (int k = 1; k < ksplit; k++) {
+        g += gu[k * split + b * 2 * F + r];
+        u += gu[k * split + b * 2 * F + F + r];
+    }
+    h[b * F + r] = (g / (1.0f + expf(-g))) * u;
+}
+
+// a[i] = silu(a[i]) * b[i]   (elementwise entry point)
+__global__ __launch_bounds__(kThreads) void silu_mul_plain_kernel(float *__restrict__ a, const float *__restrict__ b,
+                                                                  size_t n) {
+    size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) a[i] = (a[i] / (1.0f + expf(-a[i]))) * b[i];
+}
+
+// x[i] += y[i]
+__global__ __launch_bounds__(kThreads) void residual_add_kernel(float *__restrict__ x, const float *__restrict__ y,
+                                                                size_t n) {
+    size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) x[i] += y[i];
+}
+
+// f32::total_cmp order as a signed key (bit flip of negatives).
+__device__ __forceinline__ int32_t total_key(float f) {
+    int32_t b = __float_as_int(f);
+    return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+// (key, index) with the larger key; equal keys: the larger index (Iterator::max_by
+// keeps the last maximum).
+__device__ __forceinline__ void arg_better(int32_t &k, uint32_t &i, int32_t k2, uint32_t i2) {
+    if (k2 > k || (k2 == k && i2 > i)) {
+        k = k2;
+        i = i2;
+    }
+}
+
+__device__ __forceinline__ void block_argmax(int32_t &k, uint32_t &i, int32_t *rk, uint32_t *ri) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        int32_t k2 = __shfl_xor(k, o);
+        uint32_t i2 = __shfl_xor(i, o);
+        arg_better(k, i, k2, i2);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        rk[threadIdx.x >> 6] = k;
+        ri[threadIdx.x >> 6] = i;
+    }
+    __syncthreads();
+    k = rk[0];
+    i = ri[0];
+    for (int w = 1; w < kThreads / 64; w++) arg_better(k, i, rk[w], ri[w]);
+}
+
+constexpr int kArgBlocks = 64;
+
+// stage 1: grid (kArgBlocks, batch); each block scans a strided slice.
+__global__ __launch_bounds__(kThreads) void argmax_stage1(const float *__restrict__ logits, uint32_t n,
+                                                          int32_t *__restrict__ pk, uint32_t *__restrict__ pi) {
+    __shared__ int32_t rk[4];
+    __shared__ uint32_t ri[4];
+    const size_t b = blockIdx.y;
+    const float *row = logits + b * n;
+    int32_t k = INT32_MIN;
+    uint32_t idx = 0;
+    bool any = false;
+    for (uint32_t j = blockIdx.x * kThreads + threadIdx.x; j < n; j += kArgBlocks * kThreads) {
+        int32_t kk = total_key(row[j]);
+        if (!any) {
+            k = kk;
+            idx = j;
+            any = true;
+        } else {
+            arg_better(k, idx, kk, j);
+        }
+    }
+    if (!any) {
+        k = INT32_MIN;
+        idx = 0;
+    }
+    block_argmax(k, idx, rk, ri);
+    if (threadIdx.x == 0) {
+        pk[b * kArgBlocks + blockIdx.x] = k;
+        pi[b * kArgBlocks + blockIdx.x] = idx;
+    }
+}
+
+// stage 2: one wave per row.
+__global__ __launch_bounds__(64) void argmax_stage2(const int32_t *__restrict__ pk, const uint32_t *__restrict__ pi,
+                                                    uint32_t *__restrict__ out) {
+    const size_t b = blockIdx.x;
+    int32_t k = pk[b * kArgBlocks + threadIdx.x];
+    uint32_t i = pi[b * kArgBlocks + threadIdx.x];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        int32_t k2 = __shfl_xor(k, o);
+        uint32_t i2 = __shfl_xor(i, o);
+        arg_better(k, i, k2, i2);
+    }
+    if (threadIdx.x == 0) out[b] = i;
+}
+
+}  // namespace
+
+int launch_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const float *x, const float *w, float *out,
+                   float eps) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, w, out, n, eps);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const uint32_t *tokens, const float *emb,
+                         uint32_t vocab, float *x, const float *w, float *xn, float eps) {
+    hipLaunchKernelGGL(embed_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, tokens, emb, vocab, x, w, xn, n, eps);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
+                            int ksplit, const float *w, float *xn, float eps) {
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, part, ksplit, rows, w, xn, n,
+                       eps);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit,
+                            float *h) {
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((F + kThreads - 1) / kThreads, rows), dim3(kThreads), 0, s, gu, ksplit,
+                       rows, h, F);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_silu_mul(anehip_ctx *ctx, hipStream_t s, float *a, const float *b, size_t n) {
+    hipLaunchKernelGGL(silu_mul_plain_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
+                       a, b, n);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_residual_add(anehip_ctx *ctx, hipStream_t s, float *x, const float *y, size_t n) {
+    hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, x,
+                       y, n);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+size_t argmax_workspace_bytes(int rows) { return (size_t)rows * kArgBlocks * 8; }
+
+// ws: argmax_workspace_bytes(rows) bytes of device memory.
+int launch_argmax(anehip_ctx *ctx, hipStream_t s, int rows, uint32_t n, const float *logits, void *ws,
+                  uint32_t *out) {
+    int32_t *pk = static_cast<int32_t *>(ws);
+    uint32_t *pi = reinterpret_cast<uint32_t *>(pk + (size_t)rows * kArgBlocks);
+    hipLaunchKernelGGL(argmax_stage1, dim3(kArgBlocks, rows), dim3(kThreads), 0, s, logits, n, pk, pi);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    hipLaunchKernelGGL(argmax_stage2, dim3(rows), dim3(64), 0, s, pk, pi, out);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+}  // namespace anehip

@@ -142,7 +142,8 @@ template <uint32_t T, int B>
 __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_tiled(const uint8_t *__restrict__ W,
                                                                       const float *__restrict__ x,
                                                                       float *__restrict__ out, int m, int n,
-                                                                      int batch, int sb_per_split) {
+                                                                      int batch, int sb_per_split,
+                                                                      size_t split_stride) {
     constexpr int V = QTraits<T>::kSbVec;
     __shared__ u32x4 lds[kWavesPerWg][V * kWave];
     __shared__ float red[kWavesPerWg][B][kWave];
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_tiled(const uin
     if (wave != 0) return;
     const int row = row0 + lane;
     if (row >= m) return;
-    float *dst = out + (size_t)ks * batch * m;
+    float *dst = out + (size_t)ks * split_stride;
 #pragma unroll
     for (int b = 0; b < B; b++) {
         if (b < batch) {
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(256) void sum_partials(const float *__restrict__ pa
 }
 
 // K splits: the smallest divisor of the super-block count that gives at
-// least `target` waves, with at least one super-block per wave.
+// least `target` waves, or one super-block column per wave.
 int choose_ksplit(int tiles, int nsb, int target_waves) {
     for (int k = 1; k <= nsb; k++) {
         if (nsb % k) continue;
@@ -220,38 +221,25 @@ int choose_ksplit(int tiles, int nsb, int target_waves) {
 
 template <uint32_t T, int B>
 int launch_tiled(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
-                 uint32_t batch, float *y) {
+                 uint32_t batch, float *out, size_t split_stride, int ksplit) {
     const int tiles = (int)((m + kWave - 1) / kWave);
-    const int nsb = (int)(n / 256);
-    const int target = 3 * (ctx->cu_count > 0 ? ctx->cu_count : 256);
-    const int ksplit = choose_ksplit(tiles, nsb, target);
-    const int per = nsb / ksplit;
-    float *out = y;
-    const size_t count = (size_t)batch * m;
-    if (ksplit > 1) {
-        int rc = ensure_workspace(ctx, (size_t)ksplit * count, 0);
-        if (rc) return rc;
-        out = ctx->ws.partial;
-    }
+    const int per = (int)(n / 256) / ksplit;
     hipLaunchKernelGGL((quant_gemm_tiled<T, B>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
-                       static_cast<const uint8_t *>(w), x, out, (int)m, (int)n, (int)batch, per);
+                       static_cast<const uint8_t *>(w), x, out, (int)m, (int)n, (int)batch, per, split_stride);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-    if (ksplit > 1) {
-        hipLaunchKernelGGL(sum_partials, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream,
-                           (const float *)out, y, count, ksplit);
-        ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-    }
     return ANEHIP_OK;
 }
 
 template <uint32_t T>
-int dispatch_batch(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n,
-                   const float *x, uint32_t batch, float *y) {
-    if (batch == 1) return launch_tiled<T, 1>(ctx, stream, w, m, n, x, batch, y);
+int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
+                 uint32_t batch, float *out, int ksplit) {
+    const size_t split_stride = (size_t)batch * m;
+    if (batch == 1) return launch_tiled<T, 1>(ctx, stream, w, m, n, x, 1, out, split_stride, ksplit);
     // small batches: groups of up to 4 rows of x per pass over W (VALU path)
     for (uint32_t b0 = 0; b0 < batch; b0 += 4) {
         uint32_t nb = batch - b0 < 4 ? batch - b0 : 4;
-        int rc = launch_tiled<T, 4>(ctx, stream, w, m, n, x + (size_t)b0 * n, nb, y + (size_t)b0 * m);
+        int rc = launch_tiled<T, 4>(ctx, stream, w, m, n, x + (size_t)b0 * n, nb, out + (size_t)b0 * m, split_stride,
+                                    ksplit);
         if (rc) return rc;
     }
     return ANEHIP_OK;
@@ -259,10 +247,35 @@ int dispatch_batch(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t 
 
 }  // namespace
 
+int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+    const int tiles = (int)((m + kWave - 1) / kWave);
+    const int target = 3 * (ctx->cu_count > 0 ? ctx->cu_count : 256);
+    return choose_ksplit(tiles, (int)(n / 256), target);
+}
+
+int launch_gemm_raw(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,
+                    const float *x, uint32_t batch, float *out, int ksplit) {
+    if (ggml_type == ANEHIP_GGML_Q8_0) return dispatch_raw<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, x, batch, out, ksplit);
+    return dispatch_raw<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, x, batch, out, ksplit);
+}
+
+int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, float *y, size_t count, int ksplit) {
+    hipLaunchKernelGGL(sum_partials, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, part, y, count,
+                       ksplit);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
 int launch_quant_gemm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                       uint32_t n, const float *x, uint32_t batch, float *y) {
-    if (ggml_type == ANEHIP_GGML_Q8_0) return dispatch_batch<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, x, batch, y);
-    return dispatch_batch<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, x, batch, y);
+    const int ksplit = gemm_ksplit(ctx, m, n);
+    if (ksplit == 1) return launch_gemm_raw(ctx, stream, ggml_type, w, m, n, x, batch, y, 1);
+    const size_t count = (size_t)batch * m;
+    int rc = ensure_workspace(ctx, (size_t)ksplit * count, 0);
+    if (rc) return rc;
+    rc = launch_gemm_raw(ctx, stream, ggml_type, w, m, n, x, batch, ctx->ws.partial, ksplit);
+    if (rc) return rc;
+    return launch_sum_partials(ctx, stream, ctx->ws.partial, y, count, ksplit);
 }
 
 }  // namespace anehip

@@ -28,7 +28,11 @@ int set_error(ErrorSlot &slot, int code, const char *fmt, ...) {
 int ensure_workspace(anehip_ctx *ctx, size_t floats, size_t counters) {
     Workspace &ws = ctx->ws;
     if (floats > ws.partial_floats) {
-        if (ws.partial) (void)hipFree(ws.partial);
+        if (ws.partial) {
+            // queued kernels may still read the old buffer
+            ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+            (void)hipFree(ws.partial);
+        }
         ws.partial = nullptr;
         ws.partial_floats = 0;
         size_t want = floats < (1u << 20) ? (1u << 20) : floats;
@@ -117,6 +121,7 @@ void anehip_ctx_destroy(anehip_ctx *ctx) {
     for (void *p : ctx->user_allocs) (void)hipFree(p);
     if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
     if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
+    if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

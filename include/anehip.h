@@ -161,6 +161,139 @@ int anehip_timer_stop(anehip_ctx *ctx, float *ms);
 int anehip_quant_gemm(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32_t m,
                       uint32_t n, const float *x, uint32_t batch, float *y);
 
+/* Row-wise RMSNorm: out[r] = x[r] * 1/sqrt(mean(x[r]^2) + eps) * w, rows x n.
+ * rmsnorm_simple (deltanet.metal:239-272) / rmsnorm_vec (main.rs:1106-1113). */
+int anehip_rmsnorm(anehip_ctx *ctx, const float *x, const float *w, float *out, uint32_t rows, uint32_t n,
+                   float eps);
+
+/* a[i] = SiLU(a[i]) * b[i]: silu_mul (q8_gemv.metal:89-97) /
+ * vec_silu_mul_inplace (scratch.rs:181-186). */
+int anehip_silu_mul(anehip_ctx *ctx, float *a, const float *b, size_t n);
+
+/* x[i] += y[i]: residual_add (deltanet.metal:227-235) / main.rs:983-985. */
+int anehip_residual_add(anehip_ctx *ctx, float *x, const float *y, size_t n);
+
+/*
+ * Gated DeltaNet core for `batch` independent sequences: conv1d_silu +
+ * l2_normalize_scale + compute_beta_decay + deltanet_recurrence
+ * (deltanet.metal:16-177) = deltanet.rs:444-512 of deltanet_decode_step.
+ * Layouts (C = 3 * n_heads * 128, head dims 128, conv width 4):
+ *   qkv [batch][C], beta_raw / alpha_raw [batch][n_heads], conv_w [C][4],
+ *   ssm_a / dt_bias [n_heads], conv_state [batch][C][4] (updated),
+ *   S [batch][n_heads][128][128] (updated), out_heads [batch][n_heads*128].
+ */
+int anehip_deltanet_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, const float *qkv,
+                         const float *beta_raw, const float *alpha_raw, const float *conv_w, const float *ssm_a,
+                         const float *dt_bias, float *conv_state, float *S, float *out_heads);
+
+/* Per-head RMSNorm with norm_w[128], then * SiLU(gate): rmsnorm_gated with a
+ * gate (deltanet.metal:184-220) = deltanet.rs:517-533.  heads, gate, out:
+ * [batch][n_heads*128]. */
+int anehip_gated_rmsnorm(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, const float *heads,
+                         const float *gate, const float *norm_w, float eps, float *out);
+
+/*
+ * Full-attention core for `batch` sequences: q/gate split, q/k RMSNorm
+ * (eps 1e-6), RoPE, KV append at pos[b], softmax attention over 0..pos[b],
+ * * sigmoid(gate): q_gate_split + rmsnorm_gated + rope_apply + gpu_memcpy +
+ * sdpa_causal + sigmoid_gate (attention.metal:9-121) = deltanet.rs:565-669.
+ * head_dim is 256; n_heads / n_kv_heads in {1, 2, 4}.
+ *   qkv [batch][n_heads*512 + 2*n_kv_heads*256]: per sequence the wq output
+ *       ([n_heads][q(256) | gate(256)]), then k, then v (wk, wv outputs);
+ *   pos: device array [batch] (must be < max_seq);
+ *   k_cache, v_cache: fp16 bits, [batch][n_kv_heads][max_seq][256] (written
+ *       at pos);  out [batch][n_heads*256].
+ */
+int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads,
+                          uint32_t max_seq, const float *qkv, const float *q_norm, const float *k_norm,
+                          float rope_base, const uint32_t *pos, uint16_t *k_cache, uint16_t *v_cache,
+                          float *out);
+
+/* Greedy sampling per row: index of the maximum under f32::total_cmp, the
+ * last of equal maxima (greedy_sample, main.rs:1767-1775).  logits
+ * [rows][n], out [rows] (device). */
+int anehip_argmax(anehip_ctx *ctx, const float *logits, uint32_t rows, uint32_t n, uint32_t *out);
+
+/* Set-up utilities for synthetic weights and states (no counterpart in the
+ * reference, which loads GGUF files): fill n device values (fp32, or fp16
+ * bits if is_f16) with seeded, counter-based draws, dist 0 = N(a, b^2),
+ * dist 1 = U(a, b); and quantise a device fp32 [m x n] matrix into Q8_0
+ * (d = absmax/127) or Q4_0 (d = absmax/7, +8 offset) blocks. */
+int anehip_fill_random(anehip_ctx *ctx, void *dptr, size_t n, uint32_t dist, uint32_t is_f16, uint64_t seed,
+                       float a, float b);
+int anehip_quantize(anehip_ctx *ctx, uint32_t ggml_type, const float *w, uint32_t m, uint32_t n, void *out);
+
+/* ---- model-level decode step (context created with a model desc) -------- */
+
+/* Uploads one quantised tensor (host bytes, copied).  Checks ggml_type, the
+ * byte count m*(n/32)*{34|18} as Q8Tensor::from_raw does (q8_gemv.rs:33-57)
+ * and the [m x n] shape the kind has in this model.  Replaces
+ * GpuContext::upload_q8_weights (metal_graph.rs:208-221) inside
+ * upload_model_weights (gpu_decode.rs:152-283). */
+int anehip_upload_quant(anehip_ctx *ctx, int32_t layer, uint32_t kind, const uint8_t *blocks, size_t nbytes,
+                        uint32_t m, uint32_t n, uint32_t ggml_type);
+
+/* Uploads one fp32 tensor (norm weights, conv1d, ssm_a, dt_bias, embedding). */
+int anehip_upload_f32(anehip_ctx *ctx, int32_t layer, uint32_t kind, const float *data, size_t n);
+
+/* Device address where tensor `kind` of `layer` lives (allocated on first
+ * use, with ggml_type for quantised kinds, ignored for fp32 kinds), so a
+ * caller can write it in place (e.g. with anehip_quantize); the tensor then
+ * counts as uploaded.  *nbytes receives its size. */
+int anehip_tensor_ptr(anehip_ctx *ctx, int32_t layer, uint32_t kind, uint32_t ggml_type, void **dptr,
+                      size_t *nbytes);
+
+/* Allocates zeroed per-sequence state for `batch` (1..32) sequences with KV
+ * capacity max_seq, all positions 0: HybridCache::new (deltanet_cache.rs:
+ * 76-136) and the state buffers of upload_model_weights (gpu_decode.rs:
+ * 205-256).  Frees any previous state. */
+int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq);
+
+/* Zeroes all state and sets every position to 0. */
+int anehip_reset_state(anehip_ctx *ctx);
+
+/* Position of one sequence (HybridCache::pos, deltanet_cache.rs:71). */
+int anehip_set_pos(anehip_ctx *ctx, uint32_t seq, uint32_t pos);
+int anehip_get_pos(anehip_ctx *ctx, uint32_t seq, uint32_t *pos);
+
+/* Device pointer and size of one state buffer of layer `layer`:
+ * which 0: conv window [batch][3*dim][4] f32      (DeltaNet layers)
+ *       1: recurrent S [batch][H][128][128] f32    (DeltaNet layers)
+ *       2: K cache [batch][n_kv][max_seq][256] f16 (attention layers)
+ *       3: V cache, same layout.
+ * Lets a caller load state produced elsewhere or read it back. */
+int anehip_state_ptr(anehip_ctx *ctx, uint32_t layer, uint32_t which, void **dptr, size_t *nbytes);
+
+/* Enables (default) or disables replay of the captured step graph; with it
+ * disabled the same kernels are launched one by one. */
+int anehip_set_graph(anehip_ctx *ctx, int enabled);
+
+/*
+ * One decode step for every sequence: token_ids[batch] (ids >= vocab give a
+ * zero embedding, main.rs:960-963), positions advance by one.  Writes the
+ * logits [batch][vocab] to logits_out if not NULL and returns when the step
+ * is done.  Fails with ANEHIP_ERANGE if a position reached max_seq.
+ * Replaces encode_full_token_gpu (gpu_full_decode.rs:221-1044) and, as a
+ * computation, qwen35_forward_token (main.rs:953-1023).
+ */
+int anehip_decode_step(anehip_ctx *ctx, const uint32_t *token_ids, uint32_t batch, float *logits_out);
+
+/* Same, but only enqueues the step on the context stream. */
+int anehip_decode_step_async(anehip_ctx *ctx, const uint32_t *token_ids, uint32_t batch);
+
+/* Device pointer of the last step's logits [batch][vocab]. */
+int anehip_logits_ptr(anehip_ctx *ctx, const float **dptr);
+
+/* Greedy tokens of the last step (argmax of its logits), [batch]. */
+int anehip_sampled_tokens(anehip_ctx *ctx, uint32_t *out);
+
+/* `steps` greedy decode steps with on-device token feedback: step 0 consumes
+ * first_tokens, step i consumes the argmax of step i-1.  out_tokens
+ * [steps][batch].  The reference's host loop (main.rs:473-487) with
+ * greedy_sample moved on device. */
+int anehip_generate(anehip_ctx *ctx, const uint32_t *first_tokens, uint32_t batch, uint32_t steps,
+                    uint32_t *out_tokens);
+
 #ifdef __cplusplus
 }
 #endif

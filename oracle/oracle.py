@@ -231,3 +231,69 @@ def argmax(logits: np.ndarray) -> int:
 
 def max_threads() -> int:
     return int(lib().ao_max_threads())
+
+
+class OracleModel:
+    """The oracle's qwen35_forward_token over host tensors registered by kind
+    (same kinds and shapes as include/anehip.h).  Arrays passed to set_* are
+    kept alive here because the C side borrows them."""
+
+    def __init__(self, dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, vocab_size, ssm_state_size,
+                 ssm_conv_kernel, ssm_group_count, rope_freq_base, rms_norm_eps, layer_types):
+        self.layer_types = np.ascontiguousarray(layer_types, np.uint8)
+        self.vocab = vocab_size
+        self.n_layers = n_layers
+        self.h = lib().ao_model_create(dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim, vocab_size,
+                                       ssm_state_size, ssm_conv_kernel, ssm_group_count, rope_freq_base,
+                                       rms_norm_eps, self.layer_types)
+        self._keep = []
+
+    def set_quant(self, layer, kind, data, rows, cols, ggml_type):
+        data = np.ascontiguousarray(data, np.uint8)
+        self._keep.append(data)
+        assert lib().ao_model_set_quant(self.h, layer, kind, data.ctypes.data, rows, cols, ggml_type) == 0
+
+    def set_f32(self, layer, kind, data):
+        data = np.ascontiguousarray(data, np.float32)
+        self._keep.append(data)
+        assert lib().ao_model_set_f32(self.h, layer, kind, data.ctypes.data, data.size) == 0
+
+    def close(self):
+        if self.h:
+            lib().ao_model_destroy(self.h)
+            self.h = None
+
+
+class OracleSeq:
+    """One sequence's state (conv windows, recurrent states, KV cache, pos)."""
+
+    def __init__(self, model: OracleModel, max_seq: int, kv_f16: bool = True):
+        self.m, self.max_seq = model, max_seq
+        self.h = lib().ao_seq_create(model.h, max_seq, 1 if kv_f16 else 0)
+
+    def view(self, layer, which, count, dtype):
+        fn = {0: lib().ao_seq_conv_state, 1: lib().ao_seq_recurrent_state, 2: lib().ao_seq_k_cache,
+              3: lib().ao_seq_v_cache}[which]
+        ptr = fn(self.h, layer)
+        buf = (C.c_char * (count * np.dtype(dtype).itemsize)).from_address(ptr)
+        return np.frombuffer(buf, dtype=dtype, count=count)
+
+    @property
+    def pos(self):
+        return int(lib().ao_seq_get_pos(self.h))
+
+    @pos.setter
+    def pos(self, p):
+        lib().ao_seq_set_pos(self.h, p)
+
+    def forward(self, token: int, threads: int = 0) -> np.ndarray:
+        logits = np.empty(self.m.vocab, np.float32)
+        rc = lib().ao_forward_token(self.m.h, self.h, token, logits, threads)
+        if rc != 0:
+            raise RuntimeError("oracle forward failed (missing tensor or pos >= max_seq)")
+        return logits
+
+    def close(self):
+        if self.h:
+            lib().ao_seq_destroy(self.h)
+            self.h = None

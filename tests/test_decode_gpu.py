@@ -1,0 +1,171 @@
+"""GPU parity of the full decode step (anehip_decode_step) against the oracle's
+restatement of qwen35_forward_token (crates/cli/src/main.rs:953-1023).
+Bound: logits within 1e-3 relative (rel L2 and max-abs / max |ref|)."""
+import numpy as np
+import pytest
+
+import anehip
+import oracle
+from conftest import rel_errs
+from model_util import SMALL, HostModel, copy_state_to_oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def small_host():
+    return HostModel(anehip.Spec(**SMALL), seed=3)
+
+
+def _model(host, batch, max_seq, graph=True):
+    gm = anehip.Model(host.spec)
+    host.upload(gm)
+    gm.alloc_state(batch, max_seq)
+    gm.set_graph(graph)
+    return gm
+
+
+def test_small_model_steps_from_zero(small_host):
+    gm = _model(small_host, 1, 64)
+    oseq = small_host.seq(64)
+    toks = oracle.randint(5, 1, 10, small_host.spec.vocab_size)
+    for i, t in enumerate(toks):
+        g = gm.step([t])[0]
+        r = oseq.forward(int(t))
+        l2, mx = rel_errs(g, r)
+        print(f"step {i}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+        assert l2 <= TOL and mx <= TOL
+    assert gm.get_pos(0) == 10 and oseq.pos == 10
+    # recurrent state after 10 steps
+    for l in range(small_host.spec.n_layers):
+        if small_host.spec.layer_types[l] == anehip.LAYER_DELTANET:
+            S = gm.get_state(l, 1)
+            assert max(rel_errs(S, oseq.view(l, 1, S.size, np.float32))) <= TOL
+    gm.close()
+    oseq.close()
+
+
+def test_batch_is_independent_sequences(small_host):
+    B = 3
+    gm = _model(small_host, B, 32)
+    seqs = [small_host.seq(32) for _ in range(B)]
+    toks = oracle.randint(6, 2, 5 * B, small_host.spec.vocab_size).reshape(5, B)
+    for step in range(5):
+        g = gm.step(toks[step])
+        for b in range(B):
+            l2, mx = rel_errs(g[b], seqs[b].forward(int(toks[step, b])))
+            assert l2 <= TOL and mx <= TOL
+    gm.close()
+
+
+def test_graph_replay_matches_eager_bits(small_host):
+    toks = oracle.randint(7, 3, 6, small_host.spec.vocab_size)
+    outs = []
+    for graph in (False, True):
+        gm = _model(small_host, 1, 16, graph=graph)
+        outs.append(np.stack([gm.step([t])[0] for t in toks]))
+        gm.close()
+    assert np.array_equal(outs[0], outs[1])
+
+
+def test_token_beyond_vocab_uses_zero_embedding(small_host):
+    gm = _model(small_host, 1, 8)
+    oseq = small_host.seq(8)
+    g = gm.step([small_host.spec.vocab_size + 5])[0]
+    r = oseq.forward(small_host.spec.vocab_size + 5)
+    assert max(rel_errs(g, r)) <= TOL
+    gm.close()
+
+
+def test_generate_feeds_back_on_device(small_host):
+    gm = _model(small_host, 2, 40)
+    out = gm.generate([1, 2], 12)
+    gm2 = _model(small_host, 2, 40)
+    tok = np.array([1, 2], np.uint32)
+    for i in range(12):
+        gm2.step(tok, want_logits=False)
+        tok = gm2.sampled()
+        assert np.array_equal(out[i], tok)
+    # the greedy choice is the oracle's argmax of the same logits
+    oseq = small_host.seq(40)
+    t = 1
+    for i in range(4):
+        t = oracle.argmax(oseq.forward(t))
+        assert t == out[i, 0]
+    gm.close()
+    gm2.close()
+
+
+def test_errors(small_host):
+    gm = anehip.Model(small_host.spec)
+    with pytest.raises(anehip.AnehipError) as e:
+        gm.alloc_state(1, 4)
+        gm.step([1])
+    assert e.value.code == -6 and "not uploaded" in str(e.value)
+    small_host.upload(gm)
+    gm.alloc_state(1, 2)
+    gm.step([1])
+    gm.step([2])
+    with pytest.raises(anehip.AnehipError) as e:
+        gm.step([3])
+    assert e.value.code == -7
+    with pytest.raises(anehip.AnehipError) as e:
+        gm.step([1, 2])
+    assert e.value.code == -2
+    with pytest.raises(anehip.AnehipError) as e:
+        gm.upload_quant(0, anehip.T["QKV"], np.zeros(10, np.uint8), 768, 256)
+    assert e.value.code == -2
+    gm.close()
+
+
+def test_q4_0_model(small_host):
+    host = HostModel(anehip.Spec(**SMALL), seed=4, ggml_type=2)
+    gm = _model(host, 1, 16)
+    oseq = host.seq(16)
+    for t in (3, 999, 0, 500):
+        assert max(rel_errs(gm.step([t])[0], oseq.forward(t))) <= TOL
+    gm.close()
+
+
+# ---------------------------------------------- Qwen3.5-2B shape (config 4) --
+
+@pytest.fixture(scope="module")
+def big_host():
+    return HostModel(anehip.Spec(), seed=11)
+
+
+@pytest.mark.parametrize("ctx_len,batch", [(1024, 1), (8192, 1), (32768, 1), (1024, 32)])
+def test_qwen35_2b_shape_step(big_host, ctx_len, batch):
+    """Random-init 24-layer Qwen3.5-2B shape, Q8_0 weights, fp16 KV cache
+    filled with N(0,1) at positions < ctx-1, DeltaNet states N(0, 0.01)
+    (windows N(0,1)); one step at pos = ctx-1 vs the oracle."""
+    spec = big_host.spec
+    gm = _model(big_host, batch, ctx_len)
+    for l in range(spec.n_layers):
+        if spec.layer_types[l] == anehip.LAYER_DELTANET:
+            p, n = gm.state_ptr(l, 0)
+            gm.fill_random(p, n // 4, 0, 100 + l, 0.0, 1.0)
+            p, n = gm.state_ptr(l, 1)
+            gm.fill_random(p, n // 4, 0, 200 + l, 0.0, 0.01)
+        else:
+            for which in (2, 3):
+                p, n = gm.state_ptr(l, which)
+                gm.fill_random(p, n // 2, 0, 300 + 10 * l + which, 0.0, 1.0, f16=True)
+    for b in range(batch):
+        gm.set_pos(b, ctx_len - 1)
+    toks = oracle.randint(12, ctx_len, batch, spec.vocab_size)
+    check = sorted({0, batch - 1})
+    seqs = {}
+    for b in check:
+        seqs[b] = big_host.seq(ctx_len)
+        copy_state_to_oracle(gm, seqs[b], b)
+    g = gm.step(toks)
+    for b in check:
+        r = seqs[b].forward(int(toks[b]))
+        l2, mx = rel_errs(g[b], r)
+        print(f"2B ctx={ctx_len} B={batch} seq {b}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+        assert l2 <= TOL and mx <= TOL
+        seqs[b].close()
+    gm.close()
