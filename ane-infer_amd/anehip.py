@@ -57,6 +57,7 @@ def lib():
             "anehip_h2d": (C.c_int, [vp, vp, vp, sz]),
             "anehip_d2h": (C.c_int, [vp, vp, vp, sz]),
             "anehip_dev_memset": (C.c_int, [vp, vp, C.c_int, sz]),
+            "anehip_d2d": (C.c_int, [vp, vp, vp, sz]),
             "anehip_timer_start": (C.c_int, [vp]),
             "anehip_timer_stop": (C.c_int, [vp, C.POINTER(f32)]),
             "anehip_quant_gemm": (C.c_int, [vp, u32, vp, u32, u32, vp, u32, vp]),
@@ -172,6 +173,18 @@ class Context:
         self._check(lib().anehip_timer_stop(self.h, C.byref(ms)))
         return ms.value
 
+    def fill_random(self, dptr, n, dist, seed, a, b, f16=False):
+        """dist 0: N(a, b^2), dist 1: U(a, b); fp32 or fp16 values."""
+        dptr = dptr.ptr if isinstance(dptr, DevBuf) else dptr
+        self._check(lib().anehip_fill_random(self.h, C.c_void_p(dptr), n, dist, 1 if f16 else 0, seed, a, b))
+
+    def quantize(self, ggml_type, w_f32, m, n, out):
+        ptr = lambda b: b.ptr if isinstance(b, DevBuf) else b
+        self._check(lib().anehip_quantize(self.h, ggml_type, C.c_void_p(ptr(w_f32)), m, n, C.c_void_p(ptr(out))))
+
+    def d2d(self, dst, src, nbytes):
+        self._check(lib().anehip_d2d(self.h, C.c_void_p(dst), C.c_void_p(src), nbytes))
+
     def call(self, name, *args):
         """Calls anehip_<name>(ctx, *args); DevBuf arguments pass their device pointer."""
         conv = [C.c_void_p(a.ptr) if isinstance(a, DevBuf) else a for a in args]
@@ -278,9 +291,6 @@ class Model(Context):
         p, n = C.c_void_p(), C.c_size_t()
         self._check(lib().anehip_tensor_ptr(self.h, layer, kind, ggml_type, C.byref(p), C.byref(n)))
         return p.value, n.value
-
-    def fill_random(self, dptr, n, dist, seed, a, b, f16=False):
-        self._check(lib().anehip_fill_random(self.h, C.c_void_p(dptr), n, dist, 1 if f16 else 0, seed, a, b))
 
     def randomize(self, seed: int = 0, ggml_type: int = Q8_0):
         """Random-init every tensor on the device (seeded; see F32_RECIPE)."""

@@ -77,8 +77,10 @@ int ensure_workspace(anehip_ctx *ctx, size_t floats, size_t counters);
 int launch_quant_gemm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w,
                       uint32_t m, uint32_t n, const float *x, uint32_t batch, float *y);
 int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
+// xsplit: device scratch of batch * n floats (x split into fp16 hi / lo
+// planes for the MFMA path); may be null when batch == 1.
 int launch_gemm_raw(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
-                    uint32_t n, const float *x, uint32_t batch, float *out, int ksplit);
+                    uint32_t n, const float *x, uint32_t batch, float *out, int ksplit, void *xsplit);
 int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, float *y, size_t count,
                         int ksplit);
 

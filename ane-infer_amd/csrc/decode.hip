@@ -70,6 +70,7 @@ struct Model {
     // scratch
     float *x = nullptr, *xn = nullptr, *mixbuf = nullptr, *heads = nullptr, *normed = nullptr;
     float *attn_out = nullptr, *h = nullptr, *part = nullptr, *logits = nullptr, *attn_part = nullptr;
+    float *xsplit = nullptr;  // fp16 hi/lo planes of a GEMM input (batch > 1)
     void *argmax_ws = nullptr;
     // graph
     hipGraph_t graph = nullptr;
@@ -105,12 +106,13 @@ void free_state(Model *M) {
         L.kc = L.vc = nullptr;
     }
     void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->x, M->xn, M->mixbuf, M->heads, M->normed,
-                    M->attn_out, M->h, M->part, M->logits, M->attn_part, M->argmax_ws};
+                    M->attn_out, M->h, M->part, M->logits, M->attn_part, M->argmax_ws, M->xsplit};
     for (void *p : bufs) free_ptr(p);
     if (M->h_tokens) (void)hipHostFree(M->h_tokens);
     M->d_pos = M->d_tokens = M->d_sampled = M->h_tokens = nullptr;
     M->x = M->xn = M->mixbuf = M->heads = M->normed = M->attn_out = M->h = M->part = M->logits = nullptr;
     M->attn_part = nullptr;
+    M->xsplit = nullptr;
     M->argmax_ws = nullptr;
     M->batch = M->max_seq = 0;
     M->host_pos.clear();
@@ -276,9 +278,9 @@ int enqueue_step(anehip_ctx *ctx, Model *M, hipStream_t s) {
         // mixer input projections (stacked), final values in mixbuf [B][rows_in]
         int ks = gemm_ksplit(ctx, rows_in, d);
         if (ks == 1) {
-            TRY(launch_gemm_raw(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, M->xn, B, M->mixbuf, 1));
+            TRY(launch_gemm_raw(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, M->xn, B, M->mixbuf, 1, M->xsplit));
         } else {
-            TRY(launch_gemm_raw(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, M->xn, B, M->part, ks));
+            TRY(launch_gemm_raw(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, M->xn, B, M->part, ks, M->xsplit));
             TRY(launch_sum_partials(ctx, s, M->part, M->mixbuf, (size_t)B * rows_in, ks));
         }
         const float *mix_x;
@@ -300,23 +302,23 @@ int enqueue_step(anehip_ctx *ctx, Model *M, hipStream_t s) {
         }
         // mixer output projection + residual + post-attention RMSNorm
         ks = gemm_ksplit(ctx, (uint32_t)d, mix_cols);
-        TRY(launch_gemm_raw(ctx, s, L.mix_out.type, L.mix_out.d, (uint32_t)d, mix_cols, mix_x, B, M->part, ks));
+        TRY(launch_gemm_raw(ctx, s, L.mix_out.type, L.mix_out.d, (uint32_t)d, mix_cols, mix_x, B, M->part, ks, M->xsplit));
         TRY(launch_residual_rmsnorm(ctx, s, B, d, M->x, M->part, ks, L.post_attn_norm, M->xn, eps));
         // FFN: stacked gate/up + SiLU-mul, down + residual + next RMSNorm
         ks = gemm_ksplit(ctx, 2 * (uint32_t)F, d);
-        TRY(launch_gemm_raw(ctx, s, L.ffn_gu.type, L.ffn_gu.d, 2 * (uint32_t)F, d, M->xn, B, M->part, ks));
+        TRY(launch_gemm_raw(ctx, s, L.ffn_gu.type, L.ffn_gu.d, 2 * (uint32_t)F, d, M->xn, B, M->part, ks, M->xsplit));
         TRY(launch_silu_mul_stacked(ctx, s, B, F, M->part, ks, M->h));
         ks = gemm_ksplit(ctx, (uint32_t)d, F);
-        TRY(launch_gemm_raw(ctx, s, L.ffn_down.type, L.ffn_down.d, (uint32_t)d, F, M->h, B, M->part, ks));
+        TRY(launch_gemm_raw(ctx, s, L.ffn_down.type, L.ffn_down.d, (uint32_t)d, F, M->h, B, M->part, ks, M->xsplit));
         const float *next_norm = l + 1 < nl ? M->layers[l + 1].attn_norm : M->final_norm;
         TRY(launch_residual_rmsnorm(ctx, s, B, d, M->x, M->part, ks, next_norm, M->xn, eps));
     }
     // lm_head + greedy sample + position advance
     int ks = gemm_ksplit(ctx, D.vocab_size, d);
     if (ks == 1) {
-        TRY(launch_gemm_raw(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, M->xn, B, M->logits, 1));
+        TRY(launch_gemm_raw(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, M->xn, B, M->logits, 1, M->xsplit));
     } else {
-        TRY(launch_gemm_raw(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, M->xn, B, M->part, ks));
+        TRY(launch_gemm_raw(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, M->xn, B, M->part, ks, M->xsplit));
         TRY(launch_sum_partials(ctx, s, M->part, M->logits, (size_t)B * D.vocab_size, ks));
     }
     TRY(launch_argmax(ctx, s, B, D.vocab_size, M->logits, M->argmax_ws, M->d_sampled));
@@ -632,6 +634,7 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     r = r ? r : alloc((void **)&M->normed, batch * d * sizeof(float));
     r = r ? r : alloc((void **)&M->attn_out, batch * (qd ? qd : 1) * sizeof(float));
     r = r ? r : alloc((void **)&M->h, batch * F * sizeof(float));
+    r = r ? r : alloc((void **)&M->xsplit, batch * (F > d ? F : d) * sizeof(float));
     r = r ? r : alloc((void **)&M->part, part_floats(ctx, M) * sizeof(float));
     r = r ? r : alloc((void **)&M->logits, batch * (size_t)D.vocab_size * sizeof(float));
     r = r ? r : alloc(&M->argmax_ws, argmax_workspace_bytes((int)batch));

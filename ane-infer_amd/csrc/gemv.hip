@@ -197,6 +197,190 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_tiled(const uin
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small-batch GEMM on MFMA (batch 2..32).  Weights are exact in fp16 (int8 or
+// nibble - 8); each fp32 activation is split into fp16 hi + lo = x to ~2^-22
+// relative, so two v_mfma_f32_16x16x32_f16 per (16 rows x 32 columns x 16
+// batch) tile give fp32-accurate block sums, which are scaled by the block's
+// fp16 scale in fp32 and accumulated: the same per-block order as
+// compute_row (q8_gemv.rs:234-242).  One K=32 MFMA step is exactly one quant
+// block.
+//
+// Lane layout of v_mfma_f32_16x16x32_f16 (checked on gfx950): A[i][k] in lane
+// i + 16*(k/8), element k%8; B[k][j] in lane j + 16*(k/8), element k%8;
+// D[i][j] in lane j + 16*(i/4), element i%4.
+// ---------------------------------------------------------------------------
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// fp32 x[batch][n] -> fp16 planes hi[batch][n], lo[batch][n] with hi + lo ~= x.
+__global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ x, _Float16 *__restrict__ hi,
+                                                     _Float16 *__restrict__ lo, size_t count) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= count) return;
+    const float v = x[i];
+    const _Float16 h = (_Float16)v;
+    hi[i] = h;
+    lo[i] = (_Float16)(v - (float)h);
+}
+
+// 8 weights of one row of one block, as fp16, from the LDS tile row `wl`
+// (u32 words of the row's super-block segment): quant bytes 8g..8g+7 of block
+// `blk` (Q8_0: int8; Q4_0: element k < 16 is the low nibble of byte k, k >= 16
+// the high nibble of byte k - 16, so group g reads bytes 8(g%2).. and nibble
+// g/2).  ODD = blk % 2, which fixes the byte alignment of the quants: blocks
+// are 34 / 18 bytes, so odd blocks' quants start on a 4-byte boundary and even
+// blocks' 2 bytes past one.
+template <uint32_t T, int ODD>
+__device__ __forceinline__ f16x8 w_frag(const uint32_t *wl, int blk, int g) {
+    constexpr int kBB = QTraits<T>::kBlockBytes;
+    const int off = blk * kBB + 2 + (T == ANEHIP_GGML_Q8_0 ? 8 * g : 8 * (g & 1));
+    const int w0 = off >> 2;
+    uint32_t d0, d1;
+    if constexpr (ODD) {
+        d0 = wl[w0];
+        d1 = wl[w0 + 1];
+    } else {
+        const uint32_t x0 = wl[w0], x1 = wl[w0 + 1], x2 = wl[w0 + 2];
+        d0 = __builtin_amdgcn_alignbyte(x1, x0, 2);
+        d1 = __builtin_amdgcn_alignbyte(x2, x1, 2);
+    }
+    f16x8 a;
+    if constexpr (T == ANEHIP_GGML_Q8_0) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            a[e] = (_Float16)(int)(int8_t)(d0 >> (8 * e));
+            a[4 + e] = (_Float16)(int)(int8_t)(d1 >> (8 * e));
+        }
+    } else {
+        const int sh = (g >> 1) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            a[e] = (_Float16)((int)((d0 >> (8 * e + sh)) & 15u) - 8);
+            a[4 + e] = (_Float16)((int)((d1 >> (8 * e + sh)) & 15u) - 8);
+        }
+    }
+    return a;
+}
+
+template <uint32_t T>
+__device__ __forceinline__ float blk_scale(const uint32_t *wl, int blk) {
+    return half_at(wl, blk * QTraits<T>::kBlockBytes);
+}
+
+// grid = (row tiles of 64, K splits); 4 waves per workgroup, as the GEMV.
+// NT = 16-wide batch tiles (1: batch <= 16, 2: batch <= 32).  xh / xl: fp16
+// planes [batch][n].  Output as quant_gemm_tiled.
+//
+// Operands: A = activations (16 batch rows x 32 columns), B = weights (32
+// columns x 16 weight rows), so D[b][r] = sum_k x[b][k] W[r][k]; a lane's four
+// D values share one weight row and therefore one block scale.
+template <uint32_t T, int NT>
+__global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint8_t *__restrict__ W,
+                                                                     const _Float16 *__restrict__ xh,
+                                                                     const _Float16 *__restrict__ xl,
+                                                                     float *__restrict__ out, int m, int n,
+                                                                     int batch, int sb_per_split,
+                                                                     size_t split_stride) {
+    constexpr int V = QTraits<T>::kSbVec;
+    __shared__ u32x4 lds[kWavesPerWg][V * kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int tile = blockIdx.x;
+    const int ks = blockIdx.y;
+    const int nsb = n >> 8;
+    const size_t row_bytes = (size_t)nsb * QTraits<T>::kSbBytes;
+    const int row0 = tile * kWave;
+    const int sb_begin = ks * sb_per_split;
+    const int sb_end = min(nsb, sb_begin + sb_per_split);
+    const int li = lane & 15;  // A row (batch) / B column (weight row) within a 16 tile
+    const int g = lane >> 4;   // k group (8 columns) / D row group
+
+    f32x4 acc[4][NT];
+#pragma unroll
+    for (int rs = 0; rs < 4; rs++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[rs][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 regs[V];
+    uint32_t off[V];
+    tile_offsets<T>(off, (uint32_t)row_bytes, m - row0, lane);
+    const uint8_t *tile_base = W + (size_t)row0 * row_bytes;
+    const uint32_t *lds_words = reinterpret_cast<const uint32_t *>(lds[wave]);
+    constexpr int kSegWords = QTraits<T>::kSbBytes / 4;
+
+    int sb = sb_begin + wave;
+    if (sb < sb_end) load_tile<T>(regs, tile_base + (size_t)sb * QTraits<T>::kSbBytes, off);
+    for (; sb < sb_end; sb += kWavesPerWg) {
+        stage_tile<T>(regs, lds[wave], lane);
+        if (sb + kWavesPerWg < sb_end)
+            load_tile<T>(regs, tile_base + (size_t)(sb + kWavesPerWg) * QTraits<T>::kSbBytes, off);
+        // blocks in pairs (even, odd): a runtime loop bounds the live registers
+#pragma unroll 1
+        for (int bp = 0; bp < 4; bp++)
+#pragma unroll
+        for (int odd = 0; odd < 2; odd++) {
+            const int blk = 2 * bp + odd;
+            // A fragments: x[b = li + 16 nt][sb*256 + 32 blk + 8 g + e]
+            f16x8 ah[NT], al[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int b = li + 16 * nt;
+                if (b < batch) {
+                    const size_t xo = (size_t)b * n + (size_t)sb * 256 + 32 * blk + 8 * g;
+                    ah[nt] = *reinterpret_cast<const f16x8 *>(xh + xo);
+                    al[nt] = *reinterpret_cast<const f16x8 *>(xl + xo);
+                } else {
+                    ah[nt] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                    al[nt] = ah[nt];
+                }
+            }
+#pragma unroll
+            for (int rs = 0; rs < 4; rs++) {
+                const uint32_t *wl = lds_words + (rs * 16 + li) * kSegWords;
+                const f16x8 bw = odd ? w_frag<T, 1>(wl, blk, g) : w_frag<T, 0>(wl, blk, g);
+                const float d = blk_scale<T>(wl, blk);
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[nt], bw, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[nt], bw, c, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[rs][nt][r] = fmaf(c[r], d, acc[rs][nt][r]);
+                }
+            }
+        }
+        wave_sync_lds();
+    }
+    // reduce the 4 waves through LDS (the staging buffer is free now)
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(&lds[0][0]);  // [4 waves][4 rs][NT][4][64]
+    constexpr int per = 4 * NT * 4;
+#pragma unroll
+    for (int rs = 0; rs < 4; rs++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[((wave * per) + (rs * NT + nt) * 4 + r) * kWave + lane] = acc[rs][nt][r];
+    __syncthreads();
+    if (wave != 0) return;
+    float *dst = out + (size_t)ks * split_stride;
+#pragma unroll
+    for (int rs = 0; rs < 4; rs++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int idx = (rs * NT + nt) * 4 + r;
+                float sum = red[idx * kWave + lane];
+#pragma unroll
+                for (int v = 1; v < kWavesPerWg; v++) sum += red[(v * per + idx) * kWave + lane];
+                const int row = row0 + rs * 16 + li;
+                const int b = 16 * nt + 4 * g + r;
+                if (row < m && b < batch) dst[(size_t)b * m + row] = sum;
+            }
+}
+
 // y[i] = sum over k of part[k][i], k ascending (deterministic).
 __global__ __launch_bounds__(256) void sum_partials(const float *__restrict__ part, float *__restrict__ y,
                                                    size_t count, int ksplit) {
@@ -230,19 +414,29 @@ int launch_tiled(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
     return ANEHIP_OK;
 }
 
+template <uint32_t T, int NT>
+int launch_mfma(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const _Float16 *xh,
+                const _Float16 *xl, uint32_t batch, float *out, size_t split_stride, int ksplit) {
+    const int tiles = (int)((m + kWave - 1) / kWave);
+    const int per = (int)(n / 256) / ksplit;
+    hipLaunchKernelGGL((quant_gemm_mfma<T, NT>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
+                       static_cast<const uint8_t *>(w), xh, xl, out, (int)m, (int)n, (int)batch, per, split_stride);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
 template <uint32_t T>
 int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
-                 uint32_t batch, float *out, int ksplit) {
+                 uint32_t batch, float *out, int ksplit, _Float16 *xsplit) {
     const size_t split_stride = (size_t)batch * m;
     if (batch == 1) return launch_tiled<T, 1>(ctx, stream, w, m, n, x, 1, out, split_stride, ksplit);
-    // small batches: groups of up to 4 rows of x per pass over W (VALU path)
-    for (uint32_t b0 = 0; b0 < batch; b0 += 4) {
-        uint32_t nb = batch - b0 < 4 ? batch - b0 : 4;
-        int rc = launch_tiled<T, 4>(ctx, stream, w, m, n, x + (size_t)b0 * n, nb, out + (size_t)b0 * m, split_stride,
-                                    ksplit);
-        if (rc) return rc;
-    }
-    return ANEHIP_OK;
+    // batch 2..32: split x into fp16 hi/lo planes, then the MFMA kernel
+    const size_t count = (size_t)batch * n;
+    _Float16 *xh = xsplit, *xl = xsplit + count;
+    hipLaunchKernelGGL(split_x_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, x, xh, xl, count);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    if (batch <= 16) return launch_mfma<T, 1>(ctx, stream, w, m, n, xh, xl, batch, out, split_stride, ksplit);
+    return launch_mfma<T, 2>(ctx, stream, w, m, n, xh, xl, batch, out, split_stride, ksplit);
 }
 
 }  // namespace
@@ -254,9 +448,12 @@ int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
 }
 
 int launch_gemm_raw(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,
-                    const float *x, uint32_t batch, float *out, int ksplit) {
-    if (ggml_type == ANEHIP_GGML_Q8_0) return dispatch_raw<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, x, batch, out, ksplit);
-    return dispatch_raw<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, x, batch, out, ksplit);
+                    const float *x, uint32_t batch, float *out, int ksplit, void *xsplit) {
+    _Float16 *xs = static_cast<_Float16 *>(xsplit);
+    if (batch > 1 && !xs) return set_error(ctx->err, ANEHIP_EINVAL, "gemm: batch > 1 needs an x split buffer");
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        return dispatch_raw<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, x, batch, out, ksplit, xs);
+    return dispatch_raw<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, x, batch, out, ksplit, xs);
 }
 
 int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, float *y, size_t count, int ksplit) {
@@ -269,11 +466,15 @@ int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, 
 int launch_quant_gemm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                       uint32_t n, const float *x, uint32_t batch, float *y) {
     const int ksplit = gemm_ksplit(ctx, m, n);
-    if (ksplit == 1) return launch_gemm_raw(ctx, stream, ggml_type, w, m, n, x, batch, y, 1);
     const size_t count = (size_t)batch * m;
-    int rc = ensure_workspace(ctx, (size_t)ksplit * count, 0);
+    // workspace: [ksplit partials][x hi/lo planes (2 * batch * n halves)]
+    const size_t part = ksplit > 1 ? (size_t)ksplit * count : 0;
+    const size_t xs_floats = batch > 1 ? (size_t)batch * n : 0;
+    int rc = ensure_workspace(ctx, part + xs_floats, 0);
     if (rc) return rc;
-    rc = launch_gemm_raw(ctx, stream, ggml_type, w, m, n, x, batch, ctx->ws.partial, ksplit);
+    void *xs = batch > 1 ? static_cast<void *>(ctx->ws.partial + part) : nullptr;
+    if (ksplit == 1) return launch_gemm_raw(ctx, stream, ggml_type, w, m, n, x, batch, y, 1, xs);
+    rc = launch_gemm_raw(ctx, stream, ggml_type, w, m, n, x, batch, ctx->ws.partial, ksplit, xs);
     if (rc) return rc;
     return launch_sum_partials(ctx, stream, ctx->ws.partial, y, count, ksplit);
 }

@@ -183,6 +183,13 @@ int anehip_dev_memset(anehip_ctx *ctx, void *dst, int value, size_t nbytes) {
     return ANEHIP_OK;
 }
 
+int anehip_d2d(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes) {
+    if (!ctx || (!dst && nbytes) || (!src && nbytes)) return set_error(ctx ? ctx->err : global_error(), ANEHIP_EINVAL, "d2d: bad argument");
+    if (!nbytes) return ANEHIP_OK;
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return ANEHIP_OK;
+}
+
 int anehip_timer_start(anehip_ctx *ctx) {
     if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "timer_start: ctx is NULL");
     ANEHIP_HIP_TRY(ctx->err, hipEventRecord(ctx->ev_start, ctx->stream));

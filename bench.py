@@ -1,23 +1,25 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X decode-path kernels (one GPU).
+"""Benchmark of the MI355X decode path (one GPU).  Prints ONE JSON line.
 
-Prints ONE JSON line.  Workload: the Q8_0 GEMV /
-small-batch GEMM sweep over the shapes [6144 x 2048], [2048 x 6144] and
-[151936 x 2048] with batch M in {1, 4, 16, 32}.  One "step" is one pass over
-the 12 (shape, M) points; `value` is the whole sweep's algorithmic bytes per
-second (weights + activations in + outputs), with inputs resident in HBM.
+Workload for `value`: the Q8_0 GEMV / small-batch
+GEMM sweep over the shapes [6144 x 2048], [2048 x 6144], [151936 x 2048] with
+batch M in {1, 4, 16, 32}.  One "step" is one pass over the 12 (shape, M)
+points; `value` is the sweep's algorithmic bytes (weights once + fp32
+activations in + fp32 outputs) per second, inputs resident in HBM.  Weights
+are rotated over enough distinct copies (> 512 MiB per shape) that the 256 MiB
+MALL cannot serve repeated reads.
 
-Weights are rotated over enough distinct copies (> 512 MiB per shape) that the
-256 MiB MALL cannot serve repeated reads.  Timing uses HIP events recorded on
-the library's own stream (anehip_timer_start/stop), around exactly `--steps`
-steps after `--warmup` untimed steps, with a stream synchronisation on both
-sides.
+`decode` reports configs[4]: the full random-init Qwen3.5-2B-shape Q8_0 decode
+step (24 layers, fp16 KV cache) at batch 1 and 32 and context 1k / 8k / 32k,
+as tokens/s of greedy decoding with on-device token feedback (one captured
+hipGraph per step).
 
-The `roofline` object is for the dominant kernel (the lm_head GEMV, M = 1):
-achieved = its algorithmic bytes per launch / its average launch duration
-(HIP events over a run of back-to-back launches).  `cpu_baseline` times the
-oracle's row-parallel restatement of the reference's rayon q8_gemv on this
-host over a bounded sample (same byte formula).
+Timing: HIP events recorded on the library's own stream (anehip_timer_*),
+around exactly `--steps` steps after `--warmup` untimed steps, with a stream
+synchronisation on both sides.  All GPU inputs are generated on the device
+(seeded fill + on-device quantiser); the CPU oracle is used only by the
+`cpu_baseline` leg, which times the row-parallel restatement of the
+reference's rayon q8_gemv and CPU decode on this host.
 """
 from __future__ import annotations
 
@@ -31,41 +33,58 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "ane-infer_amd"))
-sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 HBM_PEAK_GBS = 8000.0
 SHAPES = [(6144, 2048), (2048, 6144), (151936, 2048)]
 BATCHES = [1, 4, 16, 32]
 MALL_DEFEAT_BYTES = 512 << 20
 Q8 = 8
+DECODE_POINTS = [(1, 1024), (1, 8192), (1, 32768), (32, 1024), (32, 8192), (32, 32768)]
+# algorithmic bytes of one decode step: every weight once, KV rows read, DeltaNet
+# state read + written (S and the 4-wide conv window), per sequence
+DECODE_WEIGHT_BYTES = 18 * 62_459_904 + 6 * 55_705_600 + 330_612_736
+KV_BYTES_PER_POS = 6 * 2 * 2 * 256 * 2
+DN_STATE_BYTES = 18 * (2 * 16 * 128 * 128 * 4 + 2 * 6144 * 4 * 4)
 
 
 def algo_bytes(m: int, n: int, batch: int) -> int:
-    """Weights once + fp32 activations in + fp32 outputs."""
     return m * (n // 32) * 34 + 4 * batch * (n + m)
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--decode-steps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of each CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only run the roofline kernel (lm_head GEMV, M=1) back to back, for rocprofv3")
+    ap.add_argument("--decode-only", default=None,
+                    help="only run decode points, e.g. '1:1024,32:1024' (batch:ctx), and print their line")
     return ap.parse_args()
 
 
 class Shape:
-    def __init__(self, ctx, oracle, m, n, seed):
+    """One sweep shape: Q8_0 weights generated and quantised on the device,
+    replicated into `copies` distinct buffers."""
+
+    def __init__(self, ctx, m, n, seed):
         self.m, self.n = m, n
-        self.w_host = oracle.gen_quant(Q8, seed, m, m, n, std=0.02)
-        self.wbytes = self.w_host.nbytes
+        self.wbytes = m * (n // 32) * 34
         self.copies = max(2, -(-MALL_DEFEAT_BYTES // self.wbytes))
         self.w = ctx.alloc(self.wbytes * self.copies)
-        for c in range(self.copies):
-            self.w.upload(self.w_host, offset=c * self.wbytes)
-        self.x_host = oracle.normal(seed, 7, 32 * n).reshape(32, n)
-        self.x = ctx.to_device(self.x_host)
+        tmp = ctx.alloc(m * n * 4)
+        ctx.fill_random(tmp, m * n, 0, seed, 0.0, 0.02)
+        ctx.quantize(Q8, tmp, m, n, self.w.ptr)
+        for c in range(1, self.copies):
+            ctx.d2d(self.w.ptr + c * self.wbytes, self.w.ptr, self.wbytes)
+        ctx.sync()
+        tmp.free()
+        self.x = ctx.alloc(32 * n * 4)
+        ctx.fill_random(self.x, 32 * n, 0, seed + 1, 0.0, 1.0)
         self.y = ctx.alloc(32 * m * 4)
         self.next = 0
 
@@ -91,23 +110,73 @@ def time_kernel(ctx, s, batch, launches):
     return ctx.timer_stop() / launches
 
 
-def cpu_baseline(oracle, shapes, budget_s):
-    """Row-parallel CPU GEMV (the reference's rayon path restated) on the config-1
-    shapes at M = 1, repeated until the time budget is used."""
+def bench_decode(anehip, steps, warmup, points=DECODE_POINTS):
+    """Greedy decode tok/s of the random-init Qwen3.5-2B shape at each (batch, ctx)."""
+    spec = anehip.Spec()
+    gm = anehip.Model(spec)
+    gm.randomize(seed=1)
+    out = {}
+    for batch, ctx_len in points:
+        gm.alloc_state(batch, ctx_len)
+        for l in range(spec.n_layers):
+            if spec.layer_types[l] == anehip.LAYER_DELTANET:
+                p, n = gm.state_ptr(l, 0)
+                gm.fill_random(p, n // 4, 0, 100 + l, 0.0, 1.0)
+                p, n = gm.state_ptr(l, 1)
+                gm.fill_random(p, n // 4, 0, 200 + l, 0.0, 0.01)
+            else:
+                for which in (2, 3):
+                    p, n = gm.state_ptr(l, which)
+                    gm.fill_random(p, n // 2, 0, 300 + 10 * l + which, 0.0, 1.0, f16=True)
+        start = ctx_len - 1 - (steps + warmup)
+        for b in range(batch):
+            gm.set_pos(b, start)
+        toks = (np.arange(batch, dtype=np.uint32) * 7919) % spec.vocab_size
+        gm.generate(toks, warmup)
+        gm.sync()
+        gm.timer_start()
+        gm.generate(toks, steps)
+        ms = gm.timer_stop()
+        step_ms = ms / steps
+        step_bytes = DECODE_WEIGHT_BYTES + batch * (ctx_len * KV_BYTES_PER_POS + DN_STATE_BYTES)
+        out[f"B{batch}_ctx{ctx_len}"] = {
+            "tok_s": round(batch * steps / (ms * 1e-3), 1),
+            "ms_per_step": round(step_ms, 3),
+            "algorithmic_GB_per_step": round(step_bytes / 1e9, 3),
+            "effective_GB_s": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
+        }
+    gm.close()
+    return out
+
+
+def cpu_baseline(anehip, ctx, shapes, budget_s, decode):
+    """Oracle (restated reference CPU path) on this host: row-parallel q8_gemv
+    over the config-1 shapes at M = 1, and, if `decode`, qwen35_forward_token
+    tok/s at B = 1 on the same random-init 2B-shape weights."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    if not os.path.exists(oracle.LIB_PATH):
+        oracle.build()
     threads = oracle.max_threads()
+    hosts = []
+    for s in shapes:
+        w = np.empty(s.wbytes, np.uint8)
+        ctx._check(anehip.lib().anehip_d2h(ctx.h, w.ctypes.data, anehip.C.c_void_p(s.w.ptr), s.wbytes))
+        x = s.x.download(np.float32, s.n)
+        hosts.append((s, w, x, np.empty(s.m, np.float32)))
+    for s, w, x, y in hosts:
+        oracle.lib().ao_quant_gemv_mt(Q8, w, s.m, s.n, x, y, threads)
     total_bytes, total_t, reps = 0, 0.0, 0
     t_end = time.perf_counter() + budget_s
-    ys = [np.empty(s.m, np.float32) for s in shapes]
-    for s, y in zip(shapes, ys):  # warm up
-        oracle.lib().ao_quant_gemv_mt(Q8, s.w_host, s.m, s.n, s.x_host[0], y, threads)
     while time.perf_counter() < t_end:
-        for s, y in zip(shapes, ys):
+        for s, w, x, y in hosts:
             t0 = time.perf_counter()
-            oracle.lib().ao_quant_gemv_mt(Q8, s.w_host, s.m, s.n, s.x_host[0], y, threads)
+            oracle.lib().ao_quant_gemv_mt(Q8, w, s.m, s.n, x, y, threads)
             total_t += time.perf_counter() - t0
             total_bytes += algo_bytes(s.m, s.n, 1)
         reps += 1
-    return {
+    res = {
         "value": round(total_bytes / total_t / 1e9, 2),
         "unit": "GB/s",
         "cores": threads,
@@ -115,6 +184,37 @@ def cpu_baseline(oracle, shapes, budget_s):
         "sample": f"{reps} passes of the three config-1 shapes at M=1 (row-parallel q8_gemv restatement, "
                   f"{total_t:.1f} s of GEMV time)",
     }
+    if decode:
+        spec = anehip.Spec()
+        gm = anehip.Model(spec)
+        gm.randomize(seed=1)
+        om = oracle.OracleModel(spec.dim, spec.hidden_dim, spec.n_layers, spec.n_heads, spec.n_kv_heads,
+                                spec.head_dim, spec.vocab_size, spec.ssm_state_size, spec.ssm_conv_kernel,
+                                spec.ssm_group_count, spec.rope_freq_base, spec.rms_norm_eps, spec.layer_types)
+        for layer in [-1] + list(range(spec.n_layers)):
+            for kind, (rows, cols, quant) in spec.shapes(layer).items():
+                arr = gm.download_tensor(layer, kind)
+                if quant:
+                    om.set_quant(layer, kind, arr, rows, cols, Q8)
+                else:
+                    om.set_f32(layer, kind, arr)
+        gm.close()
+        seq = oracle.OracleSeq(om, 1024)
+        seq.forward(1, threads)
+        n_tok, t_dec = 0, 0.0
+        t_end = time.perf_counter() + budget_s
+        tok = 1
+        while time.perf_counter() < t_end or n_tok < 2:
+            t0 = time.perf_counter()
+            tok = oracle.argmax(seq.forward(tok, threads))
+            t_dec += time.perf_counter() - t0
+            n_tok += 1
+        res["decode_tok_s_B1_ctx1k"] = round(n_tok / t_dec, 2)
+        res["decode_sample"] = (f"{n_tok} greedy tokens of qwen35_forward_token (restated) from pos 0, "
+                                f"2B shape, Q8_0, {threads} threads for the GEMVs")
+        seq.close()
+        om.close()
+    return res
 
 
 def main():
@@ -124,16 +224,23 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     import anehip
-    import oracle
 
-    if not os.path.exists(oracle.LIB_PATH):
-        oracle.build()
     rc = anehip.lib().anehip_init()
     if rc != 0:
         raise SystemExit(f"no gfx950 device: {anehip.lib().anehip_last_error(None).decode()}")
+    if args.decode_only:
+        pts = [tuple(int(v) for v in p.split(":")) for p in args.decode_only.split(",")]
+        print(json.dumps({"decode": bench_decode(anehip, args.decode_steps, 3, pts)}), flush=True)
+        return
     ctx = anehip.Context(0)
-    shapes = [Shape(ctx, oracle, m, n, 100 + i) for i, (m, n) in enumerate(SHAPES)]
-    ctx.sync()
+    if args.profile_kernel:
+        lm = Shape(ctx, 151936, 2048, 102)
+        t = time_kernel(ctx, lm, 1, args.steps)
+        print(json.dumps({"kernel": "lm_head GEMV M=1", "avg_launch_us": round(t * 1e3, 2),
+                          "GB/s": round(algo_bytes(lm.m, lm.n, 1) / (t * 1e-3) / 1e9, 1)}), flush=True)
+        ctx.close()
+        return
+    shapes = [Shape(ctx, m, n, 100 + i) for i, (m, n) in enumerate(SHAPES)]
 
     for _ in range(args.warmup):
         run_sweep(ctx, shapes)
@@ -146,14 +253,12 @@ def main():
     sweep_bytes = sum(algo_bytes(s.m, s.n, b) for s in shapes for b in BATCHES)
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # per-point kernel times (HIP events over back-to-back launches)
     points = {}
     for s in shapes:
         for b in BATCHES:
-            launches = 20 if s.m > 100000 else 200
-            t = time_kernel(ctx, s, b, launches)
-            gbs = algo_bytes(s.m, s.n, b) / (t * 1e-3) / 1e9
-            points[f"{s.m}x{s.n}_M{b}"] = {"us": round(t * 1e3, 2), "GB/s": round(gbs, 1)}
+            t = time_kernel(ctx, s, b, 20 if s.m > 100000 else 200)
+            points[f"{s.m}x{s.n}_M{b}"] = {"us": round(t * 1e3, 2),
+                                           "GB/s": round(algo_bytes(s.m, s.n, b) / (t * 1e-3) / 1e9, 1)}
     lm = shapes[2]
     t_lm = time_kernel(ctx, lm, 1, 50)
     lm_bytes = algo_bytes(lm.m, lm.n, 1)
@@ -171,8 +276,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0 weights, fp32 activations/accumulate",
-        "data": "synthetic: seeded N(0,0.02) weights quantised absmax/127, N(0,1) activations",
+        "dtype": "q8_0 weights, fp32 activations and accumulation",
+        "data": "synthetic: seeded N(0,0.02) weights quantised absmax/127 on device, N(0,1) activations",
         "config": {
             "workload": "configs[1]: Q8_0 GEMV/GEMM sweep, shapes 6144x2048, 2048x6144, 151936x2048, "
                         "M in {1,4,16,32}, weights rotated over >512 MiB of copies",
@@ -181,7 +286,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "quant_gemm_rows64<Q8_0,1> lm_head 151936x2048 M=1",
+            "kernel": "quant_gemm_tiled<Q8_0,1> (lm_head 151936x2048, M=1)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -194,8 +299,10 @@ def main():
                                "pct_of_hbm_peak": round(100 * c0["GB/s"] / HBM_PEAK_GBS, 1)},
         "sweep_points": points,
     }
+    if not args.no_decode:
+        out["decode"] = bench_decode(anehip, args.decode_steps, 3)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(oracle, shapes, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(anehip, ctx, shapes, args.cpu_seconds, decode=not args.no_decode)
     ctx.close()
     print(json.dumps(out), flush=True)
 

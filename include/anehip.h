@@ -138,6 +138,7 @@ int anehip_dev_free(anehip_ctx *ctx, void *dptr);
 int anehip_h2d(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes);
 int anehip_d2h(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes);
 int anehip_dev_memset(anehip_ctx *ctx, void *dst, int value, size_t nbytes);
+int anehip_d2d(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes);
 
 /* ---- timing on the context's stream (hipEvent pairs) -------------------- */
 /* Records a start event; anehip_timer_stop records the stop event, waits for
