@@ -126,11 +126,18 @@ int anehip_deltanet_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, cons
         return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_step: null pointer");
     if (!batch || !n_heads) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_step: batch and n_heads must be > 0");
     const int chunk = (int)n_heads * 128;
-    int rc = launch_deltanet_step(ctx, ctx->stream, (int)batch, (int)n_heads, qkv, 3 * chunk, beta_raw, alpha_raw,
-                                  (int)n_heads, conv_w, ssm_a, dt_bias, conv_state, S, out_heads);
+    MixIn mq, mb, ma;
+    mq.p = qkv;
+    mq.stride = 3 * chunk;
+    mb.p = beta_raw;
+    mb.stride = (int)n_heads;
+    ma.p = alpha_raw;
+    ma.stride = (int)n_heads;
+    int rc = launch_deltanet_step(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
+                                  conv_state, S, out_heads);
     if (rc) return rc;
-    return launch_dn_finish(ctx, ctx->stream, (int)batch, (int)n_heads, qkv, 3 * chunk, conv_state, nullptr, nullptr,
-                            0, nullptr, nullptr, 0.0f);
+    return launch_dn_finish(ctx, ctx->stream, (int)batch, (int)n_heads, mq, conv_state, nullptr, 0, nullptr, nullptr,
+                            nullptr, nullptr, 0.0f);
 }
 
 int anehip_gated_rmsnorm(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, const float *heads, const float *gate,
@@ -138,8 +145,11 @@ int anehip_gated_rmsnorm(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, cons
     NEED_CTX(ctx, "gated_rmsnorm");
     if (!heads || !gate || !norm_w || !out || !batch || !n_heads)
         return set_error(ctx->err, ANEHIP_EINVAL, "gated_rmsnorm: bad argument");
-    return launch_dn_finish(ctx, ctx->stream, (int)batch, (int)n_heads, nullptr, 0, nullptr, heads, gate,
-                            (int)n_heads * 128, norm_w, out, eps);
+    MixIn mg;
+    mg.p = gate;
+    mg.stride = (int)n_heads * 128;
+    return launch_dn_finish(ctx, ctx->stream, (int)batch, (int)n_heads, mg, nullptr, heads, 0, norm_w, out, nullptr,
+                            nullptr, eps);
 }
 
 int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads, uint32_t max_seq,
@@ -164,10 +174,12 @@ int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uin
     const int G = (int)(n_heads / n_kv_heads);
     int rc = ensure_workspace(ctx, attn_partial_floats((int)batch, (int)n_kv_heads, (int)max_seq, G), 0);
     if (rc) return rc;
-    const int stride = (int)(n_heads * 2 * 256 + 2 * n_kv_heads * 256);
-    return launch_attention(ctx, ctx->stream, (int)batch, (int)n_heads, (int)n_kv_heads, (int)max_seq, qkv, stride,
-                            q_norm, k_norm, ctx->inv_freq, pos, reinterpret_cast<__half *>(k_cache),
-                            reinterpret_cast<__half *>(v_cache), ctx->ws.partial, out);
+    MixIn mix;
+    mix.p = qkv;
+    mix.stride = (int)(n_heads * 2 * 256 + 2 * n_kv_heads * 256);
+    return launch_attention(ctx, ctx->stream, (int)batch, (int)n_heads, (int)n_kv_heads, (int)max_seq, mix, q_norm,
+                            k_norm, ctx->inv_freq, pos, reinterpret_cast<__half *>(k_cache),
+                            reinterpret_cast<__half *>(v_cache), ctx->ws.partial, out, nullptr, nullptr);
 }
 
 int anehip_argmax(anehip_ctx *ctx, const float *logits, uint32_t rows, uint32_t n, uint32_t *out) {

@@ -45,10 +45,10 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // RMSNorm (eps 1e-6, deltanet.rs:575-598) + RoPE (deltanet.rs:600-623) of one
 // 256-dim head by one wave: lane l owns dims 4l..4l+3 = rotary pairs 2l, 2l+1.
-__device__ __forceinline__ void norm_rope_head(const float *__restrict__ src, const float *__restrict__ w,
+__device__ __forceinline__ void norm_rope_head(const MixIn &mix, int b, int base, const float *__restrict__ w,
                                                const float *__restrict__ inv_freq, uint32_t pos, int lane,
                                                float *dst) {
-    float4 x = *reinterpret_cast<const float4 *>(src + 4 * lane);
+    float4 x = mix.at4(b, base + 4 * lane);
     float ss = wave_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
     const float inv_rms = 1.0f / sqrtf(ss / (float)kHd + 1e-6f);
     float4 wv = *reinterpret_cast<const float4 *>(w + 4 * lane);
@@ -63,11 +63,11 @@ __device__ __forceinline__ void norm_rope_head(const float *__restrict__ src, co
     dst[3] = a2 * s1 + a3 * c1;
 }
 
-// grid = (chunks, n_kv_heads, batch).  qkv: per sequence [q_full | k | v] with
-// row stride `stride` floats; q_full is [n_heads][q(256) | gate(256)].
+// grid = (chunks, n_kv_heads, batch).  mix: per sequence [q_full | k | v]
+// rows (K-split partial slices); q_full is [n_heads][q(256) | gate(256)].
 template <int G>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
-    const float *__restrict__ qkv, int stride, const float *__restrict__ q_norm, const float *__restrict__ k_norm,
+    MixIn mix, const float *__restrict__ q_norm, const float *__restrict__ k_norm,
     const float *__restrict__ inv_freq, const uint32_t *__restrict__ pos_arr, __half *__restrict__ k_cache,
     __half *__restrict__ v_cache, int max_seq, int n_heads, int n_kv, float *__restrict__ part_o,
     float *__restrict__ part_ml) {
@@ -83,7 +83,6 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     const int start = c * kCh;
     if (start >= len) return;  // uniform exit: nothing of this sequence here
     const int nch = gridDim.x;
-    const float *row = qkv + (size_t)b * stride;
     const size_t cache_base = ((size_t)b * n_kv + kvh) * (size_t)max_seq * kHd;
     const bool has_new = (int)pos < start + kCh;  // this chunk holds the current position
 
@@ -91,16 +90,16 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     if (wave < G) {
         const int h = kvh * G + wave;
         float q4[4];
-        norm_rope_head(row + (size_t)h * 2 * kHd, q_norm, inv_freq, pos, lane, q4);
+        norm_rope_head(mix, b, h * 2 * kHd, q_norm, inv_freq, pos, lane, q4);
         *reinterpret_cast<float4 *>(&qs[wave][4 * lane]) = make_float4(q4[0], q4[1], q4[2], q4[3]);
     }
     if (has_new && wave == G % 4) {
         // k: RMSNorm + RoPE, v: as is; both rounded to fp16 and appended
-        const float *kin = row + (size_t)n_heads * 2 * kHd + (size_t)kvh * kHd;
-        const float *vin = row + (size_t)n_heads * 2 * kHd + (size_t)n_kv * kHd + (size_t)kvh * kHd;
+        const int kin = n_heads * 2 * kHd + kvh * kHd;
+        const int vin = n_heads * 2 * kHd + n_kv * kHd + kvh * kHd;
         float k4[4];
-        norm_rope_head(kin, k_norm, inv_freq, pos, lane, k4);
-        float4 v4 = *reinterpret_cast<const float4 *>(vin + 4 * lane);
+        norm_rope_head(mix, b, kin, k_norm, inv_freq, pos, lane, k4);
+        float4 v4 = mix.at4(b, vin + 4 * lane);
         const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -191,13 +190,15 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
 
 // grid = (n_heads, batch), 256 threads (one per dim): merge the chunks of one
 // head with a log-sum-exp rescale, normalise, multiply by sigmoid(gate)
-// (deltanet.rs:667-669).  out: [batch][n_heads * 256].
+// (deltanet.rs:667-669).  out: [batch][n_heads * 256] fp32, or fp16 hi/lo
+// planes out_hi / out_lo when out_hi is not null.
 template <int G>
-__global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float *__restrict__ qkv, int stride,
-                                                                const uint32_t *__restrict__ pos_arr,
+__global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const uint32_t *__restrict__ pos_arr,
                                                                 const float *__restrict__ part_o,
                                                                 const float *__restrict__ part_ml, int nch,
-                                                                int n_heads, int n_kv, float *__restrict__ out) {
+                                                                int n_heads, int n_kv, float *__restrict__ out,
+                                                                _Float16 *__restrict__ out_hi,
+                                                                _Float16 *__restrict__ out_lo) {
     const int d = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int kvh = h / G, hh = h % G;
     const int len = (int)pos_arr[b] + 1;
@@ -212,8 +213,16 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(const float *__r
         num += w * part_o[((base + c) * G + hh) * kHd + d];
         den += w * ml[1];
     }
-    const float g = qkv[(size_t)b * stride + (size_t)h * 2 * kHd + kHd + d];
-    out[(size_t)b * n_heads * kHd + (size_t)h * kHd + d] = (num / den) * (1.0f / (1.0f + expf(-g)));
+    const float g = mix.at(b, h * 2 * kHd + kHd + d);
+    const float v = (num / den) * (1.0f / (1.0f + expf(-g)));
+    const size_t o = (size_t)b * n_heads * kHd + (size_t)h * kHd + d;
+    if (out_hi) {
+        const _Float16 hi = (_Float16)v;
+        out_hi[o] = hi;
+        out_lo[o] = (_Float16)(v - (float)hi);
+    } else {
+        out[o] = v;
+    }
 }
 
 }  // namespace
@@ -225,8 +234,9 @@ size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G) {
 
 // part: workspace of attn_partial_floats() floats.
 int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
-                     const float *qkv, int stride, const float *q_norm, const float *k_norm, const float *inv_freq,
-                     const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out) {
+                     const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
+                     const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,
+                     _Float16 *out_hi, _Float16 *out_lo) {
     const int G = n_heads / n_kv;
     const int nch = (max_seq + kCh - 1) / kCh;
     float *part_o = part;
@@ -234,11 +244,11 @@ int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
     dim3 g1(nch, n_kv, batch), g2(n_heads, batch);
 #define ANEHIP_ATTN_CASE(GG)                                                                                   \
     case GG:                                                                                                   \
-        hipLaunchKernelGGL(attn_partial_kernel<GG>, g1, dim3(kThreads), 0, stream, qkv, stride, q_norm, k_norm, \
+        hipLaunchKernelGGL(attn_partial_kernel<GG>, g1, dim3(kThreads), 0, stream, mix, q_norm, k_norm,        \
                            inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, part_o, part_ml);         \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
-        hipLaunchKernelGGL(attn_combine_kernel<GG>, g2, dim3(kThreads), 0, stream, qkv, stride, pos, part_o,   \
-                           part_ml, nch, n_heads, n_kv, out);                                                  \
+        hipLaunchKernelGGL(attn_combine_kernel<GG>, g2, dim3(kThreads), 0, stream, mix, pos, part_o, part_ml,  \
+                           nch, n_heads, n_kv, out, out_hi, out_lo);                                          \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
         return ANEHIP_OK;
     switch (G) {

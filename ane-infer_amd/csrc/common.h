@@ -68,6 +68,70 @@ namespace anehip {
 // `counters` counters (grown with hipMalloc, cleared once).
 int ensure_workspace(anehip_ctx *ctx, size_t floats, size_t counters);
 
+// How a batch-1 GEMV forms its input vector from what the previous kernels
+// left in memory (the element-wise step is fused into the GEMV's prologue, so
+// it costs no launch of its own).  Each workgroup computes only the slice of
+// the input its K range needs (plus any full-row reduction).
+enum GemvInMode : int {
+    GEMV_IN_PLAIN = 0,     // x
+    GEMV_IN_RMSNORM,       // rmsnorm(x, w)
+    GEMV_IN_RESID_RMSNORM, // r = x + sum_p part[p]; rmsnorm(r, w); r -> x_out
+    GEMV_IN_EMBED_RMSNORM, // r = emb[token] (0 if token >= vocab); rmsnorm(r, w); r -> x_out
+    GEMV_IN_GATED_NORM,    // per-128 head rmsnorm(x, w) * SiLU(gate), gate = sum_p part[p][gate_off..]
+    GEMV_IN_SILU_MUL,      // SiLU(sum_p part[p][k]) * sum_p part[p][n + k]
+};
+
+struct GemvInput {
+    int mode = GEMV_IN_PLAIN;
+    const float *x = nullptr;
+    const float *part = nullptr;  // partial slices, part_stride floats apart
+    int kp = 0;
+    size_t part_stride = 0;
+    const float *w = nullptr;
+    float eps = 0.0f;
+    float *x_out = nullptr;       // new residual stream (written by workgroup (0, 0))
+    const uint32_t *token = nullptr;
+    const float *emb = nullptr;
+    uint32_t vocab = 0;
+    int gate_off = 0;
+    // GATED_NORM only: the q/k conv windows [2n][4] are committed (shift left,
+    // append part rows [0, 2n)) by the workgroups of this launch
+    float *conv_state = nullptr;
+};
+
+// A GEMV output read by a later kernel as kp partial slices: value (b, i) =
+// sum over q < kp of p[q * split + b * stride + i], q ascending.
+struct MixIn {
+    const float *p = nullptr;
+    int kp = 1;
+    size_t split = 0;
+    int stride = 0;
+    // the same slices, starting `off` values into each row
+    MixIn shifted(int off) const {
+        MixIn m = *this;
+        m.p = p + off;
+        return m;
+    }
+    __host__ __device__ __forceinline__ float at(int b, int i) const {
+        const float *q0 = p + (size_t)b * stride + i;
+        float s = q0[0];
+        for (int q = 1; q < kp; q++) s += q0[(size_t)q * split];
+        return s;
+    }
+    __host__ __device__ __forceinline__ float4 at4(int b, int i) const {
+        const float *q0 = p + (size_t)b * stride + i;
+        float4 s = *reinterpret_cast<const float4 *>(q0);
+        for (int q = 1; q < kp; q++) {
+            const float4 v = *reinterpret_cast<const float4 *>(q0 + (size_t)q * split);
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+        return s;
+    }
+};
+
 // ---- kernel launchers (all pointers are device pointers; work is queued on
 // `stream`; they return ANEHIP_OK or set ctx->err) ---------------------------
 
@@ -83,32 +147,46 @@ int launch_gemm_raw(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, con
                     uint32_t n, const float *x, uint32_t batch, float *out, int ksplit, void *xsplit);
 int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, float *y, size_t count,
                         int ksplit);
+// Small-batch GEMM (batch 2..32) on MFMA from fp16 hi/lo input planes
+// [batch][n]; writes out[ks][batch][m].
+int launch_gemm_planes(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
+                       uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit);
+// Batch-1 GEMV whose input is formed by `in` (see GemvInMode); writes
+// out[ks][m] partials (final values if ksplit == 1).
+int launch_gemv_fused(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
+                      uint32_t n, const GemvInput &in, float *out, int ksplit);
 
-// deltanet.hip
-int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const float *qkv,
-                         int qkv_stride, const float *beta_raw, const float *alpha_raw, int ba_stride,
-                         const float *conv_w, const float *ssm_a, const float *dt_bias, float *conv_state,
-                         float *S, float *out);
-int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const float *qkv,
-                     int qkv_stride, float *conv_state, const float *heads, const float *gate, int gate_stride,
-                     const float *norm_w, float *out, float eps);
+// deltanet.hip.  mix: qkv [3*chunk]; beta, alpha: [n_heads] per sequence.
+int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
+                         const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
+                         const float *dt_bias, float *conv_state, float *S, float *out);
+// Commits the q/k conv windows (if conv_state) and, if heads, writes the gated
+// RMSNorm of the heads (gate from mix rows at gate_off) to out (fp32) or, if
+// out_hi, to fp16 hi/lo planes out_hi / out_lo.
+int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
+                     float *conv_state, const float *heads, int gate_off, const float *norm_w, float *out,
+                     _Float16 *out_hi, _Float16 *out_lo, float eps);
 
-// attention.hip
+// attention.hip.  mix per sequence: [q_full | k | v] rows.
 size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G);
 int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
-                     const float *qkv, int stride, const float *q_norm, const float *k_norm,
-                     const float *inv_freq, const uint32_t *pos, __half *k_cache, __half *v_cache,
-                     float *part, float *out);
+                     const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
+                     const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,
+                     _Float16 *out_hi, _Float16 *out_lo);
 
 // elementwise.hip
 int launch_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const float *x, const float *w, float *out,
                    float eps);
+// The next three write their result as fp32 (xn / h) or, when hi is not null,
+// as fp16 hi/lo planes for the small-batch MFMA GEMM.
 int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const uint32_t *tokens,
-                         const float *emb, uint32_t vocab, float *x, const float *w, float *xn, float eps);
+                         const float *emb, uint32_t vocab, float *x, const float *w, float *xn, float eps,
+                         _Float16 *hi = nullptr, _Float16 *lo = nullptr);
 int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
-                            int ksplit, const float *w, float *xn, float eps);
+                            int ksplit, const float *w, float *xn, float eps, _Float16 *hi = nullptr,
+                            _Float16 *lo = nullptr);
 int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit,
-                            float *h);
+                            float *h, _Float16 *hi = nullptr, _Float16 *lo = nullptr);
 int launch_silu_mul(anehip_ctx *ctx, hipStream_t s, float *a, const float *b, size_t n);
 int launch_residual_add(anehip_ctx *ctx, hipStream_t s, float *x, const float *y, size_t n);
 size_t argmax_workspace_bytes(int rows);

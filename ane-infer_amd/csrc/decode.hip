@@ -68,9 +68,12 @@ struct Model {
     uint32_t *d_pos = nullptr, *d_tokens = nullptr, *d_sampled = nullptr;
     uint32_t *h_tokens = nullptr;  // pinned staging
     // scratch
-    float *x = nullptr, *xn = nullptr, *mixbuf = nullptr, *heads = nullptr, *normed = nullptr;
-    float *attn_out = nullptr, *h = nullptr, *part = nullptr, *logits = nullptr, *attn_part = nullptr;
-    float *xsplit = nullptr;  // fp16 hi/lo planes of a GEMM input (batch > 1)
+    float *x0 = nullptr, *x1 = nullptr;                  // residual stream (two buffers, alternating)
+    float *pmix = nullptr, *p0 = nullptr, *p1 = nullptr;  // GEMV outputs as K-split partial slices
+    float *heads = nullptr, *attn_out = nullptr, *logits = nullptr, *attn_part = nullptr;
+    _Float16 *planes = nullptr;  // fp16 hi / lo planes of a GEMM input (batch > 1)
+    size_t plane_len = 0;        // halves per plane
+    size_t part_len = 0;         // floats per partial buffer
     void *argmax_ws = nullptr;
     // graph
     hipGraph_t graph = nullptr;
@@ -105,14 +108,13 @@ void free_state(Model *M) {
         L.conv_state = L.S = nullptr;
         L.kc = L.vc = nullptr;
     }
-    void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->x, M->xn, M->mixbuf, M->heads, M->normed,
-                    M->attn_out, M->h, M->part, M->logits, M->attn_part, M->argmax_ws, M->xsplit};
+    void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->x0,       M->x1,        M->pmix,      M->p0,
+                    M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->planes};
     for (void *p : bufs) free_ptr(p);
     if (M->h_tokens) (void)hipHostFree(M->h_tokens);
     M->d_pos = M->d_tokens = M->d_sampled = M->h_tokens = nullptr;
-    M->x = M->xn = M->mixbuf = M->heads = M->normed = M->attn_out = M->h = M->part = M->logits = nullptr;
-    M->attn_part = nullptr;
-    M->xsplit = nullptr;
+    M->x0 = M->x1 = M->pmix = M->p0 = M->p1 = M->heads = M->attn_out = M->logits = M->attn_part = nullptr;
+    M->planes = nullptr;
     M->argmax_ws = nullptr;
     M->batch = M->max_seq = 0;
     M->host_pos.clear();
@@ -262,67 +264,175 @@ int check_model(anehip_ctx *ctx, Model *M) {
         if (_rc) return _rc;        \
     } while (0)
 
-// Enqueues one decode step for all sequences on `s` (captured or eager).
-int enqueue_step(anehip_ctx *ctx, Model *M, hipStream_t s) {
+// Batch 1: every projection is one GEMV launch whose prologue forms its input
+// (embedding / residual sum + RMSNorm, gated RMSNorm, SiLU-mul) from what the
+// previous kernels left, so a DeltaNet layer is 5 launches (mixer-in GEMV,
+// DeltaNet, ssm_out GEMV, gate/up GEMV, down GEMV) and an attention layer 6.
+int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     const anehip_model_desc &D = M->desc;
-    const int B = (int)M->batch;
-    const int d = (int)D.dim, F = (int)D.hidden_dim, H = (int)D.ssm_group_count, C = 3 * d;
+    const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
+    const uint32_t qd = D.n_heads * D.head_dim;
     const float eps = D.rms_norm_eps;
-    const uint32_t nl = D.n_layers;
-    TRY(launch_embed_rmsnorm(ctx, s, B, d, M->d_tokens, M->embedding, D.vocab_size, M->x,
-                             M->layers[0].attn_norm, M->xn, eps));
-    for (uint32_t l = 0; l < nl; l++) {
+    float *cur = M->x0, *nxt = M->x1;
+    const float *prev_part = nullptr;
+    int prev_kp = 0;
+    for (uint32_t l = 0; l < D.n_layers; l++) {
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
         const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
-        // mixer input projections (stacked), final values in mixbuf [B][rows_in]
-        int ks = gemm_ksplit(ctx, rows_in, d);
-        if (ks == 1) {
-            TRY(launch_gemm_raw(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, M->xn, B, M->mixbuf, 1, M->xsplit));
-        } else {
-            TRY(launch_gemm_raw(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, M->xn, B, M->part, ks, M->xsplit));
-            TRY(launch_sum_partials(ctx, s, M->part, M->mixbuf, (size_t)B * rows_in, ks));
-        }
-        const float *mix_x;
-        uint32_t mix_cols;
+        // 1. mixer input projections, input = RMSNorm(residual)
+        GemvInput in1;
+        in1.mode = l == 0 ? GEMV_IN_EMBED_RMSNORM : GEMV_IN_RESID_RMSNORM;
+        in1.x = cur;
+        in1.part = prev_part;
+        in1.kp = prev_kp;
+        in1.part_stride = d;
+        in1.w = L.attn_norm;
+        in1.eps = eps;
+        in1.x_out = nxt;
+        in1.token = M->d_tokens;
+        in1.emb = M->embedding;
+        in1.vocab = D.vocab_size;
+        const int k1 = gemm_ksplit(ctx, rows_in, d);
+        TRY(launch_gemv_fused(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, in1, M->pmix, k1));
+        std::swap(cur, nxt);
+        MixIn mix;
+        mix.p = M->pmix;
+        mix.kp = k1;
+        mix.split = rows_in;
+        mix.stride = (int)rows_in;
+        // 2. mixer core, 3. output projection (its input formed in the prologue)
+        GemvInput in3;
+        uint32_t cols3;
         if (dn) {
-            const float *qkv = M->mixbuf;
-            TRY(launch_deltanet_step(ctx, s, B, H, qkv, (int)rows_in, qkv + C + d, qkv + C + d + H, (int)rows_in,
+            TRY(launch_deltanet_step(ctx, s, 1, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
                                      L.conv1d, L.ssm_a, L.dt_bias, L.conv_state, L.S, M->heads));
-            TRY(launch_dn_finish(ctx, s, B, H, qkv, (int)rows_in, L.conv_state, M->heads, qkv + C, (int)rows_in,
-                                 L.ssm_norm, M->normed, eps));
-            mix_x = M->normed;
-            mix_cols = (uint32_t)d;
+            in3.mode = GEMV_IN_GATED_NORM;
+            in3.x = M->heads;
+            in3.part = M->pmix;
+            in3.kp = k1;
+            in3.part_stride = rows_in;
+            in3.w = L.ssm_norm;
+            in3.eps = eps;
+            in3.gate_off = (int)C;
+            in3.conv_state = L.conv_state;
+            cols3 = d;
         } else {
-            TRY(launch_attention(ctx, s, B, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, M->mixbuf,
-                                 (int)rows_in, L.q_norm, L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part,
-                                 M->attn_out));
-            mix_x = M->attn_out;
-            mix_cols = D.n_heads * D.head_dim;
+            TRY(launch_attention(ctx, s, 1, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
+                                 L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part, M->attn_out, nullptr,
+                                 nullptr));
+            in3.mode = GEMV_IN_PLAIN;
+            in3.x = M->attn_out;
+            cols3 = qd;
         }
-        // mixer output projection + residual + post-attention RMSNorm
-        ks = gemm_ksplit(ctx, (uint32_t)d, mix_cols);
-        TRY(launch_gemm_raw(ctx, s, L.mix_out.type, L.mix_out.d, (uint32_t)d, mix_cols, mix_x, B, M->part, ks, M->xsplit));
-        TRY(launch_residual_rmsnorm(ctx, s, B, d, M->x, M->part, ks, L.post_attn_norm, M->xn, eps));
-        // FFN: stacked gate/up + SiLU-mul, down + residual + next RMSNorm
-        ks = gemm_ksplit(ctx, 2 * (uint32_t)F, d);
-        TRY(launch_gemm_raw(ctx, s, L.ffn_gu.type, L.ffn_gu.d, 2 * (uint32_t)F, d, M->xn, B, M->part, ks, M->xsplit));
-        TRY(launch_silu_mul_stacked(ctx, s, B, F, M->part, ks, M->h));
-        ks = gemm_ksplit(ctx, (uint32_t)d, F);
-        TRY(launch_gemm_raw(ctx, s, L.ffn_down.type, L.ffn_down.d, (uint32_t)d, F, M->h, B, M->part, ks, M->xsplit));
-        const float *next_norm = l + 1 < nl ? M->layers[l + 1].attn_norm : M->final_norm;
-        TRY(launch_residual_rmsnorm(ctx, s, B, d, M->x, M->part, ks, next_norm, M->xn, eps));
+        const int k3 = gemm_ksplit(ctx, d, cols3);
+        TRY(launch_gemv_fused(ctx, s, L.mix_out.type, L.mix_out.d, d, cols3, in3, M->p0, k3));
+        // 4. FFN gate/up, input = RMSNorm(residual + mixer output)
+        GemvInput in4;
+        in4.mode = GEMV_IN_RESID_RMSNORM;
+        in4.x = cur;
+        in4.part = M->p0;
+        in4.kp = k3;
+        in4.part_stride = d;
+        in4.w = L.post_attn_norm;
+        in4.eps = eps;
+        in4.x_out = nxt;
+        const int k4 = gemm_ksplit(ctx, 2 * F, d);
+        TRY(launch_gemv_fused(ctx, s, L.ffn_gu.type, L.ffn_gu.d, 2 * F, d, in4, M->p1, k4));
+        std::swap(cur, nxt);
+        // 5. FFN down, input = SiLU(gate) * up
+        GemvInput in5;
+        in5.mode = GEMV_IN_SILU_MUL;
+        in5.part = M->p1;
+        in5.kp = k4;
+        in5.part_stride = 2 * F;
+        const int k5 = gemm_ksplit(ctx, d, F);
+        TRY(launch_gemv_fused(ctx, s, L.ffn_down.type, L.ffn_down.d, d, F, in5, M->p0, k5));
+        prev_part = M->p0;
+        prev_kp = k5;
     }
-    // lm_head + greedy sample + position advance
-    int ks = gemm_ksplit(ctx, D.vocab_size, d);
-    if (ks == 1) {
-        TRY(launch_gemm_raw(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, M->xn, B, M->logits, 1, M->xsplit));
+    // lm_head, input = final RMSNorm(residual + last FFN output)
+    GemvInput inf;
+    inf.mode = GEMV_IN_RESID_RMSNORM;
+    inf.x = cur;
+    inf.part = prev_part;
+    inf.kp = prev_kp;
+    inf.part_stride = d;
+    inf.w = M->final_norm;
+    inf.eps = eps;
+    inf.x_out = nxt;
+    const int kf = gemm_ksplit(ctx, D.vocab_size, d);
+    if (kf == 1) {
+        TRY(launch_gemv_fused(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, inf, M->logits, 1));
     } else {
-        TRY(launch_gemm_raw(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, M->xn, B, M->part, ks, M->xsplit));
-        TRY(launch_sum_partials(ctx, s, M->part, M->logits, (size_t)B * D.vocab_size, ks));
+        TRY(launch_gemv_fused(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, inf, M->pmix, kf));
+        TRY(launch_sum_partials(ctx, s, M->pmix, M->logits, D.vocab_size, kf));
     }
-    TRY(launch_argmax(ctx, s, B, D.vocab_size, M->logits, M->argmax_ws, M->d_sampled));
-    hipLaunchKernelGGL(pos_advance_kernel, dim3(1), dim3(64), 0, s, M->d_pos, B);
+    return ANEHIP_OK;
+}
+
+// Batch 2..32: element-wise kernels write the next GEMM's input as fp16 hi/lo
+// planes; projections run on the MFMA GEMM.
+int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
+    const anehip_model_desc &D = M->desc;
+    const int B = (int)M->batch;
+    const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
+    const uint32_t qd = D.n_heads * D.head_dim;
+    const float eps = D.rms_norm_eps;
+    _Float16 *xh = M->planes, *xl = M->planes + M->plane_len;
+    float *x = M->x0;
+    TRY(launch_embed_rmsnorm(ctx, s, B, (int)d, M->d_tokens, M->embedding, D.vocab_size, x, M->layers[0].attn_norm,
+                             nullptr, eps, xh, xl));
+    for (uint32_t l = 0; l < D.n_layers; l++) {
+        Layer &L = M->layers[l];
+        const bool dn = L.type == ANEHIP_LAYER_DELTANET;
+        const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
+        const int k1 = gemm_ksplit(ctx, rows_in, d);
+        TRY(launch_gemm_planes(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, xh, xl, B, M->pmix, k1));
+        MixIn mix;
+        mix.p = M->pmix;
+        mix.kp = k1;
+        mix.split = (size_t)B * rows_in;
+        mix.stride = (int)rows_in;
+        uint32_t cols3;
+        if (dn) {
+            TRY(launch_deltanet_step(ctx, s, B, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
+                                     L.conv1d, L.ssm_a, L.dt_bias, L.conv_state, L.S, M->heads));
+            TRY(launch_dn_finish(ctx, s, B, (int)H, mix, L.conv_state, M->heads, (int)C, L.ssm_norm, nullptr, xh, xl,
+                                 eps));
+            cols3 = d;
+        } else {
+            TRY(launch_attention(ctx, s, B, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
+                                 L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part, nullptr, xh, xl));
+            cols3 = qd;
+        }
+        const int k3 = gemm_ksplit(ctx, d, cols3);
+        TRY(launch_gemm_planes(ctx, s, L.mix_out.type, L.mix_out.d, d, cols3, xh, xl, B, M->p0, k3));
+        TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, nullptr, eps, xh, xl));
+        const int k4 = gemm_ksplit(ctx, 2 * F, d);
+        TRY(launch_gemm_planes(ctx, s, L.ffn_gu.type, L.ffn_gu.d, 2 * F, d, xh, xl, B, M->p1, k4));
+        TRY(launch_silu_mul_stacked(ctx, s, B, (int)F, M->p1, k4, nullptr, xh, xl));
+        const int k5 = gemm_ksplit(ctx, d, F);
+        TRY(launch_gemm_planes(ctx, s, L.ffn_down.type, L.ffn_down.d, d, F, xh, xl, B, M->p0, k5));
+        const float *next_norm = l + 1 < D.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
+        TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k5, next_norm, nullptr, eps, xh, xl));
+    }
+    const int kf = gemm_ksplit(ctx, D.vocab_size, d);
+    if (kf == 1) {
+        TRY(launch_gemm_planes(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, xh, xl, B, M->logits, 1));
+    } else {
+        TRY(launch_gemm_planes(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, xh, xl, B, M->pmix, kf));
+        TRY(launch_sum_partials(ctx, s, M->pmix, M->logits, (size_t)B * D.vocab_size, kf));
+    }
+    return ANEHIP_OK;
+}
+
+// Enqueues one decode step for all sequences on `s` (captured or eager):
+// the projections, greedy argmax of the logits and the position advance.
+int enqueue_step(anehip_ctx *ctx, Model *M, hipStream_t s) {
+    TRY(M->batch == 1 ? enqueue_step_b1(ctx, M, s) : enqueue_step_bn(ctx, M, s));
+    TRY(launch_argmax(ctx, s, (int)M->batch, M->desc.vocab_size, M->logits, M->argmax_ws, M->d_sampled));
+    hipLaunchKernelGGL(pos_advance_kernel, dim3(1), dim3(64), 0, s, M->d_pos, (int)M->batch);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
@@ -622,20 +732,22 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
             r = r ? r : alloc((void **)&L.vc, batch * kvd * max_seq * sizeof(__half));
         }
     }
-    const size_t rows_in = M->rows_dn > M->rows_attn ? M->rows_dn : M->rows_attn;
     const size_t qd = (size_t)D.n_heads * D.head_dim;
+    size_t nmax = d > F ? d : F;
+    if (qd > nmax) nmax = qd;
+    M->plane_len = batch * nmax;
+    M->part_len = part_floats(ctx, M);
     r = r ? r : alloc((void **)&M->d_pos, 64 * sizeof(uint32_t));
     r = r ? r : alloc((void **)&M->d_tokens, 64 * sizeof(uint32_t));
     r = r ? r : alloc((void **)&M->d_sampled, 64 * sizeof(uint32_t));
-    r = r ? r : alloc((void **)&M->x, batch * d * sizeof(float));
-    r = r ? r : alloc((void **)&M->xn, batch * d * sizeof(float));
-    r = r ? r : alloc((void **)&M->mixbuf, batch * rows_in * sizeof(float));
+    r = r ? r : alloc((void **)&M->x0, batch * d * sizeof(float));
+    r = r ? r : alloc((void **)&M->x1, batch * d * sizeof(float));
+    r = r ? r : alloc((void **)&M->pmix, M->part_len * sizeof(float));
+    r = r ? r : alloc((void **)&M->p0, M->part_len * sizeof(float));
+    r = r ? r : alloc((void **)&M->p1, M->part_len * sizeof(float));
     r = r ? r : alloc((void **)&M->heads, batch * d * sizeof(float));
-    r = r ? r : alloc((void **)&M->normed, batch * d * sizeof(float));
     r = r ? r : alloc((void **)&M->attn_out, batch * (qd ? qd : 1) * sizeof(float));
-    r = r ? r : alloc((void **)&M->h, batch * F * sizeof(float));
-    r = r ? r : alloc((void **)&M->xsplit, batch * (F > d ? F : d) * sizeof(float));
-    r = r ? r : alloc((void **)&M->part, part_floats(ctx, M) * sizeof(float));
+    r = r ? r : alloc((void **)&M->planes, 2 * M->plane_len * sizeof(_Float16));
     r = r ? r : alloc((void **)&M->logits, batch * (size_t)D.vocab_size * sizeof(float));
     r = r ? r : alloc(&M->argmax_ws, argmax_workspace_bytes((int)batch));
     if (M->rows_attn) {

@@ -54,13 +54,13 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// grid = (dv / 32, n_heads, batch).  qkv_stride / ba_stride are the row
-// strides (floats) of the per-sequence inputs.
+// grid = (dv / 32, n_heads, batch).  mix / mbeta / malpha: the qkv, beta and
+// alpha projections of each sequence ([3 chunk], [n_heads], [n_heads]), read
+// as K-split partial slices.
 __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
-    const float *__restrict__ qkv, int qkv_stride, const float *__restrict__ beta_raw,
-    const float *__restrict__ alpha_raw, int ba_stride, const float *__restrict__ conv_w,
-    const float *__restrict__ ssm_a, const float *__restrict__ dt_bias, float *__restrict__ conv_state,
-    float *__restrict__ S, float *__restrict__ out, int n_heads) {
+    MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
+    const float *__restrict__ dt_bias, float *__restrict__ conv_state, float *__restrict__ S, float *__restrict__ out,
+    int n_heads) {
     __shared__ float qn[kDk], kn[kDk], vv[kCols];
     __shared__ float red[1][4];
     __shared__ float part[32][kCols];
@@ -71,13 +71,13 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
     const int chunk = n_heads * kDk;  // = dim
     const int C = 3 * chunk;
     const int c0 = slice * kCols;
-    const float *xin = qkv + (size_t)b * qkv_stride;
     float *cs = conv_state + (size_t)b * C * kKsize;
 
-    // 1. conv + SiLU of the head's q (t < 128) and k (t >= 128) channels
+    // 1. conv + SiLU of the head's q (t < 128) and k (t >= 128) channels, from
+    // the old window (committed later by dn_finish / the ssm_out GEMV)
     {
         const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + (t - kDk);
-        float y = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, xin[ch], false));
+        float y = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, mix.at(b, ch), false));
         // sum of squares per half (waves 0-1: q, waves 2-3: k)
         float sq = wave_sum(y * y);
         if ((t & 63) == 0) red[0][t >> 6] = sq;
@@ -86,12 +86,12 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
     }
     if (t < kCols) {
         const int ch = 2 * chunk + h * kDk + c0 + t;
-        vv[t] = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, xin[ch], true));
+        vv[t] = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, mix.at(b, ch), true));
     }
     if (t == 0) {
         // deltanet.rs:474-480
-        const float br = beta_raw[(size_t)b * ba_stride + h];
-        const float ar = alpha_raw[(size_t)b * ba_stride + h];
+        const float br = mbeta.at(b, h);
+        const float ar = malpha.at(b, h);
         misc[0] = 1.0f / (1.0f + expf(-br));
         const float g = ssm_a[h] * logf(1.0f + expf(ar + dt_bias[h]));
         misc[1] = expf(g);
@@ -160,26 +160,26 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
 
 // Runs after deltanet_step_kernel.  If `conv_state` is not null, commits the
 // q/k conv windows of head h (shift left, append the new input:
-// deltanet_cache.rs:34-42); if `heads` is not null, applies the per-head RMSNorm with ssm_norm and the
-// SiLU(gate) product (deltanet.rs:517-533).  grid = (n_heads, batch), 128
-// threads (one per element of the head).
-__global__ __launch_bounds__(kDk) void dn_finish_kernel(const float *__restrict__ qkv, int qkv_stride,
-                                                        float *__restrict__ conv_state,
-                                                        const float *__restrict__ heads,
-                                                        const float *__restrict__ gate, int gate_stride,
-                                                        const float *__restrict__ norm_w,
-                                                        float *__restrict__ out, int n_heads, float eps) {
+// deltanet_cache.rs:34-42); if `heads` is not null, applies the per-head
+// RMSNorm with ssm_norm and the SiLU(gate) product (deltanet.rs:517-533),
+// written as fp32 (out) or as fp16 hi/lo planes (out_hi / out_lo, the input
+// format of the small-batch MFMA GEMM).  grid = (n_heads, batch), 128 threads
+// (one per element of the head).
+__global__ __launch_bounds__(kDk) void dn_finish_kernel(MixIn mix, float *__restrict__ conv_state,
+                                                        const float *__restrict__ heads, int gate_off,
+                                                        const float *__restrict__ norm_w, float *__restrict__ out,
+                                                        _Float16 *__restrict__ out_hi, _Float16 *__restrict__ out_lo,
+                                                        int n_heads, float eps) {
     __shared__ float red[2];
     const int t = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int chunk = n_heads * kDk;
     if (conv_state) {
-        const float *xin = qkv + (size_t)b * qkv_stride;
         float *cs = conv_state + (size_t)b * 3 * chunk * kKsize;
         const int cq = h * kDk + t, ck = chunk + h * kDk + t;
         float4 a = *reinterpret_cast<const float4 *>(cs + (size_t)cq * kKsize);
         float4 c = *reinterpret_cast<const float4 *>(cs + (size_t)ck * kKsize);
-        *reinterpret_cast<float4 *>(cs + (size_t)cq * kKsize) = make_float4(a.y, a.z, a.w, xin[cq]);
-        *reinterpret_cast<float4 *>(cs + (size_t)ck * kKsize) = make_float4(c.y, c.z, c.w, xin[ck]);
+        *reinterpret_cast<float4 *>(cs + (size_t)cq * kKsize) = make_float4(a.y, a.z, a.w, mix.at(b, cq));
+        *reinterpret_cast<float4 *>(cs + (size_t)ck * kKsize) = make_float4(c.y, c.z, c.w, mix.at(b, ck));
     }
     if (!heads) return;
     const float x = heads[(size_t)b * chunk + h * kDk + t];
@@ -188,29 +188,34 @@ __global__ __launch_bounds__(kDk) void dn_finish_kernel(const float *__restrict_
     __syncthreads();
     const float ms = (red[0] + red[1]) / (float)kDk;
     const float inv_rms = 1.0f / sqrtf(ms + eps);
-    const float g = gate[(size_t)b * gate_stride + h * kDk + t];
-    out[(size_t)b * chunk + h * kDk + t] = ((x * inv_rms) * norm_w[t]) * (g / (1.0f + expf(-g)));
+    const float g = mix.at(b, gate_off + h * kDk + t);
+    const float v = ((x * inv_rms) * norm_w[t]) * (g / (1.0f + expf(-g)));
+    const size_t o = (size_t)b * chunk + h * kDk + t;
+    if (out_hi) {
+        const _Float16 hi = (_Float16)v;
+        out_hi[o] = hi;
+        out_lo[o] = (_Float16)(v - (float)hi);
+    } else {
+        out[o] = v;
+    }
 }
 
 }  // namespace
 
-int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const float *qkv,
-                         int qkv_stride, const float *beta_raw, const float *alpha_raw, int ba_stride,
-                         const float *conv_w, const float *ssm_a, const float *dt_bias, float *conv_state, float *S,
-                         float *out) {
-    hipLaunchKernelGGL(deltanet_step_kernel, dim3(kDk / kCols, n_heads, batch), dim3(kThreads), 0, stream, qkv,
-                       qkv_stride, beta_raw, alpha_raw, ba_stride, conv_w, ssm_a, dt_bias, conv_state, S, out,
-                       n_heads);
+int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
+                         const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
+                         const float *dt_bias, float *conv_state, float *S, float *out) {
+    hipLaunchKernelGGL(deltanet_step_kernel, dim3(kDk / kCols, n_heads, batch), dim3(kThreads), 0, stream, mix,
+                       beta, alpha, conv_w, ssm_a, dt_bias, conv_state, S, out, n_heads);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 
-// heads == nullptr: only commit the q/k conv windows.
-int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const float *qkv, int qkv_stride,
-                     float *conv_state, const float *heads, const float *gate, int gate_stride, const float *norm_w,
-                     float *out, float eps) {
-    hipLaunchKernelGGL(dn_finish_kernel, dim3(n_heads, batch), dim3(kDk), 0, stream, qkv, qkv_stride, conv_state,
-                       heads, gate, gate_stride, norm_w, out, n_heads, eps);
+int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
+                     float *conv_state, const float *heads, int gate_off, const float *norm_w, float *out,
+                     _Float16 *out_hi, _Float16 *out_lo, float eps) {
+    hipLaunchKernelGGL(dn_finish_kernel, dim3(n_heads, batch), dim3(kDk), 0, stream, mix, conv_state, heads, gate_off,
+                       norm_w, out, out_hi, out_lo, n_heads, eps);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

@@ -33,14 +33,25 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return s;
 }
 
-// out[b] = x[b] * (1/sqrt(mean(x[b]^2) + eps)) * w     (main.rs:1106-1113)
+// out[b] = x[b] * (1/sqrt(mean(x[b]^2) + eps)) * w     (main.rs:1106-1113),
+// written as fp32, or as fp16 hi/lo planes (hi + lo ~= value, the input
+// format of the small-batch MFMA GEMM) when hi is not null.
 __device__ __forceinline__ void rmsnorm_row(const float *x, const float *__restrict__ w, float *out, int n,
-                                            float eps, float *red) {
+                                            float eps, float *red, _Float16 *hi = nullptr, _Float16 *lo = nullptr) {
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kThreads) ss += x[i] * x[i];
     ss = block_sum(ss, red);
     const float inv_rms = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += kThreads) out[i] = (x[i] * inv_rms) * w[i];
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const float v = (x[i] * inv_rms) * w[i];
+        if (hi) {
+            const _Float16 h = (_Float16)v;
+            hi[i] = h;
+            lo[i] = (_Float16)(v - (float)h);
+        } else {
+            out[i] = v;
+        }
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
@@ -55,14 +66,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
 __global__ __launch_bounds__(kThreads) void embed_rmsnorm_kernel(const uint32_t *__restrict__ tokens,
                                                                  const float *__restrict__ emb, uint32_t vocab,
                                                                  float *__restrict__ x, const float *__restrict__ w,
-                                                                 float *__restrict__ xn, int n, float eps) {
+                                                                 float *__restrict__ xn, int n, float eps,
+                                                                 _Float16 *__restrict__ hi, _Float16 *__restrict__ lo) {
     __shared__ float red[4];
     const size_t b = blockIdx.x;
     const uint32_t tok = tokens[b];
     float *xb = x + b * n;
     for (int i = threadIdx.x; i < n; i += kThreads) xb[i] = tok < vocab ? emb[(size_t)tok * n + i] : 0.0f;
     __syncthreads();
-    rmsnorm_row(xb, w, xn + b * n, n, eps, red);
+    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi ? hi + b * n : nullptr, lo ? lo + b * n : nullptr);
 }
 
 // x[b] += sum_k part[k][b]; if w: xn[b] = rmsnorm(x[b], w).   part stride between
@@ -70,7 +82,9 @@ __global__ __launch_bounds__(kThreads) void embed_rmsnorm_kernel(const uint32_t 
 __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(float *__restrict__ x,
                                                                     const float *__restrict__ part, int ksplit,
                                                                     int rows, const float *__restrict__ w,
-                                                                    float *__restrict__ xn, int n, float eps) {
+                                                                    float *__restrict__ xn, int n, float eps,
+                                                                    _Float16 *__restrict__ hi,
+                                                                    _Float16 *__restrict__ lo) {
     __shared__ float red[4];
     const size_t b = blockIdx.x;
     float *xb = x + b * n;
@@ -82,13 +96,14 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(float *__res
     }
     if (!w) return;
     __syncthreads();
-    rmsnorm_row(xb, w, xn + b * n, n, eps, red);
+    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi ? hi + b * n : nullptr, lo ? lo + b * n : nullptr);
 }
 
 // Stacked [gate; up] GEMV output gu[k][b][2F]: h[b][r] = SiLU(gate) * up
 // (scratch.rs:181-186: a = (a / (1 + exp(-a))) * b).
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restrict__ gu, int ksplit, int rows,
-                                                            float *__restrict__ h, int F) {
+                                                            float *__restrict__ h, int F, _Float16 *__restrict__ hi,
+                                                            _Float16 *__restrict__ lo) {
     const size_t b = blockIdx.y;
     const int r = blockIdx.x * kThreads + threadIdx.x;
     if (r >= F) return;
@@ -98,7 +113,14 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restr
         g += gu[k * split + b * 2 * F + r];
         u += gu[k * split + b * 2 * F + F + r];
     }
-    h[b * F + r] = (g / (1.0f + expf(-g))) * u;
+    const float v = (g / (1.0f + expf(-g))) * u;
+    if (hi) {
+        const _Float16 hh = (_Float16)v;
+        hi[b * F + r] = hh;
+        lo[b * F + r] = (_Float16)(v - (float)hh);
+    } else {
+        h[b * F + r] = v;
+    }
 }
 
 // a[i] = silu(a[i]) * b[i]   (elementwise entry point)
@@ -205,24 +227,25 @@ int launch_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const float 
 }
 
 int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const uint32_t *tokens, const float *emb,
-                         uint32_t vocab, float *x, const float *w, float *xn, float eps) {
-    hipLaunchKernelGGL(embed_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, tokens, emb, vocab, x, w, xn, n, eps);
+                         uint32_t vocab, float *x, const float *w, float *xn, float eps, _Float16 *hi, _Float16 *lo) {
+    hipLaunchKernelGGL(embed_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, tokens, emb, vocab, x, w, xn, n, eps,
+                       hi, lo);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 
 int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
-                            int ksplit, const float *w, float *xn, float eps) {
+                            int ksplit, const float *w, float *xn, float eps, _Float16 *hi, _Float16 *lo) {
     hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, part, ksplit, rows, w, xn, n,
-                       eps);
+                       eps, hi, lo);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 
-int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit,
-                            float *h) {
+int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit, float *h,
+                            _Float16 *hi, _Float16 *lo) {
     hipLaunchKernelGGL(silu_mul_kernel, dim3((F + kThreads - 1) / kThreads, rows), dim3(kThreads), 0, s, gu, ksplit,
-                       rows, h, F);
+                       rows, h, F, hi, lo);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

@@ -133,20 +133,150 @@ __device__ __forceinline__ void wave_sync_lds() {
 
 constexpr int kWavesPerWg = 4;
 
-// grid = (row tiles of 64, K splits); 4 waves per workgroup.  Workgroup
-// (tile, ks) covers super-blocks [ks * sb_per_split, ...) of its 64 rows; wave
-// w takes every 4th of them.  The 4 waves are reduced through LDS.  With one
-// K split the workgroup writes y; otherwise it writes its partial row sums to
-// part[ks][batch][m], which the consumer adds in ks order.
-template <uint32_t T, int B>
-__global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_tiled(const uint8_t *__restrict__ W,
-                                                                      const float *__restrict__ x,
-                                                                      float *__restrict__ out, int m, int n,
-                                                                      int batch, int sb_per_split,
-                                                                      size_t split_stride) {
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Sum over a 256-thread workgroup; every thread gets the total.
+__device__ __forceinline__ float wg_sum(float v, float *red4) {
+    v = wave_sum64(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
+constexpr int kMaxSplit = 8;     // K splits a consumer may have to add
+constexpr int kMaxSliceSb = 8;   // super-blocks of input one workgroup may need
+
+// sum over p < kp of part[p * stride + i], p ascending.  All kMaxSplit loads
+// are issued unconditionally (slices past kp re-read slice 0) so they overlap
+// instead of costing kp dependent round trips.
+__device__ __forceinline__ float sum_parts(const float *__restrict__ part, int kp, size_t stride, size_t i) {
+    float v[kMaxSplit];
+#pragma unroll
+    for (int p = 0; p < kMaxSplit; p++) v[p] = part[(p < kp ? (size_t)p * stride : 0) + i];
+    float s = v[0];
+#pragma unroll
+    for (int p = 1; p < kMaxSplit; p++) s += p < kp ? v[p] : 0.0f;
+    return s;
+}
+
+// Forms the workgroup's input slice xs[0, len) = input[c0, c0 + len) of length-n
+// input vector `in` (see GemvInMode).  256 threads.  Every mode first issues
+// all of its global loads, then computes, so the prologue costs about one
+// memory round trip.
+template <int MODE>
+__device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0, int len, float *xs, float *red4) {
+    const int t = threadIdx.x;
+    if constexpr (MODE == GEMV_IN_PLAIN) {
+        float v[kMaxSliceSb];
+#pragma unroll
+        for (int i = 0; i < kMaxSliceSb; i++) v[i] = t + 256 * i < len ? in.x[c0 + t + 256 * i] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxSliceSb; i++)
+            if (t + 256 * i < len) xs[t + 256 * i] = v[i];
+    } else if constexpr (MODE == GEMV_IN_SILU_MUL) {
+        // scratch.rs:181-186: a = (a / (1 + exp(-a))) * b
+        float g[kMaxSliceSb], u[kMaxSliceSb];
+#pragma unroll
+        for (int i = 0; i < kMaxSliceSb; i++) {
+            const int j = min(t + 256 * i, len - 1);
+            g[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)c0 + j);
+            u[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)n + c0 + j);
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxSliceSb; i++)
+            if (t + 256 * i < len) xs[t + 256 * i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+    } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
+        // deltanet.rs:517-533, per 128-wide head; a wave handles whole heads
+        // (at most 4 per wave for a slice of 8 super-blocks)
+        const int lane = t & 63, wave = t >> 6;
+        const int nh = len / 128;
+        float a[4], b[4], ga[4], gb[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int hh = min(wave + 4 * i, nh - 1);
+            const int k0 = c0 + hh * 128;
+            a[i] = in.x[k0 + lane];
+            b[i] = in.x[k0 + 64 + lane];
+            ga[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)in.gate_off + k0 + lane);
+            gb[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)in.gate_off + k0 + 64 + lane);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int hh = wave + 4 * i;
+            const float ss = wave_sum64(a[i] * a[i] + b[i] * b[i]);
+            if (hh < nh) {
+                const float inv_rms = 1.0f / sqrtf(ss / 128.0f + in.eps);
+                xs[hh * 128 + lane] = ((a[i] * inv_rms) * in.w[lane]) * (ga[i] / (1.0f + expf(-ga[i])));
+                xs[hh * 128 + 64 + lane] = ((b[i] * inv_rms) * in.w[64 + lane]) * (gb[i] / (1.0f + expf(-gb[i])));
+            }
+        }
+        // commit the q/k conv windows, spread over the launch's workgroups
+        if (in.conv_state) {
+            const int nwg = gridDim.x * gridDim.y, wg = blockIdx.y * gridDim.x + blockIdx.x;
+            for (int c = wg * 256 + t; c < 2 * n; c += nwg * 256) {
+                float4 *cs = reinterpret_cast<float4 *>(in.conv_state) + c;
+                const float4 o = *cs;
+                const float nv = sum_parts(in.part, in.kp, in.part_stride, (size_t)c);
+                *cs = make_float4(o.y, o.z, o.w, nv);
+            }
+        }
+    } else {
+        // RMSNORM / RESID_RMSNORM / EMBED_RMSNORM: the full row is needed for
+        // mean(r^2); the slice is kept in xs and scaled after the reduction
+        // (main.rs:1106-1113: out = (r * inv_rms) * w).  Residual: r = x + s
+        // with s the partials added in split order.
+        const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+        const uint32_t tok = MODE == GEMV_IN_EMBED_RMSNORM ? in.token[0] : 0u;
+        float ss = 0.0f;
+        for (int base = 0; base < n; base += 256 * 8) {
+            float r[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int k = min(base + t + 256 * i, n - 1);
+                if constexpr (MODE == GEMV_IN_EMBED_RMSNORM) {
+                    r[i] = tok < in.vocab ? in.emb[(size_t)tok * n + k] : 0.0f;
+                } else if constexpr (MODE == GEMV_IN_RESID_RMSNORM) {
+                    r[i] = in.x[k] + sum_parts(in.part, in.kp, in.part_stride, (size_t)k);
+                } else {
+                    r[i] = in.x[k];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int k = base + t + 256 * i;
+                if (k < n) {
+                    ss += r[i] * r[i];
+                    if (k >= c0 && k < c0 + len) xs[k - c0] = r[i];
+                    if (MODE != GEMV_IN_RMSNORM && writer) in.x_out[k] = r[i];
+                }
+            }
+        }
+        ss = wg_sum(ss, red4);
+        const float inv_rms = 1.0f / sqrtf(ss / (float)n + in.eps);
+        for (int j = t; j < len; j += 256) xs[j] = (xs[j] * inv_rms) * in.w[c0 + j];
+    }
+    __syncthreads();
+}
+
+// Batch-1 GEMV: grid = (row tiles of 64, K splits); 4 waves per workgroup.
+// Workgroup (tile, ks) covers super-blocks [ks * sb_per_split, ...) of its 64
+// rows; wave w takes every 4th of them.  The input slice is formed in LDS by
+// the prologue and read with wave-uniform (broadcast) LDS loads.  The 4
+// waves are reduced through LDS; the result (or this split's partial sum) goes
+// to out[ks * split_stride + row].
+template <uint32_t T, int MODE>
+__global__ __launch_bounds__(kWave *kWavesPerWg) void gemv_fused(const uint8_t *__restrict__ W, GemvInput in,
+                                                                float *__restrict__ out, int m, int n,
+                                                                int sb_per_split, size_t split_stride) {
     constexpr int V = QTraits<T>::kSbVec;
     __shared__ u32x4 lds[kWavesPerWg][V * kWave];
-    __shared__ float red[kWavesPerWg][B][kWave];
+    __shared__ float xs[kMaxSliceSb * 256];
+    __shared__ float red4[4];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
     const int tile = blockIdx.x;
@@ -157,44 +287,36 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_tiled(const uin
     const int sb_begin = ks * sb_per_split;
     const int sb_end = min(nsb, sb_begin + sb_per_split);
 
-    float acc[B];
-#pragma unroll
-    for (int b = 0; b < B; b++) acc[b] = 0.0f;
-
-    // regs hold the tile in flight; after it is staged into LDS they are
-    // reused for the next tile's loads, which overlap this tile's compute.
+    // issue the first weight tile before the prologue so both overlap
     u32x4 regs[V];
     uint32_t off[V];
-    const uint32_t *wl = reinterpret_cast<const uint32_t *>(&lds[wave][lane * V]);
     tile_offsets<T>(off, (uint32_t)row_bytes, m - row0, lane);
     const uint8_t *tile_base = W + (size_t)row0 * row_bytes;
     int sb = sb_begin + wave;
     if (sb < sb_end) load_tile<T>(regs, tile_base + (size_t)sb * QTraits<T>::kSbBytes, off);
+
+    gemv_prologue<MODE>(in, n, sb_begin * 256, (sb_end - sb_begin) * 256, xs, red4);
+
+    float acc = 0.0f;
+    const uint32_t *wl = reinterpret_cast<const uint32_t *>(&lds[wave][lane * V]);
     for (; sb < sb_end; sb += kWavesPerWg) {
         stage_tile<T>(regs, lds[wave], lane);
         if (sb + kWavesPerWg < sb_end)
             load_tile<T>(regs, tile_base + (size_t)(sb + kWavesPerWg) * QTraits<T>::kSbBytes, off);
-#pragma unroll
-        for (int b = 0; b < B; b++)
-            if (b < batch) acc[b] = sb_dot<T>(wl, x + (size_t)b * n + (size_t)sb * 256, acc[b]);
+        acc = sb_dot<T>(wl, xs + (sb - sb_begin) * 256, acc);
         wave_sync_lds();  // this tile's reads precede the next tile's writes
     }
-#pragma unroll
-    for (int b = 0; b < B; b++) red[wave][b][lane] = acc[b];
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(&lds[0][0]);
+    red[wave * kWave + lane] = acc;
     __syncthreads();
     if (wave != 0) return;
     const int row = row0 + lane;
     if (row >= m) return;
-    float *dst = out + (size_t)ks * split_stride;
+    float sum = red[lane];
 #pragma unroll
-    for (int b = 0; b < B; b++) {
-        if (b < batch) {
-            float s = red[0][b][lane];
-#pragma unroll
-            for (int v = 1; v < kWavesPerWg; v++) s += red[v][b][lane];
-            dst[(size_t)b * m + row] = s;
-        }
-    }
+    for (int v = 1; v < kWavesPerWg; v++) sum += red[v * kWave + lane];
+    out[(size_t)ks * split_stride + row] = sum;
 }
 
 // ---------------------------------------------------------------------------
@@ -391,27 +513,47 @@ __global__ __launch_bounds__(256) void sum_partials(const float *__restrict__ pa
     y[i] = s;
 }
 
-// K splits: the smallest divisor of the super-block count that gives at
-// least `target` waves, or one super-block column per wave.
-int choose_ksplit(int tiles, int nsb, int target_waves) {
-    for (int k = 1; k <= nsb; k++) {
+// K splits: the smallest divisor k of the super-block count with at most 8
+// super-blocks per workgroup, and at most one per wave (4) unless the row
+// tiles alone already fill the chip (tiles * k >= 2 workgroups per CU).
+int choose_ksplit(int tiles, int nsb, int cus) {
+    int best = 0;
+    for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
         if (nsb % k) continue;
-        int per = nsb / k;
-        int waves = tiles * k * min(per, kWavesPerWg);
-        if (waves >= target_waves || per <= kWavesPerWg) return k;
+        const int per = nsb / k;
+        if (per > kMaxSliceSb) continue;
+        if (!best) best = k;
+        if (per <= kWavesPerWg || tiles * k >= 2 * cus) return k;
     }
-    return 1;
+    return best ? best : 1;
 }
 
-template <uint32_t T, int B>
-int launch_tiled(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
-                 uint32_t batch, float *out, size_t split_stride, int ksplit) {
+template <uint32_t T, int MODE>
+int launch_fused(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const GemvInput &in,
+                 float *out, size_t split_stride, int ksplit) {
     const int tiles = (int)((m + kWave - 1) / kWave);
     const int per = (int)(n / 256) / ksplit;
-    hipLaunchKernelGGL((quant_gemm_tiled<T, B>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
-                       static_cast<const uint8_t *>(w), x, out, (int)m, (int)n, (int)batch, per, split_stride);
+    hipLaunchKernelGGL((gemv_fused<T, MODE>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
+                       static_cast<const uint8_t *>(w), in, out, (int)m, (int)n, per, split_stride);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
+}
+
+template <uint32_t T>
+int dispatch_fused(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const GemvInput &in,
+                   float *out, int ksplit) {
+    const size_t ss = m;
+    switch (in.mode) {
+        case GEMV_IN_PLAIN: return launch_fused<T, GEMV_IN_PLAIN>(ctx, stream, w, m, n, in, out, ss, ksplit);
+        case GEMV_IN_RMSNORM: return launch_fused<T, GEMV_IN_RMSNORM>(ctx, stream, w, m, n, in, out, ss, ksplit);
+        case GEMV_IN_RESID_RMSNORM:
+            return launch_fused<T, GEMV_IN_RESID_RMSNORM>(ctx, stream, w, m, n, in, out, ss, ksplit);
+        case GEMV_IN_EMBED_RMSNORM:
+            return launch_fused<T, GEMV_IN_EMBED_RMSNORM>(ctx, stream, w, m, n, in, out, ss, ksplit);
+        case GEMV_IN_GATED_NORM: return launch_fused<T, GEMV_IN_GATED_NORM>(ctx, stream, w, m, n, in, out, ss, ksplit);
+        case GEMV_IN_SILU_MUL: return launch_fused<T, GEMV_IN_SILU_MUL>(ctx, stream, w, m, n, in, out, ss, ksplit);
+        default: return set_error(ctx->err, ANEHIP_EINVAL, "gemv: input mode %d", in.mode);
+    }
 }
 
 template <uint32_t T, int NT>
@@ -429,7 +571,11 @@ template <uint32_t T>
 int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
                  uint32_t batch, float *out, int ksplit, _Float16 *xsplit) {
     const size_t split_stride = (size_t)batch * m;
-    if (batch == 1) return launch_tiled<T, 1>(ctx, stream, w, m, n, x, 1, out, split_stride, ksplit);
+    if (batch == 1) {
+        GemvInput in;
+        in.x = x;
+        return dispatch_fused<T>(ctx, stream, w, m, n, in, out, ksplit);
+    }
     // batch 2..32: split x into fp16 hi/lo planes, then the MFMA kernel
     const size_t count = (size_t)batch * n;
     _Float16 *xh = xsplit, *xl = xsplit + count;
@@ -443,8 +589,24 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
 
 int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
     const int tiles = (int)((m + kWave - 1) / kWave);
-    const int target = 3 * (ctx->cu_count > 0 ? ctx->cu_count : 256);
-    return choose_ksplit(tiles, (int)(n / 256), target);
+    return choose_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256);
+}
+
+int launch_gemm_planes(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
+                       uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit) {
+    const size_t ss = (size_t)batch * m;
+    if (ggml_type == ANEHIP_GGML_Q8_0) {
+        if (batch <= 16) return launch_mfma<ANEHIP_GGML_Q8_0, 1>(ctx, stream, w, m, n, xh, xl, batch, out, ss, ksplit);
+        return launch_mfma<ANEHIP_GGML_Q8_0, 2>(ctx, stream, w, m, n, xh, xl, batch, out, ss, ksplit);
+    }
+    if (batch <= 16) return launch_mfma<ANEHIP_GGML_Q4_0, 1>(ctx, stream, w, m, n, xh, xl, batch, out, ss, ksplit);
+    return launch_mfma<ANEHIP_GGML_Q4_0, 2>(ctx, stream, w, m, n, xh, xl, batch, out, ss, ksplit);
+}
+
+int launch_gemv_fused(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
+                      uint32_t n, const GemvInput &in, float *out, int ksplit) {
+    if (ggml_type == ANEHIP_GGML_Q8_0) return dispatch_fused<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, in, out, ksplit);
+    return dispatch_fused<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, in, out, ksplit);
 }
 
 int launch_gemm_raw(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,
