@@ -61,6 +61,9 @@ def lib():
             "anehip_timer_start": (C.c_int, [vp]),
             "anehip_timer_stop": (C.c_int, [vp, C.POINTER(f32)]),
             "anehip_quant_gemm": (C.c_int, [vp, u32, vp, u32, u32, vp, u32, vp]),
+            "anehip_quant_packed_bytes": (sz, [u32, u32, u32]),
+            "anehip_quant_pack": (C.c_int, [vp, u32, vp, u32, u32, vp]),
+            "anehip_quant_gemv_packed": (C.c_int, [vp, u32, vp, u32, u32, vp, vp]),
             "anehip_rmsnorm": (C.c_int, [vp, vp, vp, vp, u32, u32, f32]),
             "anehip_silu_mul": (C.c_int, [vp, vp, vp, sz]),
             "anehip_residual_add": (C.c_int, [vp, vp, vp, sz]),

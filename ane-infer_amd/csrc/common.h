@@ -140,13 +140,24 @@ struct MixIn {
 // ksplit == 1), with ksplit from gemm_ksplit().
 int launch_quant_gemm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w,
                       uint32_t m, uint32_t n, const float *x, uint32_t batch, float *y);
-int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
+// Number of K splits for an [m x n] product: split ks covers super-blocks
+// [ks * per, min(nsb, (ks + 1) * per)) with per = split_len(nsb, ksplit);
+// max_k bounds the splits a consumer has to add (fused consumers take 8).
+int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int max_k = 8);
+inline int split_len(int nsb, int ksplit) { return (nsb + ksplit - 1) / ksplit; }
 // xsplit: device scratch of batch * n floats (x split into fp16 hi / lo
 // planes for the MFMA path); may be null when batch == 1.
 int launch_gemm_raw(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                     uint32_t n, const float *x, uint32_t batch, float *out, int ksplit, void *xsplit);
 int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, float *y, size_t count,
                         int ksplit);
+// Panel layout (see gemv.hip): bytes of an [m x n] matrix, repack from GGUF
+// blocks, and the batch-1 GEMV over panels.
+size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
+int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
+                  void *dst);
+int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
+                       uint32_t n, const GemvInput &in, float *out, int ksplit);
 // Small-batch GEMM (batch 2..32) on MFMA from fp16 hi/lo input planes
 // [batch][n]; writes out[ks][batch][m].
 int launch_gemm_planes(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,

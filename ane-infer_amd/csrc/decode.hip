@@ -34,9 +34,13 @@ constexpr uint32_t kDk = 128;
 constexpr uint32_t kConvK = 4;
 constexpr uint32_t kHd = 256;
 
+// A quantised matrix: GGUF blocks (d, as uploaded) and, once the batch-1
+// path has run, its panel copy (p) for the batch-1 GEMV; `stale` marks a
+// panel copy that has to be rebuilt from d before the next step.
 struct QMat {
-    void *d = nullptr;
+    void *d = nullptr, *p = nullptr;
     uint32_t type = 0, rows = 0, cols = 0;
+    bool stale = true;
 };
 
 struct Layer {
@@ -294,7 +298,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in1.emb = M->embedding;
         in1.vocab = D.vocab_size;
         const int k1 = gemm_ksplit(ctx, rows_in, d);
-        TRY(launch_gemv_fused(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, in1, M->pmix, k1));
+        TRY(launch_gemv_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, in1, M->pmix, k1));
         std::swap(cur, nxt);
         MixIn mix;
         mix.p = M->pmix;
@@ -326,7 +330,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
             cols3 = qd;
         }
         const int k3 = gemm_ksplit(ctx, d, cols3);
-        TRY(launch_gemv_fused(ctx, s, L.mix_out.type, L.mix_out.d, d, cols3, in3, M->p0, k3));
+        TRY(launch_gemv_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, in3, M->p0, k3));
         // 4. FFN gate/up, input = RMSNorm(residual + mixer output)
         GemvInput in4;
         in4.mode = GEMV_IN_RESID_RMSNORM;
@@ -338,7 +342,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in4.eps = eps;
         in4.x_out = nxt;
         const int k4 = gemm_ksplit(ctx, 2 * F, d);
-        TRY(launch_gemv_fused(ctx, s, L.ffn_gu.type, L.ffn_gu.d, 2 * F, d, in4, M->p1, k4));
+        TRY(launch_gemv_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, in4, M->p1, k4));
         std::swap(cur, nxt);
         // 5. FFN down, input = SiLU(gate) * up
         GemvInput in5;
@@ -347,7 +351,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in5.kp = k4;
         in5.part_stride = 2 * F;
         const int k5 = gemm_ksplit(ctx, d, F);
-        TRY(launch_gemv_fused(ctx, s, L.ffn_down.type, L.ffn_down.d, d, F, in5, M->p0, k5));
+        TRY(launch_gemv_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, in5, M->p0, k5));
         prev_part = M->p0;
         prev_kp = k5;
     }
@@ -363,9 +367,9 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     inf.x_out = nxt;
     const int kf = gemm_ksplit(ctx, D.vocab_size, d);
     if (kf == 1) {
-        TRY(launch_gemv_fused(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, inf, M->logits, 1));
+        TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->logits, 1));
     } else {
-        TRY(launch_gemv_fused(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, inf, M->pmix, kf));
+        TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->pmix, kf));
         TRY(launch_sum_partials(ctx, s, M->pmix, M->logits, D.vocab_size, kf));
     }
     return ANEHIP_OK;
@@ -454,8 +458,35 @@ size_t part_floats(anehip_ctx *ctx, Model *M) {
     return mx;
 }
 
+// Builds the panel copy of every matrix whose GGUF blocks changed since the
+// last step (all of them on the first batch-1 step).
+int pack_mat(anehip_ctx *ctx, QMat &Q) {
+    if (!Q.d || !Q.stale) return ANEHIP_OK;
+    if (!Q.p) {
+        const size_t bytes = packed_bytes(Q.type, Q.rows, Q.cols);
+        if (hipMalloc(&Q.p, bytes) != hipSuccess) {
+            Q.p = nullptr;
+            return set_error(ctx->err, ANEHIP_ENOMEM, "decode: cannot allocate %zu bytes of panel weights", bytes);
+        }
+    }
+    TRY(launch_repack(ctx, ctx->stream, Q.type, Q.d, Q.rows, Q.cols, Q.p));
+    Q.stale = false;
+    return ANEHIP_OK;
+}
+
+int pack_weights(anehip_ctx *ctx, Model *M) {
+    for (Layer &L : M->layers) {
+        TRY(pack_mat(ctx, L.mix_in));
+        TRY(pack_mat(ctx, L.mix_out));
+        TRY(pack_mat(ctx, L.ffn_gu));
+        TRY(pack_mat(ctx, L.ffn_down));
+    }
+    return pack_mat(ctx, M->lm_head);
+}
+
 int launch_step(anehip_ctx *ctx, Model *M) {
     hipStream_t s = ctx->stream;
+    if (M->batch == 1) TRY(pack_weights(ctx, M));
     if (!M->use_graph) return enqueue_step(ctx, M, s);
     if (!M->exec) {
         ANEHIP_HIP_TRY(ctx->err, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -571,13 +602,15 @@ __attribute__((visibility("hidden"))) void anehip_model_teardown(anehip_ctx *ctx
     if (!M) return;
     free_state(M);
     for (Layer &L : M->layers) {
-        void *ps[] = {L.mix_in.d, L.mix_out.d, L.ffn_gu.d, L.ffn_down.d, L.attn_norm, L.post_attn_norm,
-                      L.ssm_a,    L.conv1d,    L.dt_bias,  L.ssm_norm,   L.q_norm,    L.k_norm};
+        void *ps[] = {L.mix_in.d, L.mix_out.d, L.ffn_gu.d, L.ffn_down.d, L.mix_in.p, L.mix_out.p,
+                      L.ffn_gu.p, L.ffn_down.p, L.attn_norm, L.post_attn_norm, L.ssm_a, L.conv1d,
+                      L.dt_bias, L.ssm_norm, L.q_norm, L.k_norm};
         for (void *p : ps) free_ptr(p);
     }
     free_ptr(M->embedding);
     free_ptr(M->final_norm);
     free_ptr(M->lm_head.d);
+    free_ptr(M->lm_head.p);
     free_ptr(M->inv_freq);
     delete M;
     ctx->model = nullptr;
@@ -624,6 +657,7 @@ int anehip_upload_quant(anehip_ctx *ctx, int32_t layer, uint32_t kind, const uin
     }
     char *dst = static_cast<char *>(Q.d) + (size_t)slot.row_off * qrow_bytes(ggml_type, n);
     ANEHIP_HIP_TRY(ctx->err, hipMemcpy(dst, blocks, nbytes, hipMemcpyHostToDevice));
+    Q.stale = true;
     if (layer < 0) M->glob_have |= 1ull << kind;
     else M->layers[layer].have |= 1ull << kind;
     return ANEHIP_OK;
@@ -683,6 +717,7 @@ int anehip_tensor_ptr(anehip_ctx *ctx, int32_t layer, uint32_t kind, uint32_t gg
             Q.cols = ks.cols;
         }
         *dptr = static_cast<char *>(Q.d) + (size_t)slot.row_off * qrow_bytes(ggml_type, ks.cols);
+        Q.stale = true;  // writes through *dptr reach the batch-1 path at the next step
         *nbytes = (size_t)ks.rows * qrow_bytes(ggml_type, ks.cols);
     } else {
         float **slot = f32_slot(M, layer, kind);

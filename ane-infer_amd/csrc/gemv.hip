@@ -165,11 +165,17 @@ __device__ __forceinline__ float sum_parts(const float *__restrict__ part, int k
 }
 
 // Forms the workgroup's input slice xs[0, len) = input[c0, c0 + len) of length-n
-// input vector `in` (see GemvInMode).  256 threads.  Every mode first issues
-// all of its global loads, then computes, so the prologue costs about one
-// memory round trip.
-template <int MODE>
-__device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0, int len, float *xs, float *red4) {
+// input vector `in` (see GemvInMode).  256 threads.  Every mode issues its
+// global loads in batches of RB elements per thread, then computes, so with
+// RB = 8 the prologue costs about one memory round trip; smaller RB trades
+// round trips for registers.
+//
+// `first` is false when a workgroup forms a second slice of the same input in
+// one launch: the one-off side effects (the x_out copy, the conv-window
+// commit) are then skipped.
+template <int MODE, int RB = 8>
+__device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0, int len, float *xs, float *red4,
+                                              bool first = true) {
     const int t = threadIdx.x;
     if constexpr (MODE == GEMV_IN_PLAIN) {
         float v[kMaxSliceSb];
@@ -180,43 +186,49 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
             if (t + 256 * i < len) xs[t + 256 * i] = v[i];
     } else if constexpr (MODE == GEMV_IN_SILU_MUL) {
         // scratch.rs:181-186: a = (a / (1 + exp(-a))) * b
-        float g[kMaxSliceSb], u[kMaxSliceSb];
+        for (int i0 = 0; i0 < kMaxSliceSb && 256 * i0 < len; i0 += RB) {
+            float g[RB], u[RB];
 #pragma unroll
-        for (int i = 0; i < kMaxSliceSb; i++) {
-            const int j = min(t + 256 * i, len - 1);
-            g[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)c0 + j);
-            u[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)n + c0 + j);
+            for (int i = 0; i < RB; i++) {
+                const int j = min(t + 256 * (i0 + i), len - 1);
+                g[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)c0 + j);
+                u[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)n + c0 + j);
+            }
+#pragma unroll
+            for (int i = 0; i < RB; i++)
+                if (t + 256 * (i0 + i) < len) xs[t + 256 * (i0 + i)] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
         }
-#pragma unroll
-        for (int i = 0; i < kMaxSliceSb; i++)
-            if (t + 256 * i < len) xs[t + 256 * i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
     } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
         // deltanet.rs:517-533, per 128-wide head; a wave handles whole heads
         // (at most 4 per wave for a slice of 8 super-blocks)
         const int lane = t & 63, wave = t >> 6;
         const int nh = len / 128;
-        float a[4], b[4], ga[4], gb[4];
+        constexpr int HB = RB >= 8 ? 4 : (RB >= 4 ? 2 : 1);
+        for (int i0 = 0; i0 < 4; i0 += HB) {
+            float a[HB], b[HB], ga[HB], gb[HB];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int hh = min(wave + 4 * i, nh - 1);
-            const int k0 = c0 + hh * 128;
-            a[i] = in.x[k0 + lane];
-            b[i] = in.x[k0 + 64 + lane];
-            ga[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)in.gate_off + k0 + lane);
-            gb[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)in.gate_off + k0 + 64 + lane);
-        }
+            for (int i = 0; i < HB; i++) {
+                const int hh = min(wave + 4 * (i0 + i), nh - 1);
+                const int k0 = c0 + hh * 128;
+                a[i] = in.x[k0 + lane];
+                b[i] = in.x[k0 + 64 + lane];
+                ga[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)in.gate_off + k0 + lane);
+                gb[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)in.gate_off + k0 + 64 + lane);
+            }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int hh = wave + 4 * i;
-            const float ss = wave_sum64(a[i] * a[i] + b[i] * b[i]);
-            if (hh < nh) {
-                const float inv_rms = 1.0f / sqrtf(ss / 128.0f + in.eps);
-                xs[hh * 128 + lane] = ((a[i] * inv_rms) * in.w[lane]) * (ga[i] / (1.0f + expf(-ga[i])));
-                xs[hh * 128 + 64 + lane] = ((b[i] * inv_rms) * in.w[64 + lane]) * (gb[i] / (1.0f + expf(-gb[i])));
+            for (int i = 0; i < HB; i++) {
+                const int hh = wave + 4 * (i0 + i);
+                const float ss = wave_sum64(a[i] * a[i] + b[i] * b[i]);
+                if (hh < nh) {
+                    const float inv_rms = 1.0f / sqrtf(ss / 128.0f + in.eps);
+                    xs[hh * 128 + lane] = ((a[i] * inv_rms) * in.w[lane]) * (ga[i] / (1.0f + expf(-ga[i])));
+                    xs[hh * 128 + 64 + lane] =
+                        ((b[i] * inv_rms) * in.w[64 + lane]) * (gb[i] / (1.0f + expf(-gb[i])));
+                }
             }
         }
         // commit the q/k conv windows, spread over the launch's workgroups
-        if (in.conv_state) {
+        if (in.conv_state && first) {
             const int nwg = gridDim.x * gridDim.y, wg = blockIdx.y * gridDim.x + blockIdx.x;
             for (int c = wg * 256 + t; c < 2 * n; c += nwg * 256) {
                 float4 *cs = reinterpret_cast<float4 *>(in.conv_state) + c;
@@ -230,13 +242,13 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
         // mean(r^2); the slice is kept in xs and scaled after the reduction
         // (main.rs:1106-1113: out = (r * inv_rms) * w).  Residual: r = x + s
         // with s the partials added in split order.
-        const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+        const bool writer = first && blockIdx.x == 0 && blockIdx.y == 0;
         const uint32_t tok = MODE == GEMV_IN_EMBED_RMSNORM ? in.token[0] : 0u;
         float ss = 0.0f;
-        for (int base = 0; base < n; base += 256 * 8) {
-            float r[8];
+        for (int base = 0; base < n; base += 256 * RB) {
+            float r[RB];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < RB; i++) {
                 const int k = min(base + t + 256 * i, n - 1);
                 if constexpr (MODE == GEMV_IN_EMBED_RMSNORM) {
                     r[i] = tok < in.vocab ? in.emb[(size_t)tok * n + k] : 0.0f;
@@ -247,7 +259,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
                 }
             }
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < RB; i++) {
                 const int k = base + t + 256 * i;
                 if (k < n) {
                     ss += r[i] * r[i];
@@ -316,6 +328,160 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void gemv_fused(const uint8_t *
     float sum = red[lane];
 #pragma unroll
     for (int v = 1; v < kWavesPerWg; v++) sum += red[v * kWave + lane];
+    out[(size_t)ks * split_stride + row] = sum;
+}
+
+// ---------------------------------------------------------------------------
+// Panel layout.  The decode step keeps its weights in a GPU-native
+// permutation of the GGUF blocks (same bytes, same values), built once at
+// upload: row tiles of 64 rows, each cut into panels of 256 columns (8
+// blocks).  A panel is
+//   quants: [chunk][64 rows][16 bytes]  (Q8_0: 16 chunks = 2 per block;
+//                                        Q4_0: 8 chunks = 1 per block, the
+//                                        block's 16 nibble bytes)
+//   scales: [64 rows][8 x fp16]          (the rows' 8 block scales)
+// so 17 (Q8_0) or 9 (Q4_0) 1 KiB-contiguous wave loads bring every lane its
+// own row's 256 weights and scales, with no LDS transposition.  Panels of a
+// tile are consecutive; rows past m are zero.
+// ---------------------------------------------------------------------------
+
+template <uint32_t T> struct Panel;
+template <> struct Panel<ANEHIP_GGML_Q8_0> {
+    static constexpr int kChunks = 16;
+    static constexpr int kBytes = 17 * 1024;
+};
+template <> struct Panel<ANEHIP_GGML_Q4_0> {
+    static constexpr int kChunks = 8;
+    static constexpr int kBytes = 9 * 1024;
+};
+
+// One thread per 16-byte destination vector of the panel buffer.
+template <uint32_t T>
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                    int m, int n, size_t nvec) {
+    const size_t v = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (v >= nvec) return;
+    constexpr int BB = QTraits<T>::kBlockBytes;
+    const int nsb = n >> 8;
+    const size_t panel = v / (Panel<T>::kBytes / 16);
+    const int within = (int)(v % (Panel<T>::kBytes / 16));  // 16-byte vector index inside the panel
+    const int tile = (int)(panel / nsb), sb = (int)(panel % nsb);
+    const int chunk = within / 64, r = within % 64;  // chunk == kChunks: the scale vector
+    const int row = tile * 64 + r;
+    uint8_t out[16];
+    const size_t row_off = (size_t)row * (n / 32) * BB;
+    for (int i = 0; i < 16; i++) {
+        uint8_t b = 0;
+        if (row < m) {
+            if (chunk < Panel<T>::kChunks) {
+                const int blk = T == ANEHIP_GGML_Q8_0 ? chunk / 2 : chunk;
+                const int q0 = T == ANEHIP_GGML_Q8_0 ? 2 + 16 * (chunk & 1) : 2;
+                b = src[row_off + (size_t)(sb * 8 + blk) * BB + q0 + i];
+            } else {
+                b = src[row_off + (size_t)(sb * 8 + i / 2) * BB + (i & 1)];
+            }
+        }
+        out[i] = b;
+    }
+    u32x4 w;
+    w.x = out[0] | (out[1] << 8) | (out[2] << 16) | ((uint32_t)out[3] << 24);
+    w.y = out[4] | (out[5] << 8) | (out[6] << 16) | ((uint32_t)out[7] << 24);
+    w.z = out[8] | (out[9] << 8) | (out[10] << 16) | ((uint32_t)out[11] << 24);
+    w.w = out[12] | (out[13] << 8) | (out[14] << 16) | ((uint32_t)out[15] << 24);
+    reinterpret_cast<u32x4 *>(dst)[v] = w;
+}
+
+// Dot product of one panel row held in registers (q: quant vectors of the
+// lane's row; sc: its 8 block scales) with x[0..255] (wave-uniform, so
+// scalar loads), per block then scaled (q8_gemv.rs:234-242).
+template <uint32_t T>
+__device__ __forceinline__ float panel_dot(const u32x4 *q, const u32x4 &sc, const float *__restrict__ x, float acc) {
+    const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const float d = __half2float(__ushort_as_half((unsigned short)(scw[b >> 1] >> (16 * (b & 1)))));
+        float bs = 0.0f;
+        if constexpr (T == ANEHIP_GGML_Q8_0) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t w4[4] = {q[2 * b + h].x, q[2 * b + h].y, q[2 * b + h].z, q[2 * b + h].w};
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int qi = (int)(int8_t)(w4[i >> 2] >> (8 * (i & 3)));
+                    bs = fmaf((float)qi, x[32 * b + 16 * h + i], bs);
+                }
+            }
+        } else {
+            const uint32_t w4[4] = {q[b].x, q[b].y, q[b].z, q[b].w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t byte = (w4[i >> 2] >> (8 * (i & 3))) & 0xffu;
+                bs = fmaf((float)((int)(byte & 15u) - 8), x[32 * b + i], bs);
+                bs = fmaf((float)((int)(byte >> 4) - 8), x[32 * b + 16 + i], bs);
+            }
+        }
+        acc = fmaf(bs, d, acc);
+    }
+    return acc;
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void load_panel(u32x4 *q, u32x4 &sc, const uint8_t *panel, int lane) {
+    const u32x4 *p = reinterpret_cast<const u32x4 *>(panel);
+#pragma unroll
+    for (int c = 0; c < Panel<T>::kChunks; c++) q[c] = __builtin_nontemporal_load(p + c * 64 + lane);
+    sc = __builtin_nontemporal_load(p + Panel<T>::kChunks * 64 + lane);
+}
+
+// Batch-1 GEMV over panels: grid = (row tiles, K splits), 4 waves per
+// workgroup.  The workgroup's K range is taken in rounds of up to 8 panels
+// (one round unless n is large); in a round wave w owns panels r0 + w and
+// r0 + w + 4 and issues both loads before any other work.  The 4 waves are
+// reduced through LDS.  The input slice comes straight from in.x (plain:
+// wave-uniform, so scalar loads) or from the prologue (fused modes: LDS,
+// broadcast reads).
+template <uint32_t T, int MODE>
+__global__ __launch_bounds__(kWave *kWavesPerWg) void gemv_packed(const uint8_t *__restrict__ Wp, GemvInput in,
+                                                                 float *__restrict__ out, int m, int n,
+                                                                 int sb_per_split, size_t split_stride) {
+    constexpr int NC = Panel<T>::kChunks;
+    __shared__ float xs[kMaxSliceSb * 256];
+    __shared__ float red[kWavesPerWg][kWave];
+    __shared__ float red4[4];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int tile = blockIdx.x, ks = blockIdx.y;
+    const int nsb = n >> 8;
+    const int sb_begin = ks * sb_per_split;
+    const int sb_end = min(nsb, sb_begin + sb_per_split);
+    const uint8_t *tile_base = Wp + (size_t)tile * nsb * Panel<T>::kBytes;
+
+    float acc = 0.0f;
+    for (int r0 = sb_begin; r0 < sb_end; r0 += kMaxSliceSb) {
+        const int r1 = min(sb_end, r0 + kMaxSliceSb);
+        const int sb0 = r0 + wave, sb1 = sb0 + kWavesPerWg;
+        u32x4 qa[NC], sa, qb[NC], sbk;
+        if (sb0 < r1) load_panel<T>(qa, sa, tile_base + (size_t)sb0 * Panel<T>::kBytes, lane);
+        if (sb1 < r1) load_panel<T>(qb, sbk, tile_base + (size_t)sb1 * Panel<T>::kBytes, lane);
+        const float *xg;
+        if constexpr (MODE == GEMV_IN_PLAIN) {
+            xg = in.x + r0 * 256;
+        } else {
+            if (r0 != sb_begin) __syncthreads();  // the previous round's reads of xs are done
+            gemv_prologue<MODE, 2>(in, n, r0 * 256, (r1 - r0) * 256, xs, red4, r0 == sb_begin);
+            xg = xs;
+        }
+        if (sb0 < r1) acc = panel_dot<T>(qa, sa, xg + (sb0 - r0) * 256, acc);
+        if (sb1 < r1) acc = panel_dot<T>(qb, sbk, xg + (sb1 - r0) * 256, acc);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    const int row = tile * kWave + lane;
+    if (row >= m) return;
+    float sum = red[0][lane];
+#pragma unroll
+    for (int v = 1; v < kWavesPerWg; v++) sum += red[v][lane];
     out[(size_t)ks * split_stride + row] = sum;
 }
 
@@ -516,23 +682,25 @@ __global__ __launch_bounds__(256) void sum_partials(const float *__restrict__ pa
 // K splits: the smallest divisor k of the super-block count with at most 8
 // super-blocks per workgroup, and at most one per wave (4) unless the row
 // tiles alone already fill the chip (tiles * k >= 2 workgroups per CU).
-int choose_ksplit(int tiles, int nsb, int cus) {
+int choose_ksplit(int tiles, int nsb, int cus, int max_k) {
     int best = 0;
-    for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
-        if (nsb % k) continue;
-        const int per = nsb / k;
+    for (int k = 1; k <= nsb && k <= max_k; k++) {
+        const int per = (nsb + k - 1) / k;
+        if ((k - 1) * per >= nsb) continue;  // would leave a split empty
         if (per > kMaxSliceSb) continue;
         if (!best) best = k;
         if (per <= kWavesPerWg || tiles * k >= 2 * cus) return k;
     }
-    return best ? best : 1;
+    return best ? best : min(nsb, max_k);
 }
 
 template <uint32_t T, int MODE>
 int launch_fused(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const GemvInput &in,
                  float *out, size_t split_stride, int ksplit) {
     const int tiles = (int)((m + kWave - 1) / kWave);
-    const int per = (int)(n / 256) / ksplit;
+    const int per = split_len((int)(n / 256), ksplit);
+    if (per > kMaxSliceSb)
+        return set_error(ctx->err, ANEHIP_EINVAL, "gemv: %d super-blocks per split (max %d)", per, kMaxSliceSb);
     hipLaunchKernelGGL((gemv_fused<T, MODE>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
                        static_cast<const uint8_t *>(w), in, out, (int)m, (int)n, per, split_stride);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
@@ -560,7 +728,7 @@ template <uint32_t T, int NT>
 int launch_mfma(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const _Float16 *xh,
                 const _Float16 *xl, uint32_t batch, float *out, size_t split_stride, int ksplit) {
     const int tiles = (int)((m + kWave - 1) / kWave);
-    const int per = (int)(n / 256) / ksplit;
+    const int per = split_len((int)(n / 256), ksplit);
     hipLaunchKernelGGL((quant_gemm_mfma<T, NT>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
                        static_cast<const uint8_t *>(w), xh, xl, out, (int)m, (int)n, (int)batch, per, split_stride);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
@@ -587,9 +755,63 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
 
 }  // namespace
 
-int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int max_k) {
     const int tiles = (int)((m + kWave - 1) / kWave);
-    return choose_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256);
+    return choose_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256, max_k);
+}
+
+size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n) {
+    const size_t tiles = (m + 63) / 64, nsb = n / 256;
+    return tiles * nsb * (ggml_type == ANEHIP_GGML_Q8_0 ? Panel<ANEHIP_GGML_Q8_0>::kBytes : Panel<ANEHIP_GGML_Q4_0>::kBytes);
+}
+
+int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
+                  void *dst) {
+    const size_t nvec = packed_bytes(ggml_type, m, n) / 16;
+    const unsigned grid = (unsigned)((nvec + 255) / 256);
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        hipLaunchKernelGGL(repack_kernel<ANEHIP_GGML_Q8_0>, dim3(grid), dim3(256), 0, stream,
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec);
+    else
+        hipLaunchKernelGGL(repack_kernel<ANEHIP_GGML_Q4_0>, dim3(grid), dim3(256), 0, stream,
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+template <uint32_t T, int MODE>
+int launch_packed_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const GemvInput &in,
+                    float *out, int ksplit) {
+    const int tiles = (int)((m + kWave - 1) / kWave);
+    const int per = split_len((int)(n / 256), ksplit);
+    hipLaunchKernelGGL((gemv_packed<T, MODE>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
+                       static_cast<const uint8_t *>(w), in, out, (int)m, (int)n, per, (size_t)m);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+template <uint32_t T>
+int dispatch_packed(anehip_ctx *ctx, hipStream_t s, const void *w, uint32_t m, uint32_t n, const GemvInput &in,
+                    float *out, int ksplit) {
+    switch (in.mode) {
+        case GEMV_IN_PLAIN: return launch_packed_t<T, GEMV_IN_PLAIN>(ctx, s, w, m, n, in, out, ksplit);
+        case GEMV_IN_RMSNORM: return launch_packed_t<T, GEMV_IN_RMSNORM>(ctx, s, w, m, n, in, out, ksplit);
+        case GEMV_IN_RESID_RMSNORM:
+            return launch_packed_t<T, GEMV_IN_RESID_RMSNORM>(ctx, s, w, m, n, in, out, ksplit);
+        case GEMV_IN_EMBED_RMSNORM:
+            return launch_packed_t<T, GEMV_IN_EMBED_RMSNORM>(ctx, s, w, m, n, in, out, ksplit);
+        case GEMV_IN_GATED_NORM:
+            return launch_packed_t<T, GEMV_IN_GATED_NORM>(ctx, s, w, m, n, in, out, ksplit);
+        case GEMV_IN_SILU_MUL: return launch_packed_t<T, GEMV_IN_SILU_MUL>(ctx, s, w, m, n, in, out, ksplit);
+        default: return set_error(ctx->err, ANEHIP_EINVAL, "gemv: input mode %d", in.mode);
+    }
+}
+
+int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,
+                       const GemvInput &in, float *out, int ksplit) {
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        return dispatch_packed<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, in, out, ksplit);
+    return dispatch_packed<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, in, out, ksplit);
 }
 
 int launch_gemm_planes(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
@@ -627,7 +849,9 @@ int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, 
 
 int launch_quant_gemm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                       uint32_t n, const float *x, uint32_t batch, float *y) {
-    const int ksplit = gemm_ksplit(ctx, m, n);
+    // the sum_partials consumer takes any number of splits, so the batch-1
+    // kernel never needs more than kMaxSliceSb super-blocks per split
+    const int ksplit = gemm_ksplit(ctx, m, n, batch == 1 ? 1 << 20 : kMaxSplit);
     const size_t count = (size_t)batch * m;
     // workspace: [ksplit partials][x hi/lo planes (2 * batch * n halves)]
     const size_t part = ksplit > 1 ? (size_t)ksplit * count : 0;

@@ -219,4 +219,40 @@ int anehip_quant_gemm(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32
     return launch_quant_gemm(ctx, ctx->stream, ggml_type, w, m, n, x, batch, y);
 }
 
+size_t anehip_quant_packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n) {
+    if ((ggml_type != ANEHIP_GGML_Q8_0 && ggml_type != ANEHIP_GGML_Q4_0) || m == 0 || n == 0 || n % 256) return 0;
+    return packed_bytes(ggml_type, m, n);
+}
+
+static int check_packed_args(anehip_ctx *ctx, const char *what, uint32_t ggml_type, uint32_t m, uint32_t n) {
+    if (ggml_type != ANEHIP_GGML_Q8_0 && ggml_type != ANEHIP_GGML_Q4_0)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "%s: ggml type %u (only Q4_0=2, Q8_0=8)", what, ggml_type);
+    if (m == 0 || n == 0 || n % 256)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "%s: n=%u must be a positive multiple of 256 (m=%u)", what, n, m);
+    return ANEHIP_OK;
+}
+
+int anehip_quant_pack(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n, void *dst) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "quant_pack: ctx is NULL");
+    if (!w || !dst) return set_error(ctx->err, ANEHIP_EINVAL, "quant_pack: null pointer");
+    int rc = check_packed_args(ctx, "quant_pack", ggml_type, m, n);
+    if (rc) return rc;
+    return launch_repack(ctx, ctx->stream, ggml_type, w, m, n, dst);
+}
+
+int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
+                             const float *x, float *y) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "quant_gemv_packed: ctx is NULL");
+    if (!wp || !x || !y) return set_error(ctx->err, ANEHIP_EINVAL, "quant_gemv_packed: null pointer");
+    int rc = check_packed_args(ctx, "quant_gemv_packed", ggml_type, m, n);
+    if (rc) return rc;
+    const int ksplit = gemm_ksplit(ctx, m, n);  // the decode step's choice (<= 8 splits)
+    GemvInput in;
+    in.x = x;
+    if (ksplit == 1) return launch_gemv_packed(ctx, ctx->stream, ggml_type, wp, m, n, in, y, 1);
+    if ((rc = ensure_workspace(ctx, (size_t)ksplit * m, 0))) return rc;
+    if ((rc = launch_gemv_packed(ctx, ctx->stream, ggml_type, wp, m, n, in, ctx->ws.partial, ksplit))) return rc;
+    return launch_sum_partials(ctx, ctx->stream, ctx->ws.partial, y, m, ksplit);
+}
+
 }  // extern "C"

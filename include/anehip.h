@@ -162,6 +162,26 @@ int anehip_timer_stop(anehip_ctx *ctx, float *ms);
 int anehip_quant_gemm(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32_t m,
                       uint32_t n, const float *x, uint32_t batch, float *y);
 
+/*
+ * Panel layout: a GPU-native permutation of the same Q8_0 / Q4_0 bytes (rows
+ * in tiles of 64, each cut into 256-column panels whose 16-byte quant chunks
+ * are interleaved across the 64 rows, the rows' block scales after them) that
+ * lets every lane of a wave stream its own row with fully coalesced loads.
+ * No counterpart in the reference, which reads the GGUF blocks directly
+ * (q8_gemv.metal:15-87); the decode step builds it itself, these entry points
+ * expose it to callers that run their own batch-1 GEMVs over resident weights.
+ *
+ * anehip_quant_packed_bytes: size of the panel copy of an [m x n] matrix
+ * (n a multiple of 256), or 0 for an unsupported type / shape.
+ * anehip_quant_pack: dst <- panel copy of the m*(n/32) GGUF blocks at w.
+ * anehip_quant_gemv_packed: y[r] = W[r] . x for r < m from the panel copy wp
+ * (same result as anehip_quant_gemm with batch 1, up to fp32 summation order).
+ */
+size_t anehip_quant_packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
+int anehip_quant_pack(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n, void *dst);
+int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
+                             const float *x, float *y);
+
 /* Row-wise RMSNorm: out[r] = x[r] * 1/sqrt(mean(x[r]^2) + eps) * w, rows x n.
  * rmsnorm_simple (deltanet.metal:239-272) / rmsnorm_vec (main.rs:1106-1113). */
 int anehip_rmsnorm(anehip_ctx *ctx, const float *x, const float *w, float *out, uint32_t rows, uint32_t n,

@@ -1,0 +1,102 @@
+"""The panel weight layout of the batch-1 decode path (anehip_quant_pack /
+anehip_quant_gemv_packed): the repack is a pure byte permutation, pinned here
+bit-exactly against an independent numpy statement of the layout, and the
+GEMV over panels matches the oracle's q8_gemv / q4_gemv_cpu restatement
+(crates/engine/src/q8_gemv.rs:67-148) to 1e-4 relative, including ragged row
+counts and K ranges long enough to take several rounds per workgroup."""
+import numpy as np
+import pytest
+
+from conftest import rel_errs
+
+TOL = 1e-4
+
+
+def pack_ref(t, w, m, n):
+    """Panel layout: row tiles of 64 (zero rows past m), 256-column panels;
+    a panel is [chunk][64 rows][16 B] quant bytes then [64 rows][8 fp16] scales.
+    Q8_0 chunk c = half (c % 2) of block c // 2; Q4_0 chunk c = block c's nibbles."""
+    bb = 34 if t == 8 else 18
+    nb, nsb, tiles = n // 32, n // 256, (m + 63) // 64
+    pad = np.zeros((tiles * 64, nb, bb), np.uint8)
+    pad[:m] = w.reshape(m, nb, bb)
+    b = pad.reshape(tiles, 64, nsb, 8, bb)
+    if t == 8:
+        q = b[..., 2:34].reshape(tiles, 64, nsb, 16, 16)
+    else:
+        q = b[..., 2:18]
+    q = q.transpose(0, 2, 3, 1, 4)                                   # tile, sb, chunk, row, byte
+    sc = b[..., 0:2].reshape(tiles, 64, nsb, 16).transpose(0, 2, 1, 3)  # tile, sb, row, scale bytes
+    return np.concatenate([q.reshape(tiles, nsb, -1), sc.reshape(tiles, nsb, -1)], axis=2).reshape(-1)
+
+
+def test_packed_bytes(anehip_mod):
+    f = anehip_mod.lib().anehip_quant_packed_bytes
+    assert f(8, 64, 256) == 17 * 1024
+    assert f(2, 64, 256) == 9 * 1024
+    assert f(8, 65, 512) == 2 * 2 * 17 * 1024
+    assert f(8, 64, 100) == 0 and f(14, 64, 256) == 0 and f(8, 0, 256) == 0
+
+
+def test_pack_ref_is_a_permutation(oracle_lib):
+    """The numpy layout keeps every byte once (rows padded with zeros)."""
+    m, n = 70, 512
+    w = oracle_lib.gen_quant(8, 1, 2, m, n)
+    p = pack_ref(8, w, m, n)
+    assert p.size == 2 * 2 * 17 * 1024
+    assert np.array_equal(np.sort(p[p != 0]), np.sort(w[w != 0]))
+
+
+def _pack(ctx, t, w, m, n):
+    import anehip
+
+    nbytes = int(anehip.lib().anehip_quant_packed_bytes(t, m, n))
+    dw, dp = ctx.to_device(w), ctx.alloc(nbytes)
+    ctx.call("quant_pack", t, dw, m, n, dp)
+    return dw, dp, nbytes
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("m,n", [(64, 256), (100, 512), (130, 2048), (1, 256)])
+def test_repack_bit_exact(gpu_ctx, oracle_lib, t, m, n):
+    w = oracle_lib.gen_quant(t, 21, m + n + t, m, n, std=0.02)
+    dw, dp, nbytes = _pack(gpu_ctx, t, w, m, n)
+    got = dp.download(np.uint8, nbytes)
+    assert np.array_equal(got, pack_ref(t, w, m, n))
+    dw.free()
+    dp.free()
+
+
+SHAPES = [(6144, 2048), (2048, 6144), (248320, 2048), (16, 2048), (100, 256), (8224, 2048), (300, 20480),
+          (64, 32768)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("m,n", SHAPES)
+def test_packed_gemv_parity(gpu_ctx, oracle_lib, t, m, n):
+    w = oracle_lib.gen_quant(t, 4321, m * 3 + n + t, m, n, std=0.02)
+    x = oracle_lib.normal(4321, 7 + n, n)
+    dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
+    dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(m * 4)
+    gpu_ctx.call("quant_gemv_packed", t, dp, m, n, dx, dy)
+    y = dy.download(np.float32, m)
+    ref = oracle_lib.gemv(t, w, m, n, x)
+    l2, mx = rel_errs(y, ref)
+    print(f"type={t} m={m} n={n}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+    assert l2 <= TOL and mx <= TOL
+    for b in (dw, dp, dx, dy):
+        b.free()
+
+
+@pytest.mark.gpu
+def test_packed_rejects_bad_shapes(gpu_ctx, anehip_mod):
+    d = gpu_ctx.alloc(17 * 1024)
+    with pytest.raises(anehip_mod.AnehipError) as e:
+        gpu_ctx.call("quant_pack", 8, d, 64, 100, d)
+    assert e.value.code == -2
+    with pytest.raises(anehip_mod.AnehipError) as e:
+        gpu_ctx.call("quant_gemv_packed", 14, d, 64, 256, d, d)
+    assert e.value.code == -3
+    d.free()
