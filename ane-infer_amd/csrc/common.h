@@ -156,6 +156,8 @@ int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, 
 size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
 int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
                   void *dst);
+// K splits the batch-1 panel GEMV takes for an [m x n] matrix (<= 8).
+int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
 int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                        uint32_t n, const GemvInput &in, float *out, int ksplit);
 // Small-batch GEMM (batch 2..32) on MFMA from fp16 hi/lo input planes

@@ -297,7 +297,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in1.token = M->d_tokens;
         in1.emb = M->embedding;
         in1.vocab = D.vocab_size;
-        const int k1 = gemm_ksplit(ctx, rows_in, d);
+        const int k1 = gemv_packed_ksplit(ctx, rows_in, d);
         TRY(launch_gemv_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, in1, M->pmix, k1));
         std::swap(cur, nxt);
         MixIn mix;
@@ -329,7 +329,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
             in3.x = M->attn_out;
             cols3 = qd;
         }
-        const int k3 = gemm_ksplit(ctx, d, cols3);
+        const int k3 = gemv_packed_ksplit(ctx, d, cols3);
         TRY(launch_gemv_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, in3, M->p0, k3));
         // 4. FFN gate/up, input = RMSNorm(residual + mixer output)
         GemvInput in4;
@@ -341,7 +341,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in4.w = L.post_attn_norm;
         in4.eps = eps;
         in4.x_out = nxt;
-        const int k4 = gemm_ksplit(ctx, 2 * F, d);
+        const int k4 = gemv_packed_ksplit(ctx, 2 * F, d);
         TRY(launch_gemv_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, in4, M->p1, k4));
         std::swap(cur, nxt);
         // 5. FFN down, input = SiLU(gate) * up
@@ -350,7 +350,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in5.part = M->p1;
         in5.kp = k4;
         in5.part_stride = 2 * F;
-        const int k5 = gemm_ksplit(ctx, d, F);
+        const int k5 = gemv_packed_ksplit(ctx, d, F);
         TRY(launch_gemv_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, in5, M->p0, k5));
         prev_part = M->p0;
         prev_kp = k5;
@@ -365,7 +365,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     inf.w = M->final_norm;
     inf.eps = eps;
     inf.x_out = nxt;
-    const int kf = gemm_ksplit(ctx, D.vocab_size, d);
+    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d);
     if (kf == 1) {
         TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->logits, 1));
     } else {
@@ -452,7 +452,8 @@ size_t part_floats(anehip_ctx *ctx, Model *M) {
     size_t mx = 0;
     for (auto &e : g) {
         if (!e.m) continue;
-        size_t need = (size_t)gemm_ksplit(ctx, e.m, e.n) * M->batch * e.m;
+        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n) : gemm_ksplit(ctx, e.m, e.n);
+        size_t need = (size_t)k * M->batch * e.m;
         if (need > mx) mx = need;
     }
     return mx;

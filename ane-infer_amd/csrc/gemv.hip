@@ -139,13 +139,18 @@ __device__ __forceinline__ float wave_sum64(float v) {
     return v;
 }
 
-// Sum over a 256-thread workgroup; every thread gets the total.
-__device__ __forceinline__ float wg_sum(float v, float *red4) {
+// Sum over an NT-thread workgroup (red: NT / 64 floats of LDS); every thread
+// gets the total.
+template <int NT = 256>
+__device__ __forceinline__ float wg_sum(float v, float *red) {
     v = wave_sum64(v);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return (red4[0] + red4[1]) + (red4[2] + red4[3]);
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) s += red[w];
+    return s;
 }
 
 constexpr int kMaxSplit = 8;     // K splits a consumer may have to add
@@ -165,50 +170,53 @@ __device__ __forceinline__ float sum_parts(const float *__restrict__ part, int k
 }
 
 // Forms the workgroup's input slice xs[0, len) = input[c0, c0 + len) of length-n
-// input vector `in` (see GemvInMode).  256 threads.  Every mode issues its
-// global loads in batches of RB elements per thread, then computes, so with
-// RB = 8 the prologue costs about one memory round trip; smaller RB trades
-// round trips for registers.
+// input vector `in` (see GemvInMode), with NT threads (red: NT / 64 floats of
+// LDS).  Every mode issues its global loads in batches of RB elements per
+// thread, then computes, so with RB = 8 the prologue costs about one memory
+// round trip; smaller RB trades round trips for registers.
 //
 // `first` is false when a workgroup forms a second slice of the same input in
 // one launch: the one-off side effects (the x_out copy, the conv-window
 // commit) are then skipped.
-template <int MODE, int RB = 8>
-__device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0, int len, float *xs, float *red4,
+template <int MODE, int RB = 8, int NT = 256>
+__device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0, int len, float *xs, float *red,
                                               bool first = true) {
+    constexpr int IT = kMaxSliceSb * 256 / NT;  // slice elements per thread
     const int t = threadIdx.x;
     if constexpr (MODE == GEMV_IN_PLAIN) {
-        float v[kMaxSliceSb];
+        float v[IT];
 #pragma unroll
-        for (int i = 0; i < kMaxSliceSb; i++) v[i] = t + 256 * i < len ? in.x[c0 + t + 256 * i] : 0.0f;
+        for (int i = 0; i < IT; i++) v[i] = t + NT * i < len ? in.x[c0 + t + NT * i] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < kMaxSliceSb; i++)
-            if (t + 256 * i < len) xs[t + 256 * i] = v[i];
+        for (int i = 0; i < IT; i++)
+            if (t + NT * i < len) xs[t + NT * i] = v[i];
     } else if constexpr (MODE == GEMV_IN_SILU_MUL) {
         // scratch.rs:181-186: a = (a / (1 + exp(-a))) * b
-        for (int i0 = 0; i0 < kMaxSliceSb && 256 * i0 < len; i0 += RB) {
-            float g[RB], u[RB];
+        constexpr int B = RB < IT ? RB : IT;
+        for (int i0 = 0; i0 < IT && NT * i0 < len; i0 += B) {
+            float g[B], u[B];
 #pragma unroll
-            for (int i = 0; i < RB; i++) {
-                const int j = min(t + 256 * (i0 + i), len - 1);
+            for (int i = 0; i < B; i++) {
+                const int j = min(t + NT * (i0 + i), len - 1);
                 g[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)c0 + j);
                 u[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)n + c0 + j);
             }
 #pragma unroll
-            for (int i = 0; i < RB; i++)
-                if (t + 256 * (i0 + i) < len) xs[t + 256 * (i0 + i)] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+            for (int i = 0; i < B; i++)
+                if (t + NT * (i0 + i) < len) xs[t + NT * (i0 + i)] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
         }
     } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
         // deltanet.rs:517-533, per 128-wide head; a wave handles whole heads
-        // (at most 4 per wave for a slice of 8 super-blocks)
+        constexpr int W = NT / 64;                      // waves
+        constexpr int HI = kMaxSliceSb * 2 / W;         // heads per wave for a full slice
+        constexpr int HB = RB >= 8 ? HI : (RB >= 4 ? (HI < 2 ? HI : 2) : 1);
         const int lane = t & 63, wave = t >> 6;
         const int nh = len / 128;
-        constexpr int HB = RB >= 8 ? 4 : (RB >= 4 ? 2 : 1);
-        for (int i0 = 0; i0 < 4; i0 += HB) {
+        for (int i0 = 0; i0 < HI; i0 += HB) {
             float a[HB], b[HB], ga[HB], gb[HB];
 #pragma unroll
             for (int i = 0; i < HB; i++) {
-                const int hh = min(wave + 4 * (i0 + i), nh - 1);
+                const int hh = min(wave + W * (i0 + i), nh - 1);
                 const int k0 = c0 + hh * 128;
                 a[i] = in.x[k0 + lane];
                 b[i] = in.x[k0 + 64 + lane];
@@ -217,7 +225,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
             }
 #pragma unroll
             for (int i = 0; i < HB; i++) {
-                const int hh = wave + 4 * (i0 + i);
+                const int hh = wave + W * (i0 + i);
                 const float ss = wave_sum64(a[i] * a[i] + b[i] * b[i]);
                 if (hh < nh) {
                     const float inv_rms = 1.0f / sqrtf(ss / 128.0f + in.eps);
@@ -230,7 +238,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
         // commit the q/k conv windows, spread over the launch's workgroups
         if (in.conv_state && first) {
             const int nwg = gridDim.x * gridDim.y, wg = blockIdx.y * gridDim.x + blockIdx.x;
-            for (int c = wg * 256 + t; c < 2 * n; c += nwg * 256) {
+            for (int c = wg * NT + t; c < 2 * n; c += nwg * NT) {
                 float4 *cs = reinterpret_cast<float4 *>(in.conv_state) + c;
                 const float4 o = *cs;
                 const float nv = sum_parts(in.part, in.kp, in.part_stride, (size_t)c);
@@ -243,13 +251,13 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
         // (main.rs:1106-1113: out = (r * inv_rms) * w).  Residual: r = x + s
         // with s the partials added in split order.
         const bool writer = first && blockIdx.x == 0 && blockIdx.y == 0;
-        const uint32_t tok = MODE == GEMV_IN_EMBED_RMSNORM ? in.token[0] : 0u;
+        const uint32_t tok = MODE == GEMV_IN_EMBED_RMSNORM ? in.token[0] : 0;
         float ss = 0.0f;
-        for (int base = 0; base < n; base += 256 * RB) {
+        for (int base = 0; base < n; base += NT * RB) {
             float r[RB];
 #pragma unroll
             for (int i = 0; i < RB; i++) {
-                const int k = min(base + t + 256 * i, n - 1);
+                const int k = min(base + t + NT * i, n - 1);
                 if constexpr (MODE == GEMV_IN_EMBED_RMSNORM) {
                     r[i] = tok < in.vocab ? in.emb[(size_t)tok * n + k] : 0.0f;
                 } else if constexpr (MODE == GEMV_IN_RESID_RMSNORM) {
@@ -260,7 +268,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
             }
 #pragma unroll
             for (int i = 0; i < RB; i++) {
-                const int k = base + t + 256 * i;
+                const int k = base + t + NT * i;
                 if (k < n) {
                     ss += r[i] * r[i];
                     if (k >= c0 && k < c0 + len) xs[k - c0] = r[i];
@@ -268,9 +276,9 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
                 }
             }
         }
-        ss = wg_sum(ss, red4);
+        ss = wg_sum<NT>(ss, red);
         const float inv_rms = 1.0f / sqrtf(ss / (float)n + in.eps);
-        for (int j = t; j < len; j += 256) xs[j] = (xs[j] * inv_rms) * in.w[c0 + j];
+        for (int j = t; j < len; j += NT) xs[j] = (xs[j] * inv_rms) * in.w[c0 + j];
     }
     __syncthreads();
 }
@@ -391,33 +399,69 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     reinterpret_cast<u32x4 *>(dst)[v] = w;
 }
 
-// Dot product of one panel row held in registers (q: quant vectors of the
-// lane's row; sc: its 8 block scales) with x[0..255] (wave-uniform, so
-// scalar loads), per block then scaled (q8_gemv.rs:234-242).
-template <uint32_t T>
-__device__ __forceinline__ float panel_dot(const u32x4 *q, const u32x4 &sc, const float *__restrict__ x, float acc) {
+// A wave's share of a panel: blocks [NB * part, NB * (part + 1)) of the 8,
+// i.e. kChunks * NB / 8 quant vectors, plus the panel's scale vector.
+template <uint32_t T, int NB>
+struct PanelPart {
+    static constexpr int kVecs = Panel<T>::kChunks * NB / 8;
+};
+
+// Loads one wave's share of a panel.  Idle waves (valid false) load one
+// 16-byte vector of the panel base with all lanes instead, so every wave
+// issues the same, unconditional load sequence.
+template <uint32_t T, int NB>
+__device__ __forceinline__ void load_part(u32x4 *q, u32x4 &sc, const uint8_t *panel, const uint8_t *dummy, int part,
+                                          int lane, bool valid) {
+    const u32x4 *p4 = reinterpret_cast<const u32x4 *>(valid ? panel : dummy);
+    const int l = valid ? lane : 0;
+    constexpr int V = PanelPart<T, NB>::kVecs;
+    const int c0 = valid ? V * part : 0;
+#pragma unroll
+    for (int c = 0; c < V; c++) q[c] = __builtin_nontemporal_load(p4 + (c0 + c) * 64 + l);
+    sc = __builtin_nontemporal_load(p4 + Panel<T>::kChunks * 64 + l);
+}
+
+// Dot product of a wave's panel share held in registers (q, sc: see
+// load_part) with x[32 * blk] for its blocks (x: the panel's 256 inputs,
+// wave-uniform, so scalar loads from global memory or broadcast LDS reads):
+// per block, then scaled (q8_gemv.rs:234-242).
+template <uint32_t T, int NB>
+__device__ __forceinline__ float panel_dot(const u32x4 *q, const u32x4 &sc, const float *__restrict__ x, int part,
+                                           float acc) {
     const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
-    for (int b = 0; b < 8; b++) {
-        const float d = __half2float(__ushort_as_half((unsigned short)(scw[b >> 1] >> (16 * (b & 1)))));
+    for (int j = 0; j < NB; j++) {
+        const int b = NB * part + j;  // block within the panel
+        uint32_t word;
+        if constexpr (NB == 8) {
+            word = scw[j >> 1];
+        } else {
+            // b >> 1 is wave-uniform but not a compile-time index
+            const int wi = b >> 1;
+            word = wi == 0 ? scw[0] : wi == 1 ? scw[1] : wi == 2 ? scw[2] : scw[3];
+        }
+        const float d = __half2float(__ushort_as_half((unsigned short)(word >> (16 * (b & 1)))));
+        const float *xb = x + 32 * b;
         float bs = 0.0f;
         if constexpr (T == ANEHIP_GGML_Q8_0) {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const uint32_t w4[4] = {q[2 * b + h].x, q[2 * b + h].y, q[2 * b + h].z, q[2 * b + h].w};
+                const u32x4 v = q[2 * j + h];
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int qi = (int)(int8_t)(w4[i >> 2] >> (8 * (i & 3)));
-                    bs = fmaf((float)qi, x[32 * b + 16 * h + i], bs);
+                    bs = fmaf((float)qi, xb[16 * h + i], bs);
                 }
             }
         } else {
-            const uint32_t w4[4] = {q[b].x, q[b].y, q[b].z, q[b].w};
+            const u32x4 v = q[j];
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const uint32_t byte = (w4[i >> 2] >> (8 * (i & 3))) & 0xffu;
-                bs = fmaf((float)((int)(byte & 15u) - 8), x[32 * b + i], bs);
-                bs = fmaf((float)((int)(byte >> 4) - 8), x[32 * b + 16 + i], bs);
+                bs = fmaf((float)((int)(byte & 15u) - 8), xb[i], bs);
+                bs = fmaf((float)((int)(byte >> 4) - 8), xb[16 + i], bs);
             }
         }
         acc = fmaf(bs, d, acc);
@@ -425,64 +469,239 @@ __device__ __forceinline__ float panel_dot(const u32x4 *q, const u32x4 &sc, cons
     return acc;
 }
 
-template <uint32_t T>
-__device__ __forceinline__ void load_panel(u32x4 *q, u32x4 &sc, const uint8_t *panel, int lane) {
-    const u32x4 *p = reinterpret_cast<const u32x4 *>(panel);
-#pragma unroll
-    for (int c = 0; c < Panel<T>::kChunks; c++) q[c] = __builtin_nontemporal_load(p + c * 64 + lane);
-    sc = __builtin_nontemporal_load(p + Panel<T>::kChunks * 64 + lane);
+// ---------------------------------------------------------------------------
+// Overlapped prologue of the panel GEMV.  The slow part of a prologue is its
+// global-load round trip, and vmcnt waits are in issue order, so the loads
+// of the input (x, residual partial slices, norm weights, gates) are issued
+// first, then `issue()` starts the workgroup's weight loads, and only then is
+// the input formed -- its wait no longer includes the weights.  Fast paths
+// take the shapes of the decode step (norms over n <= 2048, SiLU-mul and
+// gated-norm slices <= 1024, 16-byte aligned slices) with float4 loads and KP
+// (2 or 8) partial slices per value; anything else falls back to issue() +
+// the generic prologue.  Same arithmetic per element as gemv_prologue.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
 
-// Batch-1 GEMV over panels: grid = (row tiles, K splits), 4 waves per
-// workgroup.  The workgroup's K range is taken in rounds of up to 8 panels
-// (one round unless n is large); in a round wave w owns panels r0 + w and
-// r0 + w + 4 and issues both loads before any other work.  The 4 waves are
-// reduced through LDS.  The input slice comes straight from in.x (plain:
-// wave-uniform, so scalar loads) or from the prologue (fused modes: LDS,
-// broadcast reads).
-template <uint32_t T, int MODE>
-__global__ __launch_bounds__(kWave *kWavesPerWg) void gemv_packed(const uint8_t *__restrict__ Wp, GemvInput in,
-                                                                 float *__restrict__ out, int m, int n,
-                                                                 int sb_per_split, size_t split_stride) {
-    constexpr int NC = Panel<T>::kChunks;
-    __shared__ float xs[kMaxSliceSb * 256];
-    __shared__ float red[kWavesPerWg][kWave];
-    __shared__ float red4[4];
+__device__ __forceinline__ float half_sum32(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float silu1(float g) { return g / (1.0f + expf(-g)); }
+
+// KP unconditional loads (slices past kp re-read slice kp - 1) and their
+// branch-free sum in split order: straight-line code keeps the compiler's
+// vmcnt accounting exact, so waiting for these loads does not wait for
+// loads issued after them.
+template <int KP>
+__device__ __forceinline__ void load_parts4(float4 *v, const float *part, int kp, size_t stride, size_t off4) {
+    const float4 *p4 = reinterpret_cast<const float4 *>(part);
+#pragma unroll
+    for (int p = 0; p < KP; p++) v[p] = p4[(size_t)min(p, max(kp - 1, 0)) * (stride / 4) + off4];
+}
+
+template <int KP>
+__device__ __forceinline__ float4 sum_parts4(const float4 *v, int kp) {
+    float4 s = v[0];
+#pragma unroll
+    for (int p = 1; p < KP; p++) {
+        const bool on = p < kp;
+        s.x += on ? v[p].x : 0.0f;
+        s.y += on ? v[p].y : 0.0f;
+        s.z += on ? v[p].z : 0.0f;
+        s.w += on ? v[p].w : 0.0f;
+    }
+    return s;
+}
+
+// Whether prologue_overlapped covers this launch (a single slice of len
+// floats per workgroup; uniform).
+template <int MODE, int NT>
+__device__ __forceinline__ bool overlapped_ok(const GemvInput &in, int n, int len) {
+    if constexpr (MODE == GEMV_IN_PLAIN) return false;
+    const bool aligned = ((in.part_stride | (size_t)in.gate_off) & 3) == 0;
+    if constexpr (MODE == GEMV_IN_RMSNORM || MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_EMBED_RMSNORM)
+        return n <= 4 * NT && aligned;
+    if constexpr (MODE == GEMV_IN_SILU_MUL) return len <= 4 * NT && aligned;
+    if constexpr (MODE == GEMV_IN_GATED_NORM)
+        return len <= 4 * NT && aligned && (!in.conv_state || 2 * n <= (int)(gridDim.x * gridDim.y) * NT);
+    return false;
+}
+
+template <int MODE, int KP, int NT, class Issue>
+__device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, int c0, int len, float *xs,
+                                                    float *red, Issue &&issue) {
+    const int t = threadIdx.x;
+    float4 *xs4 = reinterpret_cast<float4 *>(xs);
+    if constexpr (MODE == GEMV_IN_RMSNORM || MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_EMBED_RMSNORM) {
+        // one float4 of the n-vector per thread
+        const int n4 = n >> 2, e4 = min(t, n4 - 1);
+        const float4 *src;
+        bool zero = false;
+        if constexpr (MODE == GEMV_IN_EMBED_RMSNORM) {
+            const uint32_t tok = in.token[0];
+            zero = tok >= in.vocab;
+            src = reinterpret_cast<const float4 *>(in.emb + (size_t)(zero ? 0u : tok) * n);
+        } else {
+            src = reinterpret_cast<const float4 *>(in.x);
+        }
+        float4 r = src[e4];
+        const float4 w = reinterpret_cast<const float4 *>(in.w)[e4];
+        float4 pv[KP];
+        if constexpr (MODE == GEMV_IN_RESID_RMSNORM) load_parts4<KP>(pv, in.part, in.kp, in.part_stride, e4);
+        issue();
+        if (zero) r = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (MODE == GEMV_IN_RESID_RMSNORM) r = f4_add(r, sum_parts4<KP>(pv, in.kp));
+        float ss = 0.0f;
+        if (t < n4) {
+            ss = r.x * r.x;
+            ss += r.y * r.y;
+            ss += r.z * r.z;
+            ss += r.w * r.w;
+            if (MODE != GEMV_IN_RMSNORM && blockIdx.x == 0 && blockIdx.y == 0)
+                reinterpret_cast<float4 *>(in.x_out)[t] = r;
+        }
+        ss = wg_sum<NT>(ss, red);
+        const float inv_rms = 1.0f / sqrtf(ss / (float)n + in.eps);
+        const int e = 4 * t;
+        if (t < n4 && e >= c0 && e < c0 + len)
+            xs4[(e - c0) >> 2] = make_float4((r.x * inv_rms) * w.x, (r.y * inv_rms) * w.y, (r.z * inv_rms) * w.z,
+                                             (r.w * inv_rms) * w.w);
+        __syncthreads();
+    } else if constexpr (MODE == GEMV_IN_SILU_MUL) {
+        const int e4 = min(t, (len >> 2) - 1);
+        float4 g[KP], u[KP];
+        load_parts4<KP>(g, in.part, in.kp, in.part_stride, (size_t)(c0 >> 2) + e4);
+        load_parts4<KP>(u, in.part, in.kp, in.part_stride, (size_t)((n + c0) >> 2) + e4);
+        issue();
+        const float4 gs = sum_parts4<KP>(g, in.kp), us = sum_parts4<KP>(u, in.kp);
+        if (t < (len >> 2))
+            xs4[t] = make_float4(silu1(gs.x) * us.x, silu1(gs.y) * us.y, silu1(gs.z) * us.z, silu1(gs.w) * us.w);
+        __syncthreads();
+    } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
+        const int nwg = gridDim.x * gridDim.y, wg = blockIdx.y * gridDim.x + blockIdx.x;
+        const bool commit = in.conv_state != nullptr;
+        // one 128-wide head per 32 threads (deltanet.rs:517-533)
+        const int e4 = min(t, (len >> 2) - 1);
+        const float4 a = reinterpret_cast<const float4 *>(in.x)[(c0 >> 2) + e4];
+        const float4 w = reinterpret_cast<const float4 *>(in.w)[e4 & 31];
+        float4 ga[KP];
+        load_parts4<KP>(ga, in.part, in.kp, in.part_stride, (size_t)((in.gate_off + c0) >> 2) + e4);
+        // the q/k conv-window commit, at most one window per thread of the launch
+        const int c = wg * NT + t;
+        const bool has = commit && c < 2 * n;
+        float4 old = make_float4(0.f, 0.f, 0.f, 0.f);
+        float nv[KP];
+        {
+            // (loads stay in bounds and unconditional; only `has` lanes store)
+            const int cc = commit ? min(c, 2 * n - 1) : 0;
+            old = reinterpret_cast<const float4 *>(commit ? in.conv_state : in.x)[cc];
+#pragma unroll
+            for (int p = 0; p < KP; p++) nv[p] = in.part[(size_t)min(p, max(in.kp - 1, 0)) * in.part_stride + cc];
+        }
+        issue();
+        const float ss = half_sum32(a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w);
+        const float inv_rms = 1.0f / sqrtf(ss / 128.0f + in.eps);
+        const float4 g = sum_parts4<KP>(ga, in.kp);
+        if (t < (len >> 2))
+            xs4[t] = make_float4(((a.x * inv_rms) * w.x) * silu1(g.x), ((a.y * inv_rms) * w.y) * silu1(g.y),
+                                 ((a.z * inv_rms) * w.z) * silu1(g.z), ((a.w * inv_rms) * w.w) * silu1(g.w));
+        if (has) {
+            float sv = nv[0];
+#pragma unroll
+            for (int p = 1; p < KP; p++) sv += p < in.kp ? nv[p] : 0.0f;
+            reinterpret_cast<float4 *>(in.conv_state)[c] = make_float4(old.y, old.z, old.w, sv);
+        }
+        __syncthreads();
+    }
+}
+
+// Batch-1 GEMV over panels: grid = (row-tile groups, K splits), 8 waves per
+// workgroup.  Each panel is shared by S waves (S = 1, 2, 4, 8; wave w takes
+// part w % S, 8 / S blocks, of panel w / S), so a round covers 8 / S panels
+// and small K slices still keep all 8 waves loading.  A workgroup covers
+// `tiles_per_wg` consecutive 64-row tiles with one input slice (the prologue
+// runs once).  When the slice fits one round, the input loads are issued
+// before the weight loads (prologue_overlapped); otherwise rounds take the
+// generic prologue.  Every wave issues its weight loads unconditionally (idle
+// waves read one shared vector), which keeps the vmcnt waits exact.  The 8
+// waves are reduced through LDS; the result (or this split's partial sum)
+// goes to out[ks * split_stride + row].
+constexpr int kPackedWaves = 8;
+
+template <uint32_t T, int MODE, int KP, int S>
+__global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t *__restrict__ Wp, GemvInput in,
+                                                                  float *__restrict__ out, int m, int n,
+                                                                  int sb_per_split, size_t split_stride,
+                                                                  int tiles_per_wg) {
+    constexpr int NB = 8 / S, P = kPackedWaves / S, V = PanelPart<T, NB>::kVecs;
+    constexpr int NT = kWave * kPackedWaves;
+    __shared__ __align__(16) float xs[kMaxSliceSb * 256];
+    __shared__ float red[kPackedWaves][kWave];
+    __shared__ float redw[kPackedWaves];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int tile = blockIdx.x, ks = blockIdx.y;
-    const int nsb = n >> 8;
+    const int pi = wave / S, part = wave % S;
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
+    const int ks = blockIdx.y;
     const int sb_begin = ks * sb_per_split;
     const int sb_end = min(nsb, sb_begin + sb_per_split);
-    const uint8_t *tile_base = Wp + (size_t)tile * nsb * Panel<T>::kBytes;
+    const int t0 = blockIdx.x * tiles_per_wg, t1 = min(tiles, t0 + tiles_per_wg);
+    const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
+    bool fast = sb_end - sb_begin <= P;
+    if constexpr (MODE != GEMV_IN_PLAIN) fast = fast && overlapped_ok<MODE, NT>(in, n, (sb_end - sb_begin) * 256);
 
-    float acc = 0.0f;
-    for (int r0 = sb_begin; r0 < sb_end; r0 += kMaxSliceSb) {
-        const int r1 = min(sb_end, r0 + kMaxSliceSb);
-        const int sb0 = r0 + wave, sb1 = sb0 + kWavesPerWg;
-        u32x4 qa[NC], sa, qb[NC], sbk;
-        if (sb0 < r1) load_panel<T>(qa, sa, tile_base + (size_t)sb0 * Panel<T>::kBytes, lane);
-        if (sb1 < r1) load_panel<T>(qb, sbk, tile_base + (size_t)sb1 * Panel<T>::kBytes, lane);
-        const float *xg;
-        if constexpr (MODE == GEMV_IN_PLAIN) {
-            xg = in.x + r0 * 256;
+    u32x4 q[V], sc;
+    for (int tile = t0; tile < t1; tile++) {
+        const uint8_t *tb = Wp + (size_t)tile * tile_bytes;
+        float acc = 0.0f;
+        if (fast) {
+            const int sb = sb_begin + pi;
+            const bool valid = sb < sb_end;
+            const uint8_t *pp = tb + (size_t)sb * Panel<T>::kBytes;
+            if (MODE != GEMV_IN_PLAIN && tile == t0) {
+                auto issue = [&]() { load_part<T, NB>(q, sc, pp, Wp, part, lane, valid); };
+                prologue_overlapped<MODE, KP, NT>(in, n, sb_begin * 256, (sb_end - sb_begin) * 256, xs, redw, issue);
+            } else {
+                load_part<T, NB>(q, sc, pp, Wp, part, lane, valid);
+            }
+            const float *xg = MODE == GEMV_IN_PLAIN ? in.x + sb_begin * 256 : xs;
+            if (valid) acc = panel_dot<T, NB>(q, sc, xg + pi * 256, part, acc);
         } else {
-            if (r0 != sb_begin) __syncthreads();  // the previous round's reads of xs are done
-            gemv_prologue<MODE, 2>(in, n, r0 * 256, (r1 - r0) * 256, xs, red4, r0 == sb_begin);
-            xg = xs;
+            for (int r0 = sb_begin; r0 < sb_end; r0 += P) {
+                const int r1 = min(sb_end, r0 + P);
+                const int sb = r0 + pi;
+                const bool valid = sb < r1;
+                load_part<T, NB>(q, sc, tb + (size_t)sb * Panel<T>::kBytes, Wp, part, lane, valid);
+                const float *xg;
+                if constexpr (MODE == GEMV_IN_PLAIN) {
+                    xg = in.x + r0 * 256;
+                } else {
+                    if (r0 != sb_begin) __syncthreads();  // the previous round's reads of xs are done
+                    gemv_prologue<MODE, 2, NT>(in, n, r0 * 256, (r1 - r0) * 256, xs, redw,
+                                               tile == t0 && r0 == sb_begin);
+                    xg = xs;
+                }
+                if (valid) acc = panel_dot<T, NB>(q, sc, xg + (sb - r0) * 256, part, acc);
+            }
         }
-        if (sb0 < r1) acc = panel_dot<T>(qa, sa, xg + (sb0 - r0) * 256, acc);
-        if (sb1 < r1) acc = panel_dot<T>(qb, sbk, xg + (sb1 - r0) * 256, acc);
-    }
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave != 0) return;
-    const int row = tile * kWave + lane;
-    if (row >= m) return;
-    float sum = red[0][lane];
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave == 0) {
+            const int row = tile * kWave + lane;
+            if (row < m) {
+                float sum = red[0][lane];
 #pragma unroll
-    for (int v = 1; v < kWavesPerWg; v++) sum += red[v][lane];
-    out[(size_t)ks * split_stride + row] = sum;
+                for (int v = 1; v < kPackedWaves; v++) sum += red[v][lane];
+                out[(size_t)ks * split_stride + row] = sum;
+            }
+        }
+        __syncthreads();  // red (and, in the generic path, xs) are reused by the next tile
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -755,9 +974,27 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
 
 }  // namespace
 
+// K splits of the batch-1 panel GEMV: the fewest that give every CU a
+// workgroup (at most kMaxSplit, whole panels, no empty split).
+static int packed_ksplit(int tiles, int nsb, int cus) {
+    int best = 1;
+    for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
+        const int per = (nsb + k - 1) / k;
+        if ((k - 1) * per >= nsb) continue;
+        best = k;
+        if (tiles * k >= cus && per <= kMaxSliceSb) return k;
+    }
+    return best;
+}
+
 int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int max_k) {
     const int tiles = (int)((m + kWave - 1) / kWave);
     return choose_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256, max_k);
+}
+
+int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+    const int tiles = (int)((m + kWave - 1) / kWave);
+    return packed_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256);
 }
 
 size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n) {
@@ -779,13 +1016,44 @@ int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const
     return ANEHIP_OK;
 }
 
+
+template <uint32_t T, int MODE, int KP, int S>
+void launch_packed_s(hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n, const GemvInput &in, float *out,
+                     int ksplit, int per, int tpw) {
+    const int tiles = (int)((m + kWave - 1) / kWave);
+    const dim3 grid((tiles + tpw - 1) / tpw, ksplit), block(kWave * kPackedWaves);
+    hipLaunchKernelGGL((gemv_packed<T, MODE, KP, S>), grid, block, 0, stream, w, in, out, (int)m, (int)n, per,
+                       (size_t)m, tpw);
+}
+
+template <uint32_t T, int MODE, int KP>
+void launch_packed_k(hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n, const GemvInput &in, float *out,
+                     int ksplit, int per, int tpw) {
+    // waves per panel: as many as keep one round covering the slice
+    if (per <= 1) launch_packed_s<T, MODE, KP, 8>(stream, w, m, n, in, out, ksplit, per, tpw);
+    else if (per <= 2) launch_packed_s<T, MODE, KP, 4>(stream, w, m, n, in, out, ksplit, per, tpw);
+    else if (per <= 4) launch_packed_s<T, MODE, KP, 2>(stream, w, m, n, in, out, ksplit, per, tpw);
+    else launch_packed_s<T, MODE, KP, 1>(stream, w, m, n, in, out, ksplit, per, tpw);
+}
+
 template <uint32_t T, int MODE>
 int launch_packed_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const GemvInput &in,
                     float *out, int ksplit) {
     const int tiles = (int)((m + kWave - 1) / kWave);
     const int per = split_len((int)(n / 256), ksplit);
-    hipLaunchKernelGGL((gemv_packed<T, MODE>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
-                       static_cast<const uint8_t *>(w), in, out, (int)m, (int)n, per, (size_t)m);
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    // a workgroup takes several row tiles when there are many: the prologue's
+    // re-reads of the input vector are then shared
+    const int tpw = MODE != GEMV_IN_PLAIN && tiles * ksplit >= 8 * cus ? 2 : 1;
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+    constexpr bool has_parts =
+        MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_SILU_MUL || MODE == GEMV_IN_GATED_NORM;
+    if constexpr (has_parts) {
+        if (in.kp > 2) launch_packed_k<T, MODE, kMaxSplit>(stream, wb, m, n, in, out, ksplit, per, tpw);
+        else launch_packed_k<T, MODE, 2>(stream, wb, m, n, in, out, ksplit, per, tpw);
+    } else {
+        launch_packed_k<T, MODE, 2>(stream, wb, m, n, in, out, ksplit, per, tpw);
+    }
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

@@ -246,7 +246,7 @@ int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
     if (!wp || !x || !y) return set_error(ctx->err, ANEHIP_EINVAL, "quant_gemv_packed: null pointer");
     int rc = check_packed_args(ctx, "quant_gemv_packed", ggml_type, m, n);
     if (rc) return rc;
-    const int ksplit = gemm_ksplit(ctx, m, n);  // the decode step's choice (<= 8 splits)
+    const int ksplit = gemv_packed_ksplit(ctx, m, n);  // the decode step's choice (<= 8 splits)
     GemvInput in;
     in.x = x;
     if (ksplit == 1) return launch_gemv_packed(ctx, ctx->stream, ggml_type, wp, m, n, in, y, 1);
