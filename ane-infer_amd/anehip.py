@@ -61,6 +61,10 @@ def lib():
             "anehip_timer_start": (C.c_int, [vp]),
             "anehip_timer_stop": (C.c_int, [vp, C.POINTER(f32)]),
             "anehip_quant_gemm": (C.c_int, [vp, u32, vp, u32, u32, vp, u32, vp]),
+            "anehip_capture_begin": (C.c_int, [vp]),
+            "anehip_capture_end": (C.c_int, [vp, C.POINTER(vp)]),
+            "anehip_graph_launch": (C.c_int, [vp, vp]),
+            "anehip_graph_destroy": (None, [vp]),
             "anehip_quant_packed_bytes": (sz, [u32, u32, u32]),
             "anehip_quant_pack": (C.c_int, [vp, u32, vp, u32, u32, vp]),
             "anehip_quant_gemv_packed": (C.c_int, [vp, u32, vp, u32, u32, vp, vp]),
@@ -187,6 +191,21 @@ class Context:
 
     def d2d(self, dst, src, nbytes):
         self._check(lib().anehip_d2d(self.h, C.c_void_p(dst), C.c_void_p(src), nbytes))
+
+    def capture_begin(self):
+        self._check(lib().anehip_capture_begin(self.h))
+
+    def capture_end(self) -> int:
+        g = C.c_void_p()
+        self._check(lib().anehip_capture_end(self.h, C.byref(g)))
+        return g.value
+
+    def graph_launch(self, g: int):
+        self._check(lib().anehip_graph_launch(self.h, C.c_void_p(g)))
+
+    @staticmethod
+    def graph_destroy(g: int):
+        lib().anehip_graph_destroy(C.c_void_p(g))
 
     def call(self, name, *args):
         """Calls anehip_<name>(ctx, *args); DevBuf arguments pass their device pointer."""

@@ -172,7 +172,7 @@ int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uin
         ctx->inv_freq_base = rope_base;
     }
     const int G = (int)(n_heads / n_kv_heads);
-    int rc = ensure_workspace(ctx, attn_partial_floats((int)batch, (int)n_kv_heads, (int)max_seq, G), 0);
+    int rc = ensure_workspace(ctx, attn_partial_floats((int)batch, (int)n_kv_heads, (int)max_seq, G));
     if (rc) return rc;
     MixIn mix;
     mix.p = qkv;
@@ -185,7 +185,7 @@ int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uin
 int anehip_argmax(anehip_ctx *ctx, const float *logits, uint32_t rows, uint32_t n, uint32_t *out) {
     NEED_CTX(ctx, "argmax");
     if (!logits || !out || !rows || !n) return set_error(ctx->err, ANEHIP_EINVAL, "argmax: bad argument");
-    int rc = ensure_workspace(ctx, (argmax_workspace_bytes((int)rows) + 3) / 4, 0);
+    int rc = ensure_workspace(ctx, (argmax_workspace_bytes((int)rows) + 3) / 4);
     if (rc) return rc;
     return launch_argmax(ctx, ctx->stream, (int)rows, n, logits, ctx->ws.partial, out);
 }

@@ -37,14 +37,11 @@ struct DevBuf {
     size_t bytes = 0;
 };
 
-// Device workspace used by split-K reductions: partial sums and per-tile
-// arrival counters.  Counters are returned to zero by the kernel that uses
-// them, so the workspace needs clearing only once, at allocation.
+// Device scratch of the kernel-level entry points: split-K partial sums,
+// fp16 input planes, attention partials, argmax candidates.
 struct Workspace {
-    float *partial = nullptr;      // split-K partial sums
+    float *partial = nullptr;
     size_t partial_floats = 0;
-    uint32_t *counters = nullptr;  // per-row-tile arrival counters
-    size_t n_counters = 0;
 };
 
 }  // namespace anehip
@@ -64,9 +61,9 @@ struct anehip_ctx {
 
 namespace anehip {
 
-// Ensures the split-K workspace holds at least `floats` partials and
-// `counters` counters (grown with hipMalloc, cleared once).
-int ensure_workspace(anehip_ctx *ctx, size_t floats, size_t counters);
+// Ensures the workspace holds at least `floats` floats (grown with
+// hipMalloc; refused while the context stream is being captured).
+int ensure_workspace(anehip_ctx *ctx, size_t floats);
 
 // How a batch-1 GEMV forms its input vector from what the previous kernels
 // left in memory (the element-wise step is fused into the GEMV's prologue, so

@@ -1124,7 +1124,7 @@ int launch_quant_gemm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, c
     // workspace: [ksplit partials][x hi/lo planes (2 * batch * n halves)]
     const size_t part = ksplit > 1 ? (size_t)ksplit * count : 0;
     const size_t xs_floats = batch > 1 ? (size_t)batch * n : 0;
-    int rc = ensure_workspace(ctx, part + xs_floats, 0);
+    int rc = ensure_workspace(ctx, part + xs_floats);
     if (rc) return rc;
     void *xs = batch > 1 ? static_cast<void *>(ctx->ws.partial + part) : nullptr;
     if (ksplit == 1) return launch_gemm_raw(ctx, stream, ggml_type, w, m, n, x, batch, y, 1, xs);

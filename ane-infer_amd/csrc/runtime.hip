@@ -25,35 +25,27 @@ int set_error(ErrorSlot &slot, int code, const char *fmt, ...) {
     return code;
 }
 
-int ensure_workspace(anehip_ctx *ctx, size_t floats, size_t counters) {
+int ensure_workspace(anehip_ctx *ctx, size_t floats) {
     Workspace &ws = ctx->ws;
-    if (floats > ws.partial_floats) {
-        if (ws.partial) {
-            // queued kernels may still read the old buffer
-            ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
-            (void)hipFree(ws.partial);
-        }
-        ws.partial = nullptr;
-        ws.partial_floats = 0;
-        size_t want = floats < (1u << 20) ? (1u << 20) : floats;
-        if (hipMalloc(&ws.partial, want * sizeof(float)) != hipSuccess)
-            return set_error(ctx->err, ANEHIP_ENOMEM, "workspace: cannot allocate %zu partials", want);
-        ws.partial_floats = want;
+    if (floats <= ws.partial_floats) return ANEHIP_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    ANEHIP_HIP_TRY(ctx->err, hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return set_error(ctx->err, ANEHIP_ESTATE,
+                         "workspace must grow to %zu floats during capture: make the same call once before "
+                         "anehip_capture_begin",
+                         floats);
+    if (ws.partial) {
+        // queued kernels may still read the old buffer
+        ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+        (void)hipFree(ws.partial);
     }
-    if (counters > ws.n_counters) {
-        if (ws.counters) {
-            // outstanding kernels may still use the old counters
-            ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
-            (void)hipFree(ws.counters);
-        }
-        ws.counters = nullptr;
-        ws.n_counters = 0;
-        size_t want = counters < 65536 ? 65536 : counters;
-        if (hipMalloc(&ws.counters, want * sizeof(uint32_t)) != hipSuccess)
-            return set_error(ctx->err, ANEHIP_ENOMEM, "workspace: cannot allocate %zu counters", want);
-        ANEHIP_HIP_TRY(ctx->err, hipMemset(ws.counters, 0, want * sizeof(uint32_t)));
-        ws.n_counters = want;
-    }
+    ws.partial = nullptr;
+    ws.partial_floats = 0;
+    size_t want = floats < (1u << 20) ? (1u << 20) : floats;
+    if (hipMalloc(&ws.partial, want * sizeof(float)) != hipSuccess)
+        return set_error(ctx->err, ANEHIP_ENOMEM, "workspace: cannot allocate %zu floats", want);
+    ws.partial_floats = want;
     return ANEHIP_OK;
 }
 
@@ -102,7 +94,7 @@ int anehip_ctx_create(int device, const anehip_model_desc *desc, anehip_ctx **ou
         anehip_ctx_destroy(ctx);
         return set_error(global_error(), ANEHIP_EHIP, "ctx_create: stream/event creation failed");
     }
-    int rc = ensure_workspace(ctx, 0, 0);
+    int rc = ensure_workspace(ctx, 0);
     if (rc == ANEHIP_OK && desc) rc = anehip_model_setup(ctx, desc);
     if (rc != ANEHIP_OK) {
         set_error(global_error(), rc, "ctx_create: %s", ctx->err.msg.c_str());
@@ -120,7 +112,6 @@ void anehip_ctx_destroy(anehip_ctx *ctx) {
     anehip_model_teardown(ctx);
     for (void *p : ctx->user_allocs) (void)hipFree(p);
     if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
-    if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
     if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
@@ -219,6 +210,52 @@ int anehip_quant_gemm(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32
     return launch_quant_gemm(ctx, ctx->stream, ggml_type, w, m, n, x, batch, y);
 }
 
+struct anehip_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int anehip_capture_begin(anehip_ctx *ctx) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "capture_begin: ctx is NULL");
+    ANEHIP_HIP_TRY(ctx->err, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return ANEHIP_OK;
+}
+
+int anehip_capture_end(anehip_ctx *ctx, anehip_graph **out) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "capture_end: ctx is NULL");
+    if (!out) return set_error(ctx->err, ANEHIP_EINVAL, "capture_end: out is NULL");
+    *out = nullptr;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return set_error(ctx->err, ANEHIP_EHIP, "capture_end: %s", hipGetErrorString(e));
+    }
+    anehip_graph *G = new anehip_graph();
+    G->graph = g;
+    e = hipGraphInstantiate(&G->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        anehip_graph_destroy(G);
+        return set_error(ctx->err, ANEHIP_EHIP, "capture_end: instantiate: %s", hipGetErrorString(e));
+    }
+    *out = G;
+    return ANEHIP_OK;
+}
+
+int anehip_graph_launch(anehip_ctx *ctx, anehip_graph *graph) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "graph_launch: ctx is NULL");
+    if (!graph || !graph->exec) return set_error(ctx->err, ANEHIP_EINVAL, "graph_launch: no graph");
+    ANEHIP_HIP_TRY(ctx->err, hipGraphLaunch(graph->exec, ctx->stream));
+    return ANEHIP_OK;
+}
+
+void anehip_graph_destroy(anehip_graph *graph) {
+    if (!graph) return;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+}
+
 size_t anehip_quant_packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n) {
     if ((ggml_type != ANEHIP_GGML_Q8_0 && ggml_type != ANEHIP_GGML_Q4_0) || m == 0 || n == 0 || n % 256) return 0;
     return packed_bytes(ggml_type, m, n);
@@ -250,7 +287,7 @@ int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
     GemvInput in;
     in.x = x;
     if (ksplit == 1) return launch_gemv_packed(ctx, ctx->stream, ggml_type, wp, m, n, in, y, 1);
-    if ((rc = ensure_workspace(ctx, (size_t)ksplit * m, 0))) return rc;
+    if ((rc = ensure_workspace(ctx, (size_t)ksplit * m))) return rc;
     if ((rc = launch_gemv_packed(ctx, ctx->stream, ggml_type, wp, m, n, in, ctx->ws.partial, ksplit))) return rc;
     return launch_sum_partials(ctx, ctx->stream, ctx->ws.partial, y, m, ksplit);
 }

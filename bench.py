@@ -5,9 +5,13 @@ Workload for `value`: the Q8_0 GEMV / small-batch
 GEMM sweep over the shapes [6144 x 2048], [2048 x 6144], [151936 x 2048] with
 batch M in {1, 4, 16, 32}.  One "step" is one pass over the 12 (shape, M)
 points; `value` is the sweep's algorithmic bytes (weights once + fp32
-activations in + fp32 outputs) per second, inputs resident in HBM.  Weights
-are rotated over enough distinct copies (> 512 MiB per shape) that the 256 MiB
-MALL cannot serve repeated reads.
+activations in + fp32 outputs) per second, inputs resident in HBM.  M = 1
+runs the batch-1 GEMV over the panel copy of the weights (the layout the
+decode step keeps resident: same bytes, permuted once at upload); M > 1 runs
+the MFMA GEMM over the GGUF blocks.  Weights are rotated over enough distinct
+copies (> 512 MiB per shape) that the 256 MiB MALL cannot serve repeated
+reads.  Each sweep pass is one captured hipGraph (anehip_capture_*), so the
+host's launch rate does not enter the figure.
 
 `decode` reports configs[4]: the full random-init Qwen3.5-2B-shape Q8_0 decode
 step (24 layers, fp16 KV cache) at batch 1 and 32 and context 1k / 8k / 32k,
@@ -69,45 +73,72 @@ def parse():
 
 class Shape:
     """One sweep shape: Q8_0 weights generated and quantised on the device,
-    replicated into `copies` distinct buffers."""
+    replicated into `copies` distinct GGUF buffers, each with its panel copy."""
 
-    def __init__(self, ctx, m, n, seed):
+    def __init__(self, anehip, ctx, m, n, seed):
         self.m, self.n = m, n
         self.wbytes = m * (n // 32) * 34
+        self.pbytes = int(anehip.lib().anehip_quant_packed_bytes(Q8, m, n))
         self.copies = max(2, -(-MALL_DEFEAT_BYTES // self.wbytes))
         self.w = ctx.alloc(self.wbytes * self.copies)
+        self.p = ctx.alloc(self.pbytes * self.copies)
         tmp = ctx.alloc(m * n * 4)
         ctx.fill_random(tmp, m * n, 0, seed, 0.0, 0.02)
         ctx.quantize(Q8, tmp, m, n, self.w.ptr)
         for c in range(1, self.copies):
             ctx.d2d(self.w.ptr + c * self.wbytes, self.w.ptr, self.wbytes)
+        for c in range(self.copies):
+            ctx.call("quant_pack", Q8, self.wptr(c), m, n, self.pptr(c))
         ctx.sync()
         tmp.free()
         self.x = ctx.alloc(32 * n * 4)
         ctx.fill_random(self.x, 32 * n, 0, seed + 1, 0.0, 1.0)
         self.y = ctx.alloc(32 * m * 4)
-        self.next = 0
 
-    def wptr(self):
-        p = self.w.ptr + self.next * self.wbytes
-        self.next = (self.next + 1) % self.copies
-        return p
+    def wptr(self, c):
+        return self.w.ptr + (c % self.copies) * self.wbytes
 
-
-def run_sweep(ctx, shapes):
-    for s in shapes:
-        for b in BATCHES:
-            ctx.quant_gemm(Q8, s.wptr(), s.m, s.n, s.x, b, s.y)
+    def pptr(self, c):
+        return self.p.ptr + (c % self.copies) * self.pbytes
 
 
-def time_kernel(ctx, s, batch, launches):
-    for _ in range(3):
-        ctx.quant_gemm(Q8, s.wptr(), s.m, s.n, s.x, batch, s.y)
+def launch_point(ctx, s, batch, c):
+    """One GEMV (M = 1, panel layout) or MFMA GEMM (M > 1, GGUF blocks) on copy c."""
+    if batch == 1:
+        ctx.call("quant_gemv_packed", Q8, s.pptr(c), s.m, s.n, s.x.ptr, s.y.ptr)
+    else:
+        ctx.quant_gemm(Q8, s.wptr(c), s.m, s.n, s.x, batch, s.y)
+
+
+def capture(ctx, enqueue):
+    """A hipGraph of the kernel-level calls `enqueue` makes (run once eagerly
+    first, so no workspace grows during capture)."""
+    enqueue()
+    ctx.sync()
+    ctx.capture_begin()
+    try:
+        enqueue()
+    finally:
+        g = ctx.capture_end()
+    return g
+
+
+def time_graphs(ctx, graphs, launches, warmup=2):
+    for i in range(warmup):
+        ctx.graph_launch(graphs[i % len(graphs)])
     ctx.sync()
     ctx.timer_start()
-    for _ in range(launches):
-        ctx.quant_gemm(Q8, s.wptr(), s.m, s.n, s.x, batch, s.y)
-    return ctx.timer_stop() / launches
+    for i in range(launches):
+        ctx.graph_launch(graphs[i % len(graphs)])
+    return ctx.timer_stop()
+
+
+def time_point(ctx, s, batch, launches):
+    """Average time of one launch, `launches` back to back in one graph (copies rotated)."""
+    g = capture(ctx, lambda: [launch_point(ctx, s, batch, c) for c in range(launches)])
+    ms = time_graphs(ctx, [g], 3) / 3
+    ctx.graph_destroy(g)
+    return ms / launches
 
 
 def bench_decode(anehip, steps, warmup, points=DECODE_POINTS):
@@ -234,21 +265,28 @@ def main():
         return
     ctx = anehip.Context(0)
     if args.profile_kernel:
-        lm = Shape(ctx, 151936, 2048, 102)
-        t = time_kernel(ctx, lm, 1, args.steps)
-        print(json.dumps({"kernel": "lm_head GEMV M=1", "avg_launch_us": round(t * 1e3, 2),
+        lm = Shape(anehip, ctx, 151936, 2048, 102)
+        t = time_point(ctx, lm, 1, args.steps)
+        print(json.dumps({"kernel": "gemv_packed<Q8_0, PLAIN> lm_head 151936x2048, M=1",
+                          "avg_launch_us": round(t * 1e3, 2),
                           "GB/s": round(algo_bytes(lm.m, lm.n, 1) / (t * 1e-3) / 1e9, 1)}), flush=True)
         ctx.close()
         return
-    shapes = [Shape(ctx, m, n, 100 + i) for i, (m, n) in enumerate(SHAPES)]
+    shapes = [Shape(anehip, ctx, m, n, 100 + i) for i, (m, n) in enumerate(SHAPES)]
 
-    for _ in range(args.warmup):
-        run_sweep(ctx, shapes)
+    # one graph per rotation phase r: every shape's points on copy r
+    phases = max(s.copies for s in shapes)
+    sweeps = [capture(ctx, lambda r=r: [launch_point(ctx, s, b, r) for s in shapes for b in BATCHES])
+              for r in range(phases)]
+    for i in range(args.warmup):
+        ctx.graph_launch(sweeps[i % phases])
     ctx.sync()
     ctx.timer_start()
-    for _ in range(args.steps):
-        run_sweep(ctx, shapes)
+    for i in range(args.steps):
+        ctx.graph_launch(sweeps[i % phases])
     ms_total = ctx.timer_stop()
+    for g in sweeps:
+        ctx.graph_destroy(g)
     ms_per_step = ms_total / args.steps
     sweep_bytes = sum(algo_bytes(s.m, s.n, b) for s in shapes for b in BATCHES)
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
@@ -256,11 +294,11 @@ def main():
     points = {}
     for s in shapes:
         for b in BATCHES:
-            t = time_kernel(ctx, s, b, 20 if s.m > 100000 else 200)
+            t = time_point(ctx, s, b, max(s.copies, 20))
             points[f"{s.m}x{s.n}_M{b}"] = {"us": round(t * 1e3, 2),
                                            "GB/s": round(algo_bytes(s.m, s.n, b) / (t * 1e-3) / 1e9, 1)}
     lm = shapes[2]
-    t_lm = time_kernel(ctx, lm, 1, 50)
+    t_lm = time_point(ctx, lm, 1, 50)
     lm_bytes = algo_bytes(lm.m, lm.n, 1)
     achieved = lm_bytes / (t_lm * 1e-3) / 1e9
     c0 = points["6144x2048_M1"]
@@ -286,7 +324,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "quant_gemm_tiled<Q8_0,1> (lm_head 151936x2048, M=1)",
+            "kernel": "gemv_packed<Q8_0, PLAIN> (lm_head 151936x2048, M=1, panel layout)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -146,6 +146,21 @@ int anehip_d2d(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes);
 int anehip_timer_start(anehip_ctx *ctx);
 int anehip_timer_stop(anehip_ctx *ctx, float *ms);
 
+/* ---- graph capture of kernel-level calls -------------------------------- */
+/* anehip_capture_begin starts capturing the context stream: the kernel-level
+ * entry points called until anehip_capture_end are recorded, not run, into a
+ * graph that anehip_graph_launch replays on the stream (same pointers, same
+ * sizes).  Calls that would have to grow the context workspace fail during
+ * capture: make each call once before capturing.  The decode-step entry
+ * points keep their own per-step graph and are not capturable.  Replaces the
+ * per-token command-buffer encoding of the reference (metal_graph.rs:79-138)
+ * for callers that chain kernel-level calls themselves. */
+typedef struct anehip_graph anehip_graph;
+int anehip_capture_begin(anehip_ctx *ctx);
+int anehip_capture_end(anehip_ctx *ctx, anehip_graph **out);
+int anehip_graph_launch(anehip_ctx *ctx, anehip_graph *graph);
+void anehip_graph_destroy(anehip_graph *graph);
+
 /* ---- kernel-level entry points (device pointers, context stream) ------- */
 
 /*
