@@ -51,6 +51,20 @@ KV_BYTES_PER_POS = 6 * 2 * 2 * 256 * 2
 DN_STATE_BYTES = 18 * (2 * 16 * 128 * 128 * 4 + 2 * 6144 * 4 * 4)
 
 
+def profiled_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by a copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_packed_lm_head_m1.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def algo_bytes(m: int, n: int, batch: int) -> int:
     return m * (n // 32) * 34 + 4 * batch * (n + m)
 
@@ -267,9 +281,16 @@ def main():
     if args.profile_kernel:
         lm = Shape(anehip, ctx, 151936, 2048, 102)
         t = time_point(ctx, lm, 1, args.steps)
+        # reference for the HBM byte counters: plain device copies of known size
+        cp = 256 << 20
+        a, b = ctx.alloc(cp), ctx.alloc(cp)
+        for _ in range(5):
+            ctx.d2d(b.ptr, a.ptr, cp)
+        ctx.sync()
         print(json.dumps({"kernel": "gemv_packed<Q8_0, PLAIN> lm_head 151936x2048, M=1",
                           "avg_launch_us": round(t * 1e3, 2),
-                          "GB/s": round(algo_bytes(lm.m, lm.n, 1) / (t * 1e-3) / 1e9, 1)}), flush=True)
+                          "GB/s": round(algo_bytes(lm.m, lm.n, 1) / (t * 1e-3) / 1e9, 1),
+                          "copy_reference_bytes": cp}), flush=True)
         ctx.close()
         return
     shapes = [Shape(anehip, ctx, m, n, 100 + i) for i, (m, n) in enumerate(SHAPES)]
@@ -329,7 +350,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(),
+            "traffic_source": "profiles/gemv_packed_lm_head_m1.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-scaled)",
             "algorithmic_bytes": lm_bytes,
             "avg_launch_us": round(t_lm * 1e3, 2),
         },

@@ -275,7 +275,9 @@ int anehip_upload_f32(anehip_ctx *ctx, int32_t layer, uint32_t kind, const float
 /* Device address where tensor `kind` of `layer` lives (allocated on first
  * use, with ggml_type for quantised kinds, ignored for fp32 kinds), so a
  * caller can write it in place (e.g. with anehip_quantize); the tensor then
- * counts as uploaded.  *nbytes receives its size. */
+ * counts as uploaded.  *nbytes receives its size.  The batch-1 step reads a
+ * panel copy of quantised weights that is rebuilt at the first step after
+ * this call (or after anehip_upload_quant): write before that step. */
 int anehip_tensor_ptr(anehip_ctx *ctx, int32_t layer, uint32_t kind, uint32_t ggml_type, void **dptr,
                       size_t *nbytes);
 
