@@ -68,6 +68,7 @@ def lib():
             "anehip_quant_packed_bytes": (sz, [u32, u32, u32]),
             "anehip_quant_pack": (C.c_int, [vp, u32, vp, u32, u32, vp]),
             "anehip_quant_gemv_packed": (C.c_int, [vp, u32, vp, u32, u32, vp, vp]),
+            "anehip_quant_gemm_packed": (C.c_int, [vp, u32, vp, u32, u32, vp, u32, vp]),
             "anehip_rmsnorm": (C.c_int, [vp, vp, vp, vp, u32, u32, f32]),
             "anehip_silu_mul": (C.c_int, [vp, vp, vp, sz]),
             "anehip_residual_add": (C.c_int, [vp, vp, vp, sz]),

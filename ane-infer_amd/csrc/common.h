@@ -153,6 +153,13 @@ int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, 
 size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
 int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
                   void *dst);
+// Panel MFMA GEMM for batch 2..32: out[ks][b][r] (final values when ksplit
+// is 1) from the fp16 hi / lo planes of x [batch][n] (launch_split_x, or the
+// hi / lo outputs of the element-wise kernels), ksplit from gemm_packed_ksplit.
+int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
+int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
+                       uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit);
+int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, size_t count, _Float16 *xh, _Float16 *xl);
 // K splits the batch-1 panel GEMV takes for an [m x n] matrix (<= 8).
 int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
 int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,

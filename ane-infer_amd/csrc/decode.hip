@@ -34,9 +34,9 @@ constexpr uint32_t kDk = 128;
 constexpr uint32_t kConvK = 4;
 constexpr uint32_t kHd = 256;
 
-// A quantised matrix: GGUF blocks (d, as uploaded) and, once the batch-1
-// path has run, its panel copy (p) for the batch-1 GEMV; `stale` marks a
-// panel copy that has to be rebuilt from d before the next step.
+// A quantised matrix: GGUF blocks (d, as uploaded) and, once a step has run,
+// its panel copy (p) that the step's GEMV / GEMM kernels read; `stale` marks
+// a panel copy that has to be rebuilt from d before the next step.
 struct QMat {
     void *d = nullptr, *p = nullptr;
     uint32_t type = 0, rows = 0, cols = 0;
@@ -75,8 +75,8 @@ struct Model {
     float *x0 = nullptr, *x1 = nullptr;                  // residual stream (two buffers, alternating)
     float *pmix = nullptr, *p0 = nullptr, *p1 = nullptr;  // GEMV outputs as K-split partial slices
     float *heads = nullptr, *attn_out = nullptr, *logits = nullptr, *attn_part = nullptr;
-    _Float16 *planes = nullptr;  // fp16 hi / lo planes of a GEMM input (batch > 1)
-    size_t plane_len = 0;        // halves per plane
+    float *xin = nullptr;        // GEMM input planes (batch > 1): hi then lo, xin_len halves each
+    size_t xin_len = 0;          // batch * widest GEMM input
     size_t part_len = 0;         // floats per partial buffer
     void *argmax_ws = nullptr;
     // graph
@@ -113,12 +113,12 @@ void free_state(Model *M) {
         L.kc = L.vc = nullptr;
     }
     void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->x0,       M->x1,        M->pmix,      M->p0,
-                    M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->planes};
+                    M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->xin};
     for (void *p : bufs) free_ptr(p);
     if (M->h_tokens) (void)hipHostFree(M->h_tokens);
     M->d_pos = M->d_tokens = M->d_sampled = M->h_tokens = nullptr;
     M->x0 = M->x1 = M->pmix = M->p0 = M->p1 = M->heads = M->attn_out = M->logits = M->attn_part = nullptr;
-    M->planes = nullptr;
+    M->xin = nullptr;
     M->argmax_ws = nullptr;
     M->batch = M->max_seq = 0;
     M->host_pos.clear();
@@ -375,15 +375,16 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     return ANEHIP_OK;
 }
 
-// Batch 2..32: element-wise kernels write the next GEMM's input as fp16 hi/lo
-// planes; projections run on the MFMA GEMM.
+// Batch 2..32: element-wise kernels (residual + RMSNorm, gated norm, SiLU-mul,
+// attention combine) write the next GEMM's input as fp16 hi / lo planes;
+// projections run on the panel MFMA GEMM.
 int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
     const anehip_model_desc &D = M->desc;
     const int B = (int)M->batch;
     const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
     const uint32_t qd = D.n_heads * D.head_dim;
     const float eps = D.rms_norm_eps;
-    _Float16 *xh = M->planes, *xl = M->planes + M->plane_len;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(M->xin), *xl = xh + M->xin_len;  // GEMM input planes
     float *x = M->x0;
     TRY(launch_embed_rmsnorm(ctx, s, B, (int)d, M->d_tokens, M->embedding, D.vocab_size, x, M->layers[0].attn_norm,
                              nullptr, eps, xh, xl));
@@ -391,8 +392,8 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
         const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
-        const int k1 = gemm_ksplit(ctx, rows_in, d);
-        TRY(launch_gemm_planes(ctx, s, L.mix_in.type, L.mix_in.d, rows_in, d, xh, xl, B, M->pmix, k1));
+        const int k1 = gemm_packed_ksplit(ctx, rows_in, d);
+        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xh, xl, B, M->pmix, k1));
         MixIn mix;
         mix.p = M->pmix;
         mix.kp = k1;
@@ -402,30 +403,30 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
         if (dn) {
             TRY(launch_deltanet_step(ctx, s, B, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
                                      L.conv1d, L.ssm_a, L.dt_bias, L.conv_state, L.S, M->heads));
-            TRY(launch_dn_finish(ctx, s, B, (int)H, mix, L.conv_state, M->heads, (int)C, L.ssm_norm, nullptr, xh, xl,
-                                 eps));
+            TRY(launch_dn_finish(ctx, s, B, (int)H, mix, L.conv_state, M->heads, (int)C, L.ssm_norm, nullptr, xh,
+                                 xl, eps));
             cols3 = d;
         } else {
             TRY(launch_attention(ctx, s, B, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
                                  L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part, nullptr, xh, xl));
             cols3 = qd;
         }
-        const int k3 = gemm_ksplit(ctx, d, cols3);
-        TRY(launch_gemm_planes(ctx, s, L.mix_out.type, L.mix_out.d, d, cols3, xh, xl, B, M->p0, k3));
+        const int k3 = gemm_packed_ksplit(ctx, d, cols3);
+        TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xh, xl, B, M->p0, k3));
         TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, nullptr, eps, xh, xl));
-        const int k4 = gemm_ksplit(ctx, 2 * F, d);
-        TRY(launch_gemm_planes(ctx, s, L.ffn_gu.type, L.ffn_gu.d, 2 * F, d, xh, xl, B, M->p1, k4));
+        const int k4 = gemm_packed_ksplit(ctx, 2 * F, d);
+        TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xh, xl, B, M->p1, k4));
         TRY(launch_silu_mul_stacked(ctx, s, B, (int)F, M->p1, k4, nullptr, xh, xl));
-        const int k5 = gemm_ksplit(ctx, d, F);
-        TRY(launch_gemm_planes(ctx, s, L.ffn_down.type, L.ffn_down.d, d, F, xh, xl, B, M->p0, k5));
+        const int k5 = gemm_packed_ksplit(ctx, d, F);
+        TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xh, xl, B, M->p0, k5));
         const float *next_norm = l + 1 < D.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
         TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k5, next_norm, nullptr, eps, xh, xl));
     }
-    const int kf = gemm_ksplit(ctx, D.vocab_size, d);
+    const int kf = gemm_packed_ksplit(ctx, D.vocab_size, d);
     if (kf == 1) {
-        TRY(launch_gemm_planes(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, xh, xl, B, M->logits, 1));
+        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xh, xl, B, M->logits, 1));
     } else {
-        TRY(launch_gemm_planes(ctx, s, M->lm_head.type, M->lm_head.d, D.vocab_size, d, xh, xl, B, M->pmix, kf));
+        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xh, xl, B, M->pmix, kf));
         TRY(launch_sum_partials(ctx, s, M->pmix, M->logits, (size_t)B * D.vocab_size, kf));
     }
     return ANEHIP_OK;
@@ -452,7 +453,7 @@ size_t part_floats(anehip_ctx *ctx, Model *M) {
     size_t mx = 0;
     for (auto &e : g) {
         if (!e.m) continue;
-        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n) : gemm_ksplit(ctx, e.m, e.n);
+        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n) : gemm_packed_ksplit(ctx, e.m, e.n);
         size_t need = (size_t)k * M->batch * e.m;
         if (need > mx) mx = need;
     }
@@ -460,7 +461,7 @@ size_t part_floats(anehip_ctx *ctx, Model *M) {
 }
 
 // Builds the panel copy of every matrix whose GGUF blocks changed since the
-// last step (all of them on the first batch-1 step).
+// last step (all of them on the first step).
 int pack_mat(anehip_ctx *ctx, QMat &Q) {
     if (!Q.d || !Q.stale) return ANEHIP_OK;
     if (!Q.p) {
@@ -487,7 +488,7 @@ int pack_weights(anehip_ctx *ctx, Model *M) {
 
 int launch_step(anehip_ctx *ctx, Model *M) {
     hipStream_t s = ctx->stream;
-    if (M->batch == 1) TRY(pack_weights(ctx, M));
+    TRY(pack_weights(ctx, M));
     if (!M->use_graph) return enqueue_step(ctx, M, s);
     if (!M->exec) {
         ANEHIP_HIP_TRY(ctx->err, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -718,7 +719,7 @@ int anehip_tensor_ptr(anehip_ctx *ctx, int32_t layer, uint32_t kind, uint32_t gg
             Q.cols = ks.cols;
         }
         *dptr = static_cast<char *>(Q.d) + (size_t)slot.row_off * qrow_bytes(ggml_type, ks.cols);
-        Q.stale = true;  // writes through *dptr reach the batch-1 path at the next step
+        Q.stale = true;  // writes through *dptr reach the step's panel copy at the next step
         *nbytes = (size_t)ks.rows * qrow_bytes(ggml_type, ks.cols);
     } else {
         float **slot = f32_slot(M, layer, kind);
@@ -771,7 +772,7 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     const size_t qd = (size_t)D.n_heads * D.head_dim;
     size_t nmax = d > F ? d : F;
     if (qd > nmax) nmax = qd;
-    M->plane_len = batch * nmax;
+    M->xin_len = batch * nmax;
     M->part_len = part_floats(ctx, M);
     r = r ? r : alloc((void **)&M->d_pos, 64 * sizeof(uint32_t));
     r = r ? r : alloc((void **)&M->d_tokens, 64 * sizeof(uint32_t));
@@ -783,7 +784,7 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     r = r ? r : alloc((void **)&M->p1, M->part_len * sizeof(float));
     r = r ? r : alloc((void **)&M->heads, batch * d * sizeof(float));
     r = r ? r : alloc((void **)&M->attn_out, batch * (qd ? qd : 1) * sizeof(float));
-    r = r ? r : alloc((void **)&M->planes, 2 * M->plane_len * sizeof(_Float16));
+    r = r ? r : alloc((void **)&M->xin, M->xin_len * sizeof(float));
     r = r ? r : alloc((void **)&M->logits, batch * (size_t)D.vocab_size * sizeof(float));
     r = r ? r : alloc(&M->argmax_ws, argmax_workspace_bytes((int)batch));
     if (M->rows_attn) {

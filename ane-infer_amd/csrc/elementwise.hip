@@ -99,6 +99,63 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(float *__res
     rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi ? hi + b * n : nullptr, lo ? lo + b * n : nullptr);
 }
 
+// The same for rows of n <= 2048 (n % 4 == 0) with one workgroup of 512
+// threads per row: each thread owns one float4 and issues every load it needs
+// (x, the KP partial slices, w) before any arithmetic, so the row costs one
+// memory round trip instead of one per 256 elements and per pass.
+template <int KP>
+__global__ __launch_bounds__(512) void residual_rmsnorm_v4(float *__restrict__ x, const float *__restrict__ part,
+                                                           int ksplit, int rows, const float *__restrict__ w,
+                                                           float *__restrict__ xn, int n, float eps,
+                                                           _Float16 *__restrict__ hi, _Float16 *__restrict__ lo) {
+    __shared__ float red[8];
+    const int t = threadIdx.x;
+    const size_t b = blockIdx.x;
+    const int n4 = n >> 2, e4 = min(t, n4 - 1);
+    float4 *x4 = reinterpret_cast<float4 *>(x) + b * n4;
+    const float4 *p4 = reinterpret_cast<const float4 *>(part) + b * n4;
+    const size_t split4 = (size_t)rows * n4;
+    float4 r = x4[e4];
+    float4 pv[KP];
+#pragma unroll
+    for (int k = 0; k < KP; k++) pv[k] = p4[(size_t)min(k, ksplit - 1) * split4 + e4];
+    const float4 wv = w ? reinterpret_cast<const float4 *>(w)[e4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 s = pv[0];
+#pragma unroll
+    for (int k = 1; k < KP; k++) {
+        const bool on = k < ksplit;
+        s.x += on ? pv[k].x : 0.0f;
+        s.y += on ? pv[k].y : 0.0f;
+        s.z += on ? pv[k].z : 0.0f;
+        s.w += on ? pv[k].w : 0.0f;
+    }
+    r = make_float4(r.x + s.x, r.y + s.y, r.z + s.z, r.w + s.w);
+    const bool mine = t < n4;
+    if (mine) x4[t] = r;
+    if (!w) return;
+    float ss = mine ? r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w : 0.0f;
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    float tot = red[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) tot += red[i];
+    const float inv_rms = 1.0f / sqrtf(tot / (float)n + eps);
+    if (!mine) return;
+    const float v[4] = {(r.x * inv_rms) * wv.x, (r.y * inv_rms) * wv.y, (r.z * inv_rms) * wv.z,
+                        (r.w * inv_rms) * wv.w};
+    if (hi) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const _Float16 h = (_Float16)v[c];
+            hi[b * n + 4 * t + c] = h;
+            lo[b * n + 4 * t + c] = (_Float16)(v[c] - (float)h);
+        }
+    } else if (xn) {
+        reinterpret_cast<float4 *>(xn)[b * n4 + t] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
 // Stacked [gate; up] GEMV output gu[k][b][2F]: h[b][r] = SiLU(gate) * up
 // (scratch.rs:181-186: a = (a / (1 + exp(-a))) * b).
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restrict__ gu, int ksplit, int rows,
@@ -236,8 +293,17 @@ int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const 
 
 int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
                             int ksplit, const float *w, float *xn, float eps, _Float16 *hi, _Float16 *lo) {
-    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, part, ksplit, rows, w, xn, n,
-                       eps, hi, lo);
+    if (n % 4 == 0 && n <= 2048 && ksplit >= 1 && ksplit <= 8) {
+        if (ksplit <= 2)
+            hipLaunchKernelGGL(residual_rmsnorm_v4<2>, dim3(rows), dim3(512), 0, s, x, part, ksplit, rows, w, xn, n,
+                               eps, hi, lo);
+        else
+            hipLaunchKernelGGL(residual_rmsnorm_v4<8>, dim3(rows), dim3(512), 0, s, x, part, ksplit, rows, w, xn, n,
+                               eps, hi, lo);
+    } else {
+        hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, part, ksplit, rows, w, xn,
+                           n, eps, hi, lo);
+    }
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

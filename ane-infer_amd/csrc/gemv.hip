@@ -583,7 +583,7 @@ __device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, 
             xs4[t] = make_float4(silu1(gs.x) * us.x, silu1(gs.y) * us.y, silu1(gs.z) * us.z, silu1(gs.w) * us.w);
         __syncthreads();
     } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
-        const int nwg = gridDim.x * gridDim.y, wg = blockIdx.y * gridDim.x + blockIdx.x;
+        const int wg = blockIdx.y * gridDim.x + blockIdx.x;
         const bool commit = in.conv_state != nullptr;
         // one 128-wide head per 32 threads (deltanet.rs:517-533)
         const int e4 = min(t, (len >> 2) - 1);
@@ -701,6 +701,232 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
             }
         }
         __syncthreads();  // red (and, in the generic path, xs) are reused by the next tile
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Small-batch GEMM over panels on MFMA (batch 2..32).
+//
+// v_mfma_f32_32x32x16_f16 with A = activations (32 batch rows x 16 columns,
+// lane l: row l % 32, columns 8 (l / 32) .. +7) and B = weights (16 columns x
+// 32 weight rows, lane l: weight row l % 32, columns 8 (l / 32) .. +7), so a
+// lane's 16 outputs D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32] share one weight
+// row and therefore one block scale.  A panel chunk gives lane l the 16
+// columns of tile row l; one v_permlane32_swap per dword pair exchanges the
+// upper lanes' first 8 columns with the lower lanes' last 8, which turns the
+// chunk into the B operands of rows 0-31 and rows 32-63 with no LDS round
+// trip.  int8 / nibble values become fp16 exactly (0x6400 | (u8) is 1024 + u8,
+// minus 1152 or 1032).  Activations arrive as fp16 hi and lo planes (hi =
+// fp16(x), lo = fp16(x - hi), |x - hi - lo| <= 2^-22 |x|), written by the
+// producer of x, and are staged per panel in LDS: the two products summed in
+// fp32 reproduce the fp32 GEMV within its tolerance.
+// Per block: C = sum over its 2 column steps and the 2 planes, then
+// acc += C * d (q8_gemv.rs:234-242 order within a block up to fp32 summation).
+//
+// grid = (groups of 4 row tiles, K splits); 4 waves, wave w owns row tile
+// 4 blockIdx.x + w and walks the split's panels.
+// ---------------------------------------------------------------------------
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kGemmWaves = 4;
+constexpr int kXRow = 256 + 8;  // halfs per staged activation row (pad: conflict-free 16-byte reads)
+
+// Four signed int8 (one dword) -> four fp16, exact.
+__device__ __forceinline__ void i8x4_to_h(uint32_t d, _Float16 *o) {
+    const uint32_t u = d ^ 0x80808080u;  // q + 128 as unsigned bytes
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // (1024 + u0, 1024 + u1)
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // (1024 + u2, 1024 + u3)
+    const h2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2v a = __builtin_bit_cast(h2v, p0) - bias, b = __builtin_bit_cast(h2v, p1) - bias;
+    o[0] = a[0];
+    o[1] = a[1];
+    o[2] = b[0];
+    o[3] = b[1];
+}
+
+// Four nibbles in bytes (values 0..15, one dword) -> four fp16 of (v - 8), exact.
+__device__ __forceinline__ void u4x4_to_h(uint32_t nib, _Float16 *o) {
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, nib, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, nib, 0x04030402u);
+    const h2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const h2v a = __builtin_bit_cast(h2v, p0) - bias, b = __builtin_bit_cast(h2v, p1) - bias;
+    o[0] = a[0];
+    o[1] = a[1];
+    o[2] = b[0];
+    o[3] = b[1];
+}
+
+__device__ __forceinline__ h8v dwords_to_h8_i8(uint32_t d0, uint32_t d1) {
+    _Float16 t[8];
+    i8x4_to_h(d0, t);
+    i8x4_to_h(d1, t + 4);
+    return h8v{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
+}
+
+__device__ __forceinline__ h8v dwords_to_h8_u4(uint32_t d0, uint32_t d1) {
+    _Float16 t[8];
+    u4x4_to_h(d0, t);
+    u4x4_to_h(d1, t + 4);
+    return h8v{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
+}
+
+// Swaps the upper lanes' (a0, a1) with the lower lanes' (b0, b1): afterwards
+// (a0, a1) hold the columns of rows 0-31 and (b0, b1) those of rows 32-63.
+__device__ __forceinline__ void swap_halves(uint32_t &a0, uint32_t &a1, uint32_t &b0, uint32_t &b1) {
+    const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+    a0 = s0[0];
+    b0 = s0[1];
+    a1 = s1[0];
+    b1 = s1[1];
+}
+
+// Half a panel (4 blocks) of one wave's tile: quant vectors + the panel's
+// scale vector.  `valid` false: every lane reads one vector of `dummy`.
+template <uint32_t T>
+__device__ __forceinline__ void load_half(u32x4 *q, const uint8_t *panel, const uint8_t *dummy, int half, int lane,
+                                          bool valid) {
+    constexpr int V = Panel<T>::kChunks / 2;
+    const u32x4 *p4 = reinterpret_cast<const u32x4 *>(valid ? panel : dummy);
+    const int l = valid ? lane : 0, c0 = valid ? V * half : 0;
+#pragma unroll
+    for (int c = 0; c < V; c++) q[c] = __builtin_nontemporal_load(p4 + (c0 + c) * 64 + l);
+}
+
+template <uint32_t T>
+__device__ __forceinline__ u32x4 load_scales(const uint8_t *panel, const uint8_t *dummy, int lane, bool valid) {
+    const u32x4 *p4 = reinterpret_cast<const u32x4 *>(valid ? panel : dummy);
+    return __builtin_nontemporal_load(p4 + Panel<T>::kChunks * 64 + (valid ? lane : 0));
+}
+
+// Stages the fp16 hi / lo planes of x[:, 256 sb .. +256] (rows >= batch as
+// zeros) into LDS: 32 rows x 32 sixteen-byte chunks per plane, 8 per thread.
+__device__ __forceinline__ void stage_planes(const _Float16 *__restrict__ ph, const _Float16 *__restrict__ pl,
+                                             _Float16 *xh, _Float16 *xl, int n, int batch, int sb, int t) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {  // two rounds of 4 (fewer live registers)
+        u32x4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int idx = t + 256 * (4 * h + j), plane = idx >> 10, b = (idx >> 5) & 31, c = idx & 31;
+            const _Float16 *src = plane ? pl : ph;
+            const size_t off = b < batch ? (size_t)b * n + 256 * sb + 8 * c : 0;
+            v[j] = *reinterpret_cast<const u32x4 *>(src + off);
+            if (b >= batch) v[j] = u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int idx = t + 256 * (4 * h + j), plane = idx >> 10, b = (idx >> 5) & 31, c = idx & 31;
+            *reinterpret_cast<u32x4 *>((plane ? xl : xh) + b * kXRow + 8 * c) = v[j];
+        }
+    }
+}
+
+// Blocks [4 half, 4 half + 4) of a panel: q holds their quant vectors, s0 / s1
+// the block scales of rows l % 32 and l % 32 + 32, xh / xl the staged panel.
+template <uint32_t T>
+__device__ __forceinline__ void mfma_half(const u32x4 *q, const uint32_t *s0, const uint32_t *s1,
+                                          const _Float16 *xh, const _Float16 *xl, int half, int xi, int xg,
+                                          f32x16 &acc0, f32x16 &acc1) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int blk = 4 * half + j;
+        f32x16 c0 = {}, c1 = {};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {  // 16-column steps of the block
+            h8v b0, b1;
+            if constexpr (T == ANEHIP_GGML_Q8_0) {
+                const u32x4 v = q[2 * j + h];
+                uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
+                swap_halves(a0, a1, c0w, c1w);
+                b0 = dwords_to_h8_i8(a0, a1);
+                b1 = dwords_to_h8_i8(c0w, c1w);
+            } else {
+                const u32x4 v = q[j];
+                uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
+                swap_halves(a0, a1, c0w, c1w);
+                const uint32_t sh = 4 * h;  // step 0: low nibbles, step 1: high nibbles
+                b0 = dwords_to_h8_u4((a0 >> sh) & 0x0F0F0F0Fu, (a1 >> sh) & 0x0F0F0F0Fu);
+                b1 = dwords_to_h8_u4((c0w >> sh) & 0x0F0F0F0Fu, (c1w >> sh) & 0x0F0F0F0Fu);
+            }
+            const int col = 32 * blk + 16 * h + 8 * xg;
+            const h8v ah = *reinterpret_cast<const h8v *>(xh + xi * kXRow + col);
+            const h8v al = *reinterpret_cast<const h8v *>(xl + xi * kXRow + col);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0, c0, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1, c1, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1, c1, 0, 0, 0);
+        }
+        const float d0 = __half2float(__ushort_as_half((unsigned short)(s0[blk >> 1] >> (16 * (blk & 1)))));
+        const float d1 = __half2float(__ushort_as_half((unsigned short)(s1[blk >> 1] >> (16 * (blk & 1)))));
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            acc0[r] = fmaf(c0[r], d0, acc0[r]);
+            acc1[r] = fmaf(c1[r], d1, acc1[r]);
+        }
+    }
+}
+
+// One wave per 64-row tile, the split's panels in order; per panel the x
+// planes are staged once for the 4 waves and each half panel's weights are
+// loaded into registers just before use.  No cross-panel prefetch: the
+// registers stay under 168, so 3 workgroups share a CU and hide each other's
+// load latency.  Loads are unconditional (idle waves read one vector of the
+// weight buffer) so the vmcnt waits stay exact.
+template <uint32_t T>
+__global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(3))) void gemm_packed(
+    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ ph, const _Float16 *__restrict__ pl,
+    float *__restrict__ out, int m, int n, int batch, int sb_per_split, size_t split_stride) {
+    constexpr int NH = Panel<T>::kChunks / 2;
+    __shared__ __align__(16) _Float16 xh[32 * kXRow];
+    __shared__ __align__(16) _Float16 xl[32 * kXRow];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int tiles = (m + kWave - 1) / kWave;
+    const int tile = blockIdx.x * kGemmWaves + wave;
+    const bool valid = tile < tiles;
+    const int nsb = n >> 8;
+    const int ks = blockIdx.y;
+    const int sb_begin = ks * sb_per_split;
+    const int sb_end = min(nsb, sb_begin + sb_per_split);
+    const uint8_t *tb = Wp + (size_t)(valid ? tile : 0) * nsb * Panel<T>::kBytes;
+    const int xi = lane & 31, xg = lane >> 5;  // A operand: batch row, column group
+
+    f32x16 acc0 = {}, acc1 = {};
+    for (int sb = sb_begin; sb < sb_end; sb++) {
+        const uint8_t *pc = tb + (size_t)sb * Panel<T>::kBytes;
+        u32x4 q[NH];
+        load_half<T>(q, pc, Wp, 0, lane, valid);
+        const u32x4 sc = load_scales<T>(pc, Wp, lane, valid);
+        if (sb != sb_begin) __syncthreads();  // the previous panel's reads of the planes are done
+        stage_planes(ph, pl, xh, xl, n, batch, sb, t);
+        __syncthreads();
+        // block scales of row (l % 32) and (l % 32) + 32
+        uint32_t s0[4] = {sc.x, sc.y, sc.z, sc.w}, s1[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const auto p = __builtin_amdgcn_permlane32_swap(s0[i], s1[i], false, false);
+            s0[i] = p[0];
+            s1[i] = p[1];
+        }
+        if (valid) mfma_half<T>(q, s0, s1, xh, xl, 0, xi, xg, acc0, acc1);
+        load_half<T>(q, pc, Wp, 1, lane, valid);
+        if (valid) mfma_half<T>(q, s0, s1, xh, xl, 1, xi, xg, acc0, acc1);
+    }
+    if (!valid) return;
+    const int row0 = tile * kWave + xi, row1 = row0 + 32;
+    float *o = out + (size_t)ks * split_stride;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int b = 8 * (r >> 2) + 4 * xg + (r & 3);
+        if (b < batch) {
+            if (row0 < m) o[(size_t)b * m + row0] = acc0[r];
+            if (row1 < m) o[(size_t)b * m + row1] = acc1[r];
+        }
     }
 }
 
@@ -997,6 +1223,38 @@ int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
     return packed_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256);
 }
 
+// K splits of the panel MFMA GEMM: the fewest that give half the CUs a
+// workgroup (at most kMaxSplit, no empty split).
+int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+    const int groups = (int)((m + kWave * kGemmWaves - 1) / (kWave * kGemmWaves));
+    const int nsb = (int)(n / 256), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    int best = 1;
+    for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
+        const int per = (nsb + k - 1) / k;
+        if ((k - 1) * per >= nsb) continue;
+        best = k;
+        if (2 * groups * k >= cus) return k;
+    }
+    return best;
+}
+
+int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
+                       uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit) {
+    const int groups = (int)((m + kWave * kGemmWaves - 1) / (kWave * kGemmWaves));
+    const int per = split_len((int)(n / 256), ksplit);
+    const dim3 grid(groups, ksplit), block(kWave * kGemmWaves);
+    const uint8_t *w = static_cast<const uint8_t *>(wp);
+    const size_t ss = (size_t)batch * m;
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        hipLaunchKernelGGL(gemm_packed<ANEHIP_GGML_Q8_0>, grid, block, 0, stream, w, xh, xl, out, (int)m, (int)n,
+                           (int)batch, per, ss);
+    else
+        hipLaunchKernelGGL(gemm_packed<ANEHIP_GGML_Q4_0>, grid, block, 0, stream, w, xh, xl, out, (int)m, (int)n,
+                           (int)batch, per, ss);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
 size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n) {
     const size_t tiles = (m + 63) / 64, nsb = n / 256;
     return tiles * nsb * (ggml_type == ANEHIP_GGML_Q8_0 ? Panel<ANEHIP_GGML_Q8_0>::kBytes : Panel<ANEHIP_GGML_Q4_0>::kBytes);
@@ -1080,6 +1338,12 @@ int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     if (ggml_type == ANEHIP_GGML_Q8_0)
         return dispatch_packed<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, in, out, ksplit);
     return dispatch_packed<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, in, out, ksplit);
+}
+
+int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, size_t count, _Float16 *xh, _Float16 *xl) {
+    hipLaunchKernelGGL(split_x_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, x, xh, xl, count);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
 }
 
 int launch_gemm_planes(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,

@@ -210,6 +210,32 @@ int anehip_quant_gemm(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32
     return launch_quant_gemm(ctx, ctx->stream, ggml_type, w, m, n, x, batch, y);
 }
 
+int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
+                             const float *x, uint32_t batch, float *y) {
+    if (!ctx) return set_error(global_error(), ANEHIP_EINVAL, "quant_gemm_packed: ctx is NULL");
+    if (!wp || !x || !y) return set_error(ctx->err, ANEHIP_EINVAL, "quant_gemm_packed: null pointer");
+    if (ggml_type != ANEHIP_GGML_Q8_0 && ggml_type != ANEHIP_GGML_Q4_0)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: ggml type %u (only Q4_0=2, Q8_0=8)",
+                         ggml_type);
+    if (m == 0 || n == 0 || n % 256)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "quant_gemm_packed: n=%u must be a positive multiple of 256", n);
+    if (batch == 0 || batch > 32)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: batch=%u outside 1..32", batch);
+    if (batch == 1) return anehip_quant_gemv_packed(ctx, ggml_type, wp, m, n, x, y);
+    const int ksplit = gemm_packed_ksplit(ctx, m, n);
+    const size_t count = (size_t)batch * m, xcount = (size_t)batch * n;
+    // workspace: [x hi plane][x lo plane] (fp16, xcount each) then the partials
+    const size_t planes = xcount;  // floats holding both planes (xcount is a multiple of 256)
+    int rc = ensure_workspace(ctx, planes + (ksplit > 1 ? (size_t)ksplit * count : 0));
+    if (rc) return rc;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(ctx->ws.partial), *xl = xh + xcount;
+    if ((rc = launch_split_x(ctx, ctx->stream, x, xcount, xh, xl))) return rc;
+    if (ksplit == 1) return launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xh, xl, batch, y, 1);
+    float *part = ctx->ws.partial + planes;
+    if ((rc = launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xh, xl, batch, part, ksplit))) return rc;
+    return launch_sum_partials(ctx, ctx->stream, part, y, count, ksplit);
+}
+
 struct anehip_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;

@@ -6,9 +6,10 @@ GEMM sweep over the shapes [6144 x 2048], [2048 x 6144], [151936 x 2048] with
 batch M in {1, 4, 16, 32}.  One "step" is one pass over the 12 (shape, M)
 points; `value` is the sweep's algorithmic bytes (weights once + fp32
 activations in + fp32 outputs) per second, inputs resident in HBM.  M = 1
-runs the batch-1 GEMV over the panel copy of the weights (the layout the
-decode step keeps resident: same bytes, permuted once at upload); M > 1 runs
-the MFMA GEMM over the GGUF blocks.  Weights are rotated over enough distinct
+runs the batch-1 GEMV and M > 1 the MFMA GEMM over the panel copy of the
+weights (the layout the decode step keeps resident: same bytes, permuted once
+at upload); `gguf_layout_points` times the same points through the entry
+point that reads the GGUF blocks directly (anehip_quant_gemm).  Weights are rotated over enough distinct
 copies (> 512 MiB per shape) that the 256 MiB MALL cannot serve repeated
 reads.  Each sweep pass is one captured hipGraph (anehip_capture_*), so the
 host's launch rate does not enter the figure.
@@ -116,12 +117,13 @@ class Shape:
         return self.p.ptr + (c % self.copies) * self.pbytes
 
 
-def launch_point(ctx, s, batch, c):
-    """One GEMV (M = 1, panel layout) or MFMA GEMM (M > 1, GGUF blocks) on copy c."""
-    if batch == 1:
-        ctx.call("quant_gemv_packed", Q8, s.pptr(c), s.m, s.n, s.x.ptr, s.y.ptr)
-    else:
+def launch_point(ctx, s, batch, c, gguf=False):
+    """One GEMV (M = 1) or MFMA GEMM (M > 1) on copy c: over the panel copy
+    (the decode step's layout), or with gguf=True over the GGUF blocks."""
+    if gguf:
         ctx.quant_gemm(Q8, s.wptr(c), s.m, s.n, s.x, batch, s.y)
+    else:
+        ctx.call("quant_gemm_packed", Q8, s.pptr(c), s.m, s.n, s.x.ptr, batch, s.y.ptr)
 
 
 def capture(ctx, enqueue):
@@ -147,9 +149,9 @@ def time_graphs(ctx, graphs, launches, warmup=2):
     return ctx.timer_stop()
 
 
-def time_point(ctx, s, batch, launches):
+def time_point(ctx, s, batch, launches, gguf=False):
     """Average time of one launch, `launches` back to back in one graph (copies rotated)."""
-    g = capture(ctx, lambda: [launch_point(ctx, s, batch, c) for c in range(launches)])
+    g = capture(ctx, lambda: [launch_point(ctx, s, batch, c, gguf) for c in range(launches)])
     ms = time_graphs(ctx, [g], 3) / 3
     ctx.graph_destroy(g)
     return ms / launches
@@ -312,12 +314,13 @@ def main():
     sweep_bytes = sum(algo_bytes(s.m, s.n, b) for s in shapes for b in BATCHES)
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
 
-    points = {}
+    points, gguf_points = {}, {}
     for s in shapes:
         for b in BATCHES:
-            t = time_point(ctx, s, b, max(s.copies, 20))
-            points[f"{s.m}x{s.n}_M{b}"] = {"us": round(t * 1e3, 2),
-                                           "GB/s": round(algo_bytes(s.m, s.n, b) / (t * 1e-3) / 1e9, 1)}
+            for gguf, dst in ((False, points), (True, gguf_points)):
+                t = time_point(ctx, s, b, max(s.copies, 20), gguf)
+                dst[f"{s.m}x{s.n}_M{b}"] = {"us": round(t * 1e3, 2),
+                                            "GB/s": round(algo_bytes(s.m, s.n, b) / (t * 1e-3) / 1e9, 1)}
     lm = shapes[2]
     t_lm = time_point(ctx, lm, 1, 50)
     lm_bytes = algo_bytes(lm.m, lm.n, 1)
@@ -358,6 +361,7 @@ def main():
         "c0_gemv_6144x2048": {"us": c0["us"], "GB/s": c0["GB/s"],
                                "pct_of_hbm_peak": round(100 * c0["GB/s"] / HBM_PEAK_GBS, 1)},
         "sweep_points": points,
+        "gguf_layout_points": gguf_points,
     }
     if not args.no_decode:
         out["decode"] = bench_decode(anehip, args.decode_steps, 3)

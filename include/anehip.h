@@ -196,6 +196,12 @@ size_t anehip_quant_packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
 int anehip_quant_pack(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n, void *dst);
 int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
                              const float *x, float *y);
+/* anehip_quant_gemm_packed: y[b][r] = W[r] . x[b] for b < batch (1..32), from
+ * the panel copy wp; x [batch][n] fp32.  batch 1 is
+ * anehip_quant_gemv_packed; batch > 1 runs on MFMA (the small-batch form of
+ * anehip_quant_gemm, same tolerance). */
+int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
+                             const float *x, uint32_t batch, float *y);
 
 /* Row-wise RMSNorm: out[r] = x[r] * 1/sqrt(mean(x[r]^2) + eps) * w, rows x n.
  * rmsnorm_simple (deltanet.metal:239-272) / rmsnorm_vec (main.rs:1106-1113). */
@@ -275,7 +281,7 @@ int anehip_upload_f32(anehip_ctx *ctx, int32_t layer, uint32_t kind, const float
 /* Device address where tensor `kind` of `layer` lives (allocated on first
  * use, with ggml_type for quantised kinds, ignored for fp32 kinds), so a
  * caller can write it in place (e.g. with anehip_quantize); the tensor then
- * counts as uploaded.  *nbytes receives its size.  The batch-1 step reads a
+ * counts as uploaded.  *nbytes receives its size.  The decode step reads a
  * panel copy of quantised weights that is rebuilt at the first step after
  * this call (or after anehip_upload_quant): write before that step. */
 int anehip_tensor_ptr(anehip_ctx *ctx, int32_t layer, uint32_t kind, uint32_t ggml_type, void **dptr,

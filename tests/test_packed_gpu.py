@@ -100,3 +100,39 @@ def test_packed_rejects_bad_shapes(gpu_ctx, anehip_mod):
         gpu_ctx.call("quant_gemv_packed", 14, d, 64, 256, d, d)
     assert e.value.code == -3
     d.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("batch", [2, 3, 4, 7, 16, 17, 32])
+@pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144), (100, 256), (8224, 2048)])
+def test_packed_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
+    """Panel MFMA GEMM, ragged batch (not padded to the 32-row MFMA tile)."""
+    w = oracle_lib.gen_quant(t, 99, m + 5 * n + t, m, n, std=0.02)
+    x = oracle_lib.normal(99, 300 + batch, batch * n).reshape(batch, n)
+    dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
+    dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(batch * m * 4)
+    gpu_ctx.call("quant_gemm_packed", t, dp, m, n, dx, batch, dy)
+    y = dy.download(np.float32, batch * m).reshape(batch, m)
+    ref = oracle_lib.gemm(t, w, m, n, x)
+    l2, mx = rel_errs(y, ref)
+    print(f"type={t} m={m} n={n} batch={batch}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+    assert l2 <= TOL and mx <= TOL
+    for b in (dw, dp, dx, dy):
+        b.free()
+
+
+@pytest.mark.gpu
+def test_packed_gemm_lm_head_batch32(gpu_ctx, oracle_lib):
+    m, n, batch = 151936, 2048, 32
+    w = oracle_lib.gen_quant(8, 6, 6, m, n, std=0.02)
+    x = oracle_lib.normal(6, 7, batch * n).reshape(batch, n)
+    dw, dp, _ = _pack(gpu_ctx, 8, w, m, n)
+    dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(batch * m * 4)
+    gpu_ctx.call("quant_gemm_packed", 8, dp, m, n, dx, batch, dy)
+    y = dy.download(np.float32, batch * m).reshape(batch, m)
+    for b in (0, 17, 31):
+        l2, mx = rel_errs(y[b], oracle_lib.gemv(8, w, m, n, x[b]))
+        assert l2 <= TOL and mx <= TOL
+    for buf in (dw, dp, dx, dy):
+        buf.free()
