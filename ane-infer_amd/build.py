@@ -1,7 +1,8 @@
-"""Builds libanehip.so (all HIP sources in csrc/) for gfx950 with hipcc.
+"""Builds libanehip.so (all HIP sources in csrc/) for gfx950 with hipcc, and
+libane_engine.so (the C++ host API in engine/, over libanehip) with g++.
 
 Usage: python ane-infer_amd/build.py
-The library is written next to this file so it travels with the source tree.
+The libraries are written next to this file so they travel with the source tree.
 """
 import glob
 import os
@@ -10,6 +11,8 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "libanehip.so")
+ENGINE_LIB = os.path.join(HERE, "libane_engine.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
 HIPCC_FLAGS = [
     "-O3",
@@ -42,7 +45,22 @@ def build(verbose: bool = False) -> str:
     if errs and verbose:
         print("\n".join(errs), file=sys.stderr)
     os.replace(tmp, LIB)
+    build_engine(verbose)
     return LIB
+
+
+def build_engine(verbose: bool = False) -> str:
+    tmp = ENGINE_LIB + ".tmp"
+    cmd = [os.environ.get("CXX", "g++"), "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
+           f"-I{INCLUDE}", os.path.join(HERE, "engine", "ane_engine.cpp"), f"-L{HERE}", "-lanehip",
+           "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("g++ failed:\n" + res.stderr)
+    os.replace(tmp, ENGINE_LIB)
+    return ENGINE_LIB
 
 
 if __name__ == "__main__":
