@@ -86,6 +86,22 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     const size_t cache_base = ((size_t)b * n_kv + kvh) * (size_t)max_seq * kHd;
     const bool has_new = (int)pos < start + kCh;  // this chunk holds the current position
 
+    // K and V rows of the chunk (positions < pos) are loaded first, so their
+    // memory latency overlaps the q / k preparation below.  Row pos comes from
+    // this step's k / v (knew / vnew); rows past pos are zero.
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int kPer = (kCh * kHd / 8) / kThreads;  // 16-byte vectors per thread and tile
+    u32x4 kreg[kPer], vreg[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int q = i * kThreads + t;
+        const int r = q >> 5, part = q & 31;
+        const int p = min(start + r, (int)pos - 1);  // in bounds; rows >= pos are replaced below
+        const size_t off = cache_base + (size_t)max(p, 0) * kHd + part * 8;
+        kreg[i] = *reinterpret_cast<const u32x4 *>(k_cache + off);
+        vreg[i] = *reinterpret_cast<const u32x4 *>(v_cache + off);
+    }
+
     // q heads of this kv group: wave w < G prepares head kvh*G + w
     if (wave < G) {
         const int h = kvh * G + wave;
@@ -116,26 +132,20 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     }
     __syncthreads();
 
-    // K tile: 64 rows x 32 chunks of 16 bytes; chunk q = i*256 + t
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    auto load_tile = [&](const __half *cache, const __half *fresh) {
+    // tile: 64 rows x 32 vectors of 16 bytes; vector q = i*256 + t
+    auto store_tile = [&](const u32x4 *reg, const __half *fresh) {
 #pragma unroll
-        for (int i = 0; i < (kCh * kHd / 8) / kThreads; i++) {
+        for (int i = 0; i < kPer; i++) {
             const int q = i * kThreads + t;
             const int r = q >> 5, part = q & 31;
             const int p = start + r;
-            u32x4 v;
-            if (p < (int)pos) {
-                v = *reinterpret_cast<const u32x4 *>(cache + cache_base + (size_t)p * kHd + part * 8);
-            } else if (p == (int)pos) {
-                v = *reinterpret_cast<const u32x4 *>(fresh + part * 8);
-            } else {
-                v = u32x4{0u, 0u, 0u, 0u};
-            }
+            u32x4 v = reg[i];
+            if (p == (int)pos) v = *reinterpret_cast<const u32x4 *>(fresh + part * 8);
+            if (p > (int)pos) v = u32x4{0u, 0u, 0u, 0u};
             *reinterpret_cast<u32x4 *>(&tile[r * kRowH + part * 8]) = v;
         }
     };
-    load_tile(k_cache, knew);
+    store_tile(kreg, knew);
     __syncthreads();
 
     // scores: wave = query head of the group, lane = position in the chunk
@@ -167,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         }
     }
     __syncthreads();
-    load_tile(v_cache, vnew);
+    store_tile(vreg, vnew);
     __syncthreads();
 
     // PV: wave = query head, lane = 4 consecutive dims
@@ -199,21 +209,52 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
                                                                 int n_heads, int n_kv, float *__restrict__ out,
                                                                 _Float16 *__restrict__ out_hi,
                                                                 _Float16 *__restrict__ out_lo) {
+    __shared__ float wts[kThreads], red[4];
     const int d = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int kvh = h / G, hh = h % G;
     const int len = (int)pos_arr[b] + 1;
     const int nc = (len + kCh - 1) / kCh;
     const size_t base = ((size_t)b * n_kv + kvh) * nch;
-    float M = -INFINITY;
-    for (int c = 0; c < nc; c++) M = fmaxf(M, part_ml[((base + c) * G + hh) * 2]);
-    float num = 0.f, den = 0.f;
-    for (int c = 0; c < nc; c++) {
-        const float *ml = &part_ml[((base + c) * G + hh) * 2];
-        const float w = expf(ml[0] - M);
-        num += w * part_o[((base + c) * G + hh) * kHd + d];
-        den += w * ml[1];
+    const float g = mix.at(b, h * 2 * kHd + kHd + d);  // issued early: independent of the partials
+    // rounds of up to 256 chunks; the running maximum only grows, earlier
+    // rounds are rescaled to it (log-sum-exp merge)
+    float num = 0.f, den = 0.f, M = -INFINITY;
+    for (int c0 = 0; c0 < nc; c0 += kThreads) {
+        const int cc = c0 + d;
+        const float m = cc < nc ? part_ml[((base + cc) * G + hh) * 2] : -INFINITY;
+        float mx = m;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        if ((d & 63) == 0) red[d >> 6] = mx;
+        __syncthreads();
+        const float Mn = fmaxf(M, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+        const float rescale = expf(M - Mn);  // 0 in the first round (num = den = 0)
+        num *= rescale;
+        den *= rescale;
+        M = Mn;
+        wts[d] = cc < nc ? expf(m - M) : 0.0f;
+        __syncthreads();
+        const int n = min(kThreads, nc - c0);
+        int c = 0;
+        for (; c + 4 <= n; c += 4) {  // 4 independent loads per trip
+            float o4[4], l4[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                o4[i] = part_o[((base + c0 + c + i) * G + hh) * kHd + d];
+                l4[i] = part_ml[((base + c0 + c + i) * G + hh) * 2 + 1];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                num += wts[c + i] * o4[i];
+                den += wts[c + i] * l4[i];
+            }
+        }
+        for (; c < n; c++) {
+            num += wts[c] * part_o[((base + c0 + c) * G + hh) * kHd + d];
+            den += wts[c] * part_ml[((base + c0 + c) * G + hh) * 2 + 1];
+        }
+        __syncthreads();  // wts / red are rewritten by the next round
     }
-    const float g = mix.at(b, h * 2 * kHd + kHd + d);
     const float v = (num / den) * (1.0f / (1.0f + expf(-g)));
     const size_t o = (size_t)b * n_heads * kHd + (size_t)h * kHd + d;
     if (out_hi) {
