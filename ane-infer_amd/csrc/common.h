@@ -160,8 +160,10 @@ int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                        uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit);
 int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, size_t count, _Float16 *xh, _Float16 *xl);
-// K splits the batch-1 panel GEMV takes for an [m x n] matrix (<= 8).
-int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
+// K splits the batch-1 panel GEMV takes for an [m x n] matrix (<= 8);
+// norm_prologue: the input is formed by a (residual / embedding) RMSNorm
+// prologue, which favours fewer splits.
+int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, bool norm_prologue = false);
 int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                        uint32_t n, const GemvInput &in, float *out, int ksplit);
 // Small-batch GEMM (batch 2..32) on MFMA from fp16 hi/lo input planes

@@ -297,7 +297,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in1.token = M->d_tokens;
         in1.emb = M->embedding;
         in1.vocab = D.vocab_size;
-        const int k1 = gemv_packed_ksplit(ctx, rows_in, d);
+        const int k1 = gemv_packed_ksplit(ctx, rows_in, d, true);
         TRY(launch_gemv_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, in1, M->pmix, k1));
         std::swap(cur, nxt);
         MixIn mix;
@@ -341,7 +341,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in4.w = L.post_attn_norm;
         in4.eps = eps;
         in4.x_out = nxt;
-        const int k4 = gemv_packed_ksplit(ctx, 2 * F, d);
+        const int k4 = gemv_packed_ksplit(ctx, 2 * F, d, true);
         TRY(launch_gemv_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, in4, M->p1, k4));
         std::swap(cur, nxt);
         // 5. FFN down, input = SiLU(gate) * up
@@ -365,7 +365,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     inf.w = M->final_norm;
     inf.eps = eps;
     inf.x_out = nxt;
-    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d);
+    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d, true);
     if (kf == 1) {
         TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->logits, 1));
     } else {
@@ -448,12 +448,13 @@ size_t part_floats(anehip_ctx *ctx, Model *M) {
     const uint32_t d = D.dim, F = D.hidden_dim;
     struct {
         uint32_t m, n;
-    } g[] = {{M->rows_dn, d}, {M->rows_attn, d}, {d, d}, {d, D.n_heads * D.head_dim}, {2 * F, d}, {d, F},
-             {D.vocab_size, d}};
+        bool norm;
+    } g[] = {{M->rows_dn, d, true}, {M->rows_attn, d, true}, {d, d, false}, {d, D.n_heads * D.head_dim, false},
+             {2 * F, d, true}, {d, F, false}, {D.vocab_size, d, true}};
     size_t mx = 0;
     for (auto &e : g) {
         if (!e.m) continue;
-        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n) : gemm_packed_ksplit(ctx, e.m, e.n);
+        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n, e.norm) : gemm_packed_ksplit(ctx, e.m, e.n);
         size_t need = (size_t)k * M->batch * e.m;
         if (need > mx) mx = need;
     }

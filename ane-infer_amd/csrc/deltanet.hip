@@ -73,6 +73,15 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
     const int c0 = slice * kCols;
     float *cs = conv_state + (size_t)b * C * kKsize;
 
+    // the state slice is loaded first: its memory latency overlaps steps 1-2
+    // (thread -> 4 columns (cq) x 4 rows (rg))
+    const int cq = t & 7;          // column quad: columns c0 + 4cq .. +3
+    const int rg = t >> 3;         // row group: rows 4rg .. 4rg+3
+    float *Sh = S + (((size_t)b * n_heads + h) * kDk) * kDk + c0 + 4 * cq;
+    float4 s[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(4 * rg + r) * kDk);
+
     // 1. conv + SiLU of the head's q (t < 128) and k (t >= 128) channels, from
     // the old window (committed later by dn_finish / the ssm_out GEMV)
     {
@@ -108,15 +117,8 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
     }
     __syncthreads();
 
-    // 3. state slice: thread -> 4 columns (cq) x 4 rows (rg)
-    const int cq = t & 7;          // column quad: columns c0 + 4cq .. +3
-    const int rg = t >> 3;         // row group: rows 4rg .. 4rg+3
     const float beta = misc[0], decay = misc[1];
-    float *Sh = S + (((size_t)b * n_heads + h) * kDk) * kDk + c0 + 4 * cq;
-    float4 s[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(4 * rg + r) * kDk);
-    // S' = decay * S, partial recall sum_i S'_ij k_i over this thread's rows
+    // 3. S' = decay * S, partial recall sum_i S'_ij k_i over this thread's rows
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int r = 0; r < 4; r++) {

@@ -1200,15 +1200,15 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
 
 }  // namespace
 
-// K splits of the batch-1 panel GEMV: the fewest that give every CU a
-// workgroup (at most kMaxSplit, whole panels, no empty split).
-static int packed_ksplit(int tiles, int nsb, int cus) {
+// K splits of the batch-1 panel GEMV: the fewest that give `want` workgroups
+// (at most kMaxSplit, whole panels, no empty split).
+static int packed_ksplit(int tiles, int nsb, int want) {
     int best = 1;
     for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
         const int per = (nsb + k - 1) / k;
         if ((k - 1) * per >= nsb) continue;
         best = k;
-        if (tiles * k >= cus && per <= kMaxSliceSb) return k;
+        if (tiles * k >= want && per <= kMaxSliceSb) return k;
     }
     return best;
 }
@@ -1218,9 +1218,12 @@ int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int max_k) {
     return choose_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256, max_k);
 }
 
-int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, bool norm_prologue) {
     const int tiles = (int)((m + kWave - 1) / kWave);
-    return packed_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256);
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    // a norm prologue re-reads the whole input vector (and its partial slices)
+    // in every workgroup, so such GEMVs stop splitting at half the CUs
+    return packed_ksplit(tiles, (int)(n / 256), norm_prologue ? cus / 2 : cus);
 }
 
 // K splits of the panel MFMA GEMM: the fewest that give half the CUs a
