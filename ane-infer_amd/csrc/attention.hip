@@ -256,13 +256,13 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
         __syncthreads();  // wts / red are rewritten by the next round
     }
     const float v = (num / den) * (1.0f / (1.0f + expf(-g)));
-    const size_t o = (size_t)b * n_heads * kHd + (size_t)h * kHd + d;
     if (out_hi) {
+        const size_t o = xf_index(b, h * kHd + d);
         const _Float16 hi = (_Float16)v;
         out_hi[o] = hi;
         out_lo[o] = (_Float16)(v - (float)hi);
     } else {
-        out[o] = v;
+        out[(size_t)b * n_heads * kHd + (size_t)h * kHd + d] = v;
     }
 }
 

@@ -153,13 +153,27 @@ int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, 
 size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
 int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
                   void *dst);
+// Input planes of the panel MFMA GEMM (batch 2..32): fp16 hi / lo planes of
+// x in "fragment order", 32 rows (batch entries) x n columns per plane.
+// Element (b, c) lies in the 1 KiB block of its 16-column step c / 16, at the
+// lane that holds it in the A operand of v_mfma_f32_32x32x16_f16 (lane
+// b + 32 * ((c / 8) % 2), 8 consecutive columns per lane), so a wave loads
+// one step's operand with one fully contiguous 1 KiB load.  Rows past the
+// batch are never read.
+__host__ __device__ inline size_t xf_index(int b, int c) {
+    return ((size_t)(c >> 4) * 64 + (size_t)(b + 32 * ((c >> 3) & 1))) * 8 + (size_t)(c & 7);
+}
+inline size_t xf_plane_len(size_t n) { return 32 * n; }
 // Panel MFMA GEMM for batch 2..32: out[ks][b][r] (final values when ksplit
-// is 1) from the fp16 hi / lo planes of x [batch][n] (launch_split_x, or the
+// is 1) from the fragment-order hi / lo planes of x (launch_split_x, or the
 // hi / lo outputs of the element-wise kernels), ksplit from gemm_packed_ksplit.
+// m must be a multiple of 4.
 int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                        uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit);
-int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, size_t count, _Float16 *xh, _Float16 *xl);
+// x [batch][n] fp32 -> fragment-order hi / lo planes (xf_plane_len(n) halves each).
+int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t batch, uint32_t n, _Float16 *xh,
+                   _Float16 *xl);
 // K splits the batch-1 panel GEMV takes for an [m x n] matrix (<= 8);
 // norm_prologue: the input is formed by a (residual / embedding) RMSNorm
 // prologue, which favours fewer splits.
@@ -181,7 +195,7 @@ int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
                          const float *dt_bias, float *conv_state, float *S, float *out);
 // Commits the q/k conv windows (if conv_state) and, if heads, writes the gated
 // RMSNorm of the heads (gate from mix rows at gate_off) to out (fp32) or, if
-// out_hi, to fp16 hi/lo planes out_hi / out_lo.
+// out_hi, to fragment-order fp16 hi/lo planes out_hi / out_lo (xf_index).
 int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                      float *conv_state, const float *heads, int gate_off, const float *norm_w, float *out,
                      _Float16 *out_hi, _Float16 *out_lo, float eps);
@@ -197,7 +211,7 @@ int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
 int launch_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const float *x, const float *w, float *out,
                    float eps);
 // The next three write their result as fp32 (xn / h) or, when hi is not null,
-// as fp16 hi/lo planes for the small-batch MFMA GEMM.
+// as fragment-order fp16 hi/lo planes (xf_index) for the panel MFMA GEMM.
 int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const uint32_t *tokens,
                          const float *emb, uint32_t vocab, float *x, const float *w, float *xn, float eps,
                          _Float16 *hi = nullptr, _Float16 *lo = nullptr);

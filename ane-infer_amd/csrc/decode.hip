@@ -76,7 +76,7 @@ struct Model {
     float *pmix = nullptr, *p0 = nullptr, *p1 = nullptr;  // GEMV outputs as K-split partial slices
     float *heads = nullptr, *attn_out = nullptr, *logits = nullptr, *attn_part = nullptr;
     float *xin = nullptr;        // GEMM input planes (batch > 1): hi then lo, xin_len halves each
-    size_t xin_len = 0;          // batch * widest GEMM input
+    size_t xin_len = 0;          // fragment-order plane of the widest GEMM input (32 rows)
     size_t part_len = 0;         // floats per partial buffer
     void *argmax_ws = nullptr;
     // graph
@@ -773,7 +773,7 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     const size_t qd = (size_t)D.n_heads * D.head_dim;
     size_t nmax = d > F ? d : F;
     if (qd > nmax) nmax = qd;
-    M->xin_len = batch * nmax;
+    M->xin_len = xf_plane_len(nmax);
     M->part_len = part_floats(ctx, M);
     r = r ? r : alloc((void **)&M->d_pos, 64 * sizeof(uint32_t));
     r = r ? r : alloc((void **)&M->d_tokens, 64 * sizeof(uint32_t));

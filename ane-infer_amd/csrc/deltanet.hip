@@ -164,8 +164,8 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
 // q/k conv windows of head h (shift left, append the new input:
 // deltanet_cache.rs:34-42); if `heads` is not null, applies the per-head
 // RMSNorm with ssm_norm and the SiLU(gate) product (deltanet.rs:517-533),
-// written as fp32 (out) or as fp16 hi/lo planes (out_hi / out_lo, the input
-// format of the small-batch MFMA GEMM).  grid = (n_heads, batch), 128 threads
+// written as fp32 (out) or as fragment-order fp16 hi/lo planes (out_hi /
+// out_lo, the input format of the panel MFMA GEMM).  grid = (n_heads, batch), 128 threads
 // (one per element of the head).
 __global__ __launch_bounds__(kDk) void dn_finish_kernel(MixIn mix, float *__restrict__ conv_state,
                                                         const float *__restrict__ heads, int gate_off,
@@ -192,13 +192,13 @@ __global__ __launch_bounds__(kDk) void dn_finish_kernel(MixIn mix, float *__rest
     const float inv_rms = 1.0f / sqrtf(ms + eps);
     const float g = mix.at(b, gate_off + h * kDk + t);
     const float v = ((x * inv_rms) * norm_w[t]) * (g / (1.0f + expf(-g)));
-    const size_t o = (size_t)b * chunk + h * kDk + t;
     if (out_hi) {
+        const size_t o = xf_index(b, h * kDk + t);
         const _Float16 hi = (_Float16)v;
         out_hi[o] = hi;
         out_lo[o] = (_Float16)(v - (float)hi);
     } else {
-        out[o] = v;
+        out[(size_t)b * chunk + h * kDk + t] = v;
     }
 }
 

@@ -34,10 +34,12 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 }
 
 // out[b] = x[b] * (1/sqrt(mean(x[b]^2) + eps)) * w     (main.rs:1106-1113),
-// written as fp32, or as fp16 hi/lo planes (hi + lo ~= value, the input
-// format of the small-batch MFMA GEMM) when hi is not null.
+// written as fp32, or as row `brow` of fragment-order fp16 hi/lo planes
+// (hi + lo ~= value, the input format of the panel MFMA GEMM) when hi is not
+// null.
 __device__ __forceinline__ void rmsnorm_row(const float *x, const float *__restrict__ w, float *out, int n,
-                                            float eps, float *red, _Float16 *hi = nullptr, _Float16 *lo = nullptr) {
+                                            float eps, float *red, _Float16 *hi = nullptr, _Float16 *lo = nullptr,
+                                            int brow = 0) {
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kThreads) ss += x[i] * x[i];
     ss = block_sum(ss, red);
@@ -46,8 +48,8 @@ __device__ __forceinline__ void rmsnorm_row(const float *x, const float *__restr
         const float v = (x[i] * inv_rms) * w[i];
         if (hi) {
             const _Float16 h = (_Float16)v;
-            hi[i] = h;
-            lo[i] = (_Float16)(v - (float)h);
+            hi[xf_index(brow, i)] = h;
+            lo[xf_index(brow, i)] = (_Float16)(v - (float)h);
         } else {
             out[i] = v;
         }
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(kThreads) void embed_rmsnorm_kernel(const uint32_t 
     float *xb = x + b * n;
     for (int i = threadIdx.x; i < n; i += kThreads) xb[i] = tok < vocab ? emb[(size_t)tok * n + i] : 0.0f;
     __syncthreads();
-    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi ? hi + b * n : nullptr, lo ? lo + b * n : nullptr);
+    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi, lo, (int)b);
 }
 
 // x[b] += sum_k part[k][b]; if w: xn[b] = rmsnorm(x[b], w).   part stride between
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(float *__res
     }
     if (!w) return;
     __syncthreads();
-    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi ? hi + b * n : nullptr, lo ? lo + b * n : nullptr);
+    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi, lo, (int)b);
 }
 
 // The same for rows of n <= 2048 (n % 4 == 0) with one workgroup of 512
@@ -148,8 +150,8 @@ __global__ __launch_bounds__(512) void residual_rmsnorm_v4(float *__restrict__ x
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const _Float16 h = (_Float16)v[c];
-            hi[b * n + 4 * t + c] = h;
-            lo[b * n + 4 * t + c] = (_Float16)(v[c] - (float)h);
+            hi[xf_index((int)b, 4 * t + c)] = h;
+            lo[xf_index((int)b, 4 * t + c)] = (_Float16)(v[c] - (float)h);
         }
     } else if (xn) {
         reinterpret_cast<float4 *>(xn)[b * n4 + t] = make_float4(v[0], v[1], v[2], v[3]);
@@ -173,8 +175,8 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restr
     const float v = (g / (1.0f + expf(-g))) * u;
     if (hi) {
         const _Float16 hh = (_Float16)v;
-        hi[b * F + r] = hh;
-        lo[b * F + r] = (_Float16)(v - (float)hh);
+        hi[xf_index((int)b, r)] = hh;
+        lo[xf_index((int)b, r)] = (_Float16)(v - (float)hh);
     } else {
         h[b * F + r] = v;
     }

@@ -718,13 +718,11 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
 // trip.  int8 / nibble values become fp16 exactly (0x6400 | (u8) is 1024 + u8,
 // minus 1152 or 1032).  Activations arrive as fp16 hi and lo planes (hi =
 // fp16(x), lo = fp16(x - hi), |x - hi - lo| <= 2^-22 |x|), written by the
-// producer of x, and are staged per panel in LDS: the two products summed in
-// fp32 reproduce the fp32 GEMV within its tolerance.
+// producer of x, and read by each wave straight from global memory (a few
+// hundred KiB, cache-resident): the two products summed in fp32 reproduce the
+// fp32 GEMV within its tolerance.
 // Per block: C = sum over its 2 column steps and the 2 planes, then
 // acc += C * d (q8_gemv.rs:234-242 order within a block up to fp32 summation).
-//
-// grid = (groups of 4 row tiles, K splits); 4 waves, wave w owns row tile
-// 4 blockIdx.x + w and walks the split's panels.
 // ---------------------------------------------------------------------------
 
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
@@ -732,7 +730,9 @@ typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmWaves = 4;
-constexpr int kXRow = 256 + 8;  // halfs per staged activation row (pad: conflict-free 16-byte reads)
+constexpr int kGemmRing = 2;  // panel GEMM: units in flight per wave
+// word 3 of a raw buffer resource on gfx9-family parts (data format 32 bit)
+constexpr int kBufferWord3 = 0x00020000;
 
 // Four signed int8 (one dword) -> four fp16, exact.
 __device__ __forceinline__ void i8x4_to_h(uint32_t d, _Float16 *o) {
@@ -784,84 +784,83 @@ __device__ __forceinline__ void swap_halves(uint32_t &a0, uint32_t &a1, uint32_t
     b1 = s1[1];
 }
 
-// Half a panel (4 blocks) of one wave's tile: quant vectors + the panel's
-// scale vector.  `valid` false: every lane reads one vector of `dummy`.
-template <uint32_t T>
-__device__ __forceinline__ void load_half(u32x4 *q, const uint8_t *panel, const uint8_t *dummy, int half, int lane,
-                                          bool valid) {
-    constexpr int V = Panel<T>::kChunks / 2;
-    const u32x4 *p4 = reinterpret_cast<const u32x4 *>(valid ? panel : dummy);
-    const int l = valid ? lane : 0, c0 = valid ? V * half : 0;
-#pragma unroll
-    for (int c = 0; c < V; c++) q[c] = __builtin_nontemporal_load(p4 + (c0 + c) * 64 + l);
+// Barrier for LDS traffic only: the fences order LDS accesses, so waves do
+// not wait for their outstanding global loads (the prefetched units) here.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <uint32_t T>
-__device__ __forceinline__ u32x4 load_scales(const uint8_t *panel, const uint8_t *dummy, int lane, bool valid) {
-    const u32x4 *p4 = reinterpret_cast<const u32x4 *>(valid ? panel : dummy);
-    return __builtin_nontemporal_load(p4 + Panel<T>::kChunks * 64 + (valid ? lane : 0));
-}
+// One wave's operands for one panel of its tile: the quant vectors of its
+// column quarter q (blocks 2q, 2q + 1: Q8_0 chunks 4q..4q+3, Q4_0 chunks
+// 2q, 2q+1), the lane row's 16-byte scale vector, and the A fragments of x for
+// the quarter's 4 column steps (hi and lo planes, fragment order).
+template <uint32_t T> struct GemmUnit {
+    static constexpr int kQ = T == ANEHIP_GGML_Q8_0 ? 4 : 2;
+    u32x4 q[kQ];
+    u32x4 sc;
+    h8v ah[4], al[4];
+};
 
-// Stages the fp16 hi / lo planes of x[:, 256 sb .. +256] (rows >= batch as
-// zeros) into LDS: 32 rows x 32 sixteen-byte chunks per plane, 8 per thread.
-__device__ __forceinline__ void stage_planes(const _Float16 *__restrict__ ph, const _Float16 *__restrict__ pl,
-                                             _Float16 *xh, _Float16 *xl, int n, int batch, int sb, int t) {
+// Loads one unit: every lane issues the same, fully contiguous 1 KiB loads
+// (no lane masking, so the compiler's vmcnt waits stay exact).  `xo` is the
+// lane's element offset of its first A fragment in the fragment-order planes
+// (rows past the batch are redirected to row batch - 1: those lanes only feed
+// MFMA output rows that are never stored, and their loads hit the cache).
+template <uint32_t T>
+__device__ __forceinline__ void gemm_load(GemmUnit<T> &u, const uint8_t *panel, const _Float16 *__restrict__ xh,
+                                          const _Float16 *__restrict__ xl, size_t xo, int quarter, int lane) {
+    constexpr int Q = GemmUnit<T>::kQ;
+    const u32x4 *p4 = reinterpret_cast<const u32x4 *>(panel);
 #pragma unroll
-    for (int h = 0; h < 2; h++) {  // two rounds of 4 (fewer live registers)
-        u32x4 v[4];
+    for (int c = 0; c < Q; c++) u.q[c] = __builtin_nontemporal_load(p4 + (Q * quarter + c) * kWave + lane);
+    u.sc = __builtin_nontemporal_load(p4 + Panel<T>::kChunks * kWave + lane);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int idx = t + 256 * (4 * h + j), plane = idx >> 10, b = (idx >> 5) & 31, c = idx & 31;
-            const _Float16 *src = plane ? pl : ph;
-            const size_t off = b < batch ? (size_t)b * n + 256 * sb + 8 * c : 0;
-            v[j] = *reinterpret_cast<const u32x4 *>(src + off);
-            if (b >= batch) v[j] = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int idx = t + 256 * (4 * h + j), plane = idx >> 10, b = (idx >> 5) & 31, c = idx & 31;
-            *reinterpret_cast<u32x4 *>((plane ? xl : xh) + b * kXRow + 8 * c) = v[j];
-        }
+    for (int s = 0; s < 4; s++) {
+        u.ah[s] = *reinterpret_cast<const h8v *>(xh + xo + 512 * s);
+        u.al[s] = *reinterpret_cast<const h8v *>(xl + xo + 512 * s);
     }
 }
 
-// Blocks [4 half, 4 half + 4) of a panel: q holds their quant vectors, s0 / s1
-// the block scales of rows l % 32 and l % 32 + 32, xh / xl the staged panel.
+// acc{0,1} += the unit's two blocks: per block C = sum over its 2 column steps
+// and the 2 planes (4 MFMAs per 32 weight rows), then acc += C * d
+// (q8_gemv.rs:234-242 order within a block up to fp32 summation).
 template <uint32_t T>
-__device__ __forceinline__ void mfma_half(const u32x4 *q, const uint32_t *s0, const uint32_t *s1,
-                                          const _Float16 *xh, const _Float16 *xl, int half, int xi, int xg,
-                                          f32x16 &acc0, f32x16 &acc1) {
+__device__ __forceinline__ void gemm_mma(const GemmUnit<T> &u, int quarter, f32x16 &acc0, f32x16 &acc1) {
+    // dword `quarter` of the scale vector holds blocks 2q, 2q + 1; after the
+    // swap s0 / s1 are those of weight rows l % 32 (acc0) and 32 + l % 32 (acc1)
+    const uint32_t sw = quarter == 0 ? u.sc.x : quarter == 1 ? u.sc.y : quarter == 2 ? u.sc.z : u.sc.w;
+    const auto sp = __builtin_amdgcn_permlane32_swap(sw, sw, false, false);
+    const uint32_t s0 = sp[0], s1 = sp[1];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int blk = 4 * half + j;
+    for (int j = 0; j < 2; j++) {
         f32x16 c0 = {}, c1 = {};
 #pragma unroll
-        for (int h = 0; h < 2; h++) {  // 16-column steps of the block
+        for (int h = 0; h < 2; h++) {
+            const int s = 2 * j + h;  // column step: columns 16 s .. 16 s + 15 of the quarter
             h8v b0, b1;
             if constexpr (T == ANEHIP_GGML_Q8_0) {
-                const u32x4 v = q[2 * j + h];
+                const u32x4 v = u.q[s];
                 uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
                 swap_halves(a0, a1, c0w, c1w);
                 b0 = dwords_to_h8_i8(a0, a1);
                 b1 = dwords_to_h8_i8(c0w, c1w);
             } else {
-                const u32x4 v = q[j];
+                const u32x4 v = u.q[j];
                 uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
                 swap_halves(a0, a1, c0w, c1w);
                 const uint32_t sh = 4 * h;  // step 0: low nibbles, step 1: high nibbles
                 b0 = dwords_to_h8_u4((a0 >> sh) & 0x0F0F0F0Fu, (a1 >> sh) & 0x0F0F0F0Fu);
                 b1 = dwords_to_h8_u4((c0w >> sh) & 0x0F0F0F0Fu, (c1w >> sh) & 0x0F0F0F0Fu);
             }
-            const int col = 32 * blk + 16 * h + 8 * xg;
-            const h8v ah = *reinterpret_cast<const h8v *>(xh + xi * kXRow + col);
-            const h8v al = *reinterpret_cast<const h8v *>(xl + xi * kXRow + col);
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b0, c0, 0, 0, 0);
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b0, c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b1, c1, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b1, c1, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.ah[s], b0, c0, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.al[s], b0, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.ah[s], b1, c1, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.al[s], b1, c1, 0, 0, 0);
         }
-        const float d0 = __half2float(__ushort_as_half((unsigned short)(s0[blk >> 1] >> (16 * (blk & 1)))));
-        const float d1 = __half2float(__ushort_as_half((unsigned short)(s1[blk >> 1] >> (16 * (blk & 1)))));
+        const float d0 = __half2float(__ushort_as_half((unsigned short)(s0 >> (16 * j))));
+        const float d1 = __half2float(__ushort_as_half((unsigned short)(s1 >> (16 * j))));
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             acc0[r] = fmaf(c0[r], d0, acc0[r]);
@@ -870,64 +869,143 @@ __device__ __forceinline__ void mfma_half(const u32x4 *q, const uint32_t *s0, co
     }
 }
 
-// One wave per 64-row tile, the split's panels in order; per panel the x
-// planes are staged once for the 4 waves and each half panel's weights are
-// loaded into registers just before use.  No cross-panel prefetch: the
-// registers stay under 168, so 3 workgroups share a CU and hide each other's
-// load latency.  Loads are unconditional (idle waves read one vector of the
-// weight buffer) so the vmcnt waits stay exact.
-template <uint32_t T>
-__global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(3))) void gemm_packed(
-    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ ph, const _Float16 *__restrict__ pl,
-    float *__restrict__ out, int m, int n, int batch, int sb_per_split, size_t split_stride) {
-    constexpr int NH = Panel<T>::kChunks / 2;
-    __shared__ __align__(16) _Float16 xh[32 * kXRow];
-    __shared__ __align__(16) _Float16 xl[32 * kXRow];
-    const int t = threadIdx.x;
-    const int lane = t & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-    const int tiles = (m + kWave - 1) / kWave;
-    const int tile = blockIdx.x * kGemmWaves + wave;
-    const bool valid = tile < tiles;
-    const int nsb = n >> 8;
-    const int ks = blockIdx.y;
-    const int sb_begin = ks * sb_per_split;
-    const int sb_end = min(nsb, sb_begin + sb_per_split);
-    const uint8_t *tb = Wp + (size_t)(valid ? tile : 0) * nsb * Panel<T>::kBytes;
-    const int xi = lane & 31, xg = lane >> 5;  // A operand: batch row, column group
+// Persistent panel GEMM.  A workgroup has 4 * TPW waves and covers TPW
+// consecutive 64-row tiles: wave w works on tile w / 4 of the group and column
+// quarter q = w % 4 (blocks 2q, 2q + 1) of every panel, so the TPW waves of
+// one quarter load the same x fragments at the same time (cache hits after
+// the first).  Work items are (tile group, K split), item = group * ksplit +
+// split; workgroup g takes items g, g + G, g + 2G, ...  A tile's 4 quarter
+// sums are added through LDS.  The waves walk their (item, panel) units with
+// D units in flight in registers -- the loads of unit u + D are issued right
+// after unit u is multiplied, across item boundaries too -- so the main loop
+// has no barrier and no wait for the prefetched loads.  Output as
+// quant_gemm_tiled: out[split * split_stride + b * m + row], stored as
+// 16-byte row vectors (m % 4 == 0).
+constexpr int kBadOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
 
+template <uint32_t T, int TPW, int D>
+__global__ __launch_bounds__(kWave *kGemmWaves *TPW) __attribute__((amdgpu_waves_per_eu(2))) void gemm_packed(
+    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+    float *__restrict__ out, int m, int n, int batch, int ksplit, int per, size_t split_stride) {
+    __shared__ __align__(16) float red[TPW][kGemmWaves][32][kWave];
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave, groups = (tiles + TPW - 1) / TPW;
+    const int items = groups * ksplit, G = gridDim.x;
+    if ((int)blockIdx.x >= items) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int quarter = wave & 3, slot = wave >> 2;
+    const size_t xbase = (size_t)(4 * quarter * kWave + min(lane & 31, batch - 1) + 32 * (lane >> 5)) * 8;
+    const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
+    const __amdgpu_buffer_rsrc_t orsrc =
+        __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
+    // the wave's tile of a group (clamped: a group past the last tile re-reads
+    // the last tile, whose outputs are dropped)
+    auto tile_of = [&](int item) { return min((item / ksplit) * TPW + slot, tiles - 1); };
+
+    // compute cursor (ci, cp, ce) and load cursor (li, lp, le): item, panel, end panel
+    int ci = blockIdx.x, cp = (ci % ksplit) * per, ce = min(nsb, cp + per);
+    int li = ci, lp = cp, le = ce;
+    const uint8_t *lpanel = Wp + (size_t)tile_of(li) * tile_bytes + (size_t)lp * Panel<T>::kBytes;
+    size_t lxo = xbase + 16 * 512 * (size_t)lp;
+    // the load cursor steps to the next unit; every step issues its loads
+    auto load_next = [&](GemmUnit<T> &u) {
+        gemm_load<T>(u, lpanel, xh, xl, lxo, quarter, lane);
+        // branch-free cursor step (selects keep the loop body one basic block)
+        const bool wrap = ++lp == le;
+        const int ni = li + G;
+        const int np = (ni % ksplit) * per;
+        li = wrap ? ni : li;
+        lp = wrap ? np : lp;
+        le = wrap ? min(nsb, np + per) : le;
+        // past the last item the unit is a valid panel of the last group (lp
+        // always lies in a non-empty split), loaded and never used
+        lpanel = Wp + (size_t)tile_of(min(li, items - 1)) * tile_bytes + (size_t)lp * Panel<T>::kBytes;
+        lxo = xbase + 16 * 512 * (size_t)lp;
+    };
     f32x16 acc0 = {}, acc1 = {};
-    for (int sb = sb_begin; sb < sb_end; sb++) {
-        const uint8_t *pc = tb + (size_t)sb * Panel<T>::kBytes;
-        u32x4 q[NH];
-        load_half<T>(q, pc, Wp, 0, lane, valid);
-        const u32x4 sc = load_scales<T>(pc, Wp, lane, valid);
-        if (sb != sb_begin) __syncthreads();  // the previous panel's reads of the planes are done
-        stage_planes(ph, pl, xh, xl, n, batch, sb, t);
-        __syncthreads();
-        // block scales of row (l % 32) and (l % 32) + 32
-        uint32_t s0[4] = {sc.x, sc.y, sc.z, sc.w}, s1[4] = {sc.x, sc.y, sc.z, sc.w};
+    // multiplies unit u, refills it with the unit D ahead; at the end of an
+    // item reduces and stores it.  Past the workgroup's last item (ci >=
+    // items) a step is harmless: its loads are valid and its stores fall
+    // outside the output range and are dropped.
+    auto step = [&](GemmUnit<T> &u) {
+        gemm_mma<T>(u, quarter, acc0, acc1);
+        // the refill reuses u's registers only if it is issued after u's last
+        // use (the scale FMAs); otherwise the loop carries register copies
+        // that wait for the prefetched loads.  The empty asm pins the
+        // accumulation here.
+        asm volatile("" : "+v"(acc0), "+v"(acc1)::"memory");
+        load_next(u);
+        if (++cp < ce) return;
+        // item done: every wave parks its 32 sums per lane (accumulator
+        // element r of lane l: batch row 8 (r / 4 % 4) + 4 (l / 32) + r % 4,
+        // tile row l % 32 + 32 (r / 16)); then each thread adds the 4 quarters
+        // of two 4-row vectors of one batch row and stores them
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const auto p = __builtin_amdgcn_permlane32_swap(s0[i], s1[i], false, false);
-            s0[i] = p[0];
-            s1[i] = p[1];
+        for (int r = 0; r < 16; r++) {
+            red[slot][quarter][r][lane] = acc0[r];
+            red[slot][quarter][16 + r][lane] = acc1[r];
         }
-        if (valid) mfma_half<T>(q, s0, s1, xh, xl, 0, xi, xg, acc0, acc1);
-        load_half<T>(q, pc, Wp, 1, lane, valid);
-        if (valid) mfma_half<T>(q, s0, s1, xh, xl, 1, xi, xg, acc0, acc1);
-    }
-    if (!valid) return;
-    const int row0 = tile * kWave + xi, row1 = row0 + 32;
-    float *o = out + (size_t)ks * split_stride;
+        lds_barrier();
+        {
+            const int ks = ci % ksplit, tile = (ci / ksplit) * TPW + slot;
+            const int t = threadIdx.x & (kWave * kGemmWaves - 1);
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int b = 8 * (r >> 2) + 4 * xg + (r & 3);
-        if (b < batch) {
-            if (row0 < m) o[(size_t)b * m + row0] = acc0[r];
-            if (row1 < m) o[(size_t)b * m + row1] = acc1[r];
+            for (int i = 0; i < 2; i++) {
+                const int v = t + 256 * i;          // 512 vectors: batch row b, rows 4 j .. 4 j + 3
+                const int b = v >> 4, j = v & 15;
+                const int r = 4 * (b >> 3) + (b & 3) + (j >= 8 ? 16 : 0);
+                const int l = ((4 * j) & 31) + 32 * ((b >> 2) & 1);
+                float4 sum = *reinterpret_cast<const float4 *>(&red[slot][0][r][l]);
+#pragma unroll
+                for (int w = 1; w < kGemmWaves; w++) {
+                    const float4 o = *reinterpret_cast<const float4 *>(&red[slot][w][r][l]);
+                    sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
+                }
+                const int row = tile * kWave + 4 * j;
+                const int off = b < batch && row < m && tile < tiles && ci < items
+                                    ? 4 * (ks * (int)split_stride + b * m + row)
+                                    : kBadOffset;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0, 0);
+            }
         }
+        lds_barrier();  // red is free again
+        acc0 = f32x16{};
+        acc1 = f32x16{};
+        ci += G;
+        cp = (ci % ksplit) * per;
+        ce = min(nsb, cp + per);
+    };
+    // a ring of D units in registers (constant indices after unrolling)
+    GemmUnit<T> ring[D];
+#pragma unroll
+    for (int k = 0; k < D; k++) load_next(ring[k]);
+    // one exit, after the last step of the ring: an exit between steps would
+    // give the back edge a path that skips a refill (the compiler merges exit
+    // tests into the latch) and make the load waits conservative
+    do {
+#pragma unroll
+        for (int k = 0; k < D; k++) step(ring[k]);
+    } while (ci < items);
+}
+
+// fp32 x[batch][n] -> fragment-order fp16 planes hi, lo (hi + lo ~= x), one
+// thread per 8 consecutive columns of a row (one 16-byte fragment).
+__global__ __launch_bounds__(256) void split_x_frag_kernel(const float *__restrict__ x, _Float16 *__restrict__ hi,
+                                                          _Float16 *__restrict__ lo, int batch, int n) {
+    const int g = blockIdx.x * 256 + threadIdx.x, per_row = n >> 3;
+    if (g >= batch * per_row) return;
+    const int b = g / per_row, c = 8 * (g % per_row);
+    const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)b * n + c);
+    const float4 v0 = src[0], v1 = src[1];
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    h8v h, l;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        h[e] = (_Float16)v[e];
+        l[e] = (_Float16)(v[e] - (float)h[e]);
     }
+    *reinterpret_cast<h8v *>(hi + xf_index(b, c)) = h;
+    *reinterpret_cast<h8v *>(lo + xf_index(b, c)) = l;
 }
 
 // ---------------------------------------------------------------------------
@@ -1226,34 +1304,56 @@ int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, bool norm_
     return packed_ksplit(tiles, (int)(n / 256), norm_prologue ? cus / 2 : cus);
 }
 
-// K splits of the panel MFMA GEMM: the fewest that give half the CUs a
-// workgroup (at most kMaxSplit, no empty split).
+// K splits of the panel MFMA GEMM: the fewest that give two 1-tile work
+// items per CU (at most kMaxSplit, no empty split); matrices with 2-tile
+// workgroups (at least 4 tiles per CU) need none.
 int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
-    const int groups = (int)((m + kWave * kGemmWaves - 1) / (kWave * kGemmWaves));
+    const int tiles = (int)((m + kWave - 1) / kWave);
     const int nsb = (int)(n / 256), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     int best = 1;
     for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
         const int per = (nsb + k - 1) / k;
         if ((k - 1) * per >= nsb) continue;
         best = k;
-        if (2 * groups * k >= cus) return k;
+        if (tiles * k >= 2 * cus) return k;
     }
     return best;
 }
 
+// Persistent grid.  Matrices with many row tiles (lm_head) take 2-tile
+// workgroups of 8 waves, one per CU (half the x traffic); the others 1-tile
+// workgroups of 4 waves, two per CU (twice the items, for parallelism).
+template <uint32_t T>
+int launch_gemm_packed_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
+                         const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit, int per) {
+    const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const size_t ss = (size_t)batch * m;
+    if (tiles >= 4 * cus) {
+        const int items = (tiles + 1) / 2 * ksplit;
+        hipLaunchKernelGGL((gemm_packed<T, 2, kGemmRing>), dim3(min(items, cus)), dim3(2 * kWave * kGemmWaves), 0,
+                           stream, w, xh, xl, out, (int)m, (int)n, (int)batch, ksplit, per, ss);
+    } else {
+        const int items = tiles * ksplit;
+        hipLaunchKernelGGL((gemm_packed<T, 1, kGemmRing>), dim3(min(items, 2 * cus)), dim3(kWave * kGemmWaves), 0,
+                           stream, w, xh, xl, out, (int)m, (int)n, (int)batch, ksplit, per, ss);
+    }
+    return ANEHIP_OK;
+}
+
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                        uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit) {
-    const int groups = (int)((m + kWave * kGemmWaves - 1) / (kWave * kGemmWaves));
     const int per = split_len((int)(n / 256), ksplit);
-    const dim3 grid(groups, ksplit), block(kWave * kGemmWaves);
+    if (ksplit < 1 || (ksplit - 1) * per >= (int)(n / 256) || batch < 1 || batch > 32 || m % 4)
+        return set_error(ctx->err, ANEHIP_EINVAL,
+                         "gemm: K split %d of %u super-blocks, batch %u or m %u (multiple of 4) unsupported", ksplit,
+                         n / 256, batch, m);
+    if (4.0 * ksplit * batch * m > 1073741824.0)  // output byte offsets stay below kBadOffset
+        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
-    const size_t ss = (size_t)batch * m;
     if (ggml_type == ANEHIP_GGML_Q8_0)
-        hipLaunchKernelGGL(gemm_packed<ANEHIP_GGML_Q8_0>, grid, block, 0, stream, w, xh, xl, out, (int)m, (int)n,
-                           (int)batch, per, ss);
+        launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
     else
-        hipLaunchKernelGGL(gemm_packed<ANEHIP_GGML_Q4_0>, grid, block, 0, stream, w, xh, xl, out, (int)m, (int)n,
-                           (int)batch, per, ss);
+        launch_gemm_packed_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
@@ -1343,8 +1443,11 @@ int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     return dispatch_packed<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, in, out, ksplit);
 }
 
-int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, size_t count, _Float16 *xh, _Float16 *xl) {
-    hipLaunchKernelGGL(split_x_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, x, xh, xl, count);
+int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t batch, uint32_t n, _Float16 *xh,
+                   _Float16 *xl) {
+    const size_t vecs = (size_t)batch * (n / 8);
+    hipLaunchKernelGGL(split_x_frag_kernel, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0, stream, x, xh, xl,
+                       (int)batch, (int)n);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

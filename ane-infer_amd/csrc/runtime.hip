@@ -223,13 +223,16 @@ int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
         return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: batch=%u outside 1..32", batch);
     if (batch == 1) return anehip_quant_gemv_packed(ctx, ggml_type, wp, m, n, x, y);
     const int ksplit = gemm_packed_ksplit(ctx, m, n);
-    const size_t count = (size_t)batch * m, xcount = (size_t)batch * n;
+    if (m % 4)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: m=%u must be a multiple of 4 for batch > 1",
+                         m);
+    const size_t count = (size_t)batch * m, xcount = xf_plane_len(n);
     // workspace: [x hi plane][x lo plane] (fp16, xcount each) then the partials
-    const size_t planes = xcount;  // floats holding both planes (xcount is a multiple of 256)
+    const size_t planes = xcount;  // floats holding both planes
     int rc = ensure_workspace(ctx, planes + (ksplit > 1 ? (size_t)ksplit * count : 0));
     if (rc) return rc;
     _Float16 *xh = reinterpret_cast<_Float16 *>(ctx->ws.partial), *xl = xh + xcount;
-    if ((rc = launch_split_x(ctx, ctx->stream, x, xcount, xh, xl))) return rc;
+    if ((rc = launch_split_x(ctx, ctx->stream, x, batch, n, xh, xl))) return rc;
     if (ksplit == 1) return launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xh, xl, batch, y, 1);
     float *part = ctx->ws.partial + planes;
     if ((rc = launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xh, xl, batch, part, ksplit))) return rc;
