@@ -743,6 +743,10 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     if (!M) return rc;
     if (batch == 0 || batch > 32) return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "alloc_state: batch %u outside 1..32", batch);
     if (max_seq == 0) return set_error(ctx->err, ANEHIP_EINVAL, "alloc_state: max_seq is 0");
+    // batch > 1 runs the projections on the panel MFMA GEMM (16-byte output stores)
+    if (batch > 1 && M->desc.vocab_size % 4)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "alloc_state: batch > 1 needs vocab_size %% 4 == 0 (got %u)",
+                         M->desc.vocab_size);
     ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
     free_state(M);
     const anehip_model_desc &D = M->desc;

@@ -792,30 +792,36 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// One wave's operands for one panel of its tile: the quant vectors of its
-// column quarter q (blocks 2q, 2q + 1: Q8_0 chunks 4q..4q+3, Q4_0 chunks
-// 2q, 2q+1), the lane row's 16-byte scale vector, and the A fragments of x for
-// the quarter's 4 column steps (hi and lo planes, fragment order).
-template <uint32_t T> struct GemmUnit {
+// One wave's operands for one panel of its TV tiles: per tile the quant
+// vectors of its column quarter q (blocks 2q, 2q + 1: Q8_0 chunks 4q..4q+3,
+// Q4_0 chunks 2q, 2q+1) and the lane row's 16-byte scale vector; and the A
+// fragments of x for the quarter's 4 column steps (hi and lo planes, fragment
+// order), shared by the TV tiles.
+template <uint32_t T, int TV> struct GemmUnit {
     static constexpr int kQ = T == ANEHIP_GGML_Q8_0 ? 4 : 2;
-    u32x4 q[kQ];
-    u32x4 sc;
+    u32x4 q[TV][kQ];
+    u32x4 sc[TV];
     h8v ah[4], al[4];
 };
 
 // Loads one unit: every lane issues the same, fully contiguous 1 KiB loads
-// (no lane masking, so the compiler's vmcnt waits stay exact).  `xo` is the
-// lane's element offset of its first A fragment in the fragment-order planes
-// (rows past the batch are redirected to row batch - 1: those lanes only feed
-// MFMA output rows that are never stored, and their loads hit the cache).
-template <uint32_t T>
-__device__ __forceinline__ void gemm_load(GemmUnit<T> &u, const uint8_t *panel, const _Float16 *__restrict__ xh,
-                                          const _Float16 *__restrict__ xl, size_t xo, int quarter, int lane) {
-    constexpr int Q = GemmUnit<T>::kQ;
-    const u32x4 *p4 = reinterpret_cast<const u32x4 *>(panel);
+// (no lane masking, so the compiler's vmcnt waits stay exact).  `panel` is the
+// first tile's panel, the others follow at `tile_bytes`.  `xo` is the lane's
+// element offset of its first A fragment in the fragment-order planes (rows
+// past the batch are redirected to row batch - 1: those lanes only feed MFMA
+// output rows that are never stored, and their loads hit the cache).
+template <uint32_t T, int TV>
+__device__ __forceinline__ void gemm_load(GemmUnit<T, TV> &u, const uint8_t *panel, size_t tile_bytes,
+                                          const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl, size_t xo,
+                                          int quarter, int lane) {
+    constexpr int Q = GemmUnit<T, TV>::kQ;
 #pragma unroll
-    for (int c = 0; c < Q; c++) u.q[c] = __builtin_nontemporal_load(p4 + (Q * quarter + c) * kWave + lane);
-    u.sc = __builtin_nontemporal_load(p4 + Panel<T>::kChunks * kWave + lane);
+    for (int t = 0; t < TV; t++) {
+        const u32x4 *p4 = reinterpret_cast<const u32x4 *>(panel + t * tile_bytes);
+#pragma unroll
+        for (int c = 0; c < Q; c++) u.q[t][c] = __builtin_nontemporal_load(p4 + (Q * quarter + c) * kWave + lane);
+        u.sc[t] = __builtin_nontemporal_load(p4 + Panel<T>::kChunks * kWave + lane);
+    }
 #pragma unroll
     for (int s = 0; s < 4; s++) {
         u.ah[s] = *reinterpret_cast<const h8v *>(xh + xo + 512 * s);
@@ -823,57 +829,61 @@ __device__ __forceinline__ void gemm_load(GemmUnit<T> &u, const uint8_t *panel, 
     }
 }
 
-// acc{0,1} += the unit's two blocks: per block C = sum over its 2 column steps
-// and the 2 planes (4 MFMAs per 32 weight rows), then acc += C * d
-// (q8_gemv.rs:234-242 order within a block up to fp32 summation).
-template <uint32_t T>
-__device__ __forceinline__ void gemm_mma(const GemmUnit<T> &u, int quarter, f32x16 &acc0, f32x16 &acc1) {
-    // dword `quarter` of the scale vector holds blocks 2q, 2q + 1; after the
-    // swap s0 / s1 are those of weight rows l % 32 (acc0) and 32 + l % 32 (acc1)
-    const uint32_t sw = quarter == 0 ? u.sc.x : quarter == 1 ? u.sc.y : quarter == 2 ? u.sc.z : u.sc.w;
-    const auto sp = __builtin_amdgcn_permlane32_swap(sw, sw, false, false);
-    const uint32_t s0 = sp[0], s1 = sp[1];
+// acc[t]{0,1} += the unit's two blocks of tile t: per block C = sum over its 2
+// column steps and the 2 planes (4 MFMAs per 32 weight rows), then
+// acc += C * d (q8_gemv.rs:234-242 order within a block up to fp32 summation).
+template <uint32_t T, int TV>
+__device__ __forceinline__ void gemm_mma(const GemmUnit<T, TV> &u, int quarter, f32x16 (&acc)[TV][2]) {
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        f32x16 c0 = {}, c1 = {};
+    for (int t = 0; t < TV; t++) {
+        // dword `quarter` of the scale vector holds blocks 2q, 2q + 1; after
+        // the swap s0 / s1 are those of weight rows l % 32 and 32 + l % 32
+        const u32x4 sv = u.sc[t];
+        const uint32_t sw = quarter == 0 ? sv.x : quarter == 1 ? sv.y : quarter == 2 ? sv.z : sv.w;
+        const auto sp = __builtin_amdgcn_permlane32_swap(sw, sw, false, false);
+        const uint32_t s0 = sp[0], s1 = sp[1];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int s = 2 * j + h;  // column step: columns 16 s .. 16 s + 15 of the quarter
-            h8v b0, b1;
-            if constexpr (T == ANEHIP_GGML_Q8_0) {
-                const u32x4 v = u.q[s];
-                uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
-                swap_halves(a0, a1, c0w, c1w);
-                b0 = dwords_to_h8_i8(a0, a1);
-                b1 = dwords_to_h8_i8(c0w, c1w);
-            } else {
-                const u32x4 v = u.q[j];
-                uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
-                swap_halves(a0, a1, c0w, c1w);
-                const uint32_t sh = 4 * h;  // step 0: low nibbles, step 1: high nibbles
-                b0 = dwords_to_h8_u4((a0 >> sh) & 0x0F0F0F0Fu, (a1 >> sh) & 0x0F0F0F0Fu);
-                b1 = dwords_to_h8_u4((c0w >> sh) & 0x0F0F0F0Fu, (c1w >> sh) & 0x0F0F0F0Fu);
+        for (int j = 0; j < 2; j++) {
+            f32x16 c0 = {}, c1 = {};
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int s = 2 * j + h;  // column step: columns 16 s .. 16 s + 15 of the quarter
+                h8v b0, b1;
+                if constexpr (T == ANEHIP_GGML_Q8_0) {
+                    const u32x4 v = u.q[t][s];
+                    uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
+                    swap_halves(a0, a1, c0w, c1w);
+                    b0 = dwords_to_h8_i8(a0, a1);
+                    b1 = dwords_to_h8_i8(c0w, c1w);
+                } else {
+                    const u32x4 v = u.q[t][j];
+                    uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
+                    swap_halves(a0, a1, c0w, c1w);
+                    const uint32_t sh = 4 * h;  // step 0: low nibbles, step 1: high nibbles
+                    b0 = dwords_to_h8_u4((a0 >> sh) & 0x0F0F0F0Fu, (a1 >> sh) & 0x0F0F0F0Fu);
+                    b1 = dwords_to_h8_u4((c0w >> sh) & 0x0F0F0F0Fu, (c1w >> sh) & 0x0F0F0F0Fu);
+                }
+                c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.ah[s], b0, c0, 0, 0, 0);
+                c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.al[s], b0, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.ah[s], b1, c1, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.al[s], b1, c1, 0, 0, 0);
             }
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.ah[s], b0, c0, 0, 0, 0);
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.al[s], b0, c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.ah[s], b1, c1, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.al[s], b1, c1, 0, 0, 0);
-        }
-        const float d0 = __half2float(__ushort_as_half((unsigned short)(s0 >> (16 * j))));
-        const float d1 = __half2float(__ushort_as_half((unsigned short)(s1 >> (16 * j))));
+            const float d0 = __half2float(__ushort_as_half((unsigned short)(s0 >> (16 * j))));
+            const float d1 = __half2float(__ushort_as_half((unsigned short)(s1 >> (16 * j))));
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            acc0[r] = fmaf(c0[r], d0, acc0[r]);
-            acc1[r] = fmaf(c1[r], d1, acc1[r]);
+            for (int r = 0; r < 16; r++) {
+                acc[t][0][r] = fmaf(c0[r], d0, acc[t][0][r]);
+                acc[t][1][r] = fmaf(c1[r], d1, acc[t][1][r]);
+            }
         }
     }
 }
 
-// Persistent panel GEMM.  A workgroup has 4 * TPW waves and covers TPW
-// consecutive 64-row tiles: wave w works on tile w / 4 of the group and column
-// quarter q = w % 4 (blocks 2q, 2q + 1) of every panel, so the TPW waves of
-// one quarter load the same x fragments at the same time (cache hits after
-// the first).  Work items are (tile group, K split), item = group * ksplit +
+// Persistent panel GEMM.  A workgroup has 4 waves, one per column quarter q
+// (blocks 2q, 2q + 1 of every panel), and covers TV consecutive 64-row tiles:
+// each wave multiplies the x fragments it loads with all TV tiles' weights
+// (TV = 2 halves the x loads per weight byte, at one wave per SIMD for the
+// registers).  Work items are (tile group, K split), item = group * ksplit +
 // split; workgroup g takes items g, g + G, g + 2G, ...  A tile's 4 quarter
 // sums are added through LDS.  The waves walk their (item, panel) units with
 // D units in flight in registers -- the loads of unit u + D are issued right
@@ -883,33 +893,32 @@ __device__ __forceinline__ void gemm_mma(const GemmUnit<T> &u, int quarter, f32x
 // 16-byte row vectors (m % 4 == 0).
 constexpr int kBadOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
 
-template <uint32_t T, int TPW, int D>
-__global__ __launch_bounds__(kWave *kGemmWaves *TPW) __attribute__((amdgpu_waves_per_eu(2))) void gemm_packed(
+template <uint32_t T, int TV, int D>
+__global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(TV == 1 ? 2 : 1))) void gemm_packed(
     const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
     float *__restrict__ out, int m, int n, int batch, int ksplit, int per, size_t split_stride) {
-    __shared__ __align__(16) float red[TPW][kGemmWaves][32][kWave];
-    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave, groups = (tiles + TPW - 1) / TPW;
+    __shared__ __align__(16) float red[kGemmWaves][TV * 32][kWave];
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave, groups = (tiles + TV - 1) / TV;
     const int items = groups * ksplit, G = gridDim.x;
     if ((int)blockIdx.x >= items) return;
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int quarter = wave & 3, slot = wave >> 2;
+    const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const size_t xbase = (size_t)(4 * quarter * kWave + min(lane & 31, batch - 1) + 32 * (lane >> 5)) * 8;
     const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
     const __amdgpu_buffer_rsrc_t orsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
-    // the wave's tile of a group (clamped: a group past the last tile re-reads
-    // the last tile, whose outputs are dropped)
-    auto tile_of = [&](int item) { return min((item / ksplit) * TPW + slot, tiles - 1); };
+    // first tile of an item's group (clamped so that all TV tiles' loads stay
+    // inside the matrix; outputs of tiles past the last are dropped)
+    auto first_tile = [&](int item) { return min((item / ksplit) * TV, tiles - TV); };
 
     // compute cursor (ci, cp, ce) and load cursor (li, lp, le): item, panel, end panel
     int ci = blockIdx.x, cp = (ci % ksplit) * per, ce = min(nsb, cp + per);
     int li = ci, lp = cp, le = ce;
-    const uint8_t *lpanel = Wp + (size_t)tile_of(li) * tile_bytes + (size_t)lp * Panel<T>::kBytes;
+    const uint8_t *lpanel = Wp + (size_t)first_tile(li) * tile_bytes + (size_t)lp * Panel<T>::kBytes;
     size_t lxo = xbase + 16 * 512 * (size_t)lp;
     // the load cursor steps to the next unit; every step issues its loads
-    auto load_next = [&](GemmUnit<T> &u) {
-        gemm_load<T>(u, lpanel, xh, xl, lxo, quarter, lane);
+    auto load_next = [&](GemmUnit<T, TV> &u) {
+        gemm_load<T, TV>(u, lpanel, tile_bytes, xh, xl, lxo, quarter, lane);
         // branch-free cursor step (selects keep the loop body one basic block)
         const bool wrap = ++lp == le;
         const int ni = li + G;
@@ -919,64 +928,71 @@ __global__ __launch_bounds__(kWave *kGemmWaves *TPW) __attribute__((amdgpu_waves
         le = wrap ? min(nsb, np + per) : le;
         // past the last item the unit is a valid panel of the last group (lp
         // always lies in a non-empty split), loaded and never used
-        lpanel = Wp + (size_t)tile_of(min(li, items - 1)) * tile_bytes + (size_t)lp * Panel<T>::kBytes;
+        lpanel = Wp + (size_t)first_tile(min(li, items - 1)) * tile_bytes + (size_t)lp * Panel<T>::kBytes;
         lxo = xbase + 16 * 512 * (size_t)lp;
     };
-    f32x16 acc0 = {}, acc1 = {};
+    f32x16 acc[TV][2];
+#pragma unroll
+    for (int t = 0; t < TV; t++) acc[t][0] = acc[t][1] = f32x16{};
     // multiplies unit u, refills it with the unit D ahead; at the end of an
     // item reduces and stores it.  Past the workgroup's last item (ci >=
     // items) a step is harmless: its loads are valid and its stores fall
     // outside the output range and are dropped.
-    auto step = [&](GemmUnit<T> &u) {
-        gemm_mma<T>(u, quarter, acc0, acc1);
+    auto step = [&](GemmUnit<T, TV> &u) {
+        gemm_mma<T, TV>(u, quarter, acc);
         // the refill reuses u's registers only if it is issued after u's last
         // use (the scale FMAs); otherwise the loop carries register copies
         // that wait for the prefetched loads.  The empty asm pins the
         // accumulation here.
-        asm volatile("" : "+v"(acc0), "+v"(acc1)::"memory");
+#pragma unroll
+        for (int t = 0; t < TV; t++) asm volatile("" : "+v"(acc[t][0]), "+v"(acc[t][1])::"memory");
         load_next(u);
         if (++cp < ce) return;
-        // item done: every wave parks its 32 sums per lane (accumulator
-        // element r of lane l: batch row 8 (r / 4 % 4) + 4 (l / 32) + r % 4,
-        // tile row l % 32 + 32 (r / 16)); then each thread adds the 4 quarters
-        // of two 4-row vectors of one batch row and stores them
+        // item done: every wave parks its 32 sums per lane and tile
+        // (accumulator element r of lane l: batch row 8 (r / 4 % 4) +
+        // 4 (l / 32) + r % 4, tile row l % 32 + 32 (r / 16)); then each thread
+        // adds the 4 quarters of 4-row vectors of one batch row and stores them
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            red[slot][quarter][r][lane] = acc0[r];
-            red[slot][quarter][16 + r][lane] = acc1[r];
-        }
+        for (int t = 0; t < TV; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                red[quarter][32 * t + r][lane] = acc[t][0][r];
+                red[quarter][32 * t + 16 + r][lane] = acc[t][1][r];
+            }
         lds_barrier();
         {
-            const int ks = ci % ksplit, tile = (ci / ksplit) * TPW + slot;
-            const int t = threadIdx.x & (kWave * kGemmWaves - 1);
+            const int ks = ci % ksplit, tile0 = (ci / ksplit) * TV, ft = first_tile(ci);
+            const int th = threadIdx.x;
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int v = t + 256 * i;          // 512 vectors: batch row b, rows 4 j .. 4 j + 3
-                const int b = v >> 4, j = v & 15;
-                const int r = 4 * (b >> 3) + (b & 3) + (j >= 8 ? 16 : 0);
+            for (int i = 0; i < 2 * TV; i++) {
+                const int v = th + 256 * i;  // 512 vectors per tile: batch row b, rows 4 j .. 4 j + 3
+                const int t = v >> 9, b = (v >> 4) & 31, j = v & 15;
+                const int r = 32 * t + 4 * (b >> 3) + (b & 3) + (j >= 8 ? 16 : 0);
                 const int l = ((4 * j) & 31) + 32 * ((b >> 2) & 1);
-                float4 sum = *reinterpret_cast<const float4 *>(&red[slot][0][r][l]);
+                float4 sum = *reinterpret_cast<const float4 *>(&red[0][r][l]);
 #pragma unroll
                 for (int w = 1; w < kGemmWaves; w++) {
-                    const float4 o = *reinterpret_cast<const float4 *>(&red[slot][w][r][l]);
+                    const float4 o = *reinterpret_cast<const float4 *>(&red[w][r][l]);
                     sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
                 }
-                const int row = tile * kWave + 4 * j;
-                const int off = b < batch && row < m && tile < tiles && ci < items
+                // the group's tile t is tile ft + t of the loads; it is stored
+                // only if it is the item's own tile (not a clamped re-read)
+                const int tile = ft + t, row = tile * kWave + 4 * j;
+                const int off = b < batch && tile >= tile0 && row < m && ci < items
                                     ? 4 * (ks * (int)split_stride + b * m + row)
                                     : kBadOffset;
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0, 0);
             }
         }
         lds_barrier();  // red is free again
-        acc0 = f32x16{};
-        acc1 = f32x16{};
+#pragma unroll
+        for (int t = 0; t < TV; t++) acc[t][0] = acc[t][1] = f32x16{};
         ci += G;
         cp = (ci % ksplit) * per;
         ce = min(nsb, cp + per);
     };
     // a ring of D units in registers (constant indices after unrolling)
-    GemmUnit<T> ring[D];
+    GemmUnit<T, TV> ring[D];
 #pragma unroll
     for (int k = 0; k < D; k++) load_next(ring[k]);
     // one exit, after the last step of the ring: an exit between steps would
@@ -1304,39 +1320,42 @@ int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, bool norm_
     return packed_ksplit(tiles, (int)(n / 256), norm_prologue ? cus / 2 : cus);
 }
 
-// K splits of the panel MFMA GEMM: the fewest that give two 1-tile work
-// items per CU (at most kMaxSplit, no empty split); matrices with 2-tile
-// workgroups (at least 4 tiles per CU) need none.
+// K splits of the panel MFMA GEMM: among the even splits of the panels (at
+// most kMaxSplit), the one that minimises the panels of the busiest CU,
+// ceil(items / CUs) x panels per split, with single-panel splits counted
+// double (each unit then pays a whole item's reduction) and ties going to
+// fewer splits; no split for matrices of at least 4 tiles per CU (their
+// partial sums would cost more than the balance gains).  Measured on MI355X
+// at batch 4 and 32 this picks the fastest split of every decode shape
+// (e.g. 12288 x 2048: k = 4, 11.6 us; uneven k = 3: 15.5 us).
 int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
     const int tiles = (int)((m + kWave - 1) / kWave);
     const int nsb = (int)(n / 256), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    if (tiles >= 4 * cus) return 1;
     int best = 1;
+    double best_cost = 1e30;
     for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
-        const int per = (nsb + k - 1) / k;
-        if ((k - 1) * per >= nsb) continue;
-        best = k;
-        if (tiles * k >= 2 * cus) return k;
+        if (nsb % k) continue;
+        const int per = nsb / k;
+        const double cost = (double)((tiles * k + cus - 1) / cus) * per * (per == 1 ? 2.0 : 1.0);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = k;
+        }
     }
     return best;
 }
 
-// Persistent grid.  Matrices with many row tiles (lm_head) take 2-tile
-// workgroups of 8 waves, one per CU (half the x traffic); the others 1-tile
-// workgroups of 4 waves, two per CU (twice the items, for parallelism).
+// Persistent grid of 1-tile workgroups, two per CU.  (Two tiles per wave, at
+// one wave per SIMD, halves the x loads but measured no faster: 84 vs 90 us
+// on lm_head at batch 32, slower at batch 4 and 16 and on the small shapes.)
 template <uint32_t T>
 int launch_gemm_packed_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
                          const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit, int per) {
     const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const size_t ss = (size_t)batch * m;
-    if (tiles >= 4 * cus) {
-        const int items = (tiles + 1) / 2 * ksplit;
-        hipLaunchKernelGGL((gemm_packed<T, 2, kGemmRing>), dim3(min(items, cus)), dim3(2 * kWave * kGemmWaves), 0,
-                           stream, w, xh, xl, out, (int)m, (int)n, (int)batch, ksplit, per, ss);
-    } else {
-        const int items = tiles * ksplit;
-        hipLaunchKernelGGL((gemm_packed<T, 1, kGemmRing>), dim3(min(items, 2 * cus)), dim3(kWave * kGemmWaves), 0,
-                           stream, w, xh, xl, out, (int)m, (int)n, (int)batch, ksplit, per, ss);
-    }
+    const int items = tiles * ksplit;
+    hipLaunchKernelGGL((gemm_packed<T, 1, kGemmRing>), dim3(min(items, 2 * cus)), dim3(kWave * kGemmWaves), 0, stream,
+                       w, xh, xl, out, (int)m, (int)n, (int)batch, ksplit, per, (size_t)batch * m);
     return ANEHIP_OK;
 }
 

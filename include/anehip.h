@@ -199,7 +199,8 @@ int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
 /* anehip_quant_gemm_packed: y[b][r] = W[r] . x[b] for b < batch (1..32), from
  * the panel copy wp; x [batch][n] fp32.  batch 1 is
  * anehip_quant_gemv_packed; batch > 1 runs on MFMA (the small-batch form of
- * anehip_quant_gemm, same tolerance). */
+ * anehip_quant_gemm, same tolerance) and needs m % 4 == 0 (ANEHIP_EUNSUPPORTED
+ * otherwise). */
 int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
                              const float *x, uint32_t batch, float *y);
 
@@ -290,7 +291,8 @@ int anehip_tensor_ptr(anehip_ctx *ctx, int32_t layer, uint32_t kind, uint32_t gg
 /* Allocates zeroed per-sequence state for `batch` (1..32) sequences with KV
  * capacity max_seq, all positions 0: HybridCache::new (deltanet_cache.rs:
  * 76-136) and the state buffers of upload_model_weights (gpu_decode.rs:
- * 205-256).  Frees any previous state. */
+ * 205-256).  Frees any previous state.  batch > 1 needs vocab_size % 4 == 0
+ * (ANEHIP_EUNSUPPORTED otherwise). */
 int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq);
 
 /* Zeroes all state and sets every position to 0. */

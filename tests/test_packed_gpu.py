@@ -99,6 +99,10 @@ def test_packed_rejects_bad_shapes(gpu_ctx, anehip_mod):
     with pytest.raises(anehip_mod.AnehipError) as e:
         gpu_ctx.call("quant_gemv_packed", 14, d, 64, 256, d, d)
     assert e.value.code == -3
+    # batch > 1 needs m % 4 == 0 (16-byte output stores)
+    with pytest.raises(anehip_mod.AnehipError) as e:
+        gpu_ctx.call("quant_gemm_packed", 8, d, 62, 256, d, 2, d)
+    assert e.value.code == -3
     d.free()
 
 
@@ -107,8 +111,8 @@ def test_packed_rejects_bad_shapes(gpu_ctx, anehip_mod):
 @pytest.mark.parametrize("batch", [2, 3, 4, 7, 16, 17, 32])
 @pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144), (100, 256), (8224, 2048), (12288, 1792)])
 def test_packed_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
-    """Panel MFMA GEMM, ragged batch (not padded to the 32-row MFMA tile).
-    12288 x 1792 (7 panels per row tile) is split 3 + 3 + 1 panels over K."""
+    """Panel MFMA GEMM, ragged batch (not padded to the 32-row MFMA tile), at
+    the decode shapes, a tiny matrix and an odd panel count (12288 x 1792)."""
     w = oracle_lib.gen_quant(t, 99, m + 5 * n + t, m, n, std=0.02)
     x = oracle_lib.normal(99, 300 + batch, batch * n).reshape(batch, n)
     dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
