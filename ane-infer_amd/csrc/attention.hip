@@ -178,19 +178,24 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         // scores: wave = query head of the group, lane = position in the tile
         if (wave < G) {
             const int p = row0 + lane;
-            float dot = 0.0f;
+            // 8 independent partial sums (dims d % 8), added pairwise at the end
+            float dp[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
             const __half *krow = &tile[lane * kRowH];
 #pragma unroll 4
             for (int d = 0; d < kHd; d += 8) {
                 u32x4 kv8 = *reinterpret_cast<const u32x4 *>(krow + d);
+                const float4 qa = *reinterpret_cast<const float4 *>(&qs[wave][d]);
+                const float4 qb = *reinterpret_cast<const float4 *>(&qs[wave][d + 4]);
+                const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
                 const __half2 *h2 = reinterpret_cast<const __half2 *>(&kv8);
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float2 kf = __half22float2(h2[e]);
-                    dot += qs[wave][d + 2 * e] * kf.x;
-                    dot += qs[wave][d + 2 * e + 1] * kf.y;
+                    dp[2 * e] += qv[2 * e] * kf.x;
+                    dp[2 * e + 1] += qv[2 * e + 1] * kf.y;
                 }
             }
+            const float dot = ((dp[0] + dp[1]) + (dp[2] + dp[3])) + ((dp[4] + dp[5]) + (dp[6] + dp[7]));
             const float sc = p < len ? dot / sdiv : -INFINITY;
             const float mn = fmaxf(m_run, wave_max(sc));  // finite: the tile has a valid row
             const float scale = expf(m_run - mn);         // 0 on the first tile
@@ -208,16 +213,29 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         lds_barrier();
         // PV: wave = query head, lane = 4 consecutive dims
         if (wave < G) {
-            const int nvalid = min(kCh, len - row0);
-            for (int p = 0; p < nvalid; p++) {
-                const float pr = probs[wave][p];
-                const __half2 *v2 = reinterpret_cast<const __half2 *>(&tile[p * kRowH + 4 * lane]);
-                float2 a = __half22float2(v2[0]), bb = __half22float2(v2[1]);
-                o0 += pr * a.x;
-                o1 += pr * a.y;
-                o2 += pr * bb.x;
-                o3 += pr * bb.y;
+            // rows past the sequence have zero probability (and zero V), so
+            // all 64 rows are summed: two independent chains, even / odd rows
+            float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
+#pragma unroll 8
+            for (int p = 0; p < kCh; p += 2) {
+                const float2 pr = *reinterpret_cast<const float2 *>(&probs[wave][p]);
+                const __half2 *va2 = reinterpret_cast<const __half2 *>(&tile[p * kRowH + 4 * lane]);
+                const __half2 *vb2 = reinterpret_cast<const __half2 *>(&tile[(p + 1) * kRowH + 4 * lane]);
+                const float2 a = __half22float2(va2[0]), bb = __half22float2(va2[1]);
+                const float2 c = __half22float2(vb2[0]), dd = __half22float2(vb2[1]);
+                o0 += pr.x * a.x;
+                o1 += pr.x * a.y;
+                o2 += pr.x * bb.x;
+                o3 += pr.x * bb.y;
+                e0 += pr.y * c.x;
+                e1 += pr.y * c.y;
+                e2 += pr.y * dd.x;
+                e3 += pr.y * dd.y;
             }
+            o0 += e0;
+            o1 += e1;
+            o2 += e2;
+            o3 += e3;
         }
         lds_barrier();  // the tile is rewritten by the next K
     };
