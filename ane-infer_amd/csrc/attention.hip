@@ -8,7 +8,7 @@
 //
 // Split-K ("flash-decoding"): the positions 0..pos of one sequence are cut
 // into tiles of 64 and chunks of tiles_per_chunk() tiles (at most 128 chunks
-// at the cache's capacity); one workgroup per (chunk, kv head, sequence)
+// and ~2048 workgroups at the cache's capacity); one workgroup per (chunk, kv head, sequence)
 // streams its tiles' K and V rows once for all G query heads that share the
 // kv head (the next tile's loads in flight while the current one is used),
 // with an online softmax, and writes an unnormalised partial output with its
@@ -32,7 +32,6 @@ namespace {
 constexpr int kHd = 256;       // head_dim
 constexpr int kCh = 64;        // positions per workgroup
 constexpr int kThreads = 256;
-constexpr int kRowH = kHd + 8; // LDS row stride in halfs (pad: conflict-free 16-byte reads)
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -75,43 +74,63 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kPer = (kCh * kHd / 8) / kThreads;  // 16-byte vectors of a 64-row tile per thread
-constexpr int kWord3 = 0x00020000;               // raw buffer resource word 3 (gfx9 family)
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kWord3 = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 
-// K and V rows of one 64-position tile into registers: vector q = i * 256 + t
-// is row q / 32, 16-byte part q % 32.  The buffer resources cover positions
-// [0, pos) of this sequence and kv head only, so rows >= pos (the current
-// row, whose k / v come from this step, and rows past it) read zeros
-// without a memory access and without a branch.
-__device__ __forceinline__ void load_kv_tile(u32x4 *kr, u32x4 *vr, __amdgpu_buffer_rsrc_t krs,
-                                             __amdgpu_buffer_rsrc_t vrs, int row0, int t) {
+// LDS row of V^T (one head dim, 64 positions = 8 chunks of 8): chunk c of
+// row D sits at slot c ^ swz(D), which keeps both the transposing writes (8
+// lanes: rows 8p + d, p varying) and the MFMA operand reads (8 lanes: 8
+// consecutive rows) free of bank conflicts.
+__device__ __forceinline__ int vt_slot(int D, int c) { return c ^ ((D ^ (D >> 3)) & 7); }
+
+// fp32 x 8 -> fp16 hi / lo with hi + lo ~= x (|error| <= 2^-22 |x|)
+__device__ __forceinline__ void split8(const float *x, h8v &hi, h8v &lo) {
 #pragma unroll
-    for (int i = 0; i < kPer; i++) {
-        const int q = i * kThreads + t;
-        const int off = ((row0 + (q >> 5)) * kHd + (q & 31) * 8) * 2;
-        kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
-        vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
+    for (int e = 0; e < 8; e++) {
+        hi[e] = (_Float16)x[e];
+        lo[e] = (_Float16)(x[e] - (float)hi[e]);
     }
 }
 
 // grid = (chunks, n_kv_heads, batch); a chunk is `tpw` tiles of 64 positions
 // (tiles_per_chunk()).  mix: per sequence [q_full | k | v] rows (K-split
-// partial slices); q_full is [n_heads][q(256) | gate(256)].  The workgroup
-// walks its tiles with the next tile's K / V loads in flight while the
-// current one is used, keeping per query head (wave) an online-softmax
-// running max, sum and output; it writes one unnormalised partial.
+// partial slices); q_full is [n_heads][q(256) | gate(256)].
+//
+// Per tile, on MFMA (v_mfma_f32_16x16x32_f16; operands A[i][k] / B[k][j] in
+// lane i (j) + 16 (k / 8), element k % 8; D[i][j] in lane j + 16 (i / 4),
+// element i % 4):
+//  * scores S[pos][head] = K q^T / 16: wave w takes positions 16w..16w+15;
+//    its K fragments are loaded straight from the cache (A: lane l = row
+//    16w + l % 16, dims 32s + 8 (l / 16) of k-step s), q as fp16 hi + lo
+//    B fragments (columns = the G query heads, others zero), so K is read
+//    once for all G heads;
+//  * online softmax per head across the 4 waves (LDS);
+//  * O[head][dim] += P V: A = P (fp16 hi + lo of the probabilities), B = V
+//    from an LDS copy of the tile transposed to [dim][pos] (each thread holds
+//    an 8 x 8 block of V -- rows 8 rb .. +7, dims 8p .. +7 -- and transposes
+//    it in registers); wave w takes dims 64w..64w+63.
+// The next tiles' K / V loads are in flight while a tile is processed; the
+// buffer resources cover positions [0, pos) only, so rows >= pos read zeros
+// without a memory access (row pos takes this step's k / v), which also makes
+// the prefetch of a tile past the chunk free.  One
+// unnormalised partial per (chunk, query head) with its running max and sum.
 template <int G>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     MixIn mix, const float *__restrict__ q_norm, const float *__restrict__ k_norm,
     const float *__restrict__ inv_freq, const uint32_t *__restrict__ pos_arr, __half *__restrict__ k_cache,
     __half *__restrict__ v_cache, int max_seq, int n_heads, int n_kv, int tpw, float *__restrict__ part_o,
     float *__restrict__ part_ml) {
-    __shared__ float qs[G][kHd];
-    __shared__ __half tile[kCh * kRowH];
-    __shared__ __half knew[kHd], vnew[kHd];
-    __shared__ float probs[G][kCh];
+    __shared__ __align__(16) _Float16 vt[kHd * kCh];  // V^T of the tile, swizzled chunks
+    __shared__ __align__(16) float qs[G][kHd];
+    __shared__ __align__(16) h8v qf[8][2][64];         // q B fragments: k-step, hi / lo, lane
+    __shared__ __align__(16) float pt[G][kCh];        // probabilities of the tile
+    __shared__ __align__(16) __half knew[kHd], vnew[kHd];
+    __shared__ float rmax[4][16], rsum[4][16], rscale[16];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int li = lane & 15, lg = lane >> 4;  // MFMA operand row / column, k group
+    const int vp = t & 31, vrb = t >> 5;       // V block: dims 8 vp .., rows 8 vrb ..
     const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const uint32_t pos = pos_arr[b];
     const int len = (int)pos + 1;
@@ -120,12 +139,35 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     const int nch = gridDim.x;
     const size_t cache_base = ((size_t)b * n_kv + kvh) * (size_t)max_seq * kHd;
     const bool has_new = (int)pos < te * kCh;  // this chunk holds the current position
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(k_cache + cache_base, 0, (int)pos * kHd * 2, kWord3);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(v_cache + cache_base, 0, (int)pos * kHd * 2, kWord3);
-
-    // the first tile's loads go out before the q / k preparation
-    u32x4 ka[kPer], va[kPer], kb[kPer], vb[kPer];
-    load_kv_tile(ka, va, krs, vrs, tb * kCh, t);
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(k_cache + cache_base, 0, (int)pos * kHd * 2, kWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(v_cache + cache_base, 0, (int)pos * kHd * 2, kWord3);
+    // K fragments of this wave's 16 rows; V block of this thread.  A tile
+    // past the chunk is loaded from row kFar (>= pos: zeros, no memory access),
+    // so every step issues the same loads.
+    const int kFar = max_seq;
+    auto load_k = [&](u32x4 *kr, int row0) {
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int off = ((row0 + 16 * wave + li) * kHd + 32 * s + 8 * lg) * 2;
+            kr[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
+        }
+    };
+    auto load_v = [&](u32x4 *vr, int row0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int off = ((row0 + 8 * vrb + i) * kHd + 8 * vp) * 2;
+            vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
+        }
+    };
+    auto row_of = [&](int ti) { return ti < te ? ti * kCh : kFar; };
+    // the first tile's loads (and the second's K) go out before the q / k
+    // preparation
+    u32x4 ka[8], kb[8], vr[8];
+    load_k(ka, tb * kCh);
+    load_v(vr, tb * kCh);
+    load_k(kb, row_of(tb + 1));
 
     // q heads of this kv group: wave w < G prepares head kvh*G + w
     if (wave < G) {
@@ -156,114 +198,141 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         }
     }
     lds_barrier();
+    // q B fragments (lane l: head l % 16, dims 32s + 8 (l / 16) ..), scaled by
+    // 1/sqrt(256) = 1/16 (exact), as fp16 hi + lo; 4 (k-step, lane) pairs per thread
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int e = t + 256 * j, fs = e >> 6, fl = e & 63, fh = fl & 15, fg = fl >> 4;
+        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (fh < G) {
+            const float4 a = *reinterpret_cast<const float4 *>(&qs[fh][32 * fs + 8 * fg]);
+            const float4 bq = *reinterpret_cast<const float4 *>(&qs[fh][32 * fs + 8 * fg + 4]);
+            x[0] = a.x * 0.0625f; x[1] = a.y * 0.0625f; x[2] = a.z * 0.0625f; x[3] = a.w * 0.0625f;
+            x[4] = bq.x * 0.0625f; x[5] = bq.y * 0.0625f; x[6] = bq.z * 0.0625f; x[7] = bq.w * 0.0625f;
+        }
+        split8(x, qf[fs][0][fl], qf[fs][1][fl]);
+    }
+    lds_barrier();
 
-    // tile: 64 rows x 32 vectors of 16 bytes; row pos takes this step's k / v
-    auto store_tile = [&](const u32x4 *reg, const __half *fresh, int row0) {
-#pragma unroll
-        for (int i = 0; i < kPer; i++) {
-            const int q = i * kThreads + t;
-            const int r = q >> 5, part = q & 31;
-            u32x4 v = reg[i];
-            if (row0 + r == (int)pos) v = *reinterpret_cast<const u32x4 *>(fresh + part * 8);
-            *reinterpret_cast<u32x4 *>(&tile[r * kRowH + part * 8]) = v;
-        }
-    };
-    const float sdiv = sqrtf((float)kHd);
-    // per query head (wave < G): running max, sum and output dims 4l..4l+3
-    float m_run = -INFINITY, l_run = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-    auto process = [&](const u32x4 *kr, const u32x4 *vr, int ti) {
+    // per head li (< G): running max / sum; PV accumulators of dim block db:
+    // rows = heads 4 lg .. 4 lg + 3, column = dim 64 wave + 16 db + li
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 o[4] = {};
+    // tile ti with K in kr and V in vr; refills vr with tile ti + 1's V right
+    // after storing it, and kr with tile ti + 2's K right after the scores
+    auto process = [&](u32x4 *kr, int ti) {
         const int row0 = ti * kCh;
-        store_tile(kr, knew, row0);
-        lds_barrier();
-        // scores: wave = query head of the group, lane = position in the tile
-        if (wave < G) {
-            const int p = row0 + lane;
-            // 8 independent partial sums (dims d % 8), added pairwise at the end
-            float dp[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            const __half *krow = &tile[lane * kRowH];
-#pragma unroll 4
-            for (int d = 0; d < kHd; d += 8) {
-                u32x4 kv8 = *reinterpret_cast<const u32x4 *>(krow + d);
-                const float4 qa = *reinterpret_cast<const float4 *>(&qs[wave][d]);
-                const float4 qb = *reinterpret_cast<const float4 *>(&qs[wave][d + 4]);
-                const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-                const __half2 *h2 = reinterpret_cast<const __half2 *>(&kv8);
+        // this step's row: K from knew, V from vnew (loaded as zeros)
+        if (row0 + 16 * wave + li == (int)pos) {
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float2 kf = __half22float2(h2[e]);
-                    dp[2 * e] += qv[2 * e] * kf.x;
-                    dp[2 * e + 1] += qv[2 * e + 1] * kf.y;
-                }
-            }
-            const float dot = ((dp[0] + dp[1]) + (dp[2] + dp[3])) + ((dp[4] + dp[5]) + (dp[6] + dp[7]));
-            const float sc = p < len ? dot / sdiv : -INFINITY;
-            const float mn = fmaxf(m_run, wave_max(sc));  // finite: the tile has a valid row
-            const float scale = expf(m_run - mn);         // 0 on the first tile
-            const float e = p < len ? expf(sc - mn) : 0.0f;
-            l_run = l_run * scale + wave_sum(e);
-            o0 *= scale;
-            o1 *= scale;
-            o2 *= scale;
-            o3 *= scale;
-            m_run = mn;
-            probs[wave][lane] = e;
+            for (int s = 0; s < 8; s++) kr[s] = *reinterpret_cast<const u32x4 *>(&knew[32 * s + 8 * lg]);
         }
-        lds_barrier();
-        store_tile(vr, vnew, row0);
-        lds_barrier();
-        // PV: wave = query head, lane = 4 consecutive dims
-        if (wave < G) {
-            // rows past the sequence have zero probability (and zero V), so
-            // all 64 rows are summed: two independent chains, even / odd rows
-            float e0 = 0.f, e1 = 0.f, e2 = 0.f, e3 = 0.f;
-#pragma unroll 8
-            for (int p = 0; p < kCh; p += 2) {
-                const float2 pr = *reinterpret_cast<const float2 *>(&probs[wave][p]);
-                const __half2 *va2 = reinterpret_cast<const __half2 *>(&tile[p * kRowH + 4 * lane]);
-                const __half2 *vb2 = reinterpret_cast<const __half2 *>(&tile[(p + 1) * kRowH + 4 * lane]);
-                const float2 a = __half22float2(va2[0]), bb = __half22float2(va2[1]);
-                const float2 c = __half22float2(vb2[0]), dd = __half22float2(vb2[1]);
-                o0 += pr.x * a.x;
-                o1 += pr.x * a.y;
-                o2 += pr.x * bb.x;
-                o3 += pr.x * bb.y;
-                e0 += pr.y * c.x;
-                e1 += pr.y * c.y;
-                e2 += pr.y * dd.x;
-                e3 += pr.y * dd.y;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (row0 + 8 * vrb + i == (int)pos) vr[i] = *reinterpret_cast<const u32x4 *>(&vnew[8 * vp]);
+        // V block -> V^T rows 8 vp + d, chunk vrb
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            const int w = d >> 1;
+            u32x4 col;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t x0 = vr[2 * k][w], x1 = vr[2 * k + 1][w];
+                col[k] = (d & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
             }
-            o0 += e0;
-            o1 += e1;
-            o2 += e2;
-            o3 += e3;
+            const int D = 8 * vp + d;
+            *reinterpret_cast<u32x4 *>(&vt[D * kCh + 8 * vt_slot(D, vrb)]) = col;
         }
-        lds_barrier();  // the tile is rewritten by the next K
+        load_v(vr, row_of(ti + 1));
+        // scores of positions 16 wave + 4 lg + e, head li
+        f32x4 sc = {};
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const h8v a = __builtin_bit_cast(h8v, kr[s]);
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s][0][lane], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s][1][lane], sc, 0, 0, 0);
+        }
+        load_k(kr, row_of(ti + 2));
+        const int p0 = row0 + 16 * wave + 4 * lg;
+        float sv[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) sv[e] = p0 + e < len ? sc[e] : -INFINITY;
+        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (lane < 16) rmax[wave][lane] = mx;
+        lds_barrier();
+        const float tm = fmaxf(fmaxf(rmax[0][li], rmax[1][li]), fmaxf(rmax[2][li], rmax[3][li]));
+        const float mn = fmaxf(m_run, tm);     // finite for li < G: the tile has a valid row
+        const float scale = expf(m_run - mn);  // 0 on the first tile
+        float pe[4], ps = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            pe[e] = p0 + e < len ? expf(sv[e] - mn) : 0.0f;
+            ps += pe[e];
+        }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        if (lane < 16) rsum[wave][lane] = ps;
+        if (wave == 0 && lane < 16) rscale[lane] = scale;
+        if (li < G) *reinterpret_cast<float4 *>(&pt[li][16 * wave + 4 * lg]) = make_float4(pe[0], pe[1], pe[2], pe[3]);
+        lds_barrier();
+        l_run = l_run * scale + ((rsum[0][li] + rsum[1][li]) + (rsum[2][li] + rsum[3][li]));
+        m_run = mn;
+        // PV: rescale the rows (heads 4 lg + e), then P (hi + lo) times V^T
+        float rs[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) rs[e] = 4 * lg + e < G ? rscale[4 * lg + e] : 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; db++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[db][e] *= rs[e];
+        h8v ph[2], pl[2];
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (li < G) {
+                const float4 a = *reinterpret_cast<const float4 *>(&pt[li][32 * s + 8 * lg]);
+                const float4 bq = *reinterpret_cast<const float4 *>(&pt[li][32 * s + 8 * lg + 4]);
+                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = bq.x; x[5] = bq.y; x[6] = bq.z; x[7] = bq.w;
+            }
+            split8(x, ph[s], pl[s]);
+        }
+#pragma unroll
+        for (int db = 0; db < 4; db++) {
+            const int D = 64 * wave + 16 * db + li;
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const h8v bv = *reinterpret_cast<const h8v *>(&vt[D * kCh + 8 * vt_slot(D, 4 * s + lg)]);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bv, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], bv, o[db], 0, 0, 0);
+            }
+        }
+        lds_barrier();  // vt / pt / rmax are rewritten by the next tile
     };
-    // two register buffers.  Steady state: two tiles per trip with both next
-    // loads real and unconditional (every path into a trip carries the same
-    // loads, so the vmcnt waits stay exact); then the last one or two tiles.
+    // K in two register buffers (a tile's K is in flight during the tile
+    // before it), V in one.  Pairs of tiles, then the last one
     int ti = tb;
-    while (ti + 2 < te) {
-        load_kv_tile(kb, vb, krs, vrs, (ti + 1) * kCh, t);
-        process(ka, va, ti);
-        load_kv_tile(ka, va, krs, vrs, (ti + 2) * kCh, t);
-        process(kb, vb, ti + 1);
+    while (ti + 1 < te) {
+        process(ka, ti);
+        process(kb, ti + 1);
         ti += 2;
     }
-    if (ti + 1 < te) {
-        load_kv_tile(kb, vb, krs, vrs, (ti + 1) * kCh, t);
-        process(ka, va, ti);
-        process(kb, vb, ti + 1);
-    } else {
-        process(ka, va, ti);
-    }
-    if (wave < G) {
-        const size_t slot = (((size_t)b * n_kv + kvh) * nch + c) * G + wave;
-        *reinterpret_cast<float4 *>(part_o + slot * kHd + 4 * lane) = make_float4(o0, o1, o2, o3);
-        if (lane == 0) {
-            part_ml[slot * 2] = m_run;
-            part_ml[slot * 2 + 1] = l_run;
+    if (ti < te) process(ka, ti);
+    // lane (lg, li): heads 4 lg + e, dims 64 wave + 16 db + li
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int hh = 4 * lg + e;
+        if (hh < G) {
+            const size_t slot = (((size_t)b * n_kv + kvh) * nch + c) * G + hh;
+#pragma unroll
+            for (int db = 0; db < 4; db++) part_o[slot * kHd + 64 * wave + 16 * db + li] = o[db][e];
         }
+    }
+    if (wave == 0 && lane < G) {
+        const size_t slot = (((size_t)b * n_kv + kvh) * nch + c) * G + lane;
+        part_ml[slot * 2] = m_run;
+        part_ml[slot * 2 + 1] = l_run;
     }
 }
 
@@ -353,20 +422,23 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
     }
 }
 
-// Tiles of 64 positions per chunk (workgroup): a power of two that keeps at
-// most 128 chunks per sequence and kv head at the cache's capacity, so the
-// combine merges at most 128 partials per head.
-int tiles_per_chunk(int max_seq) {
+// Tiles of 64 positions per chunk (workgroup): the smallest power of two
+// that keeps at most 128 chunks per sequence and kv head and at most ~2048
+// workgroups (8 per CU) at the cache's capacity -- the combine merges at most
+// 128 partials per head, and each workgroup's q / k preparation is amortised
+// over several tiles when there are plenty of workgroups.
+int tiles_per_chunk(int max_seq, int batch, int n_kv) {
     const int tiles = (max_seq + kCh - 1) / kCh;
     int tpw = 1;
-    while ((tiles + tpw - 1) / tpw > 128) tpw *= 2;
+    auto chunks = [&] { return (tiles + tpw - 1) / tpw; };
+    while (chunks() > 128 || (tpw < tiles && (size_t)chunks() * n_kv * batch > 2048)) tpw *= 2;
     return tpw;
 }
 
 }  // namespace
 
 size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G) {
-    const int tpw = tiles_per_chunk(max_seq);
+    const int tpw = tiles_per_chunk(max_seq, batch, n_kv);
     const size_t nch = (size_t)((max_seq + kCh - 1) / kCh + tpw - 1) / tpw;
     return (size_t)batch * n_kv * nch * G * (kHd + 2);
 }
@@ -377,7 +449,7 @@ int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
                      const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,
                      _Float16 *out_hi, _Float16 *out_lo) {
     const int G = n_heads / n_kv;
-    const int tpw = tiles_per_chunk(max_seq);
+    const int tpw = tiles_per_chunk(max_seq, batch, n_kv);
     const int nch = ((max_seq + kCh - 1) / kCh + tpw - 1) / tpw;
     if ((size_t)max_seq * kHd * 2 >= (size_t)1 << 30)
         return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "attention: max_seq %d too large", max_seq);

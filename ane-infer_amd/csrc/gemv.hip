@@ -893,8 +893,8 @@ __device__ __forceinline__ void gemm_mma(const GemmUnit<T, TV> &u, int quarter, 
 // 16-byte row vectors (m % 4 == 0).
 constexpr int kBadOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
 
-template <uint32_t T, int TV, int D>
-__global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(TV == 1 ? 2 : 1))) void gemm_packed(
+template <uint32_t T, int TV, int D, int WPE = (TV == 1 ? 2 : 1)>
+__global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_packed(
     const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
     float *__restrict__ out, int m, int n, int batch, int ksplit, int per, size_t split_stride) {
     __shared__ __align__(16) float red[kGemmWaves][TV * 32][kWave];
