@@ -133,6 +133,10 @@ int anehip_deltanet_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, cons
     mb.stride = (int)n_heads;
     ma.p = alpha_raw;
     ma.stride = (int)n_heads;
+    // batch > 1: one workgroup per head and sequence (commits every window)
+    if (batch > 1)
+        return launch_deltanet_head(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
+                                    conv_state, S, out_heads, 0, nullptr, 0.0f, nullptr, nullptr);
     int rc = launch_deltanet_step(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
                                   conv_state, S, out_heads);
     if (rc) return rc;

@@ -193,6 +193,15 @@ int launch_gemv_fused(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, c
 int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *out);
+// Batch > 1: the whole DeltaNet step of a head in one workgroup -- conv +
+// SiLU, L2 norms, beta / decay, recurrence, all conv windows committed -- and
+// either the raw head outputs (out, fp32) or, with out == nullptr, the gated
+// RMSNorm (gate from mix rows at gate_off, norm_w, eps) as fragment-order
+// fp16 hi/lo planes out_hi / out_lo.
+int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
+                         const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
+                         const float *dt_bias, float *conv_state, float *S, float *out, int gate_off,
+                         const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo);
 // Commits the q/k conv windows (if conv_state) and, if heads, writes the gated
 // RMSNorm of the heads (gate from mix rows at gate_off) to out (fp32) or, if
 // out_hi, to fragment-order fp16 hi/lo planes out_hi / out_lo (xf_index).

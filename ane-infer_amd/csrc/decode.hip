@@ -401,10 +401,9 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
         mix.stride = (int)rows_in;
         uint32_t cols3;
         if (dn) {
-            TRY(launch_deltanet_step(ctx, s, B, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
-                                     L.conv1d, L.ssm_a, L.dt_bias, L.conv_state, L.S, M->heads));
-            TRY(launch_dn_finish(ctx, s, B, (int)H, mix, L.conv_state, M->heads, (int)C, L.ssm_norm, nullptr, xh,
-                                 xl, eps));
+            TRY(launch_deltanet_head(ctx, s, B, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
+                                     L.conv1d, L.ssm_a, L.dt_bias, L.conv_state, L.S, nullptr, (int)C, L.ssm_norm,
+                                     eps, xh, xl));
             cols3 = d;
         } else {
             TRY(launch_attention(ctx, s, B, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,

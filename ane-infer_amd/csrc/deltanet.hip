@@ -202,7 +202,142 @@ __global__ __launch_bounds__(kDk) void dn_finish_kernel(MixIn mix, float *__rest
     }
 }
 
+// Batch > 1: one workgroup (256 threads) per (head, sequence) holding the
+// whole 128 x 128 head state (thread: columns 4 cq .. +3, rows 16 rg .. +15),
+// so the same step as deltanet_step_kernel can also commit all of the head's
+// conv windows (no other workgroup reads them) and finish with the gated
+// RMSNorm (deltanet.rs:517-533), written as fragment-order fp16 hi/lo planes
+// for the panel GEMM; with `out` it writes the raw head outputs (fp32)
+// instead.  grid = (n_heads, batch).
+__global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
+    MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
+    const float *__restrict__ dt_bias, float *__restrict__ conv_state, float *__restrict__ S, float *__restrict__ out,
+    int gate_off, const float *__restrict__ norm_w, float eps, _Float16 *__restrict__ out_hi,
+    _Float16 *__restrict__ out_lo, int n_heads) {
+    __shared__ float qn[kDk], kn[kDk], vv[kDk];
+    __shared__ __align__(16) float part[8][kDk];
+    __shared__ float red[4];
+    __shared__ float misc[2];  // beta, decay
+
+    const int t = threadIdx.x;
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int chunk = n_heads * kDk;
+    const int C = 3 * chunk;
+    float *cs = conv_state + (size_t)b * C * kKsize;
+    const int cq = t & 31, rg = t >> 5;
+    float *Sh = S + (((size_t)b * n_heads + h) * kDk) * kDk + 4 * cq;
+    // the state is loaded first: its memory latency overlaps steps 1-2
+    float4 s[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(16 * rg + r) * kDk);
+
+    // 1. conv + SiLU of q (t < 128) and k (t >= 128), and of v (t < 128); the
+    // windows are committed here
+    {
+        const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + (t - kDk);
+        float y = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, mix.at(b, ch), true));
+        float sq = wave_sum(y * y);
+        if ((t & 63) == 0) red[t >> 6] = sq;
+        if (t < kDk) qn[t] = y;
+        else kn[t - kDk] = y;
+    }
+    if (t < kDk) {
+        const int ch = 2 * chunk + h * kDk + t;
+        vv[t] = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, mix.at(b, ch), true));
+    }
+    if (t == 0) {
+        // deltanet.rs:474-480
+        const float br = mbeta.at(b, h);
+        const float ar = malpha.at(b, h);
+        misc[0] = 1.0f / (1.0f + expf(-br));
+        const float g = ssm_a[h] * logf(1.0f + expf(ar + dt_bias[h]));
+        misc[1] = expf(g);
+    }
+    __syncthreads();
+    // 2. L2 normalise (deltanet.rs:25-31, 461-467): x *= 1/sqrt(sum x^2 + 1e-12); q *= 1/sqrt(dk)
+    if (t < kDk) {
+        const float inv = 1.0f / sqrtf((red[0] + red[1]) + 1e-12f);
+        const float scale = 1.0f / sqrtf((float)kDk);
+        qn[t] = (qn[t] * inv) * scale;
+    } else {
+        const float inv = 1.0f / sqrtf((red[2] + red[3]) + 1e-12f);
+        kn[t - kDk] = kn[t - kDk] * inv;
+    }
+    __syncthreads();
+
+    const float beta = misc[0], decay = misc[1];
+    // 3. S' = decay * S, partial recall sum_i S'_ij k_i over this thread's rows
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const float ki = kn[16 * rg + r];
+        s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
+        sk.x += s[r].x * ki; sk.y += s[r].y * ki; sk.z += s[r].z * ki; sk.w += s[r].w * ki;
+    }
+    *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = sk;
+    __syncthreads();
+    // delta_j = beta (v_j - sk_j), every thread for its 4 columns (fixed order)
+    float4 delta;
+    {
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            float4 p = *reinterpret_cast<const float4 *>(&part[g][4 * cq]);
+            a[0] += p.x; a[1] += p.y; a[2] += p.z; a[3] += p.w;
+        }
+        delta.x = beta * (vv[4 * cq + 0] - a[0]);
+        delta.y = beta * (vv[4 * cq + 1] - a[1]);
+        delta.z = beta * (vv[4 * cq + 2] - a[2]);
+        delta.w = beta * (vv[4 * cq + 3] - a[3]);
+    }
+    __syncthreads();  // part[] is reused below
+    // S'' = S' + k delta^T (written back), partial query sum_i S''_ij q_i
+    float4 so = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const float ki = kn[16 * rg + r], qi = qn[16 * rg + r];
+        s[r].x += ki * delta.x; s[r].y += ki * delta.y; s[r].z += ki * delta.z; s[r].w += ki * delta.w;
+        *reinterpret_cast<float4 *>(Sh + (size_t)(16 * rg + r) * kDk) = s[r];
+        so.x += s[r].x * qi; so.y += s[r].y * qi; so.z += s[r].z * qi; so.w += s[r].w * qi;
+    }
+    *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = so;
+    __syncthreads();
+    // 4. head output o_j (j = t < 128), then raw or gated-RMSNorm output
+    float o = 0.f;
+    if (t < kDk) {
+#pragma unroll
+        for (int g = 0; g < 8; g++) o += part[g][t];
+    }
+    if (out) {
+        if (t < kDk) out[(size_t)b * chunk + h * kDk + t] = o;
+        return;
+    }
+    const float ss = wave_sum(o * o);  // waves 2-3 contribute zeros
+    __syncthreads();                   // red[] is reused
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    if (t >= kDk) return;
+    const float inv_rms = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + eps);
+    const float gt = mix.at(b, gate_off + h * kDk + t);
+    const float v = ((o * inv_rms) * norm_w[t]) * (gt / (1.0f + expf(-gt)));
+    const size_t xo = xf_index(b, h * kDk + t);
+    const _Float16 hi = (_Float16)v;
+    out_hi[xo] = hi;
+    out_lo[xo] = (_Float16)(v - (float)hi);
+}
+
 }  // namespace
+
+int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
+                         const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
+                         const float *dt_bias, float *conv_state, float *S, float *out, int gate_off,
+                         const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo) {
+    if (!out && !out_hi) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_head: no output");
+    hipLaunchKernelGGL(deltanet_head_kernel, dim3(n_heads, batch), dim3(kThreads), 0, stream, mix, beta, alpha, conv_w,
+                       ssm_a, dt_bias, conv_state, S, out, gate_off, norm_w, eps, out_hi, out_lo, n_heads);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
 
 int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
