@@ -295,12 +295,15 @@ int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const 
 
 int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
                             int ksplit, const float *w, float *xn, float eps, _Float16 *hi, _Float16 *lo) {
-    if (n % 4 == 0 && n <= 2048 && ksplit >= 1 && ksplit <= 8) {
+    if (n % 4 == 0 && n <= 2048 && ksplit >= 1 && ksplit <= 16) {
         if (ksplit <= 2)
             hipLaunchKernelGGL(residual_rmsnorm_v4<2>, dim3(rows), dim3(512), 0, s, x, part, ksplit, rows, w, xn, n,
                                eps, hi, lo);
-        else
+        else if (ksplit <= 8)
             hipLaunchKernelGGL(residual_rmsnorm_v4<8>, dim3(rows), dim3(512), 0, s, x, part, ksplit, rows, w, xn, n,
+                               eps, hi, lo);
+        else
+            hipLaunchKernelGGL(residual_rmsnorm_v4<16>, dim3(rows), dim3(512), 0, s, x, part, ksplit, rows, w, xn, n,
                                eps, hi, lo);
     } else {
         hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, part, ksplit, rows, w, xn,

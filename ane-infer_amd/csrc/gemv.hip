@@ -153,7 +153,8 @@ __device__ __forceinline__ float wg_sum(float v, float *red) {
     return s;
 }
 
-constexpr int kMaxSplit = 8;     // K splits a consumer may have to add
+constexpr int kMaxSplit = 8;     // K splits a batch-1 consumer may have to add
+constexpr int kMaxGemmSplit = 16;  // K splits of the x-stationary GEMM (batch > 1)
 constexpr int kMaxSliceSb = 8;   // super-blocks of input one workgroup may need
 
 // sum over p < kp of part[p * stride + i], p ascending.  All kMaxSplit loads
@@ -829,54 +830,101 @@ __device__ __forceinline__ void gemm_load(GemmUnit<T, TV> &u, const uint8_t *pan
     }
 }
 
-// acc[t]{0,1} += the unit's two blocks of tile t: per block C = sum over its 2
-// column steps and the 2 planes (4 MFMAs per 32 weight rows), then
-// acc += C * d (q8_gemv.rs:234-242 order within a block up to fp32 summation).
+// acc{0,1} += one tile's two blocks of a quarter: q = its quant vectors, sc
+// the lane row's scale vector, ah / al the x fragments of the quarter's 4
+// column steps.  Per block C = sum over its 2 column steps and the 2 planes
+// (4 MFMAs per 32 weight rows), then acc += C * d (q8_gemv.rs:234-242 order
+// within a block up to fp32 summation).
+template <uint32_t T>
+__device__ __forceinline__ uint32_t quarter_scales(const u32x4 &sv, int quarter) {
+    return quarter == 0 ? sv.x : quarter == 1 ? sv.y : quarter == 2 ? sv.z : sv.w;
+}
+
+// sw: dword `quarter` of the lane's scale vector (blocks 2q, 2q + 1)
+template <uint32_t T>
+__device__ __forceinline__ void mma_tile(const u32x4 *q, uint32_t sw, const h8v *ah, const h8v *al, f32x16 &acc0,
+                                         f32x16 &acc1) {
+    // after the swap s0 / s1 are the scales of weight rows l % 32 and 32 + l % 32
+    const auto sp = __builtin_amdgcn_permlane32_swap(sw, sw, false, false);
+    const uint32_t s0 = sp[0], s1 = sp[1];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        f32x16 c0 = {}, c1 = {};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int s = 2 * j + h;  // column step: columns 16 s .. 16 s + 15 of the quarter
+            h8v b0, b1;
+            if constexpr (T == ANEHIP_GGML_Q8_0) {
+                const u32x4 v = q[s];
+                uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
+                swap_halves(a0, a1, c0w, c1w);
+                b0 = dwords_to_h8_i8(a0, a1);
+                b1 = dwords_to_h8_i8(c0w, c1w);
+            } else {
+                const u32x4 v = q[j];
+                uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
+                swap_halves(a0, a1, c0w, c1w);
+                const uint32_t sh = 4 * h;  // step 0: low nibbles, step 1: high nibbles
+                b0 = dwords_to_h8_u4((a0 >> sh) & 0x0F0F0F0Fu, (a1 >> sh) & 0x0F0F0F0Fu);
+                b1 = dwords_to_h8_u4((c0w >> sh) & 0x0F0F0F0Fu, (c1w >> sh) & 0x0F0F0F0Fu);
+            }
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[s], b0, c0, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[s], b0, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[s], b1, c1, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[s], b1, c1, 0, 0, 0);
+        }
+        const float d0 = __half2float(__ushort_as_half((unsigned short)(s0 >> (16 * j))));
+        const float d1 = __half2float(__ushort_as_half((unsigned short)(s1 >> (16 * j))));
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            acc0[r] = fmaf(c0[r], d0, acc0[r]);
+            acc1[r] = fmaf(c1[r], d1, acc1[r]);
+        }
+    }
+}
+
 template <uint32_t T, int TV>
 __device__ __forceinline__ void gemm_mma(const GemmUnit<T, TV> &u, int quarter, f32x16 (&acc)[TV][2]) {
 #pragma unroll
-    for (int t = 0; t < TV; t++) {
-        // dword `quarter` of the scale vector holds blocks 2q, 2q + 1; after
-        // the swap s0 / s1 are those of weight rows l % 32 and 32 + l % 32
-        const u32x4 sv = u.sc[t];
-        const uint32_t sw = quarter == 0 ? sv.x : quarter == 1 ? sv.y : quarter == 2 ? sv.z : sv.w;
-        const auto sp = __builtin_amdgcn_permlane32_swap(sw, sw, false, false);
-        const uint32_t s0 = sp[0], s1 = sp[1];
+    for (int t = 0; t < TV; t++)
+        mma_tile<T>(u.q[t], quarter_scales<T>(u.sc[t], quarter), u.ah, u.al, acc[t][0], acc[t][1]);
+}
+
+// End of a tile's item: every wave parks its 32 sums per lane (accumulator
+// element r of lane l: batch row 8 (r / 4 % 4) + 4 (l / 32) + r % 4, tile row
+// l % 32 + 32 (r / 16)); then each of the 256 threads adds the 4 quarters of
+// two 4-row vectors of one batch row and stores them with 16-byte buffer
+// stores (rows outside the batch or the matrix, or store == false, take an
+// offset past the buffer and are dropped).  red: [4][32][64] floats.
+constexpr int kBadOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
+
+__device__ __forceinline__ void gemm_tile_epilogue(float (*red)[32][kWave], const f32x16 &acc0, const f32x16 &acc1,
+                                                   int quarter, int lane, int tile, int ks, int batch, int m,
+                                                   size_t split_stride, __amdgpu_buffer_rsrc_t orsrc, bool store) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            f32x16 c0 = {}, c1 = {};
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int s = 2 * j + h;  // column step: columns 16 s .. 16 s + 15 of the quarter
-                h8v b0, b1;
-                if constexpr (T == ANEHIP_GGML_Q8_0) {
-                    const u32x4 v = u.q[t][s];
-                    uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
-                    swap_halves(a0, a1, c0w, c1w);
-                    b0 = dwords_to_h8_i8(a0, a1);
-                    b1 = dwords_to_h8_i8(c0w, c1w);
-                } else {
-                    const u32x4 v = u.q[t][j];
-                    uint32_t a0 = v.x, a1 = v.y, c0w = v.z, c1w = v.w;
-                    swap_halves(a0, a1, c0w, c1w);
-                    const uint32_t sh = 4 * h;  // step 0: low nibbles, step 1: high nibbles
-                    b0 = dwords_to_h8_u4((a0 >> sh) & 0x0F0F0F0Fu, (a1 >> sh) & 0x0F0F0F0Fu);
-                    b1 = dwords_to_h8_u4((c0w >> sh) & 0x0F0F0F0Fu, (c1w >> sh) & 0x0F0F0F0Fu);
-                }
-                c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.ah[s], b0, c0, 0, 0, 0);
-                c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.al[s], b0, c0, 0, 0, 0);
-                c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.ah[s], b1, c1, 0, 0, 0);
-                c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(u.al[s], b1, c1, 0, 0, 0);
-            }
-            const float d0 = __half2float(__ushort_as_half((unsigned short)(s0 >> (16 * j))));
-            const float d1 = __half2float(__ushort_as_half((unsigned short)(s1 >> (16 * j))));
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                acc[t][0][r] = fmaf(c0[r], d0, acc[t][0][r]);
-                acc[t][1][r] = fmaf(c1[r], d1, acc[t][1][r]);
-            }
-        }
+    for (int r = 0; r < 16; r++) {
+        red[quarter][r][lane] = acc0[r];
+        red[quarter][16 + r][lane] = acc1[r];
     }
+    lds_barrier();
+    const int th = threadIdx.x & (kWave * kGemmWaves - 1);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int v = th + 256 * i;  // 512 vectors: batch row b, rows 4 j .. 4 j + 3
+        const int b = v >> 4, j = v & 15;
+        const int r = 4 * (b >> 3) + (b & 3) + (j >= 8 ? 16 : 0);
+        const int l = ((4 * j) & 31) + 32 * ((b >> 2) & 1);
+        float4 sum = *reinterpret_cast<const float4 *>(&red[0][r][l]);
+#pragma unroll
+        for (int w = 1; w < kGemmWaves; w++) {
+            const float4 o = *reinterpret_cast<const float4 *>(&red[w][r][l]);
+            sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
+        }
+        const int row = tile * kWave + 4 * j;
+        const int off = store && b < batch && row < m ? 4 * (ks * (int)split_stride + b * m + row) : kBadOffset;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0, 0);
+    }
+    lds_barrier();  // red is free again
 }
 
 // Persistent panel GEMM.  A workgroup has 4 waves, one per column quarter q
@@ -891,8 +939,6 @@ __device__ __forceinline__ void gemm_mma(const GemmUnit<T, TV> &u, int quarter, 
 // has no barrier and no wait for the prefetched loads.  Output as
 // quant_gemm_tiled: out[split * split_stride + b * m + row], stored as
 // 16-byte row vectors (m % 4 == 0).
-constexpr int kBadOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
-
 template <uint32_t T, int TV, int D, int WPE = (TV == 1 ? 2 : 1)>
 __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_packed(
     const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
@@ -1002,6 +1048,94 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int k = 0; k < D; k++) step(ring[k]);
     } while (ci < items);
+}
+
+// x-stationary panel GEMM for K-split shapes.  Workgroup g works on split
+// ks = g % ksplit only (its P panels); each wave loads the x fragments of its
+// column quarter in those panels once (32 P VGPRs) and then streams the
+// weights of its tiles t = g / ksplit, g / ksplit + G / ksplit, ...: a unit
+// (one panel of one tile) is 5 loads -- 4 quant vectors and the quarter's
+// dword of the scale vector -- instead of 13.  R tiles (R * P units) are in flight in a register ring;
+// as in gemm_packed the loop's single exit and branch-free cursors keep the
+// vmcnt waits exact, and tiles past the workgroup's last are loaded clamped
+// and stored nowhere.  Same arithmetic and output as gemm_packed.
+template <uint32_t T> struct WUnit {
+    u32x4 q[GemmUnit<T, 1>::kQ];
+    uint32_t sc;  // the quarter's dword of the lane's scale vector
+};
+
+template <uint32_t T, int P, int R>
+__global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(2))) void gemm_xs(
+    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+    float *__restrict__ out, int m, int n, int batch, int ksplit, size_t split_stride) {
+    constexpr int Q = GemmUnit<T, 1>::kQ;
+    __shared__ __align__(16) float red[kGemmWaves][32][kWave];
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
+    const int gs = gridDim.x / ksplit;  // workgroups per split
+    const int ks = blockIdx.x % ksplit, g0 = blockIdx.x / ksplit;
+    if (g0 >= gs || g0 >= tiles) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
+    const __amdgpu_buffer_rsrc_t orsrc =
+        __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
+    // this quarter's x fragments of the split's panels
+    h8v xa[P][4], xb[P][4];
+    {
+        const size_t xbase = (size_t)(4 * quarter * kWave + min(lane & 31, batch - 1) + 32 * (lane >> 5)) * 8 +
+                             16 * 512 * (size_t)(ks * P);
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                xa[p][st] = *reinterpret_cast<const h8v *>(xh + xbase + 16 * 512 * p + 512 * st);
+                xb[p][st] = *reinterpret_cast<const h8v *>(xl + xbase + 16 * 512 * p + 512 * st);
+            }
+    }
+    const uint8_t *wsplit = Wp + (size_t)(ks * P) * Panel<T>::kBytes;
+    int lt = g0;  // next tile to load
+    auto load_tile = [&](WUnit<T> (&u)[P]) {
+        const u32x4 *p4 = reinterpret_cast<const u32x4 *>(wsplit + (size_t)min(lt, tiles - 1) * tile_bytes);
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const u32x4 *pp = p4 + p * (Panel<T>::kBytes / 16);
+#pragma unroll
+            for (int c = 0; c < Q; c++) u[p].q[c] = __builtin_nontemporal_load(pp + (Q * quarter + c) * kWave + lane);
+            u[p].sc = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(pp + Panel<T>::kChunks * kWave + lane) + quarter);
+        }
+        lt += gs;
+    };
+    // The empty asm statements order the ring: the prologue's loads stay in
+    // ring order (else the loop-header wait merges in the prologue's order),
+    // and a step waits for its own unit at its start, after the previous
+    // step's refill was issued (else the next unit's dequantisation is
+    // hoisted above that refill, with a wait for all loads in flight).
+    WUnit<T> ring[R][P];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        load_tile(ring[r]);
+        asm volatile("" ::: "memory");
+    }
+    int ct = g0;  // tile being multiplied
+    auto step = [&](WUnit<T> (&u)[P]) {
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+#pragma unroll
+            for (int c = 0; c < Q; c++) asm volatile("" : "+v"(u[p].q[c])::"memory");
+            asm volatile("" : "+v"(u[p].sc)::"memory");
+        }
+        f32x16 acc0 = {}, acc1 = {};
+#pragma unroll
+        for (int p = 0; p < P; p++) mma_tile<T>(u[p].q, u[p].sc, xa[p], xb[p], acc0, acc1);
+        asm volatile("" : "+v"(acc0), "+v"(acc1)::"memory");
+        load_tile(u);
+        gemm_tile_epilogue(red, acc0, acc1, quarter, lane, ct, ks, batch, m, split_stride, orsrc, ct < tiles);
+        ct += gs;
+    };
+    do {
+#pragma unroll
+        for (int r = 0; r < R; r++) step(ring[r]);
+    } while (ct < tiles);
 }
 
 // fp32 x[batch][n] -> fragment-order fp16 planes hi, lo (hi + lo ~= x), one
@@ -1320,17 +1454,24 @@ int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, bool norm_
     return packed_ksplit(tiles, (int)(n / 256), norm_prologue ? cus / 2 : cus);
 }
 
-// K splits of the panel MFMA GEMM: among the even splits of the panels (at
-// most kMaxSplit), the one that minimises the panels of the busiest CU,
-// ceil(items / CUs) x panels per split, with single-panel splits counted
-// double (each unit then pays a whole item's reduction) and ties going to
-// fewer splits; no split for matrices of at least 4 tiles per CU (their
-// partial sums would cost more than the balance gains).  Measured on MI355X
-// at batch 4 and 32 this picks the fastest split of every decode shape
-// (e.g. 12288 x 2048: k = 4, 11.6 us; uneven k = 3: 15.5 us).
+// K splits of the panel MFMA GEMM.  Matrices of fewer row tiles than CUs
+// take the x-stationary kernel with P = 2 panels per split (P = 1 when that
+// grid would not reach two workgroups per CU, or for an odd panel count):
+// measured on MI355X at batch 4 and 32 it beats the persistent kernel on
+// every decode shape (12288 x 2048, batch 32: 10.4 us at k = 4 against
+// 11.9 us; 2048 x 2048: 3.9 us at k = 8 against 5.4 us), and P = 2 halves
+// the partial sums the consumer reads against P = 1 where the times tie.
+// Otherwise, among the even splits of at most kMaxSplit, the one that
+// minimises the panels of the busiest CU, ceil(items / CUs) x panels per
+// split, with single-panel splits counted double and ties going to fewer
+// splits; no split for matrices of at least 4 tiles per CU.
 int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
     const int tiles = (int)((m + kWave - 1) / kWave);
     const int nsb = (int)(n / 256), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    if (tiles < cus && nsb >= 2) {
+        const int P = nsb % 2 == 0 && tiles * nsb > 2 * cus ? 2 : 1;
+        if (nsb / P <= kMaxGemmSplit) return nsb / P;
+    }
     if (tiles >= 4 * cus) return 1;
     int best = 1;
     double best_cost = 1e30;
@@ -1359,6 +1500,25 @@ int launch_gemm_packed_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, 
     return ANEHIP_OK;
 }
 
+// x-stationary grid for an even K split of P = nsb / ksplit panels (1 or 2):
+// a whole number of workgroups per split, about 3 per CU at P = 1 and 2 at
+// P = 2, each with one tile of weights in flight (deeper register rings and
+// more workgroups per split measured slower on every decode shape).
+template <uint32_t T>
+void launch_gemm_xs_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
+                      const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit, int per) {
+    const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int gs = max(1, min(tiles, (per == 1 ? 3 : 2) * cus / ksplit));
+    const dim3 grid(gs * ksplit), block(kWave * kGemmWaves);
+    const size_t ss = (size_t)batch * m;
+    if (per == 1)
+        hipLaunchKernelGGL((gemm_xs<T, 1, 1>), grid, block, 0, stream, w, xh, xl, out, (int)m, (int)n, (int)batch,
+                           ksplit, ss);
+    else
+        hipLaunchKernelGGL((gemm_xs<T, 2, 1>), grid, block, 0, stream, w, xh, xl, out, (int)m, (int)n, (int)batch,
+                           ksplit, ss);
+}
+
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                        uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit) {
     const int per = split_len((int)(n / 256), ksplit);
@@ -1369,7 +1529,12 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     if (4.0 * ksplit * batch * m > 1073741824.0)  // output byte offsets stay below kBadOffset
         return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
-    if (ggml_type == ANEHIP_GGML_Q8_0)
+    const bool xs = ksplit >= 2 && per * ksplit == (int)(n / 256) && per <= 2;
+    if (xs && ggml_type == ANEHIP_GGML_Q8_0)
+        launch_gemm_xs_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
+    else if (xs)
+        launch_gemm_xs_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
+    else if (ggml_type == ANEHIP_GGML_Q8_0)
         launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
     else
         launch_gemm_packed_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);

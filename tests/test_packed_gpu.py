@@ -109,10 +109,17 @@ def test_packed_rejects_bad_shapes(gpu_ctx, anehip_mod):
 @pytest.mark.gpu
 @pytest.mark.parametrize("t", [8, 2])
 @pytest.mark.parametrize("batch", [2, 3, 4, 7, 16, 17, 32])
-@pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144), (100, 256), (8224, 2048), (12288, 1792)])
+@pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144), (100, 256), (8224, 2048), (12288, 1792), (2048, 2048),
+                                 (100, 512), (1024, 8192), (20480, 2048)])
 def test_packed_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
     """Panel MFMA GEMM, ragged batch (not padded to the 32-row MFMA tile), at
-    the decode shapes, a tiny matrix and an odd panel count (12288 x 1792)."""
+    the decode shapes, a tiny matrix and an odd panel count (12288 x 1792).
+    Covers both kernels and both x-stationary forms: 2 panels per K split
+    (6144 x 2048, 2048 x 6144 at 12 splits, 8224 x 2048 with a ragged last
+    tile), 1 panel (2048 x 2048, 100 x 512, the odd 12288 x 1792), the
+    persistent kernel (100 x 256; 1024 x 8192, whose 32 single-panel splits
+    exceed the x-stationary limit), and a matrix of more tiles than CUs split
+    by the balance model (20480 x 2048)."""
     w = oracle_lib.gen_quant(t, 99, m + 5 * n + t, m, n, std=0.02)
     x = oracle_lib.normal(99, 300 + batch, batch * n).reshape(batch, n)
     dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
