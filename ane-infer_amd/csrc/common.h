@@ -109,6 +109,22 @@ struct MixIn {
         m.p = p + off;
         return m;
     }
+    // The KP slices of value (b, i) loaded unconditionally (slices past kp
+    // re-read the last one: an address the compiler cannot merge with another
+    // load, which would make it wait for that load), so that a kernel can
+    // issue all of its loads before it needs any; add() then sums them in
+    // slice order, as at() does.
+    template <int KP> __device__ __forceinline__ void load(int b, int i, float (&v)[KP]) const {
+        const float *q0 = p + (size_t)b * stride + i;
+#pragma unroll
+        for (int q = 0; q < KP; q++) v[q] = q0[(size_t)min(q, kp - 1) * split];
+    }
+    template <int KP> __device__ __forceinline__ float add(const float (&v)[KP]) const {
+        float s = v[0];
+#pragma unroll
+        for (int q = 1; q < KP; q++) s = q < kp ? s + v[q] : s;
+        return s;
+    }
     __host__ __device__ __forceinline__ float at(int b, int i) const {
         const float *q0 = p + (size_t)b * stride + i;
         float s = q0[0];

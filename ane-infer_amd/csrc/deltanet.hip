@@ -30,6 +30,8 @@ constexpr int kCols = 32;    // value columns per workgroup
 constexpr int kThreads = 256;
 constexpr int kKsize = 4;    // conv width (ssm_conv_kernel)
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float silu_ref(float x) { return x / (1.0f + expf(-x)); }
 
 // conv_shift_and_append + conv_apply (deltanet_cache.rs:34-54) for one channel;
@@ -208,7 +210,8 @@ __global__ __launch_bounds__(kDk) void dn_finish_kernel(MixIn mix, float *__rest
 // conv windows (no other workgroup reads them) and finish with the gated
 // RMSNorm (deltanet.rs:517-533), written as fragment-order fp16 hi/lo planes
 // for the panel GEMM; with `out` it writes the raw head outputs (fp32)
-// instead.  grid = (n_heads, batch).
+// instead.  grid = (n_heads, batch).  KP >= the K splits of the projections.
+template <int KP>
 __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
     MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
     const float *__restrict__ dt_bias, float *__restrict__ conv_state, float *__restrict__ S, float *__restrict__ out,
@@ -217,7 +220,6 @@ __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
     __shared__ float qn[kDk], kn[kDk], vv[kDk];
     __shared__ __align__(16) float part[8][kDk];
     __shared__ float red[4];
-    __shared__ float misc[2];  // beta, decay
 
     const int t = threadIdx.x;
     const int h = blockIdx.x, b = blockIdx.y;
@@ -226,33 +228,57 @@ __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
     float *cs = conv_state + (size_t)b * C * kKsize;
     const int cq = t & 31, rg = t >> 5;
     float *Sh = S + (((size_t)b * n_heads + h) * kDk) * kDk + 4 * cq;
-    // the state is loaded first: its memory latency overlaps steps 1-2
+
+    // Every small input is loaded first and the state after it: vector loads
+    // complete in order, so the conv, norms and gates wait only for the small
+    // loads while the 64 KiB state is in flight.  Thread t convolves a q
+    // (t < 128) or k channel, and the v channel t % 128 (kept by t < 128).
+    const int e = t & (kDk - 1);
+    const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + e, chv = 2 * chunk + h * kDk + e;
+    f32x4 win = *reinterpret_cast<const f32x4 *>(cs + (size_t)ch * kKsize);
+    f32x4 wk = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)ch * kKsize);
+    f32x4 winv = *reinterpret_cast<const f32x4 *>(cs + (size_t)chv * kKsize);
+    f32x4 wkv = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)chv * kKsize);
+    float xa[KP], xv[KP], xg[KP], xb[KP], xal[KP];
+    mix.load<KP>(b, ch, xa);
+    mix.load<KP>(b, chv, xv);
+    mix.load<KP>(b, gate_off + h * kDk + e, xg);
+    mbeta.load<KP>(b, h, xb);
+    malpha.load<KP>(b, h, xal);
+    const float sa = ssm_a[h], dtb = dt_bias[h], nw = out ? 0.0f : norm_w[e];
+    asm volatile("" ::: "memory");  // keeps the state loads behind the small ones
     float4 s[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(16 * rg + r) * kDk);
+    // the arithmetic on the small inputs starts here, after the state loads
+    // were issued (else it is scheduled above them, with its waits)
+    asm volatile("" : "+v"(win), "+v"(wk), "+v"(winv), "+v"(wkv)::"memory");
+#pragma unroll
+    for (int q = 0; q < KP; q++) asm volatile("" : "+v"(xa[q]), "+v"(xv[q]), "+v"(xb[q]), "+v"(xal[q]));
 
-    // 1. conv + SiLU of q (t < 128) and k (t >= 128), and of v (t < 128); the
-    // windows are committed here
+    // 1. conv + SiLU (conv_shift_and_append + conv_apply, deltanet_cache.rs:
+    // 34-54); the windows are committed here
+    const auto conv = [&](f32x4 w0, f32x4 k, float x, int c, bool write) {
+        const float4 ns = make_float4(w0.y, w0.z, w0.w, x);
+        float sum = 0.0f;
+        sum += ns.x * k.x;
+        sum += ns.y * k.y;
+        sum += ns.z * k.z;
+        sum += ns.w * k.w;
+        if (write) *reinterpret_cast<float4 *>(cs + (size_t)c * kKsize) = ns;
+        return silu_ref(sum);
+    };
     {
-        const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + (t - kDk);
-        float y = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, mix.at(b, ch), true));
-        float sq = wave_sum(y * y);
+        const float y = conv(win, wk, mix.add<KP>(xa), ch, true);
+        const float sq = wave_sum(y * y);
         if ((t & 63) == 0) red[t >> 6] = sq;
         if (t < kDk) qn[t] = y;
-        else kn[t - kDk] = y;
+        else kn[e] = y;
+        if (t < kDk) vv[t] = conv(winv, wkv, mix.add<KP>(xv), chv, true);
     }
-    if (t < kDk) {
-        const int ch = 2 * chunk + h * kDk + t;
-        vv[t] = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, mix.at(b, ch), true));
-    }
-    if (t == 0) {
-        // deltanet.rs:474-480
-        const float br = mbeta.at(b, h);
-        const float ar = malpha.at(b, h);
-        misc[0] = 1.0f / (1.0f + expf(-br));
-        const float g = ssm_a[h] * logf(1.0f + expf(ar + dt_bias[h]));
-        misc[1] = expf(g);
-    }
+    // deltanet.rs:474-480, by every thread (no shared copy needed)
+    const float beta = 1.0f / (1.0f + expf(-mbeta.add<KP>(xb)));
+    const float decay = expf(sa * logf(1.0f + expf(malpha.add<KP>(xal) + dtb)));
     __syncthreads();
     // 2. L2 normalise (deltanet.rs:25-31, 461-467): x *= 1/sqrt(sum x^2 + 1e-12); q *= 1/sqrt(dk)
     if (t < kDk) {
@@ -261,11 +287,10 @@ __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
         qn[t] = (qn[t] * inv) * scale;
     } else {
         const float inv = 1.0f / sqrtf((red[2] + red[3]) + 1e-12f);
-        kn[t - kDk] = kn[t - kDk] * inv;
+        kn[e] = kn[e] * inv;
     }
     __syncthreads();
 
-    const float beta = misc[0], decay = misc[1];
     // 3. S' = decay * S, partial recall sum_i S'_ij k_i over this thread's rows
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -318,8 +343,8 @@ __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
     __syncthreads();
     if (t >= kDk) return;
     const float inv_rms = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + eps);
-    const float gt = mix.at(b, gate_off + h * kDk + t);
-    const float v = ((o * inv_rms) * norm_w[t]) * (gt / (1.0f + expf(-gt)));
+    const float gt = mix.add<KP>(xg);
+    const float v = ((o * inv_rms) * nw) * (gt / (1.0f + expf(-gt)));
     const size_t xo = xf_index(b, h * kDk + t);
     const _Float16 hi = (_Float16)v;
     out_hi[xo] = hi;
@@ -333,8 +358,19 @@ int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
                          const float *dt_bias, float *conv_state, float *S, float *out, int gate_off,
                          const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo) {
     if (!out && !out_hi) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_head: no output");
-    hipLaunchKernelGGL(deltanet_head_kernel, dim3(n_heads, batch), dim3(kThreads), 0, stream, mix, beta, alpha, conv_w,
-                       ssm_a, dt_bias, conv_state, S, out, gate_off, norm_w, eps, out_hi, out_lo, n_heads);
+    const int kp = max(mix.kp, max(beta.kp, alpha.kp));
+    if (kp > 16) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_head: %d K splits (at most 16)", kp);
+    const dim3 grid(n_heads, batch), block(kThreads);
+#define DN_HEAD(KP)                                                                                                  \
+    hipLaunchKernelGGL(deltanet_head_kernel<KP>, grid, block, 0, stream, mix, beta, alpha, conv_w, ssm_a, dt_bias,   \
+                       conv_state, S, out, gate_off, norm_w, eps, out_hi, out_lo, n_heads)
+    if (kp <= 1)
+        DN_HEAD(1);
+    else if (kp <= 4)
+        DN_HEAD(4);
+    else
+        DN_HEAD(16);
+#undef DN_HEAD
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
