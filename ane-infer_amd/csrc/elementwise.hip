@@ -182,6 +182,56 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restr
     }
 }
 
+// The same for F % 4 == 0: one float4 of gate and of up per thread, with all
+// KP (>= ksplit) slices loaded before any is added (slices past ksplit re-read
+// the last one and are not added), so the row costs one memory round trip.
+template <int KP>
+__global__ __launch_bounds__(kThreads) void silu_mul_v4(const float *__restrict__ gu, int ksplit, int rows,
+                                                        float *__restrict__ h, int F, _Float16 *__restrict__ hi,
+                                                        _Float16 *__restrict__ lo) {
+    const int b = blockIdx.y;
+    const int r = 4 * (blockIdx.x * kThreads + threadIdx.x);
+    if (r >= F) return;
+    const size_t split = (size_t)rows * 2 * F;
+    const float *g0 = gu + (size_t)b * 2 * F + r;
+    float4 gv[KP], uv[KP];
+#pragma unroll
+    for (int k = 0; k < KP; k++) {
+        const size_t o = (size_t)min(k, ksplit - 1) * split;
+        gv[k] = *reinterpret_cast<const float4 *>(g0 + o);
+        uv[k] = *reinterpret_cast<const float4 *>(g0 + F + o);
+    }
+    float g[4] = {gv[0].x, gv[0].y, gv[0].z, gv[0].w}, u[4] = {uv[0].x, uv[0].y, uv[0].z, uv[0].w};
+#pragma unroll
+    for (int k = 1; k < KP; k++) {
+        const bool on = k < ksplit;
+        const float ga[4] = {gv[k].x, gv[k].y, gv[k].z, gv[k].w}, ua[4] = {uv[k].x, uv[k].y, uv[k].z, uv[k].w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            g[c] = on ? g[c] + ga[c] : g[c];
+            u[c] = on ? u[c] + ua[c] : u[c];
+        }
+    }
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = (g[c] / (1.0f + expf(-g[c]))) * u[c];
+    if (hi) {
+        // columns r .. r + 3 (r % 4 == 0) are consecutive in a fragment-order plane
+        typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+        h4v vh, vl;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            vh[c] = (_Float16)v[c];
+            vl[c] = (_Float16)(v[c] - (float)vh[c]);
+        }
+        const size_t o = xf_index(b, r);
+        *reinterpret_cast<h4v *>(hi + o) = vh;
+        *reinterpret_cast<h4v *>(lo + o) = vl;
+    } else {
+        *reinterpret_cast<float4 *>(h + (size_t)b * F + r) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
 // a[i] = silu(a[i]) * b[i]   (elementwise entry point)
 __global__ __launch_bounds__(kThreads) void silu_mul_plain_kernel(float *__restrict__ a, const float *__restrict__ b,
                                                                   size_t n) {
@@ -315,8 +365,18 @@ int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, flo
 
 int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit, float *h,
                             _Float16 *hi, _Float16 *lo) {
-    hipLaunchKernelGGL(silu_mul_kernel, dim3((F + kThreads - 1) / kThreads, rows), dim3(kThreads), 0, s, gu, ksplit,
-                       rows, h, F, hi, lo);
+    if (F % 4 == 0 && ksplit >= 1 && ksplit <= 16) {
+        const dim3 grid((F / 4 + kThreads - 1) / kThreads, rows);
+        if (ksplit == 1)
+            hipLaunchKernelGGL(silu_mul_v4<1>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, hi, lo);
+        else if (ksplit <= 4)
+            hipLaunchKernelGGL(silu_mul_v4<4>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, hi, lo);
+        else
+            hipLaunchKernelGGL(silu_mul_v4<16>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, hi, lo);
+    } else {
+        hipLaunchKernelGGL(silu_mul_kernel, dim3((F + kThreads - 1) / kThreads, rows), dim3(kThreads), 0, s, gu,
+                           ksplit, rows, h, F, hi, lo);
+    }
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

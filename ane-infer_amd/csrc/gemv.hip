@@ -895,9 +895,16 @@ __device__ __forceinline__ void gemm_mma(const GemmUnit<T, TV> &u, int quarter, 
 // l % 32 + 32 (r / 16)); then each of the 256 threads adds the 4 quarters of
 // two 4-row vectors of one batch row and stores them with 16-byte buffer
 // stores (rows outside the batch or the matrix, or store == false, take an
-// offset past the buffer and are dropped).  red: [4][32][64] floats.
+// offset past the buffer and are dropped).  red: [4][32][64] floats.  CPOL:
+// the stores' cache-policy bits.
 constexpr int kBadOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
+// Cache-policy bit sc1 (device scope): the store is written through to the
+// point of coherence of all XCDs.  For the K-split partials, which a later
+// kernel reads once, this measured 2 % faster over a batch-32 decode step
+// (non-temporal stores: 2 % slower).
+constexpr int kCpolDevice = 16;
 
+template <int CPOL = 0>
 __device__ __forceinline__ void gemm_tile_epilogue(float (*red)[32][kWave], const f32x16 &acc0, const f32x16 &acc1,
                                                    int quarter, int lane, int tile, int ks, int batch, int m,
                                                    size_t split_stride, __amdgpu_buffer_rsrc_t orsrc, bool store) {
@@ -922,7 +929,7 @@ __device__ __forceinline__ void gemm_tile_epilogue(float (*red)[32][kWave], cons
         }
         const int row = tile * kWave + 4 * j;
         const int off = store && b < batch && row < m ? 4 * (ks * (int)split_stride + b * m + row) : kBadOffset;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0, CPOL);
     }
     lds_barrier();  // red is free again
 }
@@ -1129,7 +1136,8 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
         for (int p = 0; p < P; p++) mma_tile<T>(u[p].q, u[p].sc, xa[p], xb[p], acc0, acc1);
         asm volatile("" : "+v"(acc0), "+v"(acc1)::"memory");
         load_tile(u);
-        gemm_tile_epilogue(red, acc0, acc1, quarter, lane, ct, ks, batch, m, split_stride, orsrc, ct < tiles);
+        gemm_tile_epilogue<kCpolDevice>(red, acc0, acc1, quarter, lane, ct, ks, batch, m, split_stride, orsrc,
+                                        ct < tiles);
         ct += gs;
     };
     do {

@@ -60,6 +60,36 @@ def test_batch_is_independent_sequences(small_host):
     gm.close()
 
 
+# A model whose batch > 1 projections all run on the x-stationary GEMM with
+# K splits (the small model's 256-wide matrices take a single split).
+MID = dict(dim=512, hidden_dim=1024, n_layers=4, n_heads=4, n_kv_heads=1, head_dim=256, vocab_size=1000,
+           ssm_state_size=128, ssm_conv_kernel=4, ssm_group_count=4)
+
+
+@pytest.fixture(scope="module")
+def mid_host():
+    return HostModel(anehip.Spec(**MID), seed=5)
+
+
+@pytest.mark.parametrize("B", [2, 7, 32])
+def test_mid_model_batched_steps(mid_host, B):
+    """Every sequence of a batched step vs the oracle over 4 steps (graph
+    replays), on the mid-size model: K-split partial sums of 2 and 4 splits
+    read by the DeltaNet / attention kernels, SiLU-mul and residual RMSNorm."""
+    steps = 4
+    toks = oracle.randint(21, B, steps * B, mid_host.spec.vocab_size).reshape(steps, B)
+    gm = _model(mid_host, B, 32)
+    seqs = [mid_host.seq(32) for _ in range(B)]
+    for step in range(steps):
+        g = gm.step(toks[step])
+        for b in range(B):
+            l2, mx = rel_errs(g[b], seqs[b].forward(int(toks[step, b])))
+            assert l2 <= TOL and mx <= TOL, (step, b, l2, mx)
+    gm.close()
+    for q in seqs:
+        q.close()
+
+
 def test_graph_replay_matches_eager_bits(small_host):
     toks = oracle.randint(7, 3, 6, small_host.spec.vocab_size)
     outs = []
