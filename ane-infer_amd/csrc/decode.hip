@@ -355,17 +355,15 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         prev_part = M->p0;
         prev_kp = k5;
     }
-    // lm_head, input = final RMSNorm(residual + last FFN output)
+    // lm_head, input = final RMSNorm(residual + last FFN output), formed once
+    // by its own kernel: as a prologue each of the lm_head's ~1200 workgroups
+    // would re-read the residual and every partial slice (measured 19 us)
+    TRY(launch_residual_rmsnorm(ctx, s, 1, (int)d, cur, prev_part, prev_kp, M->final_norm, M->heads, eps, nullptr,
+                                nullptr));
     GemvInput inf;
-    inf.mode = GEMV_IN_RESID_RMSNORM;
-    inf.x = cur;
-    inf.part = prev_part;
-    inf.kp = prev_kp;
-    inf.part_stride = d;
-    inf.w = M->final_norm;
-    inf.eps = eps;
-    inf.x_out = nxt;
-    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d, true);
+    inf.mode = GEMV_IN_PLAIN;
+    inf.x = M->heads;
+    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d, false);
     if (kf == 1) {
         TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->logits, 1));
     } else {
@@ -449,7 +447,7 @@ size_t part_floats(anehip_ctx *ctx, Model *M) {
         uint32_t m, n;
         bool norm;
     } g[] = {{M->rows_dn, d, true}, {M->rows_attn, d, true}, {d, d, false}, {d, D.n_heads * D.head_dim, false},
-             {2 * F, d, true}, {d, F, false}, {D.vocab_size, d, true}};
+             {2 * F, d, true}, {d, F, false}, {D.vocab_size, d, false}};
     size_t mx = 0;
     for (auto &e : g) {
         if (!e.m) continue;

@@ -34,22 +34,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float silu_ref(float x) { return x / (1.0f + expf(-x)); }
 
-// conv_shift_and_append + conv_apply (deltanet_cache.rs:34-54) for one channel;
-// returns the conv output before SiLU, updates the window if `write`.
-__device__ __forceinline__ float conv_channel(float *__restrict__ state, const float *__restrict__ w, float x,
-                                              bool write) {
-    float4 s = *reinterpret_cast<const float4 *>(state);
-    float4 k = *reinterpret_cast<const float4 *>(w);
-    float4 ns = make_float4(s.y, s.z, s.w, x);
-    float sum = 0.0f;
-    sum += ns.x * k.x;
-    sum += ns.y * k.y;
-    sum += ns.z * k.z;
-    sum += ns.w * k.w;
-    if (write) *reinterpret_cast<float4 *>(state) = ns;
-    return sum;
-}
-
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -58,7 +42,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // grid = (dv / 32, n_heads, batch).  mix / mbeta / malpha: the qkv, beta and
 // alpha projections of each sequence ([3 chunk], [n_heads], [n_heads]), read
-// as K-split partial slices.
+// as K-split partial slices (KP >= their number).
+template <int KP>
 __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
     MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
     const float *__restrict__ dt_bias, float *__restrict__ conv_state, float *__restrict__ S, float *__restrict__ out,
@@ -66,7 +51,6 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
     __shared__ float qn[kDk], kn[kDk], vv[kCols];
     __shared__ float red[1][4];
     __shared__ float part[32][kCols];
-    __shared__ float misc[2];  // beta, decay
 
     const int t = threadIdx.x;
     const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -75,20 +59,49 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
     const int c0 = slice * kCols;
     float *cs = conv_state + (size_t)b * C * kKsize;
 
-    // the state slice is loaded first: its memory latency overlaps steps 1-2
-    // (thread -> 4 columns (cq) x 4 rows (rg))
+    // Every small input is loaded first and the state slice after it (vector
+    // loads complete in order, so the conv and norms wait only for the small
+    // loads while the state is in flight).  Thread t convolves the head's q
+    // (t < 128) or k channel, and t < 32 also v channel c0 + t.
+    const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + (t - kDk);
+    const int chv = 2 * chunk + h * kDk + c0 + (t & (kCols - 1));
+    f32x4 win = *reinterpret_cast<const f32x4 *>(cs + (size_t)ch * kKsize);
+    f32x4 wk = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)ch * kKsize);
+    f32x4 winv = *reinterpret_cast<const f32x4 *>(cs + (size_t)chv * kKsize);
+    f32x4 wkv = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)chv * kKsize);
+    float xa[KP], xv[KP], xb[KP], xal[KP];
+    mix.load<KP>(b, ch, xa);
+    mix.load<KP>(b, chv, xv);
+    mbeta.load<KP>(b, h, xb);
+    malpha.load<KP>(b, h, xal);
+    const float sa = ssm_a[h], dtb = dt_bias[h];
+    asm volatile("" ::: "memory");  // keeps the state loads behind the small ones
+    // state slice: thread -> 4 columns (cq) x 4 rows (rg)
     const int cq = t & 7;          // column quad: columns c0 + 4cq .. +3
     const int rg = t >> 3;         // row group: rows 4rg .. 4rg+3
     float *Sh = S + (((size_t)b * n_heads + h) * kDk) * kDk + c0 + 4 * cq;
     float4 s[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(4 * rg + r) * kDk);
+    // the arithmetic on the small inputs starts after the state loads were
+    // issued (else it is scheduled above them, with its waits)
+    asm volatile("" : "+v"(win), "+v"(wk), "+v"(winv), "+v"(wkv)::"memory");
+#pragma unroll
+    for (int q = 0; q < KP; q++) asm volatile("" : "+v"(xa[q]), "+v"(xv[q]), "+v"(xb[q]), "+v"(xal[q]));
 
-    // 1. conv + SiLU of the head's q (t < 128) and k (t >= 128) channels, from
-    // the old window (committed later by dn_finish / the ssm_out GEMV)
+    // 1. conv + SiLU (conv_shift_and_append + conv_apply, deltanet_cache.rs:
+    // 34-54) of q / k from the old window (committed later by dn_finish / the
+    // ssm_out GEMV) and of v (committed here)
+    const auto conv = [](f32x4 w0, f32x4 k, float x) {
+        float sum = 0.0f;
+        sum += w0.y * k.x;
+        sum += w0.z * k.y;
+        sum += w0.w * k.z;
+        sum += x * k.w;
+        return silu_ref(sum);
+    };
     {
-        const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + (t - kDk);
-        float y = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, mix.at(b, ch), false));
+        const float y = conv(win, wk, mix.add<KP>(xa));
         // sum of squares per half (waves 0-1: q, waves 2-3: k)
         float sq = wave_sum(y * y);
         if ((t & 63) == 0) red[0][t >> 6] = sq;
@@ -96,17 +109,13 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
         else kn[t - kDk] = y;
     }
     if (t < kCols) {
-        const int ch = 2 * chunk + h * kDk + c0 + t;
-        vv[t] = silu_ref(conv_channel(cs + (size_t)ch * kKsize, conv_w + (size_t)ch * kKsize, mix.at(b, ch), true));
+        const float x = mix.add<KP>(xv);
+        vv[t] = conv(winv, wkv, x);
+        *reinterpret_cast<float4 *>(cs + (size_t)chv * kKsize) = make_float4(winv.y, winv.z, winv.w, x);
     }
-    if (t == 0) {
-        // deltanet.rs:474-480
-        const float br = mbeta.at(b, h);
-        const float ar = malpha.at(b, h);
-        misc[0] = 1.0f / (1.0f + expf(-br));
-        const float g = ssm_a[h] * logf(1.0f + expf(ar + dt_bias[h]));
-        misc[1] = expf(g);
-    }
+    // deltanet.rs:474-480, by every thread (no shared copy needed)
+    const float beta = 1.0f / (1.0f + expf(-mbeta.add<KP>(xb)));
+    const float decay = expf(sa * logf(1.0f + expf(malpha.add<KP>(xal) + dtb)));
     __syncthreads();
     // 2. L2 normalise (deltanet.rs:25-31, 461-467): x *= 1/sqrt(sum x^2 + 1e-12); q *= 1/sqrt(dk)
     if (t < kDk) {
@@ -119,7 +128,6 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
     }
     __syncthreads();
 
-    const float beta = misc[0], decay = misc[1];
     // 3. S' = decay * S, partial recall sum_i S'_ij k_i over this thread's rows
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -378,8 +386,19 @@ int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
 int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *out) {
-    hipLaunchKernelGGL(deltanet_step_kernel, dim3(kDk / kCols, n_heads, batch), dim3(kThreads), 0, stream, mix,
-                       beta, alpha, conv_w, ssm_a, dt_bias, conv_state, S, out, n_heads);
+    const int kp = max(mix.kp, max(beta.kp, alpha.kp));
+    if (kp > 16) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_step: %d K splits (at most 16)", kp);
+    const dim3 grid(kDk / kCols, n_heads, batch), block(kThreads);
+#define DN_STEP(KP)                                                                                                  \
+    hipLaunchKernelGGL(deltanet_step_kernel<KP>, grid, block, 0, stream, mix, beta, alpha, conv_w, ssm_a, dt_bias,   \
+                       conv_state, S, out, n_heads)
+    if (kp <= 1)
+        DN_STEP(1);
+    else if (kp <= 4)
+        DN_STEP(4);
+    else
+        DN_STEP(16);
+#undef DN_STEP
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
