@@ -52,7 +52,8 @@ def build(verbose: bool = False) -> str:
 def build_engine(verbose: bool = False) -> str:
     tmp = ENGINE_LIB + ".tmp"
     cmd = [os.environ.get("CXX", "g++"), "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
-           f"-I{INCLUDE}", os.path.join(HERE, "engine", "ane_engine.cpp"), f"-L{HERE}", "-lanehip",
+           f"-I{INCLUDE}", os.path.join(HERE, "engine", "ane_engine.cpp"), os.path.join(HERE, "engine", "gguf.cpp"),
+           f"-L{HERE}", "-lanehip",
            "-Wl,-rpath,$ORIGIN", "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)

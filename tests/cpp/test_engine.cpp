@@ -6,9 +6,18 @@
 // plus the SiLU-mul graph op, graph replays over new inputs, the from_raw
 // shape checks, and encode_full_token_gpu on a tiny seeded hybrid model
 // against the CPU oracle (test infrastructure, oracle/ane_oracle.h).
+// The GGUF reader (engine/gguf.hpp, mirroring crates/gguf) is checked on
+// files written here by a small GGUF writer: metadata of every value type,
+// tensor offsets and alignment, the reference's dequant known answers
+// (dequant.rs:235-270), malformed files, and the tiny model loaded from its
+// GGUF file (load_qwen35_q8) decoding bit-identically to the same weights
+// uploaded directly.
 // Prints one line per test; exit status 0 iff all pass.
+#include <unistd.h>
+
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <string>
@@ -16,6 +25,7 @@
 
 #include "ane_engine.hpp"
 #include "ane_oracle.h"
+#include "gguf.hpp"
 
 using namespace ane;
 
@@ -193,6 +203,154 @@ static Tiny make_tiny() {
     return t;
 }
 
+// ---- a GGUF v3 writer (test infrastructure) ------------------------------------
+
+struct GgufWriter {
+    std::vector<uint8_t> kv;
+    uint64_t n_kv = 0;
+    struct T {
+        std::string name;
+        std::vector<uint64_t> dims;
+        uint32_t type;
+        std::vector<uint8_t> data;
+    };
+    std::vector<T> tensors;
+    template <typename V> static void put(std::vector<uint8_t> &b, V v) {
+        const uint8_t *p = reinterpret_cast<const uint8_t *>(&v);
+        b.insert(b.end(), p, p + sizeof(V));
+    }
+    static void put_str(std::vector<uint8_t> &b, const std::string &x) {
+        put<uint64_t>(b, x.size());
+        b.insert(b.end(), x.begin(), x.end());
+    }
+    void key(const std::string &k, uint32_t type) {
+        put_str(kv, k);
+        put<uint32_t>(kv, type);
+        n_kv++;
+    }
+    void u32(const std::string &k, uint32_t v) { key(k, 4), put(kv, v); }
+    void f32(const std::string &k, float v) { key(k, 6), put(kv, v); }
+    void str(const std::string &k, const std::string &v) { key(k, 8), put_str(kv, v); }
+    void str_array(const std::string &k, const std::vector<std::string> &v) {
+        key(k, 9);
+        put<uint32_t>(kv, 8);
+        put<uint64_t>(kv, v.size());
+        for (const auto &x : v) put_str(kv, x);
+    }
+    void tensor(const std::string &name, std::vector<uint64_t> dims, uint32_t type, std::vector<uint8_t> data) {
+        tensors.push_back(T{name, std::move(dims), type, std::move(data)});
+    }
+    void f32_tensor(const std::string &name, std::vector<uint64_t> dims, const std::vector<float> &v) {
+        std::vector<uint8_t> b(v.size() * 4);
+        std::memcpy(b.data(), v.data(), b.size());
+        tensor(name, std::move(dims), 0, std::move(b));
+    }
+    void quant_tensor(const std::string &name, const Q8Tensor &q) {
+        tensor(name, {q.n, q.m}, (uint32_t)q.quant_type, q.data);
+    }
+    std::vector<uint8_t> bytes(uint64_t align = 32) const {
+        std::vector<uint8_t> b;
+        put<uint32_t>(b, 0x46554747u);
+        put<uint32_t>(b, 3);
+        put<uint64_t>(b, tensors.size());
+        put<uint64_t>(b, n_kv);
+        b.insert(b.end(), kv.begin(), kv.end());
+        uint64_t off = 0;
+        std::vector<uint64_t> offs;
+        for (const T &t : tensors) {
+            put_str(b, t.name);
+            put<uint32_t>(b, (uint32_t)t.dims.size());
+            for (uint64_t d : t.dims) put<uint64_t>(b, d);
+            put<uint32_t>(b, t.type);
+            put<uint64_t>(b, off);
+            offs.push_back(off);
+            off = (off + t.data.size() + align - 1) / align * align;
+        }
+        b.resize((b.size() + align - 1) / align * align, 0);
+        const size_t base = b.size();
+        b.resize(base + off, 0);
+        for (size_t i = 0; i < tensors.size(); i++)
+            std::memcpy(&b[base + offs[i]], tensors[i].data.data(), tensors[i].data.size());
+        return b;
+    }
+};
+
+// The tiny model's tensors under the checkpoint names load_qwen35_q8 reads
+// (crates/gguf/src/to_ane.rs:129-163, crates/cli/src/main.rs:1894-1994).
+static std::vector<uint8_t> tiny_gguf(const Tiny &t, bool tied_lm_head) {
+    GgufWriter w;
+    const ModelConfig &b = t.w.config.base;
+    w.str("general.architecture", "qwen35");
+    w.u32("general.alignment", 64);
+    w.u32("qwen35.embedding_length", (uint32_t)b.dim);
+    w.u32("qwen35.attention.head_count", (uint32_t)b.n_heads);
+    w.u32("qwen35.attention.head_count_kv", (uint32_t)b.n_kv_heads);
+    w.u32("qwen35.block_count", (uint32_t)b.n_layers);
+    w.u32("qwen35.feed_forward_length", (uint32_t)b.hidden_dim);
+    w.u32("qwen35.context_length", (uint32_t)b.max_seq_len);
+    w.u32("qwen35.attention.key_length", (uint32_t)b.head_dim);
+    w.f32("qwen35.rope.freq_base", b.rope_freq_base);
+    w.f32("qwen35.attention.layer_norm_rms_epsilon", b.rms_norm_eps);
+    w.u32("qwen35.full_attention_interval", 4);
+    w.u32("qwen35.ssm.state_size", (uint32_t)t.w.config.ssm_state_size);
+    w.u32("qwen35.ssm.conv_kernel", (uint32_t)t.w.config.ssm_conv_kernel);
+    w.u32("qwen35.ssm.group_count", (uint32_t)t.w.config.ssm_group_count);
+    w.u32("qwen35.ssm.inner_size", (uint32_t)t.w.config.ssm_inner_size);
+    std::vector<std::string> vocab(b.vocab_size);
+    for (size_t i = 0; i < vocab.size(); i++) vocab[i] = "tok" + std::to_string(i);
+    w.str_array("tokenizer.ggml.tokens", vocab);
+    const uint64_t d = b.dim;
+    if (tied_lm_head)  // the embedding stored quantised and read back as fp32 (dequantised)
+        w.quant_tensor("token_embd.weight", t.w.lm_head);
+    else
+        w.f32_tensor("token_embd.weight", {d, b.vocab_size}, t.w.embedding);
+    w.f32_tensor("output_norm.weight", {d}, t.w.final_norm);
+    if (!tied_lm_head) w.quant_tensor("output.weight", t.w.lm_head);
+    for (size_t l = 0; l < b.n_layers; l++) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        auto ffn = [&](const FfnWeights &f) {
+            w.quant_tensor(p + "ffn_gate.weight", f.gate);
+            w.quant_tensor(p + "ffn_up.weight", f.up);
+            w.quant_tensor(p + "ffn_down.weight", f.down);
+        };
+        if (const auto *x = std::get_if<DeltaNetLayerWeights>(&t.w.layers[l])) {
+            w.f32_tensor(p + "attn_norm.weight", {d}, x->attn_norm);
+            w.f32_tensor(p + "post_attention_norm.weight", {d}, x->post_attn_norm);
+            w.quant_tensor(p + "attn_qkv.weight", x->qkv);
+            w.quant_tensor(p + "attn_gate.weight", x->attn_gate);
+            w.f32_tensor(p + "ssm_a", {x->ssm_a.size()}, x->ssm_a);
+            w.quant_tensor(p + "ssm_alpha.weight", x->ssm_alpha);
+            w.quant_tensor(p + "ssm_beta.weight", x->ssm_beta);
+            w.f32_tensor(p + "ssm_conv1d.weight", {4, x->ssm_conv1d.size() / 4}, x->ssm_conv1d);
+            w.f32_tensor(p + "ssm_dt.bias", {x->ssm_dt_bias.size()}, x->ssm_dt_bias);
+            w.f32_tensor(p + "ssm_norm.weight", {x->ssm_norm.size()}, x->ssm_norm);
+            w.quant_tensor(p + "ssm_out.weight", x->ssm_out);
+            ffn(x->ffn);
+        } else {
+            const auto &a = std::get<FullAttnLayerWeights>(t.w.layers[l]);
+            w.f32_tensor(p + "attn_norm.weight", {d}, a.attn_norm);
+            w.f32_tensor(p + "post_attention_norm.weight", {d}, a.post_attn_norm);
+            w.quant_tensor(p + "attn_q.weight", a.wq);
+            w.quant_tensor(p + "attn_k.weight", a.wk);
+            w.quant_tensor(p + "attn_v.weight", a.wv);
+            w.quant_tensor(p + "attn_output.weight", a.wo);
+            w.f32_tensor(p + "attn_q_norm.weight", {a.q_norm.size()}, a.q_norm);
+            w.f32_tensor(p + "attn_k_norm.weight", {a.k_norm.size()}, a.k_norm);
+            ffn(a.ffn);
+        }
+    }
+    return w.bytes(64);
+}
+
+static bool throws_code(const std::function<void()> &fn, int code) {
+    try {
+        fn();
+    } catch (const Error &e) {
+        return e.code == code;
+    }
+    return false;
+}
+
 int main(int argc, char **argv) {
     const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu-only") == 0;
     run("test_from_raw_checks_sizes", [] {
@@ -222,6 +380,139 @@ int main(int argc, char **argv) {
         std::vector<float> r = normal(5, 1000, 0.f, 1.f);
         EXPECT(greedy_sample(r) == ao_argmax(r.data(), r.size()), "random logits");
     });
+    run("test_gguf_metadata_and_tensors", [] {
+        GgufWriter w;
+        w.str("general.architecture", "qwen35");
+        w.u32("qwen35.block_count", 7);
+        w.f32("qwen35.rope.freq_base", 1e6f);
+        w.str_array("tokenizer.ggml.tokens", {"a", "bb", "ccc"});
+        // other value types: u8, i16, i64, f64, bool, an array of u32
+        w.key("x.u8", 0), GgufWriter::put<uint8_t>(w.kv, 200);
+        w.key("x.i16", 3), GgufWriter::put<int16_t>(w.kv, -300);
+        w.key("x.i64", 11), GgufWriter::put<int64_t>(w.kv, -5);
+        w.key("x.f64", 12), GgufWriter::put<double>(w.kv, 0.25);
+        w.key("x.bool", 7), GgufWriter::put<uint8_t>(w.kv, 1);
+        w.key("x.arr", 9), GgufWriter::put<uint32_t>(w.kv, 4), GgufWriter::put<uint64_t>(w.kv, 2),
+            GgufWriter::put<uint32_t>(w.kv, 10), GgufWriter::put<uint32_t>(w.kv, 20);
+        const std::vector<float> a = {1.f, -2.f, 3.5f};
+        w.f32_tensor("a", {3}, a);
+        w.tensor("h", {4}, 1, {0x00, 0x3c, 0x00, 0xc0, 0x01, 0x00, 0x00, 0x7c});  // 1, -2, 2^-24, +inf
+        const std::vector<uint8_t> f = w.bytes(32);
+        gguf::GgufFile g = gguf::GgufFile::parse(f.data(), f.size());
+        EXPECT(g.version == 3 && g.tensors.size() == 2 && g.metadata.size() == 10, "header");
+        EXPECT(g.architecture() && *g.architecture() == "qwen35", "architecture");
+        uint32_t v = 0;
+        float x = 0;
+        EXPECT(g.arch_u32("block_count", v) && v == 7, "block_count %u", v);
+        EXPECT(g.arch_f32("rope.freq_base", x) && x == 1e6f, "freq_base");
+        EXPECT(!g.arch_u32("rope.freq_base", v), "an f32 key is not a u32 (as_u32 matches the type only)");
+        EXPECT(g.vocab_size(v) && v == 3, "vocab %u", v);
+        EXPECT(std::get<uint64_t>(g.metadata["x.u8"].v) == 200 && std::get<int64_t>(g.metadata["x.i16"].v) == -300 &&
+                   std::get<int64_t>(g.metadata["x.i64"].v) == -5 && std::get<double>(g.metadata["x.f64"].v) == 0.25 &&
+                   std::get<bool>(g.metadata["x.bool"].v) && g.metadata["x.arr"].as_array()->size() == 2,
+               "value types");
+        EXPECT((g.tensor_data_offset & 31) == 0 && g.get_tensor("h")->offset == 32, "alignment / offsets");
+        EXPECT(gguf::extract_tensor_f32(g, f.data(), f.size(), "a") == a, "f32 tensor");
+        const std::vector<float> h = gguf::extract_tensor_f32(g, f.data(), f.size(), "h");
+        EXPECT(h[0] == 1.f && h[1] == -2.f && h[2] == std::ldexp(1.f, -24) && std::isinf(h[3]), "f16 tensor");
+        EXPECT(!g.get_tensor("missing") &&
+                   throws_code([&] { gguf::extract_tensor_f32(g, f.data(), f.size(), "missing"); }, ANEHIP_EINVAL),
+               "a missing tensor is an error");
+    });
+
+    // dequant.rs:235-270 (the reference's only dequant known answers), and the
+    // Q4_0 nibble order: byte 0x1F -> element i = (15 - 8) d, element i + 16 = (1 - 8) d
+    run("test_gguf_dequant_known_answers", [] {
+        std::vector<uint8_t> q8(34, 2);
+        q8[0] = 0x00, q8[1] = 0x38;  // 0.5
+        for (float v : gguf::dequantize_tensor(q8.data(), q8.size(), gguf::GgmlType::Q8_0, 32))
+            EXPECT(v == 1.0f, "q8 %f", v);
+        std::vector<uint8_t> q4(18, 0x88);
+        q4[0] = 0x00, q4[1] = 0x3c;  // 1.0
+        for (float v : gguf::dequantize_tensor(q4.data(), q4.size(), gguf::GgmlType::Q4_0, 32))
+            EXPECT(v == 0.0f, "q4 %f", v);
+        q4[2] = 0x1f;
+        const std::vector<float> o = gguf::dequantize_tensor(q4.data(), q4.size(), gguf::GgmlType::Q4_0, 32);
+        EXPECT(o[0] == 7.0f && o[16] == -7.0f, "nibble order %f %f", o[0], o[16]);
+        // matches the oracle's block dequant on random blocks
+        std::vector<uint8_t> r(ao_quant_bytes(8, 4, 64));
+        ao_gen_quant(8, 3, 1, 0.02f, 4, 64, r.data());
+        const std::vector<float> got = gguf::dequantize_tensor(r.data(), r.size(), gguf::GgmlType::Q8_0, 256);
+        for (size_t b = 0; b < 8; b++) {
+            float ref[32];
+            ao_dequant_q8_0_block(&r[b * 34], ref);
+            for (int i = 0; i < 32; i++) EXPECT(got[b * 32 + i] == ref[i], "block %zu elem %d", b, i);
+        }
+        EXPECT(throws_code([&] { gguf::dequantize_tensor(r.data(), r.size(), gguf::GgmlType::Q6K, 256); },
+                           ANEHIP_EUNSUPPORTED) &&
+                   throws_code([&] { gguf::dequantize_tensor(r.data(), 10, gguf::GgmlType::Q8_0, 256); }, ANEHIP_EINVAL),
+               "unsupported type / short data");
+    });
+
+    run("test_gguf_rejects_malformed_files", [] {
+        GgufWriter w;
+        w.u32("general.alignment", 32);
+        w.f32_tensor("a", {3}, {1.f, 2.f, 3.f});
+        const std::vector<uint8_t> good = w.bytes();
+        auto parse = [](std::vector<uint8_t> b) { gguf::GgufFile::parse(b.data(), b.size()); };
+        std::vector<uint8_t> b = good;
+        b[0] = 'X';
+        EXPECT(throws_code([&] { parse(b); }, ANEHIP_EINVAL), "bad magic");
+        b = good;
+        b[4] = 1;
+        EXPECT(throws_code([&] { parse(b); }, ANEHIP_EINVAL), "version 1");
+        EXPECT(throws_code([&] { parse(std::vector<uint8_t>(good.begin(), good.begin() + 40)); }, ANEHIP_EINVAL),
+               "truncated");
+        GgufWriter u;
+        u.key("k", 13);  // unknown value type
+        EXPECT(throws_code([&] { parse(u.bytes()); }, ANEHIP_EINVAL), "unknown metadata type");
+        GgufWriter t;
+        t.tensor("q", {32}, 20, std::vector<uint8_t>(34));  // IQ4_NL: not a type the parser maps
+        EXPECT(throws_code([&] { parse(t.bytes()); }, ANEHIP_EUNSUPPORTED), "unsupported tensor type");
+        // a tensor whose data lies past the end of the file
+        std::vector<uint8_t> cut = good;
+        cut.resize(gguf::GgufFile::parse(good.data(), good.size()).tensor_data_offset + 4);
+        gguf::GgufFile g = gguf::GgufFile::parse(cut.data(), cut.size());
+        EXPECT(throws_code([&] { gguf::extract_tensor_f32(g, cut.data(), cut.size(), "a"); }, ANEHIP_EINVAL),
+               "tensor past the end");
+    });
+
+    run("test_gguf_config_and_weights_of_the_tiny_model", [] {
+        Tiny t = make_tiny();
+        for (bool tied : {false, true}) {
+            const std::vector<uint8_t> f = tiny_gguf(t, tied);
+            // through a mapped file, as a checkpoint is read
+            char path[] = "/tmp/ane_gguf_XXXXXX";
+            const int fd = mkstemp(path);
+            EXPECT(fd >= 0, "mkstemp");
+            EXPECT(write(fd, f.data(), f.size()) == (ssize_t)f.size(), "write");
+            close(fd);
+            gguf::MappedFile mf(path);
+            unlink(path);
+            gguf::GgufFile g = gguf::GgufFile::parse(mf.data(), mf.size());
+            Qwen35Config c = qwen35_config_from_gguf(g);
+            const ModelConfig &b = c.base, &r = t.w.config.base;
+            EXPECT(b.dim == r.dim && b.hidden_dim == r.hidden_dim && b.n_layers == r.n_layers &&
+                       b.n_heads == r.n_heads && b.n_kv_heads == r.n_kv_heads && b.head_dim == r.head_dim &&
+                       b.vocab_size == r.vocab_size && b.max_seq_len == r.max_seq_len,
+                   "shape");
+            EXPECT(c.layer_types == t.w.config.layer_types && c.ssm_group_count == t.w.config.ssm_group_count,
+                   "layer types");
+            Qwen35ModelWeights w = load_qwen35_q8(g, mf.data(), mf.size(), c);
+            EXPECT(w.lm_head.data == t.w.lm_head.data && w.final_norm == t.w.final_norm, "model tensors");
+            if (!tied) EXPECT(w.embedding == t.w.embedding, "embedding");
+            const auto &d0 = std::get<DeltaNetLayerWeights>(w.layers[0]);
+            const auto &r0 = std::get<DeltaNetLayerWeights>(t.w.layers[0]);
+            EXPECT(d0.qkv.data == r0.qkv.data && d0.qkv.m == r0.qkv.m && d0.qkv.n == r0.qkv.n &&
+                       d0.ssm_conv1d == r0.ssm_conv1d && d0.ssm_a == r0.ssm_a && d0.ffn.down.data == r0.ffn.down.data,
+                   "DeltaNet layer");
+            const auto &a3 = std::get<FullAttnLayerWeights>(w.layers[3]);
+            const auto &r3 = std::get<FullAttnLayerWeights>(t.w.layers[3]);
+            EXPECT(a3.wq.data == r3.wq.data && a3.wo.n == r3.wo.n && a3.k_norm == r3.k_norm, "attention layer");
+        }
+        ao_model_destroy(t.om);
+    });
+
     if (cpu_only) {
         std::printf("%s (%d failed)\n", failures ? "FAILED" : "OK", failures);
         return failures ? 1 : 0;
@@ -309,6 +600,33 @@ int main(int argc, char **argv) {
             EXPECT(scratch.pos == (size_t)step + 1, "pos %zu", scratch.pos);
             tok = greedy_sample(logits);
             EXPECT(tok == ao_argmax(ref.data(), 1000), "greedy choice differs from the oracle's");
+        }
+        ao_seq_destroy(seq);
+        ao_model_destroy(t.om);
+    });
+
+    // load_qwen35_q8 from a GGUF file, uploaded and stepped: the same logits
+    // bits as the weights uploaded directly, and the oracle's within 1e-3
+    run("test_gguf_model_decodes_like_the_direct_upload", [&] {
+        Tiny t = make_tiny();
+        const std::vector<uint8_t> f = tiny_gguf(t, false);
+        gguf::GgufFile g = gguf::GgufFile::parse(f.data(), f.size());
+        Qwen35ModelWeights w = load_qwen35_q8(g, f.data(), f.size(), qwen35_config_from_gguf(g));
+        GpuModelWeights gd = upload_model_weights(ctx, t.w), gg = upload_model_weights(ctx, w);
+        GpuLayerScratch sd(256, 512, 768, 2), sg(256, 512, 768, 2);
+        GpuConstantPool pool(256, 512, 768, 2, 128, 4, 1e-6f, 4, 1, 256, 10000.f);
+        ao_seq *seq = ao_seq_create(t.om, 64, 1);
+        std::vector<float> ref(1000);
+        uint32_t tok = 5;
+        for (int step = 0; step < 4; step++) {
+            const std::vector<float> a = encode_full_token_gpu(ctx, t.w, gd, sd, pool, tok);
+            const std::vector<float> b = encode_full_token_gpu(ctx, w, gg, sg, pool, tok);
+            EXPECT(a == b, "step %d: logits differ from the direct upload", step);
+            ao_forward_token(t.om, seq, tok, ref.data(), 0);
+            double num = 0, den = 0;
+            for (size_t i = 0; i < 1000; i++) num += (b[i] - ref[i]) * (b[i] - ref[i]), den += ref[i] * ref[i];
+            EXPECT(std::sqrt(num / den) < 1e-3, "step %d rel_l2 %g", step, std::sqrt(num / den));
+            tok = greedy_sample(b);
         }
         ao_seq_destroy(seq);
         ao_model_destroy(t.om);
