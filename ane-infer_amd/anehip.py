@@ -89,6 +89,7 @@ def lib():
             "anehip_set_graph": (C.c_int, [vp, C.c_int]),
             "anehip_decode_step": (C.c_int, [vp, vp, u32, vp]),
             "anehip_decode_step_async": (C.c_int, [vp, vp, u32]),
+            "anehip_prefill": (C.c_int, [vp, u32, vp, u32, vp]),
             "anehip_logits_ptr": (C.c_int, [vp, C.POINTER(vp)]),
             "anehip_sampled_tokens": (C.c_int, [vp, vp]),
             "anehip_generate": (C.c_int, [vp, vp, u32, u32, vp]),
@@ -389,6 +390,17 @@ class Model(Context):
             self._check(lib().anehip_decode_step(self.h, tok.ctypes.data, tok.size, out.ctypes.data))
             return out
         self._check(lib().anehip_decode_step(self.h, tok.ctypes.data, tok.size, None))
+        return None
+
+    def prefill(self, seq: int, tokens, want_logits=True):
+        """Runs tokens through sequence `seq` from its position (anehip_prefill);
+        returns the last token's logits [vocab]."""
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        if want_logits:
+            out = np.empty(self.spec.vocab_size, np.float32)
+            self._check(lib().anehip_prefill(self.h, seq, tok.ctypes.data, tok.size, out.ctypes.data))
+            return out
+        self._check(lib().anehip_prefill(self.h, seq, tok.ctypes.data, tok.size, None))
         return None
 
     def step_async(self, tokens):

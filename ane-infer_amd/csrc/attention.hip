@@ -115,12 +115,17 @@ __device__ __forceinline__ void split8(const float *x, h8v &hi, h8v &lo) {
 // without a memory access (row pos takes this step's k / v), which also makes
 // the prefetch of a tile past the chunk free.  One
 // unnormalised partial per (chunk, query head) with its running max and sum.
+//
+// Cache addressing: row b's cache is at cache_off + b * row_stride halves
+// (decode: every row its own sequence; prefill: row_stride 0, every row a
+// token of one sequence whose K / V rows the prefill append kernel wrote
+// before this launch -- then `append` is false and no row is written here).
 template <int G>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     MixIn mix, const float *__restrict__ q_norm, const float *__restrict__ k_norm,
     const float *__restrict__ inv_freq, const uint32_t *__restrict__ pos_arr, __half *__restrict__ k_cache,
     __half *__restrict__ v_cache, int max_seq, int n_heads, int n_kv, int tpw, float *__restrict__ part_o,
-    float *__restrict__ part_ml) {
+    float *__restrict__ part_ml, size_t cache_off, size_t row_stride, bool append) {
     __shared__ __align__(16) _Float16 vt[kHd * kCh];  // V^T of the tile, swizzled chunks
     __shared__ __align__(16) float qs[G][kHd];
     __shared__ __align__(16) h8v qf[8][2][64];         // q B fragments: k-step, hi / lo, lane
@@ -137,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     const int tb = c * tpw, te = min(tb + tpw, (len + kCh - 1) / kCh);  // tiles [tb, te)
     if (tb >= te) return;  // uniform exit: nothing of this sequence here
     const int nch = gridDim.x;
-    const size_t cache_base = ((size_t)b * n_kv + kvh) * (size_t)max_seq * kHd;
+    const size_t cache_base = cache_off + (size_t)b * row_stride + (size_t)kvh * max_seq * kHd;
     const bool has_new = (int)pos < te * kCh;  // this chunk holds the current position
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(k_cache + cache_base, 0, (int)pos * kHd * 2, kWord3);
@@ -189,12 +194,14 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
             knew[4 * lane + i] = __float2half_rn(k4[i]);
             vnew[4 * lane + i] = __float2half_rn(vv[i]);
         }
-        __half *kd = k_cache + cache_base + (size_t)pos * kHd + 4 * lane;
-        __half *vd = v_cache + cache_base + (size_t)pos * kHd + 4 * lane;
+        if (append) {
+            __half *kd = k_cache + cache_base + (size_t)pos * kHd + 4 * lane;
+            __half *vd = v_cache + cache_base + (size_t)pos * kHd + 4 * lane;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            kd[i] = knew[4 * lane + i];
-            vd[i] = vnew[4 * lane + i];
+            for (int i = 0; i < 4; i++) {
+                kd[i] = knew[4 * lane + i];
+                vd[i] = vnew[4 * lane + i];
+            }
         }
     }
     lds_barrier();
@@ -336,6 +343,31 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     }
 }
 
+// Prefill: the k / v rows of T consecutive tokens of one sequence (row t at
+// position pos_arr[t]) -- RMSNorm + RoPE of k, both rounded to fp16 -- written
+// to the cache at cache_off, as the decode kernel appends one row.  grid =
+// (n_kv, T), one wave.
+__global__ __launch_bounds__(64) void attn_append_kernel(MixIn mix, const float *__restrict__ k_norm,
+                                                         const float *__restrict__ inv_freq,
+                                                         const uint32_t *__restrict__ pos_arr,
+                                                         __half *__restrict__ k_cache, __half *__restrict__ v_cache,
+                                                         size_t cache_off, int max_seq, int n_heads, int n_kv) {
+    const int lane = threadIdx.x, kvh = blockIdx.x, b = blockIdx.y;
+    const uint32_t pos = pos_arr[b];
+    const int kin = n_heads * 2 * kHd + kvh * kHd;
+    const int vin = n_heads * 2 * kHd + n_kv * kHd + kvh * kHd;
+    float k4[4];
+    norm_rope_head(mix, b, kin, k_norm, inv_freq, pos, lane, k4);
+    const float4 v4 = mix.at4(b, vin + 4 * lane);
+    const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+    const size_t o = cache_off + ((size_t)kvh * max_seq + pos) * kHd + 4 * lane;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        k_cache[o + i] = __float2half_rn(k4[i]);
+        v_cache[o + i] = __float2half_rn(vv[i]);
+    }
+}
+
 // grid = (n_heads, batch), 256 threads: thread (g = t / 64, l = t % 64) takes
 // dims 4l..4l+3 of chunks g, g + 4, g + 8, ...; merges them with a log-sum-exp
 // rescale against the maximum over all chunks, adds the 4 groups through
@@ -443,11 +475,12 @@ size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G) {
     return (size_t)batch * n_kv * nch * G * (kHd + 2);
 }
 
-// part: workspace of attn_partial_floats() floats.
-int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
-                     const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
-                     const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,
-                     _Float16 *out_hi, _Float16 *out_lo) {
+namespace {
+
+int attention_impl(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
+                   const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
+                   const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out, _Float16 *out_hi,
+                   _Float16 *out_lo, size_t cache_off, size_t row_stride, bool append) {
     const int G = n_heads / n_kv;
     const int tpw = tiles_per_chunk(max_seq, batch, n_kv);
     const int nch = ((max_seq + kCh - 1) / kCh + tpw - 1) / tpw;
@@ -459,7 +492,8 @@ int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
 #define ANEHIP_ATTN_CASE(GG)                                                                                   \
     case GG:                                                                                                   \
         hipLaunchKernelGGL(attn_partial_kernel<GG>, g1, dim3(kThreads), 0, stream, mix, q_norm, k_norm,        \
-                           inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, tpw, part_o, part_ml);    \
+                           inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, tpw, part_o, part_ml,     \
+                           cache_off, row_stride, append);                                                    \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
         hipLaunchKernelGGL(attn_combine_kernel<GG>, g2, dim3(kThreads), 0, stream, mix, pos, part_o, part_ml,  \
                            nch, tpw, n_heads, n_kv, out, out_hi, out_lo);                                     \
@@ -473,6 +507,28 @@ int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
             return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "attention: %d query heads per kv head (1, 2 or 4)", G);
     }
 #undef ANEHIP_ATTN_CASE
+}
+
+}  // namespace
+
+// part: workspace of attn_partial_floats() floats.
+int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
+                     const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
+                     const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,
+                     _Float16 *out_hi, _Float16 *out_lo) {
+    return attention_impl(ctx, stream, batch, n_heads, n_kv, max_seq, mix, q_norm, k_norm, inv_freq, pos, k_cache,
+                          v_cache, part, out, out_hi, out_lo, 0, (size_t)n_kv * max_seq * kHd, true);
+}
+
+int launch_attention_prefill(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, int n_kv, int max_seq,
+                             const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
+                             const uint32_t *pos, __half *k_cache, __half *v_cache, size_t cache_off, float *part,
+                             _Float16 *out_hi, _Float16 *out_lo) {
+    hipLaunchKernelGGL(attn_append_kernel, dim3(n_kv, rows), dim3(64), 0, stream, mix, k_norm, inv_freq, pos, k_cache,
+                       v_cache, cache_off, max_seq, n_heads, n_kv);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return attention_impl(ctx, stream, rows, n_heads, n_kv, max_seq, mix, q_norm, k_norm, inv_freq, pos, k_cache,
+                          v_cache, part, nullptr, out_hi, out_lo, cache_off, 0, false);
 }
 
 }  // namespace anehip

@@ -218,6 +218,14 @@ int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *out, int gate_off,
                          const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo);
+// Prefill: `rows` consecutive tokens of one sequence (mix row t = token t)
+// through the DeltaNet step of every head in turn, state and conv windows
+// (the sequence's blocks conv_state / S) kept in registers across the rows;
+// row t's gated RMSNorm to the planes.
+int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, const MixIn &mix,
+                         const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
+                         const float *dt_bias, float *conv_state, float *S, int gate_off, const float *norm_w,
+                         float eps, _Float16 *out_hi, _Float16 *out_lo);
 // Commits the q/k conv windows (if conv_state) and, if heads, writes the gated
 // RMSNorm of the heads (gate from mix rows at gate_off) to out (fp32) or, if
 // out_hi, to fragment-order fp16 hi/lo planes out_hi / out_lo (xf_index).
@@ -231,6 +239,14 @@ int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
                      const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
                      const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,
                      _Float16 *out_hi, _Float16 *out_lo);
+// Prefill of `rows` consecutive tokens of one sequence (row t at position
+// pos[t], q / k / v in mix row t): appends every row's k / v to the cache at
+// cache_off (halves; the sequence's [kv_head][max_seq][256] block), then
+// attends row t over positions [0, pos[t]] and writes fragment-order planes.
+int launch_attention_prefill(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, int n_kv, int max_seq,
+                             const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
+                             const uint32_t *pos, __half *k_cache, __half *v_cache, size_t cache_off, float *part,
+                             _Float16 *out_hi, _Float16 *out_lo);
 
 // elementwise.hip
 int launch_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const float *x, const float *w, float *out,

@@ -23,6 +23,8 @@
 //     when pos >= max_seq, gpu_full_decode.rs:805).
 #include "common.h"
 
+#include <algorithm>
+
 #include <cmath>
 #include <cstring>
 
@@ -79,6 +81,14 @@ struct Model {
     size_t xin_len = 0;          // fragment-order plane of the widest GEMM input (32 rows)
     size_t part_len = 0;         // floats per partial buffer
     void *argmax_ws = nullptr;
+    // prefill scratch for chunks of up to kPrefillRows tokens of one sequence
+    // (allocated by the first anehip_prefill; rows = tokens)
+    struct {
+        float *x = nullptr, *xn = nullptr, *pmix = nullptr, *p0 = nullptr, *p1 = nullptr, *attn_part = nullptr;
+        float *logits = nullptr;
+        _Float16 *xin = nullptr;  // planes: hi then lo, xin_len halves each
+        uint32_t *d_tokens = nullptr, *d_pos = nullptr;
+    } pf;
     // graph
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -115,6 +125,10 @@ void free_state(Model *M) {
     void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->x0,       M->x1,        M->pmix,      M->p0,
                     M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->xin};
     for (void *p : bufs) free_ptr(p);
+    void *pfb[] = {M->pf.x, M->pf.xn, M->pf.pmix, M->pf.p0, M->pf.p1, M->pf.attn_part, M->pf.logits, M->pf.xin,
+                   M->pf.d_tokens, M->pf.d_pos};
+    for (void *p : pfb) free_ptr(p);
+    M->pf = {};
     if (M->h_tokens) (void)hipHostFree(M->h_tokens);
     M->d_pos = M->d_tokens = M->d_sampled = M->h_tokens = nullptr;
     M->x0 = M->x1 = M->pmix = M->p0 = M->p1 = M->heads = M->attn_out = M->logits = M->attn_part = nullptr;
@@ -482,6 +496,116 @@ int pack_weights(anehip_ctx *ctx, Model *M) {
         TRY(pack_mat(ctx, L.ffn_down));
     }
     return pack_mat(ctx, M->lm_head);
+}
+
+constexpr uint32_t kPrefillRows = 32;  // tokens per prefill chunk (rows of the MFMA GEMM)
+
+// K-split partial floats of the prefill's GEMMs at kPrefillRows rows and of
+// the batch-1 lm_head GEMV.
+size_t prefill_part_floats(anehip_ctx *ctx, Model *M) {
+    const anehip_model_desc &D = M->desc;
+    const uint32_t d = D.dim, F = D.hidden_dim;
+    const uint32_t g[][2] = {{M->rows_dn, d}, {M->rows_attn, d}, {d, d}, {d, D.n_heads * D.head_dim}, {2 * F, d}, {d, F}};
+    size_t mx = (size_t)gemv_packed_ksplit(ctx, D.vocab_size, d, false) * D.vocab_size;
+    for (auto &e : g)
+        if (e[0]) mx = std::max(mx, (size_t)gemm_packed_ksplit(ctx, e[0], e[1]) * kPrefillRows * e[0]);
+    return mx;
+}
+
+int alloc_prefill(anehip_ctx *ctx, Model *M) {
+    if (M->pf.x) return ANEHIP_OK;
+    const anehip_model_desc &D = M->desc;
+    const size_t d = D.dim;
+    const size_t part = prefill_part_floats(ctx, M);
+    size_t attn = 0;
+    if (M->rows_attn) {
+        const int G = (int)(D.n_heads / D.n_kv_heads);
+        for (uint32_t r = 1; r <= kPrefillRows; r++)
+            attn = std::max(attn, attn_partial_floats((int)r, (int)D.n_kv_heads, (int)M->max_seq, G));
+    }
+    struct {
+        void **p;
+        size_t bytes;
+    } a[] = {{(void **)&M->pf.x, kPrefillRows * d * 4}, {(void **)&M->pf.xn, kPrefillRows * d * 4},
+             {(void **)&M->pf.pmix, part * 4}, {(void **)&M->pf.p0, part * 4}, {(void **)&M->pf.p1, part * 4},
+             {(void **)&M->pf.attn_part, std::max<size_t>(attn, 1) * 4}, {(void **)&M->pf.logits, (size_t)D.vocab_size * 4},
+             {(void **)&M->pf.xin, 2 * M->xin_len * sizeof(_Float16)}, {(void **)&M->pf.d_tokens, kPrefillRows * 4},
+             {(void **)&M->pf.d_pos, kPrefillRows * 4}};
+    for (auto &e : a) {
+        if (hipMalloc(e.p, e.bytes) != hipSuccess) {
+            *e.p = nullptr;
+            (void)hipGetLastError();
+            return set_error(ctx->err, ANEHIP_ENOMEM, "prefill: cannot allocate %zu bytes", e.bytes);
+        }
+    }
+    return ANEHIP_OK;
+}
+
+// One chunk of T <= kPrefillRows tokens of sequence `seq` (tokens and their
+// positions already in pf.d_tokens / pf.d_pos): the batched step's kernels
+// with one row per token, except the DeltaNet recurrence (a scan over the
+// rows, deltanet_scan) and attention (k / v of every row appended first,
+// then row t attends over positions <= its own).  With `logits`, the final
+// RMSNorm of the last row and the lm_head GEMV into pf.logits.
+int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq, int T, bool logits) {
+    const anehip_model_desc &D = M->desc;
+    const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
+    const float eps = D.rms_norm_eps;
+    _Float16 *xh = M->pf.xin, *xl = xh + M->xin_len;
+    float *x = M->pf.x;
+    TRY(launch_embed_rmsnorm(ctx, s, T, (int)d, M->pf.d_tokens, M->embedding, D.vocab_size, x,
+                             M->layers[0].attn_norm, nullptr, eps, xh, xl));
+    for (uint32_t l = 0; l < D.n_layers; l++) {
+        Layer &L = M->layers[l];
+        const bool dn = L.type == ANEHIP_LAYER_DELTANET;
+        const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
+        const int k1 = gemm_packed_ksplit(ctx, rows_in, d);
+        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xh, xl, T, M->pf.pmix, k1));
+        MixIn mix;
+        mix.p = M->pf.pmix;
+        mix.kp = k1;
+        mix.split = (size_t)T * rows_in;
+        mix.stride = (int)rows_in;
+        uint32_t cols3;
+        if (dn) {
+            TRY(launch_deltanet_scan(ctx, s, T, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
+                                     L.conv1d, L.ssm_a, L.dt_bias, L.conv_state + (size_t)seq * C * kConvK,
+                                     L.S + (size_t)seq * H * kDk * kDk, (int)C, L.ssm_norm, eps, xh, xl));
+            cols3 = d;
+        } else {
+            const size_t cache_off = (size_t)seq * D.n_kv_heads * M->max_seq * D.head_dim;
+            TRY(launch_attention_prefill(ctx, s, T, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
+                                         L.k_norm, M->inv_freq, M->pf.d_pos, L.kc, L.vc, cache_off, M->pf.attn_part,
+                                         xh, xl));
+            cols3 = D.n_heads * D.head_dim;
+        }
+        const int k3 = gemm_packed_ksplit(ctx, d, cols3);
+        TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xh, xl, T, M->pf.p0, k3));
+        TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k3, L.post_attn_norm, nullptr, eps, xh, xl));
+        const int k4 = gemm_packed_ksplit(ctx, 2 * F, d);
+        TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xh, xl, T, M->pf.p1, k4));
+        TRY(launch_silu_mul_stacked(ctx, s, T, (int)F, M->pf.p1, k4, nullptr, xh, xl));
+        const int k5 = gemm_packed_ksplit(ctx, d, F);
+        TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xh, xl, T, M->pf.p0, k5));
+        if (l + 1 < D.n_layers)
+            TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k5, M->layers[l + 1].attn_norm, nullptr, eps,
+                                        xh, xl));
+        else if (logits)  // final RMSNorm as fp32 rows
+            TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k5, M->final_norm, M->pf.xn, eps, nullptr,
+                                        nullptr));
+    }
+    if (!logits) return ANEHIP_OK;
+    GemvInput inf;
+    inf.mode = GEMV_IN_PLAIN;
+    inf.x = M->pf.xn + (size_t)(T - 1) * d;
+    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d, false);
+    if (kf == 1) {
+        TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->pf.logits, 1));
+    } else {
+        TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->pf.pmix, kf));
+        TRY(launch_sum_partials(ctx, s, M->pf.pmix, M->pf.logits, D.vocab_size, kf));
+    }
+    return ANEHIP_OK;
 }
 
 int launch_step(anehip_ctx *ctx, Model *M) {
@@ -898,6 +1022,44 @@ int anehip_decode_step(anehip_ctx *ctx, const uint32_t *tokens, uint32_t batch, 
         ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(logits_out, M->logits, (size_t)batch * M->desc.vocab_size * sizeof(float),
                                                 hipMemcpyDeviceToHost, ctx->stream));
     ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    return ANEHIP_OK;
+}
+
+int anehip_prefill(anehip_ctx *ctx, uint32_t seq, const uint32_t *tokens, uint32_t n_tokens, float *logits_out) {
+    int rc;
+    Model *M = model_of(ctx, &rc);
+    if (!M) return rc;
+    if ((rc = check_model(ctx, M))) return rc;
+    if (!tokens || n_tokens == 0) return set_error(ctx->err, ANEHIP_EINVAL, "prefill: no tokens");
+    if (seq >= M->batch) return set_error(ctx->err, ANEHIP_EINVAL, "prefill: sequence %u of %u", seq, M->batch);
+    const uint32_t p0 = M->host_pos[seq];
+    if ((uint64_t)p0 + n_tokens > M->max_seq)
+        return set_error(ctx->err, ANEHIP_ERANGE, "prefill: sequence %u at pos %u + %u tokens exceeds capacity %u", seq,
+                         p0, n_tokens, M->max_seq);
+    hipStream_t s = ctx->stream;
+    TRY(pack_weights(ctx, M));
+    TRY(alloc_prefill(ctx, M));
+    uint32_t h_tok[kPrefillRows], h_pos[kPrefillRows];
+    for (uint32_t c0 = 0; c0 < n_tokens; c0 += kPrefillRows) {
+        const uint32_t T = std::min(kPrefillRows, n_tokens - c0);
+        for (uint32_t t = 0; t < T; t++) {
+            h_tok[t] = tokens[c0 + t];
+            h_pos[t] = p0 + c0 + t;
+        }
+        // the previous chunk's kernels read these buffers: synchronous copies
+        ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(s));
+        ANEHIP_HIP_TRY(ctx->err, hipMemcpy(M->pf.d_tokens, h_tok, T * 4, hipMemcpyHostToDevice));
+        ANEHIP_HIP_TRY(ctx->err, hipMemcpy(M->pf.d_pos, h_pos, T * 4, hipMemcpyHostToDevice));
+        TRY(enqueue_prefill_chunk(ctx, M, s, seq, (int)T, c0 + T == n_tokens));
+    }
+    // the sequence continues at p0 + n_tokens (device copy for the step graph)
+    const uint32_t pos = p0 + n_tokens;
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(s));
+    ANEHIP_HIP_TRY(ctx->err, hipMemcpy(M->d_pos + seq, &pos, sizeof(uint32_t), hipMemcpyHostToDevice));
+    M->host_pos[seq] = pos;
+    if (logits_out)
+        ANEHIP_HIP_TRY(ctx->err, hipMemcpy(logits_out, M->pf.logits, (size_t)M->desc.vocab_size * sizeof(float),
+                                           hipMemcpyDeviceToHost));
     return ANEHIP_OK;
 }
 

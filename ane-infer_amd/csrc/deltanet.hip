@@ -359,7 +359,168 @@ __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
     out_lo[xo] = (_Float16)(v - (float)hi);
 }
 
+// Prefill: T consecutive tokens of one sequence (mix row t = token t), one
+// workgroup per head holding the head's 128 x 128 state in registers across
+// all T steps (read and written once per chunk instead of once per token).
+// Token t's step is deltanet_head_kernel's step with the conv window shifted
+// by that token's input; row t of the gated RMSNorm goes to the planes.
+// conv_state / S: the sequence's own blocks.  grid = n_heads.
+template <int KP>
+__global__ __launch_bounds__(kThreads) void deltanet_scan_kernel(
+    MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
+    const float *__restrict__ dt_bias, float *__restrict__ cs, float *__restrict__ S, int gate_off,
+    const float *__restrict__ norm_w, float eps, _Float16 *__restrict__ out_hi, _Float16 *__restrict__ out_lo,
+    int n_heads, int T) {
+    __shared__ float qn[kDk], kn[kDk], vv[kDk];
+    __shared__ __align__(16) float part[8][kDk];
+    __shared__ float red[4];
+
+    const int t = threadIdx.x, h = blockIdx.x;
+    const int chunk = n_heads * kDk;
+    const int cq = t & 31, rg = t >> 5, e = t & (kDk - 1);
+    float *Sh = S + (size_t)h * kDk * kDk + 4 * cq;
+    const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + e, chv = 2 * chunk + h * kDk + e;
+    f32x4 win = *reinterpret_cast<const f32x4 *>(cs + (size_t)ch * kKsize);
+    const f32x4 wk = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)ch * kKsize);
+    f32x4 winv = *reinterpret_cast<const f32x4 *>(cs + (size_t)chv * kKsize);
+    const f32x4 wkv = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)chv * kKsize);
+    const float sa = ssm_a[h], dtb = dt_bias[h], nw = norm_w[e];
+    float4 s[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(16 * rg + r) * kDk);
+
+    // inputs of token `tok`, loaded one token ahead of their use
+    float xa[KP], xv[KP], xg[KP], xb[KP], xal[KP];
+    auto load_in = [&](int tok) {
+        mix.load<KP>(tok, ch, xa);
+        mix.load<KP>(tok, chv, xv);
+        mix.load<KP>(tok, gate_off + h * kDk + e, xg);
+        mbeta.load<KP>(tok, h, xb);
+        malpha.load<KP>(tok, h, xal);
+    };
+    load_in(0);
+    for (int tok = 0; tok < T; tok++) {
+        // this token's inputs; the next token's loads go out now
+        const float x = mix.add<KP>(xa), x2 = mix.add<KP>(xv), gt = mix.add<KP>(xg);
+        const float br = mbeta.add<KP>(xb), ar = malpha.add<KP>(xal);
+        load_in(min(tok + 1, T - 1));
+        // 1. conv + SiLU over the window shifted by this token's input
+        // (conv_shift_and_append + conv_apply, deltanet_cache.rs:34-54)
+        win = f32x4{win.y, win.z, win.w, x};
+        winv = f32x4{winv.y, winv.z, winv.w, x2};
+        const auto conv = [](f32x4 w0, f32x4 k) {
+            float sum = 0.0f;
+            sum += w0.x * k.x;
+            sum += w0.y * k.y;
+            sum += w0.z * k.z;
+            sum += w0.w * k.w;
+            return silu_ref(sum);
+        };
+        {
+            const float y = conv(win, wk);
+            const float sq = wave_sum(y * y);
+            if ((t & 63) == 0) red[t >> 6] = sq;
+            if (t < kDk) qn[t] = y;
+            else kn[e] = y;
+            if (t < kDk) vv[t] = conv(winv, wkv);
+        }
+        // deltanet.rs:474-480
+        const float beta = 1.0f / (1.0f + expf(-br));
+        const float decay = expf(sa * logf(1.0f + expf(ar + dtb)));
+        __syncthreads();
+        // 2. L2 normalise (deltanet.rs:25-31, 461-467)
+        if (t < kDk) {
+            const float inv = 1.0f / sqrtf((red[0] + red[1]) + 1e-12f);
+            const float scale = 1.0f / sqrtf((float)kDk);
+            qn[t] = (qn[t] * inv) * scale;
+        } else {
+            const float inv = 1.0f / sqrtf((red[2] + red[3]) + 1e-12f);
+            kn[e] = kn[e] * inv;
+        }
+        __syncthreads();
+        // 3. S' = decay * S, partial recall over this thread's rows
+        float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float ki = kn[16 * rg + r];
+            s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
+            sk.x += s[r].x * ki; sk.y += s[r].y * ki; sk.z += s[r].z * ki; sk.w += s[r].w * ki;
+        }
+        *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = sk;
+        __syncthreads();
+        float4 delta;
+        {
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                float4 p = *reinterpret_cast<const float4 *>(&part[g][4 * cq]);
+                acc[0] += p.x; acc[1] += p.y; acc[2] += p.z; acc[3] += p.w;
+            }
+            delta.x = beta * (vv[4 * cq + 0] - acc[0]);
+            delta.y = beta * (vv[4 * cq + 1] - acc[1]);
+            delta.z = beta * (vv[4 * cq + 2] - acc[2]);
+            delta.w = beta * (vv[4 * cq + 3] - acc[3]);
+        }
+        __syncthreads();  // part[] is reused below
+        // S'' = S' + k delta^T, partial query
+        float4 so = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float ki = kn[16 * rg + r], qi = qn[16 * rg + r];
+            s[r].x += ki * delta.x; s[r].y += ki * delta.y; s[r].z += ki * delta.z; s[r].w += ki * delta.w;
+            so.x += s[r].x * qi; so.y += s[r].y * qi; so.z += s[r].z * qi; so.w += s[r].w * qi;
+        }
+        *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = so;
+        __syncthreads();
+        // 4. head output, gated RMSNorm (deltanet.rs:517-533) -> planes row tok
+        float o = 0.f;
+        if (t < kDk) {
+#pragma unroll
+            for (int g = 0; g < 8; g++) o += part[g][t];
+        }
+        const float ss = wave_sum(o * o);  // waves 2-3 contribute zeros
+        __syncthreads();                   // red[] is reused
+        if ((t & 63) == 0) red[t >> 6] = ss;
+        __syncthreads();
+        if (t < kDk) {
+            const float inv_rms = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + eps);
+            const float v = ((o * inv_rms) * nw) * (gt / (1.0f + expf(-gt)));
+            const size_t xo = xf_index(tok, h * kDk + t);
+            const _Float16 hi = (_Float16)v;
+            out_hi[xo] = hi;
+            out_lo[xo] = (_Float16)(v - (float)hi);
+        }
+        __syncthreads();  // qn / kn / vv / red are rewritten by the next token
+    }
+    // the state and the windows after the last token
+#pragma unroll
+    for (int r = 0; r < 16; r++) *reinterpret_cast<float4 *>(Sh + (size_t)(16 * rg + r) * kDk) = s[r];
+    *reinterpret_cast<float4 *>(cs + (size_t)ch * kKsize) = make_float4(win.x, win.y, win.z, win.w);
+    if (t < kDk) *reinterpret_cast<float4 *>(cs + (size_t)chv * kKsize) = make_float4(winv.x, winv.y, winv.z, winv.w);
+}
+
 }  // namespace
+
+int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, const MixIn &mix,
+                         const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
+                         const float *dt_bias, float *conv_state, float *S, int gate_off, const float *norm_w,
+                         float eps, _Float16 *out_hi, _Float16 *out_lo) {
+    const int kp = max(mix.kp, max(beta.kp, alpha.kp));
+    if (kp > 16 || rows < 1 || rows > 32)
+        return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_scan: %d K splits (at most 16), %d rows (1..32)", kp, rows);
+#define DN_SCAN(KP)                                                                                                  \
+    hipLaunchKernelGGL(deltanet_scan_kernel<KP>, dim3(n_heads), dim3(kThreads), 0, stream, mix, beta, alpha, conv_w, \
+                       ssm_a, dt_bias, conv_state, S, gate_off, norm_w, eps, out_hi, out_lo, n_heads, rows)
+    if (kp <= 1)
+        DN_SCAN(1);
+    else if (kp <= 4)
+        DN_SCAN(4);
+    else
+        DN_SCAN(16);
+#undef DN_SCAN
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
 
 int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,

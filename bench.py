@@ -157,7 +157,7 @@ def time_point(ctx, s, batch, launches, gguf=False):
     return ms / launches
 
 
-def bench_decode(anehip, steps, warmup, points=DECODE_POINTS):
+def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
     """Greedy decode tok/s of the random-init Qwen3.5-2B shape at each (batch, ctx)."""
     spec = anehip.Spec()
     gm = anehip.Model(spec)
@@ -192,6 +192,18 @@ def bench_decode(anehip, steps, warmup, points=DECODE_POINTS):
             "algorithmic_GB_per_step": round(step_bytes / 1e9, 3),
             "effective_GB_s": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
         }
+    if prefill_tokens:
+        # anehip_prefill of one sequence from position 0 (chunks of 32 tokens),
+        # synchronous, timed on the host clock; one untimed run first
+        gm.alloc_state(1, max(1024, prefill_tokens))
+        prompt = (np.arange(prefill_tokens, dtype=np.uint32) * 7919) % spec.vocab_size
+        gm.prefill(0, prompt, want_logits=False)
+        gm.set_pos(0, 0)
+        t0 = time.perf_counter()
+        gm.prefill(0, prompt, want_logits=True)
+        dt = time.perf_counter() - t0
+        out[f"prefill_B1_tokens{prefill_tokens}"] = {"tok_s": round(prefill_tokens / dt, 1),
+                                                    "ms": round(dt * 1e3, 2)}
     gm.close()
     return out
 
@@ -364,7 +376,7 @@ def main():
         "gguf_layout_points": gguf_points,
     }
     if not args.no_decode:
-        out["decode"] = bench_decode(anehip, args.decode_steps, 3)
+        out["decode"] = bench_decode(anehip, args.decode_steps, 3, prefill_tokens=512)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(anehip, ctx, shapes, args.cpu_seconds, decode=not args.no_decode)
     ctx.close()

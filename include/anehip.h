@@ -327,6 +327,20 @@ int anehip_decode_step(anehip_ctx *ctx, const uint32_t *token_ids, uint32_t batc
 /* Same, but only enqueues the step on the context stream. */
 int anehip_decode_step_async(anehip_ctx *ctx, const uint32_t *token_ids, uint32_t batch);
 
+/*
+ * Prefill: tokens[n_tokens] of sequence `seq`, from its current position, in
+ * chunks of up to 32 tokens -- the projections on the MFMA GEMM with one row
+ * per token, the DeltaNet recurrence as a scan over each chunk's tokens with
+ * the state held on chip, attention causal within the chunk.  Leaves the
+ * sequence's state and position as n_tokens decode steps would (the other
+ * sequences untouched) and writes the last token's logits [vocab] to
+ * logits_out if not NULL.  Synchronous; ANEHIP_ERANGE if the tokens do not
+ * fit in the KV capacity.  Replaces the reference's token-serial prefill
+ * (ane_prefill_tokens, main.rs:1168-1429, with the ANE projections of
+ * ane_prefill.rs:301 and the CPU recurrence / attention per token).
+ */
+int anehip_prefill(anehip_ctx *ctx, uint32_t seq, const uint32_t *tokens, uint32_t n_tokens, float *logits_out);
+
 /* Device pointer of the last step's logits [batch][vocab]. */
 int anehip_logits_ptr(anehip_ctx *ctx, const float **dptr);
 

@@ -90,6 +90,96 @@ def test_mid_model_batched_steps(mid_host, B):
         q.close()
 
 
+def _check_state(gm, oseq, b, spec, what):
+    """Sequence b's DeltaNet states / conv windows / KV rows against an oracle sequence."""
+    for l in range(spec.n_layers):
+        if spec.layer_types[l] == anehip.LAYER_DELTANET:
+            for which in (0, 1):
+                g = gm.get_state(l, which).reshape(gm.batch, -1)[b]
+                r = oseq.view(l, which, g.size, np.float32)
+                assert max(rel_errs(g, r)) <= TOL, (what, l, which)
+        else:
+            p = gm.get_pos(b)
+            for which in (2, 3):
+                g = gm.get_state(l, which).reshape(gm.batch, spec.n_kv_heads, -1, spec.head_dim)[b][:, :p]
+                r = oseq.view(l, which, spec.n_kv_heads * oseq.max_seq * spec.head_dim,
+                              np.uint16).reshape(spec.n_kv_heads, -1, spec.head_dim)[:, :p]
+                gf = g.view(np.float16).astype(np.float32)
+                rf = r.view(np.float16).astype(np.float32)
+                assert max(rel_errs(gf, rf)) <= TOL, (what, l, which)
+
+
+@pytest.mark.parametrize("n", [1, 13, 45])
+def test_prefill_matches_token_steps(small_host, n):
+    """anehip_prefill of n prompt tokens (1, 13: one chunk; 45: 32 + 13) from
+    position 0 vs the oracle run token by token: the last token's logits, the
+    DeltaNet states / conv windows and the KV rows written, then 3 decode
+    steps continuing the sequence."""
+    spec = small_host.spec
+    gm = _model(small_host, 1, 64)
+    oseq = small_host.seq(64)
+    toks = oracle.randint(31, n, n, spec.vocab_size)
+    g = gm.prefill(0, toks)
+    for t in toks:
+        r = oseq.forward(int(t))
+    l2, mx = rel_errs(g, r)
+    print(f"prefill n={n}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+    assert l2 <= TOL and mx <= TOL
+    assert gm.get_pos(0) == n
+    _check_state(gm, oseq, 0, spec, "after prefill")
+    for t in oracle.randint(32, n, 3, spec.vocab_size):
+        assert max(rel_errs(gm.step([t])[0], oseq.forward(int(t)))) <= TOL
+    gm.close()
+    oseq.close()
+
+
+def test_prefill_one_sequence_of_a_batch(mid_host):
+    """On the mid-size model (K-split projections), batch 3: after two decode
+    steps of every sequence, sequence 1 prefills 40 tokens (32 + 8) from
+    position 2; its logits and state follow the oracle, sequences 0 and 2 keep
+    their state and positions, and a batched step afterwards matches the
+    oracle for every sequence."""
+    spec = mid_host.spec
+    B = 3
+    gm = _model(mid_host, B, 64)
+    seqs = [mid_host.seq(64) for _ in range(B)]
+    for step in range(2):
+        toks = oracle.randint(40 + step, B, B, spec.vocab_size)
+        g = gm.step(toks)
+        for b in range(B):
+            assert max(rel_errs(g[b], seqs[b].forward(int(toks[b])))) <= TOL
+    before = {b: [gm.get_state(l, 1).reshape(B, -1)[b].copy() for l in (0, 1)] for b in (0, 2)}
+    prompt = oracle.randint(50, 40, 40, spec.vocab_size)
+    g1 = gm.prefill(1, prompt)
+    for t in prompt:
+        r1 = seqs[1].forward(int(t))
+    assert max(rel_errs(g1, r1)) <= TOL
+    assert [gm.get_pos(b) for b in range(B)] == [2, 42, 2]
+    for b in (0, 2):
+        for i, l in enumerate((0, 1)):
+            assert np.array_equal(gm.get_state(l, 1).reshape(B, -1)[b], before[b][i])
+    _check_state(gm, seqs[1], 1, spec, "after prefill")
+    toks = oracle.randint(60, B, B, spec.vocab_size)
+    g = gm.step(toks)
+    for b in range(B):
+        assert max(rel_errs(g[b], seqs[b].forward(int(toks[b])))) <= TOL
+    gm.close()
+    for q in seqs:
+        q.close()
+
+
+def test_prefill_rejects_bad_arguments(small_host):
+    gm = _model(small_host, 2, 16)
+    with pytest.raises(anehip.AnehipError) as e:
+        gm.prefill(2, [1, 2, 3])
+    assert e.value.code == -1  # ANEHIP_EINVAL
+    with pytest.raises(anehip.AnehipError) as e:
+        gm.prefill(0, np.arange(17))
+    assert e.value.code == -7  # ANEHIP_ERANGE
+    assert gm.get_pos(0) == 0
+    gm.close()
+
+
 def test_graph_replay_matches_eager_bits(small_host):
     toks = oracle.randint(7, 3, 6, small_host.spec.vocab_size)
     outs = []
@@ -199,3 +289,23 @@ def test_qwen35_2b_shape_step(big_host, ctx_len, batch):
         assert l2 <= TOL and mx <= TOL
         seqs[b].close()
     gm.close()
+
+
+def test_qwen35_2b_shape_prefill(big_host):
+    """Random-init 24-layer Qwen3.5-2B shape: a 40-token prompt (32 + 8)
+    prefilled from position 0 vs the oracle run token by token (last logits),
+    then one decode step continuing the sequence."""
+    spec = big_host.spec
+    gm = _model(big_host, 1, 256)
+    oseq = big_host.seq(256)
+    prompt = oracle.randint(70, 40, 40, spec.vocab_size)
+    g = gm.prefill(0, prompt)
+    for t in prompt:
+        r = oseq.forward(int(t))
+    l2, mx = rel_errs(g, r)
+    print(f"2B prefill 40: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+    assert l2 <= TOL and mx <= TOL
+    t = int(oracle.randint(71, 1, 1, spec.vocab_size)[0])
+    assert max(rel_errs(gm.step([t])[0], oseq.forward(t))) <= TOL
+    gm.close()
+    oseq.close()
