@@ -1071,10 +1071,11 @@ template <uint32_t T> struct WUnit {
     uint32_t sc;  // the quarter's dword of the lane's scale vector
 };
 
-template <uint32_t T, int P, int R>
+template <uint32_t T, int P, int R, bool XROWS = false>
 __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(2))) void gemm_xs(
     const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-    float *__restrict__ out, int m, int n, int batch, int ksplit, size_t split_stride) {
+    const float *__restrict__ xrows, float *__restrict__ out, int m, int n, int batch, int ksplit,
+    size_t split_stride) {
     constexpr int Q = GemmUnit<T, 1>::kQ;
     __shared__ __align__(16) float red[kGemmWaves][32][kWave];
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
@@ -1086,17 +1087,35 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
     const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
     const __amdgpu_buffer_rsrc_t orsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
-    // this quarter's x fragments of the split's panels
+    // this quarter's x fragments of the split's panels: lane l holds batch row
+    // l % 32 (rows past the batch repeat the last), 8 consecutive columns;
+    // from the fragment-order planes, or (XROWS) split from fp32 rows x[b][n]
     h8v xa[P][4], xb[P][4];
-    {
-        const size_t xbase = (size_t)(4 * quarter * kWave + min(lane & 31, batch - 1) + 32 * (lane >> 5)) * 8 +
-                             16 * 512 * (size_t)(ks * P);
+    const int brow = min(lane & 31, batch - 1);
+    if constexpr (!XROWS) {
+        const size_t xbase = (size_t)(4 * quarter * kWave + brow + 32 * (lane >> 5)) * 8 + 16 * 512 * (size_t)(ks * P);
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
             for (int st = 0; st < 4; st++) {
                 xa[p][st] = *reinterpret_cast<const h8v *>(xh + xbase + 16 * 512 * p + 512 * st);
                 xb[p][st] = *reinterpret_cast<const h8v *>(xl + xbase + 16 * 512 * p + 512 * st);
+            }
+    } else {
+        const float *xr = xrows + (size_t)brow * n;
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const int c0 = 16 * (16 * (ks * P + p) + 4 * quarter + st) + 8 * (lane >> 5);
+                const float4 a = *reinterpret_cast<const float4 *>(xr + c0);
+                const float4 b = *reinterpret_cast<const float4 *>(xr + c0 + 4);
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    xa[p][st][i] = (_Float16)v[i];
+                    xb[p][st][i] = (_Float16)(v[i] - (float)xa[p][st][i]);
+                }
             }
     }
     const uint8_t *wsplit = Wp + (size_t)(ks * P) * Panel<T>::kBytes;
@@ -1512,19 +1531,42 @@ int launch_gemm_packed_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, 
 // a whole number of workgroups per split, about 3 per CU at P = 1 and 2 at
 // P = 2, each with one tile of weights in flight (deeper register rings and
 // more workgroups per split measured slower on every decode shape).
-template <uint32_t T>
+template <uint32_t T, bool XROWS = false>
 void launch_gemm_xs_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
-                      const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit, int per) {
+                      const _Float16 *xh, const _Float16 *xl, const float *xrows, uint32_t batch, float *out,
+                      int ksplit, int per) {
     const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const int gs = max(1, min(tiles, (per == 1 ? 3 : 2) * cus / ksplit));
     const dim3 grid(gs * ksplit), block(kWave * kGemmWaves);
     const size_t ss = (size_t)batch * m;
     if (per == 1)
-        hipLaunchKernelGGL((gemm_xs<T, 1, 1>), grid, block, 0, stream, w, xh, xl, out, (int)m, (int)n, (int)batch,
-                           ksplit, ss);
+        hipLaunchKernelGGL((gemm_xs<T, 1, 1, XROWS>), grid, block, 0, stream, w, xh, xl, xrows, out, (int)m, (int)n,
+                           (int)batch, ksplit, ss);
     else
-        hipLaunchKernelGGL((gemm_xs<T, 2, 1>), grid, block, 0, stream, w, xh, xl, out, (int)m, (int)n, (int)batch,
-                           ksplit, ss);
+        hipLaunchKernelGGL((gemm_xs<T, 2, 1, XROWS>), grid, block, 0, stream, w, xh, xl, xrows, out, (int)m, (int)n,
+                           (int)batch, ksplit, ss);
+}
+
+bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+    const int k = gemm_packed_ksplit(ctx, m, n), nsb = (int)(n / 256);
+    return k >= 2 && nsb % k == 0 && nsb / k <= 2;
+}
+
+int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
+                        uint32_t n, const float *x, uint32_t batch, float *out) {
+    if (!gemm_is_xs(ctx, m, n) || batch < 1 || batch > 32 || m % 4)
+        return set_error(ctx->err, ANEHIP_EINVAL, "gemm: %u x %u at batch %u is not an x-stationary shape", m, n,
+                         batch);
+    const int ksplit = gemm_packed_ksplit(ctx, m, n), per = (int)(n / 256) / ksplit;
+    if (4.0 * ksplit * batch * m > 1073741824.0)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
+    const uint8_t *w = static_cast<const uint8_t *>(wp);
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        launch_gemm_xs_t<ANEHIP_GGML_Q8_0, true>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit, per);
+    else
+        launch_gemm_xs_t<ANEHIP_GGML_Q4_0, true>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit, per);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
 }
 
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
@@ -1539,9 +1581,9 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     const bool xs = ksplit >= 2 && per * ksplit == (int)(n / 256) && per <= 2;
     if (xs && ggml_type == ANEHIP_GGML_Q8_0)
-        launch_gemm_xs_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
+        launch_gemm_xs_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit, per);
     else if (xs)
-        launch_gemm_xs_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
+        launch_gemm_xs_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit, per);
     else if (ggml_type == ANEHIP_GGML_Q8_0)
         launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
     else
