@@ -187,10 +187,11 @@ inline size_t xf_plane_len(size_t n) { return 32 * n; }
 int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                        uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit);
-// Whether gemm_packed_ksplit's split of [m x n] runs on the x-stationary kernel,
-// which can also take x as fp32 rows [batch][n] (no planes needed):
-// launch_gemm_xs_rows writes out[ks][b][r] for its gemm_packed_ksplit splits.
-bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n);
+// Whether gemm_packed_ksplit's split of [m x n] at this batch runs on an
+// x-stationary kernel, which can also take x as fp32 rows [batch][n] (no
+// planes needed): launch_gemm_xs_rows writes out[ks][b][r] for its
+// gemm_packed_ksplit splits.
+bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
 int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                         uint32_t n, const float *x, uint32_t batch, float *out);
 // x [batch][n] fp32 -> fragment-order hi / lo planes (xf_plane_len(n) halves each).

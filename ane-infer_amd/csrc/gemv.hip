@@ -729,6 +729,7 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmWaves = 4;
 constexpr int kGemmRing = 2;  // panel GEMM: units in flight per wave
@@ -1057,6 +1058,212 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
     } while (ci < items);
 }
 
+// ---- batch <= 16: v_mfma_f32_16x16x32_f16 ----
+// A 16 x 16 x 32 MFMA covers one 32-column block: lane l holds A row l % 16
+// (a batch row) and B column l % 16 (a weight row), each with columns
+// 8 (l / 16) .. 8 (l / 16) + 7, and gets C rows 4 (l / 16) .. + 3 of column
+// l % 16.  Against the 32 x 32 x 16 form at batch <= 16 it halves the MFMA
+// work, the block-scale FMAs and the x fragments a unit loads.
+
+// 4 x 4 transpose over the 16-lane groups of a wave: afterwards r[g] of the
+// lane at position i of group G holds what r[G] held at position i of group
+// g.  (v_permlane32_swap exchanges the upper half of its first operand with
+// the lower half of its second; v_permlane16_swap the odd 16-lane groups of
+// its first operand with the even groups of its second.)
+__device__ __forceinline__ void transpose_groups(uint32_t (&r)[4]) {
+    const auto s02 = __builtin_amdgcn_permlane32_swap(r[0], r[2], false, false);
+    const auto s13 = __builtin_amdgcn_permlane32_swap(r[1], r[3], false, false);
+    const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    r[0] = s01[0];
+    r[1] = s01[1];
+    r[2] = s23[0];
+    r[3] = s23[1];
+}
+
+// One wave's operands for one quarter of one panel: the quant vectors as in
+// GemmUnit, the quarter's dword of the lane row's scale vector, and the A
+// fragments of the quarter's two blocks (hi and lo planes).
+template <uint32_t T> struct GemmUnit16 {
+    static constexpr int kQ = GemmUnit<T, 1>::kQ;
+    u32x4 q[kQ];
+    uint32_t sc;
+    h8v ah[2], al[2];
+};
+
+// acc[g] += the quarter's two blocks for weight rows 16 g .. 16 g + 15 of the
+// tile.  The panel gives lane l weight row l; the B fragment of row group g
+// needs, at lane l of group G, row 16 g + l % 16 and the block's columns
+// 8 G .. 8 G + 7, so the quant dwords (and the row scales) go through
+// transpose_groups first.  Per block and row group: C = A_hi B + A_lo B, then
+// acc += C * d (q8_gemv.rs:234-242 order within a block up to fp32 summation).
+template <uint32_t T>
+__device__ __forceinline__ void mma_tile16(const u32x4 *q, uint32_t sw, const h8v *ah, const h8v *al,
+                                           f32x4 (&acc)[4], int grp) {
+    uint32_t s[4] = {sw, sw, sw, sw};
+    transpose_groups(s);  // s[g]: scales of blocks 2q, 2q + 1 of weight row 16 g + lane % 16
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        // piece G' of a row = the dwords of its block columns 8 G' .. 8 G' + 7
+        uint32_t lo[4], hi[4];
+        if constexpr (T == ANEHIP_GGML_Q8_0) {
+            const u32x4 a = q[2 * j], b = q[2 * j + 1];
+            lo[0] = a.x, hi[0] = a.y, lo[1] = a.z, hi[1] = a.w;
+            lo[2] = b.x, hi[2] = b.y, lo[3] = b.z, hi[3] = b.w;
+        } else {
+            // columns 0-15 are the low nibbles of the block's 16 bytes, 16-31
+            // the high ones: pieces 2, 3 repeat the bytes of pieces 0, 1
+            const u32x4 v = q[j];
+            lo[0] = lo[2] = v.x, hi[0] = hi[2] = v.y;
+            lo[1] = lo[3] = v.z, hi[1] = hi[3] = v.w;
+        }
+        transpose_groups(lo);
+        transpose_groups(hi);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            h8v b;
+            if constexpr (T == ANEHIP_GGML_Q8_0) {
+                b = dwords_to_h8_i8(lo[g], hi[g]);
+            } else {
+                const uint32_t sh = 4 * (grp >> 1);  // groups 2, 3: high nibbles
+                b = dwords_to_h8_u4((lo[g] >> sh) & 0x0F0F0F0Fu, (hi[g] >> sh) & 0x0F0F0F0Fu);
+            }
+            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], b, f32x4{}, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], b, c, 0, 0, 0);
+            const float d = __half2float(__ushort_as_half((unsigned short)(s[g] >> (16 * j))));
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[g][r] = fmaf(c[r], d, acc[g][r]);
+        }
+    }
+}
+
+// x-stationary GEMM for batch <= 16 on the 16 x 16 x 32 MFMA.  Workgroup g
+// works on split ks = g % ksplit (P consecutive panels) and the tiles
+// g / ksplit + i * (gridDim.x / ksplit); each of its 4 waves holds its column
+// quarter's A fragments of the split's P panels (16 P VGPRs) and streams
+// units of one panel quarter of one tile (4 quant vectors and one scale
+// dword, 17 VGPRs), D of them in flight in a register ring.  The loop body
+// covers U = max(P, D) units so that ring slots and panels are compile-time
+// indices; a tile's sums are added over the quarters through LDS.  Loads
+// past the last tile are clamped to it and their results stored nowhere.
+// Output: out[ks * split_stride + b * m + row] (device-scope stores).
+template <uint32_t T, int P, int D, int WPE>
+__global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_xs16(
+    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+    const float *__restrict__ xrows, float *__restrict__ out, int m, int n, int batch, int ksplit,
+    size_t split_stride) {
+    constexpr int Q = GemmUnit16<T>::kQ;
+    constexpr int U = P > D ? P : D;
+    static_assert(U % P == 0 && U % D == 0, "ring and panel counts must divide the loop body");
+    __shared__ __align__(16) float red[kGemmWaves][16][kWave];
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
+    const int gs = gridDim.x / ksplit;  // workgroups per split
+    const int ks = blockIdx.x % ksplit, g0 = blockIdx.x / ksplit;
+    if (g0 >= gs || g0 >= tiles) return;
+    const int lane = threadIdx.x & (kWave - 1), grp = lane >> 4;
+    const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
+    const __amdgpu_buffer_rsrc_t orsrc =
+        __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
+    // A fragments: batch row lane % 16 (clamped to the batch), columns
+    // 64 quarter + 32 j + 8 (lane / 16) of each panel of the split
+    h8v xa[P][2], xb[P][2];
+    const int brow = min(lane & 15, batch - 1);
+    if (xrows == nullptr) {
+        const size_t xbase = (size_t)((4 * quarter + (grp >> 1)) * kWave + brow + 32 * (grp & 1)) * 8 +
+                             16 * 512 * (size_t)(ks * P);
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                xa[p][j] = *reinterpret_cast<const h8v *>(xh + xbase + 16 * 512 * p + 1024 * j);
+                xb[p][j] = *reinterpret_cast<const h8v *>(xl + xbase + 16 * 512 * p + 1024 * j);
+            }
+    } else {
+        const float *xr = xrows + (size_t)brow * n;
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int c0 = 256 * (ks * P + p) + 64 * quarter + 32 * j + 8 * grp;
+                const float4 a = *reinterpret_cast<const float4 *>(xr + c0);
+                const float4 b = *reinterpret_cast<const float4 *>(xr + c0 + 4);
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    xa[p][j][i] = (_Float16)v[i];
+                    xb[p][j][i] = (_Float16)(v[i] - (float)xa[p][j][i]);
+                }
+            }
+    }
+    const uint8_t *wsplit = Wp + (size_t)(ks * P) * Panel<T>::kBytes;
+    int lt = g0, lp = 0;  // load cursor: tile, panel within the split
+    auto load_next = [&](GemmUnit16<T> &u) {
+        const u32x4 *p4 = reinterpret_cast<const u32x4 *>(wsplit + (size_t)min(lt, tiles - 1) * tile_bytes +
+                                                          (size_t)lp * Panel<T>::kBytes);
+#pragma unroll
+        for (int c = 0; c < Q; c++) u.q[c] = __builtin_nontemporal_load(p4 + (Q * quarter + c) * kWave + lane);
+        u.sc = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p4 + Panel<T>::kChunks * kWave + lane) +
+                                          quarter);
+        const bool wrap = ++lp == P;
+        lp = wrap ? 0 : lp;
+        lt = wrap ? lt + gs : lt;
+    };
+    // the empty asm statements keep the ring in order (as in gemm_xs)
+    GemmUnit16<T> ring[D];
+#pragma unroll
+    for (int k = 0; k < D; k++) {
+        load_next(ring[k]);
+        asm volatile("" ::: "memory");
+    }
+    int ct = g0;  // tile being multiplied
+    f32x4 acc[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) acc[g] = f32x4{};
+    do {
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            GemmUnit16<T> &u = ring[k % D];
+#pragma unroll
+            for (int c = 0; c < Q; c++) asm volatile("" : "+v"(u.q[c])::"memory");
+            asm volatile("" : "+v"(u.sc)::"memory");
+            mma_tile16<T>(u.q, u.sc, xa[k % P], xb[k % P], acc, grp);
+#pragma unroll
+            for (int g = 0; g < 4; g++) asm volatile("" : "+v"(acc[g])::"memory");
+            load_next(u);
+            if (k % P == P - 1) {
+                // tile done: park the 16 sums per lane (acc[g][r] of lane l:
+                // batch row 4 (l / 16) + r, tile row 16 g + l % 16), then each
+                // thread adds the 4 quarters of one 4-row vector of one batch row
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) red[quarter][4 * g + r][lane] = acc[g][r];
+                lds_barrier();
+                {
+                    const int th = threadIdx.x, b = th >> 4, j = th & 15;
+                    const int reg = 4 * (j >> 2) + (b & 3), l = 16 * (b >> 2) + 4 * (j & 3);
+                    float4 sum = *reinterpret_cast<const float4 *>(&red[0][reg][l]);
+#pragma unroll
+                    for (int w = 1; w < kGemmWaves; w++) {
+                        const float4 o = *reinterpret_cast<const float4 *>(&red[w][reg][l]);
+                        sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
+                    }
+                    const int row = ct * kWave + 4 * j;
+                    const int off = b < batch && row < m && ct < tiles ? 4 * (ks * (int)split_stride + b * m + row)
+                                                                       : kBadOffset;
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0,
+                                                           kCpolDevice);
+                }
+                lds_barrier();  // red is free again
+#pragma unroll
+                for (int g = 0; g < 4; g++) acc[g] = f32x4{};
+                ct += gs;
+            }
+        }
+    } while (ct < tiles);
+}
+
 // x-stationary panel GEMM for K-split shapes.  Workgroup g works on split
 // ks = g % ksplit only (its P panels); each wave loads the x fragments of its
 // column quarter in those panels once (32 P VGPRs) and then streams the
@@ -1200,7 +1407,6 @@ __global__ __launch_bounds__(256) void split_x_frag_kernel(const float *__restri
 // ---------------------------------------------------------------------------
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // fp32 x[batch][n] -> fp16 planes hi[batch][n], lo[batch][n] with hi + lo ~= x.
 __global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ x, _Float16 *__restrict__ hi,
@@ -1547,24 +1753,70 @@ void launch_gemm_xs_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uin
                            (int)batch, ksplit, ss);
 }
 
-bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+// The 16-wide x-stationary kernel takes batch <= 16 on an even split of 1, 2,
+// 4 or 8 panels per split (its A fragments: 16 VGPRs per panel).  Grids,
+// measured on MI355X at batch 4 and 16: P = 1 four workgroups per CU with one
+// unit in flight (a smaller register file), P >= 2 two per CU with two.
+// Against the 32-wide kernels at batch 4 / 16: 6144 x 2048 5.1 / 5.7 us
+// (P = 1) against 5.7 / 6.0; 12288 x 2048 7.4 / 7.9 (P = 2) against 8.7 / 8.8;
+// lm_head 151936 x 2048 60-65 us (P = 8) against 67-73.
+static bool xs16_split(uint32_t batch, int nsb, int ksplit) {
+    const int per = nsb / ksplit;
+    return batch <= 16 && per * ksplit == nsb && (per == 1 || per == 2 || per == 4 || per == 8);
+}
+static bool xs32_split(int nsb, int ksplit) {
+    const int per = nsb / ksplit;
+    return ksplit >= 2 && per * ksplit == nsb && per <= 2;
+}
+
+template <uint32_t T>
+void launch_gemm_xs16_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
+                        const _Float16 *xh, const _Float16 *xl, const float *xrows, uint32_t batch, float *out,
+                        int ksplit) {
+    const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int per = (int)(n / 256) / ksplit;
+    const int gs = max(1, min(tiles, (per == 1 ? 4 : 2) * cus / ksplit));
+    const dim3 grid(gs * ksplit), block(kWave * kGemmWaves);
+    const size_t ss = (size_t)batch * m;
+#define ANEHIP_XS16(P, D, W)                                                                                         \
+    hipLaunchKernelGGL((gemm_xs16<T, P, D, W>), grid, block, 0, stream, w, xh, xl, xrows, out, (int)m, (int)n,      \
+                       (int)batch, ksplit, ss)
+    if (per == 1)
+        ANEHIP_XS16(1, 1, 4);
+    else if (per == 2)
+        ANEHIP_XS16(2, 2, 2);
+    else if (per == 4)
+        ANEHIP_XS16(4, 2, 2);
+    else
+        ANEHIP_XS16(8, 2, 2);
+#undef ANEHIP_XS16
+}
+
+bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch) {
     const int k = gemm_packed_ksplit(ctx, m, n), nsb = (int)(n / 256);
-    return k >= 2 && nsb % k == 0 && nsb / k <= 2;
+    return xs16_split(batch, nsb, k) || xs32_split(nsb, k);
 }
 
 int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                         uint32_t n, const float *x, uint32_t batch, float *out) {
-    if (!gemm_is_xs(ctx, m, n) || batch < 1 || batch > 32 || m % 4)
+    if (batch < 1 || batch > 32 || m % 4 || !gemm_is_xs(ctx, m, n, batch))
         return set_error(ctx->err, ANEHIP_EINVAL, "gemm: %u x %u at batch %u is not an x-stationary shape", m, n,
                          batch);
     const int ksplit = gemm_packed_ksplit(ctx, m, n), per = (int)(n / 256) / ksplit;
     if (4.0 * ksplit * batch * m > 1073741824.0)
         return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
-    if (ggml_type == ANEHIP_GGML_Q8_0)
+    const bool q8 = ggml_type == ANEHIP_GGML_Q8_0;
+    if (xs16_split(batch, (int)(n / 256), ksplit)) {
+        if (q8)
+            launch_gemm_xs16_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit);
+        else
+            launch_gemm_xs16_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit);
+    } else if (q8) {
         launch_gemm_xs_t<ANEHIP_GGML_Q8_0, true>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit, per);
-    else
+    } else {
         launch_gemm_xs_t<ANEHIP_GGML_Q4_0, true>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit, per);
+    }
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
@@ -1579,8 +1831,12 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     if (4.0 * ksplit * batch * m > 1073741824.0)  // output byte offsets stay below kBadOffset
         return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
-    const bool xs = ksplit >= 2 && per * ksplit == (int)(n / 256) && per <= 2;
-    if (xs && ggml_type == ANEHIP_GGML_Q8_0)
+    const bool xs = xs32_split((int)(n / 256), ksplit);
+    if (xs16_split(batch, (int)(n / 256), ksplit) && ggml_type == ANEHIP_GGML_Q8_0)
+        launch_gemm_xs16_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit);
+    else if (xs16_split(batch, (int)(n / 256), ksplit))
+        launch_gemm_xs16_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit);
+    else if (xs && ggml_type == ANEHIP_GGML_Q8_0)
         launch_gemm_xs_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit, per);
     else if (xs)
         launch_gemm_xs_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit, per);

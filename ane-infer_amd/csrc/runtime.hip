@@ -227,8 +227,9 @@ int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
         return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: m=%u must be a multiple of 4 for batch > 1",
                          m);
     const size_t count = (size_t)batch * m, xcount = xf_plane_len(n);
-    if (gemm_is_xs(ctx, m, n)) {
-        // the x-stationary kernel reads the fp32 rows itself: partials, then their sum
+    if (gemm_is_xs(ctx, m, n, batch)) {
+        // the x-stationary kernels read the fp32 rows themselves: partials, then their sum
+        if (ksplit == 1) return launch_gemm_xs_rows(ctx, ctx->stream, ggml_type, wp, m, n, x, batch, y);
         int rc = ensure_workspace(ctx, (size_t)ksplit * count);
         if (rc) return rc;
         if ((rc = launch_gemm_xs_rows(ctx, ctx->stream, ggml_type, wp, m, n, x, batch, ctx->ws.partial))) return rc;
