@@ -184,7 +184,7 @@ inline size_t xf_plane_len(size_t n) { return 32 * n; }
 // is 1) from the fragment-order hi / lo planes of x (launch_split_x, or the
 // hi / lo outputs of the element-wise kernels), ksplit from gemm_packed_ksplit.
 // m must be a multiple of 4.
-int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n);
+int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                        uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit);
 // Whether gemm_packed_ksplit's split of [m x n] at this batch runs on an

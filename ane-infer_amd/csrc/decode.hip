@@ -404,7 +404,7 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
         const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
-        const int k1 = gemm_packed_ksplit(ctx, rows_in, d);
+        const int k1 = gemm_packed_ksplit(ctx, rows_in, d, B);
         TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xh, xl, B, M->pmix, k1));
         MixIn mix;
         mix.p = M->pmix;
@@ -422,18 +422,18 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
                                  L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part, nullptr, xh, xl));
             cols3 = qd;
         }
-        const int k3 = gemm_packed_ksplit(ctx, d, cols3);
+        const int k3 = gemm_packed_ksplit(ctx, d, cols3, B);
         TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xh, xl, B, M->p0, k3));
         TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, nullptr, eps, xh, xl));
-        const int k4 = gemm_packed_ksplit(ctx, 2 * F, d);
+        const int k4 = gemm_packed_ksplit(ctx, 2 * F, d, B);
         TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xh, xl, B, M->p1, k4));
         TRY(launch_silu_mul_stacked(ctx, s, B, (int)F, M->p1, k4, nullptr, xh, xl));
-        const int k5 = gemm_packed_ksplit(ctx, d, F);
+        const int k5 = gemm_packed_ksplit(ctx, d, F, B);
         TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xh, xl, B, M->p0, k5));
         const float *next_norm = l + 1 < D.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
         TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k5, next_norm, nullptr, eps, xh, xl));
     }
-    const int kf = gemm_packed_ksplit(ctx, D.vocab_size, d);
+    const int kf = gemm_packed_ksplit(ctx, D.vocab_size, d, B);
     if (kf == 1) {
         TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xh, xl, B, M->logits, 1));
     } else {
@@ -465,7 +465,8 @@ size_t part_floats(anehip_ctx *ctx, Model *M) {
     size_t mx = 0;
     for (auto &e : g) {
         if (!e.m) continue;
-        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n, e.norm) : gemm_packed_ksplit(ctx, e.m, e.n);
+        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n, e.norm)
+                                    : gemm_packed_ksplit(ctx, e.m, e.n, M->batch);
         size_t need = (size_t)k * M->batch * e.m;
         if (need > mx) mx = need;
     }
@@ -500,15 +501,17 @@ int pack_weights(anehip_ctx *ctx, Model *M) {
 
 constexpr uint32_t kPrefillRows = 32;  // tokens per prefill chunk (rows of the MFMA GEMM)
 
-// K-split partial floats of the prefill's GEMMs at kPrefillRows rows and of
-// the batch-1 lm_head GEMV.
+// K-split partial floats of the prefill's GEMMs at up to kPrefillRows rows
+// (the split depends on the rows only through rows <= 16 or not) and of the
+// batch-1 lm_head GEMV.
 size_t prefill_part_floats(anehip_ctx *ctx, Model *M) {
     const anehip_model_desc &D = M->desc;
     const uint32_t d = D.dim, F = D.hidden_dim;
     const uint32_t g[][2] = {{M->rows_dn, d}, {M->rows_attn, d}, {d, d}, {d, D.n_heads * D.head_dim}, {2 * F, d}, {d, F}};
     size_t mx = (size_t)gemv_packed_ksplit(ctx, D.vocab_size, d, false) * D.vocab_size;
     for (auto &e : g)
-        if (e[0]) mx = std::max(mx, (size_t)gemm_packed_ksplit(ctx, e[0], e[1]) * kPrefillRows * e[0]);
+        for (uint32_t rows : {16u, kPrefillRows})
+            if (e[0]) mx = std::max(mx, (size_t)gemm_packed_ksplit(ctx, e[0], e[1], rows) * rows * e[0]);
     return mx;
 }
 
@@ -559,7 +562,7 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
         const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
-        const int k1 = gemm_packed_ksplit(ctx, rows_in, d);
+        const int k1 = gemm_packed_ksplit(ctx, rows_in, d, T);
         TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xh, xl, T, M->pf.pmix, k1));
         MixIn mix;
         mix.p = M->pf.pmix;
@@ -579,13 +582,13 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
                                          xh, xl));
             cols3 = D.n_heads * D.head_dim;
         }
-        const int k3 = gemm_packed_ksplit(ctx, d, cols3);
+        const int k3 = gemm_packed_ksplit(ctx, d, cols3, T);
         TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xh, xl, T, M->pf.p0, k3));
         TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k3, L.post_attn_norm, nullptr, eps, xh, xl));
-        const int k4 = gemm_packed_ksplit(ctx, 2 * F, d);
+        const int k4 = gemm_packed_ksplit(ctx, 2 * F, d, T);
         TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xh, xl, T, M->pf.p1, k4));
         TRY(launch_silu_mul_stacked(ctx, s, T, (int)F, M->pf.p1, k4, nullptr, xh, xl));
-        const int k5 = gemm_packed_ksplit(ctx, d, F);
+        const int k5 = gemm_packed_ksplit(ctx, d, F, T);
         TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xh, xl, T, M->pf.p0, k5));
         if (l + 1 < D.n_layers)
             TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k5, M->layers[l + 1].attn_norm, nullptr, eps,

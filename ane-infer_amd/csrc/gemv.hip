@@ -1372,6 +1372,130 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
     } while (ct < tiles);
 }
 
+// x-stationary 32-wide GEMM with the split's panels shared by H groups of 4
+// waves: wave w takes column quarter w % 4 of panels ks * H * PW + (w / 4) * PW
+// .. + PW - 1, holds their A fragments (32 PW VGPRs) and streams its units
+// (4 quant vectors + 1 scale dword) D deep; a tile's sums are added over the
+// 4 H waves through LDS.  With H = 2 the split's x fragments (up to 8 panels)
+// fit in registers at two waves per SIMD, so lm_head needs no K split and no
+// x loads in its main loop.  Output as gemm_xs.
+template <uint32_t T, int PW, int D, int H>
+__global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_per_eu(2))) void gemm_xsh(
+    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+    const float *__restrict__ xrows, float *__restrict__ out, int m, int n, int batch, int ksplit,
+    size_t split_stride) {
+    constexpr int Q = GemmUnit<T, 1>::kQ;
+    constexpr int U = PW > D ? PW : D;
+    constexpr int NW = kGemmWaves * H;
+    static_assert(U % PW == 0 && U % D == 0, "ring and panel counts must divide the loop body");
+    __shared__ __align__(16) float red[NW][32][kWave];
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
+    const int gs = gridDim.x / ksplit;  // workgroups per split
+    const int ks = blockIdx.x % ksplit, g0 = blockIdx.x / ksplit;
+    if (g0 >= gs || g0 >= tiles) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int quarter = wave & 3, panel0 = (ks * H + (wave >> 2)) * PW;
+    const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
+    const __amdgpu_buffer_rsrc_t orsrc =
+        __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
+    h8v xa[PW][4], xb[PW][4];
+    const int brow = min(lane & 31, batch - 1);
+    if (xrows == nullptr) {
+        const size_t xbase = (size_t)(4 * quarter * kWave + brow + 32 * (lane >> 5)) * 8 + 16 * 512 * (size_t)panel0;
+#pragma unroll
+        for (int p = 0; p < PW; p++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                xa[p][st] = *reinterpret_cast<const h8v *>(xh + xbase + 16 * 512 * p + 512 * st);
+                xb[p][st] = *reinterpret_cast<const h8v *>(xl + xbase + 16 * 512 * p + 512 * st);
+            }
+    } else {
+        const float *xr = xrows + (size_t)brow * n;
+#pragma unroll
+        for (int p = 0; p < PW; p++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const int c0 = 16 * (16 * (panel0 + p) + 4 * quarter + st) + 8 * (lane >> 5);
+                const float4 a = *reinterpret_cast<const float4 *>(xr + c0);
+                const float4 b = *reinterpret_cast<const float4 *>(xr + c0 + 4);
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    xa[p][st][i] = (_Float16)v[i];
+                    xb[p][st][i] = (_Float16)(v[i] - (float)xa[p][st][i]);
+                }
+            }
+    }
+    const uint8_t *wpart = Wp + (size_t)panel0 * Panel<T>::kBytes;
+    int lt = g0, lp = 0;  // load cursor: tile, panel of the wave's part
+    auto load_next = [&](WUnit<T> &u) {
+        const u32x4 *p4 = reinterpret_cast<const u32x4 *>(wpart + (size_t)min(lt, tiles - 1) * tile_bytes +
+                                                          (size_t)lp * Panel<T>::kBytes);
+#pragma unroll
+        for (int c = 0; c < Q; c++) u.q[c] = __builtin_nontemporal_load(p4 + (Q * quarter + c) * kWave + lane);
+        u.sc = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p4 + Panel<T>::kChunks * kWave + lane) +
+                                          quarter);
+        const bool wrap = ++lp == PW;
+        lp = wrap ? 0 : lp;
+        lt = wrap ? lt + gs : lt;
+    };
+    WUnit<T> ring[D];
+#pragma unroll
+    for (int k = 0; k < D; k++) {
+        load_next(ring[k]);
+        asm volatile("" ::: "memory");
+    }
+    int ct = g0;  // tile being multiplied
+    f32x16 acc0 = {}, acc1 = {};
+    do {
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            WUnit<T> &u = ring[k % D];
+#pragma unroll
+            for (int c = 0; c < Q; c++) asm volatile("" : "+v"(u.q[c])::"memory");
+            asm volatile("" : "+v"(u.sc)::"memory");
+            mma_tile<T>(u.q, u.sc, xa[k % PW], xb[k % PW], acc0, acc1);
+            asm volatile("" : "+v"(acc0), "+v"(acc1)::"memory");
+            load_next(u);
+            if (k % PW == PW - 1) {
+                // tile done: park the 32 sums per lane (element r of lane l:
+                // batch row 8 (r / 4 % 4) + 4 (l / 32) + r % 4, tile row
+                // l % 32 + 32 (r / 16)); each thread then adds the NW waves'
+                // sums of 4-row vectors of one batch row and stores them
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    red[wave][r][lane] = acc0[r];
+                    red[wave][16 + r][lane] = acc1[r];
+                }
+                lds_barrier();
+#pragma unroll
+                for (int i = 0; i < 512 / (kWave * NW); i++) {
+                    const int v = threadIdx.x + kWave * NW * i;  // 512 vectors: batch row b, rows 4 j .. 4 j + 3
+                    const int b = v >> 4, j = v & 15;
+                    const int r = 4 * (b >> 3) + (b & 3) + (j >= 8 ? 16 : 0);
+                    const int l = ((4 * j) & 31) + 32 * ((b >> 2) & 1);
+                    float4 sum = *reinterpret_cast<const float4 *>(&red[0][r][l]);
+#pragma unroll
+                    for (int w = 1; w < NW; w++) {
+                        const float4 o = *reinterpret_cast<const float4 *>(&red[w][r][l]);
+                        sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
+                    }
+                    const int row = ct * kWave + 4 * j;
+                    const int off = b < batch && row < m && ct < tiles ? 4 * (ks * (int)split_stride + b * m + row)
+                                                                       : kBadOffset;
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0,
+                                                           kCpolDevice);
+                }
+                lds_barrier();  // red is free again
+                acc0 = f32x16{};
+                acc1 = f32x16{};
+                ct += gs;
+            }
+        }
+    } while (ct < tiles);
+}
+
 // fp32 x[batch][n] -> fragment-order fp16 planes hi, lo (hi + lo ~= x), one
 // thread per 8 consecutive columns of a row (one 16-byte fragment).
 __global__ __launch_bounds__(256) void split_x_frag_kernel(const float *__restrict__ x, _Float16 *__restrict__ hi,
@@ -1688,24 +1812,27 @@ int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, bool norm_
 }
 
 // K splits of the panel MFMA GEMM.  Matrices of fewer row tiles than CUs
-// take the x-stationary kernel with P = 2 panels per split (P = 1 when that
+// take an x-stationary kernel with P = 2 panels per split (P = 1 when that
 // grid would not reach two workgroups per CU, or for an odd panel count):
 // measured on MI355X at batch 4 and 32 it beats the persistent kernel on
 // every decode shape (12288 x 2048, batch 32: 10.4 us at k = 4 against
 // 11.9 us; 2048 x 2048: 3.9 us at k = 8 against 5.4 us), and P = 2 halves
 // the partial sums the consumer reads against P = 1 where the times tie.
+// Matrices of at least 4 tiles per CU: no split at batch <= 16 (the 16-wide
+// kernel holds 8 panels of x), splits of 4 panels above (lm_head at batch 32:
+// 74 us at k = 2 on gemm_xsh against 94 us unsplit on the persistent kernel).
 // Otherwise, among the even splits of at most kMaxSplit, the one that
 // minimises the panels of the busiest CU, ceil(items / CUs) x panels per
 // split, with single-panel splits counted double and ties going to fewer
-// splits; no split for matrices of at least 4 tiles per CU.
-int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+// splits.
+int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch) {
     const int tiles = (int)((m + kWave - 1) / kWave);
     const int nsb = (int)(n / 256), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     if (tiles < cus && nsb >= 2) {
         const int P = nsb % 2 == 0 && tiles * nsb > 2 * cus ? 2 : 1;
         if (nsb / P <= kMaxGemmSplit) return nsb / P;
     }
-    if (tiles >= 4 * cus) return 1;
+    if (tiles >= 4 * cus) return batch > 16 && nsb % 4 == 0 && nsb / 4 <= kMaxGemmSplit ? nsb / 4 : 1;
     int best = 1;
     double best_cost = 1e30;
     for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
@@ -1733,114 +1860,107 @@ int launch_gemm_packed_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, 
     return ANEHIP_OK;
 }
 
-// x-stationary grid for an even K split of P = nsb / ksplit panels (1 or 2):
-// a whole number of workgroups per split, about 3 per CU at P = 1 and 2 at
-// P = 2, each with one tile of weights in flight (deeper register rings and
-// more workgroups per split measured slower on every decode shape).
-template <uint32_t T, bool XROWS = false>
-void launch_gemm_xs_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
-                      const _Float16 *xh, const _Float16 *xl, const float *xrows, uint32_t batch, float *out,
-                      int ksplit, int per) {
-    const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const int gs = max(1, min(tiles, (per == 1 ? 3 : 2) * cus / ksplit));
-    const dim3 grid(gs * ksplit), block(kWave * kGemmWaves);
-    const size_t ss = (size_t)batch * m;
-    if (per == 1)
-        hipLaunchKernelGGL((gemm_xs<T, 1, 1, XROWS>), grid, block, 0, stream, w, xh, xl, xrows, out, (int)m, (int)n,
-                           (int)batch, ksplit, ss);
-    else
-        hipLaunchKernelGGL((gemm_xs<T, 2, 1, XROWS>), grid, block, 0, stream, w, xh, xl, xrows, out, (int)m, (int)n,
-                           (int)batch, ksplit, ss);
+// Which kernel runs an even or uneven K split of nsb panels at a batch size.
+// Batch <= 16: the 16-wide x-stationary kernel on splits of 1, 2, 4 or 8
+// panels.  Batch 17-32: gemm_xsh (8 waves, the split's panels shared by two
+// groups of 4) on splits of 2 or 4 panels, gemm_xs on single-panel splits.
+// Measured on MI355X against the 4-wave x-stationary kernel at P = 2, batch
+// 17 / 32: 12288 x 2048 8.7 / 8.8 us against 9.2 / 9.6, 6144 x 2048 6.4 / 6.7
+// against 6.8 / 7.1, 2048 x 6144 6.4 / 6.7 against 6.7 / 7.2.  Everything
+// else (uneven splits) on the persistent kernel.
+enum class GemmKernel { Persistent, Xs16, Xs32, Xsh };
+static GemmKernel gemm_kernel(uint32_t batch, int nsb, int ksplit) {
+    const int per = nsb / ksplit;
+    if (per * ksplit != nsb) return GemmKernel::Persistent;
+    if (batch <= 16) return per == 1 || per == 2 || per == 4 || per == 8 ? GemmKernel::Xs16 : GemmKernel::Persistent;
+    if (per == 2 || per == 4) return GemmKernel::Xsh;
+    if (per == 1 && ksplit >= 2) return GemmKernel::Xs32;
+    return GemmKernel::Persistent;
 }
 
-// The 16-wide x-stationary kernel takes batch <= 16 on an even split of 1, 2,
-// 4 or 8 panels per split (its A fragments: 16 VGPRs per panel).  Grids,
-// measured on MI355X at batch 4 and 16: P = 1 four workgroups per CU with one
-// unit in flight (a smaller register file), P >= 2 two per CU with two.
-// Against the 32-wide kernels at batch 4 / 16: 6144 x 2048 5.1 / 5.7 us
-// (P = 1) against 5.7 / 6.0; 12288 x 2048 7.4 / 7.9 (P = 2) against 8.7 / 8.8;
-// lm_head 151936 x 2048 60-65 us (P = 8) against 67-73.
-static bool xs16_split(uint32_t batch, int nsb, int ksplit) {
-    const int per = nsb / ksplit;
-    return batch <= 16 && per * ksplit == nsb && (per == 1 || per == 2 || per == 4 || per == 8);
-}
-static bool xs32_split(int nsb, int ksplit) {
-    const int per = nsb / ksplit;
-    return ksplit >= 2 && per * ksplit == nsb && per <= 2;
-}
-
+// Grids (measured on MI355X at batch 4 to 32): gemm_xs16 four workgroups per
+// CU at P = 1 (one unit in flight, a small register file), two at P >= 2
+// (two in flight); gemm_xs three per CU; gemm_xsh one 8-wave workgroup per CU
+// with one unit in flight at 1 panel per wave, two at 2.  A whole number of
+// workgroups per split in every case.
 template <uint32_t T>
-void launch_gemm_xs16_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
-                        const _Float16 *xh, const _Float16 *xl, const float *xrows, uint32_t batch, float *out,
-                        int ksplit) {
+void launch_gemm_xs_any(anehip_ctx *ctx, hipStream_t stream, GemmKernel kind, const uint8_t *w, uint32_t m,
+                        uint32_t n, const _Float16 *xh, const _Float16 *xl, const float *xrows, uint32_t batch,
+                        float *out, int ksplit) {
     const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const int per = (int)(n / 256) / ksplit;
-    const int gs = max(1, min(tiles, (per == 1 ? 4 : 2) * cus / ksplit));
-    const dim3 grid(gs * ksplit), block(kWave * kGemmWaves);
     const size_t ss = (size_t)batch * m;
-#define ANEHIP_XS16(P, D, W)                                                                                         \
-    hipLaunchKernelGGL((gemm_xs16<T, P, D, W>), grid, block, 0, stream, w, xh, xl, xrows, out, (int)m, (int)n,      \
-                       (int)batch, ksplit, ss)
-    if (per == 1)
-        ANEHIP_XS16(1, 1, 4);
-    else if (per == 2)
-        ANEHIP_XS16(2, 2, 2);
-    else if (per == 4)
-        ANEHIP_XS16(4, 2, 2);
-    else
-        ANEHIP_XS16(8, 2, 2);
-#undef ANEHIP_XS16
+    const int wgs = kind == GemmKernel::Xs16 ? (per == 1 ? 4 : 2) : kind == GemmKernel::Xs32 ? 3 : 1;
+    const int gs = max(1, min(tiles, wgs * cus / ksplit));
+    const dim3 grid(gs * ksplit), block(kWave * kGemmWaves);
+#define ANEHIP_XS(KERNEL, NT)                                                                                       \
+    hipLaunchKernelGGL(KERNEL, grid, dim3(NT), 0, stream, w, xh, xl, xrows, out, (int)m, (int)n, (int)batch, ksplit, ss)
+    if (kind == GemmKernel::Xs16) {
+        if (per == 1)
+            ANEHIP_XS((gemm_xs16<T, 1, 1, 4>), 256);
+        else if (per == 2)
+            ANEHIP_XS((gemm_xs16<T, 2, 2, 2>), 256);
+        else if (per == 4)
+            ANEHIP_XS((gemm_xs16<T, 4, 2, 2>), 256);
+        else
+            ANEHIP_XS((gemm_xs16<T, 8, 2, 2>), 256);
+    } else if (kind == GemmKernel::Xsh) {
+        if (per == 2)
+            ANEHIP_XS((gemm_xsh<T, 1, 1, 2>), 512);
+        else
+            ANEHIP_XS((gemm_xsh<T, 2, 2, 2>), 512);
+    } else if (xrows) {
+        ANEHIP_XS((gemm_xs<T, 1, 1, true>), 256);
+    } else {
+        ANEHIP_XS((gemm_xs<T, 1, 1, false>), 256);
+    }
+#undef ANEHIP_XS
 }
 
 bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch) {
-    const int k = gemm_packed_ksplit(ctx, m, n), nsb = (int)(n / 256);
-    return xs16_split(batch, nsb, k) || xs32_split(nsb, k);
+    return gemm_kernel(batch, (int)(n / 256), gemm_packed_ksplit(ctx, m, n, batch)) != GemmKernel::Persistent;
+}
+
+static int check_gemm_args(anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch, int ksplit) {
+    const int nsb = (int)(n / 256), per = split_len(nsb, ksplit);
+    if (ksplit < 1 || (ksplit - 1) * per >= nsb || batch < 1 || batch > 32 || m % 4)
+        return set_error(ctx->err, ANEHIP_EINVAL,
+                         "gemm: K split %d of %d super-blocks, batch %u or m %u (multiple of 4) unsupported", ksplit,
+                         nsb, batch, m);
+    if (4.0 * ksplit * batch * m > 1073741824.0)  // output byte offsets stay below kBadOffset
+        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
+    return ANEHIP_OK;
 }
 
 int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                         uint32_t n, const float *x, uint32_t batch, float *out) {
-    if (batch < 1 || batch > 32 || m % 4 || !gemm_is_xs(ctx, m, n, batch))
+    const int ksplit = gemm_packed_ksplit(ctx, m, n, batch);
+    if (int rc = check_gemm_args(ctx, m, n, batch, ksplit)) return rc;
+    const GemmKernel kind = gemm_kernel(batch, (int)(n / 256), ksplit);
+    if (kind == GemmKernel::Persistent)
         return set_error(ctx->err, ANEHIP_EINVAL, "gemm: %u x %u at batch %u is not an x-stationary shape", m, n,
                          batch);
-    const int ksplit = gemm_packed_ksplit(ctx, m, n), per = (int)(n / 256) / ksplit;
-    if (4.0 * ksplit * batch * m > 1073741824.0)
-        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
-    const bool q8 = ggml_type == ANEHIP_GGML_Q8_0;
-    if (xs16_split(batch, (int)(n / 256), ksplit)) {
-        if (q8)
-            launch_gemm_xs16_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit);
-        else
-            launch_gemm_xs16_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit);
-    } else if (q8) {
-        launch_gemm_xs_t<ANEHIP_GGML_Q8_0, true>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit, per);
-    } else {
-        launch_gemm_xs_t<ANEHIP_GGML_Q4_0, true>(ctx, stream, w, m, n, nullptr, nullptr, x, batch, out, ksplit, per);
-    }
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, nullptr, nullptr, x, batch, out, ksplit);
+    else
+        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, nullptr, nullptr, x, batch, out, ksplit);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                        uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit) {
+    if (int rc = check_gemm_args(ctx, m, n, batch, ksplit)) return rc;
     const int per = split_len((int)(n / 256), ksplit);
-    if (ksplit < 1 || (ksplit - 1) * per >= (int)(n / 256) || batch < 1 || batch > 32 || m % 4)
-        return set_error(ctx->err, ANEHIP_EINVAL,
-                         "gemm: K split %d of %u super-blocks, batch %u or m %u (multiple of 4) unsupported", ksplit,
-                         n / 256, batch, m);
-    if (4.0 * ksplit * batch * m > 1073741824.0)  // output byte offsets stay below kBadOffset
-        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
-    const bool xs = xs32_split((int)(n / 256), ksplit);
-    if (xs16_split(batch, (int)(n / 256), ksplit) && ggml_type == ANEHIP_GGML_Q8_0)
-        launch_gemm_xs16_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit);
-    else if (xs16_split(batch, (int)(n / 256), ksplit))
-        launch_gemm_xs16_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit);
-    else if (xs && ggml_type == ANEHIP_GGML_Q8_0)
-        launch_gemm_xs_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit, per);
-    else if (xs)
-        launch_gemm_xs_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, nullptr, batch, out, ksplit, per);
-    else if (ggml_type == ANEHIP_GGML_Q8_0)
+    const GemmKernel kind = gemm_kernel(batch, (int)(n / 256), ksplit);
+    const bool q8 = ggml_type == ANEHIP_GGML_Q8_0;
+    if (kind != GemmKernel::Persistent && q8)
+        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, xh, xl, nullptr, batch, out, ksplit);
+    else if (kind != GemmKernel::Persistent)
+        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, xh, xl, nullptr, batch, out, ksplit);
+    else if (q8)
         launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
     else
         launch_gemm_packed_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);

@@ -222,7 +222,7 @@ int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
     if (batch == 0 || batch > 32)
         return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: batch=%u outside 1..32", batch);
     if (batch == 1) return anehip_quant_gemv_packed(ctx, ggml_type, wp, m, n, x, y);
-    const int ksplit = gemm_packed_ksplit(ctx, m, n);
+    const int ksplit = gemm_packed_ksplit(ctx, m, n, batch);
     if (m % 4)
         return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: m=%u must be a multiple of 4 for batch > 1",
                          m);

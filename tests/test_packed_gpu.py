@@ -115,8 +115,9 @@ def test_packed_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
     """Panel MFMA GEMM, ragged batch (not padded to the 32-row MFMA tile), at
     the decode shapes, a tiny matrix and an odd panel count (12288 x 1792).
     Batch <= 16 runs on the 16-wide x-stationary kernel wherever the split
-    has 1, 2, 4 or 8 panels, batch 17 and 32 on the 32-wide kernels.
-    Covers both 32-wide kernels and both x-stationary forms: 2 panels per K split
+    has 1, 2, 4 or 8 panels; batch 17 and 32 on the 8-wave x-stationary kernel
+    for splits of 2 panels, the 4-wave one for single-panel splits and the
+    persistent kernel otherwise.  Shapes: 2 panels per K split
     (6144 x 2048, 2048 x 6144 at 12 splits, 8224 x 2048 with a ragged last
     tile), 1 panel (2048 x 2048, 100 x 512, the odd 12288 x 1792), the
     persistent kernel (100 x 256; 1024 x 8192, whose 32 single-panel splits
@@ -137,14 +138,15 @@ def test_packed_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("t,m,n,batch", [(8, 151936, 2048, 32), (8, 151936, 2048, 4), (8, 151936, 2048, 16),
-                                         (2, 151936, 2048, 11), (8, 65600, 1024, 16), (2, 65600, 1024, 5)])
+@pytest.mark.parametrize("t,m,n,batch", [(8, 151936, 2048, 32), (2, 151936, 2048, 19), (8, 151936, 2048, 4),
+                                         (8, 151936, 2048, 16), (2, 151936, 2048, 11), (8, 65600, 1024, 16),
+                                         (2, 65600, 1024, 5)])
 def test_packed_gemm_many_tiles(gpu_ctx, oracle_lib, t, m, n, batch):
-    """Matrices of at least 4 row tiles per CU (no K split): lm_head on the
-    persistent 32-wide kernel at batch 32 and on the 16-wide x-stationary
-    kernel with 8 panels per workgroup at batch <= 16; 4 panels (n = 1024)
-    with a ragged last tile.  Checked on the first, a middle and the last
-    batch row."""
+    """Matrices of at least 4 row tiles per CU: lm_head unsplit on the 16-wide
+    x-stationary kernel with 8 panels per workgroup at batch <= 16, and at
+    batch 32 in two K splits of 4 panels on the 8-wave kernel (gemm_xsh, 2
+    panels per wave); n = 1024 (4 panels, unsplit at batch <= 16) with a
+    ragged last tile.  Checked on the first, a middle and the last batch row."""
     w = oracle_lib.gen_quant(t, 6, 6 + m % 7, m, n, std=0.02)
     x = oracle_lib.normal(6, 7 + batch, batch * n).reshape(batch, n)
     dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
