@@ -573,7 +573,7 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
         if (dn) {
             TRY(launch_deltanet_scan(ctx, s, T, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
                                      L.conv1d, L.ssm_a, L.dt_bias, L.conv_state + (size_t)seq * C * kConvK,
-                                     L.S + (size_t)seq * H * kDk * kDk, (int)C, L.ssm_norm, eps, xh, xl));
+                                     L.S + (size_t)seq * H * kDk * kDk, M->pf.xn, (int)C, L.ssm_norm, eps, xh, xl));
             cols3 = d;
         } else {
             const size_t cache_off = (size_t)seq * D.n_kv_heads * M->max_seq * D.head_dim;

@@ -34,10 +34,25 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float silu_ref(float x) { return x / (1.0f + expf(-x)); }
 
+// Cross-lane sums on DPP (VALU, no LDS round trip).  Each step adds a lane's
+// value to its partner's, and partners get the same two operands, so every
+// lane of a group ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf,
+                                                                     false));
+}
+// sum over each group of 8 lanes: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror
+__device__ __forceinline__ float sum8(float v) { return dpp_add<0x141>(dpp_add<0x4E>(dpp_add<0xB1>(v))); }
+// sum over the wave: row_ror 8, 4, 2, 1 sums each 16-lane row, then the 4 rows
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v = dpp_add<0x128>(v);
+    v = dpp_add<0x124>(v);
+    v = dpp_add<0x122>(v);
+    v = dpp_add<0x121>(v);
+    const int b = __builtin_bit_cast(int, v);
+    const auto row = [&](int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, lane)); };
+    return (row(0) + row(16)) + (row(32) + row(48));
 }
 
 // grid = (dv / 32, n_heads, batch).  mix / mbeta / malpha: the qkv, beta and
@@ -359,164 +374,195 @@ __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
     out_lo[xo] = (_Float16)(v - (float)hi);
 }
 
-// Prefill: T consecutive tokens of one sequence (mix row t = token t), one
-// workgroup per head holding the head's 128 x 128 state in registers across
-// all T steps (read and written once per chunk instead of once per token).
-// Token t's step is deltanet_head_kernel's step with the conv window shifted
-// by that token's input; row t of the gated RMSNorm goes to the planes.
-// conv_state / S: the sequence's own blocks.  grid = n_heads.
-template <int KP>
-__global__ __launch_bounds__(kThreads) void deltanet_scan_kernel(
-    MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
-    const float *__restrict__ dt_bias, float *__restrict__ cs, float *__restrict__ S, int gate_off,
-    const float *__restrict__ norm_w, float eps, _Float16 *__restrict__ out_hi, _Float16 *__restrict__ out_lo,
-    int n_heads, int T) {
-    __shared__ float qn[kDk], kn[kDk], vv[kDk];
-    __shared__ __align__(16) float part[8][kDk];
-    __shared__ float red[4];
+// Prefill: T consecutive tokens of one sequence (mix row t = token t).  The
+// recurrence is independent per value column j (recall sk_j, delta_j, column
+// j of the rank-1 update and the query o_j), so a head is split over
+// kScanGroups single-wave workgroups of kScanCols columns each, grid =
+// (kScanGroups, n_heads): 16 x more waves than one workgroup per head, and no
+// cross-wave barrier in the token loop.  Lane l holds rows 16 (l % 8) .. + 15
+// of column 8 g + l / 8 in registers across all T steps (state read and
+// written once per chunk); the sums over rows are a lane-local sum of 16 and
+// a DPP sum over the column's 8 consecutive lanes.  Every wave forms the token's normalised
+// q and k itself (lane l: channels l and 64 + l of each, conv windows in
+// registers) and its columns' v.  Raw head outputs go to out[t][chunk]; the
+// gated RMSNorm and the conv-window commit follow in dn_scan_finish_kernel.
+constexpr int kWave = 64;
+constexpr int kScanCols = 8;
+constexpr int kScanGroups = kDk / kScanCols;
 
-    const int t = threadIdx.x, h = blockIdx.x;
+template <int KP>
+__global__ __launch_bounds__(kWave) void deltanet_scan_kernel(
+    MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
+    const float *__restrict__ dt_bias, const float *__restrict__ cs, float *__restrict__ S,
+    float *__restrict__ out, int n_heads, int T) {
+    __shared__ __align__(16) float qs[kDk], ks[kDk];
+    const int l = threadIdx.x, h = blockIdx.y;
     const int chunk = n_heads * kDk;
-    const int cq = t & 31, rg = t >> 5, e = t & (kDk - 1);
-    float *Sh = S + (size_t)h * kDk * kDk + 4 * cq;
-    const int ch = t < kDk ? h * kDk + t : chunk + h * kDk + e, chv = 2 * chunk + h * kDk + e;
-    f32x4 win = *reinterpret_cast<const f32x4 *>(cs + (size_t)ch * kKsize);
-    const f32x4 wk = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)ch * kKsize);
+    const int rgp = l & 7, j = blockIdx.x * kScanCols + (l >> 3);
+    float *Sh = S + (size_t)h * kDk * kDk + j;
+    // q / k channels of this lane and the v channel of its column
+    const int chq[4] = {h * kDk + l, h * kDk + 64 + l, chunk + h * kDk + l, chunk + h * kDk + 64 + l};
+    const int chv = 2 * chunk + h * kDk + j;
+    f32x4 win[4], wk[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        win[c] = *reinterpret_cast<const f32x4 *>(cs + (size_t)chq[c] * kKsize);
+        wk[c] = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)chq[c] * kKsize);
+    }
     f32x4 winv = *reinterpret_cast<const f32x4 *>(cs + (size_t)chv * kKsize);
     const f32x4 wkv = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)chv * kKsize);
-    const float sa = ssm_a[h], dtb = dt_bias[h], nw = norm_w[e];
-    float4 s[16];
+    const float sa = ssm_a[h], dtb = dt_bias[h];
+    float st[16];
 #pragma unroll
-    for (int r = 0; r < 16; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(16 * rg + r) * kDk);
+    for (int r = 0; r < 16; r++) st[r] = Sh[(size_t)(16 * rgp + r) * kDk];
 
     // inputs of token `tok`, loaded one token ahead of their use
-    float xa[KP], xv[KP], xg[KP], xb[KP], xal[KP];
+    float xq[4][KP], xv[KP], xb[KP], xal[KP];
     auto load_in = [&](int tok) {
-        mix.load<KP>(tok, ch, xa);
+#pragma unroll
+        for (int c = 0; c < 4; c++) mix.load<KP>(tok, chq[c], xq[c]);
         mix.load<KP>(tok, chv, xv);
-        mix.load<KP>(tok, gate_off + h * kDk + e, xg);
         mbeta.load<KP>(tok, h, xb);
         malpha.load<KP>(tok, h, xal);
     };
+    const auto conv = [](f32x4 w0, f32x4 k) {
+        float sum = 0.0f;
+        sum += w0.x * k.x;
+        sum += w0.y * k.y;
+        sum += w0.z * k.z;
+        sum += w0.w * k.w;
+        return silu_ref(sum);
+    };
     load_in(0);
     for (int tok = 0; tok < T; tok++) {
-        // this token's inputs; the next token's loads go out now
-        const float x = mix.add<KP>(xa), x2 = mix.add<KP>(xv), gt = mix.add<KP>(xg);
+        float y[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            win[c] = f32x4{win[c].y, win[c].z, win[c].w, mix.add<KP>(xq[c])};
+            y[c] = conv(win[c], wk[c]);
+        }
+        winv = f32x4{winv.y, winv.z, winv.w, mix.add<KP>(xv)};
+        const float v = conv(winv, wkv);
         const float br = mbeta.add<KP>(xb), ar = malpha.add<KP>(xal);
         load_in(min(tok + 1, T - 1));
-        // 1. conv + SiLU over the window shifted by this token's input
-        // (conv_shift_and_append + conv_apply, deltanet_cache.rs:34-54)
-        win = f32x4{win.y, win.z, win.w, x};
-        winv = f32x4{winv.y, winv.z, winv.w, x2};
-        const auto conv = [](f32x4 w0, f32x4 k) {
-            float sum = 0.0f;
-            sum += w0.x * k.x;
-            sum += w0.y * k.y;
-            sum += w0.z * k.z;
-            sum += w0.w * k.w;
-            return silu_ref(sum);
-        };
-        {
-            const float y = conv(win, wk);
-            const float sq = wave_sum(y * y);
-            if ((t & 63) == 0) red[t >> 6] = sq;
-            if (t < kDk) qn[t] = y;
-            else kn[e] = y;
-            if (t < kDk) vv[t] = conv(winv, wkv);
-        }
+        // L2 normalise q (and scale by 1/sqrt(dk)) and k (deltanet.rs:25-31, 461-467)
+        const float inq = 1.0f / sqrtf(wave_sum(y[0] * y[0] + y[1] * y[1]) + 1e-12f);
+        const float ink = 1.0f / sqrtf(wave_sum(y[2] * y[2] + y[3] * y[3]) + 1e-12f);
+        const float scale = 1.0f / sqrtf((float)kDk);
+        __syncthreads();  // the previous token's reads of qs / ks are done
+        qs[l] = (y[0] * inq) * scale;
+        qs[64 + l] = (y[1] * inq) * scale;
+        ks[l] = y[2] * ink;
+        ks[64 + l] = y[3] * ink;
         // deltanet.rs:474-480
         const float beta = 1.0f / (1.0f + expf(-br));
         const float decay = expf(sa * logf(1.0f + expf(ar + dtb)));
         __syncthreads();
-        // 2. L2 normalise (deltanet.rs:25-31, 461-467)
-        if (t < kDk) {
-            const float inv = 1.0f / sqrtf((red[0] + red[1]) + 1e-12f);
-            const float scale = 1.0f / sqrtf((float)kDk);
-            qn[t] = (qn[t] * inv) * scale;
-        } else {
-            const float inv = 1.0f / sqrtf((red[2] + red[3]) + 1e-12f);
-            kn[e] = kn[e] * inv;
+        float kr[16], qr[16];
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) {
+            const float4 k4 = *reinterpret_cast<const float4 *>(&ks[16 * rgp + r]);
+            const float4 q4 = *reinterpret_cast<const float4 *>(&qs[16 * rgp + r]);
+            kr[r] = k4.x, kr[r + 1] = k4.y, kr[r + 2] = k4.z, kr[r + 3] = k4.w;
+            qr[r] = q4.x, qr[r + 1] = q4.y, qr[r + 2] = q4.z, qr[r + 3] = q4.w;
         }
-        __syncthreads();
-        // 3. S' = decay * S, partial recall over this thread's rows
-        float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
+        // S' = decay S; sk_j = sum_i S'_ij k_i
+        float sk = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const float ki = kn[16 * rg + r];
-            s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
-            sk.x += s[r].x * ki; sk.y += s[r].y * ki; sk.z += s[r].z * ki; sk.w += s[r].w * ki;
+            st[r] *= decay;
+            sk += st[r] * kr[r];
         }
-        *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = sk;
-        __syncthreads();
-        float4 delta;
-        {
-            float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int g = 0; g < 8; g++) {
-                float4 p = *reinterpret_cast<const float4 *>(&part[g][4 * cq]);
-                acc[0] += p.x; acc[1] += p.y; acc[2] += p.z; acc[3] += p.w;
-            }
-            delta.x = beta * (vv[4 * cq + 0] - acc[0]);
-            delta.y = beta * (vv[4 * cq + 1] - acc[1]);
-            delta.z = beta * (vv[4 * cq + 2] - acc[2]);
-            delta.w = beta * (vv[4 * cq + 3] - acc[3]);
-        }
-        __syncthreads();  // part[] is reused below
-        // S'' = S' + k delta^T, partial query
-        float4 so = make_float4(0.f, 0.f, 0.f, 0.f);
+        sk = sum8(sk);  // over the 8 row groups (lane bits 0-2)
+        const float delta = beta * (v - sk);
+        // S'' = S' + k delta^T; o_j = sum_i S''_ij q_i
+        float o = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const float ki = kn[16 * rg + r], qi = qn[16 * rg + r];
-            s[r].x += ki * delta.x; s[r].y += ki * delta.y; s[r].z += ki * delta.z; s[r].w += ki * delta.w;
-            so.x += s[r].x * qi; so.y += s[r].y * qi; so.z += s[r].z * qi; so.w += s[r].w * qi;
+            st[r] += kr[r] * delta;
+            o += st[r] * qr[r];
         }
-        *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = so;
-        __syncthreads();
-        // 4. head output, gated RMSNorm (deltanet.rs:517-533) -> planes row tok
-        float o = 0.f;
-        if (t < kDk) {
-#pragma unroll
-            for (int g = 0; g < 8; g++) o += part[g][t];
-        }
-        const float ss = wave_sum(o * o);  // waves 2-3 contribute zeros
-        __syncthreads();                   // red[] is reused
-        if ((t & 63) == 0) red[t >> 6] = ss;
-        __syncthreads();
-        if (t < kDk) {
-            const float inv_rms = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + eps);
-            const float v = ((o * inv_rms) * nw) * (gt / (1.0f + expf(-gt)));
-            const size_t xo = xf_index(tok, h * kDk + t);
-            const _Float16 hi = (_Float16)v;
-            out_hi[xo] = hi;
-            out_lo[xo] = (_Float16)(v - (float)hi);
-        }
-        __syncthreads();  // qn / kn / vv / red are rewritten by the next token
+        o = sum8(o);
+        if (rgp == 0) out[(size_t)tok * chunk + h * kDk + j] = o;
     }
-    // the state and the windows after the last token
 #pragma unroll
-    for (int r = 0; r < 16; r++) *reinterpret_cast<float4 *>(Sh + (size_t)(16 * rg + r) * kDk) = s[r];
-    *reinterpret_cast<float4 *>(cs + (size_t)ch * kKsize) = make_float4(win.x, win.y, win.z, win.w);
-    if (t < kDk) *reinterpret_cast<float4 *>(cs + (size_t)chv * kKsize) = make_float4(winv.x, winv.y, winv.z, winv.w);
+    for (int r = 0; r < 16; r++) Sh[(size_t)(16 * rgp + r) * kDk] = st[r];
+}
+
+// After deltanet_scan_kernel: row b of the gated RMSNorm (deltanet.rs:517-533)
+// of the raw head outputs to the planes, and (row 0's workgroups) the conv
+// windows of the head's q, k and v channels after the T tokens: the last
+// kKsize values of (old window, the T inputs).  grid = (n_heads, T), 128 threads.
+template <int KP>
+__global__ __launch_bounds__(kDk) void dn_scan_finish_kernel(MixIn mix, float *__restrict__ conv_state,
+                                                             const float *__restrict__ heads, int gate_off,
+                                                             const float *__restrict__ norm_w,
+                                                             _Float16 *__restrict__ out_hi,
+                                                             _Float16 *__restrict__ out_lo, int n_heads, float eps,
+                                                             int T) {
+    __shared__ float red[2];
+    const int t = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
+    const int chunk = n_heads * kDk;
+    // every load first (partial slices clamped to the last one, window
+    // sources clamped to row 0; unused values are discarded)
+    float xg[KP];
+    mix.load<KP>(b, gate_off + h * kDk + t, xg);
+    const float x = heads[(size_t)b * chunk + h * kDk + t];
+    if (b == 0) {
+        f32x4 old[3];
+        float xw[3][kKsize][KP];
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            old[c] = *reinterpret_cast<const f32x4 *>(conv_state + (size_t)(c * chunk + h * kDk + t) * kKsize);
+#pragma unroll
+            for (int i = 0; i < kKsize; i++) mix.load<KP>(max(T - kKsize + i, 0), c * chunk + h * kDk + t, xw[c][i]);
+        }
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            const float ov[kKsize] = {old[c].x, old[c].y, old[c].z, old[c].w};
+            float nv[kKsize];
+#pragma unroll
+            for (int i = 0; i < kKsize; i++) {
+                const int src = T - kKsize + i;  // < 0: from the old window
+                nv[i] = src >= 0 ? mix.add<KP>(xw[c][i]) : ov[(kKsize + src) & (kKsize - 1)];
+            }
+            *reinterpret_cast<f32x4 *>(conv_state + (size_t)(c * chunk + h * kDk + t) * kKsize) =
+                f32x4{nv[0], nv[1], nv[2], nv[3]};
+        }
+    }
+    const float ss = wave_sum(x * x);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float inv_rms = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + eps);
+    const float g = mix.add<KP>(xg);
+    const float v = ((x * inv_rms) * norm_w[t]) * (g / (1.0f + expf(-g)));
+    const size_t o = xf_index(b, h * kDk + t);
+    const _Float16 hi = (_Float16)v;
+    out_hi[o] = hi;
+    out_lo[o] = (_Float16)(v - (float)hi);
 }
 
 }  // namespace
 
 int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
-                         const float *dt_bias, float *conv_state, float *S, int gate_off, const float *norm_w,
-                         float eps, _Float16 *out_hi, _Float16 *out_lo) {
+                         const float *dt_bias, float *conv_state, float *S, float *heads, int gate_off,
+                         const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo) {
     const int kp = max(mix.kp, max(beta.kp, alpha.kp));
     if (kp > 16 || rows < 1 || rows > 32)
         return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_scan: %d K splits (at most 16), %d rows (1..32)", kp, rows);
 #define DN_SCAN(KP)                                                                                                  \
-    hipLaunchKernelGGL(deltanet_scan_kernel<KP>, dim3(n_heads), dim3(kThreads), 0, stream, mix, beta, alpha, conv_w, \
-                       ssm_a, dt_bias, conv_state, S, gate_off, norm_w, eps, out_hi, out_lo, n_heads, rows)
-    if (kp <= 1)
+    hipLaunchKernelGGL(deltanet_scan_kernel<KP>, dim3(kScanGroups, n_heads), dim3(kWave), 0, stream, mix, beta,      \
+                       alpha, conv_w, ssm_a, dt_bias, conv_state, S, heads, n_heads, rows);                          \
+    hipLaunchKernelGGL(dn_scan_finish_kernel<KP>, dim3(n_heads, rows), dim3(kDk), 0, stream, mix, conv_state, heads, \
+                       gate_off, norm_w, out_hi, out_lo, n_heads, eps, rows)
+    if (kp <= 1) {
         DN_SCAN(1);
-    else if (kp <= 4)
+    } else if (kp <= 4) {
         DN_SCAN(4);
-    else
+    } else {
         DN_SCAN(16);
+    }
 #undef DN_SCAN
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
