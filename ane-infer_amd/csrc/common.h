@@ -225,15 +225,17 @@ int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *out, int gate_off,
                          const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo);
-// Prefill: `rows` consecutive tokens of one sequence (mix row t = token t)
-// through the DeltaNet step of every head, the state (the sequence's block S)
-// kept in registers across the rows; raw head outputs to heads [rows][chunk]
-// (scratch), then row t's gated RMSNorm to the planes and the conv windows
-// (the sequence's block conv_state) advanced by the rows.  Two kernels.
+// Prefill: `rows` (<= 32) consecutive tokens of one sequence (mix row t =
+// token t) through the DeltaNet step of every head, the state (the sequence's
+// block S) kept in registers across the rows.  Three kernels: every token's
+// normalised q, k, v, beta and decay to prep (scratch of rows * (3 * dim + 2 *
+// n_heads) floats); the recurrence, raw head outputs to heads [rows][dim]
+// (scratch); row t's gated RMSNorm to the planes and the conv windows (the
+// sequence's block conv_state) advanced by the rows.
 int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
-                         const float *dt_bias, float *conv_state, float *S, float *heads, int gate_off,
-                         const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo);
+                         const float *dt_bias, float *conv_state, float *S, float *prep, float *heads,
+                         int gate_off, const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo);
 // Commits the q/k conv windows (if conv_state) and, if heads, writes the gated
 // RMSNorm of the heads (gate from mix rows at gate_off) to out (fp32) or, if
 // out_hi, to fragment-order fp16 hi/lo planes out_hi / out_lo (xf_index).

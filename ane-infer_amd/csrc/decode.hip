@@ -502,13 +502,15 @@ int pack_weights(anehip_ctx *ctx, Model *M) {
 constexpr uint32_t kPrefillRows = 32;  // tokens per prefill chunk (rows of the MFMA GEMM)
 
 // K-split partial floats of the prefill's GEMMs at up to kPrefillRows rows
-// (the split depends on the rows only through rows <= 16 or not) and of the
-// batch-1 lm_head GEMV.
+// (the split depends on the rows only through rows <= 16 or not), of the
+// batch-1 lm_head GEMV, and the DeltaNet scan's per-token inputs (q, k, v,
+// beta, decay; kept in the ffn partial buffer, which is free at that point).
 size_t prefill_part_floats(anehip_ctx *ctx, Model *M) {
     const anehip_model_desc &D = M->desc;
     const uint32_t d = D.dim, F = D.hidden_dim;
     const uint32_t g[][2] = {{M->rows_dn, d}, {M->rows_attn, d}, {d, d}, {d, D.n_heads * D.head_dim}, {2 * F, d}, {d, F}};
     size_t mx = (size_t)gemv_packed_ksplit(ctx, D.vocab_size, d, false) * D.vocab_size;
+    mx = std::max(mx, (size_t)kPrefillRows * (3 * d + 2 * D.ssm_group_count));
     for (auto &e : g)
         for (uint32_t rows : {16u, kPrefillRows})
             if (e[0]) mx = std::max(mx, (size_t)gemm_packed_ksplit(ctx, e[0], e[1], rows) * rows * e[0]);
@@ -573,7 +575,8 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
         if (dn) {
             TRY(launch_deltanet_scan(ctx, s, T, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
                                      L.conv1d, L.ssm_a, L.dt_bias, L.conv_state + (size_t)seq * C * kConvK,
-                                     L.S + (size_t)seq * H * kDk * kDk, M->pf.xn, (int)C, L.ssm_norm, eps, xh, xl));
+                                     L.S + (size_t)seq * H * kDk * kDk, M->pf.p1, M->pf.xn, (int)C, L.ssm_norm,
+                                     eps, xh, xl));
             cols3 = d;
         } else {
             const size_t cache_off = (size_t)seq * D.n_kv_heads * M->max_seq * D.head_dim;

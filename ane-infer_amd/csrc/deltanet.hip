@@ -374,116 +374,155 @@ __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
     out_lo[xo] = (_Float16)(v - (float)hi);
 }
 
-// Prefill: T consecutive tokens of one sequence (mix row t = token t).  The
-// recurrence is independent per value column j (recall sk_j, delta_j, column
-// j of the rank-1 update and the query o_j), so a head is split over
+// Prefill: T consecutive tokens of one sequence (mix row t = token t), in
+// three kernels.  Only the state is recurrent: the conv over time, the q / k
+// L2 norms, v, beta and the decay of every token are independent, so
+// dn_prep_kernel forms them for all (token, head) pairs at once; the scan then
+// runs the recurrence alone; dn_scan_finish_kernel applies the gated RMSNorm
+// and commits the conv windows.
+
+// Token b's conv taps for channel ch: the last kKsize values of (the old
+// window, the inputs of tokens 0..b) (conv_shift_and_append + conv_apply,
+// deltanet_cache.rs:34-54), then SiLU.
+template <int KP>
+__device__ __forceinline__ float conv_token(const MixIn &mix, const float *__restrict__ cs,
+                                            const float *__restrict__ conv_w, int ch, int b) {
+    const f32x4 old = *reinterpret_cast<const f32x4 *>(cs + (size_t)ch * kKsize);
+    const f32x4 wk = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)ch * kKsize);
+    float xs[kKsize][KP];
+#pragma unroll
+    for (int i = 0; i < kKsize; i++) mix.load<KP>(max(b - kKsize + 1 + i, 0), ch, xs[i]);
+    const float ov[kKsize] = {old.x, old.y, old.z, old.w};
+    const float kw[kKsize] = {wk.x, wk.y, wk.z, wk.w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kKsize; i++) {
+        const int src = b - kKsize + 1 + i;  // < 0: from the old window
+        sum += (src >= 0 ? mix.add<KP>(xs[i]) : ov[(kKsize + src) & (kKsize - 1)]) * kw[i];
+    }
+    return silu_ref(sum);
+}
+
+// grid = (n_heads, T), 256 threads: thread t forms channel t % 128 of q (t <
+// 128) or k, normalised (deltanet.rs:25-31, 461-467), and threads t < 128 also
+// v channel t; thread 0 the token's beta and decay (deltanet.rs:474-480).
+// prep[(b * n_heads + h) * 384 + {0, 128, 256} + c] = q, k, v; bd[(b * n_heads
+// + h) * 2 + {0, 1}] = beta, decay.
+template <int KP>
+__global__ __launch_bounds__(kThreads) void dn_prep_kernel(MixIn mix, MixIn mbeta, MixIn malpha,
+                                                           const float *__restrict__ conv_w,
+                                                           const float *__restrict__ ssm_a,
+                                                           const float *__restrict__ dt_bias,
+                                                           const float *__restrict__ cs, float *__restrict__ prep,
+                                                           float *__restrict__ bd, int n_heads) {
+    __shared__ float red[4];
+    const int t = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
+    const int chunk = n_heads * kDk, e = t & (kDk - 1);
+    const float y = conv_token<KP>(mix, cs, conv_w, t < kDk ? h * kDk + t : chunk + h * kDk + e, b);
+    const float vy = t < kDk ? conv_token<KP>(mix, cs, conv_w, 2 * chunk + h * kDk + t, b) : 0.0f;
+    const float sq = wave_sum(y * y);
+    if ((t & 63) == 0) red[t >> 6] = sq;
+    __syncthreads();
+    float *out = prep + ((size_t)b * n_heads + h) * 3 * kDk;
+    if (t < kDk) {
+        const float inv = 1.0f / sqrtf((red[0] + red[1]) + 1e-12f);
+        out[t] = (y * inv) * (1.0f / sqrtf((float)kDk));
+        out[2 * kDk + t] = vy;
+    } else {
+        out[kDk + e] = y * (1.0f / sqrtf((red[2] + red[3]) + 1e-12f));
+    }
+    if (t == 0) {
+        float xb[KP], xa[KP];
+        mbeta.load<KP>(b, h, xb);
+        malpha.load<KP>(b, h, xa);
+        float *o = bd + ((size_t)b * n_heads + h) * 2;
+        o[0] = 1.0f / (1.0f + expf(-mbeta.add<KP>(xb)));
+        o[1] = expf(ssm_a[h] * logf(1.0f + expf(malpha.add<KP>(xa) + dt_bias[h])));
+    }
+}
+
+// The recurrence is independent per value column j (recall sk_j, delta_j,
+// column j of the rank-1 update and the query o_j), so a head is split over
 // kScanGroups single-wave workgroups of kScanCols columns each, grid =
-// (kScanGroups, n_heads): 16 x more waves than one workgroup per head, and no
-// cross-wave barrier in the token loop.  Lane l holds rows 16 (l % 8) .. + 15
-// of column 8 g + l / 8 in registers across all T steps (state read and
-// written once per chunk); the sums over rows are a lane-local sum of 16 and
-// a DPP sum over the column's 8 consecutive lanes.  Every wave forms the token's normalised
-// q and k itself (lane l: channels l and 64 + l of each, conv windows in
-// registers) and its columns' v.  Raw head outputs go to out[t][chunk]; the
-// gated RMSNorm and the conv-window commit follow in dn_scan_finish_kernel.
+// (kScanGroups, n_heads).  The workgroup first copies its head's q and k of
+// all T tokens, its columns' v and the tokens' beta and decay into LDS; the
+// token loop then has no global load.  Lane l holds rows 16 (l % 8) .. + 15 of
+// column 8 g + l / 8 in registers across all T steps (state read and written
+// once per chunk); a sum over rows is 4 interleaved partial sums of 4 rows,
+// then a DPP sum over the column's 8 consecutive lanes.  Raw head outputs go
+// to out[t][chunk].
 constexpr int kWave = 64;
 constexpr int kScanCols = 8;
 constexpr int kScanGroups = kDk / kScanCols;
+constexpr int kScanMaxT = 32;
+constexpr int kDropOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
 
-template <int KP>
-__global__ __launch_bounds__(kWave) void deltanet_scan_kernel(
-    MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
-    const float *__restrict__ dt_bias, const float *__restrict__ cs, float *__restrict__ S,
-    float *__restrict__ out, int n_heads, int T) {
-    __shared__ __align__(16) float qs[kDk], ks[kDk];
+__global__ __launch_bounds__(kWave) void deltanet_scan_kernel(const float *__restrict__ prep,
+                                                              const float *__restrict__ bd, float *__restrict__ S,
+                                                              float *__restrict__ out, int n_heads, int T) {
+    __shared__ __align__(16) float qks[kScanMaxT][2 * kDk];  // q then k of each token
+    __shared__ float exs[kScanMaxT][kWave];  // lanes 0-7: v of the columns, 8-9: beta, decay
     const int l = threadIdx.x, h = blockIdx.y;
     const int chunk = n_heads * kDk;
-    const int rgp = l & 7, j = blockIdx.x * kScanCols + (l >> 3);
+    const int rgp = l & 7, jl = l >> 3, j = blockIdx.x * kScanCols + jl;
     float *Sh = S + (size_t)h * kDk * kDk + j;
-    // q / k channels of this lane and the v channel of its column
-    const int chq[4] = {h * kDk + l, h * kDk + 64 + l, chunk + h * kDk + l, chunk + h * kDk + 64 + l};
-    const int chv = 2 * chunk + h * kDk + j;
-    f32x4 win[4], wk[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        win[c] = *reinterpret_cast<const f32x4 *>(cs + (size_t)chq[c] * kKsize);
-        wk[c] = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)chq[c] * kKsize);
-    }
-    f32x4 winv = *reinterpret_cast<const f32x4 *>(cs + (size_t)chv * kKsize);
-    const f32x4 wkv = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)chv * kKsize);
-    const float sa = ssm_a[h], dtb = dt_bias[h];
     float st[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) st[r] = Sh[(size_t)(16 * rgp + r) * kDk];
-
-    // inputs of token `tok`, loaded one token ahead of their use
-    float xq[4][KP], xv[KP], xb[KP], xal[KP];
-    auto load_in = [&](int tok) {
+    // all loads of a half of the tokens in flight at once (clamped to the last
+    // token; slots past T are never read): lane l copies float4 l of q | k,
+    // lanes 0-7 also v of column l, lanes 8-9 beta / decay
 #pragma unroll
-        for (int c = 0; c < 4; c++) mix.load<KP>(tok, chq[c], xq[c]);
-        mix.load<KP>(tok, chv, xv);
-        mbeta.load<KP>(tok, h, xb);
-        malpha.load<KP>(tok, h, xal);
-    };
-    const auto conv = [](f32x4 w0, f32x4 k) {
-        float sum = 0.0f;
-        sum += w0.x * k.x;
-        sum += w0.y * k.y;
-        sum += w0.z * k.z;
-        sum += w0.w * k.w;
-        return silu_ref(sum);
-    };
-    load_in(0);
-    for (int tok = 0; tok < T; tok++) {
-        float y[4];
+    for (int b0 = 0; b0 < kScanMaxT; b0 += kScanMaxT / 2) {
+        float4 qk[kScanMaxT / 2];
+        float ex[kScanMaxT / 2];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            win[c] = f32x4{win[c].y, win[c].z, win[c].w, mix.add<KP>(xq[c])};
-            y[c] = conv(win[c], wk[c]);
+        for (int i = 0; i < kScanMaxT / 2; i++) {
+            const int b = min(b0 + i, T - 1);
+            const float *src = prep + ((size_t)b * n_heads + h) * 3 * kDk;
+            qk[i] = reinterpret_cast<const float4 *>(src)[l];
+            ex[i] = l < kScanCols ? src[2 * kDk + blockIdx.x * kScanCols + l]
+                                  : bd[((size_t)b * n_heads + h) * 2 + (l & 1)];
         }
-        winv = f32x4{winv.y, winv.z, winv.w, mix.add<KP>(xv)};
-        const float v = conv(winv, wkv);
-        const float br = mbeta.add<KP>(xb), ar = malpha.add<KP>(xal);
-        load_in(min(tok + 1, T - 1));
-        // L2 normalise q (and scale by 1/sqrt(dk)) and k (deltanet.rs:25-31, 461-467)
-        const float inq = 1.0f / sqrtf(wave_sum(y[0] * y[0] + y[1] * y[1]) + 1e-12f);
-        const float ink = 1.0f / sqrtf(wave_sum(y[2] * y[2] + y[3] * y[3]) + 1e-12f);
-        const float scale = 1.0f / sqrtf((float)kDk);
-        __syncthreads();  // the previous token's reads of qs / ks are done
-        qs[l] = (y[0] * inq) * scale;
-        qs[64 + l] = (y[1] * inq) * scale;
-        ks[l] = y[2] * ink;
-        ks[64 + l] = y[3] * ink;
-        // deltanet.rs:474-480
-        const float beta = 1.0f / (1.0f + expf(-br));
-        const float decay = expf(sa * logf(1.0f + expf(ar + dtb)));
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kScanMaxT / 2; i++) {
+            reinterpret_cast<float4 *>(qks[b0 + i])[l] = qk[i];
+            exs[b0 + i][l] = ex[i];
+        }
+    }
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(out, 0, 4 * T * chunk, 0x00020000);
+    for (int b = 0; b < T; b++) {
+        const float beta = exs[b][kScanCols], decay = exs[b][kScanCols + 1], v = exs[b][jl];
         float kr[16], qr[16];
 #pragma unroll
         for (int r = 0; r < 16; r += 4) {
-            const float4 k4 = *reinterpret_cast<const float4 *>(&ks[16 * rgp + r]);
-            const float4 q4 = *reinterpret_cast<const float4 *>(&qs[16 * rgp + r]);
+            const float4 k4 = *reinterpret_cast<const float4 *>(&qks[b][kDk + 16 * rgp + r]);
+            const float4 q4 = *reinterpret_cast<const float4 *>(&qks[b][16 * rgp + r]);
             kr[r] = k4.x, kr[r + 1] = k4.y, kr[r + 2] = k4.z, kr[r + 3] = k4.w;
             qr[r] = q4.x, qr[r + 1] = q4.y, qr[r + 2] = q4.z, qr[r + 3] = q4.w;
         }
         // S' = decay S; sk_j = sum_i S'_ij k_i
-        float sk = 0.0f;
+        float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             st[r] *= decay;
-            sk += st[r] * kr[r];
+            p[r & 3] += st[r] * kr[r];
         }
-        sk = sum8(sk);  // over the 8 row groups (lane bits 0-2)
+        const float sk = sum8((p[0] + p[1]) + (p[2] + p[3]));
         const float delta = beta * (v - sk);
         // S'' = S' + k delta^T; o_j = sum_i S''_ij q_i
-        float o = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) p[r] = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             st[r] += kr[r] * delta;
-            o += st[r] * qr[r];
+            p[r & 3] += st[r] * qr[r];
         }
-        o = sum8(o);
-        if (rgp == 0) out[(size_t)tok * chunk + h * kDk + j] = o;
+        const float o = sum8((p[0] + p[1]) + (p[2] + p[3]));
+        // lanes of row group 0 store (the others' offset is past the buffer: dropped)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o), orsrc,
+                                              rgp == 0 ? 4 * (b * chunk + h * kDk + j) : kDropOffset, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < 16; r++) Sh[(size_t)(16 * rgp + r) * kDk] = st[r];
@@ -546,14 +585,18 @@ __global__ __launch_bounds__(kDk) void dn_scan_finish_kernel(MixIn mix, float *_
 
 int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
-                         const float *dt_bias, float *conv_state, float *S, float *heads, int gate_off,
-                         const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo) {
+                         const float *dt_bias, float *conv_state, float *S, float *prep, float *heads,
+                         int gate_off, const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo) {
     const int kp = max(mix.kp, max(beta.kp, alpha.kp));
-    if (kp > 16 || rows < 1 || rows > 32)
-        return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_scan: %d K splits (at most 16), %d rows (1..32)", kp, rows);
+    if (kp > 16 || rows < 1 || rows > kScanMaxT)
+        return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_scan: %d K splits (at most 16), %d rows (1..%d)", kp, rows,
+                         kScanMaxT);
+    float *bd = prep + (size_t)rows * n_heads * 3 * kDk;
 #define DN_SCAN(KP)                                                                                                  \
-    hipLaunchKernelGGL(deltanet_scan_kernel<KP>, dim3(kScanGroups, n_heads), dim3(kWave), 0, stream, mix, beta,      \
-                       alpha, conv_w, ssm_a, dt_bias, conv_state, S, heads, n_heads, rows);                          \
+    hipLaunchKernelGGL(dn_prep_kernel<KP>, dim3(n_heads, rows), dim3(kThreads), 0, stream, mix, beta, alpha, conv_w, \
+                       ssm_a, dt_bias, conv_state, prep, bd, n_heads);                                               \
+    hipLaunchKernelGGL(deltanet_scan_kernel, dim3(kScanGroups, n_heads), dim3(kWave), 0, stream, prep, bd, S, heads, \
+                       n_heads, rows);                                                                               \
     hipLaunchKernelGGL(dn_scan_finish_kernel<KP>, dim3(n_heads, rows), dim3(kDk), 0, stream, mix, conv_state, heads, \
                        gate_off, norm_w, out_hi, out_lo, n_heads, eps, rows)
     if (kp <= 1) {
