@@ -93,6 +93,14 @@ struct Model {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
+    // prefill: graph of one full chunk (kPrefillRows tokens, no logits) of
+    // sequence pf_graph_seq, and pinned staging of a call's token / position
+    // rows ([chunk][tokens | positions], kPrefillRows each)
+    hipGraph_t pf_graph = nullptr;
+    hipGraphExec_t pf_exec = nullptr;
+    uint32_t pf_graph_seq = 0;
+    uint32_t *pf_stage = nullptr;
+    size_t pf_stage_chunks = 0;
 };
 
 namespace {
@@ -108,8 +116,10 @@ void free_ptr(void *p) {
 void drop_graph(Model *M) {
     if (M->exec) (void)hipGraphExecDestroy(M->exec);
     if (M->graph) (void)hipGraphDestroy(M->graph);
-    M->exec = nullptr;
-    M->graph = nullptr;
+    if (M->pf_exec) (void)hipGraphExecDestroy(M->pf_exec);
+    if (M->pf_graph) (void)hipGraphDestroy(M->pf_graph);
+    M->exec = M->pf_exec = nullptr;
+    M->graph = M->pf_graph = nullptr;
 }
 
 void free_state(Model *M) {
@@ -130,6 +140,9 @@ void free_state(Model *M) {
     for (void *p : pfb) free_ptr(p);
     M->pf = {};
     if (M->h_tokens) (void)hipHostFree(M->h_tokens);
+    if (M->pf_stage) (void)hipHostFree(M->pf_stage);
+    M->pf_stage = nullptr;
+    M->pf_stage_chunks = 0;
     M->d_pos = M->d_tokens = M->d_sampled = M->h_tokens = nullptr;
     M->x0 = M->x1 = M->pmix = M->p0 = M->p1 = M->heads = M->attn_out = M->logits = M->attn_part = nullptr;
     M->xin = nullptr;
@@ -1045,18 +1058,63 @@ int anehip_prefill(anehip_ctx *ctx, uint32_t seq, const uint32_t *tokens, uint32
     hipStream_t s = ctx->stream;
     TRY(pack_weights(ctx, M));
     TRY(alloc_prefill(ctx, M));
-    uint32_t h_tok[kPrefillRows], h_pos[kPrefillRows];
-    for (uint32_t c0 = 0; c0 < n_tokens; c0 += kPrefillRows) {
-        const uint32_t T = std::min(kPrefillRows, n_tokens - c0);
-        for (uint32_t t = 0; t < T; t++) {
-            h_tok[t] = tokens[c0 + t];
-            h_pos[t] = p0 + c0 + t;
+    // every chunk's rows staged in pinned memory up front, copied in stream
+    // order before its kernels (no host wait between chunks); an earlier
+    // call's copies may still read the staging buffer, hence the one sync
+    const size_t chunks = (n_tokens + kPrefillRows - 1) / kPrefillRows;
+    ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(s));
+    if (M->pf_stage_chunks < chunks) {
+        if (M->pf_stage) (void)hipHostFree(M->pf_stage);
+        M->pf_stage = nullptr;
+        M->pf_stage_chunks = 0;
+        if (hipHostMalloc((void **)&M->pf_stage, chunks * 2 * kPrefillRows * sizeof(uint32_t), 0) != hipSuccess) {
+            M->pf_stage = nullptr;
+            return set_error(ctx->err, ANEHIP_ENOMEM, "prefill: cannot allocate %zu chunks of pinned staging", chunks);
         }
-        // the previous chunk's kernels read these buffers: synchronous copies
-        ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(s));
-        ANEHIP_HIP_TRY(ctx->err, hipMemcpy(M->pf.d_tokens, h_tok, T * 4, hipMemcpyHostToDevice));
-        ANEHIP_HIP_TRY(ctx->err, hipMemcpy(M->pf.d_pos, h_pos, T * 4, hipMemcpyHostToDevice));
-        TRY(enqueue_prefill_chunk(ctx, M, s, seq, (int)T, c0 + T == n_tokens));
+        M->pf_stage_chunks = chunks;
+    }
+    for (uint32_t c0 = 0, c = 0; c0 < n_tokens; c0 += kPrefillRows, c++) {
+        const uint32_t T = std::min(kPrefillRows, n_tokens - c0);
+        uint32_t *st = M->pf_stage + (size_t)c * 2 * kPrefillRows;
+        for (uint32_t t = 0; t < T; t++) {
+            st[t] = tokens[c0 + t];
+            st[kPrefillRows + t] = p0 + c0 + t;
+        }
+        ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(M->pf.d_tokens, st, T * 4, hipMemcpyHostToDevice, s));
+        ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(M->pf.d_pos, st + kPrefillRows, T * 4, hipMemcpyHostToDevice, s));
+        const bool last = c0 + T == n_tokens;
+        if (T != kPrefillRows || last || !M->use_graph) {
+            TRY(enqueue_prefill_chunk(ctx, M, s, seq, (int)T, last));
+            continue;
+        }
+        // full chunks replay one captured graph (per sequence: its state blocks)
+        if (M->pf_exec && M->pf_graph_seq != seq) {
+            (void)hipGraphExecDestroy(M->pf_exec);
+            (void)hipGraphDestroy(M->pf_graph);
+            M->pf_exec = nullptr;
+            M->pf_graph = nullptr;
+        }
+        if (!M->pf_exec) {
+            ANEHIP_HIP_TRY(ctx->err, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            int rc2 = enqueue_prefill_chunk(ctx, M, s, seq, (int)kPrefillRows, false);
+            hipGraph_t g = nullptr;
+            hipError_t e = hipStreamEndCapture(s, &g);
+            if (rc2) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc2;
+            }
+            if (e != hipSuccess)
+                return set_error(ctx->err, ANEHIP_EHIP, "prefill graph capture failed: %s", hipGetErrorString(e));
+            e = hipGraphInstantiate(&M->pf_exec, g, nullptr, nullptr, 0);
+            if (e != hipSuccess) {
+                (void)hipGraphDestroy(g);
+                M->pf_exec = nullptr;
+                return set_error(ctx->err, ANEHIP_EHIP, "prefill graph instantiate failed: %s", hipGetErrorString(e));
+            }
+            M->pf_graph = g;
+            M->pf_graph_seq = seq;
+        }
+        ANEHIP_HIP_TRY(ctx->err, hipGraphLaunch(M->pf_exec, s));
     }
     // the sequence continues at p0 + n_tokens (device copy for the step graph)
     const uint32_t pos = p0 + n_tokens;
