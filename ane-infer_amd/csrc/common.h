@@ -197,10 +197,10 @@ int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type,
 // x [batch][n] fp32 -> fragment-order hi / lo planes (xf_plane_len(n) halves each).
 int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t batch, uint32_t n, _Float16 *xh,
                    _Float16 *xl);
-// K splits the batch-1 panel GEMV takes for an [m x n] matrix (<= 8);
-// norm_prologue: the input is formed by a (residual / embedding) RMSNorm
-// prologue, which favours fewer splits.
-int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, bool norm_prologue = false);
+// K splits the batch-1 panel GEMV takes for an [m x n] matrix (<= 8) whose
+// input is formed by prologue `mode` (a GEMV_IN_* value): norm prologues and
+// the SiLU-mul prologue favour fewer splits.
+int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int mode = GEMV_IN_PLAIN);
 int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                        uint32_t n, const GemvInput &in, float *out, int ksplit);
 // Small-batch GEMM (batch 2..32) on MFMA from fp16 hi/lo input planes

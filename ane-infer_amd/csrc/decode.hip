@@ -324,7 +324,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in1.token = M->d_tokens;
         in1.emb = M->embedding;
         in1.vocab = D.vocab_size;
-        const int k1 = gemv_packed_ksplit(ctx, rows_in, d, true);
+        const int k1 = gemv_packed_ksplit(ctx, rows_in, d, GEMV_IN_RESID_RMSNORM);
         TRY(launch_gemv_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, in1, M->pmix, k1));
         std::swap(cur, nxt);
         MixIn mix;
@@ -368,7 +368,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in4.w = L.post_attn_norm;
         in4.eps = eps;
         in4.x_out = nxt;
-        const int k4 = gemv_packed_ksplit(ctx, 2 * F, d, true);
+        const int k4 = gemv_packed_ksplit(ctx, 2 * F, d, GEMV_IN_RESID_RMSNORM);
         TRY(launch_gemv_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, in4, M->p1, k4));
         std::swap(cur, nxt);
         // 5. FFN down, input = SiLU(gate) * up
@@ -377,7 +377,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         in5.part = M->p1;
         in5.kp = k4;
         in5.part_stride = 2 * F;
-        const int k5 = gemv_packed_ksplit(ctx, d, F);
+        const int k5 = gemv_packed_ksplit(ctx, d, F, GEMV_IN_SILU_MUL);
         TRY(launch_gemv_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, in5, M->p0, k5));
         prev_part = M->p0;
         prev_kp = k5;
@@ -390,7 +390,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     GemvInput inf;
     inf.mode = GEMV_IN_PLAIN;
     inf.x = M->heads;
-    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d, false);
+    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d);
     if (kf == 1) {
         TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->logits, 1));
     } else {
@@ -472,13 +472,18 @@ size_t part_floats(anehip_ctx *ctx, Model *M) {
     const uint32_t d = D.dim, F = D.hidden_dim;
     struct {
         uint32_t m, n;
-        bool norm;
-    } g[] = {{M->rows_dn, d, true}, {M->rows_attn, d, true}, {d, d, false}, {d, D.n_heads * D.head_dim, false},
-             {2 * F, d, true}, {d, F, false}, {D.vocab_size, d, false}};
+        int mode;  // the batch-1 GEMV's input prologue
+    } g[] = {{M->rows_dn, d, GEMV_IN_RESID_RMSNORM},
+             {M->rows_attn, d, GEMV_IN_RESID_RMSNORM},
+             {d, d, GEMV_IN_GATED_NORM},
+             {d, D.n_heads * D.head_dim, GEMV_IN_PLAIN},
+             {2 * F, d, GEMV_IN_RESID_RMSNORM},
+             {d, F, GEMV_IN_SILU_MUL},
+             {D.vocab_size, d, GEMV_IN_PLAIN}};
     size_t mx = 0;
     for (auto &e : g) {
         if (!e.m) continue;
-        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n, e.norm)
+        const int k = M->batch == 1 ? gemv_packed_ksplit(ctx, e.m, e.n, e.mode)
                                     : gemm_packed_ksplit(ctx, e.m, e.n, M->batch);
         size_t need = (size_t)k * M->batch * e.m;
         if (need > mx) mx = need;
@@ -522,7 +527,7 @@ size_t prefill_part_floats(anehip_ctx *ctx, Model *M) {
     const anehip_model_desc &D = M->desc;
     const uint32_t d = D.dim, F = D.hidden_dim;
     const uint32_t g[][2] = {{M->rows_dn, d}, {M->rows_attn, d}, {d, d}, {d, D.n_heads * D.head_dim}, {2 * F, d}, {d, F}};
-    size_t mx = (size_t)gemv_packed_ksplit(ctx, D.vocab_size, d, false) * D.vocab_size;
+    size_t mx = (size_t)gemv_packed_ksplit(ctx, D.vocab_size, d) * D.vocab_size;
     mx = std::max(mx, (size_t)kPrefillRows * (3 * d + 2 * D.ssm_group_count));
     for (auto &e : g)
         for (uint32_t rows : {16u, kPrefillRows})
@@ -617,7 +622,7 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
     GemvInput inf;
     inf.mode = GEMV_IN_PLAIN;
     inf.x = M->pf.xn + (size_t)(T - 1) * d;
-    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d, false);
+    const int kf = gemv_packed_ksplit(ctx, D.vocab_size, d);
     if (kf == 1) {
         TRY(launch_gemv_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, inf, M->pf.logits, 1));
     } else {

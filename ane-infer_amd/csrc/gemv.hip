@@ -1803,12 +1803,16 @@ int gemm_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int max_k) {
     return choose_ksplit(tiles, (int)(n / 256), ctx->cu_count > 0 ? ctx->cu_count : 256, max_k);
 }
 
-int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, bool norm_prologue) {
+int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int mode) {
     const int tiles = (int)((m + kWave - 1) / kWave);
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     // a norm prologue re-reads the whole input vector (and its partial slices)
-    // in every workgroup, so such GEMVs stop splitting at half the CUs
-    return packed_ksplit(tiles, (int)(n / 256), norm_prologue ? cus / 2 : cus);
+    // in every workgroup, so such GEMVs stop splitting at half the CUs; a
+    // SiLU-mul prologue reads 2 partial slices per element of its split, and
+    // stops at 3/4 (ffn_down 2048 x 6144 at batch 1: 5.3 us at 6 splits
+    // against 5.7 at 8, measured in a graph of back-to-back launches)
+    const bool norm = mode == GEMV_IN_RMSNORM || mode == GEMV_IN_RESID_RMSNORM || mode == GEMV_IN_EMBED_RMSNORM;
+    return packed_ksplit(tiles, (int)(n / 256), norm ? cus / 2 : mode == GEMV_IN_SILU_MUL ? 3 * cus / 4 : cus);
 }
 
 // K splits of the panel MFMA GEMM.  Matrices of fewer row tiles than CUs
