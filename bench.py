@@ -83,6 +83,8 @@ def parse():
                     help="only run the roofline kernel (lm_head GEMV, M=1) back to back, for rocprofv3")
     ap.add_argument("--decode-only", default=None,
                     help="only run decode points, e.g. '1:1024,32:1024' (batch:ctx), and print their line")
+    ap.add_argument("--prefill-only", type=int, default=0,
+                    help="only run the batch-1 prefill of this many tokens (twice, the second timed)")
     return ap.parse_args()
 
 
@@ -290,6 +292,10 @@ def main():
     if args.decode_only:
         pts = [tuple(int(v) for v in p.split(":")) for p in args.decode_only.split(",")]
         print(json.dumps({"decode": bench_decode(anehip, args.decode_steps, 3, pts)}), flush=True)
+        return
+    if args.prefill_only:
+        print(json.dumps({"decode": bench_decode(anehip, args.decode_steps, 3, [],
+                                                 prefill_tokens=args.prefill_only)}), flush=True)
         return
     ctx = anehip.Context(0)
     if args.profile_kernel:
