@@ -274,8 +274,11 @@ int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, con
 int launch_silu_mul(anehip_ctx *ctx, hipStream_t s, float *a, const float *b, size_t n);
 int launch_residual_add(anehip_ctx *ctx, hipStream_t s, float *x, const float *y, size_t n);
 size_t argmax_workspace_bytes(int rows);
+// Greedy argmax of each row's n logits (f32::total_cmp order; equal keys:
+// the last index, as Iterator::max_by) into out; with pos, row r's position
+// pos[r] is also advanced by one.
 int launch_argmax(anehip_ctx *ctx, hipStream_t s, int rows, uint32_t n, const float *logits, void *ws,
-                  uint32_t *out);
+                  uint32_t *out, uint32_t *pos = nullptr);
 
 // Host helper: inv_freq[p] = 1 / base^(2p / head_dim), the
 // reference's formula (deltanet.rs:601-603) evaluated once on the host.

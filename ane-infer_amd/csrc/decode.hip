@@ -268,11 +268,6 @@ float **f32_slot(Model *M, int layer, uint32_t kind) {
     }
 }
 
-__global__ void pos_advance_kernel(uint32_t *pos, int n) {
-    int i = threadIdx.x;
-    if (i < n) pos[i] += 1u;
-}
-
 int check_model(anehip_ctx *ctx, Model *M) {
     for (uint32_t l = 0; l < M->desc.n_layers; l++) {
         uint64_t miss = required_mask(M, (int)l) & ~M->layers[l].have;
@@ -460,10 +455,9 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
 // the projections, greedy argmax of the logits and the position advance.
 int enqueue_step(anehip_ctx *ctx, Model *M, hipStream_t s) {
     TRY(M->batch == 1 ? enqueue_step_b1(ctx, M, s) : enqueue_step_bn(ctx, M, s));
-    TRY(launch_argmax(ctx, s, (int)M->batch, M->desc.vocab_size, M->logits, M->argmax_ws, M->d_sampled));
-    hipLaunchKernelGGL(pos_advance_kernel, dim3(1), dim3(64), 0, s, M->d_pos, (int)M->batch);
-    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-    return ANEHIP_OK;
+    // greedy argmax, and each sequence's position advanced by the same kernel
+    return launch_argmax(ctx, s, (int)M->batch, M->desc.vocab_size, M->logits, M->argmax_ws, M->d_sampled,
+                         M->d_pos);
 }
 
 // Largest K-split partial buffer any GEMM of the step needs.
