@@ -469,6 +469,11 @@ int tiles_per_chunk(int max_seq, int batch, int n_kv) {
 
 }  // namespace
 
+void attn_layout(int max_seq, int batch, int n_kv, int *tpw, int *nch) {
+    *tpw = tiles_per_chunk(max_seq, batch, n_kv);
+    *nch = ((max_seq + kCh - 1) / kCh + *tpw - 1) / *tpw;
+}
+
 size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G) {
     const int tpw = tiles_per_chunk(max_seq, batch, n_kv);
     const size_t nch = (size_t)((max_seq + kCh - 1) / kCh + tpw - 1) / tpw;
@@ -495,6 +500,7 @@ int attention_impl(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, 
                            inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, tpw, part_o, part_ml,     \
                            cache_off, row_stride, append);                                                    \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
+        if (!out && !out_hi) return ANEHIP_OK; /* partials only */                                             \
         hipLaunchKernelGGL(attn_combine_kernel<GG>, g2, dim3(kThreads), 0, stream, mix, pos, part_o, part_ml,  \
                            nch, tpw, n_heads, n_kv, out, out_hi, out_lo);                                     \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \

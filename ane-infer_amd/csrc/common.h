@@ -76,6 +76,8 @@ enum GemvInMode : int {
     GEMV_IN_EMBED_RMSNORM, // r = emb[token] (0 if token >= vocab); rmsnorm(r, w); r -> x_out
     GEMV_IN_GATED_NORM,    // per-128 head rmsnorm(x, w) * SiLU(gate), gate = sum_p part[p][gate_off..]
     GEMV_IN_SILU_MUL,      // SiLU(sum_p part[p][k]) * sum_p part[p][n + k]
+    GEMV_IN_ATTN_COMBINE,  // batch row 0's attention output of the slice's heads: the chunk partials
+                           // merged (running max / sum) times sigmoid(gate), gate from part
 };
 
 struct GemvInput {
@@ -94,6 +96,12 @@ struct GemvInput {
     // GATED_NORM only: the q/k conv windows [2n][4] are committed (shift left,
     // append part rows [0, 2n)) by the workgroups of this launch
     float *conv_state = nullptr;
+    // ATTN_COMBINE only: attention partials of batch row 0 (launch_attention
+    // without outputs), their chunk layout and the position; head h's gate is
+    // part[h * 512 + 256 + d] (K-split slices as above)
+    const float *att_o = nullptr, *att_ml = nullptr;
+    int att_nch = 0, att_tpw = 0, att_g = 0;
+    const uint32_t *att_pos = nullptr;
 };
 
 // A GEMV output read by a later kernel as kp partial slices: value (b, i) =
@@ -245,6 +253,11 @@ int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
 
 // attention.hip.  mix per sequence: [q_full | k | v] rows.
 size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G);
+// Chunking of the decode attention's partials: tiles of 64 positions per
+// chunk (tpw) and chunks per (sequence, kv head) (nch) for this state shape.
+void attn_layout(int max_seq, int batch, int n_kv, int *tpw, int *nch);
+// With out == out_hi == nullptr only the chunk partials are written (a
+// batch-1 GEMV with GEMV_IN_ATTN_COMBINE merges them).
 int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
                      const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
                      const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,

@@ -344,12 +344,31 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
             in3.conv_state = L.conv_state;
             cols3 = d;
         } else {
-            TRY(launch_attention(ctx, s, 1, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
-                                 L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part, M->attn_out, nullptr,
-                                 nullptr));
-            in3.mode = GEMV_IN_PLAIN;
-            in3.x = M->attn_out;
             cols3 = qd;
+            // with one head per K split the o_proj prologue merges the
+            // attention's chunk partials (no combine kernel)
+            const bool fuse = gemv_packed_ksplit(ctx, d, cols3) == (int)(qd / 256);
+            TRY(launch_attention(ctx, s, 1, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
+                                 L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part,
+                                 fuse ? nullptr : M->attn_out, nullptr, nullptr));
+            if (fuse) {
+                const int G = (int)(D.n_heads / D.n_kv_heads);
+                int tpw = 0, nch = 0;
+                attn_layout((int)M->max_seq, 1, (int)D.n_kv_heads, &tpw, &nch);
+                in3.mode = GEMV_IN_ATTN_COMBINE;
+                in3.part = M->pmix;
+                in3.kp = k1;
+                in3.part_stride = rows_in;
+                in3.att_o = M->attn_part;
+                in3.att_ml = M->attn_part + (size_t)D.n_kv_heads * nch * G * 256;
+                in3.att_nch = nch;
+                in3.att_tpw = tpw;
+                in3.att_g = G;
+                in3.att_pos = M->d_pos;
+            } else {
+                in3.mode = GEMV_IN_PLAIN;
+                in3.x = M->attn_out;
+            }
         }
         const int k3 = gemv_packed_ksplit(ctx, d, cols3);
         TRY(launch_gemv_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, in3, M->p0, k3));

@@ -156,6 +156,7 @@ __device__ __forceinline__ float wg_sum(float v, float *red) {
 constexpr int kMaxSplit = 8;     // K splits a batch-1 consumer may have to add
 constexpr int kMaxGemmSplit = 16;  // K splits of the x-stationary GEMM (batch > 1)
 constexpr int kMaxSliceSb = 8;   // super-blocks of input one workgroup may need
+constexpr int kAttnHd = 256;     // attention head dim (GEMV_IN_ATTN_COMBINE slices)
 
 // sum over p < kp of part[p * stride + i], p ascending.  All kMaxSplit loads
 // are issued unconditionally (slices past kp re-read slice 0) so they overlap
@@ -206,6 +207,9 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
             for (int i = 0; i < B; i++)
                 if (t + NT * (i0 + i) < len) xs[t + NT * (i0 + i)] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
         }
+    } else if constexpr (MODE == GEMV_IN_ATTN_COMBINE) {
+        // one head per slice (the launcher checks that each split is one panel)
+        attn_combine_slice<kMaxSplit, NT>(in, c0, xs, [] {});
     } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
         // deltanet.rs:517-533, per 128-wide head; a wave handles whole heads
         constexpr int W = NT / 64;                      // waves
@@ -530,7 +534,109 @@ __device__ __forceinline__ bool overlapped_ok(const GemvInput &in, int n, int le
     if constexpr (MODE == GEMV_IN_SILU_MUL) return len <= 4 * NT && aligned;
     if constexpr (MODE == GEMV_IN_GATED_NORM)
         return len <= 4 * NT && aligned && (!in.conv_state || 2 * n <= (int)(gridDim.x * gridDim.y) * NT);
+    if constexpr (MODE == GEMV_IN_ATTN_COMBINE) return len == kAttnHd && NT >= 4 * kWave && aligned;
     return false;
+}
+
+// GEMV_IN_ATTN_COMBINE: head c0 / 256 of batch row 0, the decode attention's
+// merge of its chunk partials (attn_combine_kernel's arithmetic and order:
+// the maximum over the active chunks, then 4 groups of 64 lanes sum chunks
+// g, g + 4, ... with weights exp(m - M), the groups added in order, num / den
+// times sigmoid(gate)) into xs[0..256).  The gate and the first 16 chunks are
+// loaded before `issue` starts the weight loads; groups 4.. (threads >= 256)
+// mirror groups 0..3 for those loads, so every address stays in bounds.
+template <int KP, int NT, class Issue>
+__device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, float *xs, Issue &&issue) {
+    static_assert(NT >= 4 * kWave, "attn_combine_slice needs 4 waves");
+    __shared__ float cmax[NT / kWave];
+    __shared__ float4 accs[4][kWave];
+    __shared__ float dens[4][kWave];
+    const int t = threadIdx.x, g = t >> 6, gq = g & 3, l = t & (kWave - 1);
+    const int h = c0 / kAttnHd, G = in.att_g, kvh = h / G, hh = h % G;
+    const int len = (int)in.att_pos[0] + 1;
+    const int nc = ((len + 63) / 64 + in.att_tpw - 1) / in.att_tpw;  // active chunks, >= 1
+    const size_t base = (size_t)kvh * in.att_nch;
+    float4 gv[KP];
+    load_parts4<KP>(gv, in.part, in.kp, in.part_stride, (size_t)((h * 2 * kAttnHd + kAttnHd) >> 2) + l);
+    float4 o4[4];
+    float m4[4], l4[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const size_t slot = (base + min(gq + 4 * i, nc - 1)) * G + hh;
+        o4[i] = *reinterpret_cast<const float4 *>(in.att_o + slot * kAttnHd + 4 * l);
+        m4[i] = in.att_ml[slot * 2];
+        l4[i] = in.att_ml[slot * 2 + 1];
+    }
+    float mx = -INFINITY;
+    for (int cc = 16 + t; cc < nc; cc += NT) mx = fmaxf(mx, in.att_ml[((base + cc) * G + hh) * 2]);
+    issue();
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (gq + 4 * i < nc) mx = fmaxf(mx, m4[i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (l == 0) cmax[g] = mx;
+    __syncthreads();
+    float M = cmax[0];
+#pragma unroll
+    for (int w = 1; w < NT / kWave; w++) M = fmaxf(M, cmax[w]);
+    if (g < 4) {
+        float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+        float den = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (g + 4 * i < nc) {
+                const float w = expf(m4[i] - M);
+                num = make_float4(num.x + w * o4[i].x, num.y + w * o4[i].y, num.z + w * o4[i].z,
+                                  num.w + w * o4[i].w);
+                den += w * l4[i];
+            }
+        int cc = g + 16;
+        for (; cc + 12 < nc; cc += 16) {  // 4 chunks per trip, their loads issued together
+            float4 p4[4];
+            float pm[4], pl[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const size_t slot = (base + cc + 4 * i) * G + hh;
+                p4[i] = *reinterpret_cast<const float4 *>(in.att_o + slot * kAttnHd + 4 * l);
+                pm[i] = in.att_ml[slot * 2];
+                pl[i] = in.att_ml[slot * 2 + 1];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float w = expf(pm[i] - M);
+                num = make_float4(num.x + w * p4[i].x, num.y + w * p4[i].y, num.z + w * p4[i].z,
+                                  num.w + w * p4[i].w);
+                den += w * pl[i];
+            }
+        }
+        for (; cc < nc; cc += 4) {
+            const size_t slot = (base + cc) * G + hh;
+            const float4 o = *reinterpret_cast<const float4 *>(in.att_o + slot * kAttnHd + 4 * l);
+            const float w = expf(in.att_ml[slot * 2] - M);
+            num = make_float4(num.x + w * o.x, num.y + w * o.y, num.z + w * o.z, num.w + w * o.w);
+            den += w * in.att_ml[slot * 2 + 1];
+        }
+        accs[g][l] = num;
+        dens[g][l] = den;
+    }
+    __syncthreads();
+    if (g == 0) {
+        float4 sum = accs[0][l];
+        float dsum = dens[0][l];
+#pragma unroll
+        for (int k = 1; k < 4; k++) {
+            const float4 o = accs[k][l];
+            sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
+            dsum += dens[k][l];
+        }
+        const float4 ga = sum_parts4<KP>(gv, in.kp);
+        reinterpret_cast<float4 *>(xs)[l] = make_float4((sum.x / dsum) * (1.0f / (1.0f + expf(-ga.x))),
+                                                        (sum.y / dsum) * (1.0f / (1.0f + expf(-ga.y))),
+                                                        (sum.z / dsum) * (1.0f / (1.0f + expf(-ga.z))),
+                                                        (sum.w / dsum) * (1.0f / (1.0f + expf(-ga.w))));
+    }
+    __syncthreads();
 }
 
 template <int MODE, int KP, int NT, class Issue>
@@ -583,6 +689,8 @@ __device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, 
         if (t < (len >> 2))
             xs4[t] = make_float4(silu1(gs.x) * us.x, silu1(gs.y) * us.y, silu1(gs.z) * us.z, silu1(gs.w) * us.w);
         __syncthreads();
+    } else if constexpr (MODE == GEMV_IN_ATTN_COMBINE) {
+        attn_combine_slice<KP, NT>(in, c0, xs, issue);
     } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
         const int wg = blockIdx.y * gridDim.x + blockIdx.x;
         const bool commit = in.conv_state != nullptr;
@@ -2022,7 +2130,12 @@ int launch_packed_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t
     const int tpw = MODE != GEMV_IN_PLAIN && tiles * ksplit >= 8 * cus ? 2 : 1;
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     constexpr bool has_parts =
-        MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_SILU_MUL || MODE == GEMV_IN_GATED_NORM;
+        MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_SILU_MUL || MODE == GEMV_IN_GATED_NORM ||
+        MODE == GEMV_IN_ATTN_COMBINE;
+    if constexpr (MODE == GEMV_IN_ATTN_COMBINE) {
+        if (per != 1 || n % 256 != 0 || !in.att_o || !in.att_ml || !in.att_pos || in.att_g <= 0 || in.att_tpw <= 0)
+            return set_error(ctx->err, ANEHIP_EINVAL, "gemv: attention combine needs one head (256 columns) per split");
+    }
     if constexpr (has_parts) {
         if (in.kp > 2) launch_packed_k<T, MODE, kMaxSplit>(stream, wb, m, n, in, out, ksplit, per, tpw);
         else launch_packed_k<T, MODE, 2>(stream, wb, m, n, in, out, ksplit, per, tpw);
@@ -2046,6 +2159,8 @@ int dispatch_packed(anehip_ctx *ctx, hipStream_t s, const void *w, uint32_t m, u
         case GEMV_IN_GATED_NORM:
             return launch_packed_t<T, GEMV_IN_GATED_NORM>(ctx, s, w, m, n, in, out, ksplit);
         case GEMV_IN_SILU_MUL: return launch_packed_t<T, GEMV_IN_SILU_MUL>(ctx, s, w, m, n, in, out, ksplit);
+        case GEMV_IN_ATTN_COMBINE:
+            return launch_packed_t<T, GEMV_IN_ATTN_COMBINE>(ctx, s, w, m, n, in, out, ksplit);
         default: return set_error(ctx->err, ANEHIP_EINVAL, "gemv: input mode %d", in.mode);
     }
 }
