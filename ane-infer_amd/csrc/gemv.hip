@@ -1931,8 +1931,9 @@ int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int mode) 
 // 11.9 us; 2048 x 2048: 3.9 us at k = 8 against 5.4 us), and P = 2 halves
 // the partial sums the consumer reads against P = 1 where the times tie.
 // Matrices of at least 4 tiles per CU: no split at batch <= 16 (the 16-wide
-// kernel holds 8 panels of x), splits of 4 panels above (lm_head at batch 32:
-// 74 us at k = 2 on gemm_xsh against 94 us unsplit on the persistent kernel).
+// kernel holds 8 panels of x); above, splits of 8 panels (gemm_xsh with 4
+// panels per wave: lm_head at batch 32 74 us in one pass, against 71 us at
+// k = 2 plus 11 us for the consumer's pass over the two partial sums), else of 4.
 // Otherwise, among the even splits of at most kMaxSplit, the one that
 // minimises the panels of the busiest CU, ceil(items / CUs) x panels per
 // split, with single-panel splits counted double and ties going to fewer
@@ -1944,7 +1945,11 @@ int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t b
         const int P = nsb % 2 == 0 && tiles * nsb > 2 * cus ? 2 : 1;
         if (nsb / P <= kMaxGemmSplit) return nsb / P;
     }
-    if (tiles >= 4 * cus) return batch > 16 && nsb % 4 == 0 && nsb / 4 <= kMaxGemmSplit ? nsb / 4 : 1;
+    if (tiles >= 4 * cus) {
+        if (batch <= 16) return 1;
+        if (nsb % 8 == 0 && nsb / 8 <= kMaxGemmSplit) return nsb / 8;
+        return nsb % 4 == 0 && nsb / 4 <= kMaxGemmSplit ? nsb / 4 : 1;
+    }
     int best = 1;
     double best_cost = 1e30;
     for (int k = 1; k <= nsb && k <= kMaxSplit; k++) {
@@ -1985,7 +1990,7 @@ static GemmKernel gemm_kernel(uint32_t batch, int nsb, int ksplit) {
     const int per = nsb / ksplit;
     if (per * ksplit != nsb) return GemmKernel::Persistent;
     if (batch <= 16) return per == 1 || per == 2 || per == 4 || per == 8 ? GemmKernel::Xs16 : GemmKernel::Persistent;
-    if (per == 2 || per == 4) return GemmKernel::Xsh;
+    if (per == 2 || per == 4 || per == 8) return GemmKernel::Xsh;
     if (per == 1 && ksplit >= 2) return GemmKernel::Xs32;
     return GemmKernel::Persistent;
 }
@@ -2019,8 +2024,10 @@ void launch_gemm_xs_any(anehip_ctx *ctx, hipStream_t stream, GemmKernel kind, co
     } else if (kind == GemmKernel::Xsh) {
         if (per == 2)
             ANEHIP_XS((gemm_xsh<T, 1, 1, 2>), 512);
-        else
+        else if (per == 4)
             ANEHIP_XS((gemm_xsh<T, 2, 2, 2>), 512);
+        else
+            ANEHIP_XS((gemm_xsh<T, 4, 2, 2>), 512);
     } else if (xrows) {
         ANEHIP_XS((gemm_xs<T, 1, 1, true>), 256);
     } else {
