@@ -443,35 +443,43 @@ __global__ __launch_bounds__(kThreads) void dn_prep_kernel(MixIn mix, MixIn mbet
 
 // The recurrence is independent per value column j (recall sk_j, delta_j,
 // column j of the rank-1 update and the query o_j), so a head is split over
-// kScanGroups single-wave workgroups of kScanCols columns each, grid =
-// (kScanGroups, n_heads).  The workgroup first copies its head's q and k of
-// all T tokens, its columns' v and the tokens' beta and decay into LDS; the
-// token loop then has no global load.  Lane l holds rows 16 (l % 8) .. + 15 of
-// column 8 g + l / 8 in registers across all T steps (state read and written
-// once per chunk); a sum over rows is 4 interleaved partial sums of 4 rows,
-// then a DPP sum over the column's 8 consecutive lanes.  Raw head outputs go
-// to out[t][chunk].
+// kDk / C single-wave workgroups of C columns each, grid = (kDk / C, n_heads).
+// The workgroup first copies its head's q and k of all T tokens, its columns'
+// v and the tokens' beta and decay into LDS; the token loop then has no global
+// load.  Lane l holds rows R (l % G) .. + R - 1 of column C g + l / G (G =
+// 64 / C lanes per column, R = 128 / G rows per lane) in registers across all
+// T steps (state read and written once per chunk); a sum over rows is 4
+// interleaved partial sums of R / 4 rows, then a DPP sum over the column's G
+// consecutive lanes.  Raw head outputs go to out[t][chunk].
 constexpr int kWave = 64;
-constexpr int kScanCols = 8;
-constexpr int kScanGroups = kDk / kScanCols;
+constexpr int kScanCols = 4;
 constexpr int kScanMaxT = 32;
 constexpr int kDropOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
 
+// sum over each 16-lane row: row_ror 8, 4, 2, 1
+__device__ __forceinline__ float sum16(float v) {
+    return dpp_add<0x121>(dpp_add<0x122>(dpp_add<0x124>(dpp_add<0x128>(v))));
+}
+
+template <int C>
 __global__ __launch_bounds__(kWave) void deltanet_scan_kernel(const float *__restrict__ prep,
                                                               const float *__restrict__ bd, float *__restrict__ S,
                                                               float *__restrict__ out, int n_heads, int T) {
+    constexpr int G = kWave / C, R = kDk / G;
+    static_assert(G == 8 || G == 16, "a column's lanes are summed within one DPP row");
+    static_assert(C % 2 == 0 && C + 2 <= kWave, "lanes C, C + 1 carry beta and decay");
     __shared__ __align__(16) float qks[kScanMaxT][2 * kDk];  // q then k of each token
-    __shared__ float exs[kScanMaxT][kWave];  // lanes 0-7: v of the columns, 8-9: beta, decay
+    __shared__ float exs[kScanMaxT][kWave];  // lanes 0..C-1: v of the columns, C, C+1: beta, decay
     const int l = threadIdx.x, h = blockIdx.y;
     const int chunk = n_heads * kDk;
-    const int rgp = l & 7, jl = l >> 3, j = blockIdx.x * kScanCols + jl;
+    const int rgp = l % G, jl = l / G, j = blockIdx.x * C + jl;
     float *Sh = S + (size_t)h * kDk * kDk + j;
-    float st[16];
+    float st[R];
 #pragma unroll
-    for (int r = 0; r < 16; r++) st[r] = Sh[(size_t)(16 * rgp + r) * kDk];
+    for (int r = 0; r < R; r++) st[r] = Sh[(size_t)(R * rgp + r) * kDk];
     // all loads of a half of the tokens in flight at once (clamped to the last
     // token; slots past T are never read): lane l copies float4 l of q | k,
-    // lanes 0-7 also v of column l, lanes 8-9 beta / decay
+    // lanes 0..C-1 also v of column l, lanes >= C beta (even) / decay (odd)
 #pragma unroll
     for (int b0 = 0; b0 < kScanMaxT; b0 += kScanMaxT / 2) {
         float4 qk[kScanMaxT / 2];
@@ -481,8 +489,7 @@ __global__ __launch_bounds__(kWave) void deltanet_scan_kernel(const float *__res
             const int b = min(b0 + i, T - 1);
             const float *src = prep + ((size_t)b * n_heads + h) * 3 * kDk;
             qk[i] = reinterpret_cast<const float4 *>(src)[l];
-            ex[i] = l < kScanCols ? src[2 * kDk + blockIdx.x * kScanCols + l]
-                                  : bd[((size_t)b * n_heads + h) * 2 + (l & 1)];
+            ex[i] = l < C ? src[2 * kDk + blockIdx.x * C + l] : bd[((size_t)b * n_heads + h) * 2 + (l & 1)];
         }
 #pragma unroll
         for (int i = 0; i < kScanMaxT / 2; i++) {
@@ -492,40 +499,41 @@ __global__ __launch_bounds__(kWave) void deltanet_scan_kernel(const float *__res
     }
     __syncthreads();
     const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(out, 0, 4 * T * chunk, 0x00020000);
+    const auto colsum = [](float v) { return G == 16 ? sum16(v) : sum8(v); };
     for (int b = 0; b < T; b++) {
-        const float beta = exs[b][kScanCols], decay = exs[b][kScanCols + 1], v = exs[b][jl];
-        float kr[16], qr[16];
+        const float beta = exs[b][C], decay = exs[b][C + 1], v = exs[b][jl];
+        float kr[R], qr[R];
 #pragma unroll
-        for (int r = 0; r < 16; r += 4) {
-            const float4 k4 = *reinterpret_cast<const float4 *>(&qks[b][kDk + 16 * rgp + r]);
-            const float4 q4 = *reinterpret_cast<const float4 *>(&qks[b][16 * rgp + r]);
+        for (int r = 0; r < R; r += 4) {
+            const float4 k4 = *reinterpret_cast<const float4 *>(&qks[b][kDk + R * rgp + r]);
+            const float4 q4 = *reinterpret_cast<const float4 *>(&qks[b][R * rgp + r]);
             kr[r] = k4.x, kr[r + 1] = k4.y, kr[r + 2] = k4.z, kr[r + 3] = k4.w;
             qr[r] = q4.x, qr[r + 1] = q4.y, qr[r + 2] = q4.z, qr[r + 3] = q4.w;
         }
         // S' = decay S; sk_j = sum_i S'_ij k_i
         float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
+        for (int r = 0; r < R; r++) {
             st[r] *= decay;
             p[r & 3] += st[r] * kr[r];
         }
-        const float sk = sum8((p[0] + p[1]) + (p[2] + p[3]));
+        const float sk = colsum((p[0] + p[1]) + (p[2] + p[3]));
         const float delta = beta * (v - sk);
         // S'' = S' + k delta^T; o_j = sum_i S''_ij q_i
 #pragma unroll
         for (int r = 0; r < 4; r++) p[r] = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
+        for (int r = 0; r < R; r++) {
             st[r] += kr[r] * delta;
             p[r & 3] += st[r] * qr[r];
         }
-        const float o = sum8((p[0] + p[1]) + (p[2] + p[3]));
+        const float o = colsum((p[0] + p[1]) + (p[2] + p[3]));
         // lanes of row group 0 store (the others' offset is past the buffer: dropped)
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o), orsrc,
                                               rgp == 0 ? 4 * (b * chunk + h * kDk + j) : kDropOffset, 0, 0);
     }
 #pragma unroll
-    for (int r = 0; r < 16; r++) Sh[(size_t)(16 * rgp + r) * kDk] = st[r];
+    for (int r = 0; r < R; r++) Sh[(size_t)(R * rgp + r) * kDk] = st[r];
 }
 
 // After deltanet_scan_kernel: row b of the gated RMSNorm (deltanet.rs:517-533)
@@ -595,8 +603,8 @@ int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_he
 #define DN_SCAN(KP)                                                                                                  \
     hipLaunchKernelGGL(dn_prep_kernel<KP>, dim3(n_heads, rows), dim3(kThreads), 0, stream, mix, beta, alpha, conv_w, \
                        ssm_a, dt_bias, conv_state, prep, bd, n_heads);                                               \
-    hipLaunchKernelGGL(deltanet_scan_kernel, dim3(kScanGroups, n_heads), dim3(kWave), 0, stream, prep, bd, S, heads, \
-                       n_heads, rows);                                                                               \
+    hipLaunchKernelGGL(deltanet_scan_kernel<kScanCols>, dim3(kDk / kScanCols, n_heads), dim3(kWave), 0, stream,     \
+                       prep, bd, S, heads, n_heads, rows);                                                           \
     hipLaunchKernelGGL(dn_scan_finish_kernel<KP>, dim3(n_heads, rows), dim3(kDk), 0, stream, mix, conv_state, heads, \
                        gate_off, norm_w, out_hi, out_lo, n_heads, eps, rows)
     if (kp <= 1) {
