@@ -455,15 +455,18 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
 }
 
 // Tiles of 64 positions per chunk (workgroup): the smallest power of two
-// that keeps at most 128 chunks per sequence and kv head and at most ~2048
-// workgroups (8 per CU) at the cache's capacity -- the combine merges at most
-// 128 partials per head, and each workgroup's q / k preparation is amortised
-// over several tiles when there are plenty of workgroups.
+// that keeps at most 128 chunks per sequence and kv head and at most ~256
+// workgroups (one per CU) at the cache's capacity -- the combine merges at
+// most 128 partials per head, and each workgroup's q / k preparation and
+// partial write are amortised over several tiles when there are plenty of
+// workgroups (batch 32 on MI355X, ctx 1k / 8k / 32k: 20.6k / 15.4k / 8.4k
+// tok/s at ~256 workgroups against 20.1–20.3k / 14.7–14.9k / 8.4k at ~2048;
+// 512-token prefill 17.3k against 16.8k tok/s).  Batch 1 stays at 128 chunks.
 int tiles_per_chunk(int max_seq, int batch, int n_kv) {
     const int tiles = (max_seq + kCh - 1) / kCh;
     int tpw = 1;
     auto chunks = [&] { return (tiles + tpw - 1) / tpw; };
-    while (chunks() > 128 || (tpw < tiles && (size_t)chunks() * n_kv * batch > 2048)) tpw *= 2;
+    while (chunks() > 128 || (tpw < tiles && (size_t)chunks() * n_kv * batch > 256)) tpw *= 2;
     return tpw;
 }
 
