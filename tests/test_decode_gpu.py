@@ -256,7 +256,7 @@ def big_host():
     return HostModel(anehip.Spec(), seed=11)
 
 
-@pytest.mark.parametrize("ctx_len,batch", [(1024, 1), (8192, 1), (32768, 1), (1024, 32)])
+@pytest.mark.parametrize("ctx_len,batch", [(1024, 1), (8192, 1), (32768, 1), (1024, 32), (8192, 32)])
 def test_qwen35_2b_shape_step(big_host, ctx_len, batch):
     """Random-init 24-layer Qwen3.5-2B shape, Q8_0 weights, fp16 KV cache
     filled with N(0,1) at positions < ctx-1, DeltaNet states N(0, 0.01)
