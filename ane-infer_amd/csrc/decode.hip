@@ -291,9 +291,10 @@ int check_model(anehip_ctx *ctx, Model *M) {
     } while (0)
 
 // Batch 1: every projection is one GEMV launch whose prologue forms its input
-// (embedding / residual sum + RMSNorm, gated RMSNorm, SiLU-mul) from what the
-// previous kernels left, so a DeltaNet layer is 5 launches (mixer-in GEMV,
-// DeltaNet, ssm_out GEMV, gate/up GEMV, down GEMV) and an attention layer 6.
+// (embedding / residual sum + RMSNorm, gated RMSNorm, SiLU-mul, the
+// attention's chunk merge) from what the previous kernels left, so a DeltaNet
+// layer is 5 launches (mixer-in GEMV, DeltaNet, ssm_out GEMV, gate/up GEMV,
+// down GEMV) and so is an attention layer when o_proj has one head per split.
 int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     const anehip_model_desc &D = M->desc;
     const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
