@@ -7,6 +7,10 @@ import oracle
 
 SMALL = dict(dim=256, hidden_dim=512, n_layers=4, n_heads=4, n_kv_heads=1, head_dim=256, vocab_size=1000,
              ssm_state_size=128, ssm_conv_kernel=4, ssm_group_count=2)
+# A model whose batch > 1 projections all run on the x-stationary GEMM with
+# K splits (the small model's 256-wide matrices take a single split).
+MID = dict(dim=512, hidden_dim=1024, n_layers=4, n_heads=4, n_kv_heads=1, head_dim=256, vocab_size=1000,
+           ssm_state_size=128, ssm_conv_kernel=4, ssm_group_count=4)
 
 
 class HostModel:

@@ -101,3 +101,75 @@ def attention_core(q_full, k_in, v_in, q_norm, k_norm, k_hist, v_hist, pos, n_he
         p /= p.sum()
         out[h] = p @ V[h // hpk]
     return (out * sigmoid(gate)).reshape(-1), k, v
+
+
+def ffn(x, w_gate, w_up, w_down):
+    """ffn_forward (main.rs:1115-1135): down(silu(gate x) * up x), float64."""
+    return w_down @ (silu(w_gate @ x) * (w_up @ x))
+
+
+class Forward64:
+    """The decode step composed in float64 from the functions above, following
+    qwen35_forward_token (crates/cli/src/main.rs:953-1023):
+
+        x = embedding[token]
+        per layer l:  x += mixer_l(rmsnorm(x, attn_norm_l))
+                      x += ffn_l(rmsnorm(x, post_attn_norm_l))
+        logits = lm_head @ rmsnorm(x, final_norm)
+
+    with the DeltaNet mixer of deltanet.rs:429-539 (qkv / beta / alpha / gate
+    projections of the normed input, the core above, per-head RMSNorm times
+    SiLU(gate), ssm_out) and the attention mixer of deltanet.rs:541-675
+    (wq -> q | gate per head, q / k RMSNorm with eps 1e-6, RoPE, K/V history
+    kept exact as the reference's fp32 cache does, or rounded to fp16 with
+    `kv_f16`, softmax, sigmoid(gate), wo).
+
+    `weights(layer, name)` returns float64 arrays: dequantised matrices
+    [rows, cols] or fp32 vectors; names are the model's tensor names
+    (attn_norm, qkv, ssm_conv1d [C, K], ...).  State is float64 and lives here:
+    conv windows [C, K], S [H, dk, dk], K / V history [n_kv, pos, hd]."""
+
+    def __init__(self, weights, layer_types, cfg, kv_f16=True):
+        self.w, self.types, self.cfg = weights, list(layer_types), dict(cfg)
+        self.kv_f16 = kv_f16
+        self.pos = 0
+        self.conv, self.S, self.K, self.V = {}, {}, {}, {}
+        c = self.cfg
+        for l, t in enumerate(self.types):
+            if t == 0:
+                self.conv[l] = np.zeros((3 * c["dim"], c["ksize"]))
+                self.S[l] = np.zeros((c["H"], c["dk"], c["dk"]))
+            else:
+                self.K[l] = np.zeros((c["n_kv"], 0, c["hd"]))
+                self.V[l] = np.zeros((c["n_kv"], 0, c["hd"]))
+
+    def forward(self, token):
+        c, w = self.cfg, self.w
+        eps = c["eps"]
+        x = np.array(w(-1, "embedding")[token], np.float64) if token < c["vocab"] else np.zeros(c["dim"])
+        for l, t in enumerate(self.types):
+            xn = rmsnorm(x, w(l, "attn_norm"), eps)
+            if t == 0:
+                qkv = w(l, "qkv") @ xn
+                heads, self.conv[l], self.S[l] = deltanet_core(
+                    qkv, w(l, "ssm_beta") @ xn, w(l, "ssm_alpha") @ xn, w(l, "ssm_conv1d"), w(l, "ssm_a"),
+                    w(l, "ssm_dt_bias"), self.conv[l], self.S[l], c["H"], c["dk"])
+                gate = w(l, "attn_gate") @ xn
+                hs = heads.reshape(c["H"], c["dk"])
+                normed = np.concatenate([rmsnorm(hs[h], w(l, "ssm_norm"), eps) for h in range(c["H"])])
+                mix = w(l, "ssm_out") @ (normed * silu(gate))
+            else:
+                f16 = (lambda a: np.asarray(a, np.float64).astype(np.float16).astype(np.float64)) \
+                    if self.kv_f16 else None
+                out, k_new, v_new = attention_core(
+                    w(l, "wq") @ xn, w(l, "wk") @ xn, w(l, "wv") @ xn, w(l, "q_norm"), w(l, "k_norm"),
+                    self.K[l], self.V[l], self.pos, c["n_heads"], c["n_kv"], c["hd"], c["rope_base"],
+                    kv_round=f16)
+                self.K[l] = np.concatenate([self.K[l], k_new[:, None, :]], axis=1)
+                self.V[l] = np.concatenate([self.V[l], v_new[:, None, :]], axis=1)
+                mix = w(l, "wo") @ out
+            x = x + mix
+            x = x + ffn(rmsnorm(x, w(l, "post_attn_norm"), eps), w(l, "ffn_gate"), w(l, "ffn_up"),
+                        w(l, "ffn_down"))
+        self.pos += 1
+        return w(-1, "lm_head") @ rmsnorm(x, w(-1, "final_norm"), eps)

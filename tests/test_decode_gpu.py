@@ -7,7 +7,7 @@ import pytest
 import anehip
 import oracle
 from conftest import rel_errs
-from model_util import SMALL, HostModel, copy_state_to_oracle
+from model_util import MID, SMALL, HostModel, copy_state_to_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -58,12 +58,6 @@ def test_batch_is_independent_sequences(small_host):
             l2, mx = rel_errs(g[b], seqs[b].forward(int(toks[step, b])))
             assert l2 <= TOL and mx <= TOL
     gm.close()
-
-
-# A model whose batch > 1 projections all run on the x-stationary GEMM with
-# K splits (the small model's 256-wide matrices take a single split).
-MID = dict(dim=512, hidden_dim=1024, n_layers=4, n_heads=4, n_kv_heads=1, head_dim=256, vocab_size=1000,
-           ssm_state_size=128, ssm_conv_kernel=4, ssm_group_count=4)
 
 
 @pytest.fixture(scope="module")

@@ -389,3 +389,164 @@ def test_argmax_total_cmp_last_of_ties(oracle_lib):
     assert oracle_lib.argmax(c) == 1  # positive NaN is the total_cmp maximum
     d = np.array([-np.inf, -np.inf], np.float32)
     assert oracle_lib.argmax(d) == 1
+
+
+# ------------------------------------------------ SiLU-mul, residual --------
+
+def test_silu_mul_inplace_vs_float64(oracle_lib):
+    """vec_silu_mul_inplace (scratch.rs:181-186): a <- a / (1 + exp(-a)) * b."""
+    a = oracle_lib.normal(40, 1, 4096, std=4.0)
+    a[:8] = [0.0, -0.0, 88.0, -88.0, 1e-30, -1e-30, 20.0, -20.0]
+    b = oracle_lib.normal(40, 2, 4096)
+    ref = np_ref.silu(a.astype(np.float64)) * b
+    got = a.copy()
+    oracle_lib.lib().ao_silu_mul_inplace(got, np.ascontiguousarray(b), got.size)
+    assert rel_l2(got, ref) < 1e-6
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < 1e-6
+    # exp(-a) overflows to inf for a < -88.7: the quotient is -0, not NaN
+    big = np.array([-100.0, -1000.0, 1000.0], np.float32)
+    one = np.ones(3, np.float32)
+    oracle_lib.lib().ao_silu_mul_inplace(big, one, 3)
+    assert big[0] == 0.0 and big[1] == 0.0 and big[2] == 1000.0 and not np.any(np.isnan(big))
+
+
+def test_residual_add_exact(oracle_lib):
+    x = oracle_lib.normal(41, 1, 1000)
+    y = oracle_lib.normal(41, 2, 1000)
+    got = x.copy()
+    oracle_lib.lib().ao_residual_add(got, y, got.size)
+    assert np.array_equal(got, x + y)
+
+
+# ------------------------------------------------ full forward --------------
+
+def _f64_weights(host):
+    """Name-keyed float64 view of a HostModel's tensors (dequantised matrices)."""
+    import anehip
+
+    names = {v: k.lower() for k, v in anehip.T.items()}
+    by = {}
+    for (layer, kind), (arr, rows, cols, quant) in host.tensors.items():
+        if quant:
+            a = np_ref.dequant(host.ggml_type, arr, rows, cols)
+        else:
+            a = np.asarray(arr, np.float64).reshape(rows, cols)
+            if rows == 1:
+                a = a.reshape(-1)
+        by[(layer, names[kind])] = a
+    return lambda layer, name: by[(layer, name)]
+
+
+def _forward64(host, kv_f16=True):
+    s = host.spec
+    cfg = dict(dim=s.dim, vocab=s.vocab_size, eps=s.rms_norm_eps, ksize=s.ssm_conv_kernel,
+               H=s.ssm_group_count, dk=s.ssm_state_size, n_heads=s.n_heads, n_kv=s.n_kv_heads,
+               hd=s.head_dim, rope_base=s.rope_freq_base)
+    return np_ref.Forward64(_f64_weights(host), s.layer_types, cfg, kv_f16)
+
+
+def _seed_state(oracle_lib, host, oseq, f64, pos, seed):
+    """Seeded mid-sequence state, written identically into the oracle's
+    sequence (fp16 KV bits) and the float64 forward."""
+    s = host.spec
+    for l, t in enumerate(s.layer_types):
+        if t == 0:
+            C, K = 3 * s.dim, s.ssm_conv_kernel
+            conv = oracle_lib.normal(seed, 10 * l + 1, C * K)
+            S = oracle_lib.normal(seed, 10 * l + 2, s.ssm_group_count * s.ssm_state_size ** 2, std=0.01)
+            oseq.view(l, 0, conv.size, np.float32)[:] = conv
+            oseq.view(l, 1, S.size, np.float32)[:] = S
+            f64.conv[l] = conv.astype(np.float64).reshape(C, K)
+            f64.S[l] = S.astype(np.float64).reshape(s.ssm_group_count, s.ssm_state_size, s.ssm_state_size)
+        else:
+            nkv, hd = s.n_kv_heads, s.head_dim
+            for which, store in ((2, f64.K), (3, f64.V)):
+                vals = oracle_lib.normal(seed, 10 * l + which, nkv * pos * hd)
+                if f64.kv_f16:
+                    vals = oracle_lib.f16_to_f32(oracle_lib.f32_to_f16(vals))
+                    cache = oseq.view(l, which, nkv * oseq.max_seq * hd, np.uint16)
+                    cache.reshape(nkv, oseq.max_seq, hd)[:, :pos] = oracle_lib.f32_to_f16(vals).reshape(nkv, pos, hd)
+                else:
+                    cache = oseq.view(l, which, nkv * oseq.max_seq * hd, np.float32)
+                    cache.reshape(nkv, oseq.max_seq, hd)[:, :pos] = vals.reshape(nkv, pos, hd)
+                store[l] = vals.astype(np.float64).reshape(nkv, pos, hd)
+    oseq.pos = pos
+    f64.pos = pos
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+@pytest.mark.parametrize("which,start", [("small", 0), ("small", 37), ("mid", 0), ("mid", 200)])
+def test_forward_vs_float64(oracle_lib, which, start, kv_f16):
+    """The oracle's qwen35_forward_token restatement (ao_forward_token) against
+    the float64 composition np_ref.Forward64 over 8 steps, from position 0 and
+    from a seeded mid-sequence state.  With the reference's fp32 KV cache the
+    two agree to float32 rounding: logits and recurrent states within 1e-5.
+    With the fp16 cache, a value that sits next to an fp16 rounding boundary can
+    round differently from fp32 and fp64 inputs (one fp16 ulp, 2^-11 relative,
+    in a few K/V elements), which moves the logits by up to ~1e-4: bound 1e-3,
+    the decode-logits bound of the parity target."""
+    import anehip
+    import oracle
+    from model_util import MID, SMALL, HostModel
+
+    spec = anehip.Spec(**(SMALL if which == "small" else MID))
+    host = HostModel(spec, seed=7 if which == "small" else 8)
+    oseq = oracle.OracleSeq(host.om, start + 16, kv_f16=kv_f16)
+    f64 = _forward64(host, kv_f16)
+    tol = 1e-3 if kv_f16 else 1e-5
+    if start:
+        _seed_state(oracle_lib, host, oseq, f64, start, seed=90 + start)
+    toks = oracle_lib.randint(11, start + 1, 8, spec.vocab_size)
+    toks[3] = spec.vocab_size + 5  # out-of-vocabulary id: x starts at zero (main.rs:967-970)
+    for i, t in enumerate(toks):
+        got = oseq.forward(int(t))
+        ref = f64.forward(int(t))
+        err = rel_l2(got, ref)
+        mx = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+        print(f"{which} pos {start + i}: rel_l2 {err:.2e} rel_max {mx:.2e}")
+        assert err < tol and mx < tol
+    assert oseq.pos == f64.pos == start + 8
+    for l, t in enumerate(spec.layer_types):
+        if t == 0:
+            S = oseq.view(l, 1, f64.S[l].size, np.float32).reshape(f64.S[l].shape)
+            assert rel_l2(S, f64.S[l]) < tol
+        else:
+            n = spec.n_kv_heads * oseq.max_seq * spec.head_dim
+            if kv_f16:
+                K = oracle_lib.f16_to_f32(oseq.view(l, 2, n, np.uint16))
+            else:
+                K = oseq.view(l, 2, n, np.float32)
+            K = K.reshape(spec.n_kv_heads, oseq.max_seq, -1)
+            assert rel_l2(K[:, :start + 8], f64.K[l]) < tol
+    oseq.close()
+    host.om.close()
+
+
+def test_forward64_detects_composition_mistakes(oracle_lib):
+    """The 1e-4 bound of the forward test is far below what a plausible
+    composition mistake does to the logits: dropping a residual, swapping the
+    FFN gate and up projections or skipping the DeltaNet decay each move them
+    by > 1e-2."""
+    import anehip
+    from model_util import SMALL, HostModel
+
+    host = HostModel(anehip.Spec(**SMALL), seed=7)
+    ref = _forward64(host)
+    toks = [3, 141, 59, 26]
+    base = [ref.forward(t) for t in toks]
+
+    def run(mut):
+        w0 = _f64_weights(host)
+        f = _forward64(host)
+        f.w = lambda l, n: mut(l, n, w0)
+        return [f.forward(t) for t in toks]
+
+    swaps = {"ffn_gate": "ffn_up", "ffn_up": "ffn_gate"}
+    variants = [
+        lambda l, n, w: w(l, swaps.get(n, n)),
+        lambda l, n, w: np.zeros_like(w(l, n)) if n == "ssm_a" else w(l, n),  # decay = 1
+        lambda l, n, w: w(l, n) * (1.0 if n != "post_attn_norm" else -1.0),
+    ]
+    for mut in variants:
+        out = run(mut)
+        assert max(rel_l2(o, b) for o, b in zip(out, base)) > 1e-2
