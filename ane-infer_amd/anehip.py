@@ -367,8 +367,13 @@ class Model(Context):
         self._check(lib().anehip_state_ptr(self.h, layer, which, C.byref(p), C.byref(n)))
         return p.value, n.value
 
-    def get_state(self, layer, which) -> np.ndarray:
+    def get_state(self, layer, which, seq=None) -> np.ndarray:
+        """State block `which` of a layer for the whole batch, or for sequence
+        `seq` only (the state is laid out with the sequence as leading dim)."""
         p, n = self.state_ptr(layer, which)
+        if seq is not None:
+            n //= self.batch
+            p += seq * n
         out = np.empty(n, np.uint8)
         self._check(lib().anehip_d2h(self.h, out.ctypes.data, C.c_void_p(p), n))
         return out.view(np.uint16 if which >= 2 else np.float32)

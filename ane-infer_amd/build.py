@@ -14,12 +14,13 @@ LIB = os.path.join(HERE, "libanehip.so")
 ENGINE_LIB = os.path.join(HERE, "libane_engine.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
+OBJ_DIR = os.path.join(HERE, "_build")
+
 HIPCC_FLAGS = [
     "-O3",
     "--offload-arch=gfx950",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # no packed fp32 instructions (v_pk_{add,mul,fma}_f32) in any kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
@@ -31,19 +32,36 @@ def sources():
     return sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
 
 
-def build(verbose: bool = False) -> str:
-    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB + ".tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, "-o", tmp, *sources()]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd, what):
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature
     errs = [l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip()]
     if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(errs))
-    if errs and verbose:
-        print("\n".join(errs), file=sys.stderr)
+        raise RuntimeError(f"{what} failed:\n" + "\n".join(errs))
+    return errs
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles every csrc/*.hip to an object (in parallel), links
+    libanehip.so, then builds libane_engine.so."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    srcs = sources()
+    objs = [os.path.join(OBJ_DIR, os.path.basename(f)[:-4] + ".o") for f in srcs]
+    cmds = [[hipcc, *HIPCC_FLAGS, "-c", "-o", o, f] for f, o in zip(srcs, objs)]
+    if verbose:
+        for c in cmds:
+            print(" ".join(c), flush=True)
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as ex:
+        warns = list(ex.map(lambda c: _run(c, "hipcc " + os.path.basename(c[-1])), cmds))
+    for w in warns:
+        if w and verbose:
+            print("\n".join(w), file=sys.stderr)
+    tmp = LIB + ".tmp"
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs], "link")
     os.replace(tmp, LIB)
     build_engine(verbose)
     return LIB

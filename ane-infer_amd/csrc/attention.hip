@@ -7,16 +7,18 @@
 // (crates/engine/src/deltanet.rs:565-669).
 //
 // Split-K ("flash-decoding"): the positions 0..pos of one sequence are cut
-// into tiles of 64 and chunks of tiles_per_chunk() tiles (at most 128 chunks
-// and ~2048 workgroups at the cache's capacity); one workgroup per (chunk, kv head, sequence)
-// streams its tiles' K and V rows once for all G query heads that share the
-// kv head (the next tile's loads in flight while the current one is used),
-// with an online softmax, and writes an unnormalised partial output with its
-// running max and sum.  attn_combine_kernel merges the chunks with a
-// log-sum-exp rescale and applies sigmoid(gate).  Chunks past the sequence's
-// length exit at once, so one launch shape (sized for the cache capacity)
-// serves every position and can be captured in a graph while pos lives in
-// device memory.
+// into tiles of 64, and the live tiles are spread evenly over the launch's
+// chunks (chunk_count(): at most 128 per sequence and kv head, about one
+// workgroup per CU over the whole batch); one workgroup per (chunk, kv head,
+// sequence) streams its tiles' K and V rows once for all G query heads that
+// share the kv head (the next tile's loads in flight while the current one is
+// used), with an online softmax, and writes an unnormalised partial output
+// with its running max and sum.  attn_combine_kernel merges the chunks with a
+// log-sum-exp rescale and applies sigmoid(gate).  Each workgroup derives its
+// tile range from the device-resident position (chunk_tiles()), so the work
+// follows the live length, not the cache's capacity, while one launch shape
+// serves every position and can be captured in a graph; with fewer live
+// tiles than chunks the chunks past the tile count exit at once.
 //
 // The KV cache keeps fp16 values (round-to-nearest-even) in the reference's
 // per-sequence layout [kv_head][max_seq][head_dim] (kv_cache.rs:7-27).  The
@@ -93,8 +95,8 @@ __device__ __forceinline__ void split8(const float *x, h8v &hi, h8v &lo) {
     }
 }
 
-// grid = (chunks, n_kv_heads, batch); a chunk is `tpw` tiles of 64 positions
-// (tiles_per_chunk()).  mix: per sequence [q_full | k | v] rows (K-split
+// grid = (chunks, n_kv_heads, batch); chunk c takes the live tiles
+// chunk_tiles() gives it.  mix: per sequence [q_full | k | v] rows (K-split
 // partial slices); q_full is [n_heads][q(256) | gate(256)].
 //
 // Per tile, on MFMA (v_mfma_f32_16x16x32_f16; operands A[i][k] / B[k][j] in
@@ -124,7 +126,7 @@ template <int G>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     MixIn mix, const float *__restrict__ q_norm, const float *__restrict__ k_norm,
     const float *__restrict__ inv_freq, const uint32_t *__restrict__ pos_arr, __half *__restrict__ k_cache,
-    __half *__restrict__ v_cache, int max_seq, int n_heads, int n_kv, int tpw, float *__restrict__ part_o,
+    __half *__restrict__ v_cache, int max_seq, int n_heads, int n_kv, float *__restrict__ part_o,
     float *__restrict__ part_ml, size_t cache_off, size_t row_stride, bool append) {
     __shared__ __align__(16) _Float16 vt[kHd * kCh];  // V^T of the tile, swizzled chunks
     __shared__ __align__(16) float qs[G][kHd];
@@ -139,9 +141,9 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const uint32_t pos = pos_arr[b];
     const int len = (int)pos + 1;
-    const int tb = c * tpw, te = min(tb + tpw, (len + kCh - 1) / kCh);  // tiles [tb, te)
-    if (tb >= te) return;  // uniform exit: nothing of this sequence here
     const int nch = gridDim.x;
+    int tb, te;  // tiles [tb, te)
+    if (!chunk_tiles(len, nch, c, &tb, &te)) return;  // uniform exit: nothing of this sequence here
     const size_t cache_base = cache_off + (size_t)b * row_stride + (size_t)kvh * max_seq * kHd;
     const bool has_new = (int)pos < te * kCh;  // this chunk holds the current position
     const __amdgpu_buffer_rsrc_t krs =
@@ -377,7 +379,7 @@ __global__ __launch_bounds__(64) void attn_append_kernel(MixIn mix, const float 
 template <int G>
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const uint32_t *__restrict__ pos_arr,
                                                                 const float *__restrict__ part_o,
-                                                                const float *__restrict__ part_ml, int nch, int tpw,
+                                                                const float *__restrict__ part_ml, int nch,
                                                                 int n_heads, int n_kv, float *__restrict__ out,
                                                                 _Float16 *__restrict__ out_hi,
                                                                 _Float16 *__restrict__ out_lo) {
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
     const int t = threadIdx.x, g = t >> 6, l = t & 63, h = blockIdx.x, b = blockIdx.y;
     const int kvh = h / G, hh = h % G;
     const int len = (int)pos_arr[b] + 1;
-    const int nc = ((len + kCh - 1) / kCh + tpw - 1) / tpw;  // active chunks
+    const int nc = active_chunks(len, nch);
     const size_t base = ((size_t)b * n_kv + kvh) * nch;
     const float4 gate = mix.at4(b, h * 2 * kHd + kHd + 4 * l);  // independent of the partials
     // maximum over the chunks
@@ -454,33 +456,25 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
     }
 }
 
-// Tiles of 64 positions per chunk (workgroup): the smallest power of two
-// that keeps at most 128 chunks per sequence and kv head and at most ~256
-// workgroups (one per CU) at the cache's capacity -- the combine merges at
-// most 128 partials per head, and each workgroup's q / k preparation and
-// partial write are amortised over several tiles when there are plenty of
-// workgroups (batch 32 on MI355X, ctx 1k / 8k / 32k: 20.6k / 15.4k / 8.4k
-// tok/s at ~256 workgroups against 20.1–20.3k / 14.7–14.9k / 8.4k at ~2048;
-// 512-token prefill 17.3k against 16.8k tok/s).  Batch 1 stays at 128 chunks.
-int tiles_per_chunk(int max_seq, int batch, int n_kv) {
+// Chunks per (sequence, kv head): at most 128 (the combine merges at most
+// 128 partials per head), at most one per 64-position tile of the cache, and
+// about one workgroup per CU over the launch (batch 32, 2 kv heads: 4
+// chunks; batch 1: 128).  Longer chunks at batch > 1 amortise each
+// workgroup's q / k preparation and partial write (batch 32, capacity =
+// context 1k / 8k / 32k: 20.6k / 15.4k / 8.4k tok/s at ~256 workgroups
+// against 20.1–20.3k / 14.7–14.9k / 8.4k at ~2048).
+int chunk_count(int max_seq, int batch, int n_kv) {
     const int tiles = (max_seq + kCh - 1) / kCh;
-    int tpw = 1;
-    auto chunks = [&] { return (tiles + tpw - 1) / tpw; };
-    while (chunks() > 128 || (tpw < tiles && (size_t)chunks() * n_kv * batch > 256)) tpw *= 2;
-    return tpw;
+    const int fill = std::max(1, kAttnWorkgroups / std::max(1, batch * n_kv));
+    return std::max(1, std::min(std::min(tiles, 128), fill));
 }
 
 }  // namespace
 
-void attn_layout(int max_seq, int batch, int n_kv, int *tpw, int *nch) {
-    *tpw = tiles_per_chunk(max_seq, batch, n_kv);
-    *nch = ((max_seq + kCh - 1) / kCh + *tpw - 1) / *tpw;
-}
+int attn_chunks(int max_seq, int batch, int n_kv) { return chunk_count(max_seq, batch, n_kv); }
 
 size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G) {
-    const int tpw = tiles_per_chunk(max_seq, batch, n_kv);
-    const size_t nch = (size_t)((max_seq + kCh - 1) / kCh + tpw - 1) / tpw;
-    return (size_t)batch * n_kv * nch * G * (kHd + 2);
+    return (size_t)batch * n_kv * chunk_count(max_seq, batch, n_kv) * G * (kHd + 2);
 }
 
 namespace {
@@ -490,8 +484,7 @@ int attention_impl(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, 
                    const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out, _Float16 *out_hi,
                    _Float16 *out_lo, size_t cache_off, size_t row_stride, bool append) {
     const int G = n_heads / n_kv;
-    const int tpw = tiles_per_chunk(max_seq, batch, n_kv);
-    const int nch = ((max_seq + kCh - 1) / kCh + tpw - 1) / tpw;
+    const int nch = chunk_count(max_seq, batch, n_kv);
     if ((size_t)max_seq * kHd * 2 >= (size_t)1 << 30)
         return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "attention: max_seq %d too large", max_seq);
     float *part_o = part;
@@ -500,12 +493,12 @@ int attention_impl(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, 
 #define ANEHIP_ATTN_CASE(GG)                                                                                   \
     case GG:                                                                                                   \
         hipLaunchKernelGGL(attn_partial_kernel<GG>, g1, dim3(kThreads), 0, stream, mix, q_norm, k_norm,        \
-                           inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, tpw, part_o, part_ml,     \
+                           inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, part_o, part_ml,          \
                            cache_off, row_stride, append);                                                    \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
         if (!out && !out_hi) return ANEHIP_OK; /* partials only */                                             \
         hipLaunchKernelGGL(attn_combine_kernel<GG>, g2, dim3(kThreads), 0, stream, mix, pos, part_o, part_ml,  \
-                           nch, tpw, n_heads, n_kv, out, out_hi, out_lo);                                     \
+                           nch, n_heads, n_kv, out, out_hi, out_lo);                                          \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
         return ANEHIP_OK;
     switch (G) {

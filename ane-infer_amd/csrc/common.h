@@ -100,9 +100,31 @@ struct GemvInput {
     // without outputs), their chunk layout and the position; head h's gate is
     // part[h * 512 + 256 + d] (K-split slices as above)
     const float *att_o = nullptr, *att_ml = nullptr;
-    int att_nch = 0, att_tpw = 0, att_g = 0;
+    int att_nch = 0, att_g = 0;
     const uint32_t *att_pos = nullptr;
 };
+
+// Decode attention split: a sequence of `len` positions has ceil(len / 64)
+// live tiles of 64 positions, spread evenly over min(nch, tiles) chunks; the
+// other chunks of the launch's nch are idle.  Shared by the attention kernels
+// and the merges of their partials.
+constexpr int kAttnTile = 64;
+// Workgroups a decode attention launch aims for over the whole batch: one per
+// CU of MI355X (256 CUs), the device this library is built for.
+constexpr int kAttnWorkgroups = 256;
+__host__ __device__ __forceinline__ int active_chunks(int len, int nch) {
+    const int tiles = (len + kAttnTile - 1) / kAttnTile;
+    return tiles < nch ? tiles : nch;
+}
+// Tiles [*tb, *te) of chunk c; false if the chunk is idle.
+__host__ __device__ __forceinline__ bool chunk_tiles(int len, int nch, int c, int *tb, int *te) {
+    const int tiles = (len + kAttnTile - 1) / kAttnTile;
+    const int na = tiles < nch ? tiles : nch;
+    if (c >= na) return false;
+    *tb = (int)(((long long)c * tiles) / na);
+    *te = (int)(((long long)(c + 1) * tiles) / na);
+    return true;
+}
 
 // A GEMV output read by a later kernel as kp partial slices: value (b, i) =
 // sum over q < kp of p[q * split + b * stride + i], q ascending.
@@ -253,9 +275,9 @@ int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
 
 // attention.hip.  mix per sequence: [q_full | k | v] rows.
 size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G);
-// Chunking of the decode attention's partials: tiles of 64 positions per
-// chunk (tpw) and chunks per (sequence, kv head) (nch) for this state shape.
-void attn_layout(int max_seq, int batch, int n_kv, int *tpw, int *nch);
+// Chunks per (sequence, kv head) of the decode attention's partials for this
+// state shape (the launch's grid.x).
+int attn_chunks(int max_seq, int batch, int n_kv);
 // With out == out_hi == nullptr only the chunk partials are written (a
 // batch-1 GEMV with GEMV_IN_ATTN_COMBINE merges them).
 int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,

@@ -354,8 +354,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
                                  fuse ? nullptr : M->attn_out, nullptr, nullptr));
             if (fuse) {
                 const int G = (int)(D.n_heads / D.n_kv_heads);
-                int tpw = 0, nch = 0;
-                attn_layout((int)M->max_seq, 1, (int)D.n_kv_heads, &tpw, &nch);
+                const int nch = attn_chunks((int)M->max_seq, 1, (int)D.n_kv_heads);
                 in3.mode = GEMV_IN_ATTN_COMBINE;
                 in3.part = M->pmix;
                 in3.kp = k1;
@@ -363,7 +362,6 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
                 in3.att_o = M->attn_part;
                 in3.att_ml = M->attn_part + (size_t)D.n_kv_heads * nch * G * 256;
                 in3.att_nch = nch;
-                in3.att_tpw = tpw;
                 in3.att_g = G;
                 in3.att_pos = M->d_pos;
             } else {

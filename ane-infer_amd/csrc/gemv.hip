@@ -180,6 +180,9 @@ __device__ __forceinline__ float sum_parts(const float *__restrict__ part, int k
 // `first` is false when a workgroup forms a second slice of the same input in
 // one launch: the one-off side effects (the x_out copy, the conv-window
 // commit) are then skipped.
+template <int KP, int NT, class Issue>
+__device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, float *xs, Issue &&issue);
+
 template <int MODE, int RB = 8, int NT = 256>
 __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0, int len, float *xs, float *red,
                                               bool first = true) {
@@ -554,7 +557,7 @@ __device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, 
     const int t = threadIdx.x, g = t >> 6, gq = g & 3, l = t & (kWave - 1);
     const int h = c0 / kAttnHd, G = in.att_g, kvh = h / G, hh = h % G;
     const int len = (int)in.att_pos[0] + 1;
-    const int nc = ((len + 63) / 64 + in.att_tpw - 1) / in.att_tpw;  // active chunks, >= 1
+    const int nc = active_chunks(len, in.att_nch);  // >= 1
     const size_t base = (size_t)kvh * in.att_nch;
     float4 gv[KP];
     load_parts4<KP>(gv, in.part, in.kp, in.part_stride, (size_t)((h * 2 * kAttnHd + kAttnHd) >> 2) + l);
@@ -2009,7 +2012,7 @@ void launch_gemm_xs_any(anehip_ctx *ctx, hipStream_t stream, GemmKernel kind, co
     const size_t ss = (size_t)batch * m;
     const int wgs = kind == GemmKernel::Xs16 ? (per == 1 ? 4 : 2) : kind == GemmKernel::Xs32 ? 3 : 1;
     const int gs = max(1, min(tiles, wgs * cus / ksplit));
-    const dim3 grid(gs * ksplit), block(kWave * kGemmWaves);
+    const dim3 grid(gs * ksplit);
 #define ANEHIP_XS(KERNEL, NT)                                                                                       \
     hipLaunchKernelGGL(KERNEL, grid, dim3(NT), 0, stream, w, xh, xl, xrows, out, (int)m, (int)n, (int)batch, ksplit, ss)
     if (kind == GemmKernel::Xs16) {
@@ -2140,7 +2143,7 @@ int launch_packed_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t
         MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_SILU_MUL || MODE == GEMV_IN_GATED_NORM ||
         MODE == GEMV_IN_ATTN_COMBINE;
     if constexpr (MODE == GEMV_IN_ATTN_COMBINE) {
-        if (per != 1 || n % 256 != 0 || !in.att_o || !in.att_ml || !in.att_pos || in.att_g <= 0 || in.att_tpw <= 0)
+        if (per != 1 || n % 256 != 0 || !in.att_o || !in.att_ml || !in.att_pos || in.att_g <= 0 || in.att_nch <= 0)
             return set_error(ctx->err, ANEHIP_EINVAL, "gemv: attention combine needs one head (256 columns) per split");
     }
     if constexpr (has_parts) {

@@ -53,12 +53,12 @@ def copy_state_to_oracle(gm: "anehip.Model", oseq: "oracle.OracleSeq", b: int):
     s = gm.spec
     for l in range(s.n_layers):
         if s.layer_types[l] == anehip.LAYER_DELTANET:
-            conv = gm.get_state(l, 0).reshape(gm.batch, -1)[b]
-            S = gm.get_state(l, 1).reshape(gm.batch, -1)[b]
+            conv = gm.get_state(l, 0, b)
+            S = gm.get_state(l, 1, b)
             oseq.view(l, 0, conv.size, np.float32)[:] = conv
             oseq.view(l, 1, S.size, np.float32)[:] = S
         else:
             for which in (2, 3):
-                kv = gm.get_state(l, which).reshape(gm.batch, -1)[b]
+                kv = gm.get_state(l, which, b)
                 oseq.view(l, which, kv.size, np.uint16)[:] = kv
     oseq.pos = gm.get_pos(b)

@@ -89,13 +89,13 @@ def _check_state(gm, oseq, b, spec, what):
     for l in range(spec.n_layers):
         if spec.layer_types[l] == anehip.LAYER_DELTANET:
             for which in (0, 1):
-                g = gm.get_state(l, which).reshape(gm.batch, -1)[b]
+                g = gm.get_state(l, which, b)
                 r = oseq.view(l, which, g.size, np.float32)
                 assert max(rel_errs(g, r)) <= TOL, (what, l, which)
         else:
             p = gm.get_pos(b)
             for which in (2, 3):
-                g = gm.get_state(l, which).reshape(gm.batch, spec.n_kv_heads, -1, spec.head_dim)[b][:, :p]
+                g = gm.get_state(l, which, b).reshape(spec.n_kv_heads, -1, spec.head_dim)[:, :p]
                 r = oseq.view(l, which, spec.n_kv_heads * oseq.max_seq * spec.head_dim,
                               np.uint16).reshape(spec.n_kv_heads, -1, spec.head_dim)[:, :p]
                 gf = g.view(np.float16).astype(np.float32)
@@ -250,39 +250,107 @@ def big_host():
     return HostModel(anehip.Spec(), seed=11)
 
 
-@pytest.mark.parametrize("ctx_len,batch", [(1024, 1), (8192, 1), (32768, 1), (1024, 32), (8192, 32)])
-def test_qwen35_2b_shape_step(big_host, ctx_len, batch):
-    """Random-init 24-layer Qwen3.5-2B shape, Q8_0 weights, fp16 KV cache
-    filled with N(0,1) at positions < ctx-1, DeltaNet states N(0, 0.01)
-    (windows N(0,1)); one step at pos = ctx-1 vs the oracle."""
-    spec = big_host.spec
-    gm = _model(big_host, batch, ctx_len)
+def _fill_state(gm, spec, seed=0):
+    """DeltaNet states N(0, 0.01), conv windows N(0, 1), fp16 KV N(0, 1)."""
     for l in range(spec.n_layers):
         if spec.layer_types[l] == anehip.LAYER_DELTANET:
             p, n = gm.state_ptr(l, 0)
-            gm.fill_random(p, n // 4, 0, 100 + l, 0.0, 1.0)
+            gm.fill_random(p, n // 4, 0, seed + 100 + l, 0.0, 1.0)
             p, n = gm.state_ptr(l, 1)
-            gm.fill_random(p, n // 4, 0, 200 + l, 0.0, 0.01)
+            gm.fill_random(p, n // 4, 0, seed + 200 + l, 0.0, 0.01)
         else:
             for which in (2, 3):
                 p, n = gm.state_ptr(l, which)
-                gm.fill_random(p, n // 2, 0, 300 + 10 * l + which, 0.0, 1.0, f16=True)
-    for b in range(batch):
-        gm.set_pos(b, ctx_len - 1)
-    toks = oracle.randint(12, ctx_len, batch, spec.vocab_size)
-    check = sorted({0, batch - 1})
+                gm.fill_random(p, n // 2, 0, seed + 300 + 10 * l + which, 0.0, 1.0, f16=True)
+
+
+def _step_vs_oracle(host, gm, positions, check, tok_seed, steps=1, label=""):
+    """Sets every sequence's position, copies the checked sequences' state to
+    oracle sequences and compares `steps` decode steps' logits."""
+    spec = host.spec
+    for b, p in enumerate(positions):
+        gm.set_pos(b, int(p))
     seqs = {}
     for b in check:
-        seqs[b] = big_host.seq(ctx_len)
+        seqs[b] = host.seq(gm.max_seq)
         copy_state_to_oracle(gm, seqs[b], b)
-    g = gm.step(toks)
-    for b in check:
-        r = seqs[b].forward(int(toks[b]))
-        l2, mx = rel_errs(g[b], r)
-        print(f"2B ctx={ctx_len} B={batch} seq {b}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
-        assert l2 <= TOL and mx <= TOL
-        seqs[b].close()
+    for step in range(steps):
+        toks = oracle.randint(tok_seed, step, len(positions), spec.vocab_size)
+        g = gm.step(toks)
+        for b in check:
+            r = seqs[b].forward(int(toks[b]))
+            l2, mx = rel_errs(g[b], r)
+            print(f"{label} step {step} seq {b} pos {int(positions[b]) + step}: rel_l2={l2:.2e} rel_max={mx:.2e}",
+                  flush=True)
+            assert l2 <= TOL and mx <= TOL, (label, step, b)
+    for q in seqs.values():
+        q.close()
+
+
+@pytest.mark.parametrize("ctx_len,batch", [(1024, 1), (8192, 1), (32768, 1), (1024, 32), (8192, 32),
+                                           (32768, 32)])
+def test_qwen35_2b_shape_step(big_host, ctx_len, batch):
+    """Random-init 24-layer Qwen3.5-2B shape, Q8_0 weights, fp16 KV cache
+    filled with N(0,1) at positions < ctx-1, DeltaNet states N(0, 0.01)
+    (windows N(0,1)); one step at pos = ctx-1 (cache capacity = ctx) vs the
+    oracle, sequences 0 and batch-1."""
+    gm = _model(big_host, batch, ctx_len)
+    _fill_state(gm, big_host.spec)
+    _step_vs_oracle(big_host, gm, [ctx_len - 1] * batch, sorted({0, batch - 1}), 12,
+                    label=f"2B ctx={ctx_len} B={batch}")
     gm.close()
+
+
+@pytest.mark.parametrize("batch,positions,check", [
+    (1, [1023], [0]),
+    (1, [8191], [0]),
+    # ragged live lengths in one batch: a single position, a partial first
+    # tile, tile and chunk boundaries, mid-tile / mid-chunk positions and the
+    # cache's last position
+    (32, [1023, 0, 5, 63, 64, 3000, 8191, 8192, 12345, 20000, 32767] + [1000 + 977 * i for i in range(21)],
+     [0, 1, 2, 5, 6, 7, 10, 31]),
+])
+def test_qwen35_2b_shape_live_length(big_host, batch, positions, check):
+    """2B shape with a 32k-position cache holding shorter live contexts: the
+    attention splits the live tiles, not the capacity, over its chunks; one
+    step per sequence vs the oracle."""
+    gm = _model(big_host, batch, 32768)
+    _fill_state(gm, big_host.spec, seed=7)
+    _step_vs_oracle(big_host, gm, positions, check, 13, label=f"2B cap=32k B={batch}")
+    gm.close()
+
+
+def test_ragged_positions_across_chunk_boundaries(mid_host):
+    """Mid-size model, batch 4, 4096-position cache, positions 5 / 3000 / 63 /
+    4090: 4 steps per sequence, so live lengths cross tile boundaries and the
+    split of the live tiles over the chunks changes from step to step."""
+    gm = _model(mid_host, 4, 4096)
+    _fill_state(gm, mid_host.spec, seed=21)
+    _step_vs_oracle(mid_host, gm, [5, 3000, 63, 4090], [0, 1, 2, 3], 14, steps=4, label="mid ragged")
+    gm.close()
+
+
+@pytest.mark.parametrize("n", [100])
+def test_prefill_long_prompt_large_cache(mid_host, n):
+    """anehip_prefill of a 100-token prompt (chunks of 32, 32, 32, 4) into a
+    2048-position cache: chunk rows see 1 and 2 live tiles spread over the
+    attention's chunks; the last logits, states and KV rows vs the oracle run
+    token by token, then 2 decode steps."""
+    spec = mid_host.spec
+    gm = _model(mid_host, 1, 2048)
+    oseq = mid_host.seq(2048)
+    toks = oracle.randint(33, n, n, spec.vocab_size)
+    g = gm.prefill(0, toks)
+    for t in toks:
+        r = oseq.forward(int(t))
+    l2, mx = rel_errs(g, r)
+    print(f"prefill n={n} cap 2048: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+    assert l2 <= TOL and mx <= TOL
+    _check_state(gm, oseq, 0, spec, "after prefill")
+    for t in oracle.randint(34, n, 2, spec.vocab_size):
+        assert max(rel_errs(gm.step([t])[0], oseq.forward(int(t)))) <= TOL
+    gm.close()
+    oseq.close()
 
 
 def test_qwen35_2b_shape_prefill(big_host):

@@ -146,6 +146,13 @@ def test_attention_chunk_boundaries(gpu_ctx, oracle_lib, positions):
     _attn_case(gpu_ctx, oracle_lib, 2, 8, 2, 300, positions, seed=sum(positions) + 11)
 
 
+def test_attention_live_length_split(gpu_ctx, oracle_lib):
+    """An 8192-position cache at batch 8 (16 chunks per sequence and kv head)
+    holding ragged live lengths: fewer live tiles than chunks, uneven splits
+    of the live tiles over all chunks, the cache's last position."""
+    _attn_case(gpu_ctx, oracle_lib, 8, 8, 2, 8192, [0, 63, 64, 700, 4095, 5000, 8000, 8191], seed=77, tol=5e-4)
+
+
 @pytest.mark.parametrize("n_heads,n_kv", [(8, 2), (4, 2), (2, 2)])
 def test_attention_gqa_ratios(gpu_ctx, oracle_lib, n_heads, n_kv):
     _attn_case(gpu_ctx, oracle_lib, 1, n_heads, n_kv, 200, [150], seed=n_heads * 10 + n_kv)
