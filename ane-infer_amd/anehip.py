@@ -75,6 +75,7 @@ def lib():
             "anehip_deltanet_step": (C.c_int, [vp, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
             "anehip_gated_rmsnorm": (C.c_int, [vp, u32, u32, vp, vp, vp, f32, vp]),
             "anehip_attention_step": (C.c_int, [vp, u32, u32, u32, u32, vp, vp, vp, f32, vp, vp, vp, vp]),
+            "anehip_attention_step_noalloc": (C.c_int, [vp, u32, u32, u32, u32, vp, vp, vp, f32, vp, vp, vp, vp]),
             "anehip_argmax": (C.c_int, [vp, vp, u32, u32, vp]),
             "anehip_fill_random": (C.c_int, [vp, vp, sz, u32, u32, C.c_uint64, f32, f32]),
             "anehip_quantize": (C.c_int, [vp, u32, vp, u32, u32, vp]),

@@ -5,6 +5,7 @@
 // (crates/engine/src/deltanet.rs, scratch.rs, crates/cli/src/main.rs).
 #include "common.h"
 
+#include <mutex>
 #include <vector>
 
 using namespace anehip;
@@ -91,6 +92,50 @@ __global__ void quantize_kernel(const float *__restrict__ w, size_t nblocks, uin
 #pragma unroll
         for (int i = 0; i < 16; i++) o[2 + i] = (uint8_t)(q[i] | (q[i + 16] << 4));
     }
+}
+
+// Scratch of anehip_attention_step_noalloc: the RoPE table (first 256
+// floats) and the attention's chunk partials, at most kScratchFloats floats
+// (4 MiB) in all.  Each GPU the library runs on holds its own copy until the
+// process ends.  In host code `scratch` names a host-side stand-in, never the
+// device memory: host code uses the address hipGetSymbolAddress returned for
+// the device (NoAllocSlot::ptr).
+constexpr size_t kScratchFloats = (size_t)1 << 20;
+constexpr size_t kScratchTable = 256;  // floats reserved for the RoPE table
+__device__ __align__(256) float scratch[kScratchFloats];
+
+struct NoAllocSlot {
+    float *ptr = nullptr;     // device address of `scratch` on this device
+    float table_base = 0.0f;  // rope base of the table now in the scratch (0: none)
+};
+constexpr int kMaxDevices = 64;
+NoAllocSlot g_noalloc[kMaxDevices];
+std::mutex g_noalloc_mu;
+
+// The scratch address on ctx's device (looked up once per device, with that
+// device current), and a RoPE table for `rope_base` at its start.
+int noalloc_scratch(anehip_ctx *ctx, float rope_base, float **out) {
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "noalloc: device %d beyond %d", ctx->device, kMaxDevices);
+    NoAllocSlot &slot = g_noalloc[ctx->device];
+    ANEHIP_HIP_TRY(ctx->err, hipSetDevice(ctx->device));
+    if (!slot.ptr) {
+        void *p = nullptr;
+        ANEHIP_HIP_TRY(ctx->err, hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return set_error(ctx->err, ANEHIP_EHIP, "noalloc: no device address for the scratch array");
+        slot.ptr = static_cast<float *>(p);
+    }
+    if (slot.table_base != rope_base) {
+        float f[128];
+        rope_inv_freq(rope_base, 256, f);
+        // ordered after the stream's queued work; the host array must outlive the copy
+        ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(slot.ptr, f, sizeof f, hipMemcpyHostToDevice, ctx->stream));
+        ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+        slot.table_base = rope_base;
+    }
+    *out = slot.ptr;
+    return ANEHIP_OK;
 }
 
 }  // namespace
@@ -184,6 +229,37 @@ int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uin
     return launch_attention(ctx, ctx->stream, (int)batch, (int)n_heads, (int)n_kv_heads, (int)max_seq, mix, q_norm,
                             k_norm, ctx->inv_freq, pos, reinterpret_cast<__half *>(k_cache),
                             reinterpret_cast<__half *>(v_cache), ctx->ws.partial, out, nullptr, nullptr);
+}
+
+int anehip_attention_step_noalloc(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads,
+                                  uint32_t max_seq, const float *qkv, const float *q_norm, const float *k_norm,
+                                  float rope_base, const uint32_t *pos, uint16_t *k_cache, uint16_t *v_cache,
+                                  float *out) {
+    NEED_CTX(ctx, "attention_step_noalloc");
+    if (!qkv || !q_norm || !k_norm || !pos || !k_cache || !v_cache || !out)
+        return set_error(ctx->err, ANEHIP_EINVAL, "attention_step_noalloc: null pointer");
+    if (!batch || !n_heads || !n_kv_heads || !max_seq || n_heads % n_kv_heads)
+        return set_error(ctx->err, ANEHIP_EINVAL, "attention_step_noalloc: bad shape");
+    if (!(rope_base > 0.0f))
+        return set_error(ctx->err, ANEHIP_EINVAL, "attention_step_noalloc: rope_base must be > 0");
+    const uint32_t G = n_heads / n_kv_heads;
+    if (G != 1 && G != 2 && G != 4)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "attention_step_noalloc: %u query heads per kv head", G);
+    const size_t need = attn_partial_floats((int)batch, (int)n_kv_heads, (int)max_seq, (int)G);
+    if (need > kScratchFloats - kScratchTable)
+        return set_error(ctx->err, ANEHIP_ERANGE,
+                         "attention_step_noalloc: %zu partial floats needed, the static scratch holds %zu "
+                         "(batch %u, %u kv heads, max_seq %u)",
+                         need, kScratchFloats - kScratchTable, batch, n_kv_heads, max_seq);
+    float *ptr = nullptr;
+    int rc = noalloc_scratch(ctx, rope_base, &ptr);
+    if (rc) return rc;
+    MixIn mix;
+    mix.p = qkv;
+    mix.stride = (int)(n_heads * 2 * 256 + 2 * n_kv_heads * 256);
+    return launch_attention(ctx, ctx->stream, (int)batch, (int)n_heads, (int)n_kv_heads, (int)max_seq, mix, q_norm,
+                            k_norm, ptr, pos, reinterpret_cast<__half *>(k_cache),
+                            reinterpret_cast<__half *>(v_cache), ptr + kScratchTable, out, nullptr, nullptr);
 }
 
 int anehip_argmax(anehip_ctx *ctx, const float *logits, uint32_t rows, uint32_t n, uint32_t *out) {

@@ -252,6 +252,26 @@ int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uin
                           float rope_base, const uint32_t *pos, uint16_t *k_cache, uint16_t *v_cache,
                           float *out);
 
+/*
+ * anehip_attention_step that allocates nothing: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as anehip_attention_step.  The RoPE table and
+ * the chunk partials live in a static device array of 4 MiB per GPU, held
+ * until the process ends; a call whose partials do not fit (more than
+ * 1,048,320 floats: batch x n_kv_heads x chunks x (n_heads / n_kv_heads) x 258,
+ * about 4 MB whatever max_seq at batch x n_kv_heads <= 256) returns
+ * ANEHIP_ERANGE and launches nothing.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (other streams or contexts on the same
+ * device) race.  The first call on a device, and a call with a rope_base
+ * other than the last one's on that device, synchronises ctx's stream once to
+ * upload the table.
+ */
+int anehip_attention_step_noalloc(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads,
+                                  uint32_t max_seq, const float *qkv, const float *q_norm, const float *k_norm,
+                                  float rope_base, const uint32_t *pos, uint16_t *k_cache, uint16_t *v_cache,
+                                  float *out);
+
 /* Greedy sampling per row: index of the maximum under f32::total_cmp, the
  * last of equal maxima (greedy_sample, main.rs:1767-1775).  logits
  * [rows][n], out [rows] (device). */
