@@ -181,12 +181,12 @@ int anehip_deltanet_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, cons
     // batch > 1: one workgroup per head and sequence (commits every window)
     if (batch > 1)
         return launch_deltanet_head(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
-                                    conv_state, S, out_heads, 0, nullptr, 0.0f, nullptr, nullptr);
+                                    conv_state, S, out_heads, 0, nullptr, 0.0f, Planes{});
     int rc = launch_deltanet_step(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
                                   conv_state, S, out_heads);
     if (rc) return rc;
     return launch_dn_finish(ctx, ctx->stream, (int)batch, (int)n_heads, mq, conv_state, nullptr, 0, nullptr, nullptr,
-                            nullptr, nullptr, 0.0f);
+                            Planes{}, 0.0f);
 }
 
 int anehip_gated_rmsnorm(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, const float *heads, const float *gate,
@@ -197,8 +197,8 @@ int anehip_gated_rmsnorm(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, cons
     MixIn mg;
     mg.p = gate;
     mg.stride = (int)n_heads * 128;
-    return launch_dn_finish(ctx, ctx->stream, (int)batch, (int)n_heads, mg, nullptr, heads, 0, norm_w, out, nullptr,
-                            nullptr, eps);
+    return launch_dn_finish(ctx, ctx->stream, (int)batch, (int)n_heads, mg, nullptr, heads, 0, norm_w, out, Planes{},
+                            eps);
 }
 
 int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads, uint32_t max_seq,
@@ -228,7 +228,7 @@ int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uin
     mix.stride = (int)(n_heads * 2 * 256 + 2 * n_kv_heads * 256);
     return launch_attention(ctx, ctx->stream, (int)batch, (int)n_heads, (int)n_kv_heads, (int)max_seq, mix, q_norm,
                             k_norm, ctx->inv_freq, pos, reinterpret_cast<__half *>(k_cache),
-                            reinterpret_cast<__half *>(v_cache), ctx->ws.partial, out, nullptr, nullptr);
+                            reinterpret_cast<__half *>(v_cache), ctx->ws.partial, out, Planes{});
 }
 
 int anehip_attention_step_noalloc(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads,
@@ -259,7 +259,7 @@ int anehip_attention_step_noalloc(anehip_ctx *ctx, uint32_t batch, uint32_t n_he
     mix.stride = (int)(n_heads * 2 * 256 + 2 * n_kv_heads * 256);
     return launch_attention(ctx, ctx->stream, (int)batch, (int)n_heads, (int)n_kv_heads, (int)max_seq, mix, q_norm,
                             k_norm, ptr, pos, reinterpret_cast<__half *>(k_cache),
-                            reinterpret_cast<__half *>(v_cache), ptr + kScratchTable, out, nullptr, nullptr);
+                            reinterpret_cast<__half *>(v_cache), ptr + kScratchTable, out, Planes{});
 }
 
 int anehip_argmax(anehip_ctx *ctx, const float *logits, uint32_t rows, uint32_t n, uint32_t *out) {

@@ -79,6 +79,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWord3 = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
+constexpr float kPScale = 16384.0f;  // 2^14: probabilities in the PV MFMA operands
 
 // LDS row of V^T (one head dim, 64 positions = 8 chunks of 8): chunk c of
 // row D sits at slot c ^ swz(D), which keeps both the transposing writes (8
@@ -134,6 +135,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     __shared__ __align__(16) float pt[G][kCh];        // probabilities of the tile
     __shared__ __align__(16) __half knew[kHd], vnew[kHd];
     __shared__ float rmax[4][16], rsum[4][16], rscale[16];
+    __shared__ float qmax[G];  // largest |q| / 16 of each query head (range-safe q fragments)
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int li = lane & 15, lg = lane >> 4;  // MFMA operand row / column, k group
@@ -182,6 +184,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         float q4[4];
         norm_rope_head(mix, b, h * 2 * kHd, q_norm, inv_freq, pos, lane, q4);
         *reinterpret_cast<float4 *>(&qs[wave][4 * lane]) = make_float4(q4[0], q4[1], q4[2], q4[3]);
+        const float qm = wave_max(fmaxf(fmaxf(fabsf(q4[0]), fabsf(q4[1])), fmaxf(fabsf(q4[2]), fabsf(q4[3]))));
+        if (lane == 0) qmax[wave] = qm * 0.0625f;
     }
     if (has_new && wave == G % 4) {
         // k: RMSNorm + RoPE, v: as is; both rounded to fp16 and appended
@@ -208,20 +212,27 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     }
     lds_barrier();
     // q B fragments (lane l: head l % 16, dims 32s + 8 (l / 16) ..), scaled by
-    // 1/sqrt(256) = 1/16 (exact), as fp16 hi + lo; 4 (k-step, lane) pairs per thread
+    // 1/sqrt(256) = 1/16 (exact) and by 2^-qe per head (qe from the head's
+    // largest value, so that fp16 neither overflows nor loses the low bits;
+    // the scores are scaled back by 2^qe), as fp16 hi + lo; 4 (k-step, lane)
+    // pairs per thread
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int e = t + 256 * j, fs = e >> 6, fl = e & 63, fh = fl & 15, fg = fl >> 4;
         float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (fh < G) {
+            const int qe = group_exp(qmax[fh]);
             const float4 a = *reinterpret_cast<const float4 *>(&qs[fh][32 * fs + 8 * fg]);
             const float4 bq = *reinterpret_cast<const float4 *>(&qs[fh][32 * fs + 8 * fg + 4]);
-            x[0] = a.x * 0.0625f; x[1] = a.y * 0.0625f; x[2] = a.z * 0.0625f; x[3] = a.w * 0.0625f;
-            x[4] = bq.x * 0.0625f; x[5] = bq.y * 0.0625f; x[6] = bq.z * 0.0625f; x[7] = bq.w * 0.0625f;
+            const float qv[8] = {a.x, a.y, a.z, a.w, bq.x, bq.y, bq.z, bq.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) x[i] = ldexpf(qv[i] * 0.0625f, -qe);
         }
         split8(x, qf[fs][0][fl], qf[fs][1][fl]);
     }
     lds_barrier();
+    // scores of head li come out scaled by 2^-qe (li < G)
+    const int qe_li = li < G ? group_exp(qmax[li]) : 0;
 
     // per head li (< G): running max / sum; PV accumulators of dim block db:
     // rows = heads 4 lg .. 4 lg + 3, column = dim 64 wave + 16 db + li
@@ -265,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         const int p0 = row0 + 16 * wave + 4 * lg;
         float sv[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) sv[e] = p0 + e < len ? sc[e] : -INFINITY;
+        for (int e = 0; e < 4; e++) sv[e] = p0 + e < len ? ldexpf(sc[e], qe_li) : -INFINITY;
         float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -296,6 +307,9 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         for (int db = 0; db < 4; db++)
 #pragma unroll
             for (int e = 0; e < 4; e++) o[db][e] *= rs[e];
+        // probabilities (<= 1) times 2^14 as fp16 hi + lo: the low bits of
+        // small probabilities stay out of fp16's subnormal range; the
+        // partial output is scaled back by 2^-14 at the end
         h8v ph[2], pl[2];
 #pragma unroll
         for (int s = 0; s < 2; s++) {
@@ -303,7 +317,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
             if (li < G) {
                 const float4 a = *reinterpret_cast<const float4 *>(&pt[li][32 * s + 8 * lg]);
                 const float4 bq = *reinterpret_cast<const float4 *>(&pt[li][32 * s + 8 * lg + 4]);
-                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = bq.x; x[5] = bq.y; x[6] = bq.z; x[7] = bq.w;
+                x[0] = a.x * kPScale; x[1] = a.y * kPScale; x[2] = a.z * kPScale; x[3] = a.w * kPScale;
+                x[4] = bq.x * kPScale; x[5] = bq.y * kPScale; x[6] = bq.z * kPScale; x[7] = bq.w * kPScale;
             }
             split8(x, ph[s], pl[s]);
         }
@@ -335,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         if (hh < G) {
             const size_t slot = (((size_t)b * n_kv + kvh) * nch + c) * G + hh;
 #pragma unroll
-            for (int db = 0; db < 4; db++) part_o[slot * kHd + 64 * wave + 16 * db + li] = o[db][e];
+            for (int db = 0; db < 4; db++) part_o[slot * kHd + 64 * wave + 16 * db + li] = o[db][e] * (1.0f / kPScale);
         }
     }
     if (wave == 0 && lane < G) {
@@ -374,15 +389,14 @@ __global__ __launch_bounds__(64) void attn_append_kernel(MixIn mix, const float 
 // dims 4l..4l+3 of chunks g, g + 4, g + 8, ...; merges them with a log-sum-exp
 // rescale against the maximum over all chunks, adds the 4 groups through
 // LDS, normalises and multiplies by sigmoid(gate) (deltanet.rs:667-669).
-// out: [batch][n_heads * 256] fp32, or fragment-order fp16 hi/lo planes
-// out_hi / out_lo when out_hi is not null.
+// out: [batch][n_heads * 256] fp32, or range-safe fragment-order planes xp
+// (Planes) when xp.hi is not null.
 template <int G>
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const uint32_t *__restrict__ pos_arr,
                                                                 const float *__restrict__ part_o,
                                                                 const float *__restrict__ part_ml, int nch,
                                                                 int n_heads, int n_kv, float *__restrict__ out,
-                                                                _Float16 *__restrict__ out_hi,
-                                                                _Float16 *__restrict__ out_lo) {
+                                                                Planes xp) {
     __shared__ float red[4];
     __shared__ float4 accs[4][64];
     __shared__ float dens[4][64];
@@ -441,18 +455,21 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
     }
     const float gv[4] = {gate.x, gate.y, gate.z, gate.w};
     const float sv[4] = {s.x, s.y, s.z, s.w};
+    float v[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int d = 4 * l + i;
-        const float v = (sv[i] / dsum) * (1.0f / (1.0f + expf(-gv[i])));
-        if (out_hi) {
-            const size_t o = xf_index(b, h * kHd + d);
-            const _Float16 hi = (_Float16)v;
-            out_hi[o] = hi;
-            out_lo[o] = (_Float16)(v - (float)hi);
-        } else {
-            out[(size_t)b * n_heads * kHd + (size_t)h * kHd + d] = v;
-        }
+    for (int i = 0; i < 4; i++) v[i] = (sv[i] / dsum) * (1.0f / (1.0f + expf(-gv[i])));
+    if (xp.hi) {
+        // the head is two 128-column groups: lanes 0-31 and 32-63
+        const int e = group_exp(half_max32(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])))));
+        h4v vh, vl;  // 4 consecutive columns of a fragment-order plane
+        split4_scaled(v, e, vh, vl);
+        const size_t o = xf_index(b, h * kHd + 4 * l);
+        *reinterpret_cast<h4v *>(xp.hi + o) = vh;
+        *reinterpret_cast<h4v *>(xp.lo + o) = vl;
+        if ((l & 31) == 0) xp.xe[xe_index(b, h * kHd + 4 * l, n_heads * kHd)] = (int8_t)e;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[(size_t)b * n_heads * kHd + (size_t)h * kHd + 4 * l + i] = v[i];
     }
 }
 
@@ -481,8 +498,8 @@ namespace {
 
 int attention_impl(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
                    const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
-                   const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out, _Float16 *out_hi,
-                   _Float16 *out_lo, size_t cache_off, size_t row_stride, bool append) {
+                   const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out, const Planes &xp,
+                   size_t cache_off, size_t row_stride, bool append) {
     const int G = n_heads / n_kv;
     const int nch = chunk_count(max_seq, batch, n_kv);
     if ((size_t)max_seq * kHd * 2 >= (size_t)1 << 30)
@@ -496,9 +513,9 @@ int attention_impl(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, 
                            inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, part_o, part_ml,          \
                            cache_off, row_stride, append);                                                    \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
-        if (!out && !out_hi) return ANEHIP_OK; /* partials only */                                             \
+        if (!out && !xp.hi) return ANEHIP_OK; /* partials only */                                              \
         hipLaunchKernelGGL(attn_combine_kernel<GG>, g2, dim3(kThreads), 0, stream, mix, pos, part_o, part_ml,  \
-                           nch, n_heads, n_kv, out, out_hi, out_lo);                                          \
+                           nch, n_heads, n_kv, out, xp);                                                      \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
         return ANEHIP_OK;
     switch (G) {
@@ -517,20 +534,20 @@ int attention_impl(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, 
 int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
                      const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
                      const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,
-                     _Float16 *out_hi, _Float16 *out_lo) {
+                     const Planes &xp) {
     return attention_impl(ctx, stream, batch, n_heads, n_kv, max_seq, mix, q_norm, k_norm, inv_freq, pos, k_cache,
-                          v_cache, part, out, out_hi, out_lo, 0, (size_t)n_kv * max_seq * kHd, true);
+                          v_cache, part, out, xp, 0, (size_t)n_kv * max_seq * kHd, true);
 }
 
 int launch_attention_prefill(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, int n_kv, int max_seq,
                              const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
                              const uint32_t *pos, __half *k_cache, __half *v_cache, size_t cache_off, float *part,
-                             _Float16 *out_hi, _Float16 *out_lo) {
+                             const Planes &xp) {
     hipLaunchKernelGGL(attn_append_kernel, dim3(n_kv, rows), dim3(64), 0, stream, mix, k_norm, inv_freq, pos, k_cache,
                        v_cache, cache_off, max_seq, n_heads, n_kv);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return attention_impl(ctx, stream, rows, n_heads, n_kv, max_seq, mix, q_norm, k_norm, inv_freq, pos, k_cache,
-                          v_cache, part, nullptr, out_hi, out_lo, cache_off, 0, false);
+                          v_cache, part, nullptr, xp, cache_off, 0, false);
 }
 
 }  // namespace anehip

@@ -210,13 +210,88 @@ __host__ __device__ inline size_t xf_index(int b, int c) {
     return ((size_t)(c >> 4) * 64 + (size_t)(b + 32 * ((c >> 3) & 1))) * 8 + (size_t)(c & 7);
 }
 inline size_t xf_plane_len(size_t n) { return 32 * n; }
+
+// Range-safe planes.  fp16 alone covers 2^-24 .. 65504 and fp32 activations
+// do not stay inside it, so each batch row is stored in groups of 128
+// columns scaled by a power of two: group g of row b holds hi + lo of
+// x * 2^-e, e = xe[b * xe_stride(n) + g] (int8), chosen so that the group's
+// largest |x| scales into [2^14, 2^15) (hi cannot overflow; lo keeps the full
+// 2^-22 relative accuracy down to 2^-17 of the group's largest value).
+// Power-of-two scaling is exact.  A GEMM brings the groups it reads to one
+// exponent per batch row (the largest) and scales its fp32 sums back.  e is
+// kept in int8: it is clamped to -128 (groups whose largest |x| is below
+// 2^-113 still scale into fp16's normal range by 2^128 down to |x| ~ 2^-142),
+// an all-zero group has e = kXeEmpty (-128), a group holding inf / NaN e = 0
+// (they propagate, as in fp32).  A row's exponents are padded to 16 bytes,
+// so a GEMM reads those of the groups of its K split (2 per panel, splits
+// aligned to their size) with one load.
+constexpr int kXeGroup = 128;
+constexpr int kXeEmpty = -128;
+__host__ __device__ __forceinline__ int xe_stride(int n) { return ((n + kXeGroup - 1) / kXeGroup + 15) & ~15; }
+inline size_t xe_bytes(size_t n) { return 32 * (size_t)xe_stride((int)n); }
+struct Planes {
+    _Float16 *hi = nullptr, *lo = nullptr;
+    int8_t *xe = nullptr;
+};
+__host__ __device__ __forceinline__ int xe_index(int b, int c, int n) { return b * xe_stride(n) + c / kXeGroup; }
+// Group exponent from the group's largest |x|.
+__device__ __forceinline__ int group_exp(float amax) {
+    if (amax == 0.0f) return kXeEmpty;
+    if (!(amax <= 3.402823466e38f)) return 0;  // inf / NaN
+    int ex;
+    (void)frexpf(amax, &ex);  // amax in [2^(ex-1), 2^ex)
+    return ex - 15 < -128 ? -128 : ex - 15;
+}
+// hi + lo of v * 2^-e.
+__device__ __forceinline__ void split_scaled(float v, int e, _Float16 &hi, _Float16 &lo) {
+    const float s = ldexpf(v, -e);
+    hi = (_Float16)s;
+    lo = (_Float16)(s - (float)hi);
+}
+// Lane maxima on DPP (VALU, no LDS round trip).  dpp_max<CTRL>: the max of a
+// lane's value and its DPP partner's; row_max16: every lane gets the max of
+// its 16-lane row (xor 1, xor 2 by quad_perm, then row_half_mirror and
+// row_mirror); half_max32: of its 32-lane half (two rows combined through
+// readlane).  All lanes of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v),
+                                                                        __builtin_bit_cast(int, v), CTRL, 0xf, 0xf,
+                                                                        false)));
+}
+__device__ __forceinline__ float row_max16(float v) {
+    return dpp_max<0x140>(dpp_max<0x141>(dpp_max<0x4E>(dpp_max<0xB1>(v))));
+}
+__device__ __forceinline__ float half_max32(float v) {
+    const int b = __builtin_bit_cast(int, row_max16(v));
+    const auto rd = [&](int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, lane)); };
+    return (threadIdx.x & 32) ? fmaxf(rd(32), rd(48)) : fmaxf(rd(0), rd(16));
+}
+__device__ __forceinline__ float wave_max64(float v) {
+    const int b = __builtin_bit_cast(int, row_max16(v));
+    const auto rd = [&](int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, lane)); };
+    return fmaxf(fmaxf(rd(0), rd(16)), fmaxf(rd(32), rd(48)));
+}
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+// 4 values (consecutive columns of one fragment-order row) split at once.
+__device__ __forceinline__ void split4_scaled(const float (&v)[4], int e, h4v &hi, h4v &lo) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        _Float16 h, l;
+        split_scaled(v[c], e, h, l);
+        hi[c] = h;
+        lo[c] = l;
+    }
+}
+// Factor 2^(e - E) (e <= E) as fp16; 0 once below fp16's range.
+__device__ __forceinline__ _Float16 xe_factor(int e, int E) { return (_Float16)ldexpf(1.0f, e - E); }
 // Panel MFMA GEMM for batch 2..32: out[ks][b][r] (final values when ksplit
 // is 1) from the fragment-order hi / lo planes of x (launch_split_x, or the
 // hi / lo outputs of the element-wise kernels), ksplit from gemm_packed_ksplit.
 // m must be a multiple of 4.
 int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
-                       uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit);
+                       uint32_t n, const Planes &xp, uint32_t batch, float *out, int ksplit);
 // Whether gemm_packed_ksplit's split of [m x n] at this batch runs on an
 // x-stationary kernel, which can also take x as fp32 rows [batch][n] (no
 // planes needed): launch_gemm_xs_rows writes out[ks][b][r] for its
@@ -225,18 +300,13 @@ bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
 int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                         uint32_t n, const float *x, uint32_t batch, float *out);
 // x [batch][n] fp32 -> fragment-order hi / lo planes (xf_plane_len(n) halves each).
-int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t batch, uint32_t n, _Float16 *xh,
-                   _Float16 *xl);
+int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t batch, uint32_t n, const Planes &xp);
 // K splits the batch-1 panel GEMV takes for an [m x n] matrix (<= 8) whose
 // input is formed by prologue `mode` (a GEMV_IN_* value): norm prologues and
 // the SiLU-mul prologue favour fewer splits.
 int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int mode = GEMV_IN_PLAIN);
 int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                        uint32_t n, const GemvInput &in, float *out, int ksplit);
-// Small-batch GEMM (batch 2..32) on MFMA from fp16 hi/lo input planes
-// [batch][n]; writes out[ks][batch][m].
-int launch_gemm_planes(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
-                       uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit);
 // Batch-1 GEMV whose input is formed by `in` (see GemvInMode); writes
 // out[ks][m] partials (final values if ksplit == 1).
 int launch_gemv_fused(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
@@ -249,12 +319,12 @@ int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
 // Batch > 1: the whole DeltaNet step of a head in one workgroup -- conv +
 // SiLU, L2 norms, beta / decay, recurrence, all conv windows committed -- and
 // either the raw head outputs (out, fp32) or, with out == nullptr, the gated
-// RMSNorm (gate from mix rows at gate_off, norm_w, eps) as fragment-order
-// fp16 hi/lo planes out_hi / out_lo.
+// RMSNorm (gate from mix rows at gate_off, norm_w, eps) as range-safe
+// fragment-order planes xp.
 int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *out, int gate_off,
-                         const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo);
+                         const float *norm_w, float eps, const Planes &xp);
 // Prefill: `rows` (<= 32) consecutive tokens of one sequence (mix row t =
 // token t) through the DeltaNet step of every head, the state (the sequence's
 // block S) kept in registers across the rows.  Three kernels: every token's
@@ -265,25 +335,25 @@ int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
 int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *prep, float *heads,
-                         int gate_off, const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo);
+                         int gate_off, const float *norm_w, float eps, const Planes &xp);
 // Commits the q/k conv windows (if conv_state) and, if heads, writes the gated
 // RMSNorm of the heads (gate from mix rows at gate_off) to out (fp32) or, if
-// out_hi, to fragment-order fp16 hi/lo planes out_hi / out_lo (xf_index).
+// xp.hi, to range-safe fragment-order planes (Planes).
 int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                      float *conv_state, const float *heads, int gate_off, const float *norm_w, float *out,
-                     _Float16 *out_hi, _Float16 *out_lo, float eps);
+                     const Planes &xp, float eps);
 
 // attention.hip.  mix per sequence: [q_full | k | v] rows.
 size_t attn_partial_floats(int batch, int n_kv, int max_seq, int G);
 // Chunks per (sequence, kv head) of the decode attention's partials for this
 // state shape (the launch's grid.x).
 int attn_chunks(int max_seq, int batch, int n_kv);
-// With out == out_hi == nullptr only the chunk partials are written (a
+// With out == xp.hi == nullptr only the chunk partials are written (a
 // batch-1 GEMV with GEMV_IN_ATTN_COMBINE merges them).
 int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, int n_kv, int max_seq,
                      const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
                      const uint32_t *pos, __half *k_cache, __half *v_cache, float *part, float *out,
-                     _Float16 *out_hi, _Float16 *out_lo);
+                     const Planes &xp);
 // Prefill of `rows` consecutive tokens of one sequence (row t at position
 // pos[t], q / k / v in mix row t): appends every row's k / v to the cache at
 // cache_off (halves; the sequence's [kv_head][max_seq][256] block), then
@@ -291,21 +361,20 @@ int launch_attention(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads
 int launch_attention_prefill(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, int n_kv, int max_seq,
                              const MixIn &mix, const float *q_norm, const float *k_norm, const float *inv_freq,
                              const uint32_t *pos, __half *k_cache, __half *v_cache, size_t cache_off, float *part,
-                             _Float16 *out_hi, _Float16 *out_lo);
+                             const Planes &xp);
 
 // elementwise.hip
 int launch_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const float *x, const float *w, float *out,
                    float eps);
-// The next three write their result as fp32 (xn / h) or, when hi is not null,
-// as fragment-order fp16 hi/lo planes (xf_index) for the panel MFMA GEMM.
+// The next three write their result as fp32 (xn / h) or, when xp.hi is not
+// null, as range-safe fragment-order planes (Planes) for the panel MFMA GEMM.
 int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const uint32_t *tokens,
                          const float *emb, uint32_t vocab, float *x, const float *w, float *xn, float eps,
-                         _Float16 *hi = nullptr, _Float16 *lo = nullptr);
+                         const Planes &xp = Planes{});
 int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
-                            int ksplit, const float *w, float *xn, float eps, _Float16 *hi = nullptr,
-                            _Float16 *lo = nullptr);
+                            int ksplit, const float *w, float *xn, float eps, const Planes &xp = Planes{});
 int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit,
-                            float *h, _Float16 *hi = nullptr, _Float16 *lo = nullptr);
+                            float *h, const Planes &xp = Planes{});
 int launch_silu_mul(anehip_ctx *ctx, hipStream_t s, float *a, const float *b, size_t n);
 int launch_residual_add(anehip_ctx *ctx, hipStream_t s, float *x, const float *y, size_t n);
 size_t argmax_workspace_bytes(int rows);

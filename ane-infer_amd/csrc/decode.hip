@@ -77,8 +77,10 @@ struct Model {
     float *x0 = nullptr, *x1 = nullptr;                  // residual stream (two buffers, alternating)
     float *pmix = nullptr, *p0 = nullptr, *p1 = nullptr;  // GEMV outputs as K-split partial slices
     float *heads = nullptr, *attn_out = nullptr, *logits = nullptr, *attn_part = nullptr;
-    float *xin = nullptr;        // GEMM input planes (batch > 1): hi then lo, xin_len halves each
+    float *xin = nullptr;        // GEMM input planes (batch > 1): hi then lo, xin_len halves each,
+                                 // then the group exponents (xe_cnt bytes)
     size_t xin_len = 0;          // fragment-order plane of the widest GEMM input (32 rows)
+    size_t xe_cnt = 0;
     size_t part_len = 0;         // floats per partial buffer
     void *argmax_ws = nullptr;
     // prefill scratch for chunks of up to kPrefillRows tokens of one sequence
@@ -86,9 +88,19 @@ struct Model {
     struct {
         float *x = nullptr, *xn = nullptr, *pmix = nullptr, *p0 = nullptr, *p1 = nullptr, *attn_part = nullptr;
         float *logits = nullptr;
-        _Float16 *xin = nullptr;  // planes: hi then lo, xin_len halves each
+        _Float16 *xin = nullptr;  // planes: hi then lo, xin_len halves each, then xe_cnt exponents
         uint32_t *d_tokens = nullptr, *d_pos = nullptr;
     } pf;
+    static Planes planes_at(void *base, size_t len) {
+        Planes p;
+        p.hi = static_cast<_Float16 *>(base);
+        p.lo = p.hi + len;
+        p.xe = reinterpret_cast<int8_t *>(p.lo + len);
+        return p;
+    }
+    size_t planes_bytes() const { return 2 * xin_len * sizeof(_Float16) + xe_cnt; }
+    Planes planes() const { return planes_at(xin, xin_len); }
+    Planes pf_planes() const { return planes_at(pf.xin, xin_len); }
     // graph
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -351,7 +363,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
             const bool fuse = gemv_packed_ksplit(ctx, d, cols3) == (int)(qd / 256);
             TRY(launch_attention(ctx, s, 1, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
                                  L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part,
-                                 fuse ? nullptr : M->attn_out, nullptr, nullptr));
+                                 fuse ? nullptr : M->attn_out, Planes{}));
             if (fuse) {
                 const int G = (int)(D.n_heads / D.n_kv_heads);
                 const int nch = attn_chunks((int)M->max_seq, 1, (int)D.n_kv_heads);
@@ -398,8 +410,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     // lm_head, input = final RMSNorm(residual + last FFN output), formed once
     // by its own kernel: as a prologue each of the lm_head's ~1200 workgroups
     // would re-read the residual and every partial slice (measured 19 us)
-    TRY(launch_residual_rmsnorm(ctx, s, 1, (int)d, cur, prev_part, prev_kp, M->final_norm, M->heads, eps, nullptr,
-                                nullptr));
+    TRY(launch_residual_rmsnorm(ctx, s, 1, (int)d, cur, prev_part, prev_kp, M->final_norm, M->heads, eps));
     GemvInput inf;
     inf.mode = GEMV_IN_PLAIN;
     inf.x = M->heads;
@@ -422,16 +433,16 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
     const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
     const uint32_t qd = D.n_heads * D.head_dim;
     const float eps = D.rms_norm_eps;
-    _Float16 *xh = reinterpret_cast<_Float16 *>(M->xin), *xl = xh + M->xin_len;  // GEMM input planes
+    const Planes xp = M->planes();  // GEMM input planes
     float *x = M->x0;
     TRY(launch_embed_rmsnorm(ctx, s, B, (int)d, M->d_tokens, M->embedding, D.vocab_size, x, M->layers[0].attn_norm,
-                             nullptr, eps, xh, xl));
+                             nullptr, eps, xp));
     for (uint32_t l = 0; l < D.n_layers; l++) {
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
         const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
         const int k1 = gemm_packed_ksplit(ctx, rows_in, d, B);
-        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xh, xl, B, M->pmix, k1));
+        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xp, B, M->pmix, k1));
         MixIn mix;
         mix.p = M->pmix;
         mix.kp = k1;
@@ -441,29 +452,29 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
         if (dn) {
             TRY(launch_deltanet_head(ctx, s, B, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
                                      L.conv1d, L.ssm_a, L.dt_bias, L.conv_state, L.S, nullptr, (int)C, L.ssm_norm,
-                                     eps, xh, xl));
+                                     eps, xp));
             cols3 = d;
         } else {
             TRY(launch_attention(ctx, s, B, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
-                                 L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part, nullptr, xh, xl));
+                                 L.k_norm, M->inv_freq, M->d_pos, L.kc, L.vc, M->attn_part, nullptr, xp));
             cols3 = qd;
         }
         const int k3 = gemm_packed_ksplit(ctx, d, cols3, B);
-        TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xh, xl, B, M->p0, k3));
-        TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, nullptr, eps, xh, xl));
+        TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xp, B, M->p0, k3));
+        TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, nullptr, eps, xp));
         const int k4 = gemm_packed_ksplit(ctx, 2 * F, d, B);
-        TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xh, xl, B, M->p1, k4));
-        TRY(launch_silu_mul_stacked(ctx, s, B, (int)F, M->p1, k4, nullptr, xh, xl));
+        TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, B, M->p1, k4));
+        TRY(launch_silu_mul_stacked(ctx, s, B, (int)F, M->p1, k4, nullptr, xp));
         const int k5 = gemm_packed_ksplit(ctx, d, F, B);
-        TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xh, xl, B, M->p0, k5));
+        TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xp, B, M->p0, k5));
         const float *next_norm = l + 1 < D.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
-        TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k5, next_norm, nullptr, eps, xh, xl));
+        TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k5, next_norm, nullptr, eps, xp));
     }
     const int kf = gemm_packed_ksplit(ctx, D.vocab_size, d, B);
     if (kf == 1) {
-        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xh, xl, B, M->logits, 1));
+        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xp, B, M->logits, 1));
     } else {
-        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xh, xl, B, M->pmix, kf));
+        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xp, B, M->pmix, kf));
         TRY(launch_sum_partials(ctx, s, M->pmix, M->logits, (size_t)B * D.vocab_size, kf));
     }
     return ANEHIP_OK;
@@ -564,7 +575,7 @@ int alloc_prefill(anehip_ctx *ctx, Model *M) {
     } a[] = {{(void **)&M->pf.x, kPrefillRows * d * 4}, {(void **)&M->pf.xn, kPrefillRows * d * 4},
              {(void **)&M->pf.pmix, part * 4}, {(void **)&M->pf.p0, part * 4}, {(void **)&M->pf.p1, part * 4},
              {(void **)&M->pf.attn_part, std::max<size_t>(attn, 1) * 4}, {(void **)&M->pf.logits, (size_t)D.vocab_size * 4},
-             {(void **)&M->pf.xin, 2 * M->xin_len * sizeof(_Float16)}, {(void **)&M->pf.d_tokens, kPrefillRows * 4},
+             {(void **)&M->pf.xin, M->planes_bytes()}, {(void **)&M->pf.d_tokens, kPrefillRows * 4},
              {(void **)&M->pf.d_pos, kPrefillRows * 4}};
     for (auto &e : a) {
         if (hipMalloc(e.p, e.bytes) != hipSuccess) {
@@ -586,16 +597,16 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
     const anehip_model_desc &D = M->desc;
     const uint32_t d = D.dim, F = D.hidden_dim, H = D.ssm_group_count, C = 3 * d;
     const float eps = D.rms_norm_eps;
-    _Float16 *xh = M->pf.xin, *xl = xh + M->xin_len;
+    const Planes xp = M->pf_planes();
     float *x = M->pf.x;
     TRY(launch_embed_rmsnorm(ctx, s, T, (int)d, M->pf.d_tokens, M->embedding, D.vocab_size, x,
-                             M->layers[0].attn_norm, nullptr, eps, xh, xl));
+                             M->layers[0].attn_norm, nullptr, eps, xp));
     for (uint32_t l = 0; l < D.n_layers; l++) {
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
         const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
         const int k1 = gemm_packed_ksplit(ctx, rows_in, d, T);
-        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xh, xl, T, M->pf.pmix, k1));
+        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xp, T, M->pf.pmix, k1));
         MixIn mix;
         mix.p = M->pf.pmix;
         mix.kp = k1;
@@ -606,29 +617,28 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
             TRY(launch_deltanet_scan(ctx, s, T, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
                                      L.conv1d, L.ssm_a, L.dt_bias, L.conv_state + (size_t)seq * C * kConvK,
                                      L.S + (size_t)seq * H * kDk * kDk, M->pf.p1, M->pf.xn, (int)C, L.ssm_norm,
-                                     eps, xh, xl));
+                                     eps, xp));
             cols3 = d;
         } else {
             const size_t cache_off = (size_t)seq * D.n_kv_heads * M->max_seq * D.head_dim;
             TRY(launch_attention_prefill(ctx, s, T, (int)D.n_heads, (int)D.n_kv_heads, (int)M->max_seq, mix, L.q_norm,
                                          L.k_norm, M->inv_freq, M->pf.d_pos, L.kc, L.vc, cache_off, M->pf.attn_part,
-                                         xh, xl));
+                                         xp));
             cols3 = D.n_heads * D.head_dim;
         }
         const int k3 = gemm_packed_ksplit(ctx, d, cols3, T);
-        TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xh, xl, T, M->pf.p0, k3));
-        TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k3, L.post_attn_norm, nullptr, eps, xh, xl));
+        TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xp, T, M->pf.p0, k3));
+        TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k3, L.post_attn_norm, nullptr, eps, xp));
         const int k4 = gemm_packed_ksplit(ctx, 2 * F, d, T);
-        TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xh, xl, T, M->pf.p1, k4));
-        TRY(launch_silu_mul_stacked(ctx, s, T, (int)F, M->pf.p1, k4, nullptr, xh, xl));
+        TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, T, M->pf.p1, k4));
+        TRY(launch_silu_mul_stacked(ctx, s, T, (int)F, M->pf.p1, k4, nullptr, xp));
         const int k5 = gemm_packed_ksplit(ctx, d, F, T);
-        TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xh, xl, T, M->pf.p0, k5));
+        TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xp, T, M->pf.p0, k5));
         if (l + 1 < D.n_layers)
             TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k5, M->layers[l + 1].attn_norm, nullptr, eps,
-                                        xh, xl));
+                                        xp));
         else if (logits)  // final RMSNorm as fp32 rows
-            TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k5, M->final_norm, M->pf.xn, eps, nullptr,
-                                        nullptr));
+            TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k5, M->final_norm, M->pf.xn, eps));
     }
     if (!logits) return ANEHIP_OK;
     GemvInput inf;
@@ -935,6 +945,7 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     size_t nmax = d > F ? d : F;
     if (qd > nmax) nmax = qd;
     M->xin_len = xf_plane_len(nmax);
+    M->xe_cnt = xe_bytes(nmax);
     M->part_len = part_floats(ctx, M);
     r = r ? r : alloc((void **)&M->d_pos, 64 * sizeof(uint32_t));
     r = r ? r : alloc((void **)&M->d_tokens, 64 * sizeof(uint32_t));
@@ -946,7 +957,7 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     r = r ? r : alloc((void **)&M->p1, M->part_len * sizeof(float));
     r = r ? r : alloc((void **)&M->heads, batch * d * sizeof(float));
     r = r ? r : alloc((void **)&M->attn_out, batch * (qd ? qd : 1) * sizeof(float));
-    r = r ? r : alloc((void **)&M->xin, M->xin_len * sizeof(float));
+    r = r ? r : alloc((void **)&M->xin, M->planes_bytes());
     r = r ? r : alloc((void **)&M->logits, batch * (size_t)D.vocab_size * sizeof(float));
     r = r ? r : alloc(&M->argmax_ws, argmax_workspace_bytes((int)batch));
     if (M->rows_attn) {

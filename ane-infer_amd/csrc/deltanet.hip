@@ -55,6 +55,19 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (row(0) + row(16)) + (row(32) + row(48));
 }
 
+// Range-safe plane write (see Planes) of one head's gated-norm output: a
+// head is one 128-column group, column c0 + t held by thread t < 128.  The
+// group's exponent e comes from the caller, which takes the largest |value|
+// along with the norm's sum of squares: |v| = inv_rms * |o * w * SiLU(g)|,
+// so max |o * w * SiLU(g)| times inv_rms gives the group's binade (to a few
+// ulps, which only moves the scaled maximum within [2^14, 2^15] by as much).
+__device__ __forceinline__ void head_to_planes(float v, int b, int c0, int n, int e, const Planes &xp) {
+    const int t = threadIdx.x;
+    const size_t o = xf_index(b, c0 + t);
+    split_scaled(v, e, xp.hi[o], xp.lo[o]);
+    if (t == 0) xp.xe[xe_index(b, c0, n)] = (int8_t)e;
+}
+
 // grid = (dv / 32, n_heads, batch).  mix / mbeta / malpha: the qkv, beta and
 // alpha projections of each sequence ([3 chunk], [n_heads], [n_heads]), read
 // as K-split partial slices (KP >= their number).
@@ -189,15 +202,14 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(
 // q/k conv windows of head h (shift left, append the new input:
 // deltanet_cache.rs:34-42); if `heads` is not null, applies the per-head
 // RMSNorm with ssm_norm and the SiLU(gate) product (deltanet.rs:517-533),
-// written as fp32 (out) or as fragment-order fp16 hi/lo planes (out_hi /
-// out_lo, the input format of the panel MFMA GEMM).  grid = (n_heads, batch), 128 threads
-// (one per element of the head).
+// written as fp32 (out) or as range-safe fragment-order planes (xp, the
+// input format of the panel MFMA GEMM).  grid = (n_heads, batch), 128
+// threads (one per element of the head).
 __global__ __launch_bounds__(kDk) void dn_finish_kernel(MixIn mix, float *__restrict__ conv_state,
                                                         const float *__restrict__ heads, int gate_off,
                                                         const float *__restrict__ norm_w, float *__restrict__ out,
-                                                        _Float16 *__restrict__ out_hi, _Float16 *__restrict__ out_lo,
-                                                        int n_heads, float eps) {
-    __shared__ float red[2];
+                                                        Planes xp, int n_heads, float eps) {
+    __shared__ float red[2], mred[2];
     const int t = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int chunk = n_heads * kDk;
     if (conv_state) {
@@ -210,21 +222,20 @@ __global__ __launch_bounds__(kDk) void dn_finish_kernel(MixIn mix, float *__rest
     }
     if (!heads) return;
     const float x = heads[(size_t)b * chunk + h * kDk + t];
+    const float g = mix.at(b, gate_off + h * kDk + t);
+    const float gs = g / (1.0f + expf(-g));
     float ss = wave_sum(x * x);
-    if ((t & 63) == 0) red[t >> 6] = ss;
+    const float wm = xp.hi ? wave_max64(fabsf(x * norm_w[t] * gs)) : 0.0f;
+    if ((t & 63) == 0) {
+        red[t >> 6] = ss;
+        mred[t >> 6] = wm;
+    }
     __syncthreads();
     const float ms = (red[0] + red[1]) / (float)kDk;
     const float inv_rms = 1.0f / sqrtf(ms + eps);
-    const float g = mix.at(b, gate_off + h * kDk + t);
-    const float v = ((x * inv_rms) * norm_w[t]) * (g / (1.0f + expf(-g)));
-    if (out_hi) {
-        const size_t o = xf_index(b, h * kDk + t);
-        const _Float16 hi = (_Float16)v;
-        out_hi[o] = hi;
-        out_lo[o] = (_Float16)(v - (float)hi);
-    } else {
-        out[(size_t)b * chunk + h * kDk + t] = v;
-    }
+    const float v = ((x * inv_rms) * norm_w[t]) * gs;
+    if (xp.hi) head_to_planes(v, b, h * kDk, chunk, group_exp(fmaxf(mred[0], mred[1]) * inv_rms), xp);
+    else out[(size_t)b * chunk + h * kDk + t] = v;
 }
 
 // Batch > 1: one workgroup (256 threads) per (head, sequence) holding the
@@ -238,11 +249,10 @@ template <int KP>
 __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
     MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
     const float *__restrict__ dt_bias, float *__restrict__ conv_state, float *__restrict__ S, float *__restrict__ out,
-    int gate_off, const float *__restrict__ norm_w, float eps, _Float16 *__restrict__ out_hi,
-    _Float16 *__restrict__ out_lo, int n_heads) {
+    int gate_off, const float *__restrict__ norm_w, float eps, Planes xp, int n_heads) {
     __shared__ float qn[kDk], kn[kDk], vv[kDk];
     __shared__ __align__(16) float part[8][kDk];
-    __shared__ float red[4];
+    __shared__ float red[4], mred[2];
 
     const int t = threadIdx.x;
     const int h = blockIdx.x, b = blockIdx.y;
@@ -360,18 +370,20 @@ __global__ __launch_bounds__(kThreads) void deltanet_head_kernel(
         if (t < kDk) out[(size_t)b * chunk + h * kDk + t] = o;
         return;
     }
+    const float gt = mix.add<KP>(xg);
+    const float gs = gt / (1.0f + expf(-gt));
     const float ss = wave_sum(o * o);  // waves 2-3 contribute zeros
+    const float wm = wave_max64(fabsf(o * nw * gs));
     __syncthreads();                   // red[] is reused
-    if ((t & 63) == 0) red[t >> 6] = ss;
+    if ((t & 63) == 0) {
+        red[t >> 6] = ss;
+        if (t < kDk) mred[t >> 6] = wm;  // waves 0-1 hold the head's outputs
+    }
     __syncthreads();
     if (t >= kDk) return;
     const float inv_rms = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + eps);
-    const float gt = mix.add<KP>(xg);
-    const float v = ((o * inv_rms) * nw) * (gt / (1.0f + expf(-gt)));
-    const size_t xo = xf_index(b, h * kDk + t);
-    const _Float16 hi = (_Float16)v;
-    out_hi[xo] = hi;
-    out_lo[xo] = (_Float16)(v - (float)hi);
+    const float v = ((o * inv_rms) * nw) * gs;
+    head_to_planes(v, b, h * kDk, chunk, group_exp(fmaxf(mred[0], mred[1]) * inv_rms), xp);
 }
 
 // Prefill: T consecutive tokens of one sequence (mix row t = token t), in
@@ -543,11 +555,9 @@ __global__ __launch_bounds__(kWave) void deltanet_scan_kernel(const float *__res
 template <int KP>
 __global__ __launch_bounds__(kDk) void dn_scan_finish_kernel(MixIn mix, float *__restrict__ conv_state,
                                                              const float *__restrict__ heads, int gate_off,
-                                                             const float *__restrict__ norm_w,
-                                                             _Float16 *__restrict__ out_hi,
-                                                             _Float16 *__restrict__ out_lo, int n_heads, float eps,
-                                                             int T) {
-    __shared__ float red[2];
+                                                             const float *__restrict__ norm_w, Planes xp,
+                                                             int n_heads, float eps, int T) {
+    __shared__ float red[2], mred[2];
     const int t = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int chunk = n_heads * kDk;
     // every load first (partial slices clamped to the last one, window
@@ -577,16 +587,18 @@ __global__ __launch_bounds__(kDk) void dn_scan_finish_kernel(MixIn mix, float *_
                 f32x4{nv[0], nv[1], nv[2], nv[3]};
         }
     }
+    const float g = mix.add<KP>(xg);
+    const float gs = g / (1.0f + expf(-g));
     const float ss = wave_sum(x * x);
-    if ((t & 63) == 0) red[t >> 6] = ss;
+    const float wm = wave_max64(fabsf(x * norm_w[t] * gs));
+    if ((t & 63) == 0) {
+        red[t >> 6] = ss;
+        mred[t >> 6] = wm;
+    }
     __syncthreads();
     const float inv_rms = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + eps);
-    const float g = mix.add<KP>(xg);
-    const float v = ((x * inv_rms) * norm_w[t]) * (g / (1.0f + expf(-g)));
-    const size_t o = xf_index(b, h * kDk + t);
-    const _Float16 hi = (_Float16)v;
-    out_hi[o] = hi;
-    out_lo[o] = (_Float16)(v - (float)hi);
+    const float v = ((x * inv_rms) * norm_w[t]) * gs;
+    head_to_planes(v, b, h * kDk, chunk, group_exp(fmaxf(mred[0], mred[1]) * inv_rms), xp);
 }
 
 }  // namespace
@@ -594,7 +606,7 @@ __global__ __launch_bounds__(kDk) void dn_scan_finish_kernel(MixIn mix, float *_
 int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *prep, float *heads,
-                         int gate_off, const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo) {
+                         int gate_off, const float *norm_w, float eps, const Planes &xp) {
     const int kp = max(mix.kp, max(beta.kp, alpha.kp));
     if (kp > 16 || rows < 1 || rows > kScanMaxT)
         return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_scan: %d K splits (at most 16), %d rows (1..%d)", kp, rows,
@@ -606,7 +618,7 @@ int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_he
     hipLaunchKernelGGL(deltanet_scan_kernel<kScanCols>, dim3(kDk / kScanCols, n_heads), dim3(kWave), 0, stream,     \
                        prep, bd, S, heads, n_heads, rows);                                                           \
     hipLaunchKernelGGL(dn_scan_finish_kernel<KP>, dim3(n_heads, rows), dim3(kDk), 0, stream, mix, conv_state, heads, \
-                       gate_off, norm_w, out_hi, out_lo, n_heads, eps, rows)
+                       gate_off, norm_w, xp, n_heads, eps, rows)
     if (kp <= 1) {
         DN_SCAN(1);
     } else if (kp <= 4) {
@@ -622,14 +634,14 @@ int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_he
 int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *out, int gate_off,
-                         const float *norm_w, float eps, _Float16 *out_hi, _Float16 *out_lo) {
-    if (!out && !out_hi) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_head: no output");
+                         const float *norm_w, float eps, const Planes &xp) {
+    if (!out && !xp.hi) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_head: no output");
     const int kp = max(mix.kp, max(beta.kp, alpha.kp));
     if (kp > 16) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_head: %d K splits (at most 16)", kp);
     const dim3 grid(n_heads, batch), block(kThreads);
 #define DN_HEAD(KP)                                                                                                  \
     hipLaunchKernelGGL(deltanet_head_kernel<KP>, grid, block, 0, stream, mix, beta, alpha, conv_w, ssm_a, dt_bias,   \
-                       conv_state, S, out, gate_off, norm_w, eps, out_hi, out_lo, n_heads)
+                       conv_state, S, out, gate_off, norm_w, eps, xp, n_heads)
     if (kp <= 1)
         DN_HEAD(1);
     else if (kp <= 4)
@@ -663,9 +675,9 @@ int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
 
 int launch_dn_finish(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                      float *conv_state, const float *heads, int gate_off, const float *norm_w, float *out,
-                     _Float16 *out_hi, _Float16 *out_lo, float eps) {
+                     const Planes &xp, float eps) {
     hipLaunchKernelGGL(dn_finish_kernel, dim3(n_heads, batch), dim3(kDk), 0, stream, mix, conv_state, heads, gate_off,
-                       norm_w, out, out_hi, out_lo, n_heads, eps);
+                       norm_w, out, xp, n_heads, eps);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

@@ -33,26 +33,36 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return s;
 }
 
+// Largest |value| per 128-column group of a row, gathered in LDS by the
+// threads of a workgroup (bit patterns of non-negative floats order as ints).
+constexpr int kMaxGroups = 512;  // rows of up to 65536 columns
+
 // out[b] = x[b] * (1/sqrt(mean(x[b]^2) + eps)) * w     (main.rs:1106-1113),
-// written as fp32, or as row `brow` of fragment-order fp16 hi/lo planes
-// (hi + lo ~= value, the input format of the panel MFMA GEMM) when hi is not
-// null.
+// written as fp32, or as row `brow` of range-safe fragment-order fp16 hi/lo
+// planes (the input format of the panel MFMA GEMM, see Planes) when xp.hi is
+// not null: a first pass takes each group's largest |value|, a second writes
+// the planes.
 __device__ __forceinline__ void rmsnorm_row(const float *x, const float *__restrict__ w, float *out, int n,
-                                            float eps, float *red, _Float16 *hi = nullptr, _Float16 *lo = nullptr,
-                                            int brow = 0) {
+                                            float eps, float *red, Planes xp = Planes{}, int brow = 0) {
+    __shared__ int gmax[kMaxGroups];
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kThreads) ss += x[i] * x[i];
-    ss = block_sum(ss, red);
+    if (xp.hi)
+        for (int g = threadIdx.x; g < (n + kXeGroup - 1) / kXeGroup; g += kThreads) gmax[g] = 0;
+    ss = block_sum(ss, red);  // its barriers also order the gmax clearing
     const float inv_rms = 1.0f / sqrtf(ss / (float)n + eps);
+    if (!xp.hi) {
+        for (int i = threadIdx.x; i < n; i += kThreads) out[i] = (x[i] * inv_rms) * w[i];
+        return;
+    }
+    for (int i = threadIdx.x; i < n; i += kThreads)
+        atomicMax(&gmax[i / kXeGroup], __float_as_int(fabsf((x[i] * inv_rms) * w[i])));
+    __syncthreads();
     for (int i = threadIdx.x; i < n; i += kThreads) {
         const float v = (x[i] * inv_rms) * w[i];
-        if (hi) {
-            const _Float16 h = (_Float16)v;
-            hi[xf_index(brow, i)] = h;
-            lo[xf_index(brow, i)] = (_Float16)(v - (float)h);
-        } else {
-            out[i] = v;
-        }
+        const int e = group_exp(__int_as_float(gmax[i / kXeGroup]));
+        split_scaled(v, e, xp.hi[xf_index(brow, i)], xp.lo[xf_index(brow, i)]);
+        if (i % kXeGroup == 0) xp.xe[xe_index(brow, i, n)] = (int8_t)e;
     }
 }
 
@@ -69,14 +79,14 @@ __global__ __launch_bounds__(kThreads) void embed_rmsnorm_kernel(const uint32_t 
                                                                  const float *__restrict__ emb, uint32_t vocab,
                                                                  float *__restrict__ x, const float *__restrict__ w,
                                                                  float *__restrict__ xn, int n, float eps,
-                                                                 _Float16 *__restrict__ hi, _Float16 *__restrict__ lo) {
+                                                                 Planes xp) {
     __shared__ float red[4];
     const size_t b = blockIdx.x;
     const uint32_t tok = tokens[b];
     float *xb = x + b * n;
     for (int i = threadIdx.x; i < n; i += kThreads) xb[i] = tok < vocab ? emb[(size_t)tok * n + i] : 0.0f;
     __syncthreads();
-    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi, lo, (int)b);
+    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, xp, (int)b);
 }
 
 // x[b] += sum_k part[k][b]; if w: xn[b] = rmsnorm(x[b], w).   part stride between
@@ -85,8 +95,7 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(float *__res
                                                                     const float *__restrict__ part, int ksplit,
                                                                     int rows, const float *__restrict__ w,
                                                                     float *__restrict__ xn, int n, float eps,
-                                                                    _Float16 *__restrict__ hi,
-                                                                    _Float16 *__restrict__ lo) {
+                                                                    Planes xp) {
     __shared__ float red[4];
     const size_t b = blockIdx.x;
     float *xb = x + b * n;
@@ -98,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(float *__res
     }
     if (!w) return;
     __syncthreads();
-    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, hi, lo, (int)b);
+    rmsnorm_row(xb, w, xn ? xn + b * n : nullptr, n, eps, red, xp, (int)b);
 }
 
 // The same for rows of n <= 2048 (n % 4 == 0) with one workgroup of 512
@@ -108,8 +117,7 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(float *__res
 template <int KP>
 __global__ __launch_bounds__(512) void residual_rmsnorm_v4(float *__restrict__ x, const float *__restrict__ part,
                                                            int ksplit, int rows, const float *__restrict__ w,
-                                                           float *__restrict__ xn, int n, float eps,
-                                                           _Float16 *__restrict__ hi, _Float16 *__restrict__ lo) {
+                                                           float *__restrict__ xn, int n, float eps, Planes xp) {
     __shared__ float red[8];
     const int t = threadIdx.x;
     const size_t b = blockIdx.x;
@@ -138,22 +146,32 @@ __global__ __launch_bounds__(512) void residual_rmsnorm_v4(float *__restrict__ x
     float ss = mine ? r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w : 0.0f;
     ss = wave_sum(ss);
     if ((t & 63) == 0) red[t >> 6] = ss;
+    // planes: the largest |r * w| of each 128-column group (32 consecutive
+    // threads of one wave, all inside the row or all outside: n % 128 == 0),
+    // taken while the sum of squares crosses the barrier; times inv_rms it
+    // gives the group's binade (to a few ulps)
+    const float gmax = xp.hi ? half_max32(mine ? fmaxf(fmaxf(fabsf(r.x * wv.x), fabsf(r.y * wv.y)),
+                                                      fmaxf(fabsf(r.z * wv.z), fabsf(r.w * wv.w)))
+                                               : 0.0f)
+                             : 0.0f;
     __syncthreads();
     float tot = red[0];
 #pragma unroll
     for (int i = 1; i < 8; i++) tot += red[i];
     const float inv_rms = 1.0f / sqrtf(tot / (float)n + eps);
-    if (!mine) return;
     const float v[4] = {(r.x * inv_rms) * wv.x, (r.y * inv_rms) * wv.y, (r.z * inv_rms) * wv.z,
                         (r.w * inv_rms) * wv.w};
-    if (hi) {
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const _Float16 h = (_Float16)v[c];
-            hi[xf_index((int)b, 4 * t + c)] = h;
-            lo[xf_index((int)b, 4 * t + c)] = (_Float16)(v[c] - (float)h);
-        }
-    } else if (xn) {
+    if (xp.hi) {
+        if (!mine) return;
+        const int e = group_exp(gmax * inv_rms);
+        // columns 4t .. 4t + 3 are consecutive in a fragment-order plane
+        h4v vh, vl;
+        split4_scaled(v, e, vh, vl);
+        const size_t o = xf_index((int)b, 4 * t);
+        *reinterpret_cast<h4v *>(xp.hi + o) = vh;
+        *reinterpret_cast<h4v *>(xp.lo + o) = vl;
+        if ((t & 31) == 0) xp.xe[xe_index((int)b, 4 * t, n)] = (int8_t)e;
+    } else if (mine && xn) {
         reinterpret_cast<float4 *>(xn)[b * n4 + t] = make_float4(v[0], v[1], v[2], v[3]);
     }
 }
@@ -161,23 +179,32 @@ __global__ __launch_bounds__(512) void residual_rmsnorm_v4(float *__restrict__ x
 // Stacked [gate; up] GEMV output gu[k][b][2F]: h[b][r] = SiLU(gate) * up
 // (scratch.rs:181-186: a = (a / (1 + exp(-a))) * b).
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restrict__ gu, int ksplit, int rows,
-                                                            float *__restrict__ h, int F, _Float16 *__restrict__ hi,
-                                                            _Float16 *__restrict__ lo) {
+                                                            float *__restrict__ h, int F, Planes xp) {
+    __shared__ float wm[kThreads / 64];
     const size_t b = blockIdx.y;
     const int r = blockIdx.x * kThreads + threadIdx.x;
-    if (r >= F) return;
+    const bool in = r < F;
+    const int rr = in ? r : F - 1;
     const size_t split = (size_t)rows * 2 * F;
-    float g = gu[b * 2 * F + r], u = gu[b * 2 * F + F + r];
+    float g = gu[b * 2 * F + rr], u = gu[b * 2 * F + F + rr];
     for (int k = 1; k < ksplit; k++) {
-        g += gu[k * split + b * 2 * F + r];
-        u += gu[k * split + b * 2 * F + F + r];
+        g += gu[k * split + b * 2 * F + rr];
+        u += gu[k * split + b * 2 * F + F + rr];
     }
     const float v = (g / (1.0f + expf(-g))) * u;
-    if (hi) {
-        const _Float16 hh = (_Float16)v;
-        hi[xf_index((int)b, r)] = hh;
-        lo[xf_index((int)b, r)] = (_Float16)(v - (float)hh);
-    } else {
+    if (xp.hi) {
+        // a 128-column group is two waves of this workgroup
+        float amax = in ? fabsf(v) : 0.0f;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = amax;
+        __syncthreads();
+        const int w0 = (threadIdx.x >> 6) & ~1;
+        const int e = group_exp(fmaxf(wm[w0], wm[w0 + 1]));
+        if (!in) return;
+        split_scaled(v, e, xp.hi[xf_index((int)b, r)], xp.lo[xf_index((int)b, r)]);
+        if (r % kXeGroup == 0) xp.xe[xe_index((int)b, r, F)] = (int8_t)e;
+    } else if (in) {
         h[b * F + r] = v;
     }
 }
@@ -187,13 +214,13 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restr
 // the last one and are not added), so the row costs one memory round trip.
 template <int KP>
 __global__ __launch_bounds__(kThreads) void silu_mul_v4(const float *__restrict__ gu, int ksplit, int rows,
-                                                        float *__restrict__ h, int F, _Float16 *__restrict__ hi,
-                                                        _Float16 *__restrict__ lo) {
+                                                        float *__restrict__ h, int F, Planes xp) {
     const int b = blockIdx.y;
     const int r = 4 * (blockIdx.x * kThreads + threadIdx.x);
-    if (r >= F) return;
+    const bool in = r < F;
+    if (!xp.hi && !in) return;
     const size_t split = (size_t)rows * 2 * F;
-    const float *g0 = gu + (size_t)b * 2 * F + r;
+    const float *g0 = gu + (size_t)b * 2 * F + (in ? r : F - 4);
     float4 gv[KP], uv[KP];
 #pragma unroll
     for (int k = 0; k < KP; k++) {
@@ -215,18 +242,20 @@ __global__ __launch_bounds__(kThreads) void silu_mul_v4(const float *__restrict_
     float v[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) v[c] = (g[c] / (1.0f + expf(-g[c]))) * u[c];
-    if (hi) {
+    if (xp.hi) {
+        // a 128-column group is 32 consecutive threads of one wave (all of
+        // them inside the row or all outside: F % 128 == 0 for planes)
+        const float amax =
+            half_max32(in ? fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) : 0.0f);
+        if (!in) return;
+        const int e = group_exp(amax);
         // columns r .. r + 3 (r % 4 == 0) are consecutive in a fragment-order plane
-        typedef _Float16 h4v __attribute__((ext_vector_type(4)));
         h4v vh, vl;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            vh[c] = (_Float16)v[c];
-            vl[c] = (_Float16)(v[c] - (float)vh[c]);
-        }
+        split4_scaled(v, e, vh, vl);
         const size_t o = xf_index(b, r);
-        *reinterpret_cast<h4v *>(hi + o) = vh;
-        *reinterpret_cast<h4v *>(lo + o) = vl;
+        *reinterpret_cast<h4v *>(xp.hi + o) = vh;
+        *reinterpret_cast<h4v *>(xp.lo + o) = vl;
+        if ((threadIdx.x & 31) == 0) xp.xe[xe_index(b, r, F)] = (int8_t)e;
     } else {
         *reinterpret_cast<float4 *>(h + (size_t)b * F + r) = make_float4(v[0], v[1], v[2], v[3]);
     }
@@ -339,47 +368,57 @@ int launch_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const float 
     return ANEHIP_OK;
 }
 
+static int check_planes(anehip_ctx *ctx, const Planes &xp, int n) {
+    if (xp.hi && (!xp.lo || !xp.xe || n % kXeGroup || n > kMaxGroups * kXeGroup))
+        return set_error(ctx->err, ANEHIP_EINVAL, "planes: incomplete, or n=%d not a multiple of %d up to %d", n,
+                         kXeGroup, kMaxGroups * kXeGroup);
+    return ANEHIP_OK;
+}
+
 int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const uint32_t *tokens, const float *emb,
-                         uint32_t vocab, float *x, const float *w, float *xn, float eps, _Float16 *hi, _Float16 *lo) {
+                         uint32_t vocab, float *x, const float *w, float *xn, float eps, const Planes &xp) {
+    if (int rc = check_planes(ctx, xp, n)) return rc;
     hipLaunchKernelGGL(embed_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, tokens, emb, vocab, x, w, xn, n, eps,
-                       hi, lo);
+                       xp);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 
 int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
-                            int ksplit, const float *w, float *xn, float eps, _Float16 *hi, _Float16 *lo) {
+                            int ksplit, const float *w, float *xn, float eps, const Planes &xp) {
+    if (int rc = check_planes(ctx, xp, n)) return rc;
     if (n % 4 == 0 && n <= 2048 && ksplit >= 1 && ksplit <= 16) {
         if (ksplit <= 2)
             hipLaunchKernelGGL(residual_rmsnorm_v4<2>, dim3(rows), dim3(512), 0, s, x, part, ksplit, rows, w, xn, n,
-                               eps, hi, lo);
+                               eps, xp);
         else if (ksplit <= 8)
             hipLaunchKernelGGL(residual_rmsnorm_v4<8>, dim3(rows), dim3(512), 0, s, x, part, ksplit, rows, w, xn, n,
-                               eps, hi, lo);
+                               eps, xp);
         else
             hipLaunchKernelGGL(residual_rmsnorm_v4<16>, dim3(rows), dim3(512), 0, s, x, part, ksplit, rows, w, xn, n,
-                               eps, hi, lo);
+                               eps, xp);
     } else {
         hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, part, ksplit, rows, w, xn,
-                           n, eps, hi, lo);
+                           n, eps, xp);
     }
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 
 int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit, float *h,
-                            _Float16 *hi, _Float16 *lo) {
+                            const Planes &xp) {
+    if (int rc = check_planes(ctx, xp, F)) return rc;
     if (F % 4 == 0 && ksplit >= 1 && ksplit <= 16) {
         const dim3 grid((F / 4 + kThreads - 1) / kThreads, rows);
         if (ksplit == 1)
-            hipLaunchKernelGGL(silu_mul_v4<1>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, hi, lo);
+            hipLaunchKernelGGL(silu_mul_v4<1>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, xp);
         else if (ksplit <= 4)
-            hipLaunchKernelGGL(silu_mul_v4<4>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, hi, lo);
+            hipLaunchKernelGGL(silu_mul_v4<4>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, xp);
         else
-            hipLaunchKernelGGL(silu_mul_v4<16>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, hi, lo);
+            hipLaunchKernelGGL(silu_mul_v4<16>, grid, dim3(kThreads), 0, s, gu, ksplit, rows, h, F, xp);
     } else {
         hipLaunchKernelGGL(silu_mul_kernel, dim3((F + kThreads - 1) / kThreads, rows), dim3(kThreads), 0, s, gu,
-                           ksplit, rows, h, F, hi, lo);
+                           ksplit, rows, h, F, xp);
     }
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;

@@ -838,6 +838,59 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
 // ---------------------------------------------------------------------------
 
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+
+// Range-safe planes on the GEMM side (see Planes): the largest exponent of
+// groups [g0, g0 + ng) of batch row b.
+__device__ __forceinline__ int xe_max(const int8_t *__restrict__ xe, int b, int g0, int ng, int n) {
+    int E = kXeEmpty;
+    const int8_t *p = xe + (size_t)b * xe_stride(n) + g0;
+    for (int g = 0; g < ng; g++) E = max(E, (int)p[g]);
+    return E;
+}
+
+// fp32 sums of x * 2^-E back to x's scale.
+__device__ __forceinline__ float4 ldexp4(float4 v, int E) {
+    return make_float4(ldexpf(v.x, E), ldexpf(v.y, E), ldexpf(v.z, E), ldexpf(v.w, E));
+}
+// The same as one multiply by 2^E: exact for every exponent group_exp gives
+// (2^E is an fp32 value for E >= -149).
+__device__ __forceinline__ float xe_scale(int E) { return ldexpf(1.0f, E); }
+__device__ __forceinline__ float4 mul4(float4 v, float f) { return make_float4(v.x * f, v.y * f, v.z * f, v.w * f); }
+// The exponent of batch row first + (threadIdx / 16) % 4, read from lanes
+// first .. first + 3 (which hold rows first .. first + 3; first uniform):
+// readlane, no LDS -- an LDS permute here measured slower.
+__device__ __forceinline__ int row_exp4(int E, int first) {
+    const int e0 = __builtin_amdgcn_readlane(E, first), e1 = __builtin_amdgcn_readlane(E, first + 1);
+    const int e2 = __builtin_amdgcn_readlane(E, first + 2), e3 = __builtin_amdgcn_readlane(E, first + 3);
+    const int k = (threadIdx.x >> 4) & 3;
+    return k == 0 ? e0 : k == 1 ? e1 : k == 2 ? e2 : e3;
+}
+
+// The fp32-rows path of the x-stationary kernels: 8 consecutive columns of a
+// row, and their hi / lo fragments for x * 2^-E.
+__device__ __forceinline__ void load8(const float *p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+__device__ __forceinline__ float amax8(const float *p, float m) {
+    float v[8];
+    load8(p, v);
+#pragma unroll
+    for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
+    return m;
+}
+__device__ __forceinline__ void split8_scaled(const float *p, int E, h8v &hi, h8v &lo) {
+    float v[8];
+    load8(p, v);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        _Float16 h, l;
+        split_scaled(v[i], E, h, l);
+        hi[i] = h;
+        lo[i] = l;
+    }
+}
+
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -915,6 +968,7 @@ template <uint32_t T, int TV> struct GemmUnit {
     u32x4 q[TV][kQ];
     u32x4 sc[TV];
     h8v ah[4], al[4];
+    int xe;  // exponent of the fragments' column group (range-safe planes)
 };
 
 // Loads one unit: every lane issues the same, fully contiguous 1 KiB loads
@@ -926,7 +980,7 @@ template <uint32_t T, int TV> struct GemmUnit {
 template <uint32_t T, int TV>
 __device__ __forceinline__ void gemm_load(GemmUnit<T, TV> &u, const uint8_t *panel, size_t tile_bytes,
                                           const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl, size_t xo,
-                                          int quarter, int lane) {
+                                          const int8_t *__restrict__ xe, int quarter, int lane) {
     constexpr int Q = GemmUnit<T, TV>::kQ;
 #pragma unroll
     for (int t = 0; t < TV; t++) {
@@ -940,6 +994,7 @@ __device__ __forceinline__ void gemm_load(GemmUnit<T, TV> &u, const uint8_t *pan
         u.ah[s] = *reinterpret_cast<const h8v *>(xh + xo + 512 * s);
         u.al[s] = *reinterpret_cast<const h8v *>(xl + xo + 512 * s);
     }
+    u.xe = *xe;
 }
 
 // acc{0,1} += one tile's two blocks of a quarter: q = its quant vectors, sc
@@ -1017,9 +1072,10 @@ constexpr int kBadOffset = 0x7ffffff0;  // buffer offset past any output: the st
 constexpr int kCpolDevice = 16;
 
 template <int CPOL = 0>
-__device__ __forceinline__ void gemm_tile_epilogue(float (*red)[32][kWave], const f32x16 &acc0, const f32x16 &acc1,
-                                                   int quarter, int lane, int tile, int ks, int batch, int m,
-                                                   size_t split_stride, __amdgpu_buffer_rsrc_t orsrc, bool store) {
+__device__ __forceinline__ void gemm_tile_epilogue(float (*red)[32][kWave], const float (&fEb)[2], const f32x16 &acc0,
+                                                   const f32x16 &acc1, int quarter, int lane, int tile, int ks,
+                                                   int batch, int m, size_t split_stride,
+                                                   __amdgpu_buffer_rsrc_t orsrc, bool store) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         red[quarter][r][lane] = acc0[r];
@@ -1039,6 +1095,7 @@ __device__ __forceinline__ void gemm_tile_epilogue(float (*red)[32][kWave], cons
             const float4 o = *reinterpret_cast<const float4 *>(&red[w][r][l]);
             sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
         }
+        sum = mul4(sum, fEb[i]);  // the fragments' exponent of batch row b
         const int row = tile * kWave + 4 * j;
         const int off = store && b < batch && row < m ? 4 * (ks * (int)split_stride + b * m + row) : kBadOffset;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0, CPOL);
@@ -1060,15 +1117,24 @@ __device__ __forceinline__ void gemm_tile_epilogue(float (*red)[32][kWave], cons
 // 16-byte row vectors (m % 4 == 0).
 template <uint32_t T, int TV, int D, int WPE = (TV == 1 ? 2 : 1)>
 __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_packed(
-    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-    float *__restrict__ out, int m, int n, int batch, int ksplit, int per, size_t split_stride) {
+    const uint8_t *__restrict__ Wp, Planes xp, float *__restrict__ out, int m, int n, int batch, int ksplit, int per,
+    size_t split_stride) {
     __shared__ __align__(16) float red[kGemmWaves][TV * 32][kWave];
+    __shared__ int xeE[32];
+    const _Float16 *__restrict__ xh = xp.hi;
+    const _Float16 *__restrict__ xl = xp.lo;
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave, groups = (tiles + TV - 1) / TV;
     const int items = groups * ksplit, G = gridDim.x;
     if ((int)blockIdx.x >= items) return;
     const int lane = threadIdx.x & (kWave - 1);
     const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const size_t xbase = (size_t)(4 * quarter * kWave + min(lane & 31, batch - 1) + 32 * (lane >> 5)) * 8;
+    const int brow = min(lane & 31, batch - 1);
+    const size_t xbase = (size_t)(4 * quarter * kWave + brow + 32 * (lane >> 5)) * 8;
+    // range-safe planes: every unit's fragments are brought to one exponent
+    // per batch row over the whole row (units are loaded across items)
+    const int E = xe_max(xp.xe, brow, 0, 2 * nsb, n);
+    if (quarter == 0 && lane < 32) xeE[lane] = E;  // read after the first epilogue barrier
+    const int8_t *xe_lane = xp.xe + (size_t)brow * xe_stride(n) + (quarter >> 1);  // + 2 per panel
     const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
     const __amdgpu_buffer_rsrc_t orsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
@@ -1083,7 +1149,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
     size_t lxo = xbase + 16 * 512 * (size_t)lp;
     // the load cursor steps to the next unit; every step issues its loads
     auto load_next = [&](GemmUnit<T, TV> &u) {
-        gemm_load<T, TV>(u, lpanel, tile_bytes, xh, xl, lxo, quarter, lane);
+        gemm_load<T, TV>(u, lpanel, tile_bytes, xh, xl, lxo, xe_lane + 2 * lp, quarter, lane);
         // branch-free cursor step (selects keep the loop body one basic block)
         const bool wrap = ++lp == le;
         const int ni = li + G;
@@ -1104,6 +1170,12 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
     // items) a step is harmless: its loads are valid and its stores fall
     // outside the output range and are dropped.
     auto step = [&](GemmUnit<T, TV> &u) {
+        const _Float16 f = xe_factor(u.xe, E);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            u.ah[s] = u.ah[s] * f;
+            u.al[s] = u.al[s] * f;
+        }
         gemm_mma<T, TV>(u, quarter, acc);
         // the refill reuses u's registers only if it is issued after u's last
         // use (the scale FMAs); otherwise the loop carries register copies
@@ -1140,6 +1212,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
                     const float4 o = *reinterpret_cast<const float4 *>(&red[w][r][l]);
                     sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
                 }
+                sum = ldexp4(sum, xeE[b]);
                 // the group's tile t is tile ft + t of the loads; it is stored
                 // only if it is the item's own tile (not a clamped re-read)
                 const int tile = ft + t, row = tile * kWave + 4 * j;
@@ -1258,54 +1331,79 @@ __device__ __forceinline__ void mma_tile16(const u32x4 *q, uint32_t sw, const h8
 // indices; a tile's sums are added over the quarters through LDS.  Loads
 // past the last tile are clamped to it and their results stored nowhere.
 // Output: out[ks * split_stride + b * m + row] (device-scope stores).
-template <uint32_t T, int P, int D, int WPE>
+template <uint32_t T, int P, int D, int WPE, bool XROWS = false>
 __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_xs16(
-    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-    const float *__restrict__ xrows, float *__restrict__ out, int m, int n, int batch, int ksplit,
-    size_t split_stride) {
+    const uint8_t *__restrict__ Wp, Planes xp, const float *__restrict__ xrows, float *__restrict__ out, int m, int n,
+    int batch, int ksplit, size_t split_stride) {
     constexpr int Q = GemmUnit16<T>::kQ;
     constexpr int U = P > D ? P : D;
     static_assert(U % P == 0 && U % D == 0, "ring and panel counts must divide the loop body");
     __shared__ __align__(16) float red[kGemmWaves][16][kWave];
+    __shared__ float wmax[kGemmWaves][16];
+    __shared__ int emax[kGemmWaves][16];
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
     const int gs = gridDim.x / ksplit;  // workgroups per split
     const int ks = blockIdx.x % ksplit, g0 = blockIdx.x / ksplit;
     if (g0 >= gs || g0 >= tiles) return;
     const int lane = threadIdx.x & (kWave - 1), grp = lane >> 4;
+    // the weight base in SGPRs now: the weight ring's first loads must not
+    // wait for a kernel-argument load issued after the x loads
+    asm volatile("" ::"s"(Wp));
     const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
     const __amdgpu_buffer_rsrc_t orsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
     // A fragments: batch row lane % 16 (clamped to the batch), columns
-    // 64 quarter + 32 j + 8 (lane / 16) of each panel of the split
+    // 64 quarter + 32 j + 8 (lane / 16) of each panel of the split, brought
+    // to x * 2^-E with one exponent E per batch row for the whole split.
+    // From the planes the x loads go out first, then the weight ring's, and
+    // the fragments are scaled after both were issued: the scaling waits for
+    // the x loads only.
     h8v xa[P][2], xb[P][2];
     const int brow = min(lane & 15, batch - 1);
-    if (xrows == nullptr) {
+    const float *xr = XROWS ? xrows + (size_t)brow * n : nullptr;
+    auto xcol = [&](int p, int j) { return 256 * (ks * P + p) + 64 * quarter + 32 * j + 8 * grp; };
+    int xe_own[P];  // exponents of this quarter's group of each panel
+    // small splits load every group's exponent (no exchange between waves)
+    constexpr int NG = 2 * P;
+    constexpr bool kDirect = NG <= 8;
+    int xe_all[kDirect ? NG : 1];
+    int E = 0;
+    if constexpr (!XROWS) {
         const size_t xbase = (size_t)((4 * quarter + (grp >> 1)) * kWave + brow + 32 * (grp & 1)) * 8 +
                              16 * 512 * (size_t)(ks * P);
+        if constexpr (kDirect) {
 #pragma unroll
-        for (int p = 0; p < P; p++)
+            for (int g = 0; g < NG; g++) xe_all[g] = xp.xe[(size_t)brow * xe_stride(n) + 2 * ks * P + g];
+        }
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            if constexpr (kDirect) xe_own[p] = (quarter >> 1) ? xe_all[2 * p + 1] : xe_all[2 * p];
+            else xe_own[p] = xp.xe[(size_t)brow * xe_stride(n) + 2 * (ks * P + p) + (quarter >> 1)];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                xa[p][j] = *reinterpret_cast<const h8v *>(xh + xbase + 16 * 512 * p + 1024 * j);
-                xb[p][j] = *reinterpret_cast<const h8v *>(xl + xbase + 16 * 512 * p + 1024 * j);
+                xa[p][j] = *reinterpret_cast<const h8v *>(xp.hi + xbase + 16 * 512 * p + 1024 * j);
+                xb[p][j] = *reinterpret_cast<const h8v *>(xp.lo + xbase + 16 * 512 * p + 1024 * j);
             }
+        }
     } else {
-        const float *xr = xrows + (size_t)brow * n;
+        // fp32 rows (API path; split before the ring is issued, the register
+        // file holds no room for both): E from the row's largest |x| over the
+        // split -- lanes l, l + 16, l + 32, l + 48 and the 4 waves hold a row
+        float amax = 0.0f;
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int c0 = 256 * (ks * P + p) + 64 * quarter + 32 * j + 8 * grp;
-                const float4 a = *reinterpret_cast<const float4 *>(xr + c0);
-                const float4 b = *reinterpret_cast<const float4 *>(xr + c0 + 4);
-                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            for (int j = 0; j < 2; j++) amax = amax8(xr + xcol(p, j), amax);
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        if (lane < 16) wmax[quarter][lane] = amax;
+        lds_barrier();
+        E = group_exp(fmaxf(fmaxf(wmax[0][lane & 15], wmax[1][lane & 15]), fmaxf(wmax[2][lane & 15], wmax[3][lane & 15])));
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    xa[p][j][i] = (_Float16)v[i];
-                    xb[p][j][i] = (_Float16)(v[i] - (float)xa[p][j][i]);
-                }
-            }
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) split8_scaled(xr + xcol(p, j), E, xa[p][j], xb[p][j]);
     }
     const uint8_t *wsplit = Wp + (size_t)(ks * P) * Panel<T>::kBytes;
     int lt = g0, lp = 0;  // load cursor: tile, panel within the split
@@ -1327,6 +1425,36 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
         load_next(ring[k]);
         asm volatile("" ::: "memory");
     }
+    if constexpr (!XROWS) {
+        // planes: E over the split -- from all of its exponents, or each
+        // wave's groups and then the 4 waves through LDS (quarters 0, 1 hold
+        // a panel's first group, 2, 3 its second); the scaling waits for the
+        // x loads only
+        if constexpr (kDirect) {
+            E = kXeEmpty;
+#pragma unroll
+            for (int g = 0; g < NG; g++) E = max(E, xe_all[g]);
+        } else {
+            int e = kXeEmpty;
+#pragma unroll
+            for (int p = 0; p < P; p++) e = max(e, xe_own[p]);
+            if (lane < 16) emax[quarter][lane] = e;
+            lds_barrier();
+            E = max(max(emax[0][lane & 15], emax[1][lane & 15]), max(emax[2][lane & 15], emax[3][lane & 15]));
+        }
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const _Float16 f = xe_factor(xe_own[p], E);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                xa[p][j] = xa[p][j] * f;
+                xb[p][j] = xb[p][j] * f;
+            }
+        }
+    }
+    // the epilogue's batch row (threadIdx / 16) takes its exponent from the
+    // lane holding that row
+    const float fEb = xe_scale(row_exp4(E, 4 * quarter));
     int ct = g0;  // tile being multiplied
     f32x4 acc[4];
 #pragma unroll
@@ -1360,6 +1488,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
                         const float4 o = *reinterpret_cast<const float4 *>(&red[w][reg][l]);
                         sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
                     }
+                    sum = mul4(sum, fEb);
                     const int row = ct * kWave + 4 * j;
                     const int off = b < batch && row < m && ct < tiles ? 4 * (ks * (int)split_stride + b * m + row)
                                                                        : kBadOffset;
@@ -1391,50 +1520,71 @@ template <uint32_t T> struct WUnit {
 
 template <uint32_t T, int P, int R, bool XROWS = false>
 __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(2))) void gemm_xs(
-    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-    const float *__restrict__ xrows, float *__restrict__ out, int m, int n, int batch, int ksplit,
-    size_t split_stride) {
+    const uint8_t *__restrict__ Wp, Planes xp, const float *__restrict__ xrows, float *__restrict__ out, int m, int n,
+    int batch, int ksplit, size_t split_stride) {
     constexpr int Q = GemmUnit<T, 1>::kQ;
     __shared__ __align__(16) float red[kGemmWaves][32][kWave];
+    __shared__ float wmax[kGemmWaves][32];
+    __shared__ int emax[kGemmWaves][32];
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
     const int gs = gridDim.x / ksplit;  // workgroups per split
     const int ks = blockIdx.x % ksplit, g0 = blockIdx.x / ksplit;
     if (g0 >= gs || g0 >= tiles) return;
     const int lane = threadIdx.x & (kWave - 1);
+    // the weight base in SGPRs now: the weight ring's first loads must not
+    // wait for a kernel-argument load issued after the x loads
+    asm volatile("" ::"s"(Wp));
     const int quarter = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
     const __amdgpu_buffer_rsrc_t orsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
     // this quarter's x fragments of the split's panels: lane l holds batch row
     // l % 32 (rows past the batch repeat the last), 8 consecutive columns;
-    // from the fragment-order planes, or (XROWS) split from fp32 rows x[b][n]
+    // from the fragment-order planes, or (XROWS) split from fp32 rows x[b][n];
+    // brought to x * 2^-E with one exponent E per batch row for the whole
+    // split; from the planes after the weight ring's loads were issued (as in
+    // gemm_xs16)
     h8v xa[P][4], xb[P][4];
     const int brow = min(lane & 31, batch - 1);
+    const float *xr = XROWS ? xrows + (size_t)brow * n : nullptr;
+    auto xcol = [&](int p, int st) { return 16 * (16 * (ks * P + p) + 4 * quarter + st) + 8 * (lane >> 5); };
+    int xe_own[P];
+    constexpr int NG = 2 * P;
+    constexpr bool kDirect = NG <= 8;  // as in gemm_xs16
+    int xe_all[kDirect ? NG : 1];
+    int E = 0;
     if constexpr (!XROWS) {
         const size_t xbase = (size_t)(4 * quarter * kWave + brow + 32 * (lane >> 5)) * 8 + 16 * 512 * (size_t)(ks * P);
+        if constexpr (kDirect) {
 #pragma unroll
-        for (int p = 0; p < P; p++)
+            for (int g = 0; g < NG; g++) xe_all[g] = xp.xe[(size_t)brow * xe_stride(n) + 2 * ks * P + g];
+        }
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            if constexpr (kDirect) xe_own[p] = (quarter >> 1) ? xe_all[2 * p + 1] : xe_all[2 * p];
+            else xe_own[p] = xp.xe[(size_t)brow * xe_stride(n) + 2 * (ks * P + p) + (quarter >> 1)];
 #pragma unroll
             for (int st = 0; st < 4; st++) {
-                xa[p][st] = *reinterpret_cast<const h8v *>(xh + xbase + 16 * 512 * p + 512 * st);
-                xb[p][st] = *reinterpret_cast<const h8v *>(xl + xbase + 16 * 512 * p + 512 * st);
+                xa[p][st] = *reinterpret_cast<const h8v *>(xp.hi + xbase + 16 * 512 * p + 512 * st);
+                xb[p][st] = *reinterpret_cast<const h8v *>(xp.lo + xbase + 16 * 512 * p + 512 * st);
             }
+        }
     } else {
-        const float *xr = xrows + (size_t)brow * n;
+        // fp32 rows, split before the ring: lanes l, l + 32 and the 4 waves
+        // hold a row's columns
+        float amax = 0.0f;
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const int c0 = 16 * (16 * (ks * P + p) + 4 * quarter + st) + 8 * (lane >> 5);
-                const float4 a = *reinterpret_cast<const float4 *>(xr + c0);
-                const float4 b = *reinterpret_cast<const float4 *>(xr + c0 + 4);
-                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            for (int st = 0; st < 4; st++) amax = amax8(xr + xcol(p, st), amax);
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        if (lane < 32) wmax[quarter][lane] = amax;
+        lds_barrier();
+        E = group_exp(fmaxf(fmaxf(wmax[0][lane & 31], wmax[1][lane & 31]), fmaxf(wmax[2][lane & 31], wmax[3][lane & 31])));
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    xa[p][st][i] = (_Float16)v[i];
-                    xb[p][st][i] = (_Float16)(v[i] - (float)xa[p][st][i]);
-                }
-            }
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) split8_scaled(xr + xcol(p, st), E, xa[p][st], xb[p][st]);
     }
     const uint8_t *wsplit = Wp + (size_t)(ks * P) * Panel<T>::kBytes;
     int lt = g0;  // next tile to load
@@ -1460,6 +1610,32 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
         load_tile(ring[r]);
         asm volatile("" ::: "memory");
     }
+    if constexpr (!XROWS) {
+        if constexpr (kDirect) {
+            E = kXeEmpty;
+#pragma unroll
+            for (int g = 0; g < NG; g++) E = max(E, xe_all[g]);
+        } else {
+            int e = kXeEmpty;
+#pragma unroll
+            for (int p = 0; p < P; p++) e = max(e, xe_own[p]);
+            if (lane < 32) emax[quarter][lane] = e;
+            lds_barrier();
+            E = max(max(emax[0][lane & 31], emax[1][lane & 31]), max(emax[2][lane & 31], emax[3][lane & 31]));
+        }
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const _Float16 f = xe_factor(xe_own[p], E);
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                xa[p][st] = xa[p][st] * f;
+                xb[p][st] = xb[p][st] * f;
+            }
+        }
+    }
+    // the epilogue's batch rows (threadIdx / 16, + 16) take their exponent
+    // from the lanes holding those rows
+    const float fEb[2] = {xe_scale(row_exp4(E, 4 * quarter)), xe_scale(row_exp4(E, 16 + 4 * quarter))};
     int ct = g0;  // tile being multiplied
     auto step = [&](WUnit<T> (&u)[P]) {
 #pragma unroll
@@ -1473,7 +1649,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
         for (int p = 0; p < P; p++) mma_tile<T>(u[p].q, u[p].sc, xa[p], xb[p], acc0, acc1);
         asm volatile("" : "+v"(acc0), "+v"(acc1)::"memory");
         load_tile(u);
-        gemm_tile_epilogue<kCpolDevice>(red, acc0, acc1, quarter, lane, ct, ks, batch, m, split_stride, orsrc,
+        gemm_tile_epilogue<kCpolDevice>(red, fEb, acc0, acc1, quarter, lane, ct, ks, batch, m, split_stride, orsrc,
                                         ct < tiles);
         ct += gs;
     };
@@ -1490,53 +1666,76 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
 // 4 H waves through LDS.  With H = 2 the split's x fragments (up to 8 panels)
 // fit in registers at two waves per SIMD, so lm_head needs no K split and no
 // x loads in its main loop.  Output as gemm_xs.
-template <uint32_t T, int PW, int D, int H>
+template <uint32_t T, int PW, int D, int H, bool XROWS = false>
 __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_per_eu(2))) void gemm_xsh(
-    const uint8_t *__restrict__ Wp, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-    const float *__restrict__ xrows, float *__restrict__ out, int m, int n, int batch, int ksplit,
-    size_t split_stride) {
+    const uint8_t *__restrict__ Wp, Planes xp, const float *__restrict__ xrows, float *__restrict__ out, int m, int n,
+    int batch, int ksplit, size_t split_stride) {
     constexpr int Q = GemmUnit<T, 1>::kQ;
     constexpr int U = PW > D ? PW : D;
     constexpr int NW = kGemmWaves * H;
     static_assert(U % PW == 0 && U % D == 0, "ring and panel counts must divide the loop body");
     __shared__ __align__(16) float red[NW][32][kWave];
+    __shared__ float wmax[NW][32];
+    __shared__ int emax[NW][32];
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
     const int gs = gridDim.x / ksplit;  // workgroups per split
     const int ks = blockIdx.x % ksplit, g0 = blockIdx.x / ksplit;
     if (g0 >= gs || g0 >= tiles) return;
     const int lane = threadIdx.x & (kWave - 1);
+    // the weight base in SGPRs now: the weight ring's first loads must not
+    // wait for a kernel-argument load issued after the x loads
+    asm volatile("" ::"s"(Wp));
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int quarter = wave & 3, panel0 = (ks * H + (wave >> 2)) * PW;
     const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
     const __amdgpu_buffer_rsrc_t orsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
+    // fragments brought to x * 2^-E, one exponent E per batch row for the
+    // split (all H * PW panels of the workgroup); from the planes after the
+    // weight ring's loads were issued (as in gemm_xs16)
     h8v xa[PW][4], xb[PW][4];
     const int brow = min(lane & 31, batch - 1);
-    if (xrows == nullptr) {
+    const float *xr = XROWS ? xrows + (size_t)brow * n : nullptr;
+    auto xcol = [&](int p, int st) { return 16 * (16 * (panel0 + p) + 4 * quarter + st) + 8 * (lane >> 5); };
+    int xe_own[PW];
+    constexpr int NG = 2 * H * PW;  // groups of the split
+    constexpr bool kDirect = NG <= 8;  // as in gemm_xs16
+    int xe_all[kDirect ? NG : 1];
+    int E = 0;
+    if constexpr (!XROWS) {
         const size_t xbase = (size_t)(4 * quarter * kWave + brow + 32 * (lane >> 5)) * 8 + 16 * 512 * (size_t)panel0;
+        if constexpr (kDirect) {
 #pragma unroll
-        for (int p = 0; p < PW; p++)
+            for (int g = 0; g < NG; g++) xe_all[g] = xp.xe[(size_t)brow * xe_stride(n) + 2 * ks * H * PW + g];
+        }
+#pragma unroll
+        for (int p = 0; p < PW; p++) {
+            xe_own[p] = xp.xe[(size_t)brow * xe_stride(n) + 2 * (panel0 + p) + (quarter >> 1)];
 #pragma unroll
             for (int st = 0; st < 4; st++) {
-                xa[p][st] = *reinterpret_cast<const h8v *>(xh + xbase + 16 * 512 * p + 512 * st);
-                xb[p][st] = *reinterpret_cast<const h8v *>(xl + xbase + 16 * 512 * p + 512 * st);
+                xa[p][st] = *reinterpret_cast<const h8v *>(xp.hi + xbase + 16 * 512 * p + 512 * st);
+                xb[p][st] = *reinterpret_cast<const h8v *>(xp.lo + xbase + 16 * 512 * p + 512 * st);
             }
+        }
     } else {
-        const float *xr = xrows + (size_t)brow * n;
+        // fp32 rows, split before the ring: lanes l, l + 32 and the NW waves
+        // hold a row's columns
+        float amax = 0.0f;
 #pragma unroll
         for (int p = 0; p < PW; p++)
 #pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const int c0 = 16 * (16 * (panel0 + p) + 4 * quarter + st) + 8 * (lane >> 5);
-                const float4 a = *reinterpret_cast<const float4 *>(xr + c0);
-                const float4 b = *reinterpret_cast<const float4 *>(xr + c0 + 4);
-                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            for (int st = 0; st < 4; st++) amax = amax8(xr + xcol(p, st), amax);
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        if (lane < 32) wmax[wave][lane] = amax;
+        lds_barrier();
+        float rmax = wmax[0][lane & 31];
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    xa[p][st][i] = (_Float16)v[i];
-                    xb[p][st][i] = (_Float16)(v[i] - (float)xa[p][st][i]);
-                }
-            }
+        for (int w = 1; w < NW; w++) rmax = fmaxf(rmax, wmax[w][lane & 31]);
+        E = group_exp(rmax);
+#pragma unroll
+        for (int p = 0; p < PW; p++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) split8_scaled(xr + xcol(p, st), E, xa[p][st], xb[p][st]);
     }
     const uint8_t *wpart = Wp + (size_t)panel0 * Panel<T>::kBytes;
     int lt = g0, lp = 0;  // load cursor: tile, panel of the wave's part
@@ -1557,6 +1756,35 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
         load_next(ring[k]);
         asm volatile("" ::: "memory");
     }
+    if constexpr (!XROWS) {
+        if constexpr (kDirect) {
+            E = kXeEmpty;
+#pragma unroll
+            for (int g = 0; g < NG; g++) E = max(E, xe_all[g]);
+        } else {
+            int e = kXeEmpty;
+#pragma unroll
+            for (int p = 0; p < PW; p++) e = max(e, xe_own[p]);
+            if (lane < 32) emax[wave][lane] = e;
+            lds_barrier();
+            E = emax[0][lane & 31];
+#pragma unroll
+            for (int w = 1; w < NW; w++) E = max(E, emax[w][lane & 31]);
+        }
+#pragma unroll
+        for (int p = 0; p < PW; p++) {
+            const _Float16 f = xe_factor(xe_own[p], E);
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                xa[p][st] = xa[p][st] * f;
+                xb[p][st] = xb[p][st] * f;
+            }
+        }
+    }
+    // the epilogue's batch row (threadIdx / 16) takes its exponent from the
+    // lane holding that row
+    static_assert(512 / (kWave * NW) == 1, "one output vector per thread");
+    const float fEb = xe_scale(row_exp4(E, 4 * wave));
     int ct = g0;  // tile being multiplied
     f32x16 acc0 = {}, acc1 = {};
     do {
@@ -1592,6 +1820,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
                         const float4 o = *reinterpret_cast<const float4 *>(&red[w][r][l]);
                         sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
                     }
+                    sum = mul4(sum, fEb);
                     const int row = ct * kWave + 4 * j;
                     const int off = b < batch && row < m && ct < tiles ? 4 * (ks * (int)split_stride + b * m + row)
                                                                        : kBadOffset;
@@ -1607,24 +1836,32 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
     } while (ct < tiles);
 }
 
-// fp32 x[batch][n] -> fragment-order fp16 planes hi, lo (hi + lo ~= x), one
-// thread per 8 consecutive columns of a row (one 16-byte fragment).
-__global__ __launch_bounds__(256) void split_x_frag_kernel(const float *__restrict__ x, _Float16 *__restrict__ hi,
-                                                          _Float16 *__restrict__ lo, int batch, int n) {
+// fp32 x[batch][n] -> range-safe fragment-order fp16 planes (hi + lo = x *
+// 2^-e per 128-column group, the exponents to xe), one thread per 8
+// consecutive columns of a row (one 16-byte fragment): a group is 16
+// consecutive threads of one wave (n % 128 == 0).
+__global__ __launch_bounds__(256) void split_x_frag_kernel(const float *__restrict__ x, Planes xp, int batch, int n) {
     const int g = blockIdx.x * 256 + threadIdx.x, per_row = n >> 3;
-    if (g >= batch * per_row) return;
+    if (g >= batch * per_row) return;  // whole 16-thread groups leave together
     const int b = g / per_row, c = 8 * (g % per_row);
     const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)b * n + c);
     const float4 v0 = src[0], v1 = src[1];
     const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    const int ex = group_exp(row_max16(amax));  // a group is a 16-lane row
     h8v h, l;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        h[e] = (_Float16)v[e];
-        l[e] = (_Float16)(v[e] - (float)h[e]);
+        _Float16 hh, ll;
+        split_scaled(v[e], ex, hh, ll);
+        h[e] = hh;
+        l[e] = ll;
     }
-    *reinterpret_cast<h8v *>(hi + xf_index(b, c)) = h;
-    *reinterpret_cast<h8v *>(lo + xf_index(b, c)) = l;
+    *reinterpret_cast<h8v *>(xp.hi + xf_index(b, c)) = h;
+    *reinterpret_cast<h8v *>(xp.lo + xf_index(b, c)) = l;
+    if ((g & 15) == 0) xp.xe[xe_index(b, c, n)] = (int8_t)ex;
 }
 
 // ---------------------------------------------------------------------------
@@ -1643,15 +1880,31 @@ __global__ __launch_bounds__(256) void split_x_frag_kernel(const float *__restri
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-// fp32 x[batch][n] -> fp16 planes hi[batch][n], lo[batch][n] with hi + lo ~= x.
-__global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ x, _Float16 *__restrict__ hi,
-                                                     _Float16 *__restrict__ lo, size_t count) {
-    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= count) return;
-    const float v = x[i];
-    const _Float16 h = (_Float16)v;
-    hi[i] = h;
-    lo[i] = (_Float16)(v - (float)h);
+// fp32 x[batch][n] -> range-safe fp16 planes hi[batch][n], lo[batch][n]
+// (row-major; hi + lo = x * 2^-e per 128-column group, exponents to xe), one
+// thread per 8 consecutive columns, 16 threads per group (n % 128 == 0).
+__global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ x, Planes xp, int batch, int n) {
+    const int g = blockIdx.x * 256 + threadIdx.x, per_row = n >> 3;
+    if (g >= batch * per_row) return;  // whole 16-thread groups leave together
+    const int b = g / per_row, c = 8 * (g % per_row);
+    const size_t o = (size_t)b * n + c;
+    const float4 v0 = *reinterpret_cast<const float4 *>(x + o), v1 = *reinterpret_cast<const float4 *>(x + o + 4);
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    const int ex = group_exp(row_max16(amax));  // a group is a 16-lane row
+    f16x8 h, l;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        _Float16 hh, ll;
+        split_scaled(v[e], ex, hh, ll);
+        h[e] = hh;
+        l[e] = ll;
+    }
+    *reinterpret_cast<f16x8 *>(xp.hi + o) = h;
+    *reinterpret_cast<f16x8 *>(xp.lo + o) = l;
+    if ((g & 15) == 0) xp.xe[xe_index(b, c, n)] = (int8_t)ex;
 }
 
 // 8 weights of one row of one block, as fp16, from the LDS tile row `wl`
@@ -1706,14 +1959,15 @@ __device__ __forceinline__ float blk_scale(const uint32_t *wl, int blk) {
 // columns x 16 weight rows), so D[b][r] = sum_k x[b][k] W[r][k]; a lane's four
 // D values share one weight row and therefore one block scale.
 template <uint32_t T, int NT>
-__global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint8_t *__restrict__ W,
-                                                                     const _Float16 *__restrict__ xh,
-                                                                     const _Float16 *__restrict__ xl,
+__global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint8_t *__restrict__ W, Planes xp,
                                                                      float *__restrict__ out, int m, int n,
                                                                      int batch, int sb_per_split,
                                                                      size_t split_stride) {
     constexpr int V = QTraits<T>::kSbVec;
     __shared__ u32x4 lds[kWavesPerWg][V * kWave];
+    __shared__ int xeE[32];
+    const _Float16 *__restrict__ xh = xp.hi;
+    const _Float16 *__restrict__ xl = xp.lo;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int tile = blockIdx.x;
@@ -1725,6 +1979,15 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint
     const int sb_end = min(nsb, sb_begin + sb_per_split);
     const int li = lane & 15;  // A row (batch) / B column (weight row) within a 16 tile
     const int g = lane >> 4;   // k group (8 columns) / D row group
+    // range-safe planes: the split's groups (2 per super-block) of batch row
+    // li + 16 nt brought to one exponent En[nt]
+    int En[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int b = min(li + 16 * nt, batch - 1);
+        En[nt] = xe_max(xp.xe, b, 2 * sb_begin, 2 * (sb_end - sb_begin), n);
+        if (wave == 0 && g == 0) xeE[li + 16 * nt] = En[nt];  // read after the reduction barrier
+    }
 
     f32x4 acc[4][NT];
 #pragma unroll
@@ -1758,8 +2021,9 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint
                 const int b = li + 16 * nt;
                 if (b < batch) {
                     const size_t xo = (size_t)b * n + (size_t)sb * 256 + 32 * blk + 8 * g;
-                    ah[nt] = *reinterpret_cast<const f16x8 *>(xh + xo);
-                    al[nt] = *reinterpret_cast<const f16x8 *>(xl + xo);
+                    const _Float16 f = xe_factor(xp.xe[(size_t)b * xe_stride(n) + 2 * sb + (blk >> 2)], En[nt]);
+                    ah[nt] = *reinterpret_cast<const f16x8 *>(xh + xo) * f;
+                    al[nt] = *reinterpret_cast<const f16x8 *>(xl + xo) * f;
                 } else {
                     ah[nt] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
                     al[nt] = ah[nt];
@@ -1806,7 +2070,7 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint
                 for (int v = 1; v < kWavesPerWg; v++) sum += red[(v * per + idx) * kWave + lane];
                 const int row = row0 + rs * 16 + li;
                 const int b = 16 * nt + 4 * g + r;
-                if (row < m && b < batch) dst[(size_t)b * m + row] = sum;
+                if (row < m && b < batch) dst[(size_t)b * m + row] = ldexpf(sum, xeE[b]);
             }
 }
 
@@ -1866,12 +2130,12 @@ int dispatch_fused(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t 
 }
 
 template <uint32_t T, int NT>
-int launch_mfma(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const _Float16 *xh,
-                const _Float16 *xl, uint32_t batch, float *out, size_t split_stride, int ksplit) {
+int launch_mfma(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const Planes &xp,
+                uint32_t batch, float *out, size_t split_stride, int ksplit) {
     const int tiles = (int)((m + kWave - 1) / kWave);
     const int per = split_len((int)(n / 256), ksplit);
     hipLaunchKernelGGL((quant_gemm_mfma<T, NT>), dim3(tiles, ksplit), dim3(kWave * kWavesPerWg), 0, stream,
-                       static_cast<const uint8_t *>(w), xh, xl, out, (int)m, (int)n, (int)batch, per, split_stride);
+                       static_cast<const uint8_t *>(w), xp, out, (int)m, (int)n, (int)batch, per, split_stride);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
@@ -1885,13 +2149,19 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
         in.x = x;
         return dispatch_fused<T>(ctx, stream, w, m, n, in, out, ksplit);
     }
-    // batch 2..32: split x into fp16 hi/lo planes, then the MFMA kernel
+    // batch 2..32: split x into range-safe fp16 hi/lo planes (row-major),
+    // then the MFMA kernel
     const size_t count = (size_t)batch * n;
-    _Float16 *xh = xsplit, *xl = xsplit + count;
-    hipLaunchKernelGGL(split_x_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, x, xh, xl, count);
+    Planes xp;
+    xp.hi = xsplit;
+    xp.lo = xsplit + count;
+    xp.xe = reinterpret_cast<int8_t *>(xsplit + 2 * count);
+    const size_t vecs = count / 8;
+    hipLaunchKernelGGL(split_x_kernel, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0, stream, x, xp, (int)batch,
+                       (int)n);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-    if (batch <= 16) return launch_mfma<T, 1>(ctx, stream, w, m, n, xh, xl, batch, out, split_stride, ksplit);
-    return launch_mfma<T, 2>(ctx, stream, w, m, n, xh, xl, batch, out, split_stride, ksplit);
+    if (batch <= 16) return launch_mfma<T, 1>(ctx, stream, w, m, n, xp, batch, out, split_stride, ksplit);
+    return launch_mfma<T, 2>(ctx, stream, w, m, n, xp, batch, out, split_stride, ksplit);
 }
 
 }  // namespace
@@ -1972,11 +2242,11 @@ int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t b
 // on lm_head at batch 32, slower at batch 4 and 16 and on the small shapes.)
 template <uint32_t T>
 int launch_gemm_packed_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
-                         const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit, int per) {
+                         const Planes &xp, uint32_t batch, float *out, int ksplit, int per) {
     const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const int items = tiles * ksplit;
     hipLaunchKernelGGL((gemm_packed<T, 1, kGemmRing>), dim3(min(items, 2 * cus)), dim3(kWave * kGemmWaves), 0, stream,
-                       w, xh, xl, out, (int)m, (int)n, (int)batch, ksplit, per, (size_t)batch * m);
+                       w, xp, out, (int)m, (int)n, (int)batch, ksplit, per, (size_t)batch * m);
     return ANEHIP_OK;
 }
 
@@ -2005,8 +2275,7 @@ static GemmKernel gemm_kernel(uint32_t batch, int nsb, int ksplit) {
 // workgroups per split in every case.
 template <uint32_t T>
 void launch_gemm_xs_any(anehip_ctx *ctx, hipStream_t stream, GemmKernel kind, const uint8_t *w, uint32_t m,
-                        uint32_t n, const _Float16 *xh, const _Float16 *xl, const float *xrows, uint32_t batch,
-                        float *out, int ksplit) {
+                        uint32_t n, const Planes &xp, const float *xrows, uint32_t batch, float *out, int ksplit) {
     const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const int per = (int)(n / 256) / ksplit;
     const size_t ss = (size_t)batch * m;
@@ -2014,28 +2283,38 @@ void launch_gemm_xs_any(anehip_ctx *ctx, hipStream_t stream, GemmKernel kind, co
     const int gs = max(1, min(tiles, wgs * cus / ksplit));
     const dim3 grid(gs * ksplit);
 #define ANEHIP_XS(KERNEL, NT)                                                                                       \
-    hipLaunchKernelGGL(KERNEL, grid, dim3(NT), 0, stream, w, xh, xl, xrows, out, (int)m, (int)n, (int)batch, ksplit, ss)
+    hipLaunchKernelGGL(KERNEL, grid, dim3(NT), 0, stream, w, xp, xrows, out, (int)m, (int)n, (int)batch, ksplit, ss)
+#define ANEHIP_XS2(KERNEL, NT, ...)                                                                                \
+    do {                                                                                                           \
+        if (xrows) ANEHIP_XS((KERNEL<__VA_ARGS__, true>), NT);                                                     \
+        else ANEHIP_XS((KERNEL<__VA_ARGS__, false>), NT);                                                          \
+    } while (0)
+#define ANEHIP_XSH(PW, D)                                                                                          \
+    do {                                                                                                           \
+        if (xrows) ANEHIP_XS((gemm_xsh<T, PW, D, 2, true>), 512);                                                  \
+        else ANEHIP_XS((gemm_xsh<T, PW, D, 2, false>), 512);                                                       \
+    } while (0)
     if (kind == GemmKernel::Xs16) {
         if (per == 1)
-            ANEHIP_XS((gemm_xs16<T, 1, 1, 4>), 256);
+            ANEHIP_XS2(gemm_xs16, 256, T, 1, 1, 4);
         else if (per == 2)
-            ANEHIP_XS((gemm_xs16<T, 2, 2, 2>), 256);
+            ANEHIP_XS2(gemm_xs16, 256, T, 2, 2, 2);
         else if (per == 4)
-            ANEHIP_XS((gemm_xs16<T, 4, 2, 2>), 256);
+            ANEHIP_XS2(gemm_xs16, 256, T, 4, 2, 2);
         else
-            ANEHIP_XS((gemm_xs16<T, 8, 2, 2>), 256);
+            ANEHIP_XS2(gemm_xs16, 256, T, 8, 2, 2);
     } else if (kind == GemmKernel::Xsh) {
         if (per == 2)
-            ANEHIP_XS((gemm_xsh<T, 1, 1, 2>), 512);
+            ANEHIP_XSH(1, 1);
         else if (per == 4)
-            ANEHIP_XS((gemm_xsh<T, 2, 2, 2>), 512);
+            ANEHIP_XSH(2, 2);
         else
-            ANEHIP_XS((gemm_xsh<T, 4, 2, 2>), 512);
-    } else if (xrows) {
-        ANEHIP_XS((gemm_xs<T, 1, 1, true>), 256);
+            ANEHIP_XSH(4, 2);
     } else {
-        ANEHIP_XS((gemm_xs<T, 1, 1, false>), 256);
+        ANEHIP_XS2(gemm_xs, 256, T, 1, 1);
     }
+#undef ANEHIP_XSH
+#undef ANEHIP_XS2
 #undef ANEHIP_XS
 }
 
@@ -2064,28 +2343,29 @@ int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type,
                          batch);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     if (ggml_type == ANEHIP_GGML_Q8_0)
-        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, nullptr, nullptr, x, batch, out, ksplit);
+        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, Planes{}, x, batch, out, ksplit);
     else
-        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, nullptr, nullptr, x, batch, out, ksplit);
+        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, Planes{}, x, batch, out, ksplit);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
-                       uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit) {
+                       uint32_t n, const Planes &xp, uint32_t batch, float *out, int ksplit) {
     if (int rc = check_gemm_args(ctx, m, n, batch, ksplit)) return rc;
+    if (!xp.hi || !xp.lo || !xp.xe) return set_error(ctx->err, ANEHIP_EINVAL, "gemm: input planes incomplete");
     const int per = split_len((int)(n / 256), ksplit);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     const GemmKernel kind = gemm_kernel(batch, (int)(n / 256), ksplit);
     const bool q8 = ggml_type == ANEHIP_GGML_Q8_0;
     if (kind != GemmKernel::Persistent && q8)
-        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, xh, xl, nullptr, batch, out, ksplit);
+        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, xp, nullptr, batch, out, ksplit);
     else if (kind != GemmKernel::Persistent)
-        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, xh, xl, nullptr, batch, out, ksplit);
+        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, xp, nullptr, batch, out, ksplit);
     else if (q8)
-        launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
+        launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xp, batch, out, ksplit, per);
     else
-        launch_gemm_packed_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xh, xl, batch, out, ksplit, per);
+        launch_gemm_packed_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xp, batch, out, ksplit, per);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
@@ -2182,24 +2462,13 @@ int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     return dispatch_packed<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, in, out, ksplit);
 }
 
-int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t batch, uint32_t n, _Float16 *xh,
-                   _Float16 *xl) {
+int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t batch, uint32_t n, const Planes &xp) {
+    if (n % kXeGroup) return set_error(ctx->err, ANEHIP_EINVAL, "split_x: n=%u not a multiple of %d", n, kXeGroup);
     const size_t vecs = (size_t)batch * (n / 8);
-    hipLaunchKernelGGL(split_x_frag_kernel, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0, stream, x, xh, xl,
+    hipLaunchKernelGGL(split_x_frag_kernel, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0, stream, x, xp,
                        (int)batch, (int)n);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
-}
-
-int launch_gemm_planes(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
-                       uint32_t n, const _Float16 *xh, const _Float16 *xl, uint32_t batch, float *out, int ksplit) {
-    const size_t ss = (size_t)batch * m;
-    if (ggml_type == ANEHIP_GGML_Q8_0) {
-        if (batch <= 16) return launch_mfma<ANEHIP_GGML_Q8_0, 1>(ctx, stream, w, m, n, xh, xl, batch, out, ss, ksplit);
-        return launch_mfma<ANEHIP_GGML_Q8_0, 2>(ctx, stream, w, m, n, xh, xl, batch, out, ss, ksplit);
-    }
-    if (batch <= 16) return launch_mfma<ANEHIP_GGML_Q4_0, 1>(ctx, stream, w, m, n, xh, xl, batch, out, ss, ksplit);
-    return launch_mfma<ANEHIP_GGML_Q4_0, 2>(ctx, stream, w, m, n, xh, xl, batch, out, ss, ksplit);
 }
 
 int launch_gemv_fused(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
@@ -2230,9 +2499,9 @@ int launch_quant_gemm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, c
     // kernel never needs more than kMaxSliceSb super-blocks per split
     const int ksplit = gemm_ksplit(ctx, m, n, batch == 1 ? 1 << 20 : kMaxSplit);
     const size_t count = (size_t)batch * m;
-    // workspace: [ksplit partials][x hi/lo planes (2 * batch * n halves)]
+    // workspace: [ksplit partials][x hi/lo planes (2 * batch * n halves)][group exponents]
     const size_t part = ksplit > 1 ? (size_t)ksplit * count : 0;
-    const size_t xs_floats = batch > 1 ? (size_t)batch * n : 0;
+    const size_t xs_floats = batch > 1 ? (size_t)batch * n + (xe_bytes(n) + 3) / 4 : 0;
     int rc = ensure_workspace(ctx, part + xs_floats);
     if (rc) return rc;
     void *xs = batch > 1 ? static_cast<void *>(ctx->ws.partial + part) : nullptr;

@@ -235,15 +235,19 @@ int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
         if ((rc = launch_gemm_xs_rows(ctx, ctx->stream, ggml_type, wp, m, n, x, batch, ctx->ws.partial))) return rc;
         return launch_sum_partials(ctx, ctx->stream, ctx->ws.partial, y, count, ksplit);
     }
-    // workspace: [x hi plane][x lo plane] (fp16, xcount each) then the partials
-    const size_t planes = xcount;  // floats holding both planes
+    // workspace: [x hi plane][x lo plane] (fp16, xcount each), the group
+    // exponents, then the partials
+    const size_t planes = xcount + (xe_bytes(n) + 3) / 4;  // floats holding both planes and the exponents
     int rc = ensure_workspace(ctx, planes + (ksplit > 1 ? (size_t)ksplit * count : 0));
     if (rc) return rc;
-    _Float16 *xh = reinterpret_cast<_Float16 *>(ctx->ws.partial), *xl = xh + xcount;
-    if ((rc = launch_split_x(ctx, ctx->stream, x, batch, n, xh, xl))) return rc;
-    if (ksplit == 1) return launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xh, xl, batch, y, 1);
+    Planes xp;
+    xp.hi = reinterpret_cast<_Float16 *>(ctx->ws.partial);
+    xp.lo = xp.hi + xcount;
+    xp.xe = reinterpret_cast<int8_t *>(xp.lo + xcount);
+    if ((rc = launch_split_x(ctx, ctx->stream, x, batch, n, xp))) return rc;
+    if (ksplit == 1) return launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xp, batch, y, 1);
     float *part = ctx->ws.partial + planes;
-    if ((rc = launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xh, xl, batch, part, ksplit))) return rc;
+    if ((rc = launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xp, batch, part, ksplit))) return rc;
     return launch_sum_partials(ctx, ctx->stream, part, y, count, ksplit);
 }
 

@@ -162,6 +162,35 @@ def test_prefill_one_sequence_of_a_batch(mid_host):
         q.close()
 
 
+@pytest.mark.parametrize("which,B", [("small", 2), ("small", 32), ("mid", 2), ("mid", 7), ("mid", 32)])
+def test_activations_beyond_fp16_range(which, B):
+    """Batched steps whose GEMM inputs leave fp16's range: post-attention and
+    DeltaNet output norm weights scaled by 3e4 (FFN inputs, SiLU-mul outputs
+    and gated-norm outputs reach 1e5 - 1e9) and q-norm weights by 1e5 (the
+    attention's q operand).  The element-wise kernels write range-safe planes
+    and the GEMMs / attention scale them back: logits match the fp32 oracle
+    (1e-3) over 3 steps for every sequence."""
+    spec = anehip.Spec(**(SMALL if which == "small" else MID))
+    host = HostModel(spec, seed=41)
+    scale = {anehip.T["POST_ATTN_NORM"]: 3e4, anehip.T["SSM_NORM"]: 3e4, anehip.T["Q_NORM"]: 1e5}
+    for (layer, kind), (arr, rows, cols, quant) in host.tensors.items():
+        if kind in scale:
+            arr *= np.float32(scale[kind])
+            host.om.set_f32(layer, kind, arr)
+    gm = _model(host, B, 16)
+    seqs = [host.seq(16) for _ in range(B)]
+    for step in range(3):
+        toks = oracle.randint(42, step, B, spec.vocab_size)
+        g = gm.step(toks)
+        assert np.all(np.isfinite(g))
+        for b in range(B):
+            l2, mx = rel_errs(g[b], seqs[b].forward(int(toks[b])))
+            assert l2 <= TOL and mx <= TOL, (step, b, l2, mx)
+    gm.close()
+    for q in seqs:
+        q.close()
+
+
 def test_prefill_rejects_bad_arguments(small_host):
     gm = _model(small_host, 2, 16)
     with pytest.raises(anehip.AnehipError) as e:

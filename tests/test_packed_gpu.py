@@ -159,3 +159,89 @@ def test_packed_gemm_many_tiles(gpu_ctx, oracle_lib, t, m, n, batch):
         assert l2 <= TOL and mx <= TOL
     for buf in (dw, dp, dx, dy):
         buf.free()
+
+
+def extreme_rows(oracle_lib, batch, n, seed):
+    """Batch rows outside fp16's range, cycled: N(0, 1) with +-7e4 / +-1e5
+    entries in several 128-column groups; whole rows scaled to 1e5, 1e-6 and
+    1e-30; a row of zeros; groups alternating 1e4 and 1e-4; fp32 subnormals
+    (1e-40); a plain N(0, 1) row."""
+    x = oracle_lib.normal(seed, 1, batch * n).reshape(batch, n).astype(np.float64)
+    out = np.empty_like(x)
+    for b in range(batch):
+        r, kind = x[b].copy(), b % 8
+        if kind == 0:
+            idx = np.arange(3, n, 97)
+            r[idx] = np.where(idx % 2, 7e4, -1e5) * np.where(idx % 3, 1.0, -1.0)
+        elif kind == 1:
+            r *= 1e5
+        elif kind == 2:
+            r *= 1e-6
+        elif kind == 3:
+            r *= 1e-30
+        elif kind == 4:
+            r[:] = 0.0
+        elif kind == 5:
+            r *= np.where((np.arange(n) // 128) % 2, 1e4, 1e-4)
+        elif kind == 6:
+            r *= 1e-40
+        out[b] = r
+    return out.astype(np.float32)
+
+
+def check_extreme(y, x, w, t, m, n, oracle_lib):
+    """Every row against the oracle (1e-4 relative, rel L2 and max-abs /
+    max |ref|); zero rows exactly zero; the subnormal row, where the oracle's
+    own fp32 products lose bits, against float64."""
+    import np_ref
+
+    ref = oracle_lib.gemm(t, w, m, n, x)
+    for b in range(x.shape[0]):
+        assert np.all(np.isfinite(y[b])), b
+        if not np.any(x[b]):
+            assert not np.any(y[b]), b
+            continue
+        if b % 8 == 6:
+            r = np_ref.dequant(t, w, m, n) @ x[b].astype(np.float64)
+        else:
+            r = ref[b]
+        l2, mx = rel_errs(y[b], r)
+        print(f"row {b} (kind {b % 8}): rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+        assert l2 <= TOL and mx <= TOL, (b, l2, mx)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("batch", [2, 17, 32])
+@pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 2048), (100, 256), (2048, 6144)])
+def test_packed_gemm_input_range(gpu_ctx, oracle_lib, t, batch, m, n):
+    """The batch > 1 GEMMs split fp32 x into fp16 hi + lo: rows far outside
+    fp16's range (overflow, underflow, subnormal, zero, mixed groups) match
+    the fp32 oracle, on the x-stationary kernels (fp32 rows, per-row scaling
+    over the split) and on the persistent kernel (range-safe planes)."""
+    w = oracle_lib.gen_quant(t, 55, m + n + t, m, n, std=0.02)
+    x = extreme_rows(oracle_lib, batch, n, 500 + batch)
+    dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
+    dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(batch * m * 4)
+    gpu_ctx.call("quant_gemm_packed", t, dp, m, n, dx, batch, dy)
+    y = dy.download(np.float32, batch * m).reshape(batch, m)
+    check_extreme(y, x, w, t, m, n, oracle_lib)
+    for b in (dw, dp, dx, dy):
+        b.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("batch", [2, 17, 32])
+@pytest.mark.parametrize("m,n", [(2048, 2048), (100, 256)])
+def test_gguf_gemm_input_range(gpu_ctx, oracle_lib, t, batch, m, n):
+    """The same rows through anehip_quant_gemm (GGUF blocks, row-major
+    range-safe planes)."""
+    w = oracle_lib.gen_quant(t, 56, m + n + t, m, n, std=0.02)
+    x = extreme_rows(oracle_lib, batch, n, 600 + batch)
+    dw, dx, dy = gpu_ctx.to_device(w), gpu_ctx.to_device(x), gpu_ctx.alloc(batch * m * 4)
+    gpu_ctx.quant_gemm(t, dw, m, n, dx, batch, dy)
+    y = dy.download(np.float32, batch * m).reshape(batch, m)
+    check_extreme(y, x, w, t, m, n, oracle_lib)
+    for b in (dw, dx, dy):
+        b.free()
