@@ -305,6 +305,11 @@ int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t
 // input is formed by prologue `mode` (a GEMV_IN_* value): norm prologues and
 // the SiLU-mul prologue favour fewer splits.
 int gemv_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, int mode = GEMV_IN_PLAIN);
+// One-launch batch-1 GEMV of a matrix with few row tiles (gemv.hip:
+// gemv_rows); gemv_rows_split gives its row split, or 0 when it does not apply.
+int gemv_rows_split(const anehip_ctx *ctx, uint32_t m, uint32_t n);
+int launch_gemv_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,
+                     const float *x, float *y, int H);
 int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                        uint32_t n, const GemvInput &in, float *out, int ksplit);
 // Batch-1 GEMV whose input is formed by `in` (see GemvInMode); writes

@@ -816,6 +816,104 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
     }
 }
 
+// Batch-1 GEMV of a matrix with few row tiles, in one launch: a workgroup of
+// 16 waves takes R = 64 / H rows of one tile over the whole K range, so the
+// grid has tiles * H workgroups and no K split (no partial sums, no second
+// launch).  Lane l serves row l % R of the workgroup's rows and slot
+// wave * H + l / R; slot s takes the row's Q8_0 / Q4_0 blocks s, s + 16 H,
+// ... (J of them: 8 n / 256 = 16 H J), whole blocks with their scales, every
+// load issued before any is used.  x is staged in LDS (its loads issued
+// before the weights', so waiting for them does not wait for the weights).
+// Per lane: block sums in block order, each scaled (q8_gemv.rs:234-242);
+// then the 16 H slots of a row are added through LDS in slot order.
+constexpr int kRowsWaves = 16;
+constexpr int kRowsMaxN = 8192;
+
+template <uint32_t T, int H, int J>
+__global__ __launch_bounds__(kWave *kRowsWaves) void gemv_rows(const uint8_t *__restrict__ Wp,
+                                                               const float *__restrict__ x, float *__restrict__ y,
+                                                               int m, int n) {
+    constexpr int R = kWave / H, SLOTS = kRowsWaves * H, NT = kWave * kRowsWaves;
+    constexpr int VB = T == ANEHIP_GGML_Q8_0 ? 2 : 1;  // 16-byte quant vectors per block
+    constexpr int XV = kRowsMaxN / 4 / NT;              // float4 of x per thread, at most
+    __shared__ __align__(16) float xs[kRowsMaxN];
+    __shared__ float red[kRowsWaves][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int tile = blockIdx.x / H, h = blockIdx.x % H;
+    const int r = lane % R, slot = wave * H + lane / R;
+    const int rr = h * R + r;  // row within the tile
+    const int nsb = n >> 8;
+
+    float4 xv[XV];
+    const int n4 = n >> 2;
+#pragma unroll
+    for (int i = 0; i < XV; i++) {
+        const int e = min((int)threadIdx.x + i * NT, n4 - 1);
+        xv[i] = reinterpret_cast<const float4 *>(x)[e];
+    }
+    const uint8_t *tb = Wp + (size_t)tile * nsb * Panel<T>::kBytes;
+    u32x4 q[J][VB];
+    uint32_t scw[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int b = slot + j * SLOTS, bi = b & 7;
+        const u32x4 *pp = reinterpret_cast<const u32x4 *>(tb + (size_t)(b >> 3) * Panel<T>::kBytes);
+#pragma unroll
+        for (int v = 0; v < VB; v++) q[j][v] = __builtin_nontemporal_load(pp + (VB * bi + v) * kWave + rr);
+        scw[j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(pp + Panel<T>::kChunks * kWave + rr) +
+                                            (bi >> 1));
+    }
+#pragma unroll
+    for (int i = 0; i < XV; i++) {
+        const int e = (int)threadIdx.x + i * NT;
+        if (e < n4) reinterpret_cast<float4 *>(xs)[e] = xv[i];
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int b = slot + j * SLOTS;
+        const float d = __half2float(__ushort_as_half((unsigned short)(scw[j] >> (16 * (b & 1)))));
+        const float *xb = xs + 32 * b;
+        float bs = 0.0f;
+        if constexpr (T == ANEHIP_GGML_Q8_0) {
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const u32x4 v = q[j][hh];
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int qi = (int)(int8_t)(w4[i >> 2] >> (8 * (i & 3)));
+                    bs = fmaf((float)qi, xb[16 * hh + i], bs);
+                }
+            }
+        } else {
+            const u32x4 v = q[j][0];
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t byte = (w4[i >> 2] >> (8 * (i & 3))) & 0xffu;
+                bs = fmaf((float)((int)(byte & 15u) - 8), xb[i], bs);
+                bs = fmaf((float)((int)(byte >> 4) - 8), xb[16 + i], bs);
+            }
+        }
+        acc = fmaf(bs, d, acc);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (threadIdx.x < R) {
+        const int row = tile * kWave + h * R + (int)threadIdx.x;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; w++) {
+#pragma unroll
+            for (int k = 0; k < H; k++) sum += red[w][k * R + threadIdx.x];
+        }
+        if (row < m) y[row] = sum;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Small-batch GEMM over panels on MFMA (batch 2..32).
 //
@@ -2453,6 +2551,64 @@ int dispatch_packed(anehip_ctx *ctx, hipStream_t s, const void *w, uint32_t m, u
             return launch_packed_t<T, GEMV_IN_ATTN_COMBINE>(ctx, s, w, m, n, in, out, ksplit);
         default: return set_error(ctx->err, ANEHIP_EINVAL, "gemv: input mode %d", in.mode);
     }
+}
+
+// The row split of gemv_rows for an m x n matrix: H row groups per tile (4,
+// else 2; J = n / (512 H) blocks per slot, 1 <= J <= 4) when the grid gets
+// at least half as many workgroups as CUs; 0 when gemv_rows does not apply
+// (matrices the split GEMV covers with row tiles alone keep it).  Measured on
+// MI355X at batch 1, in graphs of back-to-back launches, against the K split
+// plus its summing launch: 6144 x 2048 5.3 us (H 4 or 2) against 7.0;
+// 2048 x 2048 3.8 (4) / 4.5 (2) against 6.0; 2048 x 6144 7.5 (4) against 7.9.
+int gemv_rows_split(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+    if (n % 256 || n > (uint32_t)kRowsMaxN) return 0;
+    const int nsb = (int)(n / 256), tiles = (int)((m + kWave - 1) / kWave);
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    if (gemv_packed_ksplit(ctx, m, n) == 1) return 0;
+    for (int H : {4, 2}) {
+        if (nsb % (2 * H) || nsb / (2 * H) > 4) continue;
+        if (tiles * H >= cus / 2) return H;
+    }
+    return 0;
+}
+
+template <uint32_t T>
+int launch_rows_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
+                  float *y, int H) {
+    const int tiles = (int)((m + kWave - 1) / kWave), J = (int)(n / 256) / (2 * H);
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+    const dim3 grid(tiles * H), block(kWave * kRowsWaves);
+#define ANEHIP_ROWS(HH, JJ) hipLaunchKernelGGL((gemv_rows<T, HH, JJ>), grid, block, 0, stream, wb, x, y, (int)m, (int)n)
+    if (H == 2) {
+        switch (J) {
+            case 1: ANEHIP_ROWS(2, 1); break;
+            case 2: ANEHIP_ROWS(2, 2); break;
+            case 3: ANEHIP_ROWS(2, 3); break;
+            case 4: ANEHIP_ROWS(2, 4); break;
+            default: return set_error(ctx->err, ANEHIP_EINVAL, "gemv_rows: %d blocks per slot", J);
+        }
+    } else if (H == 4) {
+        switch (J) {
+            case 1: ANEHIP_ROWS(4, 1); break;
+            case 2: ANEHIP_ROWS(4, 2); break;
+            case 3: ANEHIP_ROWS(4, 3); break;
+            case 4: ANEHIP_ROWS(4, 4); break;
+            default: return set_error(ctx->err, ANEHIP_EINVAL, "gemv_rows: %d blocks per slot", J);
+        }
+    } else {
+        return set_error(ctx->err, ANEHIP_EINVAL, "gemv_rows: row split %d", H);
+    }
+#undef ANEHIP_ROWS
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_gemv_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,
+                     const float *x, float *y, int H) {
+    if (n % 256 || n > (uint32_t)kRowsMaxN || (n / 256) % (2 * H))
+        return set_error(ctx->err, ANEHIP_EINVAL, "gemv_rows: n=%u with row split %d", n, H);
+    if (ggml_type == ANEHIP_GGML_Q8_0) return launch_rows_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, x, y, H);
+    return launch_rows_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, x, y, H);
 }
 
 int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,

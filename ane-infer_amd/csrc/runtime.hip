@@ -324,6 +324,8 @@ int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
     if (!wp || !x || !y) return set_error(ctx->err, ANEHIP_EINVAL, "quant_gemv_packed: null pointer");
     int rc = check_packed_args(ctx, "quant_gemv_packed", ggml_type, m, n);
     if (rc) return rc;
+    // few row tiles and n <= 8192: one launch with no K split
+    if (const int H = gemv_rows_split(ctx, m, n)) return launch_gemv_rows(ctx, ctx->stream, ggml_type, wp, m, n, x, y, H);
     const int ksplit = gemv_packed_ksplit(ctx, m, n);  // the decode step's choice (<= 8 splits)
     GemvInput in;
     in.x = x;

@@ -14,10 +14,20 @@ copies (> 512 MiB per shape) that the 256 MiB MALL cannot serve repeated
 reads.  Each sweep pass is one captured hipGraph (anehip_capture_*), so the
 host's launch rate does not enter the figure.
 
+`configs2_q4` times configs[2], the same three shapes in Q4_0 at M = 1
+(panel and GGUF layouts, weights rotated past the MALL as above).
+`configs3_deltanet` times configs[3]: 256 Gated DeltaNet decode steps
+(anehip_deltanet_step: conv + SiLU, L2 norms, beta / decay, recurrence) at
+batch 1 / 8 / 32, once on one resident state (the configuration as stated:
+B MiB of state, which the 256 MiB MALL holds) and once with the steps rotated
+over > 512 MiB of distinct states (the HBM-bound figure, as in the decode
+step where 18 layers' states stream).
+
 `decode` reports configs[4]: the full random-init Qwen3.5-2B-shape Q8_0 decode
 step (24 layers, fp16 KV cache) at batch 1 and 32 and context 1k / 8k / 32k,
 as tokens/s of greedy decoding with on-device token feedback (one captured
-hipGraph per step).
+hipGraph per step); the `_cap32768` points run a 32k-position cache at a live
+length of 1k / 8k (the attention work follows the live length).
 
 Timing: HIP events recorded on the library's own stream (anehip_timer_*),
 around exactly `--steps` steps after `--warmup` untimed steps, with a stream
@@ -44,12 +54,29 @@ SHAPES = [(6144, 2048), (2048, 6144), (151936, 2048)]
 BATCHES = [1, 4, 16, 32]
 MALL_DEFEAT_BYTES = 512 << 20
 Q8 = 8
-DECODE_POINTS = [(1, 1024), (1, 8192), (1, 32768), (32, 1024), (32, 8192), (32, 32768)]
+Q4 = 2
+BLOCK_BYTES = {Q8: 34, Q4: 18}
+# (batch, live context, cache capacity)
+DECODE_POINTS = [(1, 1024, 1024), (1, 8192, 8192), (1, 32768, 32768), (32, 1024, 1024), (32, 8192, 8192),
+                 (32, 32768, 32768), (1, 1024, 32768), (1, 8192, 32768), (32, 1024, 32768), (32, 8192, 32768)]
 # algorithmic bytes of one decode step: every weight once, KV rows read, DeltaNet
 # state read + written (S and the 4-wide conv window), per sequence
 DECODE_WEIGHT_BYTES = 18 * 62_459_904 + 6 * 55_705_600 + 330_612_736
 KV_BYTES_PER_POS = 6 * 2 * 2 * 256 * 2
 DN_STATE_BYTES = 18 * (2 * 16 * 128 * 128 * 4 + 2 * 6144 * 4 * 4)
+# H = 16 heads of dk = dv = 128, 6144 conv channels (q, k, v)
+DN_HEADS, DN_CH = 16, 6144
+DN_STEPS = 256
+
+
+def dn_step_bytes(batch: int) -> int:
+    """Algorithmic bytes of one DeltaNet decode step: per sequence the state S
+    read and written (2 x 1 MiB), the window's three kept columns read and its
+    new column written (3 + 1 x 6144 fp32), qkv in (6144 fp32), o out
+    (16 x 128 fp32), beta and alpha in (2 x 16 fp32); once per step the conv
+    weights (6144 x 4 fp32)."""
+    per_seq = 2 * DN_HEADS * 128 * 128 * 4 + 3 * DN_CH * 4 + DN_CH * 4 + DN_CH * 4 + DN_HEADS * 128 * 4 + 2 * DN_HEADS * 4
+    return batch * per_seq + DN_CH * 4 * 4
 
 
 def profiled_traffic():
@@ -66,8 +93,8 @@ def profiled_traffic():
     return None
 
 
-def algo_bytes(m: int, n: int, batch: int) -> int:
-    return m * (n // 32) * 34 + 4 * batch * (n + m)
+def algo_bytes(m: int, n: int, batch: int, t: int = Q8) -> int:
+    return m * (n // 32) * BLOCK_BYTES[t] + 4 * batch * (n + m)
 
 
 def parse():
@@ -82,30 +109,37 @@ def parse():
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only run the roofline kernel (lm_head GEMV, M=1) back to back, for rocprofv3")
     ap.add_argument("--decode-only", default=None,
-                    help="only run decode points, e.g. '1:1024,32:1024' (batch:ctx), and print their line")
+                    help="only run decode points, e.g. '1:1024,32:1024:32768' (batch:ctx[:capacity]), and print "
+                         "their line")
+    ap.add_argument("--deltanet-only", action="store_true", help="only run the configs[3] DeltaNet leg")
+    ap.add_argument("--profile-c0", action="store_true",
+                    help="only run the configs[0] GEMV, the streaming-read floor and the empty kernel (for rocprofv3)")
+    ap.add_argument("--profile-points", default=None,
+                    help="only run these sweep points back to back, e.g. '151936x2048:32,6144x2048:4' (for rocprofv3)")
     ap.add_argument("--prefill-only", type=int, default=0,
                     help="only run the batch-1 prefill of this many tokens (twice, the second timed)")
     return ap.parse_args()
 
 
 class Shape:
-    """One sweep shape: Q8_0 weights generated and quantised on the device,
-    replicated into `copies` distinct GGUF buffers, each with its panel copy."""
+    """One sweep shape: Q8_0 (or Q4_0) weights generated and quantised on the
+    device, replicated into `copies` distinct GGUF buffers, each with its
+    panel copy."""
 
-    def __init__(self, anehip, ctx, m, n, seed):
-        self.m, self.n = m, n
-        self.wbytes = m * (n // 32) * 34
-        self.pbytes = int(anehip.lib().anehip_quant_packed_bytes(Q8, m, n))
+    def __init__(self, anehip, ctx, m, n, seed, t=Q8):
+        self.m, self.n, self.t = m, n, t
+        self.wbytes = m * (n // 32) * BLOCK_BYTES[t]
+        self.pbytes = int(anehip.lib().anehip_quant_packed_bytes(t, m, n))
         self.copies = max(2, -(-MALL_DEFEAT_BYTES // self.wbytes))
         self.w = ctx.alloc(self.wbytes * self.copies)
         self.p = ctx.alloc(self.pbytes * self.copies)
         tmp = ctx.alloc(m * n * 4)
         ctx.fill_random(tmp, m * n, 0, seed, 0.0, 0.02)
-        ctx.quantize(Q8, tmp, m, n, self.w.ptr)
+        ctx.quantize(t, tmp, m, n, self.w.ptr)
         for c in range(1, self.copies):
             ctx.d2d(self.w.ptr + c * self.wbytes, self.w.ptr, self.wbytes)
         for c in range(self.copies):
-            ctx.call("quant_pack", Q8, self.wptr(c), m, n, self.pptr(c))
+            ctx.call("quant_pack", t, self.wptr(c), m, n, self.pptr(c))
         ctx.sync()
         tmp.free()
         self.x = ctx.alloc(32 * n * 4)
@@ -118,14 +152,18 @@ class Shape:
     def pptr(self, c):
         return self.p.ptr + (c % self.copies) * self.pbytes
 
+    def free(self):
+        for b in (self.w, self.p, self.x, self.y):
+            b.free()
+
 
 def launch_point(ctx, s, batch, c, gguf=False):
     """One GEMV (M = 1) or MFMA GEMM (M > 1) on copy c: over the panel copy
     (the decode step's layout), or with gguf=True over the GGUF blocks."""
     if gguf:
-        ctx.quant_gemm(Q8, s.wptr(c), s.m, s.n, s.x, batch, s.y)
+        ctx.quant_gemm(s.t, s.wptr(c), s.m, s.n, s.x, batch, s.y)
     else:
-        ctx.call("quant_gemm_packed", Q8, s.pptr(c), s.m, s.n, s.x.ptr, batch, s.y.ptr)
+        ctx.call("quant_gemm_packed", s.t, s.pptr(c), s.m, s.n, s.x.ptr, batch, s.y.ptr)
 
 
 def capture(ctx, enqueue):
@@ -160,13 +198,14 @@ def time_point(ctx, s, batch, launches, gguf=False):
 
 
 def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
-    """Greedy decode tok/s of the random-init Qwen3.5-2B shape at each (batch, ctx)."""
+    """Greedy decode tok/s of the random-init Qwen3.5-2B shape at each
+    (batch, live context, cache capacity)."""
     spec = anehip.Spec()
     gm = anehip.Model(spec)
     gm.randomize(seed=1)
     out = {}
-    for batch, ctx_len in points:
-        gm.alloc_state(batch, ctx_len)
+    for batch, ctx_len, cap in points:
+        gm.alloc_state(batch, cap)
         for l in range(spec.n_layers):
             if spec.layer_types[l] == anehip.LAYER_DELTANET:
                 p, n = gm.state_ptr(l, 0)
@@ -188,7 +227,8 @@ def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
         ms = gm.timer_stop()
         step_ms = ms / steps
         step_bytes = DECODE_WEIGHT_BYTES + batch * (ctx_len * KV_BYTES_PER_POS + DN_STATE_BYTES)
-        out[f"B{batch}_ctx{ctx_len}"] = {
+        key = f"B{batch}_ctx{ctx_len}" + (f"_cap{cap}" if cap != ctx_len else "")
+        out[key] = {
             "tok_s": round(batch * steps / (ms * 1e-3), 1),
             "ms_per_step": round(step_ms, 3),
             "algorithmic_GB_per_step": round(step_bytes / 1e9, 3),
@@ -208,6 +248,137 @@ def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
                                                     "ms": round(dt * 1e3, 2)}
     gm.close()
     return out
+
+
+FLOOR_GRIDS = [(96, 1024), (192, 1024), (256, 256), (256, 512), (384, 512), (512, 256), (512, 512), (1024, 256), (1024, 512),
+               (2048, 256)]
+FLOOR_DEPTHS = [2, 4, 8]
+
+
+def c0_floor(ctx, s, launches=40):
+    """The floor under the configs[0] GEMV: a 16-byte streaming read of the
+    same bytes (one panel copy, rotated as the GEMV's weights are) on each grid
+    of FLOOR_GRIDS x FLOOR_DEPTHS, and an empty kernel, each timed as
+    `launches` back-to-back nodes of one graph (per-launch time)."""
+    sink = ctx.alloc(max(w * t for w, t in FLOOR_GRIDS) * 4)
+    res = {}
+    for wgs, threads in FLOOR_GRIDS:
+        for depth in FLOOR_DEPTHS:
+            g = capture(ctx, lambda: [ctx.call("probe_read", s.pptr(c), s.pbytes, wgs, threads, depth, sink)
+                                      for c in range(launches)])
+            ms = time_graphs(ctx, [g], 3) / 3 / launches
+            ctx.graph_destroy(g)
+            res[f"{wgs}x{threads}_d{depth}"] = round(ms * 1e3, 3)
+    empty = {}
+    for wgs, threads in ((256, 512), (288, 512)):
+        g = capture(ctx, lambda: [ctx.call("probe_empty", wgs, threads) for _ in range(launches)])
+        empty[f"{wgs}x{threads}"] = round(time_graphs(ctx, [g], 3) / 3 / launches * 1e3, 3)
+        ctx.graph_destroy(g)
+    sink.free()
+    best = min(res, key=res.get)
+    gbs = algo_bytes(s.m, s.n, 1) / (res[best] * 1e-6) / 1e9
+    return {"read_us": res, "best": best, "best_us": res[best], "best_GB/s": round(gbs, 1),
+            "best_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "empty_kernel_us": empty,
+            "bytes": s.pbytes}
+
+
+def bench_q4(anehip, ctx):
+    """Q4_0 GEMV at M = 1 on the three shapes (panel layout, and
+    the GGUF blocks through anehip_quant_gemm), weights rotated past the MALL."""
+    out = {}
+    for i, (m, n) in enumerate(SHAPES):
+        s = Shape(anehip, ctx, m, n, 400 + i, t=Q4)
+        for gguf in (False, True):
+            t = time_point(ctx, s, 1, max(s.copies, 20), gguf)
+            gbs = algo_bytes(m, n, 1, Q4) / (t * 1e-3) / 1e9
+            out[f"{m}x{n}_M1" + ("_gguf_layout" if gguf else "")] = {
+                "us": round(t * 1e3, 2), "GB/s": round(gbs, 1), "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        s.free()
+    return out
+
+
+def bench_deltanet(anehip, ctx):
+    """DN_STEPS anehip_deltanet_step calls at batch 1 / 8 / 32
+    (16 heads, dk = dv = 128, S0 ~ N(0, 0.01), fresh N(0, 1) qkv / beta /
+    alpha per step from 8 rotating input sets, ssm_a = -U(0, 1)), captured as
+    one graph: on one resident state, and rotated over > 512 MiB of states."""
+    out = {}
+    per_state = DN_HEADS * 128 * 128 * 4
+    cw, sa, dt = ctx.alloc(DN_CH * 4 * 4), ctx.alloc(DN_HEADS * 4), ctx.alloc(DN_HEADS * 4)
+    ctx.fill_random(cw, DN_CH * 4, 0, 31, 0.0, 0.5)
+    ctx.fill_random(sa, DN_HEADS, 1, 32, -1.0, 0.0)
+    ctx.fill_random(dt, DN_HEADS, 0, 33, 0.0, 1.0)
+    for batch in (1, 8, 32):
+        ins = []
+        for i in range(8):
+            q, b, a = ctx.alloc(batch * DN_CH * 4), ctx.alloc(batch * DN_HEADS * 4), ctx.alloc(batch * DN_HEADS * 4)
+            ctx.fill_random(q, batch * DN_CH, 0, 1000 + i, 0.0, 1.0)
+            ctx.fill_random(b, batch * DN_HEADS, 0, 2000 + i, 0.0, 1.0)
+            ctx.fill_random(a, batch * DN_HEADS, 0, 3000 + i, 0.0, 1.0)
+            ins.append((q, b, a))
+        o = ctx.alloc(batch * DN_HEADS * 128 * 4)
+        res = {}
+        for mode, copies in (("resident", 1), ("rotated", max(2, -(-MALL_DEFEAT_BYTES // (batch * per_state))))):
+            S = ctx.alloc(copies * batch * per_state)
+            W = ctx.alloc(copies * batch * DN_CH * 4 * 4)
+            ctx.fill_random(S, copies * batch * per_state // 4, 0, 40 + batch, 0.0, 0.01)
+            ctx.fill_random(W, copies * batch * DN_CH * 4, 0, 50 + batch, 0.0, 1.0)
+
+            def enqueue():
+                for step in range(DN_STEPS):
+                    c = step % copies
+                    q, b, a = ins[step % 8]
+                    ctx.call("deltanet_step", batch, DN_HEADS, q, b, a, cw, sa, dt,
+                             W.ptr + c * batch * DN_CH * 16, S.ptr + c * batch * per_state, o)
+
+            g = capture(ctx, enqueue)
+            ms = time_graphs(ctx, [g], 3, warmup=1) / 3
+            ctx.graph_destroy(g)
+            us = ms * 1e3 / DN_STEPS
+            res[mode] = {"us_per_step": round(us, 2), "ms_256_steps": round(ms, 3),
+                         "GB/s": round(dn_step_bytes(batch) / (us * 1e-6) / 1e9, 1),
+                         "states": copies}
+            S.free()
+            W.free()
+        res["algorithmic_bytes_per_step"] = dn_step_bytes(batch)
+        out[f"B{batch}"] = res
+        o.free()
+        for t in ins:
+            for buf in t:
+                buf.free()
+    for buf in (cw, sa, dt):
+        buf.free()
+    return out
+
+
+def host_info():
+    """nproc and the CPU model of this host (for the CPU baseline)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"nproc": usable, "cpu_count": os.cpu_count(), "cpu_model": model}
+
+
+def time_cpu(fn, budget_s, min_runs=20):
+    """Median wall time (s) of fn() over at least `min_runs` runs or `budget_s`, after one warm-up run."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times), float(sum(times))
 
 
 def cpu_baseline(anehip, ctx, shapes, budget_s, decode):
@@ -245,6 +416,38 @@ def cpu_baseline(anehip, ctx, shapes, budget_s, decode):
         "sample": f"{reps} passes of the three config-1 shapes at M=1 (row-parallel q8_gemv restatement, "
                   f"{total_t:.1f} s of GEMV time)",
     }
+    res.update(host_info())
+    # Q4_0 GEMV (row-parallel q4_gemv_cpu restatement), M = 1, host-side quantisation
+    q4 = {}
+    for i, (m, n) in enumerate(SHAPES):
+        w = oracle.gen_quant(Q4, 400 + i, 1, m, n, std=0.02)
+        x = oracle.normal(401 + i, 2, n)
+        y = np.empty(m, np.float32)
+        med, runs, _ = time_cpu(lambda: oracle.lib().ao_quant_gemv_mt(Q4, w, m, n, x, y, threads), budget_s / 6)
+        q4[f"{m}x{n}_M1"] = {"us_median": round(med * 1e6, 1),
+                             "GB/s": round(algo_bytes(m, n, 1, Q4) / med / 1e9, 2), "runs": runs}
+    res["q4_gemv"] = q4
+    res["q4_sample"] = f"median of >= 20 runs per shape, {threads} threads"
+    # one sequence's DeltaNet step (deltanet_decode_step's mixer core, single thread)
+    conv_w = oracle.normal(31, 1, DN_CH * 4, std=0.5)
+    ssm_a = -oracle.uniform(32, 2, DN_HEADS)
+    dt_bias = oracle.normal(33, 3, DN_HEADS)
+    S = oracle.normal(34, 4, DN_HEADS * 128 * 128, std=0.01)
+    win = oracle.normal(35, 5, DN_CH * 4)
+    steps_in = [(oracle.normal(36, 10 + i, DN_CH), oracle.normal(36, 20 + i, DN_HEADS),
+                 oracle.normal(36, 30 + i, DN_HEADS)) for i in range(8)]
+    k = [0]
+
+    def dn_step():
+        q, b, a = steps_in[k[0] % 8]
+        k[0] += 1
+        oracle.deltanet_core(q, b, a, conv_w, ssm_a, dt_bias, win, S, DN_HEADS, 128)
+
+    med, runs, _ = time_cpu(dn_step, budget_s / 4)
+    res["deltanet_B1"] = {"us_per_step_median": round(med * 1e6, 1),
+                          "GB/s": round(dn_step_bytes(1) / med / 1e9, 2), "runs": runs, "cores": 1,
+                          "sample": "deltanet_decode_step's conv + norms + gates + recurrence (restated), "
+                                    "one sequence, single thread (the reference's loop is serial)"}
     if decode:
         spec = anehip.Spec()
         gm = anehip.Model(spec)
@@ -260,19 +463,23 @@ def cpu_baseline(anehip, ctx, shapes, budget_s, decode):
                 else:
                     om.set_f32(layer, kind, arr)
         gm.close()
-        seq = oracle.OracleSeq(om, 1024)
+        # attention at ctx ~1k: the sequence starts at position 1023 (the cache
+        # below it zero; attention's cost does not depend on the values)
+        start, cap = 1023, 1024 + 512
+        seq = oracle.OracleSeq(om, cap)
+        seq.pos = start
         seq.forward(1, threads)
         n_tok, t_dec = 0, 0.0
         t_end = time.perf_counter() + budget_s
         tok = 1
-        while time.perf_counter() < t_end or n_tok < 2:
+        while (time.perf_counter() < t_end or n_tok < 2) and seq.pos < cap - 1:
             t0 = time.perf_counter()
             tok = oracle.argmax(seq.forward(tok, threads))
             t_dec += time.perf_counter() - t0
             n_tok += 1
         res["decode_tok_s_B1_ctx1k"] = round(n_tok / t_dec, 2)
-        res["decode_sample"] = (f"{n_tok} greedy tokens of qwen35_forward_token (restated) from pos 0, "
-                                f"2B shape, Q8_0, {threads} threads for the GEMVs")
+        res["decode_sample"] = (f"{n_tok} greedy tokens of qwen35_forward_token (restated) at positions "
+                                f"{start + 1}..{start + n_tok}, 2B shape, Q8_0, {threads} threads for the GEMVs")
         seq.close()
         om.close()
     return res
@@ -290,7 +497,10 @@ def main():
     if rc != 0:
         raise SystemExit(f"no gfx950 device: {anehip.lib().anehip_last_error(None).decode()}")
     if args.decode_only:
-        pts = [tuple(int(v) for v in p.split(":")) for p in args.decode_only.split(",")]
+        pts = []
+        for p in args.decode_only.split(","):
+            v = [int(t) for t in p.split(":")]
+            pts.append((v[0], v[1], v[2] if len(v) > 2 else v[1]))
         print(json.dumps({"decode": bench_decode(anehip, args.decode_steps, 3, pts)}), flush=True)
         return
     if args.prefill_only:
@@ -298,6 +508,28 @@ def main():
                                                  prefill_tokens=args.prefill_only)}), flush=True)
         return
     ctx = anehip.Context(0)
+    if args.deltanet_only:
+        print(json.dumps({"configs3_deltanet": bench_deltanet(anehip, ctx)}), flush=True)
+        ctx.close()
+        return
+    if args.profile_c0:
+        c0 = Shape(anehip, ctx, 6144, 2048, 100)
+        t = time_point(ctx, c0, 1, 40)
+        print(json.dumps({"c0_us": round(t * 1e3, 3), "floor": c0_floor(ctx, c0)}), flush=True)
+        ctx.close()
+        return
+    if args.profile_points:
+        res = {}
+        for p in args.profile_points.split(","):
+            shape, batch = p.split(":")
+            m, n = (int(v) for v in shape.split("x"))
+            s = Shape(anehip, ctx, m, n, 100)
+            t = time_point(ctx, s, int(batch), max(s.copies, 20))
+            res[p] = {"us": round(t * 1e3, 2), "GB/s": round(algo_bytes(m, n, int(batch)) / (t * 1e-3) / 1e9, 1)}
+            s.free()
+        print(json.dumps(res), flush=True)
+        ctx.close()
+        return
     if args.profile_kernel:
         lm = Shape(anehip, ctx, 151936, 2048, 102)
         t = time_point(ctx, lm, 1, args.steps)
@@ -381,6 +613,10 @@ def main():
         "sweep_points": points,
         "gguf_layout_points": gguf_points,
     }
+    out["c0_gemv_6144x2048"]["floor"] = c0_floor(ctx, shapes[0])
+    out["c0_gemv_6144x2048"]["pct_of_floor"] = round(100 * out["c0_gemv_6144x2048"]["floor"]["best_us"] / c0["us"], 1)
+    out["configs2_q4"] = bench_q4(anehip, ctx)
+    out["configs3_deltanet"] = bench_deltanet(anehip, ctx)
     if not args.no_decode:
         out["decode"] = bench_decode(anehip, args.decode_steps, 3, prefill_tokens=512)
     if not args.no_cpu:

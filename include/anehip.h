@@ -286,6 +286,18 @@ int anehip_fill_random(anehip_ctx *ctx, void *dptr, size_t n, uint32_t dist, uin
                        float a, float b);
 int anehip_quantize(anehip_ctx *ctx, uint32_t ggml_type, const float *w, uint32_t m, uint32_t n, void *out);
 
+/* Roofline probes (no counterpart in the reference; the measured floor for a
+ * bandwidth-bound launch of a given size and grid): anehip_probe_read streams
+ * nbytes (a positive multiple of 16) from device memory src in 16-byte loads
+ * on workgroups x threads threads (threads a multiple of 64, at most 1024),
+ * depth (1, 2, 4 or 8) loads in flight per thread; sink (device, at least
+ * workgroups * threads * 4 bytes) is written only in the unlikely case that
+ * a thread's XOR of its loads equals a fixed constant.  anehip_probe_empty
+ * launches an empty kernel of that grid. */
+int anehip_probe_read(anehip_ctx *ctx, const void *src, size_t nbytes, uint32_t workgroups, uint32_t threads,
+                      uint32_t depth, void *sink);
+int anehip_probe_empty(anehip_ctx *ctx, uint32_t workgroups, uint32_t threads);
+
 /* ---- model-level decode step (context created with a model desc) -------- */
 
 /* Uploads one quantised tensor (host bytes, copied).  Checks ggml_type, the

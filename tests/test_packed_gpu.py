@@ -91,6 +91,36 @@ def test_packed_gemv_parity(gpu_ctx, oracle_lib, t, m, n):
 
 
 @pytest.mark.gpu
+def test_packed_gemv_back_to_back_splits(gpu_ctx, oracle_lib):
+    """K-split GEMVs finish in one launch (the last split of each row tile sums
+    the partials and resets the tile's counter): calls queued back to back on
+    matrices of different tile and split counts, each input used twice, all
+    match the oracle."""
+    t = 8
+    cases = []
+    for i, (m, n) in enumerate([(6144, 2048), (2048, 6144), (100, 2048), (6144, 2048), (2048, 2048)]):
+        w = oracle_lib.gen_quant(t, 90 + i, 91, m, n, std=0.02)
+        dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
+        xs = [oracle_lib.normal(92 + i, r, n) for r in range(2)]
+        dxs = [gpu_ctx.to_device(x) for x in xs]
+        dys = [gpu_ctx.alloc(m * 4) for _ in range(4)]
+        cases.append((m, n, w, dw, dp, xs, dxs, dys))
+    for rep in range(2):
+        for m, n, w, dw, dp, xs, dxs, dys in cases:
+            for r in range(2):
+                gpu_ctx.call("quant_gemv_packed", t, dp, m, n, dxs[r], dys[2 * rep + r])
+    for m, n, w, dw, dp, xs, dxs, dys in cases:
+        for rep in range(2):
+            for r in range(2):
+                y = dys[2 * rep + r].download(np.float32, m)
+                l2, mx = rel_errs(y, oracle_lib.gemv(t, w, m, n, xs[r]))
+                assert l2 <= TOL and mx <= TOL, (m, n, rep, r, l2, mx)
+        assert np.array_equal(dys[0].download(np.float32, m), dys[2].download(np.float32, m))
+        for b in [dw, dp, *dxs, *dys]:
+            b.free()
+
+
+@pytest.mark.gpu
 def test_packed_rejects_bad_shapes(gpu_ctx, anehip_mod):
     d = gpu_ctx.alloc(17 * 1024)
     with pytest.raises(anehip_mod.AnehipError) as e:
