@@ -199,6 +199,9 @@ int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, 
 size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
 int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
                   void *dst);
+// The inverse of launch_repack: panel bytes back to GGUF blocks (rows < m).
+int launch_unpack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
+                  void *dst);
 // Input planes of the panel MFMA GEMM (batch 2..32): fp16 hi / lo planes of
 // x in "fragment order", 32 rows (batch entries) x n columns per plane.
 // Element (b, c) lies in the 1 KiB block of its 16-column step c / 16, at the
@@ -384,10 +387,13 @@ int launch_silu_mul(anehip_ctx *ctx, hipStream_t s, float *a, const float *b, si
 int launch_residual_add(anehip_ctx *ctx, hipStream_t s, float *x, const float *y, size_t n);
 size_t argmax_workspace_bytes(int rows);
 // Greedy argmax of each row's n logits (f32::total_cmp order; equal keys:
-// the last index, as Iterator::max_by) into out; with pos, row r's position
-// pos[r] is also advanced by one.
+// the last index, as Iterator::max_by) into out (and next, if given: the
+// next step's input tokens); with pos, row r's position pos[r] is also
+// advanced by one, after the token is recorded at hist[r * hist_stride +
+// pos[r]] (if hist is given and pos[r] < hist_stride).
 int launch_argmax(anehip_ctx *ctx, hipStream_t s, int rows, uint32_t n, const float *logits, void *ws,
-                  uint32_t *out, uint32_t *pos = nullptr);
+                  uint32_t *out, uint32_t *pos = nullptr, uint32_t *next = nullptr, uint32_t *hist = nullptr,
+                  uint32_t hist_stride = 0);
 
 // Host helper: inv_freq[p] = 1 / base^(2p / head_dim), the
 // reference's formula (deltanet.rs:601-603) evaluated once on the host.

@@ -39,10 +39,15 @@ constexpr uint32_t kHd = 256;
 // A quantised matrix: GGUF blocks (d, as uploaded) and, once a step has run,
 // its panel copy (p) that the step's GEMV / GEMM kernels read; `stale` marks
 // a panel copy that has to be rebuilt from d before the next step.
+// A stacked quantised matrix: d = GGUF blocks (as uploaded), p = the panel
+// copy the step reads.  d is freed once p is built, unless a caller holds a
+// pointer into it (anehip_tensor_ptr: keep); it is rebuilt from p by the
+// inverse permutation when a later upload or tensor_ptr needs it.
 struct QMat {
     void *d = nullptr, *p = nullptr;
     uint32_t type = 0, rows = 0, cols = 0;
     bool stale = true;
+    bool keep = false;
 };
 
 struct Layer {
@@ -72,6 +77,8 @@ struct Model {
     uint32_t batch = 0, max_seq = 0;
     std::vector<uint32_t> host_pos;
     uint32_t *d_pos = nullptr, *d_tokens = nullptr, *d_sampled = nullptr;
+    // sampled tokens by (sequence, position of the step's input): [batch][max_seq]
+    uint32_t *d_hist = nullptr;
     uint32_t *h_tokens = nullptr;  // pinned staging
     // scratch
     float *x0 = nullptr, *x1 = nullptr;                  // residual stream (two buffers, alternating)
@@ -144,7 +151,7 @@ void free_state(Model *M) {
         L.conv_state = L.S = nullptr;
         L.kc = L.vc = nullptr;
     }
-    void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->x0,       M->x1,        M->pmix,      M->p0,
+    void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->d_hist, M->x0,       M->x1,        M->pmix,      M->p0,
                     M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->xin};
     for (void *p : bufs) free_ptr(p);
     void *pfb[] = {M->pf.x, M->pf.xn, M->pf.pmix, M->pf.p0, M->pf.p1, M->pf.attn_part, M->pf.logits, M->pf.xin,
@@ -155,7 +162,7 @@ void free_state(Model *M) {
     if (M->pf_stage) (void)hipHostFree(M->pf_stage);
     M->pf_stage = nullptr;
     M->pf_stage_chunks = 0;
-    M->d_pos = M->d_tokens = M->d_sampled = M->h_tokens = nullptr;
+    M->d_pos = M->d_tokens = M->d_sampled = M->d_hist = M->h_tokens = nullptr;
     M->x0 = M->x1 = M->pmix = M->p0 = M->p1 = M->heads = M->attn_out = M->logits = M->attn_part = nullptr;
     M->xin = nullptr;
     M->argmax_ws = nullptr;
@@ -484,9 +491,11 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
 // the projections, greedy argmax of the logits and the position advance.
 int enqueue_step(anehip_ctx *ctx, Model *M, hipStream_t s) {
     TRY(M->batch == 1 ? enqueue_step_b1(ctx, M, s) : enqueue_step_bn(ctx, M, s));
-    // greedy argmax, and each sequence's position advanced by the same kernel
+    // greedy argmax: the sampled tokens also become the next step's input
+    // (greedy feedback on device) and are recorded by position; each
+    // sequence's position is advanced by the same kernel
     return launch_argmax(ctx, s, (int)M->batch, M->desc.vocab_size, M->logits, M->argmax_ws, M->d_sampled,
-                         M->d_pos);
+                         M->d_pos, M->d_tokens, M->d_hist, M->max_seq);
 }
 
 // Largest K-split partial buffer any GEMM of the step needs.
@@ -527,6 +536,37 @@ int pack_mat(anehip_ctx *ctx, QMat &Q) {
     }
     TRY(launch_repack(ctx, ctx->stream, Q.type, Q.d, Q.rows, Q.cols, Q.p));
     Q.stale = false;
+    if (!Q.keep) {
+        // the panel copy is the only one the step reads: drop the GGUF copy
+        // (not while the stream is being captured: the free would wait on it)
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        ANEHIP_HIP_TRY(ctx->err, hipStreamIsCapturing(ctx->stream, &cs));
+        if (cs == hipStreamCaptureStatusNone) {
+            ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+            ANEHIP_HIP_TRY(ctx->err, hipFree(Q.d));
+            Q.d = nullptr;
+        }
+    }
+    return ANEHIP_OK;
+}
+
+// Makes Q's GGUF copy exist (allocated for total_rows x cols of ggml_type,
+// or rebuilt from the panel copy if it was dropped after packing).
+int gguf_copy(anehip_ctx *ctx, QMat &Q, uint32_t ggml_type, uint32_t total_rows, uint32_t cols, const char *who) {
+    if (Q.d) return ANEHIP_OK;
+    const size_t bytes = (size_t)total_rows * qrow_bytes(ggml_type, cols);
+    if (hipMalloc(&Q.d, bytes) != hipSuccess) {
+        Q.d = nullptr;
+        return set_error(ctx->err, ANEHIP_ENOMEM, "%s: cannot allocate %zu bytes", who, bytes);
+    }
+    if (Q.p) {
+        TRY(launch_unpack(ctx, ctx->stream, Q.type, Q.p, Q.rows, Q.cols, Q.d));
+        ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    } else {
+        Q.type = ggml_type;
+        Q.rows = total_rows;
+        Q.cols = cols;
+    }
     return ANEHIP_OK;
 }
 
@@ -811,20 +851,11 @@ int anehip_upload_quant(anehip_ctx *ctx, int32_t layer, uint32_t kind, const uin
                          kind_name(kind), layer, ks.rows, ks.cols, m, n);
     QSlot slot = quant_slot(M, layer, kind);
     QMat &Q = *slot.mat;
-    if (Q.d && Q.type != ggml_type)
+    if ((Q.d || Q.p) && Q.type != ggml_type)
         return set_error(ctx->err, ANEHIP_EUNSUPPORTED,
                          "upload_quant: %s of layer %d is type %u but its stacked matrix holds type %u",
                          kind_name(kind), layer, ggml_type, Q.type);
-    if (!Q.d) {
-        const size_t bytes = (size_t)slot.total_rows * qrow_bytes(ggml_type, n);
-        if (hipMalloc(&Q.d, bytes) != hipSuccess) {
-            Q.d = nullptr;
-            return set_error(ctx->err, ANEHIP_ENOMEM, "upload_quant: cannot allocate %zu bytes", bytes);
-        }
-        Q.type = ggml_type;
-        Q.rows = slot.total_rows;
-        Q.cols = n;
-    }
+    TRY(gguf_copy(ctx, Q, ggml_type, slot.total_rows, n, "upload_quant"));
     char *dst = static_cast<char *>(Q.d) + (size_t)slot.row_off * qrow_bytes(ggml_type, n);
     ANEHIP_HIP_TRY(ctx->err, hipMemcpy(dst, blocks, nbytes, hipMemcpyHostToDevice));
     Q.stale = true;
@@ -873,19 +904,11 @@ int anehip_tensor_ptr(anehip_ctx *ctx, int32_t layer, uint32_t kind, uint32_t gg
             return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "tensor_ptr: ggml type %u", ggml_type);
         QSlot slot = quant_slot(M, layer, kind);
         QMat &Q = *slot.mat;
-        if (Q.d && Q.type != ggml_type)
+        if ((Q.d || Q.p) && Q.type != ggml_type)
             return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "tensor_ptr: stacked matrix of %s holds type %u",
                              kind_name(kind), Q.type);
-        if (!Q.d) {
-            const size_t bytes = (size_t)slot.total_rows * qrow_bytes(ggml_type, ks.cols);
-            if (hipMalloc(&Q.d, bytes) != hipSuccess) {
-                Q.d = nullptr;
-                return set_error(ctx->err, ANEHIP_ENOMEM, "tensor_ptr: cannot allocate %zu bytes", bytes);
-            }
-            Q.type = ggml_type;
-            Q.rows = slot.total_rows;
-            Q.cols = ks.cols;
-        }
+        TRY(gguf_copy(ctx, Q, ggml_type, slot.total_rows, ks.cols, "tensor_ptr"));
+        Q.keep = true;  // the caller may read or write through *dptr at any time
         *dptr = static_cast<char *>(Q.d) + (size_t)slot.row_off * qrow_bytes(ggml_type, ks.cols);
         Q.stale = true;  // writes through *dptr reach the step's panel copy at the next step
         *nbytes = (size_t)ks.rows * qrow_bytes(ggml_type, ks.cols);
@@ -950,6 +973,7 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     r = r ? r : alloc((void **)&M->d_pos, 64 * sizeof(uint32_t));
     r = r ? r : alloc((void **)&M->d_tokens, 64 * sizeof(uint32_t));
     r = r ? r : alloc((void **)&M->d_sampled, 64 * sizeof(uint32_t));
+    r = r ? r : alloc((void **)&M->d_hist, (size_t)batch * max_seq * sizeof(uint32_t));
     r = r ? r : alloc((void **)&M->x0, batch * d * sizeof(float));
     r = r ? r : alloc((void **)&M->x1, batch * d * sizeof(float));
     r = r ? r : alloc((void **)&M->pmix, M->part_len * sizeof(float));
@@ -1187,25 +1211,23 @@ int anehip_generate(anehip_ctx *ctx, const uint32_t *first_tokens, uint32_t batc
             return set_error(ctx->err, ANEHIP_ERANGE, "generate: sequence %u at pos %u + %u steps > capacity %u", b,
                              M->host_pos[b], steps, M->max_seq);
     if ((rc = stage_tokens(ctx, M, first_tokens, batch))) return rc;
-    uint32_t *d_out = nullptr;
-    ANEHIP_HIP_TRY(ctx->err, hipMallocAsync((void **)&d_out, (size_t)steps * batch * sizeof(uint32_t), ctx->stream));
+    // each step's argmax feeds its tokens to the next step and records them
+    // at the sequence's position (d_hist), all inside the step: nothing is
+    // enqueued between steps
+    const std::vector<uint32_t> start(M->host_pos.begin(), M->host_pos.begin() + batch);
     for (uint32_t i = 0; i < steps; i++) {
         if ((rc = launch_step(ctx, M))) break;
-        // greedy feedback: the sampled tokens are the next step's input, on device
-        if (hipMemcpyAsync(M->d_tokens, M->d_sampled, batch * sizeof(uint32_t), hipMemcpyDeviceToDevice,
-                           ctx->stream) != hipSuccess ||
-            hipMemcpyAsync(d_out + (size_t)i * batch, M->d_sampled, batch * sizeof(uint32_t),
-                           hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess) {
-            rc = set_error(ctx->err, ANEHIP_EHIP, "generate: device copy failed");
-            break;
-        }
         for (uint32_t b = 0; b < batch; b++) M->host_pos[b]++;
     }
-    if (!rc && hipMemcpyAsync(out_tokens, d_out, (size_t)steps * batch * sizeof(uint32_t), hipMemcpyDeviceToHost,
-                              ctx->stream) != hipSuccess)
-        rc = set_error(ctx->err, ANEHIP_EHIP, "generate: copy-out failed");
-    (void)hipFreeAsync(d_out, ctx->stream);
+    std::vector<uint32_t> hist(rc ? 0 : (size_t)batch * steps);
+    for (uint32_t b = 0; b < batch && !rc; b++)
+        if (hipMemcpyAsync(hist.data() + (size_t)b * steps, M->d_hist + (size_t)b * M->max_seq + start[b],
+                           (size_t)steps * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
+            rc = set_error(ctx->err, ANEHIP_EHIP, "generate: copy-out failed");
     ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
+    if (!rc)
+        for (uint32_t i = 0; i < steps; i++)
+            for (uint32_t b = 0; b < batch; b++) out_tokens[(size_t)i * batch + b] = hist[(size_t)b * steps + i];
     return rc;
 }
 

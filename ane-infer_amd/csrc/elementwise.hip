@@ -343,7 +343,9 @@ __global__ __launch_bounds__(kThreads) void argmax_stage1(const float *__restric
 // stage 2: one wave per row; with `pos`, row b's position is advanced too
 // (the decode step's last operation, folded in to save a kernel boundary).
 __global__ __launch_bounds__(64) void argmax_stage2(const int32_t *__restrict__ pk, const uint32_t *__restrict__ pi,
-                                                    uint32_t *__restrict__ out, uint32_t *__restrict__ pos) {
+                                                    uint32_t *__restrict__ out, uint32_t *__restrict__ pos,
+                                                    uint32_t *__restrict__ next, uint32_t *__restrict__ hist,
+                                                    uint32_t hist_stride) {
     const size_t b = blockIdx.x;
     int32_t k = pk[b * kArgBlocks + threadIdx.x];
     uint32_t i = pi[b * kArgBlocks + threadIdx.x];
@@ -355,7 +357,12 @@ __global__ __launch_bounds__(64) void argmax_stage2(const int32_t *__restrict__ 
     }
     if (threadIdx.x == 0) {
         out[b] = i;
-        if (pos) pos[b] += 1u;
+        if (next) next[b] = i;
+        if (pos) {
+            const uint32_t p = pos[b];
+            if (hist && p < hist_stride) hist[b * hist_stride + p] = i;
+            pos[b] = p + 1u;
+        }
     }
 }
 
@@ -442,12 +449,12 @@ size_t argmax_workspace_bytes(int rows) { return (size_t)rows * kArgBlocks * 8; 
 
 // ws: argmax_workspace_bytes(rows) bytes of device memory.
 int launch_argmax(anehip_ctx *ctx, hipStream_t s, int rows, uint32_t n, const float *logits, void *ws,
-                  uint32_t *out, uint32_t *pos) {
+                  uint32_t *out, uint32_t *pos, uint32_t *next, uint32_t *hist, uint32_t hist_stride) {
     int32_t *pk = static_cast<int32_t *>(ws);
     uint32_t *pi = reinterpret_cast<uint32_t *>(pk + (size_t)rows * kArgBlocks);
     hipLaunchKernelGGL(argmax_stage1, dim3(kArgBlocks, rows), dim3(kThreads), 0, s, logits, n, pk, pi);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-    hipLaunchKernelGGL(argmax_stage2, dim3(rows), dim3(64), 0, s, pk, pi, out, pos);
+    hipLaunchKernelGGL(argmax_stage2, dim3(rows), dim3(64), 0, s, pk, pi, out, pos, next, hist, hist_stride);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

@@ -407,6 +407,37 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     reinterpret_cast<u32x4 *>(dst)[v] = w;
 }
 
+// The inverse permutation: one thread per 16-byte vector of the panel
+// buffer scatters its bytes back to their GGUF positions (rows < m; the
+// padding rows of the last tile hold zeros and have no GGUF position).
+template <uint32_t T>
+__global__ __launch_bounds__(256) void unpack_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                    int m, int n, size_t nvec) {
+    const size_t v = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (v >= nvec) return;
+    constexpr int BB = QTraits<T>::kBlockBytes;
+    const int nsb = n >> 8;
+    const size_t panel = v / (Panel<T>::kBytes / 16);
+    const int within = (int)(v % (Panel<T>::kBytes / 16));
+    const int tile = (int)(panel / nsb), sb = (int)(panel % nsb);
+    const int chunk = within / 64, r = within % 64;
+    const int row = tile * 64 + r;
+    if (row >= m) return;
+    const u32x4 w = reinterpret_cast<const u32x4 *>(src)[v];
+    const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
+    const size_t row_off = (size_t)row * (n / 32) * BB;
+    for (int i = 0; i < 16; i++) {
+        const uint8_t b = (uint8_t)(w4[i >> 2] >> (8 * (i & 3)));
+        if (chunk < Panel<T>::kChunks) {
+            const int blk = T == ANEHIP_GGML_Q8_0 ? chunk / 2 : chunk;
+            const int q0 = T == ANEHIP_GGML_Q8_0 ? 2 + 16 * (chunk & 1) : 2;
+            dst[row_off + (size_t)(sb * 8 + blk) * BB + q0 + i] = b;
+        } else {
+            dst[row_off + (size_t)(sb * 8 + i / 2) * BB + (i & 1)] = b;
+        }
+    }
+}
+
 // A wave's share of a panel: blocks [NB * part, NB * (part + 1)) of the 8,
 // i.e. kChunks * NB / 8 quant vectors, plus the panel's scale vector.
 template <uint32_t T, int NB>
@@ -2464,6 +2495,20 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
         launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xp, batch, out, ksplit, per);
     else
         launch_gemm_packed_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xp, batch, out, ksplit, per);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_unpack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
+                  void *dst) {
+    const size_t nvec = packed_bytes(ggml_type, m, n) / 16;
+    const unsigned grid = (unsigned)((nvec + 255) / 256);
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        hipLaunchKernelGGL(unpack_kernel<ANEHIP_GGML_Q8_0>, dim3(grid), dim3(256), 0, stream,
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec);
+    else
+        hipLaunchKernelGGL(unpack_kernel<ANEHIP_GGML_Q4_0>, dim3(grid), dim3(256), 0, stream,
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

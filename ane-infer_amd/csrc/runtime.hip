@@ -170,6 +170,12 @@ int anehip_d2h(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes) {
 int anehip_dev_memset(anehip_ctx *ctx, void *dst, int value, size_t nbytes) {
     if (!ctx || (!dst && nbytes)) return set_error(ctx ? ctx->err : global_error(), ANEHIP_EINVAL, "memset: bad argument");
     if (!nbytes) return ANEHIP_OK;
+    // a memset node recorded into a graph is refused (a fill kernel is the
+    // capturable way to clear memory)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    ANEHIP_HIP_TRY(ctx->err, hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return set_error(ctx->err, ANEHIP_ESTATE, "memset: not allowed while the stream is being captured");
     ANEHIP_HIP_TRY(ctx->err, hipMemsetAsync(dst, value, nbytes, ctx->stream));
     return ANEHIP_OK;
 }

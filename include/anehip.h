@@ -137,6 +137,8 @@ int anehip_dev_alloc(anehip_ctx *ctx, size_t nbytes, void **dptr);
 int anehip_dev_free(anehip_ctx *ctx, void *dptr);
 int anehip_h2d(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes);
 int anehip_d2h(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes);
+/* anehip_dev_memset enqueues on the context stream; it returns ANEHIP_ESTATE
+ * while that stream is being captured (no memset nodes in graphs). */
 int anehip_dev_memset(anehip_ctx *ctx, void *dst, int value, size_t nbytes);
 int anehip_d2d(anehip_ctx *ctx, void *dst, const void *src, size_t nbytes);
 

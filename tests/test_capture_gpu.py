@@ -66,3 +66,17 @@ def test_workspace_growth_refused_during_capture(oracle_lib, anehip_mod):
         ctx.sync()
     finally:
         ctx.close()
+
+
+def test_memset_refused_during_capture(gpu_ctx, anehip_mod):
+    ctx = gpu_ctx
+    buf = ctx.alloc(4096)
+    ctx.capture_begin()
+    with pytest.raises(anehip_mod.AnehipError) as e:
+        ctx.call("dev_memset", buf, 0, 4096)
+    assert e.value.code == -6 and "captur" in str(e.value)
+    g = ctx.capture_end()
+    ctx.graph_destroy(g)
+    ctx.call("dev_memset", buf, 0, 4096)
+    ctx.sync()
+    buf.free()

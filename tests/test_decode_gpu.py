@@ -241,6 +241,62 @@ def test_generate_feeds_back_on_device(small_host):
     gm2.close()
 
 
+def test_generate_ragged_positions_and_continuation(small_host):
+    """Greedy feedback and the token record stay inside the step graph: from
+    ragged start positions, one generate of 10 steps equals generate(4) +
+    generate(6) continued from the last sampled tokens, and equals stepping
+    one token at a time."""
+    def fresh():
+        gm = _model(small_host, 3, 48)
+        for b, p in enumerate((0, 5, 17)):
+            gm.set_pos(b, p)
+        return gm
+
+    first = [3, 7, 11]
+    gm = fresh()
+    out = gm.generate(first, 10)
+    assert [gm.get_pos(b) for b in range(3)] == [10, 15, 27]
+    gm2 = fresh()
+    a = gm2.generate(first, 4)
+    b = gm2.generate(a[-1], 6)
+    assert np.array_equal(np.concatenate([a, b]), out)
+    gm3 = fresh()
+    tok = np.array(first, np.uint32)
+    for i in range(10):
+        gm3.step(tok, want_logits=False)
+        tok = gm3.sampled()
+        assert np.array_equal(out[i], tok), i
+    for g in (gm, gm2, gm3):
+        g.close()
+
+
+def test_gguf_copy_dropped_and_rebuilt(small_host):
+    """After the first step the GGUF copy of each matrix is dropped (the step
+    reads the panel copy); re-uploading one part of a stacked matrix rebuilds
+    it from the panels (the inverse permutation) and the step then matches a
+    model uploaded with the new part from the start; a tensor read back after
+    the drop equals what was uploaded."""
+    T = anehip.T
+    s = small_host.spec
+    rows, cols, _ = s.shapes(0)[T["FFN_UP"]]
+    new_up = oracle.gen_quant(8, 77, 78, rows, cols, std=anehip.WEIGHT_STD)
+    gm = _model(small_host, 1, 16)
+    gm.step([1], want_logits=False)  # packs the weights, drops the GGUF copies
+    got = gm.download_tensor(0, T["FFN_GATE"])
+    assert np.array_equal(got, small_host.tensors[(0, T["FFN_GATE"])][0])
+    gm.upload_quant(0, T["FFN_UP"], new_up, rows, cols)
+    gm.reset_state()
+    y = gm.step([2])
+    ref = anehip.Model(s)
+    small_host.upload(ref)
+    ref.upload_quant(0, T["FFN_UP"], new_up, rows, cols)
+    ref.alloc_state(1, 16)
+    y_ref = ref.step([2])
+    assert np.array_equal(y, y_ref)
+    gm.close()
+    ref.close()
+
+
 def test_errors(small_host):
     gm = anehip.Model(small_host.spec)
     with pytest.raises(anehip.AnehipError) as e:
