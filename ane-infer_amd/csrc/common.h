@@ -251,6 +251,33 @@ __device__ __forceinline__ void split_scaled(float v, int e, _Float16 &hi, _Floa
     hi = (_Float16)s;
     lo = (_Float16)(s - (float)hi);
 }
+// Cross-lane sums on DPP (VALU, no LDS round trip).  Each step adds a lane's
+// value to its partner's, and partners get the same two operands, so every
+// lane of a group ends with the same bits.  All lanes of the wave must be
+// active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf,
+                                                                     false));
+}
+// sum over each group of 8 lanes: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror
+__device__ __forceinline__ float sum8(float v) { return dpp_add<0x141>(dpp_add<0x4E>(dpp_add<0xB1>(v))); }
+// sum over each 16-lane row: row_ror 8, 4, 2, 1
+__device__ __forceinline__ float row_sum16(float v) {
+    return dpp_add<0x121>(dpp_add<0x122>(dpp_add<0x124>(dpp_add<0x128>(v))));
+}
+// sum over the wave (the 4 row sums added through readlane; wave-uniform)
+__device__ __forceinline__ float wave_sum(float v) {
+    const int b = __builtin_bit_cast(int, row_sum16(v));
+    const auto row = [&](int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, lane)); };
+    return (row(0) + row(16)) + (row(32) + row(48));
+}
+// sum over each 32-lane half of the wave
+__device__ __forceinline__ float half_sum(float v) {
+    const int b = __builtin_bit_cast(int, row_sum16(v));
+    const auto row = [&](int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, lane)); };
+    return (threadIdx.x & 32) ? row(32) + row(48) : row(0) + row(16);
+}
 // Lane maxima on DPP (VALU, no LDS round trip).  dpp_max<CTRL>: the max of a
 // lane's value and its DPP partner's; row_max16: every lane gets the max of
 // its 16-lane row (xor 1, xor 2 by quad_perm, then row_half_mirror and

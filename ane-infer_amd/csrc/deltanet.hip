@@ -34,26 +34,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float silu_ref(float x) { return x / (1.0f + expf(-x)); }
 
-// Cross-lane sums on DPP (VALU, no LDS round trip).  Each step adds a lane's
-// value to its partner's, and partners get the same two operands, so every
-// lane of a group ends with the same bits.
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float v) {
-    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf,
-                                                                     false));
-}
-// sum over each group of 8 lanes: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror
-__device__ __forceinline__ float sum8(float v) { return dpp_add<0x141>(dpp_add<0x4E>(dpp_add<0xB1>(v))); }
-// sum over the wave: row_ror 8, 4, 2, 1 sums each 16-lane row, then the 4 rows
-__device__ __forceinline__ float wave_sum(float v) {
-    v = dpp_add<0x128>(v);
-    v = dpp_add<0x124>(v);
-    v = dpp_add<0x122>(v);
-    v = dpp_add<0x121>(v);
-    const int b = __builtin_bit_cast(int, v);
-    const auto row = [&](int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, lane)); };
-    return (row(0) + row(16)) + (row(32) + row(48));
-}
 
 // Range-safe plane write (see Planes) of one head's gated-norm output: a
 // head is one 128-column group, column c0 + t held by thread t < 128.  The

@@ -133,17 +133,11 @@ __device__ __forceinline__ void wave_sync_lds() {
 
 constexpr int kWavesPerWg = 4;
 
-__device__ __forceinline__ float wave_sum64(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
 // Sum over an NT-thread workgroup (red: NT / 64 floats of LDS); every thread
 // gets the total.
 template <int NT = 256>
 __device__ __forceinline__ float wg_sum(float v, float *red) {
-    v = wave_sum64(v);
+    v = wave_sum(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -180,8 +174,8 @@ __device__ __forceinline__ float sum_parts(const float *__restrict__ part, int k
 // `first` is false when a workgroup forms a second slice of the same input in
 // one launch: the one-off side effects (the x_out copy, the conv-window
 // commit) are then skipped.
-template <int KP, int NT, class Issue>
-__device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, float *xs, Issue &&issue);
+template <int KP, int NT, class Issue, class Store>
+__device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, Issue &&issue, Store &&store);
 
 template <int MODE, int RB = 8, int NT = 256>
 __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0, int len, float *xs, float *red,
@@ -212,7 +206,9 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
         }
     } else if constexpr (MODE == GEMV_IN_ATTN_COMBINE) {
         // one head per slice (the launcher checks that each split is one panel)
-        attn_combine_slice<kMaxSplit, NT>(in, c0, xs, [] {});
+        attn_combine_slice<kMaxSplit, NT>(in, c0, [] {}, [&](float4 v, int i4, bool ok) {
+            if (ok) reinterpret_cast<float4 *>(xs)[i4] = v;
+        });
     } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
         // deltanet.rs:517-533, per 128-wide head; a wave handles whole heads
         constexpr int W = NT / 64;                      // waves
@@ -234,7 +230,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
 #pragma unroll
             for (int i = 0; i < HB; i++) {
                 const int hh = wave + W * (i0 + i);
-                const float ss = wave_sum64(a[i] * a[i] + b[i] * b[i]);
+                const float ss = wave_sum(a[i] * a[i] + b[i] * b[i]);
                 if (hh < nh) {
                     const float inv_rms = 1.0f / sqrtf(ss / 128.0f + in.eps);
                     xs[hh * 128 + lane] = ((a[i] * inv_rms) * in.w[lane]) * (ga[i] / (1.0f + expf(-ga[i])));
@@ -460,13 +456,145 @@ __device__ __forceinline__ void load_part(u32x4 *q, u32x4 &sc, const uint8_t *pa
     sc = __builtin_nontemporal_load(p4 + Panel<T>::kChunks * 64 + l);
 }
 
+// ---------------------------------------------------------------------------
+// Batch-1 GEMV input as int8 digits.  Each 32-column block of the input slice
+// is held in LDS as x = 2^-sh (d0 + d1 / 128 + d2 / 16384) + e, with int8
+// digits d0 = trunc(x 2^sh), d1 = trunc(frac 128), d2 = rint(frac' 128), and
+// sh per block from its largest magnitude M (M 2^sh in [64, 128)), so |e| <=
+// 2^-21 M.  A block's sum q . x (q8_gemv.rs:234-242: per block, then scaled
+// by d) is then three exact int32 dot products over the int8 weights
+// (v_dot4_i32_i8, 4 products per instruction) combined in fp32: about half
+// the VALU work of one conversion and one FMA per weight, which was a third of
+// the busy time of the large batch-1 GEMVs.  The result differs from the
+// per-element fp32 sum by rounding only (both are within ~2^-21 of the exact
+// sum relative to max|x| |q|).
+// LDS per block: kXdWords dwords (digit planes 0, 1, 2; byte i of dword w is
+// column 4 w + i) and a uint4 {2^-sh as float bits, 8 sum(d0), 8 sum(d1),
+// 8 sum(d2)} (the sums serve Q4_0's -8 offset).  A block holding an inf or NaN
+// gets zero digits and a NaN factor, so its rows come out NaN.
+// ---------------------------------------------------------------------------
+constexpr int kXdWords = 24;
+
+// Digitises 4 consecutive columns v of the slice (float4 index i4); lanes
+// 8 k .. 8 k + 7 of the wave must hold one block (i4 & 7 = lane & 7).  Every
+// lane of the wave calls it (DPP needs all lanes active); only `store` lanes
+// write.
+template <int CTRL>
+__device__ __forceinline__ int dpp_iadd(int v) {
+    return v + __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void put_digits(float4 v, int i4, bool store, uint32_t *xd, uint4 *xq) {
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) mx = fmaxf(mx, __builtin_isnan(xv[i]) ? INFINITY : fabsf(xv[i]));
+    // the block's maximum over its 8 lanes on DPP (xor 1, xor 2, half-row mirror)
+    mx = dpp_max<0x141>(dpp_max<0x4E>(dpp_max<0xB1>(mx)));
+    const bool bad = mx == INFINITY;  // an inf or NaN in the block
+    // mx in [2^(e-1), 2^e): mx 2^(7-e) in [64, 128); the smallest subnormals
+    // keep sh at 149 so that 2^-sh stays representable
+    const int sh = bad || mx == 0.0f ? 0 : min(7 - __builtin_amdgcn_frexp_expf(mx), 149);
+    uint32_t p0 = 0, p1 = 0, p2 = 0;
+    int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float y = bad ? 0.0f : ldexpf(xv[i], sh);  // |y| < 128
+        const float f0 = truncf(y);
+        const float r = (y - f0) * 128.0f;  // exact
+        const float f1 = truncf(r);
+        const float f2 = fminf(fmaxf(rintf((r - f1) * 128.0f), -127.0f), 127.0f);
+        const int i0 = (int)f0, i1 = (int)f1, i2 = (int)f2;
+        p0 |= ((uint32_t)i0 & 0xffu) << (8 * i);
+        p1 |= ((uint32_t)i1 & 0xffu) << (8 * i);
+        p2 |= ((uint32_t)i2 & 0xffu) << (8 * i);
+        if constexpr (T == ANEHIP_GGML_Q4_0) {
+            s0 += i0;
+            s1 += i1;
+            s2 += i2;
+        }
+    }
+    if constexpr (T == ANEHIP_GGML_Q4_0) {
+        s0 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s0)));
+        s1 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s1)));
+        s2 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s2)));
+    }
+    if (store) {
+        const int blk = i4 >> 3, w = i4 & 7;
+        uint32_t *p = xd + blk * kXdWords + w;
+        p[0] = p0;
+        p[8] = p1;
+        p[16] = p2;
+        if (w == 0)
+            xq[blk] = make_uint4(__float_as_uint(bad ? __builtin_nanf("") : ldexpf(1.0f, -sh)), (uint32_t)(8 * s0),
+                                 (uint32_t)(8 * s1), (uint32_t)(8 * s2));
+    }
+}
+
+// Digitises xs[0, len) (floats in LDS, len a multiple of 32) into xd / xq;
+// the caller synchronises before and after.
+template <uint32_t T, int NT>
+__device__ __forceinline__ void digitize_lds(const float *xs, int len, uint32_t *xd, uint4 *xq) {
+    const int n4 = len >> 2;
+    for (int b4 = 0; b4 < n4; b4 += NT) {  // uniform trip count
+        const int i4 = b4 + (int)threadIdx.x;
+        const float4 v = reinterpret_cast<const float4 *>(xs)[min(i4, n4 - 1)];
+        put_digits<T>(v, i4, i4 < n4, xd, xq);
+    }
+}
+
+// One block's q . x from its digits, times 2^-sh (q: the block's quant
+// vectors, 2 for Q8_0 with columns 0-15 and 16-31, 1 for Q4_0; xdb: the
+// block's kXdWords digit dwords; xqv: its uint4).
+template <uint32_t T>
+__device__ __forceinline__ float block_dot_digits(const u32x4 *q, const uint32_t *xdb, const uint4 xqv) {
+    const u32x4 *x4 = reinterpret_cast<const u32x4 *>(xdb);
+    const u32x4 a0 = x4[0], b0 = x4[1], a1 = x4[2], b1 = x4[3], a2 = x4[4], b2 = x4[5];
+    const uint32_t d0[8] = {a0.x, a0.y, a0.z, a0.w, b0.x, b0.y, b0.z, b0.w};
+    const uint32_t d1[8] = {a1.x, a1.y, a1.z, a1.w, b1.x, b1.y, b1.z, b1.w};
+    const uint32_t d2[8] = {a2.x, a2.y, a2.z, a2.w, b2.x, b2.y, b2.z, b2.w};
+    int s0 = 0, s1 = 0, s2 = 0;
+    if constexpr (T == ANEHIP_GGML_Q8_0) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t w4[4] = {q[h].x, q[h].y, q[h].z, q[h].w};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                s0 = __builtin_amdgcn_sdot4((int)w4[w], (int)d0[4 * h + w], s0, false);
+                s1 = __builtin_amdgcn_sdot4((int)w4[w], (int)d1[4 * h + w], s1, false);
+                s2 = __builtin_amdgcn_sdot4((int)w4[w], (int)d2[4 * h + w], s2, false);
+            }
+        }
+    } else {
+        // byte i of the block: element i in the low nibble, i + 16 in the high
+        // one (dequant.rs:12-25); nibbles are 0..15, the -8 comes off as 8 sum(d)
+        const uint32_t w4[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const int lo = (int)(w4[w] & 0x0f0f0f0fu), hi = (int)((w4[w] >> 4) & 0x0f0f0f0fu);
+            s0 = __builtin_amdgcn_sdot4(lo, (int)d0[w], s0, false);
+            s1 = __builtin_amdgcn_sdot4(lo, (int)d1[w], s1, false);
+            s2 = __builtin_amdgcn_sdot4(lo, (int)d2[w], s2, false);
+            s0 = __builtin_amdgcn_sdot4(hi, (int)d0[4 + w], s0, false);
+            s1 = __builtin_amdgcn_sdot4(hi, (int)d1[4 + w], s1, false);
+            s2 = __builtin_amdgcn_sdot4(hi, (int)d2[4 + w], s2, false);
+        }
+        s0 -= (int)xqv.y;
+        s1 -= (int)xqv.z;
+        s2 -= (int)xqv.w;
+    }
+    const float bs = fmaf((float)s2, 1.0f / 16384.0f, fmaf((float)s1, 1.0f / 128.0f, (float)s0));
+    return bs * __uint_as_float(xqv.x);
+}
+
 // Dot product of a wave's panel share held in registers (q, sc: see
-// load_part) with x[32 * blk] for its blocks (x: the panel's 256 inputs,
-// wave-uniform, so scalar loads from global memory or broadcast LDS reads):
-// per block, then scaled (q8_gemv.rs:234-242).
+// load_part) with the digits of the panel's 256 inputs (xd, xq: the panel's
+// first block; wave-uniform, so broadcast LDS reads): per block, then scaled
+// by the block's d (q8_gemv.rs:234-242).
 template <uint32_t T, int NB>
-__device__ __forceinline__ float panel_dot(const u32x4 *q, const u32x4 &sc, const float *__restrict__ x, int part,
-                                           float acc) {
+__device__ __forceinline__ float panel_dot(const u32x4 *q, const u32x4 &sc, const uint32_t *xd, const uint4 *xq,
+                                           int part, float acc) {
     const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
     for (int j = 0; j < NB; j++) {
@@ -480,30 +608,8 @@ __device__ __forceinline__ float panel_dot(const u32x4 *q, const u32x4 &sc, cons
             word = wi == 0 ? scw[0] : wi == 1 ? scw[1] : wi == 2 ? scw[2] : scw[3];
         }
         const float d = __half2float(__ushort_as_half((unsigned short)(word >> (16 * (b & 1)))));
-        const float *xb = x + 32 * b;
-        float bs = 0.0f;
-        if constexpr (T == ANEHIP_GGML_Q8_0) {
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const u32x4 v = q[2 * j + h];
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int qi = (int)(int8_t)(w4[i >> 2] >> (8 * (i & 3)));
-                    bs = fmaf((float)qi, xb[16 * h + i], bs);
-                }
-            }
-        } else {
-            const u32x4 v = q[j];
-            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const uint32_t byte = (w4[i >> 2] >> (8 * (i & 3))) & 0xffu;
-                bs = fmaf((float)((int)(byte & 15u) - 8), xb[i], bs);
-                bs = fmaf((float)((int)(byte >> 4) - 8), xb[16 + i], bs);
-            }
-        }
-        acc = fmaf(bs, d, acc);
+        constexpr int VB = T == ANEHIP_GGML_Q8_0 ? 2 : 1;
+        acc = fmaf(block_dot_digits<T>(q + VB * j, xd + b * kXdWords, xq[b]), d, acc);
     }
     return acc;
 }
@@ -522,12 +628,6 @@ __device__ __forceinline__ float panel_dot(const u32x4 *q, const u32x4 &sc, cons
 
 __device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
-
-__device__ __forceinline__ float half_sum32(float v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
 }
 
 __device__ __forceinline__ float silu1(float g) { return g / (1.0f + expf(-g)); }
@@ -561,7 +661,7 @@ __device__ __forceinline__ float4 sum_parts4(const float4 *v, int kp) {
 // floats per workgroup; uniform).
 template <int MODE, int NT>
 __device__ __forceinline__ bool overlapped_ok(const GemvInput &in, int n, int len) {
-    if constexpr (MODE == GEMV_IN_PLAIN) return false;
+    if constexpr (MODE == GEMV_IN_PLAIN) return len <= 4 * NT && ((uintptr_t)in.x & 15) == 0;
     const bool aligned = ((in.part_stride | (size_t)in.gate_off) & 3) == 0;
     if constexpr (MODE == GEMV_IN_RMSNORM || MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_EMBED_RMSNORM)
         return n <= 4 * NT && aligned;
@@ -579,8 +679,8 @@ __device__ __forceinline__ bool overlapped_ok(const GemvInput &in, int n, int le
 // times sigmoid(gate)) into xs[0..256).  The gate and the first 16 chunks are
 // loaded before `issue` starts the weight loads; groups 4.. (threads >= 256)
 // mirror groups 0..3 for those loads, so every address stays in bounds.
-template <int KP, int NT, class Issue>
-__device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, float *xs, Issue &&issue) {
+template <int KP, int NT, class Issue, class Store>
+__device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, Issue &&issue, Store &&store) {
     static_assert(NT >= 4 * kWave, "attn_combine_slice needs 4 waves");
     __shared__ float cmax[NT / kWave];
     __shared__ float4 accs[4][kWave];
@@ -607,8 +707,7 @@ __device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, 
 #pragma unroll
     for (int i = 0; i < 4; i++)
         if (gq + 4 * i < nc) mx = fmaxf(mx, m4[i]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = wave_max64(mx);
     if (l == 0) cmax[g] = mx;
     __syncthreads();
     float M = cmax[0];
@@ -665,20 +764,23 @@ __device__ __forceinline__ void attn_combine_slice(const GemvInput &in, int c0, 
             dsum += dens[k][l];
         }
         const float4 ga = sum_parts4<KP>(gv, in.kp);
-        reinterpret_cast<float4 *>(xs)[l] = make_float4((sum.x / dsum) * (1.0f / (1.0f + expf(-ga.x))),
-                                                        (sum.y / dsum) * (1.0f / (1.0f + expf(-ga.y))),
-                                                        (sum.z / dsum) * (1.0f / (1.0f + expf(-ga.z))),
-                                                        (sum.w / dsum) * (1.0f / (1.0f + expf(-ga.w))));
+        store(make_float4((sum.x / dsum) * (1.0f / (1.0f + expf(-ga.x))), (sum.y / dsum) * (1.0f / (1.0f + expf(-ga.y))),
+                          (sum.z / dsum) * (1.0f / (1.0f + expf(-ga.z))), (sum.w / dsum) * (1.0f / (1.0f + expf(-ga.w)))),
+              l, true);
     }
     __syncthreads();
 }
 
-template <int MODE, int KP, int NT, class Issue>
-__device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, int c0, int len, float *xs,
-                                                    float *red, Issue &&issue) {
+template <int MODE, int KP, int NT, class Issue, class Store>
+__device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, int c0, int len, float *red,
+                                                    Issue &&issue, Store &&store) {
     const int t = threadIdx.x;
-    float4 *xs4 = reinterpret_cast<float4 *>(xs);
-    if constexpr (MODE == GEMV_IN_RMSNORM || MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_EMBED_RMSNORM) {
+    if constexpr (MODE == GEMV_IN_PLAIN) {
+        const float4 v = reinterpret_cast<const float4 *>(in.x + c0)[min(t, (len >> 2) - 1)];
+        issue();
+        store(v, t, t < (len >> 2));
+        __syncthreads();
+    } else if constexpr (MODE == GEMV_IN_RMSNORM || MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_EMBED_RMSNORM) {
         // one float4 of the n-vector per thread
         const int n4 = n >> 2, e4 = min(t, n4 - 1);
         const float4 *src;
@@ -706,12 +808,13 @@ __device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, 
             if (MODE != GEMV_IN_RMSNORM && blockIdx.x == 0 && blockIdx.y == 0)
                 reinterpret_cast<float4 *>(in.x_out)[t] = r;
         }
-        ss = wg_sum<NT>(ss, red);
-        const float inv_rms = 1.0f / sqrtf(ss / (float)n + in.eps);
+        // the slice is stored as r * w, and the GEMV's sums are scaled by
+        // inv_rms = 1 / sqrt(sum(r^2) / n + eps) at the end (post_scale):
+        // the reduction no longer sits between the loads and the dot products
+        ss = wave_sum(ss);
+        if ((t & (kWave - 1)) == 0) red[t / kWave] = ss;
         const int e = 4 * t;
-        if (t < n4 && e >= c0 && e < c0 + len)
-            xs4[(e - c0) >> 2] = make_float4((r.x * inv_rms) * w.x, (r.y * inv_rms) * w.y, (r.z * inv_rms) * w.z,
-                                             (r.w * inv_rms) * w.w);
+        store(make_float4(r.x * w.x, r.y * w.y, r.z * w.z, r.w * w.w), (e - c0) >> 2, t < n4 && e >= c0 && e < c0 + len);
         __syncthreads();
     } else if constexpr (MODE == GEMV_IN_SILU_MUL) {
         const int e4 = min(t, (len >> 2) - 1);
@@ -720,11 +823,11 @@ __device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, 
         load_parts4<KP>(u, in.part, in.kp, in.part_stride, (size_t)((n + c0) >> 2) + e4);
         issue();
         const float4 gs = sum_parts4<KP>(g, in.kp), us = sum_parts4<KP>(u, in.kp);
-        if (t < (len >> 2))
-            xs4[t] = make_float4(silu1(gs.x) * us.x, silu1(gs.y) * us.y, silu1(gs.z) * us.z, silu1(gs.w) * us.w);
+        store(make_float4(silu1(gs.x) * us.x, silu1(gs.y) * us.y, silu1(gs.z) * us.z, silu1(gs.w) * us.w), t,
+              t < (len >> 2));
         __syncthreads();
     } else if constexpr (MODE == GEMV_IN_ATTN_COMBINE) {
-        attn_combine_slice<KP, NT>(in, c0, xs, issue);
+        attn_combine_slice<KP, NT>(in, c0, issue, store);
     } else if constexpr (MODE == GEMV_IN_GATED_NORM) {
         const int wg = blockIdx.y * gridDim.x + blockIdx.x;
         const bool commit = in.conv_state != nullptr;
@@ -747,12 +850,12 @@ __device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, 
             for (int p = 0; p < KP; p++) nv[p] = in.part[(size_t)min(p, max(in.kp - 1, 0)) * in.part_stride + cc];
         }
         issue();
-        const float ss = half_sum32(a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w);
+        const float ss = half_sum(a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w);
         const float inv_rms = 1.0f / sqrtf(ss / 128.0f + in.eps);
         const float4 g = sum_parts4<KP>(ga, in.kp);
-        if (t < (len >> 2))
-            xs4[t] = make_float4(((a.x * inv_rms) * w.x) * silu1(g.x), ((a.y * inv_rms) * w.y) * silu1(g.y),
-                                 ((a.z * inv_rms) * w.z) * silu1(g.z), ((a.w * inv_rms) * w.w) * silu1(g.w));
+        store(make_float4(((a.x * inv_rms) * w.x) * silu1(g.x), ((a.y * inv_rms) * w.y) * silu1(g.y),
+                          ((a.z * inv_rms) * w.z) * silu1(g.z), ((a.w * inv_rms) * w.w) * silu1(g.w)),
+              t, t < (len >> 2));
         if (has) {
             float sv = nv[0];
 #pragma unroll
@@ -761,6 +864,20 @@ __device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, 
         }
         __syncthreads();
     }
+}
+
+// The factor prologue_overlapped leaves for the GEMV's sums: the norm modes
+// store r * w and defer inv_rms (main.rs:1106-1113: out = (r * inv_rms) * w,
+// here sum_k q_k (r_k w_k) * inv_rms); red holds the waves' sums of r^2.
+template <int MODE, int NT>
+__device__ __forceinline__ float post_scale(const GemvInput &in, int n, const float *red) {
+    if constexpr (MODE == GEMV_IN_RMSNORM || MODE == GEMV_IN_RESID_RMSNORM || MODE == GEMV_IN_EMBED_RMSNORM) {
+        float ss = red[0];
+#pragma unroll
+        for (int w = 1; w < NT / kWave; w++) ss += red[w];
+        return 1.0f / sqrtf(ss / (float)n + in.eps);
+    }
+    return 1.0f;
 }
 
 // Batch-1 GEMV over panels: grid = (row-tile groups, K splits), 8 waves per
@@ -783,7 +900,9 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
                                                                   int tiles_per_wg) {
     constexpr int NB = 8 / S, P = kPackedWaves / S, V = PanelPart<T, NB>::kVecs;
     constexpr int NT = kWave * kPackedWaves;
-    __shared__ __align__(16) float xs[kMaxSliceSb * 256];
+    __shared__ __align__(16) float xs[kMaxSliceSb * 256];  // the generic path's input slice
+    __shared__ __align__(16) uint32_t xd[kMaxSliceSb * 8 * kXdWords];
+    __shared__ uint4 xq[kMaxSliceSb * 8];
     __shared__ float red[kPackedWaves][kWave];
     __shared__ float redw[kPackedWaves];
     const int lane = threadIdx.x & (kWave - 1);
@@ -795,8 +914,8 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
     const int sb_end = min(nsb, sb_begin + sb_per_split);
     const int t0 = blockIdx.x * tiles_per_wg, t1 = min(tiles, t0 + tiles_per_wg);
     const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
-    bool fast = sb_end - sb_begin <= P;
-    if constexpr (MODE != GEMV_IN_PLAIN) fast = fast && overlapped_ok<MODE, NT>(in, n, (sb_end - sb_begin) * 256);
+    const bool fast = sb_end - sb_begin <= P && overlapped_ok<MODE, NT>(in, n, (sb_end - sb_begin) * 256);
+    auto digits = [&](float4 v, int i4, bool ok) { put_digits<T>(v, i4, ok, xd, xq); };
 
     u32x4 q[V], sc;
     for (int tile = t0; tile < t1; tile++) {
@@ -806,30 +925,26 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
             const int sb = sb_begin + pi;
             const bool valid = sb < sb_end;
             const uint8_t *pp = tb + (size_t)sb * Panel<T>::kBytes;
-            if (MODE != GEMV_IN_PLAIN && tile == t0) {
+            if (tile == t0) {
+                // the slice's digits are formed once and kept for later tiles
                 auto issue = [&]() { load_part<T, NB>(q, sc, pp, Wp, part, lane, valid); };
-                prologue_overlapped<MODE, KP, NT>(in, n, sb_begin * 256, (sb_end - sb_begin) * 256, xs, redw, issue);
+                prologue_overlapped<MODE, KP, NT>(in, n, sb_begin * 256, (sb_end - sb_begin) * 256, redw, issue,
+                                                  digits);
             } else {
                 load_part<T, NB>(q, sc, pp, Wp, part, lane, valid);
             }
-            const float *xg = MODE == GEMV_IN_PLAIN ? in.x + sb_begin * 256 : xs;
-            if (valid) acc = panel_dot<T, NB>(q, sc, xg + pi * 256, part, acc);
+            if (valid) acc = panel_dot<T, NB>(q, sc, xd + pi * 8 * kXdWords, xq + pi * 8, part, acc);
         } else {
             for (int r0 = sb_begin; r0 < sb_end; r0 += P) {
                 const int r1 = min(sb_end, r0 + P);
                 const int sb = r0 + pi;
                 const bool valid = sb < r1;
                 load_part<T, NB>(q, sc, tb + (size_t)sb * Panel<T>::kBytes, Wp, part, lane, valid);
-                const float *xg;
-                if constexpr (MODE == GEMV_IN_PLAIN) {
-                    xg = in.x + r0 * 256;
-                } else {
-                    if (r0 != sb_begin) __syncthreads();  // the previous round's reads of xs are done
-                    gemv_prologue<MODE, 2, NT>(in, n, r0 * 256, (r1 - r0) * 256, xs, redw,
-                                               tile == t0 && r0 == sb_begin);
-                    xg = xs;
-                }
-                if (valid) acc = panel_dot<T, NB>(q, sc, xg + (sb - r0) * 256, part, acc);
+                if (r0 != sb_begin) __syncthreads();  // the previous round's reads of xd are done
+                gemv_prologue<MODE, 2, NT>(in, n, r0 * 256, (r1 - r0) * 256, xs, redw, tile == t0 && r0 == sb_begin);
+                digitize_lds<T, NT>(xs, (r1 - r0) * 256, xd, xq);
+                __syncthreads();
+                if (valid) acc = panel_dot<T, NB>(q, sc, xd + (sb - r0) * 8 * kXdWords, xq + (sb - r0) * 8, part, acc);
             }
         }
         red[wave][lane] = acc;
@@ -840,10 +955,10 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
                 float sum = red[0][lane];
 #pragma unroll
                 for (int v = 1; v < kPackedWaves; v++) sum += red[v][lane];
-                out[(size_t)ks * split_stride + row] = sum;
+                out[(size_t)ks * split_stride + row] = fast ? sum * post_scale<MODE, NT>(in, n, redw) : sum;
             }
         }
-        __syncthreads();  // red (and, in the generic path, xs) are reused by the next tile
+        __syncthreads();  // red (and, in the generic path, xs and xd) are reused by the next tile
     }
 }
 
@@ -854,9 +969,10 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
 // wave * H + l / R; slot s takes the row's Q8_0 / Q4_0 blocks s, s + 16 H,
 // ... (J of them: 8 n / 256 = 16 H J), whole blocks with their scales, every
 // load issued before any is used.  x is staged in LDS (its loads issued
-// before the weights', so waiting for them does not wait for the weights).
-// Per lane: block sums in block order, each scaled (q8_gemv.rs:234-242);
-// then the 16 H slots of a row are added through LDS in slot order.
+// before the weights', so waiting for them does not wait for the weights) as
+// int8 digits (put_digits).  Per lane: block sums in block order, each scaled
+// (q8_gemv.rs:234-242); then the 16 H slots of a row are added through LDS in
+// slot order.
 constexpr int kRowsWaves = 16;
 constexpr int kRowsMaxN = 8192;
 
@@ -867,7 +983,8 @@ __global__ __launch_bounds__(kWave *kRowsWaves) void gemv_rows(const uint8_t *__
     constexpr int R = kWave / H, SLOTS = kRowsWaves * H, NT = kWave * kRowsWaves;
     constexpr int VB = T == ANEHIP_GGML_Q8_0 ? 2 : 1;  // 16-byte quant vectors per block
     constexpr int XV = kRowsMaxN / 4 / NT;              // float4 of x per thread, at most
-    __shared__ __align__(16) float xs[kRowsMaxN];
+    __shared__ __align__(16) uint32_t xd[kRowsMaxN / 32 * kXdWords];
+    __shared__ uint4 xq[kRowsMaxN / 32];
     __shared__ float red[kRowsWaves][kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -898,7 +1015,7 @@ __global__ __launch_bounds__(kWave *kRowsWaves) void gemv_rows(const uint8_t *__
 #pragma unroll
     for (int i = 0; i < XV; i++) {
         const int e = (int)threadIdx.x + i * NT;
-        if (e < n4) reinterpret_cast<float4 *>(xs)[e] = xv[i];
+        if (i * NT < n4) put_digits<T>(xv[i], e, e < n4, xd, xq);  // uniform condition
     }
     __syncthreads();
     float acc = 0.0f;
@@ -906,30 +1023,7 @@ __global__ __launch_bounds__(kWave *kRowsWaves) void gemv_rows(const uint8_t *__
     for (int j = 0; j < J; j++) {
         const int b = slot + j * SLOTS;
         const float d = __half2float(__ushort_as_half((unsigned short)(scw[j] >> (16 * (b & 1)))));
-        const float *xb = xs + 32 * b;
-        float bs = 0.0f;
-        if constexpr (T == ANEHIP_GGML_Q8_0) {
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                const u32x4 v = q[j][hh];
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int qi = (int)(int8_t)(w4[i >> 2] >> (8 * (i & 3)));
-                    bs = fmaf((float)qi, xb[16 * hh + i], bs);
-                }
-            }
-        } else {
-            const u32x4 v = q[j][0];
-            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const uint32_t byte = (w4[i >> 2] >> (8 * (i & 3))) & 0xffu;
-                bs = fmaf((float)((int)(byte & 15u) - 8), xb[i], bs);
-                bs = fmaf((float)((int)(byte >> 4) - 8), xb[16 + i], bs);
-            }
-        }
-        acc = fmaf(bs, d, acc);
+        acc = fmaf(block_dot_digits<T>(q[j], xd + b * kXdWords, xq[b]), d, acc);
     }
     red[wave][lane] = acc;
     __syncthreads();
