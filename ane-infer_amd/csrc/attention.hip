@@ -35,18 +35,6 @@ constexpr int kHd = 256;       // head_dim
 constexpr int kCh = 64;        // positions per workgroup
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
 // RMSNorm (eps 1e-6, deltanet.rs:575-598) + RoPE (deltanet.rs:600-623) of one
 // 256-dim head by one wave: lane l owns dims 4l..4l+3 = rotary pairs 2l, 2l+1.
 __device__ __forceinline__ void norm_rope_head(const MixIn &mix, int b, int base, const float *__restrict__ w,
@@ -134,7 +122,9 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     __shared__ __align__(16) h8v qf[8][2][64];         // q B fragments: k-step, hi / lo, lane
     __shared__ __align__(16) float pt[G][kCh];        // probabilities of the tile
     __shared__ __align__(16) __half knew[kHd], vnew[kHd];
-    __shared__ float rmax[4][16], rsum[4][16], rscale[16];
+    // per-tile maxima and sums of the 16 (wave, lane group) pieces of each
+    // head's column, [piece][head]: combined after the barrier, no shuffles
+    __shared__ float rmax[16][16], rsum[16][16], rscale[16];
     __shared__ float qmax[G];  // largest |q| / 16 of each query head (range-safe q fragments)
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -184,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         float q4[4];
         norm_rope_head(mix, b, h * 2 * kHd, q_norm, inv_freq, pos, lane, q4);
         *reinterpret_cast<float4 *>(&qs[wave][4 * lane]) = make_float4(q4[0], q4[1], q4[2], q4[3]);
-        const float qm = wave_max(fmaxf(fmaxf(fabsf(q4[0]), fabsf(q4[1])), fmaxf(fabsf(q4[2]), fabsf(q4[3]))));
+        const float qm = wave_max64(fmaxf(fmaxf(fabsf(q4[0]), fabsf(q4[1])), fmaxf(fabsf(q4[2]), fabsf(q4[3]))));
         if (lane == 0) qmax[wave] = qm * 0.0625f;
     }
     if (has_new && wave == G % 4) {
@@ -277,12 +267,11 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         float sv[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) sv[e] = p0 + e < len ? ldexpf(sc[e], qe_li) : -INFINITY;
-        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        if (lane < 16) rmax[wave][lane] = mx;
+        rmax[4 * wave + lg][li] = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         lds_barrier();
-        const float tm = fmaxf(fmaxf(rmax[0][li], rmax[1][li]), fmaxf(rmax[2][li], rmax[3][li]));
+        float tm = rmax[0][li];
+#pragma unroll
+        for (int j = 1; j < 16; j++) tm = fmaxf(tm, rmax[j][li]);
         const float mn = fmaxf(m_run, tm);     // finite for li < G: the tile has a valid row
         const float scale = expf(m_run - mn);  // 0 on the first tile
         float pe[4], ps = 0.f;
@@ -291,13 +280,15 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
             pe[e] = p0 + e < len ? expf(sv[e] - mn) : 0.0f;
             ps += pe[e];
         }
-        ps += __shfl_xor(ps, 16);
-        ps += __shfl_xor(ps, 32);
-        if (lane < 16) rsum[wave][lane] = ps;
+        rsum[4 * wave + lg][li] = ps;
         if (wave == 0 && lane < 16) rscale[lane] = scale;
         if (li < G) *reinterpret_cast<float4 *>(&pt[li][16 * wave + 4 * lg]) = make_float4(pe[0], pe[1], pe[2], pe[3]);
         lds_barrier();
-        l_run = l_run * scale + ((rsum[0][li] + rsum[1][li]) + (rsum[2][li] + rsum[3][li]));
+        float ts[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            ts[w] = (rsum[4 * w][li] + rsum[4 * w + 1][li]) + (rsum[4 * w + 2][li] + rsum[4 * w + 3][li]);
+        l_run = l_run * scale + ((ts[0] + ts[1]) + (ts[2] + ts[3]));
         m_run = mn;
         // PV: rescale the rows (heads 4 lg + e), then P (hi + lo) times V^T
         float rs[4];
@@ -409,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
     // maximum over the chunks
     float mx = -INFINITY;
     for (int cc = t; cc < nc; cc += kThreads) mx = fmaxf(mx, part_ml[((base + cc) * G + hh) * 2]);
-    mx = wave_max(mx);
+    mx = wave_max64(mx);
     if (l == 0) red[g] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

@@ -17,12 +17,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
 // Sum over a 256-thread block; every thread gets the total.
 __device__ __forceinline__ float block_sum(float v, float *red) {
     v = wave_sum(v);
@@ -195,8 +189,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restr
     if (xp.hi) {
         // a 128-column group is two waves of this workgroup
         float amax = in ? fabsf(v) : 0.0f;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        amax = wave_max64(amax);
         if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = amax;
         __syncthreads();
         const int w0 = (threadIdx.x >> 6) & ~1;
