@@ -114,6 +114,8 @@ def parse():
     ap.add_argument("--deltanet-only", action="store_true", help="only run the configs[3] DeltaNet leg")
     ap.add_argument("--profile-c0", action="store_true",
                     help="only run the configs[0] GEMV, the streaming-read floor and the empty kernel (for rocprofv3)")
+    ap.add_argument("--profile-b1-floors", action="store_true",
+                    help="only run the floors (streaming read, empty kernel) under the batch-1 decode GEMVs")
     ap.add_argument("--profile-points", default=None,
                     help="only run these sweep points back to back, e.g. '151936x2048:32,6144x2048:4' (for rocprofv3)")
     ap.add_argument("--prefill-only", type=int, default=0,
@@ -280,6 +282,42 @@ def c0_floor(ctx, s, launches=40):
     return {"read_us": res, "best": best, "best_us": res[best], "best_GB/s": round(gbs, 1),
             "best_pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "empty_kernel_us": empty,
             "bytes": s.pbytes}
+
+
+# The batch-1 decode step's GEMVs at the 2B shape: role, m x n, and the
+# workgroups of the step's kernel (its K-split grid, as the kernel trace of
+# `--decode-only 1:1024` shows it).
+B1_GEMVS = [("ffn gate/up", 12288, 2048, 192), ("DeltaNet in-proj", 8224, 2048, 129),
+            ("ffn down", 2048, 6144, 192), ("attention qkv", 5120, 2048, 160), ("ssm_out", 2048, 2048, 256),
+            ("o_proj", 2048, 2048, 256), ("lm_head", 151936, 2048, 2374)]
+
+
+def b1_floors(anehip, ctx, launches=40):
+    """Floors under each batch-1 decode GEMV: a 16-byte streaming read of its
+    panel bytes (rotated past the MALL) on the step kernel's own grid
+    (workgroups x 512 threads, the best of depths 2 / 4 / 8), and an empty
+    kernel on that grid, each timed as `launches` back-to-back graph nodes."""
+    out = {}
+    for i, (role, m, n, wgs) in enumerate(B1_GEMVS):
+        s = Shape(anehip, ctx, m, n, 500 + i)
+        sink = ctx.alloc(wgs * 512 * 4)
+        reads = {}
+        for depth in FLOOR_DEPTHS:
+            g = capture(ctx, lambda: [ctx.call("probe_read", s.pptr(c), s.pbytes, wgs, 512, depth, sink)
+                                      for c in range(launches)])
+            reads[depth] = time_graphs(ctx, [g], 3) / 3 / launches * 1e3
+            ctx.graph_destroy(g)
+        g = capture(ctx, lambda: [ctx.call("probe_empty", wgs, 512) for _ in range(launches)])
+        empty = time_graphs(ctx, [g], 3) / 3 / launches * 1e3
+        ctx.graph_destroy(g)
+        best = min(reads, key=reads.get)
+        out[role] = {"m": m, "n": n, "workgroups": wgs, "algorithmic_bytes": algo_bytes(m, n, 1),
+                     "read_us": round(reads[best], 2), "read_depth": best,
+                     "read_GB/s": round(algo_bytes(m, n, 1) / (reads[best] * 1e-6) / 1e9, 1),
+                     "empty_us": round(empty, 2)}
+        sink.free()
+        s.free()
+    return out
 
 
 def bench_q4(anehip, ctx):
@@ -516,6 +554,10 @@ def main():
         c0 = Shape(anehip, ctx, 6144, 2048, 100)
         t = time_point(ctx, c0, 1, 40)
         print(json.dumps({"c0_us": round(t * 1e3, 3), "floor": c0_floor(ctx, c0)}), flush=True)
+        ctx.close()
+        return
+    if args.profile_b1_floors:
+        print(json.dumps({"b1_floors": b1_floors(anehip, ctx)}), flush=True)
         ctx.close()
         return
     if args.profile_points:
