@@ -41,46 +41,200 @@ template <> struct QTraits<ANEHIP_GGML_Q4_0> {
     static constexpr int kSbVec = 9;
 };
 
-__device__ __forceinline__ uint32_t byte_at(const uint32_t *w, int off) {
-    return (w[off >> 2] >> ((off & 3) * 8)) & 0xffu;
-}
-
 __device__ __forceinline__ float half_at(const uint32_t *w, int off) {
     // off is even, so the two bytes never straddle a 32-bit word
     uint32_t bits = (w[off >> 2] >> ((off & 3) * 8)) & 0xffffu;
     return __half2float(__ushort_as_half((unsigned short)bits));
 }
 
-// Dot product of one super-block (8 blocks) held in registers with x[0..255]
-// (wave-uniform), accumulated per block then scaled, as compute_row does
-// (q8_gemv.rs:234-242): sum += block_sum * scale.
+// ---------------------------------------------------------------------------
+// Batch-1 GEMV input as int8 digits.  Each 32-column block of the input slice
+// is held in LDS as x = 2^-sh (d0 + d1 / 128 + d2 / 16384) + e, with int8
+// digits d0 = trunc(x 2^sh), d1 = trunc(frac 128), d2 = rint(frac' 128), and
+// sh per block from its largest magnitude M (M 2^sh in [64, 128)), so |e| <=
+// 2^-21 M.  A block's sum q . x (q8_gemv.rs:234-242: per block, then scaled
+// by d) is then three exact int32 dot products over the int8 weights
+// (v_dot4_i32_i8, 4 products per instruction) combined in fp32: about half
+// the VALU work of one conversion and one FMA per weight, which was a third of
+// the busy time of the large batch-1 GEMVs.  The result differs from the
+// per-element fp32 sum by rounding only (both are within ~2^-21 of the exact
+// sum relative to max|x| |q|).
+// LDS per block: kXdWords dwords (digit planes 0, 1, 2; byte i of dword w is
+// column 4 w + i) and a uint4 {2^-sh as float bits, 8 sum(d0), 8 sum(d1),
+// 8 sum(d2)} (the sums serve Q4_0's -8 offset).  A block holding an inf or NaN
+// gets zero digits and a NaN factor, so its rows come out NaN.
+// ---------------------------------------------------------------------------
+constexpr int kXdWords = 24;
+
+// Digitises 4 consecutive columns v of the slice (float4 index i4); lanes
+// 8 k .. 8 k + 7 of the wave must hold one block (i4 & 7 = lane & 7).  Every
+// lane of the wave calls it (DPP needs all lanes active); only `store` lanes
+// write.
+template <int CTRL>
+__device__ __forceinline__ int dpp_iadd(int v) {
+    return v + __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+
 template <uint32_t T>
-__device__ __forceinline__ float sb_dot(const uint32_t *w, const float *__restrict__ x, float acc) {
+__device__ __forceinline__ void put_digits(float4 v, int i4, bool store, uint32_t *xd, uint4 *xq) {
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    float mx = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int base = k * QTraits<T>::kBlockBytes;
-        const float d = half_at(w, base);
-        float bs = 0.0f;
-        if constexpr (T == ANEHIP_GGML_Q8_0) {
+    for (int i = 0; i < 4; i++) mx = fmaxf(mx, __builtin_isnan(xv[i]) ? INFINITY : fabsf(xv[i]));
+    // the block's maximum over its 8 lanes on DPP (xor 1, xor 2, half-row mirror)
+    mx = dpp_max<0x141>(dpp_max<0x4E>(dpp_max<0xB1>(mx)));
+    const bool bad = mx == INFINITY;  // an inf or NaN in the block
+    // mx in [2^(e-1), 2^e): mx 2^(7-e) in [64, 128); the smallest subnormals
+    // keep sh at 149 so that 2^-sh stays representable
+    const int sh = bad || mx == 0.0f ? 0 : min(7 - __builtin_amdgcn_frexp_expf(mx), 149);
+    uint32_t p0 = 0, p1 = 0, p2 = 0;
+    int s0 = 0, s1 = 0, s2 = 0;
 #pragma unroll
-            for (int i = 0; i < 32; i++) {
-                int q = (int)(int8_t)byte_at(w, base + 2 + i);
-                bs = fmaf((float)q, x[k * 32 + i], bs);
-            }
-        } else {
+    for (int i = 0; i < 4; i++) {
+        const float y = bad ? 0.0f : ldexpf(xv[i], sh);  // |y| < 128
+        const float f0 = truncf(y);
+        const float r = (y - f0) * 128.0f;  // exact
+        const float f1 = truncf(r);
+        const float f2 = fminf(fmaxf(rintf((r - f1) * 128.0f), -127.0f), 127.0f);
+        const int i0 = (int)f0, i1 = (int)f1, i2 = (int)f2;
+        p0 |= ((uint32_t)i0 & 0xffu) << (8 * i);
+        p1 |= ((uint32_t)i1 & 0xffu) << (8 * i);
+        p2 |= ((uint32_t)i2 & 0xffu) << (8 * i);
+        if constexpr (T == ANEHIP_GGML_Q4_0) {
+            s0 += i0;
+            s1 += i1;
+            s2 += i2;
+        }
+    }
+    if constexpr (T == ANEHIP_GGML_Q4_0) {
+        s0 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s0)));
+        s1 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s1)));
+        s2 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s2)));
+    }
+    if (store) {
+        const int blk = i4 >> 3, w = i4 & 7;
+        uint32_t *p = xd + blk * kXdWords + w;
+        p[0] = p0;
+        p[8] = p1;
+        p[16] = p2;
+        if (w == 0)
+            xq[blk] = make_uint4(__float_as_uint(bad ? __builtin_nanf("") : ldexpf(1.0f, -sh)), (uint32_t)(8 * s0),
+                                 (uint32_t)(8 * s1), (uint32_t)(8 * s2));
+    }
+}
+
+// Digitises xs[0, len) (floats in LDS, len a multiple of 32) into xd / xq;
+// the caller synchronises before and after.
+template <uint32_t T, int NT>
+__device__ __forceinline__ void digitize_lds(const float *xs, int len, uint32_t *xd, uint4 *xq) {
+    const int n4 = len >> 2;
+    for (int b4 = 0; b4 < n4; b4 += NT) {  // uniform trip count
+        const int i4 = b4 + (int)threadIdx.x;
+        const float4 v = reinterpret_cast<const float4 *>(xs)[min(i4, n4 - 1)];
+        put_digits<T>(v, i4, i4 < n4, xd, xq);
+    }
+}
+
+// The same in place: the digits overwrite xs itself (kXdWords dwords and a
+// uint4 per block fit in the block's 32 floats), for kernels whose LDS
+// budget has no room for a second copy.  Every value is read before any
+// digit is written; the caller synchronises after.
+template <uint32_t T, int NT, int MAXLEN>
+__device__ __forceinline__ void digitize_lds_inplace(float *xs, int len) {
+    constexpr int IT = MAXLEN / 4 / NT;
+    const int n4 = len >> 2, t = (int)threadIdx.x;
+    float4 v[IT];
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                uint32_t b = byte_at(w, base + 2 + i);
-                float v0 = (float)((int)(b & 15u) - 8);
-                float v1 = (float)((int)(b >> 4) - 8);
-                bs = fmaf(v0, x[k * 32 + i], bs);
-                bs = fmaf(v1, x[k * 32 + 16 + i], bs);
+    for (int i = 0; i < IT; i++) v[i] = reinterpret_cast<const float4 *>(xs)[min(t + i * NT, max(n4 - 1, 0))];
+    __syncthreads();
+    uint32_t *xd = reinterpret_cast<uint32_t *>(xs);
+    uint4 *xq = reinterpret_cast<uint4 *>(xs + MAXLEN / 32 * kXdWords);
+#pragma unroll
+    for (int i = 0; i < IT; i++)
+        if (i * NT < n4) put_digits<T>(v[i], t + i * NT, t + i * NT < n4, xd, xq);  // uniform condition
+}
+
+// One block's q . x from its digits, times 2^-sh (q: the block's quant
+// vectors, 2 for Q8_0 with columns 0-15 and 16-31, 1 for Q4_0; xdb: the
+// block's kXdWords digit dwords; xqv: its uint4).
+template <uint32_t T>
+__device__ __forceinline__ float block_dot_digits(const u32x4 *q, const uint32_t *xdb, const uint4 xqv) {
+    const u32x4 *x4 = reinterpret_cast<const u32x4 *>(xdb);
+    const u32x4 a0 = x4[0], b0 = x4[1], a1 = x4[2], b1 = x4[3], a2 = x4[4], b2 = x4[5];
+    const uint32_t d0[8] = {a0.x, a0.y, a0.z, a0.w, b0.x, b0.y, b0.z, b0.w};
+    const uint32_t d1[8] = {a1.x, a1.y, a1.z, a1.w, b1.x, b1.y, b1.z, b1.w};
+    const uint32_t d2[8] = {a2.x, a2.y, a2.z, a2.w, b2.x, b2.y, b2.z, b2.w};
+    int s0 = 0, s1 = 0, s2 = 0;
+    if constexpr (T == ANEHIP_GGML_Q8_0) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t w4[4] = {q[h].x, q[h].y, q[h].z, q[h].w};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                s0 = __builtin_amdgcn_sdot4((int)w4[w], (int)d0[4 * h + w], s0, false);
+                s1 = __builtin_amdgcn_sdot4((int)w4[w], (int)d1[4 * h + w], s1, false);
+                s2 = __builtin_amdgcn_sdot4((int)w4[w], (int)d2[4 * h + w], s2, false);
             }
         }
-        acc = fmaf(bs, d, acc);
-        // keep each block's LDS reads, converts and FMAs together: bounds the
-        // live registers to one block (the other waves hide the LDS latency)
-        __builtin_amdgcn_sched_barrier(0);
+    } else {
+        // byte i of the block: element i in the low nibble, i + 16 in the high
+        // one (dequant.rs:12-25); nibbles are 0..15, the -8 comes off as 8 sum(d)
+        const uint32_t w4[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const int lo = (int)(w4[w] & 0x0f0f0f0fu), hi = (int)((w4[w] >> 4) & 0x0f0f0f0fu);
+            s0 = __builtin_amdgcn_sdot4(lo, (int)d0[w], s0, false);
+            s1 = __builtin_amdgcn_sdot4(lo, (int)d1[w], s1, false);
+            s2 = __builtin_amdgcn_sdot4(lo, (int)d2[w], s2, false);
+            s0 = __builtin_amdgcn_sdot4(hi, (int)d0[4 + w], s0, false);
+            s1 = __builtin_amdgcn_sdot4(hi, (int)d1[4 + w], s1, false);
+            s2 = __builtin_amdgcn_sdot4(hi, (int)d2[4 + w], s2, false);
+        }
+        s0 -= (int)xqv.y;
+        s1 -= (int)xqv.z;
+        s2 -= (int)xqv.w;
+    }
+    const float bs = fmaf((float)s2, 1.0f / 16384.0f, fmaf((float)s1, 1.0f / 128.0f, (float)s0));
+    return bs * __uint_as_float(xqv.x);
+}
+
+// 4 dwords of a GGUF row starting at byte offset `off` (even; blocks are 34
+// or 18 bytes, so a block's quants start 2 bytes into a dword for every
+// second block): one v_alignbyte per dword when misaligned.
+__device__ __forceinline__ u32x4 words_at(const uint32_t *w, int off) {
+    u32x4 r;
+    const int i = off >> 2;
+    if ((off & 3) == 0) {
+        r = u32x4{w[i], w[i + 1], w[i + 2], w[i + 3]};
+    } else {
+        r = u32x4{__builtin_amdgcn_alignbyte(w[i + 1], w[i], 2), __builtin_amdgcn_alignbyte(w[i + 2], w[i + 1], 2),
+                  __builtin_amdgcn_alignbyte(w[i + 3], w[i + 2], 2), __builtin_amdgcn_alignbyte(w[i + 4], w[i + 3], 2)};
+    }
+    return r;
+}
+
+// Dot product of one super-block (8 GGUF blocks) of the lane's row, held in
+// LDS as words w, with the digits of the super-block's 256 inputs (xd, xq:
+// its first block; see put_digits): per block, then scaled by the block's d
+// (q8_gemv.rs:234-242).
+template <uint32_t T>
+__device__ __forceinline__ float sb_dot(const uint32_t *w, const uint32_t *xd, const uint4 *xq, float acc) {
+    // pairs of blocks: block 2 p starts at a multiple of 4 bytes, block 2 p + 1
+    // two bytes past one, so each pair's alignment is known at compile time
+#pragma unroll 1
+    for (int k = 0; k < 8; k += 2) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int base = (k + j) * QTraits<T>::kBlockBytes;
+            const uint32_t *wb = w + (base >> 2);
+            constexpr int Q = QTraits<T>::kBlockBytes;
+            const int o = ((j * Q) & 3) + 2;  // the quants' byte offset from wb
+            const float d = half_at(wb, (j * Q) & 3);
+            u32x4 q[2];
+            q[0] = words_at(wb, o);
+            if constexpr (T == ANEHIP_GGML_Q8_0) q[1] = words_at(wb, o + 16);
+            acc = fmaf(block_dot_digits<T>(q, xd + (k + j) * kXdWords, xq[k + j]), d, acc);
+        }
     }
     return acc;
 }
@@ -299,7 +453,9 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void gemv_fused(const uint8_t *
                                                                 int sb_per_split, size_t split_stride) {
     constexpr int V = QTraits<T>::kSbVec;
     __shared__ u32x4 lds[kWavesPerWg][V * kWave];
-    __shared__ float xs[kMaxSliceSb * 256];
+    // the input slice, then (in place) its digits: kept at 8 KiB so that two
+    // workgroups fit a CU's LDS
+    __shared__ __align__(16) float xs[kMaxSliceSb * 256];
     __shared__ float red4[4];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
@@ -320,6 +476,10 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void gemv_fused(const uint8_t *
     if (sb < sb_end) load_tile<T>(regs, tile_base + (size_t)sb * QTraits<T>::kSbBytes, off);
 
     gemv_prologue<MODE>(in, n, sb_begin * 256, (sb_end - sb_begin) * 256, xs, red4);
+    digitize_lds_inplace<T, kWave * kWavesPerWg, kMaxSliceSb * 256>(xs, (sb_end - sb_begin) * 256);
+    __syncthreads();
+    const uint32_t *xd = reinterpret_cast<const uint32_t *>(xs);
+    const uint4 *xq = reinterpret_cast<const uint4 *>(xs + kMaxSliceSb * 8 * kXdWords);
 
     float acc = 0.0f;
     const uint32_t *wl = reinterpret_cast<const uint32_t *>(&lds[wave][lane * V]);
@@ -327,7 +487,7 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void gemv_fused(const uint8_t *
         stage_tile<T>(regs, lds[wave], lane);
         if (sb + kWavesPerWg < sb_end)
             load_tile<T>(regs, tile_base + (size_t)(sb + kWavesPerWg) * QTraits<T>::kSbBytes, off);
-        acc = sb_dot<T>(wl, xs + (sb - sb_begin) * 256, acc);
+        acc = sb_dot<T>(wl, xd + (sb - sb_begin) * 8 * kXdWords, xq + (sb - sb_begin) * 8, acc);
         wave_sync_lds();  // this tile's reads precede the next tile's writes
     }
     __syncthreads();
@@ -454,138 +614,6 @@ __device__ __forceinline__ void load_part(u32x4 *q, u32x4 &sc, const uint8_t *pa
 #pragma unroll
     for (int c = 0; c < V; c++) q[c] = __builtin_nontemporal_load(p4 + (c0 + c) * 64 + l);
     sc = __builtin_nontemporal_load(p4 + Panel<T>::kChunks * 64 + l);
-}
-
-// ---------------------------------------------------------------------------
-// Batch-1 GEMV input as int8 digits.  Each 32-column block of the input slice
-// is held in LDS as x = 2^-sh (d0 + d1 / 128 + d2 / 16384) + e, with int8
-// digits d0 = trunc(x 2^sh), d1 = trunc(frac 128), d2 = rint(frac' 128), and
-// sh per block from its largest magnitude M (M 2^sh in [64, 128)), so |e| <=
-// 2^-21 M.  A block's sum q . x (q8_gemv.rs:234-242: per block, then scaled
-// by d) is then three exact int32 dot products over the int8 weights
-// (v_dot4_i32_i8, 4 products per instruction) combined in fp32: about half
-// the VALU work of one conversion and one FMA per weight, which was a third of
-// the busy time of the large batch-1 GEMVs.  The result differs from the
-// per-element fp32 sum by rounding only (both are within ~2^-21 of the exact
-// sum relative to max|x| |q|).
-// LDS per block: kXdWords dwords (digit planes 0, 1, 2; byte i of dword w is
-// column 4 w + i) and a uint4 {2^-sh as float bits, 8 sum(d0), 8 sum(d1),
-// 8 sum(d2)} (the sums serve Q4_0's -8 offset).  A block holding an inf or NaN
-// gets zero digits and a NaN factor, so its rows come out NaN.
-// ---------------------------------------------------------------------------
-constexpr int kXdWords = 24;
-
-// Digitises 4 consecutive columns v of the slice (float4 index i4); lanes
-// 8 k .. 8 k + 7 of the wave must hold one block (i4 & 7 = lane & 7).  Every
-// lane of the wave calls it (DPP needs all lanes active); only `store` lanes
-// write.
-template <int CTRL>
-__device__ __forceinline__ int dpp_iadd(int v) {
-    return v + __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
-}
-
-template <uint32_t T>
-__device__ __forceinline__ void put_digits(float4 v, int i4, bool store, uint32_t *xd, uint4 *xq) {
-    const float xv[4] = {v.x, v.y, v.z, v.w};
-    float mx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) mx = fmaxf(mx, __builtin_isnan(xv[i]) ? INFINITY : fabsf(xv[i]));
-    // the block's maximum over its 8 lanes on DPP (xor 1, xor 2, half-row mirror)
-    mx = dpp_max<0x141>(dpp_max<0x4E>(dpp_max<0xB1>(mx)));
-    const bool bad = mx == INFINITY;  // an inf or NaN in the block
-    // mx in [2^(e-1), 2^e): mx 2^(7-e) in [64, 128); the smallest subnormals
-    // keep sh at 149 so that 2^-sh stays representable
-    const int sh = bad || mx == 0.0f ? 0 : min(7 - __builtin_amdgcn_frexp_expf(mx), 149);
-    uint32_t p0 = 0, p1 = 0, p2 = 0;
-    int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float y = bad ? 0.0f : ldexpf(xv[i], sh);  // |y| < 128
-        const float f0 = truncf(y);
-        const float r = (y - f0) * 128.0f;  // exact
-        const float f1 = truncf(r);
-        const float f2 = fminf(fmaxf(rintf((r - f1) * 128.0f), -127.0f), 127.0f);
-        const int i0 = (int)f0, i1 = (int)f1, i2 = (int)f2;
-        p0 |= ((uint32_t)i0 & 0xffu) << (8 * i);
-        p1 |= ((uint32_t)i1 & 0xffu) << (8 * i);
-        p2 |= ((uint32_t)i2 & 0xffu) << (8 * i);
-        if constexpr (T == ANEHIP_GGML_Q4_0) {
-            s0 += i0;
-            s1 += i1;
-            s2 += i2;
-        }
-    }
-    if constexpr (T == ANEHIP_GGML_Q4_0) {
-        s0 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s0)));
-        s1 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s1)));
-        s2 = dpp_iadd<0x141>(dpp_iadd<0x4E>(dpp_iadd<0xB1>(s2)));
-    }
-    if (store) {
-        const int blk = i4 >> 3, w = i4 & 7;
-        uint32_t *p = xd + blk * kXdWords + w;
-        p[0] = p0;
-        p[8] = p1;
-        p[16] = p2;
-        if (w == 0)
-            xq[blk] = make_uint4(__float_as_uint(bad ? __builtin_nanf("") : ldexpf(1.0f, -sh)), (uint32_t)(8 * s0),
-                                 (uint32_t)(8 * s1), (uint32_t)(8 * s2));
-    }
-}
-
-// Digitises xs[0, len) (floats in LDS, len a multiple of 32) into xd / xq;
-// the caller synchronises before and after.
-template <uint32_t T, int NT>
-__device__ __forceinline__ void digitize_lds(const float *xs, int len, uint32_t *xd, uint4 *xq) {
-    const int n4 = len >> 2;
-    for (int b4 = 0; b4 < n4; b4 += NT) {  // uniform trip count
-        const int i4 = b4 + (int)threadIdx.x;
-        const float4 v = reinterpret_cast<const float4 *>(xs)[min(i4, n4 - 1)];
-        put_digits<T>(v, i4, i4 < n4, xd, xq);
-    }
-}
-
-// One block's q . x from its digits, times 2^-sh (q: the block's quant
-// vectors, 2 for Q8_0 with columns 0-15 and 16-31, 1 for Q4_0; xdb: the
-// block's kXdWords digit dwords; xqv: its uint4).
-template <uint32_t T>
-__device__ __forceinline__ float block_dot_digits(const u32x4 *q, const uint32_t *xdb, const uint4 xqv) {
-    const u32x4 *x4 = reinterpret_cast<const u32x4 *>(xdb);
-    const u32x4 a0 = x4[0], b0 = x4[1], a1 = x4[2], b1 = x4[3], a2 = x4[4], b2 = x4[5];
-    const uint32_t d0[8] = {a0.x, a0.y, a0.z, a0.w, b0.x, b0.y, b0.z, b0.w};
-    const uint32_t d1[8] = {a1.x, a1.y, a1.z, a1.w, b1.x, b1.y, b1.z, b1.w};
-    const uint32_t d2[8] = {a2.x, a2.y, a2.z, a2.w, b2.x, b2.y, b2.z, b2.w};
-    int s0 = 0, s1 = 0, s2 = 0;
-    if constexpr (T == ANEHIP_GGML_Q8_0) {
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint32_t w4[4] = {q[h].x, q[h].y, q[h].z, q[h].w};
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                s0 = __builtin_amdgcn_sdot4((int)w4[w], (int)d0[4 * h + w], s0, false);
-                s1 = __builtin_amdgcn_sdot4((int)w4[w], (int)d1[4 * h + w], s1, false);
-                s2 = __builtin_amdgcn_sdot4((int)w4[w], (int)d2[4 * h + w], s2, false);
-            }
-        }
-    } else {
-        // byte i of the block: element i in the low nibble, i + 16 in the high
-        // one (dequant.rs:12-25); nibbles are 0..15, the -8 comes off as 8 sum(d)
-        const uint32_t w4[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const int lo = (int)(w4[w] & 0x0f0f0f0fu), hi = (int)((w4[w] >> 4) & 0x0f0f0f0fu);
-            s0 = __builtin_amdgcn_sdot4(lo, (int)d0[w], s0, false);
-            s1 = __builtin_amdgcn_sdot4(lo, (int)d1[w], s1, false);
-            s2 = __builtin_amdgcn_sdot4(lo, (int)d2[w], s2, false);
-            s0 = __builtin_amdgcn_sdot4(hi, (int)d0[4 + w], s0, false);
-            s1 = __builtin_amdgcn_sdot4(hi, (int)d1[4 + w], s1, false);
-            s2 = __builtin_amdgcn_sdot4(hi, (int)d2[4 + w], s2, false);
-        }
-        s0 -= (int)xqv.y;
-        s1 -= (int)xqv.z;
-        s2 -= (int)xqv.w;
-    }
-    const float bs = fmaf((float)s2, 1.0f / 16384.0f, fmaf((float)s1, 1.0f / 128.0f, (float)s0));
-    return bs * __uint_as_float(xqv.x);
 }
 
 // Dot product of a wave's panel share held in registers (q, sc: see
@@ -1562,7 +1590,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
     constexpr int U = P > D ? P : D;
     static_assert(U % P == 0 && U % D == 0, "ring and panel counts must divide the loop body");
     __shared__ __align__(16) float red[kGemmWaves][16][kWave];
-    __shared__ float wmax[kGemmWaves][16];
+    __shared__ float wmax[4 * kGemmWaves][16];  // [wave, lane group][row]
     __shared__ int emax[kGemmWaves][16];
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
     const int gs = gridDim.x / ksplit;  // workgroups per split
@@ -1618,11 +1646,12 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
         for (int p = 0; p < P; p++)
 #pragma unroll
             for (int j = 0; j < 2; j++) amax = amax8(xr + xcol(p, j), amax);
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        if (lane < 16) wmax[quarter][lane] = amax;
+        wmax[4 * quarter + (lane >> 4)][lane & 15] = amax;
         lds_barrier();
-        E = group_exp(fmaxf(fmaxf(wmax[0][lane & 15], wmax[1][lane & 15]), fmaxf(wmax[2][lane & 15], wmax[3][lane & 15])));
+        float rmax = wmax[0][lane & 15];
+#pragma unroll
+        for (int w = 1; w < 4 * kGemmWaves; w++) rmax = fmaxf(rmax, wmax[w][lane & 15]);
+        E = group_exp(rmax);
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
@@ -1747,7 +1776,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
     int batch, int ksplit, size_t split_stride) {
     constexpr int Q = GemmUnit<T, 1>::kQ;
     __shared__ __align__(16) float red[kGemmWaves][32][kWave];
-    __shared__ float wmax[kGemmWaves][32];
+    __shared__ float wmax[2 * kGemmWaves][32];  // [wave, lane half][row]
     __shared__ int emax[kGemmWaves][32];
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
     const int gs = gridDim.x / ksplit;  // workgroups per split
@@ -1800,10 +1829,12 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
         for (int p = 0; p < P; p++)
 #pragma unroll
             for (int st = 0; st < 4; st++) amax = amax8(xr + xcol(p, st), amax);
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        if (lane < 32) wmax[quarter][lane] = amax;
+        wmax[2 * quarter + (lane >> 5)][lane & 31] = amax;
         lds_barrier();
-        E = group_exp(fmaxf(fmaxf(wmax[0][lane & 31], wmax[1][lane & 31]), fmaxf(wmax[2][lane & 31], wmax[3][lane & 31])));
+        float rmax = wmax[0][lane & 31];
+#pragma unroll
+        for (int w = 1; w < 2 * kGemmWaves; w++) rmax = fmaxf(rmax, wmax[w][lane & 31]);
+        E = group_exp(rmax);
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
@@ -1898,7 +1929,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
     constexpr int NW = kGemmWaves * H;
     static_assert(U % PW == 0 && U % D == 0, "ring and panel counts must divide the loop body");
     __shared__ __align__(16) float red[NW][32][kWave];
-    __shared__ float wmax[NW][32];
+    __shared__ float wmax[2 * NW][32];  // [wave, lane half][row]
     __shared__ int emax[NW][32];
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
     const int gs = gridDim.x / ksplit;  // workgroups per split
@@ -1948,12 +1979,11 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
         for (int p = 0; p < PW; p++)
 #pragma unroll
             for (int st = 0; st < 4; st++) amax = amax8(xr + xcol(p, st), amax);
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
-        if (lane < 32) wmax[wave][lane] = amax;
+        wmax[2 * wave + (lane >> 5)][lane & 31] = amax;
         lds_barrier();
         float rmax = wmax[0][lane & 31];
 #pragma unroll
-        for (int w = 1; w < NW; w++) rmax = fmaxf(rmax, wmax[w][lane & 31]);
+        for (int w = 1; w < 2 * NW; w++) rmax = fmaxf(rmax, wmax[w][lane & 31]);
         E = group_exp(rmax);
 #pragma unroll
         for (int p = 0; p < PW; p++)
