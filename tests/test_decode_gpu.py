@@ -162,14 +162,16 @@ def test_prefill_one_sequence_of_a_batch(mid_host):
         q.close()
 
 
-@pytest.mark.parametrize("which,B", [("small", 2), ("small", 32), ("mid", 2), ("mid", 7), ("mid", 32)])
+@pytest.mark.parametrize("which,B", [("small", 1), ("small", 2), ("small", 32), ("mid", 1), ("mid", 2), ("mid", 7),
+                                     ("mid", 32)])
 def test_activations_beyond_fp16_range(which, B):
-    """Batched steps whose GEMM inputs leave fp16's range: post-attention and
+    """Steps whose GEMM inputs leave fp16's range: post-attention and
     DeltaNet output norm weights scaled by 3e4 (FFN inputs, SiLU-mul outputs
     and gated-norm outputs reach 1e5 - 1e9) and q-norm weights by 1e5 (the
-    attention's q operand).  The element-wise kernels write range-safe planes
-    and the GEMMs / attention scale them back: logits match the fp32 oracle
-    (1e-3) over 3 steps for every sequence."""
+    attention's q operand).  At batch > 1 the element-wise kernels write
+    range-safe planes and the GEMMs / attention scale them back; at batch 1
+    the GEMV prologues digitise each block with its own exponent: logits
+    match the fp32 oracle (1e-3) over 3 steps for every sequence."""
     spec = anehip.Spec(**(SMALL if which == "small" else MID))
     host = HostModel(spec, seed=41)
     scale = {anehip.T["POST_ATTN_NORM"]: 3e4, anehip.T["SSM_NORM"]: 3e4, anehip.T["Q_NORM"]: 1e5}

@@ -262,6 +262,66 @@ def test_packed_gemm_input_range(gpu_ctx, oracle_lib, t, batch, m, n):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144), (16384, 256), (100, 256)])
+@pytest.mark.parametrize("layout", ["panel", "gguf"])
+def test_gemv_input_range(gpu_ctx, oracle_lib, t, m, n, layout):
+    """Batch 1 (x as int8 digits with a power-of-two exponent per 32-block):
+    each kind of extreme row of the batched test as its own call, on every
+    batch-1 kernel (6144 x 2048 and 2048 x 6144: the one-launch row GEMV;
+    16384 x 256: the panel GEMV without a K split; the GGUF-layout GEMV)."""
+    w = oracle_lib.gen_quant(t, 57, m + n + t, m, n, std=0.02)
+    x = extreme_rows(oracle_lib, 8, n, 700 + n)
+    if layout == "panel":
+        dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
+    else:
+        dw, dp = gpu_ctx.to_device(w), None
+    y = np.empty((8, m), np.float32)
+    for b in range(8):
+        dx, dy = gpu_ctx.to_device(x[b:b + 1]), gpu_ctx.alloc(m * 4)
+        if layout == "panel":
+            gpu_ctx.call("quant_gemm_packed", t, dp, m, n, dx, 1, dy)
+        else:
+            gpu_ctx.quant_gemm(t, dw, m, n, dx, 1, dy)
+        y[b] = dy.download(np.float32, m)
+        dx.free()
+        dy.free()
+    check_extreme(y, x, w, t, m, n, oracle_lib)
+    dw.free()
+    if dp is not None:
+        dp.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("layout", ["panel", "gguf"])
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_gemv_nonfinite_input(gpu_ctx, oracle_lib, t, layout, bad):
+    """An inf or NaN in x makes every output non-finite, as in the reference
+    (q8_gemv.rs:234-242: the product with a nonzero weight is +-inf, with a
+    zero weight NaN, and either swamps the row's sum); this build returns NaN
+    for each row whose block holds it, i.e. every row."""
+    m, n = 2048, 2048
+    w = oracle_lib.gen_quant(t, 58, 3, m, n, std=0.02)
+    x = oracle_lib.normal(9, 4, n).reshape(1, n)
+    x[0, 777] = bad
+    ref = oracle_lib.gemm(t, w, m, n, x)
+    assert not np.any(np.isfinite(ref))
+    dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(m * 4)
+    if layout == "panel":
+        dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
+        gpu_ctx.call("quant_gemm_packed", t, dp, m, n, dx, 1, dy)
+        dp.free()
+    else:
+        dw = gpu_ctx.to_device(w)
+        gpu_ctx.quant_gemm(t, dw, m, n, dx, 1, dy)
+    y = dy.download(np.float32, m)
+    assert not np.any(np.isfinite(y))
+    for b in (dw, dx, dy):
+        b.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
 @pytest.mark.parametrize("batch", [2, 17, 32])
 @pytest.mark.parametrize("m,n", [(2048, 2048), (100, 256)])
 def test_gguf_gemm_input_range(gpu_ctx, oracle_lib, t, batch, m, n):
