@@ -283,13 +283,41 @@ __device__ __forceinline__ void arg_better(int32_t &k, uint32_t &i, int32_t k2, 
     }
 }
 
-__device__ __forceinline__ void block_argmax(int32_t &k, uint32_t &i, int32_t *rk, uint32_t *ri) {
+// (key, index) as one unsigned 64-bit value (the key's sign bit flipped on
+// top, the index below): the larger value is the better pair of arg_better.
+__device__ __forceinline__ uint64_t arg_pack(int32_t k, uint32_t i) {
+    return ((uint64_t)((uint32_t)k ^ 0x80000000u) << 32) | i;
+}
+
+// v and its DPP partner's value, the larger kept (both halves moved by DPP)
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
+    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+    const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xf, 0xf, false) << 32) |
+                       (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xf, 0xf, false);
+    return o > v ? o : v;
+}
+
+// The wave's best (key, index) on DPP: quad_perm xor 1, xor 2, then the
+// half-row and row mirrors (each lane ends with its 16-lane row's best), and
+// the 4 rows through readlane.  Every lane of the wave must be active.
+__device__ __forceinline__ void wave_argmax(int32_t &k, uint32_t &i) {
+    uint64_t v = arg_pack(k, i);
+    v = dpp_max_u64<0x140>(dpp_max_u64<0x141>(dpp_max_u64<0x4E>(dpp_max_u64<0xB1>(v))));
+    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+    uint64_t best = 0;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        int32_t k2 = __shfl_xor(k, o);
-        uint32_t i2 = __shfl_xor(i, o);
-        arg_better(k, i, k2, i2);
+    for (int r = 0; r < 4; r++) {
+        const uint64_t c = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, 16 * r) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane(lo, 16 * r);
+        best = c > best ? c : best;
     }
+    k = (int32_t)((uint32_t)(best >> 32) ^ 0x80000000u);
+    i = (uint32_t)best;
+}
+
+__device__ __forceinline__ void block_argmax(int32_t &k, uint32_t &i, int32_t *rk, uint32_t *ri) {
+    wave_argmax(k, i);
     if ((threadIdx.x & 63) == 0) {
         rk[threadIdx.x >> 6] = k;
         ri[threadIdx.x >> 6] = i;
@@ -342,12 +370,7 @@ __global__ __launch_bounds__(64) void argmax_stage2(const int32_t *__restrict__ 
     const size_t b = blockIdx.x;
     int32_t k = pk[b * kArgBlocks + threadIdx.x];
     uint32_t i = pi[b * kArgBlocks + threadIdx.x];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        int32_t k2 = __shfl_xor(k, o);
-        uint32_t i2 = __shfl_xor(i, o);
-        arg_better(k, i, k2, i2);
-    }
+    wave_argmax(k, i);
     if (threadIdx.x == 0) {
         out[b] = i;
         if (next) next[b] = i;
