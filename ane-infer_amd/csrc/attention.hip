@@ -464,10 +464,12 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
     }
 }
 
-// Chunks per (sequence, kv head): at most 128 (the combine merges at most
-// 128 partials per head), at most one per 64-position tile of the cache, and
-// about one workgroup per CU over the launch (batch 32, 2 kv heads: 4
-// chunks; batch 1: 128).  Longer chunks at batch > 1 amortise each
+// Chunks per (sequence, kv head): at most 128, at most one per 64-position
+// tile of the cache, and about one workgroup per CU over the launch
+// (kAttnWorkgroups / (batch x kv heads): batch 32 with 2 kv heads 4 chunks,
+// batch 1 with 2 kv heads 128, with 4 kv heads 64).  256 chunks at batch 1
+// were slower at 32k (the o_proj prologue merges twice the partials:
+// 1049 against 1064 tok/s).  Longer chunks at batch > 1 amortise each
 // workgroup's q / k preparation and partial write (batch 32, capacity =
 // context 1k / 8k / 32k: 20.6k / 15.4k / 8.4k tok/s at ~256 workgroups
 // against 20.1–20.3k / 14.7–14.9k / 8.4k at ~2048).
