@@ -347,6 +347,35 @@ int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
 int launch_gemv_fused(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m,
                       uint32_t n, const GemvInput &in, float *out, int ksplit);
 
+// Batch-1 DeltaNet step fused into the ssm_out GEMV (gemv.hip:
+// dn_ssm_kernel).  The kernel reads the recurrent state and the conv windows
+// but writes neither (the workgroups of a K split share each head's state):
+// the head outputs are formed as o = S'^T q + delta (k . q) from the old
+// state, and the update's inputs -- delta [H][128], the normalised k [H][128],
+// decay [H], the new conv inputs [3 dim] -- go to a per-layer pending block of
+// kDnPendFloats(dim, H) floats; launch_deltanet_apply commits every layer's
+// update at the end of the step.
+__host__ __device__ constexpr size_t kDnPendFloats(size_t dim, size_t n_heads) { return 5 * dim + n_heads; }
+constexpr int kMaxDnApplyLayers = 64;
+struct DnApplyTab {
+    float *S[kMaxDnApplyLayers];
+    float *conv[kMaxDnApplyLayers];
+    const float *pend[kMaxDnApplyLayers];
+    int n = 0;
+};
+// Whether the fused kernel covers this model at batch 1 (head dim 128, an
+// even number of heads, one panel of ssm_out input per K split).
+bool dn_ssm_fusable(const anehip_ctx *ctx, uint32_t dim, uint32_t n_heads);
+// ssm_out partials [dim / 256][dim] of the batch-1 step; mix: the mixer-in
+// projection [q | k | v (3 dim)][gate (dim)][beta (H)][alpha (H)].
+int launch_dn_ssm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t dim,
+                  uint32_t n_heads, const MixIn &mix, const float *conv_w, const float *conv_state, const float *ssm_a,
+                  const float *dt_bias, const float *S, const float *norm_w, float eps, float *pend, float *out);
+// Commits the pending updates of tab's layers: S = decay S + k delta^T
+// (deltanet.rs:485-512 order), conv windows shifted and the new inputs
+// appended (deltanet_cache.rs:34-42).
+int launch_deltanet_apply(anehip_ctx *ctx, hipStream_t stream, const DnApplyTab &tab, int n_heads, int dim);
+
 // deltanet.hip.  mix: qkv [3*chunk]; beta, alpha: [n_heads] per sequence.
 int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,

@@ -84,6 +84,10 @@ struct Model {
     float *x0 = nullptr, *x1 = nullptr;                  // residual stream (two buffers, alternating)
     float *pmix = nullptr, *p0 = nullptr, *p1 = nullptr;  // GEMV outputs as K-split partial slices
     float *heads = nullptr, *attn_out = nullptr, *logits = nullptr, *attn_part = nullptr;
+    // batch 1 with the fused DeltaNet + ssm_out kernel: the DeltaNet layers'
+    // pending state updates (kDnPendFloats each, in layer order), committed
+    // by one apply launch at the end of the step; null otherwise
+    float *dn_pend = nullptr;
     float *xin = nullptr;        // GEMM input planes (batch > 1): hi then lo, xin_len halves each,
                                  // then the group exponents (xe_cnt bytes)
     size_t xin_len = 0;          // fragment-order plane of the widest GEMM input (32 rows)
@@ -151,8 +155,8 @@ void free_state(Model *M) {
         L.conv_state = L.S = nullptr;
         L.kc = L.vc = nullptr;
     }
-    void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->d_hist, M->x0,       M->x1,        M->pmix,      M->p0,
-                    M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->xin};
+    void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->d_hist,    M->x0,        M->x1,  M->pmix,   M->p0,
+                    M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->xin, M->dn_pend};
     for (void *p : bufs) free_ptr(p);
     void *pfb[] = {M->pf.x, M->pf.xn, M->pf.pmix, M->pf.p0, M->pf.p1, M->pf.attn_part, M->pf.logits, M->pf.xin,
                    M->pf.d_tokens, M->pf.d_pos};
@@ -165,6 +169,7 @@ void free_state(Model *M) {
     M->d_pos = M->d_tokens = M->d_sampled = M->d_hist = M->h_tokens = nullptr;
     M->x0 = M->x1 = M->pmix = M->p0 = M->p1 = M->heads = M->attn_out = M->logits = M->attn_part = nullptr;
     M->xin = nullptr;
+    M->dn_pend = nullptr;
     M->argmax_ws = nullptr;
     M->batch = M->max_seq = 0;
     M->host_pos.clear();
@@ -322,6 +327,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
     float *cur = M->x0, *nxt = M->x1;
     const float *prev_part = nullptr;
     int prev_kp = 0;
+    DnApplyTab tab;  // the fused DeltaNet layers' pending updates
     for (uint32_t l = 0; l < D.n_layers; l++) {
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
@@ -350,7 +356,18 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         // 2. mixer core, 3. output projection (its input formed in the prologue)
         GemvInput in3;
         uint32_t cols3;
-        if (dn) {
+        if (dn && M->dn_pend) {
+            // DeltaNet step fused into ssm_out; its state update is committed
+            // after the last layer (launch_deltanet_apply)
+            float *pend = M->dn_pend + (size_t)tab.n * kDnPendFloats(d, H);
+            TRY(launch_dn_ssm(ctx, s, L.mix_out.type, L.mix_out.p, d, H, mix, L.conv1d, L.conv_state, L.ssm_a,
+                              L.dt_bias, L.S, L.ssm_norm, eps, pend, M->p0));
+            tab.S[tab.n] = L.S;
+            tab.conv[tab.n] = L.conv_state;
+            tab.pend[tab.n] = pend;
+            tab.n++;
+            cols3 = d;
+        } else if (dn) {
             TRY(launch_deltanet_step(ctx, s, 1, (int)H, mix, mix.shifted((int)(C + d)), mix.shifted((int)(C + d + H)),
                                      L.conv1d, L.ssm_a, L.dt_bias, L.conv_state, L.S, M->heads));
             in3.mode = GEMV_IN_GATED_NORM;
@@ -388,8 +405,8 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
                 in3.x = M->attn_out;
             }
         }
-        const int k3 = gemv_packed_ksplit(ctx, d, cols3);
-        TRY(launch_gemv_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, in3, M->p0, k3));
+        const int k3 = dn && M->dn_pend ? (int)(d / 256) : gemv_packed_ksplit(ctx, d, cols3);
+        if (!(dn && M->dn_pend)) TRY(launch_gemv_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, in3, M->p0, k3));
         // 4. FFN gate/up, input = RMSNorm(residual + mixer output)
         GemvInput in4;
         in4.mode = GEMV_IN_RESID_RMSNORM;
@@ -414,6 +431,7 @@ int enqueue_step_b1(anehip_ctx *ctx, Model *M, hipStream_t s) {
         prev_part = M->p0;
         prev_kp = k5;
     }
+    if (tab.n) TRY(launch_deltanet_apply(ctx, s, tab, (int)H, (int)d));
     // lm_head, input = final RMSNorm(residual + last FFN output), formed once
     // by its own kernel: as a prologue each of the lm_head's ~1200 workgroups
     // would re-read the residual and every partial slice (measured 19 us)
@@ -987,6 +1005,12 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     if (M->rows_attn) {
         const int G = (int)(D.n_heads / D.n_kv_heads);
         r = r ? r : alloc((void **)&M->attn_part, attn_partial_floats((int)batch, (int)D.n_kv_heads, (int)max_seq, G) * sizeof(float));
+    }
+    if (batch == 1 && M->rows_dn && dn_ssm_fusable(ctx, (uint32_t)d, (uint32_t)H)) {
+        size_t n_dn = 0;
+        for (const Layer &L : M->layers) n_dn += L.type == ANEHIP_LAYER_DELTANET;
+        if (n_dn <= (size_t)kMaxDnApplyLayers)
+            r = r ? r : alloc((void **)&M->dn_pend, n_dn * kDnPendFloats(d, H) * sizeof(float));
     }
     if (!r && hipHostMalloc((void **)&M->h_tokens, 64 * sizeof(uint32_t), 0) != hipSuccess) {
         M->h_tokens = nullptr;

@@ -611,6 +611,53 @@ int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_he
     return ANEHIP_OK;
 }
 
+namespace {
+
+// The batch-1 step's deferred state updates (launch_deltanet_apply): grid =
+// (kDk / kCols, n_heads, layers); thread (cq, rg) takes columns c0 + 4 cq ..
+// + 3 and rows 4 rg .. + 3 of head h, as deltanet_step_kernel does, and
+// applies S' = decay S, S'' = S' + k delta^T in that order; threads < 3 kCols
+// commit the conv windows of the q, k and v channels of those columns.
+__global__ __launch_bounds__(kThreads) void dn_apply_kernel(DnApplyTab tab, int n_heads, int d) {
+    const int t = threadIdx.x, slice = blockIdx.x, h = blockIdx.y, l = blockIdx.z;
+    float *S = tab.S[l];
+    float *conv = tab.conv[l];
+    const float *pend = tab.pend[l];
+    const int c0 = slice * kCols;
+    const int cq = t & 7, rg = t >> 3;
+    const float decay = pend[2 * d + h];
+    const float4 delta = *reinterpret_cast<const float4 *>(pend + h * kDk + c0 + 4 * cq);
+    const float4 kv = *reinterpret_cast<const float4 *>(pend + d + h * kDk + 4 * rg);
+    const float kr[4] = {kv.x, kv.y, kv.z, kv.w};
+    float *Sh = S + (size_t)h * kDk * kDk + c0 + 4 * cq;
+    float4 s[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(4 * rg + r) * kDk);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
+        s[r].x += kr[r] * delta.x; s[r].y += kr[r] * delta.y; s[r].z += kr[r] * delta.z; s[r].w += kr[r] * delta.w;
+        *reinterpret_cast<float4 *>(Sh + (size_t)(4 * rg + r) * kDk) = s[r];
+    }
+    if (t < 3 * kCols) {
+        const int ch = (t / kCols) * d + h * kDk + c0 + t % kCols;
+        float4 *w = reinterpret_cast<float4 *>(conv + (size_t)ch * kKsize);
+        const float4 o = *w;
+        *w = make_float4(o.y, o.z, o.w, pend[2 * d + n_heads + ch]);
+    }
+}
+
+}  // namespace
+
+int launch_deltanet_apply(anehip_ctx *ctx, hipStream_t stream, const DnApplyTab &tab, int n_heads, int dim) {
+    if (tab.n <= 0 || tab.n > kMaxDnApplyLayers || dim != n_heads * kDk)
+        return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_apply: %d layers, dim %d, %d heads", tab.n, dim, n_heads);
+    hipLaunchKernelGGL(dn_apply_kernel, dim3(kDk / kCols, n_heads, tab.n), dim3(kThreads), 0, stream, tab, n_heads,
+                       dim);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
 int launch_deltanet_head(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
                          const float *dt_bias, float *conv_state, float *S, float *out, int gate_off,

@@ -990,6 +990,186 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
     }
 }
 
+// Batch-1 DeltaNet step fused into the ssm_out GEMV (one launch per DeltaNet
+// layer instead of two).  The ssm_out GEMV takes one K split per panel, i.e.
+// per two 128-wide heads; workgroup (split ks, row tile) runs the step of
+// heads 2 ks and 2 ks + 1 itself (the 32 row tiles of a split each recompute
+// it), forms their gated-RMSNorm outputs as the GEMV's input slice and
+// multiplies its tile.  The recurrent state and the conv windows are read,
+// not written: the head output is o = S'^T q + delta (k . q) with S' = decay
+// S and delta = beta (v - S'^T k) (the same value as S''^T q with S'' = S' +
+// k delta^T, deltanet.rs:485-512), and the split's row-tile-0 workgroup
+// leaves delta, k, decay and the new conv inputs in `pend` for
+// launch_deltanet_apply.  Thread t: head hh = t / 256; within the head the
+// layout of deltanet_head_kernel (a q or k channel, the v channel t % 128;
+// columns 4 cq .. + 3 and rows 16 rg .. + 15 of the state).  The linear
+// workgroup index puts a split's workgroups on one XCD (blockIdx % 8).
+constexpr int kDnDk = 128;
+constexpr int kDnK = 4;  // conv width
+
+struct DnSsmArgs {
+    MixIn mix, beta, alpha;  // [q | k | v][gate], [n_heads], [n_heads]
+    const float *conv_w = nullptr, *conv_state = nullptr, *ssm_a = nullptr, *dt_bias = nullptr, *S = nullptr;
+    const float *norm_w = nullptr;
+    float *pend = nullptr;
+    int n_heads = 0, d = 0;
+    float eps = 0.0f;
+};
+
+__device__ __forceinline__ float silu_dn(float x) { return x / (1.0f + expf(-x)); }
+
+template <uint32_t T, int KP>
+__global__ __launch_bounds__(kWave *kPackedWaves) void dn_ssm_kernel(const uint8_t *__restrict__ Wp, DnSsmArgs a,
+                                                                    float *__restrict__ out, int m, int nsplit) {
+    constexpr int V = PanelPart<T, 1>::kVecs;
+    __shared__ float qn[2][kDnDk], kn[2][kDnDk], vv[2][kDnDk];
+    __shared__ __align__(16) float4 pk[2][8][32], pq[2][8][32];  // [head][row group][column quad]
+    __shared__ float red[kPackedWaves], red2[kPackedWaves];
+    __shared__ __align__(16) uint32_t xd[8 * kXdWords];
+    __shared__ uint4 xq[8];
+    __shared__ float gred[kPackedWaves][kWave];
+    const int t = threadIdx.x, lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int ks = blockIdx.x % nsplit, tile = blockIdx.x / nsplit;
+    const int hh = t >> 8, tt = t & 255, e = tt & (kDnDk - 1);
+    const int d = a.d, h = 2 * ks + hh, C = 3 * d;
+    const bool writer = tile == 0;
+    const int nsb = d >> 8;
+
+    // small inputs first, then the weights, then the state (in-order waits)
+    const int ch = tt < kDnDk ? h * kDnDk + tt : d + h * kDnDk + e, chv = 2 * d + h * kDnDk + e;
+    const float4 win = *reinterpret_cast<const float4 *>(a.conv_state + (size_t)ch * kDnK);
+    const float4 wk = *reinterpret_cast<const float4 *>(a.conv_w + (size_t)ch * kDnK);
+    const float4 winv = *reinterpret_cast<const float4 *>(a.conv_state + (size_t)chv * kDnK);
+    const float4 wkv = *reinterpret_cast<const float4 *>(a.conv_w + (size_t)chv * kDnK);
+    float xa[KP], xv[KP], xb[KP], xl[KP];
+    a.mix.load<KP>(0, ch, xa);
+    a.mix.load<KP>(0, chv, xv);
+    a.beta.load<KP>(0, h, xb);
+    a.alpha.load<KP>(0, h, xl);
+    // gate, columns 4 (lane % 32) .. + 3 of the head (used by lanes < 32 of waves 0 and 4)
+    float4 gz[KP];
+    {
+        const float *g0 = a.mix.p + C + h * kDnDk + 4 * (lane & 31);
+#pragma unroll
+        for (int q = 0; q < KP; q++)
+            gz[q] = *reinterpret_cast<const float4 *>(g0 + (size_t)min(q, a.mix.kp - 1) * a.mix.split);
+    }
+    const float sa = a.ssm_a[h], dtb = a.dt_bias[h];
+    const float4 nw = reinterpret_cast<const float4 *>(a.norm_w)[lane & 31];
+    u32x4 q[V], sc;
+    load_part<T, 1>(q, sc, Wp + ((size_t)tile * nsb + ks) * Panel<T>::kBytes, Wp, wave, lane, true);
+    asm volatile("" ::: "memory");
+    const int cq = tt & 31, rg = tt >> 5;
+    const float *Sh = a.S + ((size_t)h * kDnDk) * kDnDk + 4 * cq;
+    float4 s[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(16 * rg + r) * kDnDk);
+
+    // 1. conv + SiLU (deltanet_cache.rs:34-54) from the old windows; beta and
+    // decay (deltanet.rs:474-480)
+    const auto conv = [](float4 w0, float4 k, float x) {
+        float sum = 0.0f;
+        sum += w0.y * k.x;
+        sum += w0.z * k.y;
+        sum += w0.w * k.z;
+        sum += x * k.w;
+        return silu_dn(sum);
+    };
+    const float xin = a.mix.add<KP>(xa), xvin = a.mix.add<KP>(xv);
+    const float y = conv(win, wk, xin);
+    const float sq = wave_sum(y * y);  // waves 4 hh + 0 / 1: q, 4 hh + 2 / 3: k
+    if (lane == 0) red[wave] = sq;
+    if (tt < kDnDk) qn[hh][tt] = y;
+    else kn[hh][e] = y;
+    if (tt < kDnDk) vv[hh][tt] = conv(winv, wkv, xvin);
+    const float beta = 1.0f / (1.0f + expf(-a.beta.add<KP>(xb)));
+    const float decay = expf(sa * logf(1.0f + expf(a.alpha.add<KP>(xl) + dtb)));
+    if (writer) {
+        float *px = a.pend + 2 * d + a.n_heads;  // new conv inputs [3 d]
+        px[ch] = xin;
+        if (tt < kDnDk) px[chv] = xvin;
+        if (tt == 0) a.pend[2 * d + h] = decay;
+    }
+    __syncthreads();
+    // 2. L2 normalise (deltanet.rs:25-31, 461-467)
+    if (tt < kDnDk) {
+        const float inv = 1.0f / sqrtf((red[4 * hh] + red[4 * hh + 1]) + 1e-12f);
+        qn[hh][tt] = (qn[hh][tt] * inv) * (1.0f / sqrtf((float)kDnDk));
+    } else {
+        const float inv = 1.0f / sqrtf((red[4 * hh + 2] + red[4 * hh + 3]) + 1e-12f);
+        kn[hh][e] = kn[hh][e] * inv;
+    }
+    __syncthreads();
+    // 3. S' = decay S, partial sums of S'^T k and S'^T q over this thread's
+    // rows; k . q by the head's first two waves
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sqv = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const float ki = kn[hh][16 * rg + r], qi = qn[hh][16 * rg + r];
+        s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
+        sk.x += s[r].x * ki; sk.y += s[r].y * ki; sk.z += s[r].z * ki; sk.w += s[r].w * ki;
+        sqv.x += s[r].x * qi; sqv.y += s[r].y * qi; sqv.z += s[r].z * qi; sqv.w += s[r].w * qi;
+    }
+    pk[hh][rg][cq] = sk;
+    pq[hh][rg][cq] = sqv;
+    {
+        const float kq = wave_sum(tt < kDnDk ? kn[hh][tt] * qn[hh][tt] : 0.0f);
+        if (lane == 0) red2[wave] = kq;
+    }
+    if (writer && tt < kDnDk) a.pend[d + h * kDnDk + tt] = kn[hh][tt];
+    __syncthreads();
+    // 4. o = S'^T q + delta (k . q), delta = beta (v - S'^T k); gated RMSNorm
+    // (deltanet.rs:517-533) into the digits of the GEMV input: lanes < 32 of
+    // waves 0 and 4 hold 4 columns each of heads 2 ks and 2 ks + 1
+    if ((wave & 3) == 0) {
+        const int c4 = lane & 31;
+        float4 a4 = pk[hh][0][c4], b4 = pq[hh][0][c4];
+#pragma unroll
+        for (int g = 1; g < 8; g++) {
+            const float4 x = pk[hh][g][c4], z = pq[hh][g][c4];
+            a4 = make_float4(a4.x + x.x, a4.y + x.y, a4.z + x.z, a4.w + x.w);
+            b4 = make_float4(b4.x + z.x, b4.y + z.y, b4.z + z.z, b4.w + z.w);
+        }
+        const float kq = red2[4 * hh] + red2[4 * hh + 1];
+        const float4 v4 = *reinterpret_cast<const float4 *>(&vv[hh][4 * c4]);
+        const float4 dl = make_float4(beta * (v4.x - a4.x), beta * (v4.y - a4.y), beta * (v4.z - a4.z),
+                                      beta * (v4.w - a4.w));
+        const float4 o = make_float4(b4.x + dl.x * kq, b4.y + dl.y * kq, b4.z + dl.z * kq, b4.w + dl.w * kq);
+        if (writer && lane < 32) *reinterpret_cast<float4 *>(a.pend + h * kDnDk + 4 * c4) = dl;
+        float4 g = gz[0];
+#pragma unroll
+        for (int p = 1; p < KP; p++) {
+            const bool on = p < a.mix.kp;
+            g.x += on ? gz[p].x : 0.0f;
+            g.y += on ? gz[p].y : 0.0f;
+            g.z += on ? gz[p].z : 0.0f;
+            g.w += on ? gz[p].w : 0.0f;
+        }
+        const float ss = half_sum(o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w);
+        const float inv_rms = 1.0f / sqrtf(ss / (float)kDnDk + a.eps);
+        const float4 u = make_float4(((o.x * inv_rms) * nw.x) * silu_dn(g.x), ((o.y * inv_rms) * nw.y) * silu_dn(g.y),
+                                     ((o.z * inv_rms) * nw.z) * silu_dn(g.z), ((o.w * inv_rms) * nw.w) * silu_dn(g.w));
+        put_digits<T>(u, 32 * hh + lane, lane < 32, xd, xq);
+    }
+    __syncthreads();
+    // 5. the tile's rows over the split's panel: wave w takes block w (two
+    // row tiles per workgroup, halving the state re-reads, measured slower:
+    // 1189 against 1210 tok/s at batch 1)
+    const float acc = panel_dot<T, 1>(q, sc, xd, xq, wave, 0.0f);
+    gred[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        const int row = tile * kWave + lane;
+        if (row < m) {
+            float sum = gred[0][lane];
+#pragma unroll
+            for (int w = 1; w < kPackedWaves; w++) sum += gred[w][lane];
+            out[(size_t)ks * m + row] = sum;
+        }
+    }
+}
+
 // Batch-1 GEMV of a matrix with few row tiles, in one launch: a workgroup of
 // 16 waves takes R = 64 / H rows of one tile over the whole K range, so the
 // grid has tiles * H workgroups and no K split (no partial sums, no second
@@ -2785,6 +2965,49 @@ int launch_gemv_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     if (ggml_type == ANEHIP_GGML_Q8_0)
         return dispatch_packed<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, in, out, ksplit);
     return dispatch_packed<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, in, out, ksplit);
+}
+
+bool dn_ssm_fusable(const anehip_ctx *ctx, uint32_t dim, uint32_t n_heads) {
+    return dim == n_heads * (uint32_t)kDnDk && n_heads % 2 == 0 &&
+           gemv_packed_ksplit(ctx, dim, dim, GEMV_IN_GATED_NORM) == (int)(dim / 256);
+}
+
+int launch_dn_ssm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t dim,
+                  uint32_t n_heads, const MixIn &mix, const float *conv_w, const float *conv_state, const float *ssm_a,
+                  const float *dt_bias, const float *S, const float *norm_w, float eps, float *pend, float *out) {
+    if (!dn_ssm_fusable(ctx, dim, n_heads) || mix.kp < 1 || mix.kp > kMaxSplit)
+        return set_error(ctx->err, ANEHIP_EINVAL, "dn_ssm: dim %u, %u heads, %d K splits not covered", dim, n_heads,
+                         mix.kp);
+    DnSsmArgs a;
+    a.mix = mix;
+    a.beta = mix.shifted((int)(4 * dim));
+    a.alpha = mix.shifted((int)(4 * dim + n_heads));
+    a.conv_w = conv_w;
+    a.conv_state = conv_state;
+    a.ssm_a = ssm_a;
+    a.dt_bias = dt_bias;
+    a.S = S;
+    a.norm_w = norm_w;
+    a.pend = pend;
+    a.n_heads = (int)n_heads;
+    a.d = (int)dim;
+    a.eps = eps;
+    const int nsplit = (int)(dim / 256), tiles = (int)((dim + kWave - 1) / kWave);
+    const dim3 grid(tiles * nsplit), block(kWave * kPackedWaves);
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+#define ANEHIP_DN(TT, KK) \
+    hipLaunchKernelGGL((dn_ssm_kernel<TT, KK>), grid, block, 0, stream, wb, a, out, (int)dim, nsplit)
+    const bool q8 = ggml_type == ANEHIP_GGML_Q8_0;
+    if (mix.kp == 1) {
+        if (q8) ANEHIP_DN(ANEHIP_GGML_Q8_0, 1);
+        else ANEHIP_DN(ANEHIP_GGML_Q4_0, 1);
+    } else {
+        if (q8) ANEHIP_DN(ANEHIP_GGML_Q8_0, kMaxSplit);
+        else ANEHIP_DN(ANEHIP_GGML_Q4_0, kMaxSplit);
+    }
+#undef ANEHIP_DN
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
 }
 
 int launch_split_x(anehip_ctx *ctx, hipStream_t stream, const float *x, uint32_t batch, uint32_t n, const Planes &xp) {

@@ -38,11 +38,9 @@ def test_small_model_steps_from_zero(small_host):
         print(f"step {i}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
         assert l2 <= TOL and mx <= TOL
     assert gm.get_pos(0) == 10 and oseq.pos == 10
-    # recurrent state after 10 steps
-    for l in range(small_host.spec.n_layers):
-        if small_host.spec.layer_types[l] == anehip.LAYER_DELTANET:
-            S = gm.get_state(l, 1)
-            assert max(rel_errs(S, oseq.view(l, 1, S.size, np.float32))) <= TOL
+    # recurrent states, conv windows and KV rows after 10 steps (at batch 1
+    # the DeltaNet updates are committed by the step's last kernels)
+    _check_state(gm, oseq, 0, small_host.spec, "after 10 steps")
     gm.close()
     oseq.close()
 
@@ -123,6 +121,7 @@ def test_prefill_matches_token_steps(small_host, n):
     _check_state(gm, oseq, 0, spec, "after prefill")
     for t in oracle.randint(32, n, 3, spec.vocab_size):
         assert max(rel_errs(gm.step([t])[0], oseq.forward(int(t)))) <= TOL
+    _check_state(gm, oseq, 0, spec, "after prefill and 3 steps")
     gm.close()
     oseq.close()
 
@@ -351,9 +350,11 @@ def _fill_state(gm, spec, seed=0):
                 gm.fill_random(p, n // 2, 0, seed + 300 + 10 * l + which, 0.0, 1.0, f16=True)
 
 
-def _step_vs_oracle(host, gm, positions, check, tok_seed, steps=1, label=""):
+def _step_vs_oracle(host, gm, positions, check, tok_seed, steps=1, label="", dn_state=False):
     """Sets every sequence's position, copies the checked sequences' state to
-    oracle sequences and compares `steps` decode steps' logits."""
+    oracle sequences and compares `steps` decode steps' logits (and with
+    dn_state, the checked sequences' DeltaNet states and conv windows after
+    the last step)."""
     spec = host.spec
     for b, p in enumerate(positions):
         gm.set_pos(b, int(p))
@@ -370,6 +371,13 @@ def _step_vs_oracle(host, gm, positions, check, tok_seed, steps=1, label=""):
             print(f"{label} step {step} seq {b} pos {int(positions[b]) + step}: rel_l2={l2:.2e} rel_max={mx:.2e}",
                   flush=True)
             assert l2 <= TOL and mx <= TOL, (label, step, b)
+    if dn_state:
+        for b in check:
+            for l in range(spec.n_layers):
+                if spec.layer_types[l] == anehip.LAYER_DELTANET:
+                    for which in (0, 1):
+                        g = gm.get_state(l, which, b)
+                        assert max(rel_errs(g, seqs[b].view(l, which, g.size, np.float32))) <= TOL, (label, l, which)
     for q in seqs.values():
         q.close()
 
@@ -380,11 +388,12 @@ def test_qwen35_2b_shape_step(big_host, ctx_len, batch):
     """Random-init 24-layer Qwen3.5-2B shape, Q8_0 weights, fp16 KV cache
     filled with N(0,1) at positions < ctx-1, DeltaNet states N(0, 0.01)
     (windows N(0,1)); one step at pos = ctx-1 (cache capacity = ctx) vs the
-    oracle, sequences 0 and batch-1."""
+    oracle, sequences 0 and batch-1: logits, then the DeltaNet states and
+    conv windows."""
     gm = _model(big_host, batch, ctx_len)
     _fill_state(gm, big_host.spec)
     _step_vs_oracle(big_host, gm, [ctx_len - 1] * batch, sorted({0, batch - 1}), 12,
-                    label=f"2B ctx={ctx_len} B={batch}")
+                    label=f"2B ctx={ctx_len} B={batch}", dn_state=True)
     gm.close()
 
 
