@@ -603,7 +603,10 @@ struct PanelPart {
 
 // Loads one wave's share of a panel.  Idle waves (valid false) load one
 // 16-byte vector of the panel base with all lanes instead, so every wave
-// issues the same, unconditional load sequence.
+// issues the same, unconditional load sequence.  The scale vector goes
+// first: every block's dot product needs it, and with it first (vmcnt waits
+// are in issue order) block j waits only for its own quant vectors, so the
+// dot products run while the later blocks are still arriving.
 template <uint32_t T, int NB>
 __device__ __forceinline__ void load_part(u32x4 *q, u32x4 &sc, const uint8_t *panel, const uint8_t *dummy, int part,
                                           int lane, bool valid) {
@@ -611,9 +614,15 @@ __device__ __forceinline__ void load_part(u32x4 *q, u32x4 &sc, const uint8_t *pa
     const int l = valid ? lane : 0;
     constexpr int V = PanelPart<T, NB>::kVecs;
     const int c0 = valid ? V * part : 0;
-#pragma unroll
-    for (int c = 0; c < V; c++) q[c] = __builtin_nontemporal_load(p4 + (c0 + c) * 64 + l);
+    // the scheduling barriers keep this issue order (and the loads together)
+    __builtin_amdgcn_sched_barrier(0);
     sc = __builtin_nontemporal_load(p4 + Panel<T>::kChunks * 64 + l);
+#pragma unroll
+    for (int c = 0; c < V; c++) {
+        __builtin_amdgcn_sched_barrier(0);
+        q[c] = __builtin_nontemporal_load(p4 + (c0 + c) * 64 + l);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Dot product of a wave's panel share held in registers (q, sc: see
@@ -946,35 +955,9 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
     auto digits = [&](float4 v, int i4, bool ok) { put_digits<T>(v, i4, ok, xd, xq); };
 
     u32x4 q[V], sc;
-    for (int tile = t0; tile < t1; tile++) {
-        const uint8_t *tb = Wp + (size_t)tile * tile_bytes;
-        float acc = 0.0f;
-        if (fast) {
-            const int sb = sb_begin + pi;
-            const bool valid = sb < sb_end;
-            const uint8_t *pp = tb + (size_t)sb * Panel<T>::kBytes;
-            if (tile == t0) {
-                // the slice's digits are formed once and kept for later tiles
-                auto issue = [&]() { load_part<T, NB>(q, sc, pp, Wp, part, lane, valid); };
-                prologue_overlapped<MODE, KP, NT>(in, n, sb_begin * 256, (sb_end - sb_begin) * 256, redw, issue,
-                                                  digits);
-            } else {
-                load_part<T, NB>(q, sc, pp, Wp, part, lane, valid);
-            }
-            if (valid) acc = panel_dot<T, NB>(q, sc, xd + pi * 8 * kXdWords, xq + pi * 8, part, acc);
-        } else {
-            for (int r0 = sb_begin; r0 < sb_end; r0 += P) {
-                const int r1 = min(sb_end, r0 + P);
-                const int sb = r0 + pi;
-                const bool valid = sb < r1;
-                load_part<T, NB>(q, sc, tb + (size_t)sb * Panel<T>::kBytes, Wp, part, lane, valid);
-                if (r0 != sb_begin) __syncthreads();  // the previous round's reads of xd are done
-                gemv_prologue<MODE, 2, NT>(in, n, r0 * 256, (r1 - r0) * 256, xs, redw, tile == t0 && r0 == sb_begin);
-                digitize_lds<T, NT>(xs, (r1 - r0) * 256, xd, xq);
-                __syncthreads();
-                if (valid) acc = panel_dot<T, NB>(q, sc, xd + (sb - r0) * 8 * kXdWords, xq + (sb - r0) * 8, part, acc);
-            }
-        }
+    // the 8 waves' sums of a tile through LDS; the result (times the input's
+    // deferred factor) goes out
+    auto finish = [&](int tile, float acc, float scale) {
         red[wave][lane] = acc;
         __syncthreads();
         if (wave == 0) {
@@ -983,10 +966,49 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void gemv_packed(const uint8_t
                 float sum = red[0][lane];
 #pragma unroll
                 for (int v = 1; v < kPackedWaves; v++) sum += red[v][lane];
-                out[(size_t)ks * split_stride + row] = fast ? sum * post_scale<MODE, NT>(in, n, redw) : sum;
+                out[(size_t)ks * split_stride + row] = sum * scale;
             }
         }
         __syncthreads();  // red (and, in the generic path, xs and xd) are reused by the next tile
+    };
+    if (fast) {
+        // a loop of its own: joined with the generic path's code, the dot
+        // products would wait for every load either path may have pending
+        const int sb = sb_begin + pi;
+        const bool valid = sb < sb_end;
+        float scale = 1.0f;
+        for (int tile = t0; tile < t1; tile++) {
+            const uint8_t *pp = Wp + (size_t)tile * tile_bytes + (size_t)sb * Panel<T>::kBytes;
+            if (tile == t0) {
+                // the slice's digits are formed once and kept for later tiles
+                auto issue = [&]() { load_part<T, NB>(q, sc, pp, Wp, part, lane, valid); };
+                prologue_overlapped<MODE, KP, NT>(in, n, sb_begin * 256, (sb_end - sb_begin) * 256, redw, issue,
+                                                  digits);
+                scale = post_scale<MODE, NT>(in, n, redw);
+            } else {
+                load_part<T, NB>(q, sc, pp, Wp, part, lane, valid);
+            }
+            float acc = 0.0f;
+            if (valid) acc = panel_dot<T, NB>(q, sc, xd + pi * 8 * kXdWords, xq + pi * 8, part, acc);
+            finish(tile, acc, scale);
+        }
+        return;
+    }
+    for (int tile = t0; tile < t1; tile++) {
+        const uint8_t *tb = Wp + (size_t)tile * tile_bytes;
+        float acc = 0.0f;
+        for (int r0 = sb_begin; r0 < sb_end; r0 += P) {
+            const int r1 = min(sb_end, r0 + P);
+            const int sb = r0 + pi;
+            const bool valid = sb < r1;
+            load_part<T, NB>(q, sc, tb + (size_t)sb * Panel<T>::kBytes, Wp, part, lane, valid);
+            if (r0 != sb_begin) __syncthreads();  // the previous round's reads of xd are done
+            gemv_prologue<MODE, 2, NT>(in, n, r0 * 256, (r1 - r0) * 256, xs, redw, tile == t0 && r0 == sb_begin);
+            digitize_lds<T, NT>(xs, (r1 - r0) * 256, xd, xq);
+            __syncthreads();
+            if (valid) acc = panel_dot<T, NB>(q, sc, xd + (sb - r0) * 8 * kXdWords, xq + (sb - r0) * 8, part, acc);
+        }
+        finish(tile, acc, 1.0f);
     }
 }
 
