@@ -454,7 +454,7 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
         const int e = group_exp(half_max32(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])))));
         h4v vh, vl;  // 4 consecutive columns of a fragment-order plane
         split4_scaled(v, e, vh, vl);
-        const size_t o = xf_index(b, h * kHd + 4 * l);
+        const size_t o = xf_index(b, h * kHd + 4 * l, n_heads * kHd);
         *reinterpret_cast<h4v *>(xp.hi + o) = vh;
         *reinterpret_cast<h4v *>(xp.lo + o) = vl;
         if ((l & 31) == 0) xp.xe[xe_index(b, h * kHd + 4 * l, n_heads * kHd)] = (int8_t)e;

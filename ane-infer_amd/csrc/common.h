@@ -208,9 +208,12 @@ int launch_unpack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const
 // lane that holds it in the A operand of v_mfma_f32_32x32x16_f16 (lane
 // b + 32 * ((c / 8) % 2), 8 consecutive columns per lane), so a wave loads
 // one step's operand with one fully contiguous 1 KiB load.  Rows past the
-// batch are never read.
-__host__ __device__ inline size_t xf_index(int b, int c) {
-    return ((size_t)(c >> 4) * 64 + (size_t)(b + 32 * ((c >> 3) & 1))) * 8 + (size_t)(c & 7);
+// batch are never read.  More than 32 rows (the prefill's chunks) are stored
+// as consecutive 32-row planes, each xf_plane_len(n) halves: row b lies in
+// plane b / 32 at row b % 32, and each 32-row group is one GEMM's input.
+__host__ __device__ inline size_t xf_index(int b, int c, int n) {
+    return (size_t)(b >> 5) * 32 * (size_t)n +
+           ((size_t)(c >> 4) * 64 + (size_t)((b & 31) + 32 * ((c >> 3) & 1))) * 8 + (size_t)(c & 7);
 }
 inline size_t xf_plane_len(size_t n) { return 32 * n; }
 
@@ -235,6 +238,14 @@ inline size_t xe_bytes(size_t n) { return 32 * (size_t)xe_stride((int)n); }
 struct Planes {
     _Float16 *hi = nullptr, *lo = nullptr;
     int8_t *xe = nullptr;
+    // the planes of rows 32 g .. 32 g + 31 for an n-column input
+    Planes group(int g, int n) const {
+        Planes p;
+        p.hi = hi ? hi + (size_t)g * xf_plane_len((size_t)n) : nullptr;
+        p.lo = lo ? lo + (size_t)g * xf_plane_len((size_t)n) : nullptr;
+        p.xe = xe ? xe + (size_t)g * 32 * xe_stride(n) : nullptr;
+        return p;
+    }
 };
 __host__ __device__ __forceinline__ int xe_index(int b, int c, int n) { return b * xe_stride(n) + c / kXeGroup; }
 // Group exponent from the group's largest |x|.
@@ -320,8 +331,16 @@ __device__ __forceinline__ _Float16 xe_factor(int e, int E) { return (_Float16)l
 // hi / lo outputs of the element-wise kernels), ksplit from gemm_packed_ksplit.
 // m must be a multiple of 4.
 int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
+// split_stride: floats between the K splits' outputs (0: batch * m).
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
-                       uint32_t n, const Planes &xp, uint32_t batch, float *out, int ksplit);
+                       uint32_t n, const Planes &xp, uint32_t batch, float *out, int ksplit, size_t split_stride = 0);
+// The same for any number of rows: rows above 32 (the prefill's chunks) run
+// as one launch per 32-row group of the planes (Planes::group), writing
+// out[ks][row][r] with a split stride of rows * m; ksplit from
+// gemm_rows_ksplit, the same for every group.
+int gemm_rows_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t rows);
+int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
+                     const Planes &xp, uint32_t rows, float *out, int ksplit);
 // Whether gemm_packed_ksplit's split of [m x n] at this batch runs on an
 // x-stationary kernel, which can also take x as fp32 rows [batch][n] (no
 // planes needed): launch_gemm_xs_rows writes out[ks][b][r] for its

@@ -64,6 +64,11 @@ struct Layer {
 
 }  // namespace
 
+// Tokens per prefill chunk: the rows of the chunk's GEMMs (launched per
+// 32-row group) and of its element-wise, DeltaNet and attention kernels.
+constexpr uint32_t kPrefillRows = 128;
+constexpr uint32_t kPrefillGroups = kPrefillRows / 32;
+
 struct Model {
     anehip_model_desc desc{};
     std::vector<uint8_t> types;
@@ -111,7 +116,9 @@ struct Model {
     }
     size_t planes_bytes() const { return 2 * xin_len * sizeof(_Float16) + xe_cnt; }
     Planes planes() const { return planes_at(xin, xin_len); }
-    Planes pf_planes() const { return planes_at(pf.xin, xin_len); }
+    // prefill: kPrefillGroups 32-row planes of each (Planes::group)
+    size_t pf_planes_bytes() const { return kPrefillGroups * planes_bytes(); }
+    Planes pf_planes() const { return planes_at(pf.xin, kPrefillGroups * xin_len); }
     // graph
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -598,7 +605,6 @@ int pack_weights(anehip_ctx *ctx, Model *M) {
     return pack_mat(ctx, M->lm_head);
 }
 
-constexpr uint32_t kPrefillRows = 32;  // tokens per prefill chunk (rows of the MFMA GEMM)
 
 // K-split partial floats of the prefill's GEMMs at up to kPrefillRows rows
 // (the split depends on the rows only through rows <= 16 or not), of the
@@ -612,7 +618,7 @@ size_t prefill_part_floats(anehip_ctx *ctx, Model *M) {
     mx = std::max(mx, (size_t)kPrefillRows * (3 * d + 2 * D.ssm_group_count));
     for (auto &e : g)
         for (uint32_t rows : {16u, kPrefillRows})
-            if (e[0]) mx = std::max(mx, (size_t)gemm_packed_ksplit(ctx, e[0], e[1], rows) * rows * e[0]);
+            if (e[0]) mx = std::max(mx, (size_t)gemm_rows_ksplit(ctx, e[0], e[1], rows) * rows * e[0]);
     return mx;
 }
 
@@ -633,7 +639,7 @@ int alloc_prefill(anehip_ctx *ctx, Model *M) {
     } a[] = {{(void **)&M->pf.x, kPrefillRows * d * 4}, {(void **)&M->pf.xn, kPrefillRows * d * 4},
              {(void **)&M->pf.pmix, part * 4}, {(void **)&M->pf.p0, part * 4}, {(void **)&M->pf.p1, part * 4},
              {(void **)&M->pf.attn_part, std::max<size_t>(attn, 1) * 4}, {(void **)&M->pf.logits, (size_t)D.vocab_size * 4},
-             {(void **)&M->pf.xin, M->planes_bytes()}, {(void **)&M->pf.d_tokens, kPrefillRows * 4},
+             {(void **)&M->pf.xin, M->pf_planes_bytes()}, {(void **)&M->pf.d_tokens, kPrefillRows * 4},
              {(void **)&M->pf.d_pos, kPrefillRows * 4}};
     for (auto &e : a) {
         if (hipMalloc(e.p, e.bytes) != hipSuccess) {
@@ -663,8 +669,8 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
         const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
-        const int k1 = gemm_packed_ksplit(ctx, rows_in, d, T);
-        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xp, T, M->pf.pmix, k1));
+        const int k1 = gemm_rows_ksplit(ctx, rows_in, d, T);
+        TRY(launch_gemm_rows(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xp, T, M->pf.pmix, k1));
         MixIn mix;
         mix.p = M->pf.pmix;
         mix.kp = k1;
@@ -684,14 +690,14 @@ int enqueue_prefill_chunk(anehip_ctx *ctx, Model *M, hipStream_t s, uint32_t seq
                                          xp));
             cols3 = D.n_heads * D.head_dim;
         }
-        const int k3 = gemm_packed_ksplit(ctx, d, cols3, T);
-        TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xp, T, M->pf.p0, k3));
+        const int k3 = gemm_rows_ksplit(ctx, d, cols3, T);
+        TRY(launch_gemm_rows(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xp, T, M->pf.p0, k3));
         TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k3, L.post_attn_norm, nullptr, eps, xp));
-        const int k4 = gemm_packed_ksplit(ctx, 2 * F, d, T);
-        TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, T, M->pf.p1, k4));
+        const int k4 = gemm_rows_ksplit(ctx, 2 * F, d, T);
+        TRY(launch_gemm_rows(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, T, M->pf.p1, k4));
         TRY(launch_silu_mul_stacked(ctx, s, T, (int)F, M->pf.p1, k4, nullptr, xp));
-        const int k5 = gemm_packed_ksplit(ctx, d, F, T);
-        TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xp, T, M->pf.p0, k5));
+        const int k5 = gemm_rows_ksplit(ctx, d, F, T);
+        TRY(launch_gemm_rows(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xp, T, M->pf.p0, k5));
         if (l + 1 < D.n_layers)
             TRY(launch_residual_rmsnorm(ctx, s, T, (int)d, x, M->pf.p0, k5, M->layers[l + 1].attn_norm, nullptr, eps,
                                         xp));

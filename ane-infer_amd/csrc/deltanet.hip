@@ -43,7 +43,7 @@ __device__ __forceinline__ float silu_ref(float x) { return x / (1.0f + expf(-x)
 // ulps, which only moves the scaled maximum within [2^14, 2^15] by as much).
 __device__ __forceinline__ void head_to_planes(float v, int b, int c0, int n, int e, const Planes &xp) {
     const int t = threadIdx.x;
-    const size_t o = xf_index(b, c0 + t);
+    const size_t o = xf_index(b, c0 + t, n);
     split_scaled(v, e, xp.hi[o], xp.lo[o]);
     if (t == 0) xp.xe[xe_index(b, c0, n)] = (int8_t)e;
 }
@@ -436,16 +436,17 @@ __global__ __launch_bounds__(kThreads) void dn_prep_kernel(MixIn mix, MixIn mbet
 // The recurrence is independent per value column j (recall sk_j, delta_j,
 // column j of the rank-1 update and the query o_j), so a head is split over
 // kDk / C single-wave workgroups of C columns each, grid = (kDk / C, n_heads).
-// The workgroup first copies its head's q and k of all T tokens, its columns'
-// v and the tokens' beta and decay into LDS; the token loop then has no global
-// load.  Lane l holds rows R (l % G) .. + R - 1 of column C g + l / G (G =
+// The workgroup copies its head's q and k, its columns' v and the tokens' beta
+// and decay into LDS, kScanMaxT tokens at a time; the token loop then has no
+// global load.  Lane l holds rows R (l % G) .. + R - 1 of column C g + l / G (G =
 // 64 / C lanes per column, R = 128 / G rows per lane) in registers across all
 // T steps (state read and written once per chunk); a sum over rows is 4
 // interleaved partial sums of R / 4 rows, then a DPP sum over the column's G
 // consecutive lanes.  Raw head outputs go to out[t][chunk].
 constexpr int kWave = 64;
 constexpr int kScanCols = 4;
-constexpr int kScanMaxT = 32;
+constexpr int kScanMaxT = 32;    // tokens staged in LDS at a time
+constexpr int kScanMaxRows = 256;  // tokens per launch
 constexpr int kDropOffset = 0x7ffffff0;  // buffer offset past any output: the store is dropped
 
 // sum over each 16-lane row: row_ror 8, 4, 2, 1
@@ -469,60 +470,67 @@ __global__ __launch_bounds__(kWave) void deltanet_scan_kernel(const float *__res
     float st[R];
 #pragma unroll
     for (int r = 0; r < R; r++) st[r] = Sh[(size_t)(R * rgp + r) * kDk];
-    // all loads of a half of the tokens in flight at once (clamped to the last
-    // token; slots past T are never read): lane l copies float4 l of q | k,
-    // lanes 0..C-1 also v of column l, lanes >= C beta (even) / decay (odd)
-#pragma unroll
-    for (int b0 = 0; b0 < kScanMaxT; b0 += kScanMaxT / 2) {
-        float4 qk[kScanMaxT / 2];
-        float ex[kScanMaxT / 2];
-#pragma unroll
-        for (int i = 0; i < kScanMaxT / 2; i++) {
-            const int b = min(b0 + i, T - 1);
-            const float *src = prep + ((size_t)b * n_heads + h) * 3 * kDk;
-            qk[i] = reinterpret_cast<const float4 *>(src)[l];
-            ex[i] = l < C ? src[2 * kDk + blockIdx.x * C + l] : bd[((size_t)b * n_heads + h) * 2 + (l & 1)];
-        }
-#pragma unroll
-        for (int i = 0; i < kScanMaxT / 2; i++) {
-            reinterpret_cast<float4 *>(qks[b0 + i])[l] = qk[i];
-            exs[b0 + i][l] = ex[i];
-        }
-    }
-    __syncthreads();
     const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(out, 0, 4 * T * chunk, 0x00020000);
     const auto colsum = [](float v) { return G == 16 ? sum16(v) : sum8(v); };
-    for (int b = 0; b < T; b++) {
-        const float beta = exs[b][C], decay = exs[b][C + 1], v = exs[b][jl];
-        float kr[R], qr[R];
+    // the tokens in sub-chunks of kScanMaxT, the state in registers throughout
+    for (int c0 = 0; c0 < T; c0 += kScanMaxT) {
+        if (c0) __syncthreads();  // the previous sub-chunk's reads of qks / exs are done
+        // all loads of a half of the sub-chunk in flight at once (clamped to
+        // the last token; slots past T are never read): lane l copies float4 l
+        // of q | k, lanes 0..C-1 also v of column l, lanes >= C beta (even) /
+        // decay (odd)
 #pragma unroll
-        for (int r = 0; r < R; r += 4) {
-            const float4 k4 = *reinterpret_cast<const float4 *>(&qks[b][kDk + R * rgp + r]);
-            const float4 q4 = *reinterpret_cast<const float4 *>(&qks[b][R * rgp + r]);
-            kr[r] = k4.x, kr[r + 1] = k4.y, kr[r + 2] = k4.z, kr[r + 3] = k4.w;
-            qr[r] = q4.x, qr[r + 1] = q4.y, qr[r + 2] = q4.z, qr[r + 3] = q4.w;
+        for (int b0 = 0; b0 < kScanMaxT; b0 += kScanMaxT / 2) {
+            float4 qk[kScanMaxT / 2];
+            float ex[kScanMaxT / 2];
+#pragma unroll
+            for (int i = 0; i < kScanMaxT / 2; i++) {
+                const int b = min(c0 + b0 + i, T - 1);
+                const float *src = prep + ((size_t)b * n_heads + h) * 3 * kDk;
+                qk[i] = reinterpret_cast<const float4 *>(src)[l];
+                ex[i] = l < C ? src[2 * kDk + blockIdx.x * C + l] : bd[((size_t)b * n_heads + h) * 2 + (l & 1)];
+            }
+#pragma unroll
+            for (int i = 0; i < kScanMaxT / 2; i++) {
+                reinterpret_cast<float4 *>(qks[b0 + i])[l] = qk[i];
+                exs[b0 + i][l] = ex[i];
+            }
         }
-        // S' = decay S; sk_j = sum_i S'_ij k_i
-        float p[4] = {0.f, 0.f, 0.f, 0.f};
+        __syncthreads();
+        const int te = min(kScanMaxT, T - c0);
+        for (int bb = 0; bb < te; bb++) {
+            const int b = c0 + bb;
+            const float beta = exs[bb][C], decay = exs[bb][C + 1], v = exs[bb][jl];
+            float kr[R], qr[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            st[r] *= decay;
-            p[r & 3] += st[r] * kr[r];
+            for (int r = 0; r < R; r += 4) {
+                const float4 k4 = *reinterpret_cast<const float4 *>(&qks[bb][kDk + R * rgp + r]);
+                const float4 q4 = *reinterpret_cast<const float4 *>(&qks[bb][R * rgp + r]);
+                kr[r] = k4.x, kr[r + 1] = k4.y, kr[r + 2] = k4.z, kr[r + 3] = k4.w;
+                qr[r] = q4.x, qr[r + 1] = q4.y, qr[r + 2] = q4.z, qr[r + 3] = q4.w;
+            }
+            // S' = decay S; sk_j = sum_i S'_ij k_i
+            float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                st[r] *= decay;
+                p[r & 3] += st[r] * kr[r];
+            }
+            const float sk = colsum((p[0] + p[1]) + (p[2] + p[3]));
+            const float delta = beta * (v - sk);
+            // S'' = S' + k delta^T; o_j = sum_i S''_ij q_i
+#pragma unroll
+            for (int r = 0; r < 4; r++) p[r] = 0.f;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                st[r] += kr[r] * delta;
+                p[r & 3] += st[r] * qr[r];
+            }
+            const float o = colsum((p[0] + p[1]) + (p[2] + p[3]));
+            // lanes of row group 0 store (the others' offset is past the buffer: dropped)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o), orsrc,
+                                                  rgp == 0 ? 4 * (b * chunk + h * kDk + j) : kDropOffset, 0, 0);
         }
-        const float sk = colsum((p[0] + p[1]) + (p[2] + p[3]));
-        const float delta = beta * (v - sk);
-        // S'' = S' + k delta^T; o_j = sum_i S''_ij q_i
-#pragma unroll
-        for (int r = 0; r < 4; r++) p[r] = 0.f;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            st[r] += kr[r] * delta;
-            p[r & 3] += st[r] * qr[r];
-        }
-        const float o = colsum((p[0] + p[1]) + (p[2] + p[3]));
-        // lanes of row group 0 store (the others' offset is past the buffer: dropped)
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o), orsrc,
-                                              rgp == 0 ? 4 * (b * chunk + h * kDk + j) : kDropOffset, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < R; r++) Sh[(size_t)(R * rgp + r) * kDk] = st[r];
@@ -588,9 +596,9 @@ int launch_deltanet_scan(anehip_ctx *ctx, hipStream_t stream, int rows, int n_he
                          const float *dt_bias, float *conv_state, float *S, float *prep, float *heads,
                          int gate_off, const float *norm_w, float eps, const Planes &xp) {
     const int kp = max(mix.kp, max(beta.kp, alpha.kp));
-    if (kp > 16 || rows < 1 || rows > kScanMaxT)
+    if (kp > 16 || rows < 1 || rows > kScanMaxRows)
         return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_scan: %d K splits (at most 16), %d rows (1..%d)", kp, rows,
-                         kScanMaxT);
+                         kScanMaxRows);
     float *bd = prep + (size_t)rows * n_heads * 3 * kDk;
 #define DN_SCAN(KP)                                                                                                  \
     hipLaunchKernelGGL(dn_prep_kernel<KP>, dim3(n_heads, rows), dim3(kThreads), 0, stream, mix, beta, alpha, conv_w, \

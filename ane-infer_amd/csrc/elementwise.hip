@@ -55,7 +55,7 @@ __device__ __forceinline__ void rmsnorm_row(const float *x, const float *__restr
     for (int i = threadIdx.x; i < n; i += kThreads) {
         const float v = (x[i] * inv_rms) * w[i];
         const int e = group_exp(__int_as_float(gmax[i / kXeGroup]));
-        split_scaled(v, e, xp.hi[xf_index(brow, i)], xp.lo[xf_index(brow, i)]);
+        split_scaled(v, e, xp.hi[xf_index(brow, i, n)], xp.lo[xf_index(brow, i, n)]);
         if (i % kXeGroup == 0) xp.xe[xe_index(brow, i, n)] = (int8_t)e;
     }
 }
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(512) void residual_rmsnorm_v4(float *__restrict__ x
         // columns 4t .. 4t + 3 are consecutive in a fragment-order plane
         h4v vh, vl;
         split4_scaled(v, e, vh, vl);
-        const size_t o = xf_index((int)b, 4 * t);
+        const size_t o = xf_index((int)b, 4 * t, n);
         *reinterpret_cast<h4v *>(xp.hi + o) = vh;
         *reinterpret_cast<h4v *>(xp.lo + o) = vl;
         if ((t & 31) == 0) xp.xe[xe_index((int)b, 4 * t, n)] = (int8_t)e;
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restr
         const int w0 = (threadIdx.x >> 6) & ~1;
         const int e = group_exp(fmaxf(wm[w0], wm[w0 + 1]));
         if (!in) return;
-        split_scaled(v, e, xp.hi[xf_index((int)b, r)], xp.lo[xf_index((int)b, r)]);
+        split_scaled(v, e, xp.hi[xf_index((int)b, r, F)], xp.lo[xf_index((int)b, r, F)]);
         if (r % kXeGroup == 0) xp.xe[xe_index((int)b, r, F)] = (int8_t)e;
     } else if (in) {
         h[b * F + r] = v;
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_v4(const float *__restrict_
         // columns r .. r + 3 (r % 4 == 0) are consecutive in a fragment-order plane
         h4v vh, vl;
         split4_scaled(v, e, vh, vl);
-        const size_t o = xf_index(b, r);
+        const size_t o = xf_index(b, r, F);
         *reinterpret_cast<h4v *>(xp.hi + o) = vh;
         *reinterpret_cast<h4v *>(xp.lo + o) = vl;
         if ((threadIdx.x & 31) == 0) xp.xe[xe_index(b, r, F)] = (int8_t)e;

@@ -2314,8 +2314,8 @@ __global__ __launch_bounds__(256) void split_x_frag_kernel(const float *__restri
         h[e] = hh;
         l[e] = ll;
     }
-    *reinterpret_cast<h8v *>(xp.hi + xf_index(b, c)) = h;
-    *reinterpret_cast<h8v *>(xp.lo + xf_index(b, c)) = l;
+    *reinterpret_cast<h8v *>(xp.hi + xf_index(b, c, n)) = h;
+    *reinterpret_cast<h8v *>(xp.lo + xf_index(b, c, n)) = l;
     if ((g & 15) == 0) xp.xe[xe_index(b, c, n)] = (int8_t)ex;
 }
 
@@ -2697,11 +2697,11 @@ int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t b
 // on lm_head at batch 32, slower at batch 4 and 16 and on the small shapes.)
 template <uint32_t T>
 int launch_gemm_packed_t(anehip_ctx *ctx, hipStream_t stream, const uint8_t *w, uint32_t m, uint32_t n,
-                         const Planes &xp, uint32_t batch, float *out, int ksplit, int per) {
+                         const Planes &xp, uint32_t batch, float *out, int ksplit, int per, size_t ss) {
     const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const int items = tiles * ksplit;
     hipLaunchKernelGGL((gemm_packed<T, 1, kGemmRing>), dim3(min(items, 2 * cus)), dim3(kWave * kGemmWaves), 0, stream,
-                       w, xp, out, (int)m, (int)n, (int)batch, ksplit, per, (size_t)batch * m);
+                       w, xp, out, (int)m, (int)n, (int)batch, ksplit, per, ss);
     return ANEHIP_OK;
 }
 
@@ -2730,10 +2730,10 @@ static GemmKernel gemm_kernel(uint32_t batch, int nsb, int ksplit) {
 // workgroups per split in every case.
 template <uint32_t T>
 void launch_gemm_xs_any(anehip_ctx *ctx, hipStream_t stream, GemmKernel kind, const uint8_t *w, uint32_t m,
-                        uint32_t n, const Planes &xp, const float *xrows, uint32_t batch, float *out, int ksplit) {
+                        uint32_t n, const Planes &xp, const float *xrows, uint32_t batch, float *out, int ksplit,
+                        size_t ss) {
     const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const int per = (int)(n / 256) / ksplit;
-    const size_t ss = (size_t)batch * m;
     const int wgs = kind == GemmKernel::Xs16 ? (per == 1 ? 4 : 2) : kind == GemmKernel::Xs32 ? 3 : 1;
     const int gs = max(1, min(tiles, wgs * cus / ksplit));
     const dim3 grid(gs * ksplit);
@@ -2777,51 +2777,71 @@ bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch) {
     return gemm_kernel(batch, (int)(n / 256), gemm_packed_ksplit(ctx, m, n, batch)) != GemmKernel::Persistent;
 }
 
-static int check_gemm_args(anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch, int ksplit) {
+static int check_gemm_args(anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch, int ksplit, size_t ss) {
     const int nsb = (int)(n / 256), per = split_len(nsb, ksplit);
-    if (ksplit < 1 || (ksplit - 1) * per >= nsb || batch < 1 || batch > 32 || m % 4)
+    if (ksplit < 1 || (ksplit - 1) * per >= nsb || batch < 1 || batch > 32 || m % 4 || ss < (size_t)batch * m)
         return set_error(ctx->err, ANEHIP_EINVAL,
-                         "gemm: K split %d of %d super-blocks, batch %u or m %u (multiple of 4) unsupported", ksplit,
-                         nsb, batch, m);
-    if (4.0 * ksplit * batch * m > 1073741824.0)  // output byte offsets stay below kBadOffset
-        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %u x %u floats too large", ksplit, batch, m);
+                         "gemm: K split %d of %d super-blocks, batch %u, m %u (multiple of 4) or split stride %zu "
+                         "unsupported",
+                         ksplit, nsb, batch, m, ss);
+    if (4.0 * ksplit * (double)ss > 1073741824.0)  // output byte offsets stay below kBadOffset
+        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm: output of %d x %zu floats too large", ksplit, ss);
     return ANEHIP_OK;
 }
 
 int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                         uint32_t n, const float *x, uint32_t batch, float *out) {
     const int ksplit = gemm_packed_ksplit(ctx, m, n, batch);
-    if (int rc = check_gemm_args(ctx, m, n, batch, ksplit)) return rc;
+    if (int rc = check_gemm_args(ctx, m, n, batch, ksplit, (size_t)batch * m)) return rc;
     const GemmKernel kind = gemm_kernel(batch, (int)(n / 256), ksplit);
     if (kind == GemmKernel::Persistent)
         return set_error(ctx->err, ANEHIP_EINVAL, "gemm: %u x %u at batch %u is not an x-stationary shape", m, n,
                          batch);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     if (ggml_type == ANEHIP_GGML_Q8_0)
-        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, Planes{}, x, batch, out, ksplit);
+        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, Planes{}, x, batch, out, ksplit,
+                                             (size_t)batch * m);
     else
-        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, Planes{}, x, batch, out, ksplit);
+        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, Planes{}, x, batch, out, ksplit,
+                                             (size_t)batch * m);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
-                       uint32_t n, const Planes &xp, uint32_t batch, float *out, int ksplit) {
-    if (int rc = check_gemm_args(ctx, m, n, batch, ksplit)) return rc;
+                       uint32_t n, const Planes &xp, uint32_t batch, float *out, int ksplit, size_t split_stride) {
+    const size_t ss = split_stride ? split_stride : (size_t)batch * m;
+    if (int rc = check_gemm_args(ctx, m, n, batch, ksplit, ss)) return rc;
     if (!xp.hi || !xp.lo || !xp.xe) return set_error(ctx->err, ANEHIP_EINVAL, "gemm: input planes incomplete");
     const int per = split_len((int)(n / 256), ksplit);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     const GemmKernel kind = gemm_kernel(batch, (int)(n / 256), ksplit);
     const bool q8 = ggml_type == ANEHIP_GGML_Q8_0;
     if (kind != GemmKernel::Persistent && q8)
-        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, xp, nullptr, batch, out, ksplit);
+        launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, xp, nullptr, batch, out, ksplit, ss);
     else if (kind != GemmKernel::Persistent)
-        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, xp, nullptr, batch, out, ksplit);
+        launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, xp, nullptr, batch, out, ksplit, ss);
     else if (q8)
-        launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xp, batch, out, ksplit, per);
+        launch_gemm_packed_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, xp, batch, out, ksplit, per, ss);
     else
-        launch_gemm_packed_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xp, batch, out, ksplit, per);
+        launch_gemm_packed_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, xp, batch, out, ksplit, per, ss);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int gemm_rows_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t rows) {
+    return gemm_packed_ksplit(ctx, m, n, std::min<uint32_t>(rows, 32));
+}
+
+int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
+                     const Planes &xp, uint32_t rows, float *out, int ksplit) {
+    if (rows <= 32) return launch_gemm_packed(ctx, stream, ggml_type, wp, m, n, xp, rows, out, ksplit);
+    for (uint32_t g = 0; 32 * g < rows; g++) {
+        const uint32_t b = std::min<uint32_t>(32, rows - 32 * g);
+        if (int rc = launch_gemm_packed(ctx, stream, ggml_type, wp, m, n, xp.group((int)g, (int)n), b,
+                                        out + (size_t)32 * g * m, ksplit, (size_t)rows * m))
+            return rc;
+    }
     return ANEHIP_OK;
 }
 

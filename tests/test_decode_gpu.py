@@ -103,7 +103,8 @@ def _check_state(gm, oseq, b, spec, what):
 
 @pytest.mark.parametrize("n", [1, 13, 45])
 def test_prefill_matches_token_steps(small_host, n):
-    """anehip_prefill of n prompt tokens (1, 13: one chunk; 45: 32 + 13) from
+    """anehip_prefill of n prompt tokens (one chunk; 45 rows run the GEMMs as
+    row groups of 32 + 13) from
     position 0 vs the oracle run token by token: the last token's logits, the
     DeltaNet states / conv windows and the KV rows written, then 3 decode
     steps continuing the sequence."""
@@ -128,7 +129,7 @@ def test_prefill_matches_token_steps(small_host, n):
 
 def test_prefill_one_sequence_of_a_batch(mid_host):
     """On the mid-size model (K-split projections), batch 3: after two decode
-    steps of every sequence, sequence 1 prefills 40 tokens (32 + 8) from
+    steps of every sequence, sequence 1 prefills 40 tokens (one chunk) from
     position 2; its logits and state follow the oracle, sequences 0 and 2 keep
     their state and positions, and a batched step afterwards matches the
     oracle for every sequence."""
@@ -426,12 +427,14 @@ def test_ragged_positions_across_chunk_boundaries(mid_host):
     gm.close()
 
 
-@pytest.mark.parametrize("n", [100])
+@pytest.mark.parametrize("n", [100, 300])
 def test_prefill_long_prompt_large_cache(mid_host, n):
-    """anehip_prefill of a 100-token prompt (chunks of 32, 32, 32, 4) into a
-    2048-position cache: chunk rows see 1 and 2 live tiles spread over the
-    attention's chunks; the last logits, states and KV rows vs the oracle run
-    token by token, then 2 decode steps."""
+    """anehip_prefill of a 100-token prompt (one chunk, GEMM row groups of 32,
+    32, 32, 4) and a 300-token one (chunks of 128, 128, 44: the two full chunks
+    replay the captured chunk graph, the DeltaNet scan runs 128 tokens per
+    launch) into a 2048-position cache: chunk rows see up to 5 live tiles of
+    attention; the last logits, states and KV rows vs the oracle run token by
+    token, then 2 decode steps."""
     spec = mid_host.spec
     gm = _model(mid_host, 1, 2048)
     oseq = mid_host.seq(2048)
@@ -450,7 +453,7 @@ def test_prefill_long_prompt_large_cache(mid_host, n):
 
 
 def test_qwen35_2b_shape_prefill(big_host):
-    """Random-init 24-layer Qwen3.5-2B shape: a 40-token prompt (32 + 8)
+    """Random-init 24-layer Qwen3.5-2B shape: a 40-token prompt (one chunk)
     prefilled from position 0 vs the oracle run token by token (last logits),
     then one decode step continuing the sequence."""
     spec = big_host.spec
