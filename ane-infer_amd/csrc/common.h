@@ -215,7 +215,7 @@ __host__ __device__ inline size_t xf_index(int b, int c, int n) {
     return (size_t)(b >> 5) * 32 * (size_t)n +
            ((size_t)(c >> 4) * 64 + (size_t)((b & 31) + 32 * ((c >> 3) & 1))) * 8 + (size_t)(c & 7);
 }
-inline size_t xf_plane_len(size_t n) { return 32 * n; }
+__host__ __device__ inline size_t xf_plane_len(size_t n) { return 32 * n; }
 
 // Range-safe planes.  fp16 alone covers 2^-24 .. 65504 and fp32 activations
 // do not stay inside it, so each batch row is stored in groups of 128
@@ -239,7 +239,7 @@ struct Planes {
     _Float16 *hi = nullptr, *lo = nullptr;
     int8_t *xe = nullptr;
     // the planes of rows 32 g .. 32 g + 31 for an n-column input
-    Planes group(int g, int n) const {
+    __host__ __device__ Planes group(int g, int n) const {
         Planes p;
         p.hi = hi ? hi + (size_t)g * xf_plane_len((size_t)n) : nullptr;
         p.lo = lo ? lo + (size_t)g * xf_plane_len((size_t)n) : nullptr;
@@ -334,10 +334,10 @@ int gemm_packed_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t b
 // split_stride: floats between the K splits' outputs (0: batch * m).
 int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                        uint32_t n, const Planes &xp, uint32_t batch, float *out, int ksplit, size_t split_stride = 0);
-// The same for any number of rows: rows above 32 (the prefill's chunks) run
-// as one launch per 32-row group of the planes (Planes::group), writing
+// The same for up to 256 rows: above 32 (the prefill's chunks) one gemm_tall
+// launch over the 32-row groups of the planes (Planes::group), writing
 // out[ks][row][r] with a split stride of rows * m; ksplit from
-// gemm_rows_ksplit, the same for every group.
+// gemm_rows_ksplit.
 int gemm_rows_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t rows);
 int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
                      const Planes &xp, uint32_t rows, float *out, int ksplit);

@@ -66,7 +66,7 @@ struct Layer {
 
 // Tokens per prefill chunk: the rows of the chunk's GEMMs (launched per
 // 32-row group) and of its element-wise, DeltaNet and attention kernels.
-constexpr uint32_t kPrefillRows = 128;
+constexpr uint32_t kPrefillRows = 256;
 constexpr uint32_t kPrefillGroups = kPrefillRows / 32;
 
 struct Model {
@@ -607,7 +607,8 @@ int pack_weights(anehip_ctx *ctx, Model *M) {
 
 
 // K-split partial floats of the prefill's GEMMs at up to kPrefillRows rows
-// (the split depends on the rows only through rows <= 16 or not), of the
+// (the split depends on the rows only through rows <= 16, <= 32, or the
+// number of 128-row blocks above 32), of the
 // batch-1 lm_head GEMV, and the DeltaNet scan's per-token inputs (q, k, v,
 // beta, decay; kept in the ffn partial buffer, which is free at that point).
 size_t prefill_part_floats(anehip_ctx *ctx, Model *M) {
@@ -617,7 +618,7 @@ size_t prefill_part_floats(anehip_ctx *ctx, Model *M) {
     size_t mx = (size_t)gemv_packed_ksplit(ctx, D.vocab_size, d) * D.vocab_size;
     mx = std::max(mx, (size_t)kPrefillRows * (3 * d + 2 * D.ssm_group_count));
     for (auto &e : g)
-        for (uint32_t rows : {16u, kPrefillRows})
+        for (uint32_t rows : {16u, 32u, kPrefillRows})  // the split depends on rows <= 16, <= 32 or above
             if (e[0]) mx = std::max(mx, (size_t)gemm_rows_ksplit(ctx, e[0], e[1], rows) * rows * e[0]);
     return mx;
 }

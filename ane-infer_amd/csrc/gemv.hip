@@ -2291,6 +2291,241 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
     } while (ct < tiles);
 }
 
+// Prefill GEMM: up to 256 rows of x (wave w takes rows 32 w .. 32 w + 31,
+// that group's 32-row planes) against 64-row weight tiles.  Work items are
+// (tile, K split); one workgroup per CU walks the panels ("units") of items
+// g, g + G, ... as one pipeline.  Per unit:
+//  * the panel was staged in LDS by direct global-to-LDS loads one unit
+//    ahead, and dequantised one unit ahead, once for all waves, into MFMA B
+//    fragments of w 2^s = (q d) 2^s as fp16 hi + lo (q d is exact in fp32:
+//    8 x 11 bits; hi + lo hold 22), s per weight row from the panel's
+//    largest |d| so that |hi| < 2^15 (weights far below the row's largest
+//    lose low bits of lo to fp16 subnormals: below 2^-24 of the row's scale);
+//    that dequantisation (VALU) runs between the unit's MFMAs;
+//  * each wave multiplies its rows' fragments of x (hi + lo at x 2^-E, E the
+//    row's largest group exponent) with them: x_hi w_hi + x_lo w_hi +
+//    x_hi w_lo on v_mfma_f32_32x32x16_f16 (x_lo w_lo is below 2^-44 of the
+//    product) over the panel's 256 columns, then adds the result times 2^-s
+//    to the item's sums; an item's sums go out at the start of the next one.
+// The products of q8_gemv.rs:234-242's (sum q x) d, up to fp32 rounding.
+// out[ks * split_stride + row * m + r] (rows past `rows` or m: not stored).
+constexpr int kTallWaves = 8;
+constexpr int kTallMaxRows = 32 * kTallWaves;
+
+// 16 bytes per lane from global memory straight into LDS: lane i's vector
+// lands at lds + 16 i (lds wave-uniform)
+__device__ __forceinline__ void global_to_lds16(const u32x4 *src, u32x4 *lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+
+// 8 weights (signed values q) of a B fragment from 8 staged bytes (Q8_0) or
+// 8 nibbles (Q4_0, q = nibble - 8), times ds, as fp16 hi + lo
+template <uint32_t T>
+__device__ __forceinline__ void tall_fragment(uint32_t w0, uint32_t w1, int nib_shift, float ds, h8v &hi, h8v &lo) {
+    const uint32_t w[2] = {w0, w1};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        int q;
+        if constexpr (T == ANEHIP_GGML_Q8_0) {
+            q = (int)(int8_t)(w[k >> 2] >> (8 * (k & 3)));
+        } else {
+            q = (int)((w[k >> 2] >> (8 * (k & 3) + nib_shift)) & 0xfu) - 8;
+        }
+        const float v = (float)q * ds;
+        const _Float16 h = (_Float16)v;
+        hi[k] = h;
+        lo[k] = (_Float16)(v - (float)h);
+    }
+}
+
+template <uint32_t T>
+__global__ __launch_bounds__(kWave *kTallWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_tall(
+    const uint8_t *__restrict__ Wp, Planes xp, float *__restrict__ out, int m, int n, int rows, int ksplit, int per,
+    size_t split_stride) {
+    constexpr int NTH = kWave * kTallWaves;
+    constexpr int VEC = Panel<T>::kBytes / 16;  // 16-byte vectors of a panel (a multiple of 64)
+    constexpr int PER_W = VEC / kWave;          // 1 KiB staging loads of a panel
+    static_assert(VEC % kWave == 0, "staging in whole 1 KiB wave loads");
+    static_assert(NTH % 128 == 0, "a thread's fragments share one weight row");
+    __shared__ u32x4 wq[VEC];               // the next unit's panel as stored
+    __shared__ h8v wf[2][2][16][2][kWave];  // B fragments [unit parity][hi / lo][16-column step][row half][lane]
+    __shared__ float sinv[2][kWave];        // 2^-s of each weight row [unit parity][row]
+    __shared__ int erow[kTallWaves][32];
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
+    const int items = tiles * ksplit, G = (int)gridDim.x;
+    // this workgroup's units: the panels of items g, g + G, ... in order
+    const int units = ((items - (int)blockIdx.x + G - 1) / G) * per;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int grows = rows - 32 * wave;  // rows of this wave's group (<= 0: it only stages and dequantises)
+    const bool active = grows > 0;
+    const Planes gp = xp.group(active ? wave : 0, n);
+    const int brow = min(lane & 31, (active ? min(grows, 32) : 1) - 1);  // rows past the group repeat its last
+    const int8_t *xe_row = gp.xe + (size_t)brow * xe_stride(n);
+    auto item_of = [&](int u) { return (int)blockIdx.x + G * (u / per); };
+    auto panel_of = [&](int u) { return (item_of(u) % ksplit) * per + u % per; };
+
+    // unit u's panel into wq: wave w issues loads w, w + 8, ...
+    auto stage = [&](int u) {
+        const int tile = item_of(u) / ksplit;
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(Wp + ((size_t)tile * nsb + panel_of(u)) * Panel<T>::kBytes);
+        for (int j = wave; j < PER_W; j += kTallWaves) global_to_lds16(src + kWave * j + lane, &wq[kWave * j]);
+    };
+    // wq -> B fragments of parity b: thread t takes fragments t, t + 512, ...
+    // of the 2048 (step s, row half h, lane l): weight row r = l % 32 + 32 h
+    // (the same for all of a thread's fragments), columns 16 s + 8 (l / 32)
+    // .. + 7; threads < 128 also leave 2^-s of their row
+    auto convert = [&](int b) {
+        const uint32_t *ws = reinterpret_cast<const uint32_t *>(wq);
+        const int l = threadIdx.x & 63, h = (threadIdx.x >> 6) & 1, r = (l & 31) + 32 * h, kh = l >> 5;
+        const u32x4 sv = wq[Panel<T>::kChunks * kWave + r];
+        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+        float dm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float a = __half2float(__ushort_as_half((unsigned short)(sw[i] & 0xffffu)));
+            const float c = __half2float(__ushort_as_half((unsigned short)(sw[i] >> 16)));
+            dm = fmaxf(dm, fmaxf(__builtin_isnan(a) ? INFINITY : fabsf(a), __builtin_isnan(c) ? INFINITY : fabsf(c)));
+        }
+        // 127 dm 2^s in [2^14, 2^15); s = 0 for an all-zero or non-finite row
+        const int sh = dm == 0.0f || dm == INFINITY ? 0 : 15 - __builtin_amdgcn_frexp_expf(127.0f * dm);
+        const float fac = ldexpf(1.0f, sh);
+        if (threadIdx.x < 128) sinv[b][r] = ldexpf(1.0f, -sh);
+#pragma unroll
+        for (int i = 0; i < 2048 / NTH; i++) {
+            const int st = (int)(threadIdx.x >> 7) + (NTH >> 7) * i;
+            const int blk = st >> 1;
+            const float d = __half2float(__ushort_as_half((unsigned short)(sw[blk >> 1] >> (16 * (blk & 1)))));
+            // Q8_0 chunk st: row r's columns 16 st .. + 15; Q4_0 chunk blk:
+            // byte i holds element i (low nibble) and i + 16 (high)
+            const uint32_t *c = ws + 4 * ((T == ANEHIP_GGML_Q8_0 ? st : blk) * kWave + r) + 2 * kh;
+            h8v hi, lo;
+            tall_fragment<T>(c[0], c[1], T == ANEHIP_GGML_Q8_0 ? 0 : 4 * (st & 1), d * fac, hi, lo);
+            wf[b][0][st][h][l] = hi;
+            wf[b][1][st][h][l] = lo;
+        }
+    };
+    // the quarter's x fragments: steps 16 p + 4 q + st of the group's planes
+    auto load_x = [&](int p, int q, h8v (&xa)[4], h8v (&xb)[4]) {
+        const size_t o = (size_t)(16 * p + 4 * q) * 512 + (size_t)(brow + 32 * (lane >> 5)) * 8;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            xa[st] = *reinterpret_cast<const h8v *>(gp.hi + o + 512 * st);
+            xb[st] = *reinterpret_cast<const h8v *>(gp.lo + o + 512 * st);
+        }
+    };
+    if (units > 0) stage(0);
+    // E over the whole row (one exponent for every K split of it)
+    int E = kXeEmpty;
+    for (int g = 0; g < 2 * nsb; g++) E = max(E, (int)xe_row[g]);
+    if (lane < 32) erow[wave][lane] = E;
+    f32x16 acc0 = {}, acc1 = {};
+    f32x16 c0, c1;
+    auto mma_quarter = [&](int b, int p, int q, const h8v (&xa)[4], const h8v (&xb)[4]) {
+        const _Float16 f = xe_factor(xe_row[2 * p + (q >> 1)], E);
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const h8v a = xa[st] * f, al = xb[st] * f;
+            const int s = 4 * q + st;
+            const h8v bh0 = wf[b][0][s][0][lane], bl0 = wf[b][1][s][0][lane];
+            const h8v bh1 = wf[b][0][s][1][lane], bl1 = wf[b][1][s][1][lane];
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh0, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh1, c1, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh0, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh1, c1, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl0, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl1, c1, 0, 0, 0);
+        }
+    };
+    // an item's sums: element r of lane l is row 8 (r / 4) + 4 (l / 32) +
+    // r % 4 of the group, weight row l % 32 (+ 32 for acc1) of the tile
+    auto store_item = [&](int item) {
+        const int tile = item / ksplit, ks = item % ksplit;
+        const int wr = tile * kWave + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int gr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (gr < grows) {
+                const float sc = xe_scale(erow[wave][gr]);
+                float *orow = out + (size_t)ks * split_stride + (size_t)(32 * wave + gr) * m;
+                if (wr < m) orow[wr] = acc0[r] * sc;
+                if (wr + 32 < m) orow[wr + 32] = acc1[r] * sc;
+            }
+        }
+        acc0 = f32x16{};
+        acc1 = f32x16{};
+    };
+    // wait for this wave's staging loads: all but the last 16 (the x loads of
+    // quarters 2 and 3, issued after them); waves without rows issue no x loads
+    auto wait_stage = [&]() {
+        if (active) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    if (units == 0) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // unit 0 staged, erow written
+    convert(0);
+    __syncthreads();  // unit 0's fragments ready, wq free
+    // unit 0's first x fragments before the next staging loads (every x
+    // wait then excludes those)
+    h8v xa0[4], xb0[4], xa1[4], xb1[4];
+    if (active) {
+        load_x(panel_of(0), 0, xa0, xb0);
+        load_x(panel_of(0), 1, xa1, xb1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (units > 1) stage(1);
+    for (int u = 0; u < units; u++) {
+        const int b = u & 1, p = panel_of(u);
+        const bool more = u + 1 < units;
+        if (active) {
+            c0 = f32x16{};
+            c1 = f32x16{};
+            __builtin_amdgcn_sched_barrier(0);
+            mma_quarter(b, p, 0, xa0, xb0);
+            __builtin_amdgcn_sched_barrier(0);
+            load_x(p, 2, xa0, xb0);
+            __builtin_amdgcn_sched_barrier(0);
+            mma_quarter(b, p, 1, xa1, xb1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_x(p, 3, xa1, xb1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (more) {
+            wait_stage();
+            __syncthreads();  // unit u + 1's panel is in wq
+        }
+        // an item's sums go out once its last unit is done (stores count in
+        // vmcnt: here they are older than the next staging loads)
+        if (active && u > 0 && u % per == 0) store_item(item_of(u - 1));
+        if (active) {
+            mma_quarter(b, p, 2, xa0, xb0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (more) load_x(panel_of(u + 1), 0, xa0, xb0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // unit u + 1's fragments (VALU and LDS) while the MFMAs drain
+        if (more) convert(b ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (active) {
+            mma_quarter(b, p, 3, xa1, xb1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (more) load_x(panel_of(u + 1), 1, xa1, xb1);
+            __builtin_amdgcn_sched_barrier(0);
+            // weight rows l % 32 and 32 + l % 32 of the tile
+            const float u0 = sinv[b][lane & 31], u1 = sinv[b][32 + (lane & 31)];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                acc0[r] = fmaf(c0[r], u0, acc0[r]);
+                acc1[r] = fmaf(c1[r], u1, acc1[r]);
+            }
+        }
+        __syncthreads();  // every wave is done with wq (convert) and with wf[b]
+        if (u + 2 < units) stage(u + 2);
+    }
+    if (active) store_item(item_of(units - 1));
+}
+
 // fp32 x[batch][n] -> range-safe fragment-order fp16 planes (hi + lo = x *
 // 2^-e per 128-column group, the exponents to xe), one thread per 8
 // consecutive columns of a row (one 16-byte fragment): a group is 16
@@ -2829,19 +3064,49 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     return ANEHIP_OK;
 }
 
+// K splits of gemm_tall: a divisor of the panel count (at most 16, the
+// partial slices a consumer sums) minimising the panels of the busiest CU,
+// ceil(workgroups / CUs) x panels per split; ties to fewer splits.
+static int gemm_tall_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+    const int tiles = (int)((m + kWave - 1) / kWave);
+    const int nsb = (int)(n / 256), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    int best = 1;
+    long best_cost = -1;
+    for (int k = 1; k <= nsb && k <= 16; k++) {
+        if (nsb % k) continue;
+        const long cost = (long)((tiles * k + cus - 1) / cus) * (nsb / k);
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = k;
+        }
+    }
+    return best;
+}
+
 int gemm_rows_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t rows) {
-    return gemm_packed_ksplit(ctx, m, n, std::min<uint32_t>(rows, 32));
+    return rows <= 32 ? gemm_packed_ksplit(ctx, m, n, rows) : gemm_tall_ksplit(ctx, m, n);
 }
 
 int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
                      const Planes &xp, uint32_t rows, float *out, int ksplit) {
     if (rows <= 32) return launch_gemm_packed(ctx, stream, ggml_type, wp, m, n, xp, rows, out, ksplit);
-    for (uint32_t g = 0; 32 * g < rows; g++) {
-        const uint32_t b = std::min<uint32_t>(32, rows - 32 * g);
-        if (int rc = launch_gemm_packed(ctx, stream, ggml_type, wp, m, n, xp.group((int)g, (int)n), b,
-                                        out + (size_t)32 * g * m, ksplit, (size_t)rows * m))
-            return rc;
-    }
+    const int nsb = (int)(n / 256), tiles = (int)((m + kWave - 1) / kWave);
+    if (rows > kTallMaxRows || ksplit < 1 || nsb % ksplit || m % 4 || !xp.hi || !xp.lo || !xp.xe)
+        return set_error(ctx->err, ANEHIP_EINVAL, "gemm_rows: %u rows (at most %d), K split %d of %d panels, m %u",
+                         rows, kTallMaxRows, ksplit, nsb, m);
+    if (4.0 * ksplit * rows * m > 1073741824.0)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm_rows: output of %d x %u x %u floats too large", ksplit, rows, m);
+    // one workgroup per CU, each walking its items' panels in one pipeline
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const dim3 grid((unsigned)std::min(tiles * ksplit, cus)), block(kWave * kTallWaves);
+    const uint8_t *w = static_cast<const uint8_t *>(wp);
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        hipLaunchKernelGGL(gemm_tall<ANEHIP_GGML_Q8_0>, grid, block, 0, stream, w, xp, out, (int)m, (int)n, (int)rows,
+                           ksplit, nsb / ksplit, (size_t)rows * m);
+    else
+        hipLaunchKernelGGL(gemm_tall<ANEHIP_GGML_Q4_0>, grid, block, 0, stream, w, xp, out, (int)m, (int)n, (int)rows,
+                           ksplit, nsb / ksplit, (size_t)rows * m);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
 

@@ -225,15 +225,17 @@ int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
                          ggml_type);
     if (m == 0 || n == 0 || n % 256)
         return set_error(ctx->err, ANEHIP_ESHAPE, "quant_gemm_packed: n=%u must be a positive multiple of 256", n);
-    if (batch == 0 || batch > 32)
-        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: batch=%u outside 1..32", batch);
+    if (batch == 0 || batch > 256)
+        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: batch=%u outside 1..256", batch);
     if (batch == 1) return anehip_quant_gemv_packed(ctx, ggml_type, wp, m, n, x, y);
-    const int ksplit = gemm_packed_ksplit(ctx, m, n, batch);
+    const int ksplit = gemm_rows_ksplit(ctx, m, n, batch);
     if (m % 4)
         return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "quant_gemm_packed: m=%u must be a multiple of 4 for batch > 1",
                          m);
-    const size_t count = (size_t)batch * m, xcount = xf_plane_len(n);
-    if (gemm_is_xs(ctx, m, n, batch)) {
+    // batch > 32: one 32-row group of planes per 32 rows (the prefill GEMM)
+    const size_t groups = (batch + 31) / 32;
+    const size_t count = (size_t)batch * m, xcount = groups * xf_plane_len(n);
+    if (batch <= 32 && gemm_is_xs(ctx, m, n, batch)) {
         // the x-stationary kernels read the fp32 rows themselves: partials, then their sum
         if (ksplit == 1) return launch_gemm_xs_rows(ctx, ctx->stream, ggml_type, wp, m, n, x, batch, y);
         int rc = ensure_workspace(ctx, (size_t)ksplit * count);
@@ -243,7 +245,7 @@ int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
     }
     // workspace: [x hi plane][x lo plane] (fp16, xcount each), the group
     // exponents, then the partials
-    const size_t planes = xcount + (xe_bytes(n) + 3) / 4;  // floats holding both planes and the exponents
+    const size_t planes = xcount + (groups * xe_bytes(n) + 3) / 4;  // floats holding both planes and the exponents
     int rc = ensure_workspace(ctx, planes + (ksplit > 1 ? (size_t)ksplit * count : 0));
     if (rc) return rc;
     Planes xp;
@@ -251,9 +253,9 @@ int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
     xp.lo = xp.hi + xcount;
     xp.xe = reinterpret_cast<int8_t *>(xp.lo + xcount);
     if ((rc = launch_split_x(ctx, ctx->stream, x, batch, n, xp))) return rc;
-    if (ksplit == 1) return launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xp, batch, y, 1);
+    if (ksplit == 1) return launch_gemm_rows(ctx, ctx->stream, ggml_type, wp, m, n, xp, batch, y, 1);
     float *part = ctx->ws.partial + planes;
-    if ((rc = launch_gemm_packed(ctx, ctx->stream, ggml_type, wp, m, n, xp, batch, part, ksplit))) return rc;
+    if ((rc = launch_gemm_rows(ctx, ctx->stream, ggml_type, wp, m, n, xp, batch, part, ksplit))) return rc;
     return launch_sum_partials(ctx, ctx->stream, part, y, count, ksplit);
 }
 

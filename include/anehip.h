@@ -198,11 +198,12 @@ size_t anehip_quant_packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
 int anehip_quant_pack(anehip_ctx *ctx, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n, void *dst);
 int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
                              const float *x, float *y);
-/* anehip_quant_gemm_packed: y[b][r] = W[r] . x[b] for b < batch (1..32), from
+/* anehip_quant_gemm_packed: y[b][r] = W[r] . x[b] for b < batch (1..256), from
  * the panel copy wp; x [batch][n] fp32.  batch 1 is
  * anehip_quant_gemv_packed; batch > 1 runs on MFMA (the small-batch form of
- * anehip_quant_gemm, same tolerance) and needs m % 4 == 0 (ANEHIP_EUNSUPPORTED
- * otherwise). */
+ * anehip_quant_gemm, same tolerance; above 32 the GEMM anehip_prefill runs
+ * its chunks of up to 256 tokens on) and needs m % 4 == 0
+ * (ANEHIP_EUNSUPPORTED otherwise). */
 int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
                              const float *x, uint32_t batch, float *y);
 

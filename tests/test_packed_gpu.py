@@ -168,6 +168,30 @@ def test_packed_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("batch", [33, 100, 256])
+@pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144), (8224, 2048), (2048, 2048), (12288, 1792), (100, 256)])
+def test_packed_gemm_tall(gpu_ctx, oracle_lib, t, batch, m, n):
+    """More than 32 rows (the prefill's chunk GEMM, gemm_tall): 32-row groups
+    of planes, 4 per workgroup row block (33: one full group and one row; 100
+    and 256: partial and full row blocks), 2 weight tiles per workgroup (8224
+    rows: a ragged last tile and a lone last tile), K splits that divide the
+    panel count (12288 x 1792: 7 panels)."""
+    w = oracle_lib.gen_quant(t, 77, m + 3 * n + t, m, n, std=0.02)
+    x = oracle_lib.normal(77, 900 + batch, batch * n).reshape(batch, n)
+    dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
+    dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(batch * m * 4)
+    gpu_ctx.call("quant_gemm_packed", t, dp, m, n, dx, batch, dy)
+    y = dy.download(np.float32, batch * m).reshape(batch, m)
+    ref = oracle_lib.gemm(t, w, m, n, x)
+    l2, mx = rel_errs(y, ref)
+    print(f"type={t} m={m} n={n} batch={batch}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+    assert l2 <= TOL and mx <= TOL
+    for b in (dw, dp, dx, dy):
+        b.free()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("t,m,n,batch", [(8, 151936, 2048, 32), (2, 151936, 2048, 19), (8, 151936, 2048, 4),
                                          (8, 151936, 2048, 16), (2, 151936, 2048, 11), (8, 65600, 1024, 16),
                                          (2, 65600, 1024, 5)])
@@ -242,13 +266,14 @@ def check_extreme(y, x, w, t, m, n, oracle_lib):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("t", [8, 2])
-@pytest.mark.parametrize("batch", [2, 17, 32])
+@pytest.mark.parametrize("batch", [2, 17, 32, 72])
 @pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 2048), (100, 256), (2048, 6144)])
 def test_packed_gemm_input_range(gpu_ctx, oracle_lib, t, batch, m, n):
     """The batch > 1 GEMMs split fp32 x into fp16 hi + lo: rows far outside
     fp16's range (overflow, underflow, subnormal, zero, mixed groups) match
     the fp32 oracle, on the x-stationary kernels (fp32 rows, per-row scaling
-    over the split) and on the persistent kernel (range-safe planes)."""
+    over the split), on the persistent kernel (range-safe planes) and above
+    32 rows on gemm_tall (range-safe planes, per-row scaling over the split)."""
     w = oracle_lib.gen_quant(t, 55, m + n + t, m, n, std=0.02)
     x = extreme_rows(oracle_lib, batch, n, 500 + batch)
     dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
