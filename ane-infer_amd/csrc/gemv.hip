@@ -2292,72 +2292,67 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
 }
 
 // Prefill GEMM: up to 256 rows of x (wave w takes rows 32 w .. 32 w + 31,
-// that group's 32-row planes) against 64-row weight tiles.  Work items are
-// (tile, K split); one workgroup per CU walks the panels ("units") of items
-// g, g + G, ... as one pipeline.  Per unit:
-//  * the panel was staged in LDS by direct global-to-LDS loads one unit
-//    ahead, and dequantised one unit ahead, once for all waves, into MFMA B
-//    fragments of w 2^s = (q d) 2^s as fp16 hi + lo (q d is exact in fp32:
-//    8 x 11 bits; hi + lo hold 22), s per weight row from the panel's
-//    largest |d| so that |hi| < 2^15 (weights far below the row's largest
-//    lose low bits of lo to fp16 subnormals: below 2^-24 of the row's scale);
-//    that dequantisation (VALU) runs between the unit's MFMAs;
-//  * each wave multiplies its rows' fragments of x (hi + lo at x 2^-E, E the
-//    row's largest group exponent) with them: x_hi w_hi + x_lo w_hi +
-//    x_hi w_lo on v_mfma_f32_32x32x16_f16 (x_lo w_lo is below 2^-44 of the
-//    product) over the panel's 256 columns, then adds the result times 2^-s
-//    to the item's sums; an item's sums go out at the start of the next one.
-// The products of q8_gemv.rs:234-242's (sum q x) d, up to fp32 rounding.
+// that group's 32-row planes) against NT 64-row weight tiles per work item.
+// Items are (tile group, K split); one workgroup per CU walks the panels
+// ("units") of items g, g + G, ... as one pipeline.  Per unit:
+//  * the panel bytes of the item's tiles were loaded into registers one unit
+//    ahead and turned, once for all waves, into MFMA B fragments of the
+//    quantised values q as fp16 (exact: |q| <= 127) in LDS, with each weight
+//    row's fp16 block scales d beside them;
+//  * each wave multiplies its rows' x fragments (hi + lo at x 2^-E, E the
+//    row's largest group exponent) with them on v_mfma_f32_32x32x16_f16,
+//    one 32-column block at a time: c = x_hi q + x_lo q over the block's two
+//    16-column steps, then sums += c d, the block's (sum q x) d of
+//    q8_gemv.rs:234-242 (x_lo q is exact in the MFMA's fp32 products; x_hi +
+//    x_lo holds x to 2^-22);
+//  * an item's sums go out, times 2^E, after its last unit.
 // out[ks * split_stride + row * m + r] (rows past `rows` or m: not stored).
 constexpr int kTallWaves = 8;
 constexpr int kTallMaxRows = 32 * kTallWaves;
 
-// 16 bytes per lane from global memory straight into LDS: lane i's vector
-// lands at lds + 16 i (lds wave-uniform)
-__device__ __forceinline__ void global_to_lds16(const u32x4 *src, u32x4 *lds) {
-    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+// 8 signed bytes q (Q8_0) as fp16 q, exactly: q + 128 placed in the
+// mantissa of 1024 (fp16 0x64xx is 1024 + xx), minus 1152
+__device__ __forceinline__ h8v q8_fragment(uint32_t w0, uint32_t w1) {
+    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+    const u32x4 p = {__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u),
+                     __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u),
+                     __builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u),
+                     __builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)};
+    const h8v k = {1152, 1152, 1152, 1152, 1152, 1152, 1152, 1152};
+    return __builtin_bit_cast(h8v, p) - k;
+}
+// 8 nibbles (Q4_0: the low, shift 0, or high, shift 4, nibbles of 8 bytes)
+// as fp16 nibble - 8, exactly (1024 + nibble, minus 1032)
+__device__ __forceinline__ h8v q4_fragment(uint32_t w0, uint32_t w1, int shift) {
+    const uint32_t n0 = (w0 >> shift) & 0x0f0f0f0fu, n1 = (w1 >> shift) & 0x0f0f0f0fu;
+    const u32x4 p = {__builtin_amdgcn_perm(0x64646464u, n0, 0x04010400u),
+                     __builtin_amdgcn_perm(0x64646464u, n0, 0x04030402u),
+                     __builtin_amdgcn_perm(0x64646464u, n1, 0x04010400u),
+                     __builtin_amdgcn_perm(0x64646464u, n1, 0x04030402u)};
+    const h8v k = {1032, 1032, 1032, 1032, 1032, 1032, 1032, 1032};
+    return __builtin_bit_cast(h8v, p) - k;
 }
 
-// 8 weights (signed values q) of a B fragment from 8 staged bytes (Q8_0) or
-// 8 nibbles (Q4_0, q = nibble - 8), times ds, as fp16 hi + lo
-template <uint32_t T>
-__device__ __forceinline__ void tall_fragment(uint32_t w0, uint32_t w1, int nib_shift, float ds, h8v &hi, h8v &lo) {
-    const uint32_t w[2] = {w0, w1};
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        int q;
-        if constexpr (T == ANEHIP_GGML_Q8_0) {
-            q = (int)(int8_t)(w[k >> 2] >> (8 * (k & 3)));
-        } else {
-            q = (int)((w[k >> 2] >> (8 * (k & 3) + nib_shift)) & 0xfu) - 8;
-        }
-        const float v = (float)q * ds;
-        const _Float16 h = (_Float16)v;
-        hi[k] = h;
-        lo[k] = (_Float16)(v - (float)h);
-    }
-}
-
-template <uint32_t T>
+template <uint32_t T, int NT>
 __global__ __launch_bounds__(kWave *kTallWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_tall(
     const uint8_t *__restrict__ Wp, Planes xp, float *__restrict__ out, int m, int n, int rows, int ksplit, int per,
     size_t split_stride) {
     constexpr int NTH = kWave * kTallWaves;
-    constexpr int VEC = Panel<T>::kBytes / 16;  // 16-byte vectors of a panel (a multiple of 64)
-    constexpr int PER_W = VEC / kWave;          // 1 KiB staging loads of a panel
-    static_assert(VEC % kWave == 0, "staging in whole 1 KiB wave loads");
-    static_assert(NTH % 128 == 0, "a thread's fragments share one weight row");
-    __shared__ u32x4 wq[VEC];               // the next unit's panel as stored
-    __shared__ h8v wf[2][2][16][2][kWave];  // B fragments [unit parity][hi / lo][16-column step][row half][lane]
-    __shared__ float sinv[2][kWave];        // 2^-s of each weight row [unit parity][row]
+    constexpr int CH = Panel<T>::kChunks;        // quant chunks of a tile's panel
+    constexpr int QV = NT * CH * kWave / NTH;    // quant vectors a thread converts per unit
+    constexpr int CB = 2 * NT;                   // 32-row weight blocks of an item
+    static_assert(NT * CH * kWave % NTH == 0 && NT * kWave <= NTH, "whole vectors per thread");
+    __shared__ h8v wf[2][16][CB][kWave];     // B fragments [unit parity][16-column step][weight block][lane]
+    __shared__ u32x4 dsc[2][NT * kWave];     // 8 fp16 block scales of each weight row [unit parity][row]
+    __shared__ uint16_t xes[2][kTallMaxRows];  // the panel's two group exponents of each x row [unit parity][row]
     __shared__ int erow[kTallWaves][32];
-    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
-    const int items = tiles * ksplit, G = (int)gridDim.x;
+    const int nsb = n >> 8, ptiles = (m + kWave - 1) / kWave, gtiles = (ptiles + NT - 1) / NT;
+    const int items = gtiles * ksplit, G = (int)gridDim.x;
     // this workgroup's units: the panels of items g, g + G, ... in order
     const int units = ((items - (int)blockIdx.x + G - 1) / G) * per;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int grows = rows - 32 * wave;  // rows of this wave's group (<= 0: it only stages and dequantises)
+    const int grows = rows - 32 * wave;  // rows of this wave's group (<= 0: it only converts)
     const bool active = grows > 0;
     const Planes gp = xp.group(active ? wave : 0, n);
     const int brow = min(lane & 31, (active ? min(grows, 32) : 1) - 1);  // rows past the group repeat its last
@@ -2365,165 +2360,180 @@ __global__ __launch_bounds__(kWave *kTallWaves) __attribute__((amdgpu_waves_per_
     auto item_of = [&](int u) { return (int)blockIdx.x + G * (u / per); };
     auto panel_of = [&](int u) { return (item_of(u) % ksplit) * per + u % per; };
 
-    // unit u's panel into wq: wave w issues loads w, w + 8, ...
-    auto stage = [&](int u) {
-        const int tile = item_of(u) / ksplit;
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(Wp + ((size_t)tile * nsb + panel_of(u)) * Panel<T>::kBytes);
-        for (int j = wave; j < PER_W; j += kTallWaves) global_to_lds16(src + kWave * j + lane, &wq[kWave * j]);
+    // unit u's panel bytes: thread t takes quant vectors t, t + 512, ... of
+    // the NT tiles' panels (vector v: tile v / (16 CH), chunk v / 64 % CH,
+    // weight row v % 64), the scale vector of row t % 64 of tile (t / 64) %
+    // NT (a tile past the matrix reads the last one again: its rows are
+    // never stored) and the two group exponents of x row t % 256 (the last
+    // row past the rows) for the unit's panel.  Buffer loads: the offset
+    // within a panel per lane, the panel's offset wave-uniform.
+    const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(Wp), 0, (int)((size_t)ptiles * nsb * Panel<T>::kBytes), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t xersrc =
+        __builtin_amdgcn_make_buffer_rsrc(xp.xe, 0, rows * xe_stride(n), kBufferWord3);
+    const int xe_off = min((int)threadIdx.x % kTallMaxRows, rows - 1) * xe_stride(n);
+    u32x4 rq[QV], rs = {};
+    uint32_t rxe = 0;
+    auto load_raw = [&](int u) {
+        const int tg = item_of(u) / ksplit, p = panel_of(u);
+#pragma unroll
+        for (int j = 0; j < QV; j++) {
+            constexpr int kTileVecs = CH * kWave;
+            const int pt = NTH * j / kTileVecs;  // the same for all threads
+            const int tile = min(tg * NT + pt, ptiles - 1);
+            rq[j] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, 16 * ((int)threadIdx.x + NTH * j - pt * kTileVecs),
+                                                             (tile * nsb + p) * Panel<T>::kBytes, 0));
+        }
+        // (every thread loads and stores them, waves w, w + NT, ... the same
+        // values, so that no load sits in a branch, where the compiler would
+        // sink it to its use)
+        const int tile = min(tg * NT + wave % NT, ptiles - 1);
+        rs = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           wrsrc, 16 * (CH * kWave + lane), (tile * nsb + p) * Panel<T>::kBytes, 0));
+        rxe = __builtin_amdgcn_raw_buffer_load_b16(xersrc, xe_off, 2 * p, 0);
     };
-    // wq -> B fragments of parity b: thread t takes fragments t, t + 512, ...
-    // of the 2048 (step s, row half h, lane l): weight row r = l % 32 + 32 h
-    // (the same for all of a thread's fragments), columns 16 s + 8 (l / 32)
-    // .. + 7; threads < 128 also leave 2^-s of their row
+    // registers -> fp16 B fragments of parity b.  Q8_0 chunk c holds a row's
+    // columns 16 c .. + 15 (step c); Q4_0 chunk c its block c, byte i the
+    // columns 32 c + i (low nibble, step 2 c) and 32 c + 16 + i (high, step
+    // 2 c + 1).  Lane l of a step's fragment: weight row l % 32 of the block,
+    // columns 8 (l / 32) .. + 7 of the step.
     auto convert = [&](int b) {
-        const uint32_t *ws = reinterpret_cast<const uint32_t *>(wq);
-        const int l = threadIdx.x & 63, h = (threadIdx.x >> 6) & 1, r = (l & 31) + 32 * h, kh = l >> 5;
-        const u32x4 sv = wq[Panel<T>::kChunks * kWave + r];
-        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
-        float dm = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float a = __half2float(__ushort_as_half((unsigned short)(sw[i] & 0xffffu)));
-            const float c = __half2float(__ushort_as_half((unsigned short)(sw[i] >> 16)));
-            dm = fmaxf(dm, fmaxf(__builtin_isnan(a) ? INFINITY : fabsf(a), __builtin_isnan(c) ? INFINITY : fabsf(c)));
+        for (int j = 0; j < QV; j++) {
+            const int v = (int)threadIdx.x + NTH * j, c = v / kWave % CH, r = v % kWave;
+            const int cb = 2 * (v / (CH * kWave)) + r / 32, l = r % 32;
+            const u32x4 q = rq[j];
+            if constexpr (T == ANEHIP_GGML_Q8_0) {
+                wf[b][c][cb][l] = q8_fragment(q.x, q.y);
+                wf[b][c][cb][l + 32] = q8_fragment(q.z, q.w);
+            } else {
+                wf[b][2 * c][cb][l] = q4_fragment(q.x, q.y, 0);
+                wf[b][2 * c][cb][l + 32] = q4_fragment(q.z, q.w, 0);
+                wf[b][2 * c + 1][cb][l] = q4_fragment(q.x, q.y, 4);
+                wf[b][2 * c + 1][cb][l + 32] = q4_fragment(q.z, q.w, 4);
+            }
         }
-        // 127 dm 2^s in [2^14, 2^15); s = 0 for an all-zero or non-finite row
-        const int sh = dm == 0.0f || dm == INFINITY ? 0 : 15 - __builtin_amdgcn_frexp_expf(127.0f * dm);
-        const float fac = ldexpf(1.0f, sh);
-        if (threadIdx.x < 128) sinv[b][r] = ldexpf(1.0f, -sh);
-#pragma unroll
-        for (int i = 0; i < 2048 / NTH; i++) {
-            const int st = (int)(threadIdx.x >> 7) + (NTH >> 7) * i;
-            const int blk = st >> 1;
-            const float d = __half2float(__ushort_as_half((unsigned short)(sw[blk >> 1] >> (16 * (blk & 1)))));
-            // Q8_0 chunk st: row r's columns 16 st .. + 15; Q4_0 chunk blk:
-            // byte i holds element i (low nibble) and i + 16 (high)
-            const uint32_t *c = ws + 4 * ((T == ANEHIP_GGML_Q8_0 ? st : blk) * kWave + r) + 2 * kh;
-            h8v hi, lo;
-            tall_fragment<T>(c[0], c[1], T == ANEHIP_GGML_Q8_0 ? 0 : 4 * (st & 1), d * fac, hi, lo);
-            wf[b][0][st][h][l] = hi;
-            wf[b][1][st][h][l] = lo;
-        }
+        dsc[b][threadIdx.x % (NT * kWave)] = rs;
+        xes[b][threadIdx.x % kTallMaxRows] = (uint16_t)rxe;
     };
-    // the quarter's x fragments: steps 16 p + 4 q + st of the group's planes
-    auto load_x = [&](int p, int q, h8v (&xa)[4], h8v (&xb)[4]) {
-        const size_t o = (size_t)(16 * p + 4 * q) * 512 + (size_t)(brow + 32 * (lane >> 5)) * 8;
-#pragma unroll
-        for (int st = 0; st < 4; st++) {
-            xa[st] = *reinterpret_cast<const h8v *>(gp.hi + o + 512 * st);
-            xb[st] = *reinterpret_cast<const h8v *>(gp.lo + o + 512 * st);
-        }
+    // block j of panel p (steps 16 p + 2 j, + 1): hi and lo fragments
+    // (buffer loads: the lane's offset in a step's 1 KiB, the step's offset
+    // wave-uniform)
+    const int plane_bytes = (int)(2 * xf_plane_len((size_t)n));
+    const __amdgpu_buffer_rsrc_t hrsrc = __builtin_amdgcn_make_buffer_rsrc(gp.hi, 0, plane_bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t lrsrc = __builtin_amdgcn_make_buffer_rsrc(gp.lo, 0, plane_bytes, kBufferWord3);
+    const int xoff = 16 * (brow + 32 * (lane >> 5));
+    auto load_x = [&](int p, int j, h8v (&a)[4]) {
+        const int so = (16 * p + 2 * j) * 1024;
+        a[0] = __builtin_bit_cast(h8v, __builtin_amdgcn_raw_buffer_load_b128(hrsrc, xoff, so, 0));
+        a[1] = __builtin_bit_cast(h8v, __builtin_amdgcn_raw_buffer_load_b128(lrsrc, xoff, so, 0));
+        a[2] = __builtin_bit_cast(h8v, __builtin_amdgcn_raw_buffer_load_b128(hrsrc, xoff, so + 1024, 0));
+        a[3] = __builtin_bit_cast(h8v, __builtin_amdgcn_raw_buffer_load_b128(lrsrc, xoff, so + 1024, 0));
     };
-    if (units > 0) stage(0);
+    f32x16 acc[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) acc[cb] = f32x16{};
+    // an item's sums: element r of lane l is row 8 (r / 4) + 4 (l / 32) +
+    // r % 4 of the group, weight row 32 cb + l % 32 of the item
+    auto store_item = [&](int item) {
+        const int tg = item / ksplit, ks = item % ksplit;
+        // opaque copies: the row addresses and scales are rebuilt here, not
+        // kept live across the unit loop
+        float *ob = out;
+        int w = wave, ln = lane;
+        asm volatile("" : "+s"(ob), "+s"(w), "+v"(ln));
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int gr = 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
+            if (gr < grows) {
+                const float sc = xe_scale(erow[w][gr]);
+                float *orow = ob + (size_t)ks * split_stride + (size_t)(32 * w + gr) * m;
+#pragma unroll
+                for (int cb = 0; cb < CB; cb++) {
+                    const int wr = tg * NT * kWave + 32 * cb + (ln & 31);
+                    if (wr < m) orow[wr] = acc[cb][r] * sc;
+                }
+            }
+        }
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) acc[cb] = f32x16{};
+    };
+    if (units == 0) return;
+    load_raw(0);
     // E over the whole row (one exponent for every K split of it)
     int E = kXeEmpty;
     for (int g = 0; g < 2 * nsb; g++) E = max(E, (int)xe_row[g]);
     if (lane < 32) erow[wave][lane] = E;
-    f32x16 acc0 = {}, acc1 = {};
-    f32x16 c0, c1;
-    auto mma_quarter = [&](int b, int p, int q, const h8v (&xa)[4], const h8v (&xb)[4]) {
-        const _Float16 f = xe_factor(xe_row[2 * p + (q >> 1)], E);
-#pragma unroll
-        for (int st = 0; st < 4; st++) {
-            const h8v a = xa[st] * f, al = xb[st] * f;
-            const int s = 4 * q + st;
-            const h8v bh0 = wf[b][0][s][0][lane], bl0 = wf[b][1][s][0][lane];
-            const h8v bh1 = wf[b][0][s][1][lane], bl1 = wf[b][1][s][1][lane];
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh0, c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh1, c1, 0, 0, 0);
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh0, c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh1, c1, 0, 0, 0);
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl0, c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl1, c1, 0, 0, 0);
-        }
-    };
-    // an item's sums: element r of lane l is row 8 (r / 4) + 4 (l / 32) +
-    // r % 4 of the group, weight row l % 32 (+ 32 for acc1) of the tile
-    auto store_item = [&](int item) {
-        const int tile = item / ksplit, ks = item % ksplit;
-        const int wr = tile * kWave + (lane & 31);
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int gr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (gr < grows) {
-                const float sc = xe_scale(erow[wave][gr]);
-                float *orow = out + (size_t)ks * split_stride + (size_t)(32 * wave + gr) * m;
-                if (wr < m) orow[wr] = acc0[r] * sc;
-                if (wr + 32 < m) orow[wr + 32] = acc1[r] * sc;
-            }
-        }
-        acc0 = f32x16{};
-        acc1 = f32x16{};
-    };
-    // wait for this wave's staging loads: all but the last 16 (the x loads of
-    // quarters 2 and 3, issued after them); waves without rows issue no x loads
-    auto wait_stage = [&]() {
-        if (active) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    };
-    if (units == 0) return;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // unit 0 staged, erow written
     convert(0);
-    __syncthreads();  // unit 0's fragments ready, wq free
-    // unit 0's first x fragments before the next staging loads (every x
-    // wait then excludes those)
-    h8v xa0[4], xb0[4], xa1[4], xb1[4];
-    if (active) {
-        load_x(panel_of(0), 0, xa0, xb0);
-        load_x(panel_of(0), 1, xa1, xb1);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (units > 1) stage(1);
-    for (int u = 0; u < units; u++) {
+    __syncthreads();  // unit 0's fragments ready, erow written
+    // x of the next three blocks is always in flight: xa[i % 4] for block i
+    // of the workgroup's sequence of units x 8 blocks.  Every wave issues
+    // the same loads and products on every unit (waves without rows take
+    // group 0's x and store nothing; past the last unit, a valid panel), so
+    // that the loop has one path and the loads in flight are the same on it.
+    h8v xa[4][4];
+    f32x16 cc[2] = {f32x16{}, f32x16{}};
+    float dd[2] = {0.0f, 0.0f};
+    load_x(panel_of(0), 0, xa[0]);
+    load_x(panel_of(0), 1, xa[1]);
+    load_x(panel_of(0), 2, xa[2]);
+    for (int u0 = 0; u0 < units; u0 += per) {
+    for (int u = u0; u < u0 + per; u++) {
         const int b = u & 1, p = panel_of(u);
-        const bool more = u + 1 < units;
-        if (active) {
-            c0 = f32x16{};
-            c1 = f32x16{};
-            __builtin_amdgcn_sched_barrier(0);
-            mma_quarter(b, p, 0, xa0, xb0);
-            __builtin_amdgcn_sched_barrier(0);
-            load_x(p, 2, xa0, xb0);
-            __builtin_amdgcn_sched_barrier(0);
-            mma_quarter(b, p, 1, xa1, xb1);
-            __builtin_amdgcn_sched_barrier(0);
-            load_x(p, 3, xa1, xb1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (more) {
-            wait_stage();
-            __syncthreads();  // unit u + 1's panel is in wq
-        }
-        // an item's sums go out once its last unit is done (stores count in
-        // vmcnt: here they are older than the next staging loads)
-        if (active && u > 0 && u % per == 0) store_item(item_of(u - 1));
-        if (active) {
-            mma_quarter(b, p, 2, xa0, xb0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (more) load_x(panel_of(u + 1), 0, xa0, xb0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // unit u + 1's fragments (VALU and LDS) while the MFMAs drain
-        if (more) convert(b ^ 1);
-        __builtin_amdgcn_sched_barrier(0);
-        if (active) {
-            mma_quarter(b, p, 3, xa1, xb1);
-            __builtin_amdgcn_sched_barrier(0);
-            if (more) load_x(panel_of(u + 1), 1, xa1, xb1);
-            __builtin_amdgcn_sched_barrier(0);
-            // weight rows l % 32 and 32 + l % 32 of the tile
-            const float u0 = sinv[b][lane & 31], u1 = sinv[b][32 + (lane & 31)];
+        const uint32_t xe2 = xes[b][32 * wave + brow];
+        const _Float16 fg[2] = {xe_factor((int)(int8_t)(xe2 & 0xffu), E), xe_factor((int)(int8_t)(xe2 >> 8), E)};
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                acc0[r] = fmaf(c0[r], u0, acc0[r]);
-                acc1[r] = fmaf(c1[r], u1, acc1[r]);
+        for (int j = 0; j < 8; j++) {
+            const _Float16 f = fg[j >> 2];
+            h8v(&a)[4] = xa[j % 4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) a[i] *= f;
+            // then x of the block three ahead (the next unit's first three)
+            // and, at block 0, the next unit's panel bytes (their wait comes
+            // at block 4; at the unit's start nothing is in flight, so block
+            // 0's x wait costs nothing)
+            __builtin_amdgcn_sched_barrier(0);
+            if (j < 5) load_x(p, j + 3, xa[(j + 3) % 4]);
+            else load_x(panel_of(u + 1), j - 5, xa[(j + 3) % 4]);
+            if (j == 0) load_raw(u + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            // (block, weight block) steps as a two-stage pipeline: step i's
+            // products into cc[i % 2] on the MFMAs while the VALU adds step
+            // i - 1's, times its scale, to its sums
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++) {
+                const h8v b0 = wf[b][2 * j][cb][lane], b1 = wf[b][2 * j + 1][cb][lane];
+                f32x16 &c = cc[cb & 1];
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b0, f32x16{}, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], b0, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[2], b1, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[3], b1, c, 0, 0, 0);
+                const int pcb = (cb + CB - 1) % CB;
+                const f32x16 &cp = cc[(cb + 1) & 1];
+                const float dp = dd[(cb + 1) & 1];
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[pcb][r] = fmaf(cp[r], dp, acc[pcb][r]);
+                // the sums are added here, not deferred (which would keep
+                // every step's products live)
+                asm volatile("" : "+v"(acc[pcb]));
+                const uint32_t dw = reinterpret_cast<const uint32_t *>(&dsc[b][32 * cb + (lane & 31)])[j >> 1];
+                dd[cb & 1] = __half2float(__ushort_as_half((unsigned short)(dw >> (16 * (j & 1)))));
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();  // every wave is done with wq (convert) and with wf[b]
-        if (u + 2 < units) stage(u + 2);
+        // unit u + 1's fragments into the parity unit u - 1 read (past the
+        // last unit: not read)
+        convert(b ^ 1);
+        __syncthreads();  // unit u + 1's fragments ready; every wave is done with parity b
     }
-    if (active) store_item(item_of(units - 1));
+    // the item's last step, then its sums out
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[CB - 1][r] = fmaf(cc[1][r], dd[1], acc[CB - 1][r]);
+    cc[1] = f32x16{};
+    dd[1] = 0.0f;
+    if (active) store_item(item_of(u0));
+    }
 }
 
 // fp32 x[batch][n] -> range-safe fragment-order fp16 planes (hi + lo = x *
@@ -3064,48 +3074,74 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     return ANEHIP_OK;
 }
 
-// K splits of gemm_tall: a divisor of the panel count (at most 16, the
-// partial slices a consumer sums) minimising the panels of the busiest CU,
-// ceil(workgroups / CUs) x panels per split; ties to fewer splits.
-static int gemm_tall_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
-    const int tiles = (int)((m + kWave - 1) / kWave);
+// Work split of gemm_tall: NT tiles per item (1 or 2) and a K split that
+// divides the panel count (at most 16, the partial slices a consumer sums),
+// minimising an estimate of the busiest CU's time, ceil(items / CUs) x
+// panels per split x the measured time of one unit, plus the traffic of the
+// extra partial slices (written here, read by the consumer: 2 x 4 bytes per
+// row and output, at 256 rows ~2 KiB per output).
+struct TallPlan {
+    int nt, ks;
+};
+static TallPlan tall_plan(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+    const int ptiles = (int)((m + kWave - 1) / kWave);
     const int nsb = (int)(n / 256), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    int best = 1;
-    long best_cost = -1;
-    for (int k = 1; k <= nsb && k <= 16; k++) {
-        if (nsb % k) continue;
-        const long cost = (long)((tiles * k + cus - 1) / cus) * (nsb / k);
-        if (best_cost < 0 || cost < best_cost) {
-            best_cost = cost;
-            best = k;
+    const double unit_us[3] = {0.0, 2.2, 4.0}, part_us_per_row = 2048.0 / 5.0e6;
+    TallPlan best{1, 1};
+    double best_cost = -1.0;
+    for (int nt = 1; nt <= 2; nt++) {
+        const int groups = (ptiles + nt - 1) / nt;
+        for (int k = 1; k <= nsb && k <= 16; k++) {
+            if (nsb % k) continue;
+            const double cost = (double)((groups * k + cus - 1) / cus) * (nsb / k) * unit_us[nt] +
+                                (k - 1) * (double)m * part_us_per_row;
+            if (best_cost < 0.0 || cost < best_cost) {
+                best_cost = cost;
+                best = {nt, k};
+            }
         }
     }
     return best;
 }
 
 int gemm_rows_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t rows) {
-    return rows <= 32 ? gemm_packed_ksplit(ctx, m, n, rows) : gemm_tall_ksplit(ctx, m, n);
+    return rows <= 32 ? gemm_packed_ksplit(ctx, m, n, rows) : tall_plan(ctx, m, n).ks;
 }
 
 int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
                      const Planes &xp, uint32_t rows, float *out, int ksplit) {
     if (rows <= 32) return launch_gemm_packed(ctx, stream, ggml_type, wp, m, n, xp, rows, out, ksplit);
-    const int nsb = (int)(n / 256), tiles = (int)((m + kWave - 1) / kWave);
+    const int nsb = (int)(n / 256), ptiles = (int)((m + kWave - 1) / kWave);
     if (rows > kTallMaxRows || ksplit < 1 || nsb % ksplit || m % 4 || !xp.hi || !xp.lo || !xp.xe)
         return set_error(ctx->err, ANEHIP_EINVAL, "gemm_rows: %u rows (at most %d), K split %d of %d panels, m %u",
                          rows, kTallMaxRows, ksplit, nsb, m);
     if (4.0 * ksplit * rows * m > 1073741824.0)
         return set_error(ctx->err, ANEHIP_ESHAPE, "gemm_rows: output of %d x %u x %u floats too large", ksplit, rows, m);
+    // the plan's tile count when its K split is the one asked for, else one
+    // tile per item
+    const TallPlan plan = tall_plan(ctx, m, n);
+    const int nt = plan.ks == ksplit ? plan.nt : 1, items = (ptiles + nt - 1) / nt * ksplit;
     // one workgroup per CU, each walking its items' panels in one pipeline
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const dim3 grid((unsigned)std::min(tiles * ksplit, cus)), block(kWave * kTallWaves);
+    const dim3 grid((unsigned)std::min(items, cus)), block(kWave * kTallWaves);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
-    if (ggml_type == ANEHIP_GGML_Q8_0)
-        hipLaunchKernelGGL(gemm_tall<ANEHIP_GGML_Q8_0>, grid, block, 0, stream, w, xp, out, (int)m, (int)n, (int)rows,
-                           ksplit, nsb / ksplit, (size_t)rows * m);
-    else
-        hipLaunchKernelGGL(gemm_tall<ANEHIP_GGML_Q4_0>, grid, block, 0, stream, w, xp, out, (int)m, (int)n, (int)rows,
-                           ksplit, nsb / ksplit, (size_t)rows * m);
+    const int per = nsb / ksplit;
+    const size_t ss = (size_t)rows * m;
+    if (ggml_type == ANEHIP_GGML_Q8_0) {
+        if (nt == 2)
+            hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q8_0, 2>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
+                               (int)rows, ksplit, per, ss);
+        else
+            hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q8_0, 1>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
+                               (int)rows, ksplit, per, ss);
+    } else {
+        if (nt == 2)
+            hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q4_0, 2>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
+                               (int)rows, ksplit, per, ss);
+        else
+            hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q4_0, 1>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
+                               (int)rows, ksplit, per, ss);
+    }
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

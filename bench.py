@@ -237,7 +237,7 @@ def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
             "effective_GB_s": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
         }
     if prefill_tokens:
-        # anehip_prefill of one sequence from position 0 (chunks of 128 tokens),
+        # anehip_prefill of one sequence from position 0 (chunks of 256 tokens),
         # synchronous, timed on the host clock; one untimed run first
         gm.alloc_state(1, max(1024, prefill_tokens))
         prompt = (np.arange(prefill_tokens, dtype=np.uint32) * 7919) % spec.vocab_size
