@@ -3088,39 +3088,34 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     return ANEHIP_OK;
 }
 
-// Work split of gemm_tall: NT tiles per item (1 or 2) and a K split that
-// divides the panel count (at most 16, the partial slices a consumer sums),
-// minimising an estimate of the busiest CU's time, ceil(items / CUs) x
-// panels per split x the measured time of one unit at 256 rows (4.6 us with
-// one tile, 9.6 us with two, on MI355X), plus the traffic of the extra
-// partial slices (written here, read by the consumer: 2 x 4 bytes per row
-// and output, at 256 rows ~2 KiB per output, at ~5 TB/s).
-struct TallPlan {
-    int nt, ks;
-};
-static TallPlan tall_plan(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
+// K split of gemm_tall (one tile per item: two tiles per item measured 9.6 us
+// per unit against 4.6 us for one, no gain per row, so gemm_tall<T, 2> is
+// not launched): a divisor of the panel count (at most 16, the partial slices
+// a consumer sums) minimising an estimate of the busiest CU's time,
+// ceil(items / CUs) x panels per split x the measured time of one unit at 256
+// rows (4.6 us on MI355X), plus the traffic of the extra partial slices
+// (written here, read by the consumer: 2 x 4 bytes per row and output, at
+// 256 rows ~2 KiB per output, at ~5 TB/s).
+static int gemm_tall_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
     const int ptiles = (int)((m + kWave - 1) / kWave);
     const int nsb = (int)(n / 256), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const double unit_us[3] = {0.0, 4.6, 9.6}, part_us_per_row = 2048.0 / 5.0e6;
-    TallPlan best{1, 1};
+    const double unit_us = 4.6, part_us_per_row = 2048.0 / 5.0e6;
+    int best = 1;
     double best_cost = -1.0;
-    for (int nt = 1; nt <= 2; nt++) {
-        const int groups = (ptiles + nt - 1) / nt;
-        for (int k = 1; k <= nsb && k <= 16; k++) {
-            if (nsb % k) continue;
-            const double cost = (double)((groups * k + cus - 1) / cus) * (nsb / k) * unit_us[nt] +
-                                (k - 1) * (double)m * part_us_per_row;
-            if (best_cost < 0.0 || cost < best_cost) {
-                best_cost = cost;
-                best = {nt, k};
-            }
+    for (int k = 1; k <= nsb && k <= 16; k++) {
+        if (nsb % k) continue;
+        const double cost =
+            (double)((ptiles * k + cus - 1) / cus) * (nsb / k) * unit_us + (k - 1) * (double)m * part_us_per_row;
+        if (best_cost < 0.0 || cost < best_cost) {
+            best_cost = cost;
+            best = k;
         }
     }
     return best;
 }
 
 int gemm_rows_ksplit(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t rows) {
-    return rows <= 32 ? gemm_packed_ksplit(ctx, m, n, rows) : tall_plan(ctx, m, n).ks;
+    return rows <= 32 ? gemm_packed_ksplit(ctx, m, n, rows) : gemm_tall_ksplit(ctx, m, n);
 }
 
 int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
@@ -3132,31 +3127,19 @@ int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, co
                          rows, kTallMaxRows, ksplit, nsb, m);
     if (4.0 * ksplit * rows * m > 1073741824.0)
         return set_error(ctx->err, ANEHIP_ESHAPE, "gemm_rows: output of %d x %u x %u floats too large", ksplit, rows, m);
-    // the plan's tile count when its K split is the one asked for, else one
-    // tile per item
-    const TallPlan plan = tall_plan(ctx, m, n);
-    const int nt = plan.ks == ksplit ? plan.nt : 1, items = (ptiles + nt - 1) / nt * ksplit;
+    const int items = ptiles * ksplit;
     // one workgroup per CU, each walking its items' panels in one pipeline
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const dim3 grid((unsigned)std::min(items, cus)), block(kWave * kTallWaves);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     const int per = nsb / ksplit;
     const size_t ss = (size_t)rows * m;
-    if (ggml_type == ANEHIP_GGML_Q8_0) {
-        if (nt == 2)
-            hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q8_0, 2>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
-                               (int)rows, ksplit, per, ss);
-        else
-            hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q8_0, 1>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
-                               (int)rows, ksplit, per, ss);
-    } else {
-        if (nt == 2)
-            hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q4_0, 2>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
-                               (int)rows, ksplit, per, ss);
-        else
-            hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q4_0, 1>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
-                               (int)rows, ksplit, per, ss);
-    }
+    if (ggml_type == ANEHIP_GGML_Q8_0)
+        hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q8_0, 1>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
+                           (int)rows, ksplit, per, ss);
+    else
+        hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q4_0, 1>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
+                           (int)rows, ksplit, per, ss);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
