@@ -3127,6 +3127,9 @@ int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, co
                          rows, kTallMaxRows, ksplit, nsb, m);
     if (4.0 * ksplit * rows * m > 1073741824.0)
         return set_error(ctx->err, ANEHIP_ESHAPE, "gemm_rows: output of %d x %u x %u floats too large", ksplit, rows, m);
+    // gemm_tall addresses the weights with 32-bit buffer offsets
+    if ((double)ptiles * nsb * Panel<ANEHIP_GGML_Q8_0>::kBytes > 2147483647.0)
+        return set_error(ctx->err, ANEHIP_ESHAPE, "gemm_rows: %u x %u weights too large (2 GiB of panels at most)", m, n);
     const int items = ptiles * ksplit;
     // one workgroup per CU, each walking its items' panels in one pipeline
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
