@@ -203,7 +203,8 @@ int anehip_quant_gemv_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
  * anehip_quant_gemv_packed; batch > 1 runs on MFMA (the small-batch form of
  * anehip_quant_gemm, same tolerance; above 32 the GEMM anehip_prefill runs
  * its chunks of up to 256 tokens on) and needs m % 4 == 0
- * (ANEHIP_EUNSUPPORTED otherwise). */
+ * (ANEHIP_EUNSUPPORTED otherwise); above 32 rows the panels must stay
+ * under 2 GiB (ANEHIP_ESHAPE otherwise). */
 int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp, uint32_t m, uint32_t n,
                              const float *x, uint32_t batch, float *y);
 
