@@ -103,11 +103,10 @@ def _check_state(gm, oseq, b, spec, what):
 
 @pytest.mark.parametrize("n", [1, 13, 45])
 def test_prefill_matches_token_steps(small_host, n):
-    """anehip_prefill of n prompt tokens (one chunk; 45 rows run the GEMMs as
-    row groups of 32 + 13) from
-    position 0 vs the oracle run token by token: the last token's logits, the
-    DeltaNet states / conv windows and the KV rows written, then 3 decode
-    steps continuing the sequence."""
+    """anehip_prefill of n prompt tokens (one chunk; 45 rows run the chunk
+    GEMM, 1 and 13 the decode GEMMs) from position 0 vs the oracle run token
+    by token: the last token's logits, the DeltaNet states / conv windows and
+    the KV rows written, then 3 decode steps continuing the sequence."""
     spec = small_host.spec
     gm = _model(small_host, 1, 64)
     oseq = small_host.seq(64)
@@ -330,6 +329,25 @@ def test_q4_0_model(small_host):
     gm.close()
 
 
+def test_q4_0_model_prefill():
+    """A Q4_0 model's 70-token prefill (the chunk GEMM on Q4_0 panels at 70
+    rows) vs the oracle run token by token: last logits and states."""
+    host = HostModel(anehip.Spec(**SMALL), seed=5, ggml_type=2)
+    spec = host.spec
+    gm = _model(host, 1, 128)
+    oseq = host.seq(128)
+    toks = oracle.randint(35, 70, 70, spec.vocab_size)
+    g = gm.prefill(0, toks)
+    for t in toks:
+        r = oseq.forward(int(t))
+    l2, mx = rel_errs(g, r)
+    print(f"Q4_0 prefill 70: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+    assert l2 <= TOL and mx <= TOL
+    _check_state(gm, oseq, 0, spec, "Q4_0 after prefill")
+    gm.close()
+    oseq.close()
+
+
 # ---------------------------------------------- Qwen3.5-2B shape (config 4) --
 
 @pytest.fixture(scope="module")
@@ -427,14 +445,14 @@ def test_ragged_positions_across_chunk_boundaries(mid_host):
     gm.close()
 
 
-@pytest.mark.parametrize("n", [100, 300])
+@pytest.mark.parametrize("n", [100, 300, 600])
 def test_prefill_long_prompt_large_cache(mid_host, n):
-    """anehip_prefill of a 100-token prompt (one chunk, GEMM row groups of 32,
-    32, 32, 4) and a 300-token one (chunks of 128, 128, 44: the two full chunks
-    replay the captured chunk graph, the DeltaNet scan runs 128 tokens per
-    launch) into a 2048-position cache: chunk rows see up to 5 live tiles of
-    attention; the last logits, states and KV rows vs the oracle run token by
-    token, then 2 decode steps."""
+    """anehip_prefill into a 2048-position cache of a 100-token prompt (one
+    chunk on the chunk GEMM at 100 rows), a 300-token one (chunks of 256 and
+    44) and a 600-token one (256, 256, 88: the second full chunk replays the
+    graph the first captured; the DeltaNet scan runs 256 tokens per launch);
+    chunk rows see up to 10 live tiles of attention; the last logits, states
+    and KV rows vs the oracle run token by token, then 2 decode steps."""
     spec = mid_host.spec
     gm = _model(mid_host, 1, 2048)
     oseq = mid_host.seq(2048)
