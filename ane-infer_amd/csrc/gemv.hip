@@ -2291,14 +2291,17 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
     } while (ct < tiles);
 }
 
-// Prefill GEMM: up to 256 rows of x (wave w takes rows 32 w .. 32 w + 31,
-// that group's 32-row planes) against NT 64-row weight tiles per work item.
-// Items are (tile group, K split); one workgroup per CU walks the panels
-// ("units") of items g, g + G, ... as one pipeline.  Per unit:
-//  * the panel bytes of the item's tiles were loaded into registers one unit
-//    ahead and turned, once for all waves, into MFMA B fragments of the
-//    quantised values q as fp16 (exact: |q| <= 127) in LDS, with each weight
-//    row's fp16 block scales d beside them;
+// Prefill GEMM: up to 256 rows of x (compute wave w takes rows 32 w .. 32 w +
+// 31, that group's 32-row planes) against 64-row weight tiles.  Items are
+// (tile, K split); one workgroup per CU walks the panels ("units") of items
+// g, g + G, ... as one pipeline.  Per unit:
+//  * a ninth wave (the loader) loaded the panel's bytes into registers a unit
+//    ahead and turned them into MFMA B fragments of the quantised values q as
+//    fp16 (exact: |q| <= 127) in LDS, with each weight row's fp16 block
+//    scales d beside them (the compute waves then wait on nothing but their
+//    own x loads, which come from L2: a load waits for every load its wave
+//    issued before it, so panel loads of their own would hold up the next x
+//    wait for an HBM round trip);
 //  * each wave multiplies its rows' x fragments (hi + lo at x 2^-E, E the
 //    row's largest group exponent) with them on v_mfma_f32_32x32x16_f16,
 //    one 32-column block at a time: c = x_hi q + x_lo q over the block's two
@@ -2333,90 +2336,99 @@ __device__ __forceinline__ h8v q4_fragment(uint32_t w0, uint32_t w1, int shift) 
     return __builtin_bit_cast(h8v, p) - k;
 }
 
-template <uint32_t T, int NT>
-__global__ __launch_bounds__(kWave *kTallWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_tall(
+template <uint32_t T>
+__global__ __launch_bounds__(kWave *(kTallWaves + 1)) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_tall(
     const uint8_t *__restrict__ Wp, Planes xp, float *__restrict__ out, int m, int n, int rows, int ksplit, int per,
     size_t split_stride) {
-    constexpr int NTH = kWave * kTallWaves;
-    constexpr int CH = Panel<T>::kChunks;        // quant chunks of a tile's panel
-    constexpr int QV = NT * CH * kWave / NTH;    // quant vectors a thread converts per unit
-    constexpr int CB = 2 * NT;                   // 32-row weight blocks of an item
-    static_assert(NT * CH * kWave % NTH == 0 && NT * kWave <= NTH, "whole vectors per thread");
-    __shared__ h8v wf[2][16][CB][kWave];     // B fragments [unit parity][16-column step][weight block][lane]
-    __shared__ u32x4 dsc[2][NT * kWave];     // 8 fp16 block scales of each weight row [unit parity][row]
+    constexpr int CH = Panel<T>::kChunks;  // quant chunks of a tile's panel
+    __shared__ h8v wf[2][16][2][kWave];    // B fragments [unit parity][16-column step][weight block][lane]
+    __shared__ u32x4 dsc[2][kWave];        // 8 fp16 block scales of each weight row [unit parity][row]
     __shared__ uint16_t xes[2][kTallMaxRows];  // the panel's two group exponents of each x row [unit parity][row]
     __shared__ int erow[kTallWaves][32];
-    const int nsb = n >> 8, ptiles = (m + kWave - 1) / kWave, gtiles = (ptiles + NT - 1) / NT;
-    const int items = gtiles * ksplit, G = (int)gridDim.x;
+    const int nsb = n >> 8, ptiles = (m + kWave - 1) / kWave;
+    const int items = ptiles * ksplit, G = (int)gridDim.x;
     // this workgroup's units: the panels of items g, g + G, ... in order
     const int units = ((items - (int)blockIdx.x + G - 1) / G) * per;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int grows = rows - 32 * wave;  // rows of this wave's group (<= 0: it only converts)
+    auto item_of = [&](int u) { return (int)blockIdx.x + G * (u / per); };
+    auto panel_of = [&](int u) { return (item_of(u) % ksplit) * per + u % per; };
+    if (units == 0) return;
+
+    if (wave == kTallWaves) {
+        // The loader wave: unit u's panel bytes (lane l: chunk c of weight row
+        // l for every c, row l's scale vector, and the two group exponents of
+        // x rows l, l + 64, l + 128, l + 192 (the last row past the rows); a
+        // tile past the matrix reads the last one again: its rows are never
+        // stored) into registers, then into the B fragments of q as fp16 of
+        // the unit's parity.  Its loads are the only ones it waits on, so
+        // each has a whole unit to arrive.  Buffer loads: the offset within a
+        // panel per lane, the panel's offset wave-uniform.
+        const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(Wp), 0, (int)((size_t)ptiles * nsb * Panel<T>::kBytes), kBufferWord3);
+        const __amdgpu_buffer_rsrc_t xersrc =
+            __builtin_amdgcn_make_buffer_rsrc(xp.xe, 0, rows * xe_stride(n), kBufferWord3);
+        u32x4 rq[CH], rs;
+        uint32_t rxe[kTallMaxRows / kWave];
+        auto load_raw = [&](int u) {
+            const int tile = min(item_of(u) / ksplit, ptiles - 1), p = panel_of(u);
+            const int base = (tile * nsb + p) * Panel<T>::kBytes;
+#pragma unroll
+            for (int c = 0; c < CH; c++)
+                rq[c] = __builtin_bit_cast(u32x4,
+                                           __builtin_amdgcn_raw_buffer_load_b128(wrsrc, 16 * (c * kWave + lane), base, 0));
+            rs = __builtin_bit_cast(u32x4,
+                                    __builtin_amdgcn_raw_buffer_load_b128(wrsrc, 16 * (CH * kWave + lane), base, 0));
+#pragma unroll
+            for (int i = 0; i < kTallMaxRows / kWave; i++)
+                rxe[i] = __builtin_amdgcn_raw_buffer_load_b16(xersrc, min(lane + kWave * i, rows - 1) * xe_stride(n),
+                                                              2 * p, 0);
+        };
+        // Q8_0 chunk c holds a row's columns 16 c .. + 15 (step c); Q4_0
+        // chunk c its block c, byte i the columns 32 c + i (low nibble, step
+        // 2 c) and 32 c + 16 + i (high, step 2 c + 1).  Lane l of a step's
+        // fragment: weight row l % 32 of the block, columns 8 (l / 32) .. + 7
+        // of the step.
+        auto convert = [&](int b) {
+            const int cb = lane / 32, l = lane % 32;
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                const u32x4 q = rq[c];
+                if constexpr (T == ANEHIP_GGML_Q8_0) {
+                    wf[b][c][cb][l] = q8_fragment(q.x, q.y);
+                    wf[b][c][cb][l + 32] = q8_fragment(q.z, q.w);
+                } else {
+                    wf[b][2 * c][cb][l] = q4_fragment(q.x, q.y, 0);
+                    wf[b][2 * c][cb][l + 32] = q4_fragment(q.z, q.w, 0);
+                    wf[b][2 * c + 1][cb][l] = q4_fragment(q.x, q.y, 4);
+                    wf[b][2 * c + 1][cb][l + 32] = q4_fragment(q.z, q.w, 4);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // one chunk's fragments at a time
+            }
+            dsc[b][lane] = rs;
+#pragma unroll
+            for (int i = 0; i < kTallMaxRows / kWave; i++) xes[b][lane + kWave * i] = (uint16_t)rxe[i];
+        };
+        load_raw(0);
+        convert(0);
+        load_raw(1);
+        __syncthreads();  // unit 0's fragments ready
+        for (int u = 0; u < units; u++) {
+            // unit u + 1 into the parity unit u - 1 read (past the last unit:
+            // not read), then the loads of unit u + 2
+            convert((u + 1) & 1);
+            load_raw(u + 2);
+            __syncthreads();  // end of unit u
+        }
+        return;
+    }
+
+    // The compute waves: wave w takes x rows 32 w .. + 31
+    const int grows = rows - 32 * wave;  // rows of this wave's group (<= 0: products not stored)
     const bool active = grows > 0;
     const Planes gp = xp.group(active ? wave : 0, n);
     const int brow = min(lane & 31, (active ? min(grows, 32) : 1) - 1);  // rows past the group repeat its last
     const int8_t *xe_row = gp.xe + (size_t)brow * xe_stride(n);
-    auto item_of = [&](int u) { return (int)blockIdx.x + G * (u / per); };
-    auto panel_of = [&](int u) { return (item_of(u) % ksplit) * per + u % per; };
-
-    // unit u's panel bytes: thread t takes quant vectors t, t + 512, ... of
-    // the NT tiles' panels (vector v: tile v / (16 CH), chunk v / 64 % CH,
-    // weight row v % 64), the scale vector of row t % 64 of tile (t / 64) %
-    // NT (a tile past the matrix reads the last one again: its rows are
-    // never stored) and the two group exponents of x row t % 256 (the last
-    // row past the rows) for the unit's panel.  Buffer loads: the offset
-    // within a panel per lane, the panel's offset wave-uniform.
-    const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(Wp), 0, (int)((size_t)ptiles * nsb * Panel<T>::kBytes), kBufferWord3);
-    const __amdgpu_buffer_rsrc_t xersrc =
-        __builtin_amdgcn_make_buffer_rsrc(xp.xe, 0, rows * xe_stride(n), kBufferWord3);
-    const int xe_off = min((int)threadIdx.x % kTallMaxRows, rows - 1) * xe_stride(n);
-    u32x4 rq[QV], rs = {};
-    uint32_t rxe = 0;
-    auto load_raw = [&](int u) {
-        const int tg = item_of(u) / ksplit, p = panel_of(u);
-#pragma unroll
-        for (int j = 0; j < QV; j++) {
-            constexpr int kTileVecs = CH * kWave;
-            const int pt = NTH * j / kTileVecs;  // the same for all threads
-            const int tile = min(tg * NT + pt, ptiles - 1);
-            rq[j] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, 16 * ((int)threadIdx.x + NTH * j - pt * kTileVecs),
-                                                             (tile * nsb + p) * Panel<T>::kBytes, 0));
-        }
-        // (every thread loads and stores them, waves w, w + NT, ... the same
-        // values, so that no load sits in a branch, where the compiler would
-        // sink it to its use)
-        const int tile = min(tg * NT + wave % NT, ptiles - 1);
-        rs = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                           wrsrc, 16 * (CH * kWave + lane), (tile * nsb + p) * Panel<T>::kBytes, 0));
-        rxe = __builtin_amdgcn_raw_buffer_load_b16(xersrc, xe_off, 2 * p, 0);
-    };
-    // registers -> fp16 B fragments of parity b.  Q8_0 chunk c holds a row's
-    // columns 16 c .. + 15 (step c); Q4_0 chunk c its block c, byte i the
-    // columns 32 c + i (low nibble, step 2 c) and 32 c + 16 + i (high, step
-    // 2 c + 1).  Lane l of a step's fragment: weight row l % 32 of the block,
-    // columns 8 (l / 32) .. + 7 of the step.
-    auto convert = [&](int b) {
-#pragma unroll
-        for (int j = 0; j < QV; j++) {
-            const int v = (int)threadIdx.x + NTH * j, c = v / kWave % CH, r = v % kWave;
-            const int cb = 2 * (v / (CH * kWave)) + r / 32, l = r % 32;
-            const u32x4 q = rq[j];
-            if constexpr (T == ANEHIP_GGML_Q8_0) {
-                wf[b][c][cb][l] = q8_fragment(q.x, q.y);
-                wf[b][c][cb][l + 32] = q8_fragment(q.z, q.w);
-            } else {
-                wf[b][2 * c][cb][l] = q4_fragment(q.x, q.y, 0);
-                wf[b][2 * c][cb][l + 32] = q4_fragment(q.z, q.w, 0);
-                wf[b][2 * c + 1][cb][l] = q4_fragment(q.x, q.y, 4);
-                wf[b][2 * c + 1][cb][l + 32] = q4_fragment(q.z, q.w, 4);
-            }
-        }
-        dsc[b][threadIdx.x % (NT * kWave)] = rs;
-        xes[b][threadIdx.x % kTallMaxRows] = (uint16_t)rxe;
-    };
     // block j of panel p (steps 16 p + 2 j, + 1): hi and lo fragments
     // (buffer loads: the lane's offset in a step's 1 KiB, the step's offset
     // wave-uniform)
@@ -2431,13 +2443,11 @@ __global__ __launch_bounds__(kWave *kTallWaves) __attribute__((amdgpu_waves_per_
         a[2] = __builtin_bit_cast(h8v, __builtin_amdgcn_raw_buffer_load_b128(hrsrc, xoff, so + 1024, 0));
         a[3] = __builtin_bit_cast(h8v, __builtin_amdgcn_raw_buffer_load_b128(lrsrc, xoff, so + 1024, 0));
     };
-    f32x16 acc[CB];
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++) acc[cb] = f32x16{};
+    f32x16 acc[2] = {f32x16{}, f32x16{}};
     // an item's sums: element r of lane l is row 8 (r / 4) + 4 (l / 32) +
-    // r % 4 of the group, weight row 32 cb + l % 32 of the item
+    // r % 4 of the group, weight row 32 cb + l % 32 of the tile
     auto store_item = [&](int item) {
-        const int tg = item / ksplit, ks = item % ksplit;
+        const int tile = item / ksplit, ks = item % ksplit;
         // opaque copies: the row addresses and scales are rebuilt here, not
         // kept live across the unit loop
         float *ob = out;
@@ -2450,17 +2460,15 @@ __global__ __launch_bounds__(kWave *kTallWaves) __attribute__((amdgpu_waves_per_
                 const float sc = xe_scale(erow[w][gr]);
                 float *orow = ob + (size_t)ks * split_stride + (size_t)(32 * w + gr) * m;
 #pragma unroll
-                for (int cb = 0; cb < CB; cb++) {
-                    const int wr = tg * NT * kWave + 32 * cb + (ln & 31);
+                for (int cb = 0; cb < 2; cb++) {
+                    const int wr = tile * kWave + 32 * cb + (ln & 31);
                     if (wr < m) orow[wr] = acc[cb][r] * sc;
                 }
             }
         }
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++) acc[cb] = f32x16{};
+        acc[0] = f32x16{};
+        acc[1] = f32x16{};
     };
-    if (units == 0) return;
-    load_raw(0);
     // E over the whole row (one exponent for every K split of it), from
     // 16-byte loads of the row's exponents (a row's are padded to 16 bytes),
     // all issued before the first is used
@@ -2479,19 +2487,15 @@ __global__ __launch_bounds__(kWave *kTallWaves) __attribute__((amdgpu_waves_per_
         for (int g = 64; g < ng; g++) E = max(E, (int)xe_row[g]);  // n > 8192
     }
     if (lane < 32) erow[wave][lane] = E;
-    convert(0);
     __syncthreads();  // unit 0's fragments ready, erow written
-    // x of the next three blocks is always in flight: xa[i % 4] for block i
+    // x of the next two blocks is always in flight: xa[i % 4] for block i
     // of the workgroup's sequence of units x 8 blocks.  Every wave issues
     // the same loads and products on every unit (waves without rows take
     // group 0's x and store nothing; past the last unit, a valid panel), so
     // that the loop has one path and the loads in flight are the same on it.
     h8v xa[4][4];
-    f32x16 cc[2] = {f32x16{}, f32x16{}};
-    float dd[2] = {0.0f, 0.0f};
     load_x(panel_of(0), 0, xa[0]);
     load_x(panel_of(0), 1, xa[1]);
-    load_x(panel_of(0), 2, xa[2]);
     for (int u0 = 0; u0 < units; u0 += per) {
     for (int u = u0; u < u0 + per; u++) {
         const int b = u & 1, p = panel_of(u);
@@ -2503,49 +2507,30 @@ __global__ __launch_bounds__(kWave *kTallWaves) __attribute__((amdgpu_waves_per_
             h8v(&a)[4] = xa[j % 4];
 #pragma unroll
             for (int i = 0; i < 4; i++) a[i] *= f;
-            // then x of the block three ahead (the next unit's first three)
-            // and, at block 0, the next unit's panel bytes (their wait comes
-            // at block 4; at the unit's start nothing is in flight, so block
-            // 0's x wait costs nothing)
+            // then x of the block two ahead (the next unit's first two)
             __builtin_amdgcn_sched_barrier(0);
-            if (j < 5) load_x(p, j + 3, xa[(j + 3) % 4]);
-            else load_x(panel_of(u + 1), j - 5, xa[(j + 3) % 4]);
-            if (j == 0) load_raw(u + 1);
+            if (j < 6) load_x(p, j + 2, xa[(j + 2) % 4]);
+            else load_x(panel_of(u + 1), j - 6, xa[(j + 2) % 4]);
             __builtin_amdgcn_sched_barrier(0);
-            // (block, weight block) steps as a two-stage pipeline: step i's
-            // products into cc[i % 2] on the MFMAs while the VALU adds step
-            // i - 1's, times its scale, to its sums
 #pragma unroll
-            for (int cb = 0; cb < CB; cb++) {
+            for (int cb = 0; cb < 2; cb++) {
                 const h8v b0 = wf[b][2 * j][cb][lane], b1 = wf[b][2 * j + 1][cb][lane];
-                f32x16 &c = cc[cb & 1];
-                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b0, f32x16{}, 0, 0, 0);
+                f32x16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b0, f32x16{}, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], b0, c, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[2], b1, c, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[3], b1, c, 0, 0, 0);
-                const int pcb = (cb + CB - 1) % CB;
-                const f32x16 &cp = cc[(cb + 1) & 1];
-                const float dp = dd[(cb + 1) & 1];
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[pcb][r] = fmaf(cp[r], dp, acc[pcb][r]);
-                // the sums are added here, not deferred (which would keep
-                // every step's products live)
-                asm volatile("" : "+v"(acc[pcb]));
                 const uint32_t dw = reinterpret_cast<const uint32_t *>(&dsc[b][32 * cb + (lane & 31)])[j >> 1];
-                dd[cb & 1] = __half2float(__ushort_as_half((unsigned short)(dw >> (16 * (j & 1)))));
+                const float d = __half2float(__ushort_as_half((unsigned short)(dw >> (16 * (j & 1)))));
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[cb][r] = fmaf(c[r], d, acc[cb][r]);
+                // the sums are added here, not deferred (which would keep
+                // every block's products live)
+                asm volatile("" : "+v"(acc[cb]));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        // unit u + 1's fragments into the parity unit u - 1 read (past the
-        // last unit: not read)
-        convert(b ^ 1);
-        __syncthreads();  // unit u + 1's fragments ready; every wave is done with parity b
+        __syncthreads();  // end of unit u: unit u + 1's fragments ready; every wave is done with parity b
     }
-    // the item's last step, then its sums out
-#pragma unroll
-    for (int r = 0; r < 16; r++) acc[CB - 1][r] = fmaf(cc[1][r], dd[1], acc[CB - 1][r]);
-    cc[1] = f32x16{};
-    dd[1] = 0.0f;
     if (active) store_item(item_of(u0));
     }
 }
@@ -3089,8 +3074,7 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
 }
 
 // K split of gemm_tall (one tile per item: two tiles per item measured 9.6 us
-// per unit against 4.6 us for one, no gain per row, so gemm_tall<T, 2> is
-// not launched): a divisor of the panel count (at most 16, the partial slices
+// per unit against 4.6 us for one, no gain per row): a divisor of the panel count (at most 16, the partial slices
 // a consumer sums) minimising an estimate of the busiest CU's time,
 // ceil(items / CUs) x panels per split x the measured time of one unit at 256
 // rows (4.6 us on MI355X), plus the traffic of the extra partial slices
@@ -3133,15 +3117,15 @@ int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, co
     const int items = ptiles * ksplit;
     // one workgroup per CU, each walking its items' panels in one pipeline
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const dim3 grid((unsigned)std::min(items, cus)), block(kWave * kTallWaves);
+    const dim3 grid((unsigned)std::min(items, cus)), block(kWave * (kTallWaves + 1));
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     const int per = nsb / ksplit;
     const size_t ss = (size_t)rows * m;
     if (ggml_type == ANEHIP_GGML_Q8_0)
-        hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q8_0, 1>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
+        hipLaunchKernelGGL(gemm_tall<ANEHIP_GGML_Q8_0>, grid, block, 0, stream, w, xp, out, (int)m, (int)n,
                            (int)rows, ksplit, per, ss);
     else
-        hipLaunchKernelGGL((gemm_tall<ANEHIP_GGML_Q4_0, 1>), grid, block, 0, stream, w, xp, out, (int)m, (int)n,
+        hipLaunchKernelGGL(gemm_tall<ANEHIP_GGML_Q4_0>, grid, block, 0, stream, w, xp, out, (int)m, (int)n,
                            (int)rows, ksplit, per, ss);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
