@@ -170,14 +170,16 @@ def test_packed_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
 @pytest.mark.gpu
 @pytest.mark.parametrize("t", [8, 2])
 @pytest.mark.parametrize("batch", [33, 100, 256])
-@pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144), (8224, 2048), (2048, 2048), (12288, 1792), (100, 256)])
+@pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144), (8224, 2048), (2048, 2048), (12288, 1792), (100, 256),
+                                 (32968, 256)])
 def test_packed_gemm_tall(gpu_ctx, oracle_lib, t, batch, m, n):
     """More than 32 rows (the prefill's chunk GEMM, gemm_tall): 32-row groups
     of planes, one per compute wave (33: one full group and one row, six
     waves without rows; 100 and 256: partial and full), a ragged last weight
-    tile (8224 rows; 100 rows: two tiles, the second ragged), workgroups
-    walking several items and K splits that divide the panel count (12288 x
-    1792: 7 panels; 2048 x 2048: 8 splits)."""
+    tile (8224 rows; 100 rows: two tiles, the second ragged), K splits that
+    divide the panel count (12288 x 1792: 7 panels; 2048 x 2048: 8 splits),
+    and workgroups walking several items (32968 x 256: 516 one-panel items,
+    2 or 3 per workgroup, the last tile ragged)."""
     w = oracle_lib.gen_quant(t, 77, m + 3 * n + t, m, n, std=0.02)
     x = oracle_lib.normal(77, 900 + batch, batch * n).reshape(batch, n)
     dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
