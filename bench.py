@@ -236,18 +236,21 @@ def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
             "algorithmic_GB_per_step": round(step_bytes / 1e9, 3),
             "effective_GB_s": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
         }
-    if prefill_tokens:
+    lengths = [prefill_tokens] if isinstance(prefill_tokens, int) else list(prefill_tokens)
+    lengths = [n for n in lengths if n]
+    if lengths:
         # anehip_prefill of one sequence from position 0 (chunks of 256 tokens),
         # synchronous, timed on the host clock; one untimed run first
-        gm.alloc_state(1, max(1024, prefill_tokens))
-        prompt = (np.arange(prefill_tokens, dtype=np.uint32) * 7919) % spec.vocab_size
-        gm.prefill(0, prompt, want_logits=False)
-        gm.set_pos(0, 0)
-        t0 = time.perf_counter()
-        gm.prefill(0, prompt, want_logits=True)
-        dt = time.perf_counter() - t0
-        out[f"prefill_B1_tokens{prefill_tokens}"] = {"tok_s": round(prefill_tokens / dt, 1),
-                                                    "ms": round(dt * 1e3, 2)}
+        gm.alloc_state(1, max([1024] + lengths))
+        for n_tok in lengths:
+            prompt = (np.arange(n_tok, dtype=np.uint32) * 7919) % spec.vocab_size
+            gm.set_pos(0, 0)
+            gm.prefill(0, prompt, want_logits=False)
+            gm.set_pos(0, 0)
+            t0 = time.perf_counter()
+            gm.prefill(0, prompt, want_logits=True)
+            dt = time.perf_counter() - t0
+            out[f"prefill_B1_tokens{n_tok}"] = {"tok_s": round(n_tok / dt, 1), "ms": round(dt * 1e3, 2)}
     gm.close()
     return out
 
@@ -660,7 +663,7 @@ def main():
     out["configs2_q4"] = bench_q4(anehip, ctx)
     out["configs3_deltanet"] = bench_deltanet(anehip, ctx)
     if not args.no_decode:
-        out["decode"] = bench_decode(anehip, args.decode_steps, 3, prefill_tokens=512)
+        out["decode"] = bench_decode(anehip, args.decode_steps, 3, prefill_tokens=(512, 2048))
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(anehip, ctx, shapes, args.cpu_seconds, decode=not args.no_decode)
     ctx.close()
