@@ -79,8 +79,6 @@ def lib():
             "anehip_argmax": (C.c_int, [vp, vp, u32, u32, vp]),
             "anehip_fill_random": (C.c_int, [vp, vp, sz, u32, u32, C.c_uint64, f32, f32]),
             "anehip_quantize": (C.c_int, [vp, u32, vp, u32, u32, vp]),
-            "anehip_probe_read": (C.c_int, [vp, vp, sz, u32, u32, u32, vp]),
-            "anehip_probe_empty": (C.c_int, [vp, u32, u32]),
             "anehip_upload_quant": (C.c_int, [vp, i32, u32, vp, sz, u32, u32, u32]),
             "anehip_upload_f32": (C.c_int, [vp, i32, u32, vp, sz]),
             "anehip_tensor_ptr": (C.c_int, [vp, i32, u32, u32, C.POINTER(vp), C.POINTER(sz)]),

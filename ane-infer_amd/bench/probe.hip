@@ -1,10 +1,12 @@
-// Roofline probes: the floor a bandwidth-bound launch of a given size and grid
-// can reach on this device, measured with the same launch path and timers as
-// the kernels it bounds.  probe_read_kernel streams a buffer in 16-byte loads
+// Roofline probes (libanehip_probe.so, loaded by bench.py only; not part of
+// the product library): the floor a bandwidth-bound launch of a given size and
+// grid can reach on this device, measured with the same launch path, stream
+// and timers as the kernels it bounds.  probe_read_kernel streams a buffer in 16-byte loads
 // (grid-stride, DEPTH independent loads in flight per thread, the values
 // folded into one XOR so the loads stay live); probe_empty_kernel does
 // nothing, which gives the fixed cost of one launch of that grid.
-#include "common.h"
+#include "../csrc/common.h"
+#include "probe.h"
 
 namespace anehip {
 namespace {

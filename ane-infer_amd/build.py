@@ -1,5 +1,7 @@
-"""Builds libanehip.so (all HIP sources in csrc/) for gfx950 with hipcc, and
-libane_engine.so (the C++ host API in engine/, over libanehip) with g++.
+"""Builds libanehip.so (all HIP sources in csrc/) for gfx950 with hipcc,
+libane_engine.so (the C++ host API in engine/, over libanehip) with g++, and
+libanehip_probe.so (bench/: the measurement-only roofline probes bench.py
+loads, over libanehip).
 
 Usage: python ane-infer_amd/build.py
 The libraries are written next to this file so they travel with the source tree.
@@ -12,6 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "libanehip.so")
 ENGINE_LIB = os.path.join(HERE, "libane_engine.so")
+PROBE_LIB = os.path.join(HERE, "libanehip_probe.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
 OBJ_DIR = os.path.join(HERE, "_build")
@@ -64,7 +67,20 @@ def build(verbose: bool = False) -> str:
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs], "link")
     os.replace(tmp, LIB)
     build_engine(verbose)
+    build_probe(hipcc, verbose)
     return LIB
+
+
+def build_probe(hipcc: str, verbose: bool = False) -> str:
+    """The measurement-only probe library (bench/probe.hip), linked to libanehip."""
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [hipcc, *HIPCC_FLAGS, "-shared", "-o", tmp, os.path.join(HERE, "bench", "probe.hip"), f"-L{HERE}",
+           "-lanehip", "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    _run(cmd, "hipcc probe.hip")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 def build_engine(verbose: bool = False) -> str:

@@ -99,46 +99,46 @@ __global__ void quantize_kernel(const float *__restrict__ w, size_t nblocks, uin
 // (4 MiB) in all.  Each GPU the library runs on holds its own copy until the
 // process ends.  In host code `scratch` names a host-side stand-in, never the
 // device memory: host code uses the address hipGetSymbolAddress returned for
-// the device (NoAllocSlot::ptr).
+// the device (anehip_ctx::noalloc_scratch, set by noalloc_setup).
 constexpr size_t kScratchFloats = (size_t)1 << 20;
 constexpr size_t kScratchTable = 256;  // floats reserved for the RoPE table
 __device__ __align__(256) float scratch[kScratchFloats];
 
-struct NoAllocSlot {
-    float *ptr = nullptr;     // device address of `scratch` on this device
-    float table_base = 0.0f;  // rope base of the table now in the scratch (0: none)
-};
 constexpr int kMaxDevices = 64;
-NoAllocSlot g_noalloc[kMaxDevices];
+float *g_noalloc[kMaxDevices];  // device address of `scratch` per device (null: not looked up yet)
 std::mutex g_noalloc_mu;
 
-// The scratch address on ctx's device (looked up once per device, with that
-// device current), and a RoPE table for `rope_base` at its start.
-int noalloc_scratch(anehip_ctx *ctx, float rope_base, float **out) {
-    std::lock_guard<std::mutex> lock(g_noalloc_mu);
-    if (ctx->device < 0 || ctx->device >= kMaxDevices)
-        return set_error(ctx->err, ANEHIP_EUNSUPPORTED, "noalloc: device %d beyond %d", ctx->device, kMaxDevices);
-    NoAllocSlot &slot = g_noalloc[ctx->device];
-    ANEHIP_HIP_TRY(ctx->err, hipSetDevice(ctx->device));
-    if (!slot.ptr) {
-        void *p = nullptr;
-        ANEHIP_HIP_TRY(ctx->err, hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-        if (!p) return set_error(ctx->err, ANEHIP_EHIP, "noalloc: no device address for the scratch array");
-        slot.ptr = static_cast<float *>(p);
-    }
-    if (slot.table_base != rope_base) {
-        float f[128];
-        rope_inv_freq(rope_base, 256, f);
-        // ordered after the stream's queued work; the host array must outlive the copy
-        ANEHIP_HIP_TRY(ctx->err, hipMemcpyAsync(slot.ptr, f, sizeof f, hipMemcpyHostToDevice, ctx->stream));
-        ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
-        slot.table_base = rope_base;
-    }
-    *out = slot.ptr;
-    return ANEHIP_OK;
+// The RoPE table of one call, by value: a kernel argument is recorded in the
+// graph node when the call is captured, so no host buffer has to outlive the
+// launch and a replay writes its own table again.
+struct RopeTab {
+    float f[128];
+};
+__global__ __launch_bounds__(128) void rope_table_kernel(RopeTab tab, float *__restrict__ dst) {
+    dst[threadIdx.x] = tab.f[threadIdx.x];
 }
 
 }  // namespace
+
+namespace anehip {
+
+// Set-up of the entry point that allocates nothing, at context creation with
+// the context's device current: the scratch address on this device, looked
+// up once per device.
+int noalloc_setup(anehip_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices) return ANEHIP_OK;  // the entry point refuses such devices
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc[ctx->device]) {
+        void *p = nullptr;
+        ANEHIP_HIP_TRY(ctx->err, hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return set_error(ctx->err, ANEHIP_EHIP, "noalloc: no device address for the scratch array");
+        g_noalloc[ctx->device] = static_cast<float *>(p);
+    }
+    ctx->noalloc_scratch = g_noalloc[ctx->device];
+    return ANEHIP_OK;
+}
+
+}  // namespace anehip
 
 extern "C" {
 
@@ -251,9 +251,16 @@ int anehip_attention_step_noalloc(anehip_ctx *ctx, uint32_t batch, uint32_t n_he
                          "attention_step_noalloc: %zu partial floats needed, the static scratch holds %zu "
                          "(batch %u, %u kv heads, max_seq %u)",
                          need, kScratchFloats - kScratchTable, batch, n_kv_heads, max_seq);
-    float *ptr = nullptr;
-    int rc = noalloc_scratch(ctx, rope_base, &ptr);
-    if (rc) return rc;
+    float *ptr = ctx->noalloc_scratch;
+    if (!ptr)
+        return set_error(ctx->err, ANEHIP_ESTATE, "attention_step_noalloc: no static scratch on device %d",
+                         ctx->device);
+    // the call's RoPE table goes to the scratch ahead of its attention launch
+    // (same host formula as the allocating entry point, so the same bits)
+    RopeTab tab;
+    rope_inv_freq(rope_base, 256, tab.f);
+    hipLaunchKernelGGL(rope_table_kernel, dim3(1), dim3(128), 0, ctx->stream, tab, ptr);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     MixIn mix;
     mix.p = qkv;
     mix.stride = (int)(n_heads * 2 * 256 + 2 * n_kv_heads * 256);

@@ -57,6 +57,7 @@ struct anehip_ctx {
     int cu_count = 0;
     float *inv_freq = nullptr;      // RoPE table of the kernel-level attention entry
     float inv_freq_base = 0.0f;
+    float *noalloc_scratch = nullptr;  // this device's static scratch (api.hip, anehip_attention_step_noalloc)
 };
 
 namespace anehip {
@@ -64,6 +65,9 @@ namespace anehip {
 // Ensures the workspace holds at least `floats` floats (grown with
 // hipMalloc; refused while the context stream is being captured).
 int ensure_workspace(anehip_ctx *ctx, size_t floats);
+// Looks up the static scratch of anehip_attention_step_noalloc on the
+// context's device (once per device; the device must be current).
+int noalloc_setup(anehip_ctx *ctx);
 
 // How a batch-1 GEMV forms its input vector from what the previous kernels
 // left in memory (the element-wise step is fused into the GEMV's prologue, so

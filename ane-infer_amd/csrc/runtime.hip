@@ -95,6 +95,7 @@ int anehip_ctx_create(int device, const anehip_model_desc *desc, anehip_ctx **ou
         return set_error(global_error(), ANEHIP_EHIP, "ctx_create: stream/event creation failed");
     }
     int rc = ensure_workspace(ctx, 0);
+    if (rc == ANEHIP_OK) rc = noalloc_setup(ctx);
     if (rc == ANEHIP_OK && desc) rc = anehip_model_setup(ctx, desc);
     if (rc != ANEHIP_OK) {
         set_error(global_error(), rc, "ctx_create: %s", ctx->err.msg.c_str());

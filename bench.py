@@ -255,6 +255,37 @@ def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
     return out
 
 
+_probe = None
+
+
+def probe_lib():
+    """libanehip_probe.so: the measurement-only roofline probes (built beside
+    libanehip.so; not part of the product library)."""
+    global _probe
+    if _probe is None:
+        import ctypes as C
+
+        path = os.path.join(ROOT, "ane-infer_amd", "libanehip_probe.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} not built; run python ane-infer_amd/build.py")
+        L = C.CDLL(path)
+        vp, u32 = C.c_void_p, C.c_uint32
+        L.anehip_probe_read.argtypes = [vp, vp, C.c_size_t, u32, u32, u32, vp]
+        L.anehip_probe_read.restype = C.c_int
+        L.anehip_probe_empty.argtypes = [vp, u32, u32]
+        L.anehip_probe_empty.restype = C.c_int
+        _probe = L
+    return _probe
+
+
+def probe_read(ctx, src, nbytes, wgs, threads, depth, sink):
+    ctx._check(probe_lib().anehip_probe_read(ctx.h, src, nbytes, wgs, threads, depth, sink.ptr))
+
+
+def probe_empty(ctx, wgs, threads):
+    ctx._check(probe_lib().anehip_probe_empty(ctx.h, wgs, threads))
+
+
 FLOOR_GRIDS = [(96, 1024), (192, 1024), (256, 256), (256, 512), (384, 512), (512, 256), (512, 512), (1024, 256), (1024, 512),
                (2048, 256)]
 FLOOR_DEPTHS = [2, 4, 8]
@@ -269,14 +300,14 @@ def c0_floor(ctx, s, launches=40):
     res = {}
     for wgs, threads in FLOOR_GRIDS:
         for depth in FLOOR_DEPTHS:
-            g = capture(ctx, lambda: [ctx.call("probe_read", s.pptr(c), s.pbytes, wgs, threads, depth, sink)
+            g = capture(ctx, lambda: [probe_read(ctx, s.pptr(c), s.pbytes, wgs, threads, depth, sink)
                                       for c in range(launches)])
             ms = time_graphs(ctx, [g], 3) / 3 / launches
             ctx.graph_destroy(g)
             res[f"{wgs}x{threads}_d{depth}"] = round(ms * 1e3, 3)
     empty = {}
     for wgs, threads in ((256, 512), (288, 512)):
-        g = capture(ctx, lambda: [ctx.call("probe_empty", wgs, threads) for _ in range(launches)])
+        g = capture(ctx, lambda: [probe_empty(ctx, wgs, threads) for _ in range(launches)])
         empty[f"{wgs}x{threads}"] = round(time_graphs(ctx, [g], 3) / 3 / launches * 1e3, 3)
         ctx.graph_destroy(g)
     sink.free()
@@ -306,11 +337,11 @@ def b1_floors(anehip, ctx, launches=40):
         sink = ctx.alloc(wgs * 512 * 4)
         reads = {}
         for depth in FLOOR_DEPTHS:
-            g = capture(ctx, lambda: [ctx.call("probe_read", s.pptr(c), s.pbytes, wgs, 512, depth, sink)
+            g = capture(ctx, lambda: [probe_read(ctx, s.pptr(c), s.pbytes, wgs, 512, depth, sink)
                                       for c in range(launches)])
             reads[depth] = time_graphs(ctx, [g], 3) / 3 / launches * 1e3
             ctx.graph_destroy(g)
-        g = capture(ctx, lambda: [ctx.call("probe_empty", wgs, 512) for _ in range(launches)])
+        g = capture(ctx, lambda: [probe_empty(ctx, wgs, 512) for _ in range(launches)])
         empty = time_graphs(ctx, [g], 3) / 3 / launches * 1e3
         ctx.graph_destroy(g)
         best = min(reads, key=reads.get)
@@ -424,8 +455,10 @@ def time_cpu(fn, budget_s, min_runs=20):
 
 def cpu_baseline(anehip, ctx, shapes, budget_s, decode):
     """Oracle (restated reference CPU path) on this host: row-parallel q8_gemv
-    over the config-1 shapes at M = 1, and, if `decode`, qwen35_forward_token
-    tok/s at B = 1 on the same random-init 2B-shape weights."""
+    over the config-1 shapes at M = 1, q4_gemv_cpu, the DeltaNet step at B = 1
+    / 8 / 32 (B independent sequences), and, if `decode`,
+    qwen35_forward_token tok/s at B = 1 and B = 32 (32 independent sequences)
+    on the same random-init 2B-shape weights."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
@@ -489,6 +522,23 @@ def cpu_baseline(anehip, ctx, shapes, budget_s, decode):
                           "GB/s": round(dn_step_bytes(1) / med / 1e9, 2), "runs": runs, "cores": 1,
                           "sample": "deltanet_decode_step's conv + norms + gates + recurrence (restated), "
                                     "one sequence, single thread (the reference's loop is serial)"}
+    # configs[3] at B = 8 / 32: the reference has no batch, so a batched step
+    # is B independent sequences' steps, each on its own state and window
+    for batch in (8, 32):
+        Ss = [S.copy() for _ in range(batch)]
+        wins = [win.copy() for _ in range(batch)]
+
+        def dn_batch(batch=batch, Ss=Ss, wins=wins):
+            q, b, a = steps_in[k[0] % 8]
+            k[0] += 1
+            for i in range(batch):
+                oracle.deltanet_core(q, b, a, conv_w, ssm_a, dt_bias, wins[i], Ss[i], DN_HEADS, 128)
+
+        med, runs, _ = time_cpu(dn_batch, budget_s / 8, min_runs=5)
+        res[f"deltanet_B{batch}"] = {"us_per_step_median": round(med * 1e6, 1),
+                                     "GB/s": round(dn_step_bytes(batch) / med / 1e9, 2), "runs": runs, "cores": 1,
+                                     "sample": f"{batch} sequences' deltanet_decode_step in turn per step "
+                                               "(restated), single thread"}
     if decode:
         spec = anehip.Spec()
         gm = anehip.Model(spec)
@@ -522,6 +572,28 @@ def cpu_baseline(anehip, ctx, shapes, budget_s, decode):
         res["decode_sample"] = (f"{n_tok} greedy tokens of qwen35_forward_token (restated) at positions "
                                 f"{start + 1}..{start + n_tok}, 2B shape, Q8_0, {threads} threads for the GEMVs")
         seq.close()
+        # B = 32 as 32 independent sequences (the reference decodes one
+        # sequence at a time): each round gives every sequence one token
+        seqs = []
+        for i in range(32):
+            q = oracle.OracleSeq(om, cap)
+            q.pos = start
+            seqs.append(q)
+        toks = [1 + i for i in range(32)]
+        rounds, t32 = 0, 0.0
+        t_end = time.perf_counter() + budget_s
+        while (time.perf_counter() < t_end or rounds < 1) and seqs[0].pos < cap - 1:
+            t0 = time.perf_counter()
+            for i, q in enumerate(seqs):
+                toks[i] = oracle.argmax(q.forward(toks[i], threads))
+            t32 += time.perf_counter() - t0
+            rounds += 1
+        res["decode_tok_s_B32_ctx1k"] = round(32 * rounds / t32, 2)
+        res["decode_B32_sample"] = (f"{rounds} rounds of one greedy token for each of 32 independent sequences "
+                                    f"(qwen35_forward_token restated, positions from {start + 1}), "
+                                    f"{threads} threads for the GEMVs")
+        for q in seqs:
+            q.close()
         om.close()
     return res
 
@@ -592,9 +664,13 @@ def main():
         return
     shapes = [Shape(anehip, ctx, m, n, 100 + i) for i, (m, n) in enumerate(SHAPES)]
 
-    # one graph per rotation phase r: every shape's points on copy r
+    # one graph per rotation phase r; every launch of a shape reads the next
+    # copy of its weights (point j of phase r: copy r * len(BATCHES) + j), so
+    # between two reads of one copy every other copy of the shape (> 512 MiB)
+    # has been read and the MALL cannot serve it
     phases = max(s.copies for s in shapes)
-    sweeps = [capture(ctx, lambda r=r: [launch_point(ctx, s, b, r) for s in shapes for b in BATCHES])
+    sweeps = [capture(ctx, lambda r=r: [launch_point(ctx, s, b, r * len(BATCHES) + j) for s in shapes
+                                        for j, b in enumerate(BATCHES)])
               for r in range(phases)]
     for i in range(args.warmup):
         ctx.graph_launch(sweeps[i % phases])

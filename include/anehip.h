@@ -267,9 +267,13 @@ int anehip_attention_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uin
  * about 4 MB whatever max_seq at batch x n_kv_heads <= 256) returns
  * ANEHIP_ERANGE and launches nothing.  Every call on one GPU shares that
  * array: calls that overlap on one GPU (other streams or contexts on the same
- * device) race.  The first call on a device, and a call with a rope_base
- * other than the last one's on that device, synchronises ctx's stream once to
- * upload the table.
+ * device) race.  Each call writes its own RoPE table into the array with a
+ * kernel launch ahead of the attention kernels (the table is a kernel
+ * argument), so the call never synchronises, copies from host memory or
+ * allocates, may be captured into a graph as its first use on a device, and a
+ * replayed graph uses the rope_base it was captured with.  The array's address
+ * on a device is looked up once, when the first context on that device is
+ * created.
  */
 int anehip_attention_step_noalloc(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, uint32_t n_kv_heads,
                                   uint32_t max_seq, const float *qkv, const float *q_norm, const float *k_norm,
@@ -289,18 +293,6 @@ int anehip_argmax(anehip_ctx *ctx, const float *logits, uint32_t rows, uint32_t 
 int anehip_fill_random(anehip_ctx *ctx, void *dptr, size_t n, uint32_t dist, uint32_t is_f16, uint64_t seed,
                        float a, float b);
 int anehip_quantize(anehip_ctx *ctx, uint32_t ggml_type, const float *w, uint32_t m, uint32_t n, void *out);
-
-/* Roofline probes (no counterpart in the reference; the measured floor for a
- * bandwidth-bound launch of a given size and grid): anehip_probe_read streams
- * nbytes (a positive multiple of 16) from device memory src in 16-byte loads
- * on workgroups x threads threads (threads a multiple of 64, at most 1024),
- * depth (1, 2, 4 or 8) loads in flight per thread; sink (device, at least
- * workgroups * threads * 4 bytes) is written only in the unlikely case that
- * a thread's XOR of its loads equals a fixed constant.  anehip_probe_empty
- * launches an empty kernel of that grid. */
-int anehip_probe_read(anehip_ctx *ctx, const void *src, size_t nbytes, uint32_t workgroups, uint32_t threads,
-                      uint32_t depth, void *sink);
-int anehip_probe_empty(anehip_ctx *ctx, uint32_t workgroups, uint32_t threads);
 
 /* ---- model-level decode step (context created with a model desc) -------- */
 

@@ -12,6 +12,14 @@ SMALL = dict(dim=256, hidden_dim=512, n_layers=4, n_heads=4, n_kv_heads=1, head_
 MID = dict(dim=512, hidden_dim=1024, n_layers=4, n_heads=4, n_kv_heads=1, head_dim=256, vocab_size=1000,
            ssm_state_size=128, ssm_conv_kernel=4, ssm_group_count=4)
 
+# A model 2304 wide (18 DeltaNet heads, 9 panels per row): its batch-1 ssm_out
+# would need 9 K splits, one per head pair, beyond the 8 partial slices a
+# consumer adds, so its batch-1 step runs the DeltaNet step as its own kernel
+# (deltanet_step_kernel) and the ssm_out GEMV's gated-norm prologue commits
+# the q / k conv windows, instead of the step fused into ssm_out.
+WIDE = dict(dim=2304, hidden_dim=512, n_layers=4, n_heads=8, n_kv_heads=2, head_dim=256, vocab_size=1000,
+            ssm_state_size=128, ssm_conv_kernel=4, ssm_group_count=18)
+
 
 class HostModel:
     def __init__(self, spec: "anehip.Spec", seed: int = 1, ggml_type: int = 8):

@@ -7,7 +7,7 @@ import pytest
 import anehip
 import oracle
 from conftest import rel_errs
-from model_util import MID, SMALL, HostModel, copy_state_to_oracle
+from model_util import MID, SMALL, WIDE, HostModel, copy_state_to_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -77,6 +77,32 @@ def test_mid_model_batched_steps(mid_host, B):
         for b in range(B):
             l2, mx = rel_errs(g[b], seqs[b].forward(int(toks[step, b])))
             assert l2 <= TOL and mx <= TOL, (step, b, l2, mx)
+    gm.close()
+    for q in seqs:
+        q.close()
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_wide_model_unfused_deltanet_step(B):
+    """The 2304-wide model (model_util.WIDE): at batch 1 the DeltaNet step is
+    deltanet_step_kernel followed by ssm_out with the gated-norm prologue that
+    commits the conv windows (the path models up to 2048 wide never take);
+    at batch 2 the 9-panel projections run on uneven K splits.  4 steps from
+    position 0 vs the oracle per sequence: logits, then every layer's
+    DeltaNet state, conv window and KV rows."""
+    host = HostModel(anehip.Spec(**WIDE), seed=9)
+    spec = host.spec
+    gm = _model(host, B, 64)
+    seqs = [host.seq(64) for _ in range(B)]
+    toks = oracle.randint(37, B, 4 * B, spec.vocab_size).reshape(4, B)
+    for step in range(4):
+        g = gm.step(toks[step])
+        for b in range(B):
+            l2, mx = rel_errs(g[b], seqs[b].forward(int(toks[step, b])))
+            print(f"wide B={B} step {step} seq {b}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+            assert l2 <= TOL and mx <= TOL, (step, b)
+    for b in range(B):
+        _check_state(gm, seqs[b], b, spec, f"wide B={B} seq {b} after 4 steps")
     gm.close()
     for q in seqs:
         q.close()
@@ -470,20 +496,26 @@ def test_prefill_long_prompt_large_cache(mid_host, n):
     oseq.close()
 
 
-def test_qwen35_2b_shape_prefill(big_host):
-    """Random-init 24-layer Qwen3.5-2B shape: a 40-token prompt (one chunk)
-    prefilled from position 0 vs the oracle run token by token (last logits),
-    then one decode step continuing the sequence."""
+@pytest.mark.parametrize("n", [40, 300])
+def test_qwen35_2b_shape_prefill(big_host, n):
+    """Random-init 24-layer Qwen3.5-2B shape: a 40-token prompt (one chunk) and
+    a 300-token one (a full 256-token chunk, recorded as the prefill's chunk
+    graph and replayed for it, then 44 rows) prefilled from position 0 vs the
+    oracle run token by token: the last logits, every layer's DeltaNet state,
+    conv window and KV rows, then one decode step continuing the sequence."""
     spec = big_host.spec
-    gm = _model(big_host, 1, 256)
-    oseq = big_host.seq(256)
-    prompt = oracle.randint(70, 40, 40, spec.vocab_size)
+    gm = _model(big_host, 1, 512)
+    oseq = big_host.seq(512)
+    prompt = oracle.randint(70, n, n, spec.vocab_size)
     g = gm.prefill(0, prompt)
-    for t in prompt:
+    for i, t in enumerate(prompt):
         r = oseq.forward(int(t))
+        if i % 64 == 63:
+            print(f"2B prefill {n}: oracle at token {i + 1}", flush=True)
     l2, mx = rel_errs(g, r)
-    print(f"2B prefill 40: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+    print(f"2B prefill {n}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
     assert l2 <= TOL and mx <= TOL
+    _check_state(gm, oseq, 0, spec, f"2B after prefill {n}")
     t = int(oracle.randint(71, 1, 1, spec.vocab_size)[0])
     assert max(rel_errs(gm.step([t])[0], oseq.forward(t))) <= TOL
     gm.close()

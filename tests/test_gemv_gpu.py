@@ -96,7 +96,9 @@ def test_gemm_lm_head_batch32(gpu_ctx, oracle_lib):
 
 
 def test_repeated_split_k_calls_are_deterministic(gpu_ctx, oracle_lib):
-    """The split-K arrival counters return to zero: repeated calls give identical bits."""
+    """The GGUF-layout GEMV (anehip_quant_gemm at batch 1) on a K-split shape:
+    gemv_fused writes its partial slices, a sum_partials launch adds them in
+    split order, so repeated calls give identical bits."""
     m, n = 2048, 6144
     w = oracle_lib.gen_quant(8, 8, 8, m, n)
     x = oracle_lib.normal(8, 9, n)

@@ -92,10 +92,12 @@ def test_packed_gemv_parity(gpu_ctx, oracle_lib, t, m, n):
 
 @pytest.mark.gpu
 def test_packed_gemv_back_to_back_splits(gpu_ctx, oracle_lib):
-    """K-split GEMVs finish in one launch (the last split of each row tile sums
-    the partials and resets the tile's counter): calls queued back to back on
-    matrices of different tile and split counts, each input used twice, all
-    match the oracle."""
+    """Batch-1 panel GEMVs queued back to back on matrices of different tile
+    and split counts share the context's workspace: few-tile matrices run on
+    gemv_rows (one launch, whole K range per workgroup, no partial sums),
+    the others as a K-split gemv_packed launch followed by a sum_partials
+    launch over the workspace's partial slices.  Each input used twice, all
+    outputs match the oracle and repeated calls give identical bits."""
     t = 8
     cases = []
     for i, (m, n) in enumerate([(6144, 2048), (2048, 6144), (100, 2048), (6144, 2048), (2048, 2048)]):

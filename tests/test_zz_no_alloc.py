@@ -1,7 +1,9 @@
 """anehip_attention_step_noalloc (the attention step on a static device
 scratch, no allocation) against anehip_attention_step on the same inputs:
 two calls in a row, the second smaller, bit-identical outputs and caches;
-a call whose partials exceed the scratch is refused before any launch."""
+the call captured into a graph as the first call of a fresh context and
+replayed, with calls of another rope_base between the replays; a call whose
+partials exceed the scratch is refused before any launch."""
 import ctypes as C
 
 import numpy as np
@@ -24,13 +26,13 @@ def _inputs(oracle_lib, batch, n_heads, n_kv, max_seq, positions, seed):
     return qkv, qn, kn, kc, vc, np.array(positions, np.uint32)
 
 
-def _run(ctx, name, case, inputs):
+def _run(ctx, name, case, inputs, rope_base=10000.0):
     batch, n_heads, n_kv, max_seq = case
     qkv, qn, kn, kc, vc, pos = inputs
     d_k, d_v = ctx.to_device(kc), ctx.to_device(vc)
     d_out = ctx.alloc(batch * n_heads * HD * 4)
     ctx.call(name, batch, n_heads, n_kv, max_seq, ctx.to_device(qkv), ctx.to_device(qn), ctx.to_device(kn),
-             10000.0, ctx.to_device(pos), d_k, d_v, d_out)
+             rope_base, ctx.to_device(pos), d_k, d_v, d_out)
     ctx.sync()
     return (d_out.download(np.float32, batch * n_heads * HD), d_k.download(np.uint16, kc.size),
             d_v.download(np.uint16, vc.size))
@@ -61,6 +63,44 @@ def test_noalloc_matches_allocating_entry_point(gpu_ctx, oracle_lib):
                                       row[n_heads * 2 * HD + n_kv * HD:], qn, kn, okc, ovc, int(pos[b]), n_heads,
                                       n_kv, HD)
         assert max(rel_errs(out[b], r)) <= 2e-4
+
+
+def test_noalloc_captured_as_first_call(gpu_ctx, oracle_lib, anehip_mod):
+    """A fresh context's first noalloc call, recorded under graph capture,
+    replays bit-identically to the allocating entry point at its own
+    rope_base, also after eager noalloc calls with another rope_base (which
+    rewrite the shared table) between the replays."""
+    case = (2, 8, 2, 512)
+    batch, n_heads, n_kv, max_seq = case
+    qkv, qn, kn, kc, vc, pos = _inputs(oracle_lib, *case, [511, 70], seed=83)
+    other = _inputs(oracle_lib, *case, [100, 3], seed=84)
+    ref = _run(gpu_ctx, "attention_step", case, (qkv, qn, kn, kc, vc, pos), rope_base=5.0e5)
+    ctx = anehip_mod.Context(0)
+    try:
+        d_q, d_qn, d_kn, d_pos = ctx.to_device(qkv), ctx.to_device(qn), ctx.to_device(kn), ctx.to_device(pos)
+        d_k, d_v = ctx.to_device(kc), ctx.to_device(vc)
+        d_out = ctx.alloc(batch * n_heads * HD * 4)
+        ctx.sync()
+        print("noalloc: capture as the context's first call", flush=True)
+        ctx.capture_begin()
+        ctx.call("attention_step_noalloc", batch, n_heads, n_kv, max_seq, d_q, d_qn, d_kn, 5.0e5, d_pos, d_k, d_v,
+                 d_out)
+        g = ctx.capture_end()
+        try:
+            for rep in range(3):
+                ctx.call("dev_memset", d_out, 0xFF, d_out.nbytes)  # poison the output between replays
+                _run(ctx, "attention_step_noalloc", case, other, rope_base=10000.0)  # rewrites the shared table
+                print(f"noalloc: replay {rep}", flush=True)
+                ctx.graph_launch(g)
+                ctx.sync()
+                got = (d_out.download(np.float32, batch * n_heads * HD), d_k.download(np.uint16, kc.size),
+                       d_v.download(np.uint16, vc.size))
+                for a, b in zip(got, ref):
+                    assert np.array_equal(a, b), f"replay {rep}"
+        finally:
+            ctx.graph_destroy(g)
+    finally:
+        ctx.close()
 
 
 def test_noalloc_refuses_oversized_call(gpu_ctx, anehip_mod):
