@@ -1294,10 +1294,24 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 
 // Range-safe planes on the GEMM side (see Planes): the largest exponent of
 // groups [g0, g0 + ng) of batch row b.
+// The row's exponents are read as dwords (a row starts 16-byte aligned, its
+// length padded to 16 bytes), four at a time with every load issued before
+// any is used, so the groups of a 2048-column row take one round trip.
 __device__ __forceinline__ int xe_max(const int8_t *__restrict__ xe, int b, int g0, int ng, int n) {
     int E = kXeEmpty;
-    const int8_t *p = xe + (size_t)b * xe_stride(n) + g0;
-    for (int g = 0; g < ng; g++) E = max(E, (int)p[g]);
+    const uint32_t *row = reinterpret_cast<const uint32_t *>(xe + (size_t)b * xe_stride(n));
+    const int w0 = g0 >> 2, w1 = (g0 + ng + 3) >> 2, wl = xe_stride(n) / 4 - 1;
+    for (int w = w0; w < w1; w += 4) {
+        uint32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = row[min(w + k, wl)];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int g = 4 * w + k;
+            const int e = (int)(int8_t)(v[k >> 2] >> (8 * (k & 3)));
+            E = g >= g0 && g < g0 + ng ? max(E, e) : E;
+        }
+    }
     return E;
 }
 
@@ -2627,22 +2641,14 @@ __device__ __forceinline__ f16x8 w_frag(const uint32_t *wl, int blk, int g) {
         d0 = __builtin_amdgcn_alignbyte(x1, x0, 2);
         d1 = __builtin_amdgcn_alignbyte(x2, x1, 2);
     }
-    f16x8 a;
+    // exact int8 (or nibble - 8) -> fp16 by placing the byte in the mantissa
+    // of 1024 (dwords_to_h8_i8 / _u4)
     if constexpr (T == ANEHIP_GGML_Q8_0) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            a[e] = (_Float16)(int)(int8_t)(d0 >> (8 * e));
-            a[4 + e] = (_Float16)(int)(int8_t)(d1 >> (8 * e));
-        }
+        return __builtin_bit_cast(f16x8, dwords_to_h8_i8(d0, d1));
     } else {
         const int sh = (g >> 1) * 4;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            a[e] = (_Float16)((int)((d0 >> (8 * e + sh)) & 15u) - 8);
-            a[4 + e] = (_Float16)((int)((d1 >> (8 * e + sh)) & 15u) - 8);
-        }
+        return __builtin_bit_cast(f16x8, dwords_to_h8_u4((d0 >> sh) & 0x0F0F0F0Fu, (d1 >> sh) & 0x0F0F0F0Fu));
     }
-    return a;
 }
 
 template <uint32_t T>
@@ -2678,15 +2684,6 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint
     const int sb_end = min(nsb, sb_begin + sb_per_split);
     const int li = lane & 15;  // A row (batch) / B column (weight row) within a 16 tile
     const int g = lane >> 4;   // k group (8 columns) / D row group
-    // range-safe planes: the split's groups (2 per super-block) of batch row
-    // li + 16 nt brought to one exponent En[nt]
-    int En[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int b = min(li + 16 * nt, batch - 1);
-        En[nt] = xe_max(xp.xe, b, 2 * sb_begin, 2 * (sb_end - sb_begin), n);
-        if (wave == 0 && g == 0) xeE[li + 16 * nt] = En[nt];  // read after the reduction barrier
-    }
 
     f32x4 acc[4][NT];
 #pragma unroll
@@ -2701,46 +2698,102 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint
     const uint32_t *lds_words = reinterpret_cast<const uint32_t *>(lds[wave]);
     constexpr int kSegWords = QTraits<T>::kSbBytes / 4;
 
+    // the two group exponents of super-block s for batch row li + 16 nt,
+    // loaded with that super-block's weights (one super-block ahead), so the
+    // block loop multiplies by a factor already in registers
+    auto xe_pair = [&](int s, int nt) {
+        const int8_t *e = xp.xe + (size_t)min(li + 16 * nt, batch - 1) * xe_stride(n) + 2 * s;
+        return make_int2(e[0], e[1]);
+    };
+    int2 xen[NT];
     int sb = sb_begin + wave;
-    if (sb < sb_end) load_tile<T>(regs, tile_base + (size_t)sb * QTraits<T>::kSbBytes, off);
-    for (; sb < sb_end; sb += kWavesPerWg) {
-        stage_tile<T>(regs, lds[wave], lane);
-        if (sb + kWavesPerWg < sb_end)
-            load_tile<T>(regs, tile_base + (size_t)(sb + kWavesPerWg) * QTraits<T>::kSbBytes, off);
-        // blocks in pairs (even, odd): a runtime loop bounds the live registers
-#pragma unroll 1
-        for (int bp = 0; bp < 4; bp++)
+    if (sb < sb_end) {
+        load_tile<T>(regs, tile_base + (size_t)sb * QTraits<T>::kSbBytes, off);
 #pragma unroll
-        for (int odd = 0; odd < 2; odd++) {
-            const int blk = 2 * bp + odd;
-            // A fragments: x[b = li + 16 nt][sb*256 + 32 blk + 8 g + e]
-            f16x8 ah[NT], al[NT];
+        for (int nt = 0; nt < NT; nt++) xen[nt] = xe_pair(sb, nt);
+    }
+    // range-safe planes: the split's groups (2 per super-block) of batch row
+    // li + 16 nt brought to one exponent En[nt] (read after the first weight
+    // loads were issued)
+    int En[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int b = min(li + 16 * nt, batch - 1);
+        En[nt] = xe_max(xp.xe, b, 2 * sb_begin, 2 * (sb_end - sb_begin), n);
+        if (wave == 0 && g == 0) xeE[li + 16 * nt] = En[nt];  // read after the reduction barrier
+    }
+    for (; sb < sb_end; sb += kWavesPerWg) {
+        _Float16 fgrp[NT][2];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            fgrp[nt][0] = xe_factor(xen[nt].x, En[nt]);
+            fgrp[nt][1] = xe_factor(xen[nt].y, En[nt]);
+        }
+        // A fragments of block blk: x[b = li + 16 nt][sb*256 + 32 blk + 8 g +
+        // e]; rows past the batch read row batch - 1 (branch-free; those MFMA
+        // output rows are never stored)
+        auto load_x = [&](int blk, f16x8 (&ah)[NT], f16x8 (&al)[NT]) {
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const int b = li + 16 * nt;
-                if (b < batch) {
-                    const size_t xo = (size_t)b * n + (size_t)sb * 256 + 32 * blk + 8 * g;
-                    const _Float16 f = xe_factor(xp.xe[(size_t)b * xe_stride(n) + 2 * sb + (blk >> 2)], En[nt]);
-                    ah[nt] = *reinterpret_cast<const f16x8 *>(xh + xo) * f;
-                    al[nt] = *reinterpret_cast<const f16x8 *>(xl + xo) * f;
-                } else {
-                    ah[nt] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-                    al[nt] = ah[nt];
-                }
+                const int b = min(li + 16 * nt, batch - 1);
+                const size_t xo = (size_t)b * n + (size_t)sb * 256 + 32 * blk + 8 * g;
+                ah[nt] = *reinterpret_cast<const f16x8 *>(xh + xo);
+                al[nt] = *reinterpret_cast<const f16x8 *>(xl + xo);
             }
+        };
+        f16x8 nh[2][NT], nl[2][NT];  // the next block pair's fragments
+        load_x(0, nh[0], nl[0]);
+        load_x(1, nh[1], nl[1]);
+        stage_tile<T>(regs, lds[wave], lane);
+        // blocks in pairs (even, odd): a runtime loop bounds the live
+        // registers; each pair's x is loaded one pair ahead (unconditionally:
+        // the last pair re-reads its own, which keeps the loop body
+        // straight-line and the waits exact).  The next super-block's weights
+        // are loaded after the loop: loads complete in issue order, so an x
+        // load issued after them would wait for their HBM round trip.
+#pragma unroll 1
+        for (int bp = 0; bp < 4; bp++) {
+            f16x8 ch[2][NT], cl[2][NT];
 #pragma unroll
-            for (int rs = 0; rs < 4; rs++) {
-                const uint32_t *wl = lds_words + (rs * 16 + li) * kSegWords;
-                const f16x8 bw = odd ? w_frag<T, 1>(wl, blk, g) : w_frag<T, 0>(wl, blk, g);
-                const float d = blk_scale<T>(wl, blk);
+            for (int odd = 0; odd < 2; odd++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
-                    f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[nt], bw, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[nt], bw, c, 0, 0, 0);
+                    ch[odd][nt] = nh[odd][nt];
+                    cl[odd][nt] = nl[odd][nt];
+                }
+            const int np = min(bp + 1, 3);
+            load_x(2 * np, nh[0], nl[0]);
+            load_x(2 * np + 1, nh[1], nl[1]);
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[rs][nt][r] = fmaf(c[r], d, acc[rs][nt][r]);
+            for (int odd = 0; odd < 2; odd++) {
+                const int blk = 2 * bp + odd;
+                f16x8 ah[NT], al[NT];
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    const _Float16 f = bp < 2 ? fgrp[nt][0] : fgrp[nt][1];
+                    ah[nt] = ch[odd][nt] * f;
+                    al[nt] = cl[odd][nt] * f;
+                }
+#pragma unroll
+                for (int rs = 0; rs < 4; rs++) {
+                    const uint32_t *wl = lds_words + (rs * 16 + li) * kSegWords;
+                    const f16x8 bw = odd ? w_frag<T, 1>(wl, blk, g) : w_frag<T, 0>(wl, blk, g);
+                    const float d = blk_scale<T>(wl, blk);
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) {
+                        f32x4 c =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[nt], bw, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[nt], bw, c, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) acc[rs][nt][r] = fmaf(c[r], d, acc[rs][nt][r]);
+                    }
                 }
             }
+        }
+        if (sb + kWavesPerWg < sb_end) {
+            load_tile<T>(regs, tile_base + (size_t)(sb + kWavesPerWg) * QTraits<T>::kSbBytes, off);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) xen[nt] = xe_pair(sb + kWavesPerWg, nt);
         }
         wave_sync_lds();
     }
