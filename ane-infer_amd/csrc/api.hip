@@ -182,6 +182,11 @@ int anehip_deltanet_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, cons
     if (batch > 1)
         return launch_deltanet_head(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
                                     conv_state, S, out_heads, 0, nullptr, 0.0f, Planes{});
+    // batch 1: one launch, the q / k windows committed in-kernel (per-head
+    // counters); beyond the counters, dn_finish commits them
+    if (n_heads <= (uint32_t)kDnCounters)
+        return launch_deltanet_step(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
+                                    conv_state, S, out_heads, ctx->dn_count);
     int rc = launch_deltanet_step(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
                                   conv_state, S, out_heads);
     if (rc) return rc;

@@ -58,9 +58,14 @@ struct anehip_ctx {
     float *inv_freq = nullptr;      // RoPE table of the kernel-level attention entry
     float inv_freq_base = 0.0f;
     float *noalloc_scratch = nullptr;  // this device's static scratch (api.hip, anehip_attention_step_noalloc)
+    uint32_t *dn_count = nullptr;      // zeroed counters of anehip_deltanet_step's window commit
 };
 
 namespace anehip {
+
+// Counters at anehip_ctx::dn_count: the (sequence, head) pairs whose q / k
+// conv windows anehip_deltanet_step commits in its kernel.
+constexpr int kDnCounters = 4096;
 
 // Ensures the workspace holds at least `floats` floats (grown with
 // hipMalloc; refused while the context stream is being captured).
@@ -400,9 +405,12 @@ int launch_dn_ssm(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const
 int launch_deltanet_apply(anehip_ctx *ctx, hipStream_t stream, const DnApplyTab &tab, int n_heads, int dim);
 
 // deltanet.hip.  mix: qkv [3*chunk]; beta, alpha: [n_heads] per sequence.
+// With count (batch * n_heads zeroed counters, left zeroed) the q / k conv
+// windows are committed too; without, launch_dn_finish (or the ssm_out
+// GEMV's gated-norm prologue) commits them.
 int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, const MixIn &mix,
                          const MixIn &beta, const MixIn &alpha, const float *conv_w, const float *ssm_a,
-                         const float *dt_bias, float *conv_state, float *S, float *out);
+                         const float *dt_bias, float *conv_state, float *S, float *out, uint32_t *count = nullptr);
 // Batch > 1: the whole DeltaNet step of a head in one workgroup -- conv +
 // SiLU, L2 norms, beta / decay, recurrence, all conv windows committed -- and
 // either the raw head outputs (out, fp32) or, with out == nullptr, the gated

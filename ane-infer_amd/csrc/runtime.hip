@@ -94,6 +94,11 @@ int anehip_ctx_create(int device, const anehip_model_desc *desc, anehip_ctx **ou
         anehip_ctx_destroy(ctx);
         return set_error(global_error(), ANEHIP_EHIP, "ctx_create: stream/event creation failed");
     }
+    if (hipMalloc(&ctx->dn_count, kDnCounters * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->dn_count, 0, kDnCounters * sizeof(uint32_t)) != hipSuccess) {
+        anehip_ctx_destroy(ctx);
+        return set_error(global_error(), ANEHIP_ENOMEM, "ctx_create: counter allocation failed");
+    }
     int rc = ensure_workspace(ctx, 0);
     if (rc == ANEHIP_OK) rc = noalloc_setup(ctx);
     if (rc == ANEHIP_OK && desc) rc = anehip_model_setup(ctx, desc);
@@ -114,6 +119,7 @@ void anehip_ctx_destroy(anehip_ctx *ctx) {
     for (void *p : ctx->user_allocs) (void)hipFree(p);
     if (ctx->ws.partial) (void)hipFree(ctx->ws.partial);
     if (ctx->inv_freq) (void)hipFree(ctx->inv_freq);
+    if (ctx->dn_count) (void)hipFree(ctx->dn_count);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
