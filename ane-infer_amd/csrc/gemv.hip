@@ -1201,21 +1201,27 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void dn_ssm_kernel(const uint8
 // load issued before any is used.  x is staged in LDS (its loads issued
 // before the weights', so waiting for them does not wait for the weights) as
 // int8 digits (put_digits).  Per lane: block sums in block order, each scaled
-// (q8_gemv.rs:234-242); then the 16 H slots of a row are added through LDS in
-// slot order.
+// (q8_gemv.rs:234-242); then the H slots of a row held by one wave are added
+// by lane exchanges and the 16 waves' sums through LDS in wave order.
+// (8 waves of 8 rows, H = 8, measured 5.06 us against 4.95 at 6144 x 2048.)
 constexpr int kRowsWaves = 16;
+// blocks per lane slot of gemv_rows for n = 256 nsb columns and row split H
+// (0 if they do not divide evenly)
+inline int rows_blocks_per_slot(int nsb, int H) {
+    const int slots = kRowsWaves * H;
+    return (8 * nsb) % slots ? 0 : 8 * nsb / slots;
+}
 constexpr int kRowsMaxN = 8192;
 
 template <uint32_t T, int H, int J>
-__global__ __launch_bounds__(kWave *kRowsWaves) void gemv_rows(const uint8_t *__restrict__ Wp,
-                                                               const float *__restrict__ x, float *__restrict__ y,
-                                                               int m, int n) {
-    constexpr int R = kWave / H, SLOTS = kRowsWaves * H, NT = kWave * kRowsWaves;
+__global__ __launch_bounds__(kWave *kRowsWaves) void gemv_rows(const uint8_t *__restrict__ Wp, const float *__restrict__ x,
+                                                       float *__restrict__ y, int m, int n) {
+    constexpr int NW = kRowsWaves, R = kWave / H, SLOTS = NW * H, NT = kWave * NW;
     constexpr int VB = T == ANEHIP_GGML_Q8_0 ? 2 : 1;  // 16-byte quant vectors per block
     constexpr int XV = kRowsMaxN / 4 / NT;              // float4 of x per thread, at most
     __shared__ __align__(16) uint32_t xd[kRowsMaxN / 32 * kXdWords];
     __shared__ uint4 xq[kRowsMaxN / 32];
-    __shared__ float red[kRowsWaves][kWave];
+    __shared__ float red[NW][kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int tile = blockIdx.x / H, h = blockIdx.x % H;
@@ -1255,16 +1261,17 @@ __global__ __launch_bounds__(kWave *kRowsWaves) void gemv_rows(const uint8_t *__
         const float d = __half2float(__ushort_as_half((unsigned short)(scw[j] >> (16 * (b & 1)))));
         acc = fmaf(block_dot_digits<T>(q[j], xd + b * kXdWords, xq[b]), d, acc);
     }
-    red[wave][lane] = acc;
+    // the H slots of a row within the wave (lanes r, r + R, ...) first, by
+    // lane exchanges, then the 16 waves' sums through LDS
+#pragma unroll
+    for (int k = R; k < kWave; k <<= 1) acc += __shfl_xor(acc, k);
+    if (lane < R) red[wave][lane] = acc;
     __syncthreads();
     if (threadIdx.x < R) {
         const int row = tile * kWave + h * R + (int)threadIdx.x;
-        float sum = 0.0f;
+        float sum = red[0][threadIdx.x];
 #pragma unroll
-        for (int w = 0; w < kRowsWaves; w++) {
-#pragma unroll
-            for (int k = 0; k < H; k++) sum += red[w][k * R + threadIdx.x];
-        }
+        for (int w = 1; w < NW; w++) sum += red[w][threadIdx.x];
         if (row < m) y[row] = sum;
     }
 }
@@ -3288,7 +3295,7 @@ int dispatch_packed(anehip_ctx *ctx, hipStream_t s, const void *w, uint32_t m, u
 // at least half as many workgroups as CUs; 0 when gemv_rows does not apply
 // (matrices the split GEMV covers with row tiles alone keep it).  Measured on
 // MI355X at batch 1, in graphs of back-to-back launches, against the K split
-// plus its summing launch: 6144 x 2048 5.3 us (H 4 or 2) against 7.0;
+// plus its summing launch: 6144 x 2048 5.1 us (H 4) / 5.2 (H 2) against 7.0;
 // 2048 x 2048 3.8 (4) / 4.5 (2) against 6.0; 2048 x 6144 7.5 (4) against 7.9.
 int gemv_rows_split(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
     if (n % 256 || n > (uint32_t)kRowsMaxN) return 0;
@@ -3296,7 +3303,8 @@ int gemv_rows_split(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     if (gemv_packed_ksplit(ctx, m, n) == 1) return 0;
     for (int H : {4, 2}) {
-        if (nsb % (2 * H) || nsb / (2 * H) > 4) continue;
+        const int J = rows_blocks_per_slot(nsb, H);
+        if (J < 1 || J > 4) continue;
         if (tiles * H >= cus / 2) return H;
     }
     return 0;
@@ -3305,7 +3313,7 @@ int gemv_rows_split(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
 template <uint32_t T>
 int launch_rows_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
                   float *y, int H) {
-    const int tiles = (int)((m + kWave - 1) / kWave), J = (int)(n / 256) / (2 * H);
+    const int tiles = (int)((m + kWave - 1) / kWave), J = rows_blocks_per_slot((int)(n / 256), H);
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     const dim3 grid(tiles * H), block(kWave * kRowsWaves);
 #define ANEHIP_ROWS(HH, JJ) hipLaunchKernelGGL((gemv_rows<T, HH, JJ>), grid, block, 0, stream, wb, x, y, (int)m, (int)n)
@@ -3335,7 +3343,7 @@ int launch_rows_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m
 
 int launch_gemv_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *w, uint32_t m, uint32_t n,
                      const float *x, float *y, int H) {
-    if (n % 256 || n > (uint32_t)kRowsMaxN || (n / 256) % (2 * H))
+    if (n % 256 || n > (uint32_t)kRowsMaxN || !rows_blocks_per_slot((int)(n / 256), H))
         return set_error(ctx->err, ANEHIP_EINVAL, "gemv_rows: n=%u with row split %d", n, H);
     if (ggml_type == ANEHIP_GGML_Q8_0) return launch_rows_t<ANEHIP_GGML_Q8_0>(ctx, stream, w, m, n, x, y, H);
     return launch_rows_t<ANEHIP_GGML_Q4_0>(ctx, stream, w, m, n, x, y, H);
