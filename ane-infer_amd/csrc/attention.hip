@@ -37,18 +37,21 @@ constexpr int kThreads = 256;
 
 // RMSNorm (eps 1e-6, deltanet.rs:575-598) + RoPE (deltanet.rs:600-623) of one
 // 256-dim head by one wave: lane l owns dims 4l..4l+3 = rotary pairs 2l, 2l+1.
+// The same arithmetic as the decode kernel's preparation (rsqrt, one sincos
+// per pair), so prefill and decode append identical k rows.
 __device__ __forceinline__ void norm_rope_head(const MixIn &mix, int b, int base, const float *__restrict__ w,
                                                const float *__restrict__ inv_freq, uint32_t pos, int lane,
                                                float *dst) {
     float4 x = mix.at4(b, base + 4 * lane);
     float ss = wave_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
-    const float inv_rms = 1.0f / sqrtf(ss / (float)kHd + 1e-6f);
+    const float inv_rms = rsqrtf(ss / (float)kHd + 1e-6f);
     float4 wv = *reinterpret_cast<const float4 *>(w + 4 * lane);
     float a0 = (x.x * inv_rms) * wv.x, a1 = (x.y * inv_rms) * wv.y;
     float a2 = (x.z * inv_rms) * wv.z, a3 = (x.w * inv_rms) * wv.w;
     const float fpos = (float)pos;
-    const float t0 = fpos * inv_freq[2 * lane], t1 = fpos * inv_freq[2 * lane + 1];
-    const float s0 = sinf(t0), c0 = cosf(t0), s1 = sinf(t1), c1 = cosf(t1);
+    float s0, c0, s1, c1;
+    sincosf(fpos * inv_freq[2 * lane], &s0, &c0);
+    sincosf(fpos * inv_freq[2 * lane + 1], &s1, &c1);
     dst[0] = a0 * c0 - a1 * s0;
     dst[1] = a0 * s0 + a1 * c0;
     dst[2] = a2 * c1 - a3 * s1;
@@ -69,43 +72,62 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWord3 = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 constexpr float kPScale = 16384.0f;  // 2^14: probabilities in the PV MFMA operands
 
-// LDS row of V^T (one head dim, 64 positions = 8 chunks of 8): chunk c of
-// row D sits at slot c ^ swz(D), which keeps both the transposing writes (8
-// lanes: rows 8p + d, p varying) and the MFMA operand reads (8 lanes: 8
-// consecutive rows) free of bank conflicts.
-__device__ __forceinline__ int vt_slot(int D, int c) { return c ^ ((D ^ (D >> 3)) & 7); }
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// fp32 x 8 -> fp16 hi / lo with hi + lo ~= x (|error| <= 2^-22 |x|)
-__device__ __forceinline__ void split8(const float *x, h8v &hi, h8v &lo) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        hi[e] = (_Float16)x[e];
-        lo[e] = (_Float16)(x[e] - (float)hi[e]);
-    }
+// max / sum over the four 16-lane groups of a wave, every lane getting the
+// result of its column (v_permlane16_swap, then v_permlane32_swap: VALU lane
+// exchanges, no LDS)
+__device__ __forceinline__ float group_max4(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float m1 = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+    const uint32_t u1 = __builtin_bit_cast(uint32_t, m1);
+    const auto b = __builtin_amdgcn_permlane32_swap(u1, u1, false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+__device__ __forceinline__ float group_sum4(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float s1 = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+    const uint32_t u1 = __builtin_bit_cast(uint32_t, s1);
+    const auto b = __builtin_amdgcn_permlane32_swap(u1, u1, false, false);
+    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
 }
 
 // grid = (chunks, n_kv_heads, batch); chunk c takes the live tiles
-// chunk_tiles() gives it.  mix: per sequence [q_full | k | v] rows (K-split
-// partial slices); q_full is [n_heads][q(256) | gate(256)].
+// [tb, te) of 64 positions that chunk_tiles() gives it.  mix: per
+// sequence [q_full | k | v] rows (K-split partial slices); q_full is
+// [n_heads][q(256) | gate(256)].
 //
-// Per tile, on MFMA (v_mfma_f32_16x16x32_f16; operands A[i][k] / B[k][j] in
-// lane i (j) + 16 (k / 8), element k % 8; D[i][j] in lane j + 16 (i / 4),
-// element i % 4):
-//  * scores S[pos][head] = K q^T / 16: wave w takes positions 16w..16w+15;
-//    its K fragments are loaded straight from the cache (A: lane l = row
-//    16w + l % 16, dims 32s + 8 (l / 16) of k-step s), q as fp16 hi + lo
-//    B fragments (columns = the G query heads, others zero), so K is read
-//    once for all G heads;
-//  * online softmax per head across the 4 waves (LDS);
-//  * O[head][dim] += P V: A = P (fp16 hi + lo of the probabilities), B = V
-//    from an LDS copy of the tile transposed to [dim][pos] (each thread holds
-//    an 8 x 8 block of V -- rows 8 rb .. +7, dims 8p .. +7 -- and transposes
-//    it in registers); wave w takes dims 64w..64w+63.
-// The next tiles' K / V loads are in flight while a tile is processed; the
+// Wave w takes positions 16 w .. 16 w + 15 of every tile and keeps its own
+// online softmax and output for them; the 4 waves merge once, at the end.
+// Per tile and wave, on MFMA (16 x 16 x K f16 forms: operands A[i][k] /
+// B[k][j] in lane i (j) + 16 (k / (K / 4)), elements k % (K / 4); D[i][j]
+// in lane j + 16 (i / 4), element i % 4):
+//  * scores S[pos][head] = K q^T / 16 (K = 32): A = the wave's 16 K rows,
+//    loaded straight from the cache (lane l: row l % 16, dims 32 s + 8 (l /
+//    16) of k-step s), B = q as fp16 hi + lo fragments (columns = the G
+//    query heads, others zero), so K is read once for all G heads;
+//  * lane l then holds the scores of head l % 16 at positions 4 (l / 16) ..
+//    + 3: the max and sum over the wave's 16 positions are two lane swaps
+//    (v_permlane16_swap / v_permlane32_swap), no LDS and no barrier;
+//  * O[head][dim] += P V (K = 16): those probabilities (x 2^14, fp16 hi +
+//    lo) are already the A operand; B = V rows 4 (l / 16) .. + 3 of the
+//    wave, loaded as 8-byte pieces (dims 64 q + 4 (l % 16) .. + 3), and MFMA
+//    (q, c) takes element c of each piece, so its output column l % 16 is
+//    dim 64 q + 4 (l % 16) + c: 16 MFMA column blocks cover the 256 dims
+//    with no transpose of V.
+// The next tile's K / V loads are in flight while a tile is processed; the
 // buffer resources cover positions [0, pos) only, so rows >= pos read zeros
 // without a memory access (row pos takes this step's k / v), which also makes
-// the prefetch of a tile past the chunk free.  One
-// unnormalised partial per (chunk, query head) with its running max and sum.
+// the prefetch of a tile past the chunk free.  One unnormalised partial per
+// (chunk, query head) with its running max and sum.
+//
+// With one or two tiles per workgroup (batch 1 at short contexts) the kernel
+// is a chain of dependent steps on one wave per SIMD, so the q / k
+// preparation issues every input load before the position is known, shares
+// one sincos per rotary pair and writes the q fragments straight from the
+// wave that normalised the head.
 //
 // Cache addressing: row b's cache is at cache_off + b * row_stride halves
 // (decode: every row its own sequence; prefill: row_stride 0, every row a
@@ -117,34 +139,50 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     const float *__restrict__ inv_freq, const uint32_t *__restrict__ pos_arr, __half *__restrict__ k_cache,
     __half *__restrict__ v_cache, int max_seq, int n_heads, int n_kv, float *__restrict__ part_o,
     float *__restrict__ part_ml, size_t cache_off, size_t row_stride, bool append) {
-    __shared__ __align__(16) _Float16 vt[kHd * kCh];  // V^T of the tile, swizzled chunks
-    __shared__ __align__(16) float qs[G][kHd];
-    __shared__ __align__(16) h8v qf[8][2][64];         // q B fragments: k-step, hi / lo, lane
-    __shared__ __align__(16) float pt[G][kCh];        // probabilities of the tile
+    __shared__ __align__(16) h8v qf[8][2][64];
     __shared__ __align__(16) __half knew[kHd], vnew[kHd];
-    // per-tile maxima and sums of the 16 (wave, lane group) pieces of each
-    // head's column, [piece][head]: combined after the barrier, no shuffles
-    __shared__ float rmax[16][16], rsum[16][16], rscale[16];
-    __shared__ float qmax[G];  // largest |q| / 16 of each query head (range-safe q fragments)
+    __shared__ int qexp[G];
+    __shared__ __align__(16) float ob[4][G][kHd];
+    __shared__ float wm[4][G], wl[4][G];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int li = lane & 15, lg = lane >> 4;  // MFMA operand row / column, k group
-    const int vp = t & 31, vrb = t >> 5;       // V block: dims 8 vp .., rows 8 vrb ..
+    const int li = lane & 15, lg = lane >> 4;
     const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    // inputs that do not depend on the position first: this wave's q head
+    // (wave < G) or k / v rows (wave G % 4, used by the chunk holding pos),
+    // the norm weights and the RoPE frequencies
+    const bool is_q = wave < G, is_k = wave == G % 4;
+    const int hq = kvh * G + (wave < G ? wave : 0);
+    const int kin = n_heads * 2 * kHd + kvh * kHd;
+    const int vin = n_heads * 2 * kHd + n_kv * kHd + kvh * kHd;
+    float4 aq[8], ak[8], av[8];
+    {
+        const float *r0 = mix.p + (size_t)b * mix.stride + 4 * lane;
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (q < mix.kp) {
+                const float *rq = r0 + (size_t)q * mix.split;
+                if (is_q) aq[q] = *reinterpret_cast<const float4 *>(rq + hq * 2 * kHd);
+                if (is_k) {
+                    ak[q] = *reinterpret_cast<const float4 *>(rq + kin);
+                    av[q] = *reinterpret_cast<const float4 *>(rq + vin);
+                }
+            }
+    }
+    const float4 wq = *reinterpret_cast<const float4 *>(q_norm + 4 * lane);
+    const float4 wk = *reinterpret_cast<const float4 *>(k_norm + 4 * lane);
+    const float2 fr = *reinterpret_cast<const float2 *>(inv_freq + 2 * lane);
     const uint32_t pos = pos_arr[b];
     const int len = (int)pos + 1;
     const int nch = gridDim.x;
     int tb, te;  // tiles [tb, te)
     if (!chunk_tiles(len, nch, c, &tb, &te)) return;  // uniform exit: nothing of this sequence here
     const size_t cache_base = cache_off + (size_t)b * row_stride + (size_t)kvh * max_seq * kHd;
-    const bool has_new = (int)pos < te * kCh;  // this chunk holds the current position
+    const bool has_new = (int)pos < te * kCh;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(k_cache + cache_base, 0, (int)pos * kHd * 2, kWord3);
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc(v_cache + cache_base, 0, (int)pos * kHd * 2, kWord3);
-    // K fragments of this wave's 16 rows; V block of this thread.  A tile
-    // past the chunk is loaded from row kFar (>= pos: zeros, no memory access),
-    // so every step issues the same loads.
     const int kFar = max_seq;
     auto load_k = [&](u32x4 *kr, int row0) {
 #pragma unroll
@@ -153,37 +191,86 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
             kr[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
         }
     };
-    auto load_v = [&](u32x4 *vr, int row0) {
+    // V rows row0 + 16 wave + 4 lg + r, dims 64 q + 4 li .. + 3 in vr[4 q + r]
+    auto load_v = [&](u32x2 *vr, int row0) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int off = ((row0 + 8 * vrb + i) * kHd + 8 * vp) * 2;
-            vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
-        }
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int off = ((row0 + 16 * wave + 4 * lg + r) * kHd + 64 * q + 4 * li) * 2;
+                vr[4 * q + r] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, off, 0, 0));
+            }
     };
     auto row_of = [&](int ti) { return ti < te ? ti * kCh : kFar; };
-    // the first tile's loads (and the second's K) go out before the q / k
-    // preparation
-    u32x4 ka[8], kb[8], vr[8];
+    u32x4 ka[8], kb[8];
+    u32x2 va[16], vb[16];
     load_k(ka, tb * kCh);
-    load_v(vr, tb * kCh);
+    load_v(va, tb * kCh);
     load_k(kb, row_of(tb + 1));
+    load_v(vb, row_of(tb + 1));
 
-    // q heads of this kv group: wave w < G prepares head kvh*G + w
-    if (wave < G) {
-        const int h = kvh * G + wave;
-        float q4[4];
-        norm_rope_head(mix, b, h * 2 * kHd, q_norm, inv_freq, pos, lane, q4);
-        *reinterpret_cast<float4 *>(&qs[wave][4 * lane]) = make_float4(q4[0], q4[1], q4[2], q4[3]);
-        const float qm = wave_max64(fmaxf(fmaxf(fabsf(q4[0]), fabsf(q4[1])), fmaxf(fabsf(q4[2]), fabsf(q4[3]))));
-        if (lane == 0) qmax[wave] = qm * 0.0625f;
+    // preparation, every input load issued first: wave w < G normalises and
+    // rotates q head kvh G + w and writes its MFMA B fragments (scaled by
+    // 1/16 and 2^-qe, fp16 hi + lo); in the chunk holding pos, wave G % 4
+    // also prepares this step's k (RMSNorm + RoPE) and v, rounded to fp16.
+    const bool do_q = is_q, do_k = has_new && is_k;
+    // rows of the q fragments that belong to no head are zero
+    for (int e = t; e < 8 * 64; e += kThreads) {
+        const int fl = e & 63;
+        if ((fl & 15) >= G) {
+            qf[e >> 6][0][fl] = h8v{};
+            qf[e >> 6][1][fl] = h8v{};
+        }
     }
-    if (has_new && wave == G % 4) {
-        // k: RMSNorm + RoPE, v: as is; both rounded to fp16 and appended
-        const int kin = n_heads * 2 * kHd + kvh * kHd;
-        const int vin = n_heads * 2 * kHd + n_kv * kHd + kvh * kHd;
+    float sn0, cs0, sn1, cs1;
+    sincosf((float)pos * fr.x, &sn0, &cs0);
+    sincosf((float)pos * fr.y, &sn1, &cs1);
+    // slices in ascending order; the GEMMs at batch > 1 split K up to 16
+    // ways, slices past the 8 held in registers are loaded here
+    auto sum4 = [&](const float4 *a, int off) {
+        float4 x = a[0];
+#pragma unroll
+        for (int q = 1; q < 8; q++)
+            if (q < mix.kp) x = make_float4(x.x + a[q].x, x.y + a[q].y, x.z + a[q].z, x.w + a[q].w);
+        for (int q = 8; q < mix.kp; q++) {
+            const float4 v = *reinterpret_cast<const float4 *>(
+                mix.p + (size_t)b * mix.stride + 4 * lane + (size_t)q * mix.split + off);
+            x = make_float4(x.x + v.x, x.y + v.y, x.z + v.z, x.w + v.w);
+        }
+        return x;
+    };
+    auto norm_rope = [&](float4 x, float4 wv, float *dst) {
+        const float ss = wave_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
+        const float inv_rms = rsqrtf(ss / (float)kHd + 1e-6f);
+        const float a0 = (x.x * inv_rms) * wv.x, a1 = (x.y * inv_rms) * wv.y;
+        const float a2 = (x.z * inv_rms) * wv.z, a3 = (x.w * inv_rms) * wv.w;
+        dst[0] = a0 * cs0 - a1 * sn0;
+        dst[1] = a0 * sn0 + a1 * cs0;
+        dst[2] = a2 * cs1 - a3 * sn1;
+        dst[3] = a2 * sn1 + a3 * cs1;
+    };
+    if (do_q) {
+        float q4[4];
+        norm_rope(sum4(aq, hq * 2 * kHd), wq, q4);
+        const float qm = wave_max64(fmaxf(fmaxf(fabsf(q4[0]), fabsf(q4[1])), fmaxf(fabsf(q4[2]), fabsf(q4[3]))));
+        const int qe = group_exp(qm * 0.0625f);
+        if (lane == 0) qexp[wave] = qe;
+        // dims 4 lane .. + 3 = k-step lane / 8, lane group (lane % 8) / 2, half lane % 2
+        h4v hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float x = ldexpf(q4[i] * 0.0625f, -qe);
+            hi[i] = (_Float16)x;
+            lo[i] = (_Float16)(x - (float)hi[i]);
+        }
+        const int fs = lane >> 3, fl = wave + 16 * ((lane & 7) >> 1), half = lane & 1;
+        reinterpret_cast<h4v *>(&qf[fs][0][fl])[half] = hi;
+        reinterpret_cast<h4v *>(&qf[fs][1][fl])[half] = lo;
+    }
+    if (do_k) {
         float k4[4];
-        norm_rope_head(mix, b, kin, k_norm, inv_freq, pos, lane, k4);
-        float4 v4 = mix.at4(b, vin + 4 * lane);
+        norm_rope(sum4(ak, kin), wk, k4);
+        const float4 v4 = sum4(av, vin);
         const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -201,153 +288,127 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         }
     }
     lds_barrier();
-    // q B fragments (lane l: head l % 16, dims 32s + 8 (l / 16) ..), scaled by
-    // 1/sqrt(256) = 1/16 (exact) and by 2^-qe per head (qe from the head's
-    // largest value, so that fp16 neither overflows nor loses the low bits;
-    // the scores are scaled back by 2^qe), as fp16 hi + lo; 4 (k-step, lane)
-    // pairs per thread
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int e = t + 256 * j, fs = e >> 6, fl = e & 63, fh = fl & 15, fg = fl >> 4;
-        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (fh < G) {
-            const int qe = group_exp(qmax[fh]);
-            const float4 a = *reinterpret_cast<const float4 *>(&qs[fh][32 * fs + 8 * fg]);
-            const float4 bq = *reinterpret_cast<const float4 *>(&qs[fh][32 * fs + 8 * fg + 4]);
-            const float qv[8] = {a.x, a.y, a.z, a.w, bq.x, bq.y, bq.z, bq.w};
-#pragma unroll
-            for (int i = 0; i < 8; i++) x[i] = ldexpf(qv[i] * 0.0625f, -qe);
-        }
-        split8(x, qf[fs][0][fl], qf[fs][1][fl]);
-    }
-    lds_barrier();
-    // scores of head li come out scaled by 2^-qe (li < G)
-    const int qe_li = li < G ? group_exp(qmax[li]) : 0;
+    const int qe_li = li < G ? qexp[li] : 0;
 
-    // per head li (< G): running max / sum; PV accumulators of dim block db:
-    // rows = heads 4 lg .. 4 lg + 3, column = dim 64 wave + 16 db + li
     float m_run = -INFINITY, l_run = 0.f;
-    f32x4 o[4] = {};
-    // tile ti with K in kr and V in vr; refills vr with tile ti + 1's V right
-    // after storing it, and kr with tile ti + 2's K right after the scores
-    auto process = [&](u32x4 *kr, int ti) {
+    f32x4 o[16] = {};
+    auto process = [&](u32x4 *kr, u32x2 *vr, int ti, bool first) {
         const int row0 = ti * kCh;
-        // this step's row: K from knew, V from vnew (loaded as zeros)
         if (row0 + 16 * wave + li == (int)pos) {
 #pragma unroll
             for (int s = 0; s < 8; s++) kr[s] = *reinterpret_cast<const u32x4 *>(&knew[32 * s + 8 * lg]);
         }
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (row0 + 8 * vrb + i == (int)pos) vr[i] = *reinterpret_cast<const u32x4 *>(&vnew[8 * vp]);
-        // V block -> V^T rows 8 vp + d, chunk vrb
+        for (int r = 0; r < 4; r++)
+            if (row0 + 16 * wave + 4 * lg + r == (int)pos) {
 #pragma unroll
-        for (int d = 0; d < 8; d++) {
-            const int w = d >> 1;
-            u32x4 col;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t x0 = vr[2 * k][w], x1 = vr[2 * k + 1][w];
-                col[k] = (d & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
+                for (int q = 0; q < 4; q++) vr[4 * q + r] = *reinterpret_cast<const u32x2 *>(&vnew[64 * q + 4 * li]);
             }
-            const int D = 8 * vp + d;
-            *reinterpret_cast<u32x4 *>(&vt[D * kCh + 8 * vt_slot(D, vrb)]) = col;
-        }
-        load_v(vr, row_of(ti + 1));
-        // scores of positions 16 wave + 4 lg + e, head li
-        f32x4 sc = {};
+        f32x4 s0 = {}, s1 = {};
 #pragma unroll
         for (int s = 0; s < 8; s++) {
             const h8v a = __builtin_bit_cast(h8v, kr[s]);
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s][0][lane], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s][1][lane], sc, 0, 0, 0);
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s][0][lane], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[s][1][lane], s1, 0, 0, 0);
         }
         load_k(kr, row_of(ti + 2));
         const int p0 = row0 + 16 * wave + 4 * lg;
         float sv[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) sv[e] = p0 + e < len ? ldexpf(sc[e], qe_li) : -INFINITY;
-        rmax[4 * wave + lg][li] = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        lds_barrier();
-        float tm = rmax[0][li];
-#pragma unroll
-        for (int j = 1; j < 16; j++) tm = fmaxf(tm, rmax[j][li]);
-        const float mn = fmaxf(m_run, tm);     // finite for li < G: the tile has a valid row
-        const float scale = expf(m_run - mn);  // 0 on the first tile
+        for (int e = 0; e < 4; e++) sv[e] = p0 + e < len ? ldexpf(s0[e] + s1[e], qe_li) : -INFINITY;
+        const float tm = group_max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+        const float mn = fmaxf(m_run, tm);
+        const float mref = mn == -INFINITY ? 0.0f : mn;
+        const float scale = expf(m_run - mref);
         float pe[4], ps = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            pe[e] = p0 + e < len ? expf(sv[e] - mn) : 0.0f;
+            pe[e] = (li < G && p0 + e < len) ? expf(sv[e] - mref) : 0.0f;
             ps += pe[e];
         }
-        rsum[4 * wave + lg][li] = ps;
-        if (wave == 0 && lane < 16) rscale[lane] = scale;
-        if (li < G) *reinterpret_cast<float4 *>(&pt[li][16 * wave + 4 * lg]) = make_float4(pe[0], pe[1], pe[2], pe[3]);
-        lds_barrier();
-        float ts[4];
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-            ts[w] = (rsum[4 * w][li] + rsum[4 * w + 1][li]) + (rsum[4 * w + 2][li] + rsum[4 * w + 3][li]);
-        l_run = l_run * scale + ((ts[0] + ts[1]) + (ts[2] + ts[3]));
+        l_run = l_run * scale + group_sum4(ps);
         m_run = mn;
-        // PV: rescale the rows (heads 4 lg + e), then P (hi + lo) times V^T
         float rs[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) rs[e] = 4 * lg + e < G ? rscale[4 * lg + e] : 0.0f;
+        for (int e = 0; e < 4; e++)
+            rs[e] = e < G ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, scale), e)) : 0.0f;
+        if (!first) {
 #pragma unroll
-        for (int db = 0; db < 4; db++)
+            for (int k = 0; k < 16; k++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[db][e] *= rs[e];
-        // probabilities (<= 1) times 2^14 as fp16 hi + lo: the low bits of
-        // small probabilities stay out of fp16's subnormal range; the
-        // partial output is scaled back by 2^-14 at the end
-        h8v ph[2], pl[2];
+                for (int e = 0; e < 4; e++) o[k][e] *= rs[e];
+        }
+        h4v ph, pl;
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (li < G) {
-                const float4 a = *reinterpret_cast<const float4 *>(&pt[li][32 * s + 8 * lg]);
-                const float4 bq = *reinterpret_cast<const float4 *>(&pt[li][32 * s + 8 * lg + 4]);
-                x[0] = a.x * kPScale; x[1] = a.y * kPScale; x[2] = a.z * kPScale; x[3] = a.w * kPScale;
-                x[4] = bq.x * kPScale; x[5] = bq.y * kPScale; x[6] = bq.z * kPScale; x[7] = bq.w * kPScale;
-            }
-            split8(x, ph[s], pl[s]);
+        for (int e = 0; e < 4; e++) {
+            const float x = pe[e] * kPScale;
+            ph[e] = (_Float16)x;
+            pl[e] = (_Float16)(x - (float)ph[e]);
         }
 #pragma unroll
-        for (int db = 0; db < 4; db++) {
-            const int D = 64 * wave + 16 * db + li;
+        for (int q = 0; q < 4; q++)
 #pragma unroll
-            for (int s = 0; s < 2; s++) {
-                const h8v bv = *reinterpret_cast<const h8v *>(&vt[D * kCh + 8 * vt_slot(D, 4 * s + lg)]);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bv, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], bv, o[db], 0, 0, 0);
+            for (int cc = 0; cc < 4; cc++) {
+                const int w = cc >> 1;
+                const uint32_t x0 = vr[4 * q][w], x1 = vr[4 * q + 1][w], x2 = vr[4 * q + 2][w], x3 = vr[4 * q + 3][w];
+                u32x2 bw;
+                if (cc & 1) {
+                    bw[0] = (x0 >> 16) | (x1 & 0xffff0000u);
+                    bw[1] = (x2 >> 16) | (x3 & 0xffff0000u);
+                } else {
+                    bw[0] = (x0 & 0xffffu) | (x1 << 16);
+                    bw[1] = (x2 & 0xffffu) | (x3 << 16);
+                }
+                const h4v bv = __builtin_bit_cast(h4v, bw);
+                o[4 * q + cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bv, o[4 * q + cc], 0, 0, 0);
+                o[4 * q + cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bv, o[4 * q + cc], 0, 0, 0);
             }
-        }
-        lds_barrier();  // vt / pt / rmax are rewritten by the next tile
+        load_v(vr, row_of(ti + 2));
     };
-    // K in two register buffers (a tile's K is in flight during the tile
-    // before it), V in one.  Pairs of tiles, then the last one
-    int ti = tb;
+    process(ka, va, tb, true);
+    int ti = tb + 1;
     while (ti + 1 < te) {
-        process(ka, ti);
-        process(kb, ti + 1);
+        process(kb, vb, ti, false);
+        process(ka, va, ti + 1, false);
         ti += 2;
     }
-    if (ti < te) process(ka, ti);
-    // lane (lg, li): heads 4 lg + e, dims 64 wave + 16 db + li
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int hh = 4 * lg + e;
-        if (hh < G) {
-            const size_t slot = (((size_t)b * n_kv + kvh) * nch + c) * G + hh;
-#pragma unroll
-            for (int db = 0; db < 4; db++) part_o[slot * kHd + 64 * wave + 16 * db + li] = o[db][e] * (1.0f / kPScale);
-        }
+    if (ti < te) process(kb, vb, ti, false);
+    // merge the 4 waves: lanes 0-15 hold heads e < G, dims 64 q + 4 li + cc
+    if (lane < G) {
+        wm[wave][lane] = m_run;
+        wl[wave][lane] = l_run;
     }
-    if (wave == 0 && lane < G) {
-        const size_t slot = (((size_t)b * n_kv + kvh) * nch + c) * G + lane;
-        part_ml[slot * 2] = m_run;
-        part_ml[slot * 2 + 1] = l_run;
+    if (lg == 0) {
+#pragma unroll
+        for (int e = 0; e < G; e++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                *reinterpret_cast<float4 *>(&ob[wave][e][64 * q + 4 * li]) =
+                    make_float4(o[4 * q][e], o[4 * q + 1][e], o[4 * q + 2][e], o[4 * q + 3][e]);
+    }
+    lds_barrier();
+    for (int idx = t; idx < G * 64; idx += kThreads) {
+        const int hh = idx >> 6, d4 = idx & 63;
+        float M = wm[0][hh];
+#pragma unroll
+        for (int w = 1; w < 4; w++) M = fmaxf(M, wm[w][hh]);
+        float L = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float sw = expf(wm[w][hh] - M);
+            const float4 v = *reinterpret_cast<const float4 *>(&ob[w][hh][4 * d4]);
+            L += sw * wl[w][hh];
+            acc = make_float4(acc.x + sw * v.x, acc.y + sw * v.y, acc.z + sw * v.z, acc.w + sw * v.w);
+        }
+        const size_t slot = (((size_t)b * n_kv + kvh) * nch + c) * G + hh;
+        const float inv = 1.0f / kPScale;
+        *reinterpret_cast<float4 *>(part_o + slot * kHd + 4 * d4) =
+            make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        if (d4 == 0) {
+            part_ml[slot * 2] = M;
+            part_ml[slot * 2 + 1] = L;
+        }
     }
 }
 

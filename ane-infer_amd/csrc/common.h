@@ -130,8 +130,9 @@ __host__ __device__ __forceinline__ bool chunk_tiles(int len, int nch, int c, in
     const int tiles = (len + kAttnTile - 1) / kAttnTile;
     const int na = tiles < nch ? tiles : nch;
     if (c >= na) return false;
-    *tb = (int)(((long long)c * tiles) / na);
-    *te = (int)(((long long)(c + 1) * tiles) / na);
+    // 32-bit: c < 128 and tiles < 2^15 (a cache row is below 1 GiB)
+    *tb = (int)((uint32_t)(c * tiles) / (uint32_t)na);
+    *te = (int)((uint32_t)((c + 1) * tiles) / (uint32_t)na);
     return true;
 }
 
