@@ -74,26 +74,6 @@ constexpr float kPScale = 16384.0f;  // 2^14: probabilities in the PV MFMA opera
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// max / sum over the four 16-lane groups of a wave, every lane getting the
-// result of its column (v_permlane16_swap, then v_permlane32_swap: VALU lane
-// exchanges, no LDS)
-__device__ __forceinline__ float group_max4(float v) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    const float m1 = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
-    const uint32_t u1 = __builtin_bit_cast(uint32_t, m1);
-    const auto b = __builtin_amdgcn_permlane32_swap(u1, u1, false, false);
-    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
-}
-__device__ __forceinline__ float group_sum4(float v) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    const float s1 = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
-    const uint32_t u1 = __builtin_bit_cast(uint32_t, s1);
-    const auto b = __builtin_amdgcn_permlane32_swap(u1, u1, false, false);
-    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
-}
-
 // grid = (chunks, n_kv_heads, batch); chunk c takes the live tiles
 // [tb, te) of 64 positions that chunk_tiles() gives it.  mix: per
 // sequence [q_full | k | v] rows (K-split partial slices); q_full is
@@ -316,7 +296,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
         float sv[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) sv[e] = p0 + e < len ? ldexpf(s0[e] + s1[e], qe_li) : -INFINITY;
-        const float tm = group_max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+        const float tm = lanes_max4(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
         const float mn = fmaxf(m_run, tm);
         const float mref = mn == -INFINITY ? 0.0f : mn;
         const float scale = expf(m_run - mref);
@@ -326,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
             pe[e] = (li < G && p0 + e < len) ? expf(sv[e] - mref) : 0.0f;
             ps += pe[e];
         }
-        l_run = l_run * scale + group_sum4(ps);
+        l_run = l_run * scale + lanes_sum4(ps);
         m_run = mn;
         float rs[4];
 #pragma unroll

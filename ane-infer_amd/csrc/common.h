@@ -323,6 +323,29 @@ __device__ __forceinline__ float wave_max64(float v) {
     const auto rd = [&](int lane) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, lane)); };
     return fmaxf(fmaxf(rd(0), rd(16)), fmaxf(rd(32), rd(48)));
 }
+// Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane groups of
+// a wave; every lane gets the result of its column) and max over l, l ^ 32:
+// v_permlane16_swap / v_permlane32_swap, VALU lane exchanges with no LDS.
+// Each swap takes two registers holding the same value and both of its
+// results are used (checked in the gfx950 code these compile to).
+__device__ __forceinline__ float lanes_max2(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+__device__ __forceinline__ float lanes_max4(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return lanes_max2(fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1])));
+}
+__device__ __forceinline__ float lanes_sum4(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float s1 = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+    const uint32_t u1 = __builtin_bit_cast(uint32_t, s1);
+    const auto b = __builtin_amdgcn_permlane32_swap(u1, u1, false, false);
+    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
+}
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 // 4 values (consecutive columns of one fragment-order row) split at once.
 __device__ __forceinline__ void split4_scaled(const float (&v)[4], int e, h4v &hi, h4v &lo) {

@@ -1353,9 +1353,7 @@ __device__ __forceinline__ float amax8(const float *p, float m) {
     for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[i]));
     return m;
 }
-__device__ __forceinline__ void split8_scaled(const float *p, int E, h8v &hi, h8v &lo) {
-    float v[8];
-    load8(p, v);
+__device__ __forceinline__ void split8_scaled(const float (&v)[8], int E, h8v &hi, h8v &lo) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         _Float16 h, l;
@@ -1813,8 +1811,8 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
     constexpr int U = P > D ? P : D;
     static_assert(U % P == 0 && U % D == 0, "ring and panel counts must divide the loop body");
     __shared__ __align__(16) float red[kGemmWaves][16][kWave];
-    __shared__ float wmax[4 * kGemmWaves][16];  // [wave, lane group][row]
     __shared__ int emax[kGemmWaves][16];
+    __shared__ int ew[kGemmWaves][16];  // [wave][batch row]: the exponent of the wave's fragments
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
     const int gs = gridDim.x / ksplit;  // workgroups per split
     const int ks = blockIdx.x % ksplit, g0 = blockIdx.x / ksplit;
@@ -1829,11 +1827,14 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
         __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
     // A fragments: batch row lane % 16 (clamped to the batch), columns
     // 64 quarter + 32 j + 8 (lane / 16) of each panel of the split, brought
-    // to x * 2^-E with one exponent E per batch row for the whole split.
-    // From the planes the x loads go out first, then the weight ring's, and
-    // the fragments are scaled after both were issued: the scaling waits for
-    // the x loads only.
+    // to x * 2^-E: from the planes one exponent E per batch row for the whole
+    // split, from fp32 rows one per batch row and wave (over the wave's
+    // columns); each wave's sums are scaled by its 2^E when the quarters are
+    // added.  The x loads go out first, then the weight ring's, and the
+    // fragments are formed after both were issued: that waits for the x
+    // loads only.
     h8v xa[P][2], xb[P][2];
+    float xv[XROWS ? P : 1][2][8];  // fp32 rows: the split's values of this lane
     const int brow = min(lane & 15, batch - 1);
     const float *xr = XROWS ? xrows + (size_t)brow * n : nullptr;
     auto xcol = [&](int p, int j) { return 256 * (ks * P + p) + 64 * quarter + 32 * j + 8 * grp; };
@@ -1861,24 +1862,10 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
             }
         }
     } else {
-        // fp32 rows (API path; split before the ring is issued, the register
-        // file holds no room for both): E from the row's largest |x| over the
-        // split -- lanes l, l + 16, l + 32, l + 48 and the 4 waves hold a row
-        float amax = 0.0f;
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) amax = amax8(xr + xcol(p, j), amax);
-        wmax[4 * quarter + (lane >> 4)][lane & 15] = amax;
-        lds_barrier();
-        float rmax = wmax[0][lane & 15];
-#pragma unroll
-        for (int w = 1; w < 4 * kGemmWaves; w++) rmax = fmaxf(rmax, wmax[w][lane & 15]);
-        E = group_exp(rmax);
-#pragma unroll
-        for (int p = 0; p < P; p++)
-#pragma unroll
-            for (int j = 0; j < 2; j++) split8_scaled(xr + xcol(p, j), E, xa[p][j], xb[p][j]);
+            for (int j = 0; j < 2; j++) load8(xr + xcol(p, j), xv[p][j]);
     }
     const uint8_t *wsplit = Wp + (size_t)(ks * P) * Panel<T>::kBytes;
     int lt = g0, lp = 0;  // load cursor: tile, panel within the split
@@ -1926,10 +1913,24 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
                 xb[p][j] = xb[p][j] * f;
             }
         }
+    } else {
+        // fp32 rows (API path, splits of at most 2 panels): E from the row's
+        // largest |x| over this wave's columns -- lanes l, l ^ 16, l ^ 32,
+        // l ^ 48 hold the row
+        float amax = 0.0f;
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(xv[p][j][i]));
+        E = group_exp(lanes_max4(amax));
+#pragma unroll
+        for (int p = 0; p < P; p++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) split8_scaled(xv[p][j], E, xa[p][j], xb[p][j]);
     }
-    // the epilogue's batch row (threadIdx / 16) takes its exponent from the
-    // lane holding that row
-    const float fEb = xe_scale(row_exp4(E, 4 * quarter));
+    if (lane < 16) ew[quarter][lane] = E;  // lane l holds batch row l (read after the tile's barrier)
     int ct = g0;  // tile being multiplied
     f32x4 acc[4];
 #pragma unroll
@@ -1957,13 +1958,13 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
                 {
                     const int th = threadIdx.x, b = th >> 4, j = th & 15;
                     const int reg = 4 * (j >> 2) + (b & 3), l = 16 * (b >> 2) + 4 * (j & 3);
-                    float4 sum = *reinterpret_cast<const float4 *>(&red[0][reg][l]);
+                    // each quarter's sums times its 2^E (exact), added in quarter order
+                    float4 sum = mul4(*reinterpret_cast<const float4 *>(&red[0][reg][l]), xe_scale(ew[0][b]));
 #pragma unroll
                     for (int w = 1; w < kGemmWaves; w++) {
-                        const float4 o = *reinterpret_cast<const float4 *>(&red[w][reg][l]);
+                        const float4 o = mul4(*reinterpret_cast<const float4 *>(&red[w][reg][l]), xe_scale(ew[w][b]));
                         sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
                     }
-                    sum = mul4(sum, fEb);
                     const int row = ct * kWave + 4 * j;
                     const int off = b < batch && row < m && ct < tiles ? 4 * (ks * (int)split_stride + b * m + row)
                                                                        : kBadOffset;
@@ -2061,7 +2062,11 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int p = 0; p < P; p++)
 #pragma unroll
-            for (int st = 0; st < 4; st++) split8_scaled(xr + xcol(p, st), E, xa[p][st], xb[p][st]);
+            for (int st = 0; st < 4; st++) {
+                float v[8];
+                load8(xr + xcol(p, st), v);
+                split8_scaled(v, E, xa[p][st], xb[p][st]);
+            }
     }
     const uint8_t *wsplit = Wp + (size_t)(ks * P) * Panel<T>::kBytes;
     int lt = g0;  // next tile to load
@@ -2152,8 +2157,8 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
     constexpr int NW = kGemmWaves * H;
     static_assert(U % PW == 0 && U % D == 0, "ring and panel counts must divide the loop body");
     __shared__ __align__(16) float red[NW][32][kWave];
-    __shared__ float wmax[2 * NW][32];  // [wave, lane half][row]
     __shared__ int emax[NW][32];
+    __shared__ int ew[NW][32];  // [wave][batch row]: the exponent of the wave's fragments
     const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
     const int gs = gridDim.x / ksplit;  // workgroups per split
     const int ks = blockIdx.x % ksplit, g0 = blockIdx.x / ksplit;
@@ -2167,10 +2172,12 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
     const size_t tile_bytes = (size_t)nsb * Panel<T>::kBytes;
     const __amdgpu_buffer_rsrc_t orsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, 0, (int)(4 * ksplit * split_stride), kBufferWord3);
-    // fragments brought to x * 2^-E, one exponent E per batch row for the
-    // split (all H * PW panels of the workgroup); from the planes after the
-    // weight ring's loads were issued (as in gemm_xs16)
+    // fragments brought to x * 2^-E: from the planes one exponent E per
+    // batch row for the split (all H * PW panels of the workgroup), from fp32
+    // rows one per batch row and wave; formed after the weight ring's loads
+    // were issued, each wave's sums scaled by its 2^E (as in gemm_xs16)
     h8v xa[PW][4], xb[PW][4];
+    float xv[XROWS ? PW : 1][4][8];  // fp32 rows: the wave's values of this lane
     const int brow = min(lane & 31, batch - 1);
     const float *xr = XROWS ? xrows + (size_t)brow * n : nullptr;
     auto xcol = [&](int p, int st) { return 16 * (16 * (panel0 + p) + 4 * quarter + st) + 8 * (lane >> 5); };
@@ -2195,23 +2202,10 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
             }
         }
     } else {
-        // fp32 rows, split before the ring: lanes l, l + 32 and the NW waves
-        // hold a row's columns
-        float amax = 0.0f;
 #pragma unroll
         for (int p = 0; p < PW; p++)
 #pragma unroll
-            for (int st = 0; st < 4; st++) amax = amax8(xr + xcol(p, st), amax);
-        wmax[2 * wave + (lane >> 5)][lane & 31] = amax;
-        lds_barrier();
-        float rmax = wmax[0][lane & 31];
-#pragma unroll
-        for (int w = 1; w < 2 * NW; w++) rmax = fmaxf(rmax, wmax[w][lane & 31]);
-        E = group_exp(rmax);
-#pragma unroll
-        for (int p = 0; p < PW; p++)
-#pragma unroll
-            for (int st = 0; st < 4; st++) split8_scaled(xr + xcol(p, st), E, xa[p][st], xb[p][st]);
+            for (int st = 0; st < 4; st++) load8(xr + xcol(p, st), xv[p][st]);
     }
     const uint8_t *wpart = Wp + (size_t)panel0 * Panel<T>::kBytes;
     int lt = g0, lp = 0;  // load cursor: tile, panel of the wave's part
@@ -2256,11 +2250,24 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
                 xb[p][st] = xb[p][st] * f;
             }
         }
+    } else {
+        // fp32 rows (API path, splits of 2 panels): E from the row's largest
+        // |x| over this wave's columns -- lanes l and l ^ 32 hold the row
+        float amax = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PW; p++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(xv[p][st][i]));
+        E = group_exp(lanes_max2(amax));
+#pragma unroll
+        for (int p = 0; p < PW; p++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) split8_scaled(xv[p][st], E, xa[p][st], xb[p][st]);
     }
-    // the epilogue's batch row (threadIdx / 16) takes its exponent from the
-    // lane holding that row
+    if (lane < 32) ew[wave][lane] = E;  // lane l holds batch row l (read after the tile's barrier)
     static_assert(512 / (kWave * NW) == 1, "one output vector per thread");
-    const float fEb = xe_scale(row_exp4(E, 4 * wave));
     int ct = g0;  // tile being multiplied
     f32x16 acc0 = {}, acc1 = {};
     do {
@@ -2290,13 +2297,13 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
                     const int b = v >> 4, j = v & 15;
                     const int r = 4 * (b >> 3) + (b & 3) + (j >= 8 ? 16 : 0);
                     const int l = ((4 * j) & 31) + 32 * ((b >> 2) & 1);
-                    float4 sum = *reinterpret_cast<const float4 *>(&red[0][r][l]);
+                    // each wave's sums times its 2^E (exact), added in wave order
+                    float4 sum = mul4(*reinterpret_cast<const float4 *>(&red[0][r][l]), xe_scale(ew[0][b]));
 #pragma unroll
                     for (int w = 1; w < NW; w++) {
-                        const float4 o = *reinterpret_cast<const float4 *>(&red[w][r][l]);
+                        const float4 o = mul4(*reinterpret_cast<const float4 *>(&red[w][r][l]), xe_scale(ew[w][b]));
                         sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
                     }
-                    sum = mul4(sum, fEb);
                     const int row = ct * kWave + 4 * j;
                     const int off = b < batch && row < m && ct < tiles ? 4 * (ks * (int)split_stride + b * m + row)
                                                                        : kBadOffset;
