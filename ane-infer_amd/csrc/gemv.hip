@@ -2927,6 +2927,20 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
                        (int)n);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     if (batch <= 16) return launch_mfma<T, 1>(ctx, stream, w, m, n, xp, batch, out, split_stride, ksplit);
+    // 17..32 rows: a matrix that stays in the 256 MiB MALL takes two 16-row
+    // passes (the second reads the weights from the MALL), a larger one the
+    // 32-row kernel.  Measured on MI355X (graphs of back-to-back launches):
+    // 6144 x 2048 at 32 rows 24.7 us in one 32-row pass against 9.3 us for
+    // one 16-row pass; lm_head 161 us against 105 per 16-row pass.
+    if ((double)m * (n / 32) * QTraits<T>::kBlockBytes <= 128.0 * (1 << 20)) {
+        int rc = launch_mfma<T, 1>(ctx, stream, w, m, n, xp, 16, out, split_stride, ksplit);
+        if (rc) return rc;
+        Planes x2;
+        x2.hi = xp.hi + (size_t)16 * n;
+        x2.lo = xp.lo + (size_t)16 * n;
+        x2.xe = xp.xe + (size_t)16 * xe_stride((int)n);
+        return launch_mfma<T, 1>(ctx, stream, w, m, n, x2, batch - 16, out + (size_t)16 * m, split_stride, ksplit);
+    }
     return launch_mfma<T, 2>(ctx, stream, w, m, n, xp, batch, out, split_stride, ksplit);
 }
 

@@ -71,10 +71,11 @@ def test_gemv_parity(gpu_ctx, oracle_lib, t, m, n):
 
 
 @pytest.mark.parametrize("t", [8, 2])
-@pytest.mark.parametrize("batch", [1, 3, 4, 7, 16, 32])
+@pytest.mark.parametrize("batch", [1, 3, 4, 7, 16, 17, 32])
 @pytest.mark.parametrize("m,n", [(6144, 2048), (2048, 6144)])
 def test_small_batch_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
-    """Ragged batches: batch is not padded to any tile; rows are read exactly."""
+    """Ragged batches: batch is not padded to any tile; rows are read exactly
+    (17 and 32 rows: two 16-row passes, the second of 1 or 16 rows)."""
     w = oracle_lib.gen_quant(t, 77, m + n + t, m, n, std=0.02)
     x = oracle_lib.normal(77, 1000 + batch, batch * n).reshape(batch, n)
     y = _run(gpu_ctx, t, w, m, n, x)
