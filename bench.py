@@ -79,18 +79,24 @@ def dn_step_bytes(batch: int) -> int:
     return batch * per_seq + DN_CH * 4 * 4
 
 
-def profiled_traffic():
-    """HBM bytes per launch of the roofline kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (scaled by a copy of known size), or None."""
+def profiled_value(key: str):
+    """A `key: value` line of the committed rocprofv3 summary of the roofline
+    kernel (HBM bytes per launch from FETCH_SIZE / WRITE_SIZE scaled by a copy
+    of known size; rocprof's average launch duration), or None."""
     path = os.path.join(ROOT, "profiles", "gemv_packed_lm_head_m1.md")
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
+                if line.startswith(key + ":"):
+                    return float(line.split(":")[1])
     except OSError:
         pass
     return None
+
+
+def profiled_traffic():
+    v = profiled_value("traffic_bytes_per_launch")
+    return None if v is None else int(v)
 
 
 def algo_bytes(m: int, n: int, batch: int, t: int = Q8) -> int:
@@ -728,12 +734,19 @@ def main():
             "traffic_source": "profiles/gemv_packed_lm_head_m1.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-scaled)",
             "algorithmic_bytes": lm_bytes,
             "avg_launch_us": round(t_lm * 1e3, 2),
+            "timing": "HIP events on the library stream around a graph of back-to-back launches, this run",
         },
         "c0_gemv_6144x2048": {"us": c0["us"], "GB/s": c0["GB/s"],
                                "pct_of_hbm_peak": round(100 * c0["GB/s"] / HBM_PEAK_GBS, 1)},
         "sweep_points": points,
         "gguf_layout_points": gguf_points,
     }
+    rp_us = profiled_value("rocprof_avg_us")
+    if rp_us:
+        # the committed rocprofv3 kernel-trace average of the same kernel and
+        # workload, and the fraction it gives (beside the live event figure)
+        out["roofline"]["rocprof_avg_us"] = rp_us
+        out["roofline"]["frac_rocprof"] = round(lm_bytes / (rp_us * 1e3) / HBM_PEAK_GBS, 4)
     out["c0_gemv_6144x2048"]["floor"] = c0_floor(ctx, shapes[0])
     out["c0_gemv_6144x2048"]["pct_of_floor"] = round(100 * out["c0_gemv_6144x2048"]["floor"]["best_us"] / c0["us"], 1)
     out["configs2_q4"] = bench_q4(anehip, ctx)
