@@ -84,7 +84,7 @@ enum GemvInMode : int {
     GEMV_IN_RESID_RMSNORM, // r = x + sum_p part[p]; rmsnorm(r, w); r -> x_out
     GEMV_IN_EMBED_RMSNORM, // r = emb[token] (0 if token >= vocab); rmsnorm(r, w); r -> x_out
     GEMV_IN_GATED_NORM,    // per-128 head rmsnorm(x, w) * SiLU(gate), gate = sum_p part[p][gate_off..]
-    GEMV_IN_SILU_MUL,      // SiLU(sum_p part[p][k]) * sum_p part[p][n + k]
+    GEMV_IN_SILU_MUL,      // SiLU(sum_p part[p][gu_index(k)]) * sum_p part[p][gu_index(k) + 32]
     GEMV_IN_ATTN_COMBINE,  // batch row 0's attention output of the slice's heads: the chunk partials
                            // merged (running max / sum) times sigmoid(gate), gate from part
 };
@@ -205,13 +205,20 @@ int launch_gemm_raw(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, con
 int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, float *y, size_t count,
                         int ksplit);
 // Panel layout (see gemv.hip): bytes of an [m x n] matrix, repack from GGUF
-// blocks, and the batch-1 GEMV over panels.
+// blocks, and the batch-1 GEMV over panels.  il = F > 0 (m = 2 F, F % 32 ==
+// 0): the rows of a stacked [gate; up] matrix are interleaved in groups of 32
+// -- panel tile t holds gate rows 32 t .. 32 t + 31, then the up rows of the
+// same features -- so every product over it leaves, per 64 output rows, 32
+// gate sums followed by the 32 matching up sums (gu_index()).
 size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n);
 int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
-                  void *dst);
+                  void *dst, uint32_t il = 0);
 // The inverse of launch_repack: panel bytes back to GGUF blocks (rows < m).
 int launch_unpack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
-                  void *dst);
+                  void *dst, uint32_t il = 0);
+// Output position of feature f's gate sum in a product over an interleaved
+// [gate; up] panel matrix; its up sum follows 32 positions later.
+__host__ __device__ __forceinline__ int gu_index(int f) { return 64 * (f >> 5) + (f & 31); }
 // Input planes of the panel MFMA GEMM (batch 2..32): fp16 hi / lo planes of
 // x in "fragment order", 32 rows (batch entries) x n columns per plane.
 // Element (b, c) lies in the 1 KiB block of its 16-column step c / 16, at the
@@ -492,6 +499,8 @@ int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const 
                          const Planes &xp = Planes{});
 int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
                             int ksplit, const float *w, float *xn, float eps, const Planes &xp = Planes{});
+// gu: the ksplit partial slices [rows][2F] of a product over the interleaved
+// [gate; up] panel matrix (feature f's gate sum at gu_index(f), up + 32).
 int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit,
                             float *h, const Planes &xp = Planes{});
 int launch_silu_mul(anehip_ctx *ctx, hipStream_t s, float *a, const float *b, size_t n);

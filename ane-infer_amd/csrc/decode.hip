@@ -46,6 +46,7 @@ constexpr uint32_t kHd = 256;
 struct QMat {
     void *d = nullptr, *p = nullptr;
     uint32_t type = 0, rows = 0, cols = 0;
+    uint32_t il = 0;  // > 0: a stacked [gate; up] matrix of il features each, its panel rows interleaved
     bool stale = true;
     bool keep = false;
 };
@@ -559,7 +560,7 @@ int pack_mat(anehip_ctx *ctx, QMat &Q) {
             return set_error(ctx->err, ANEHIP_ENOMEM, "decode: cannot allocate %zu bytes of panel weights", bytes);
         }
     }
-    TRY(launch_repack(ctx, ctx->stream, Q.type, Q.d, Q.rows, Q.cols, Q.p));
+    TRY(launch_repack(ctx, ctx->stream, Q.type, Q.d, Q.rows, Q.cols, Q.p, Q.il));
     Q.stale = false;
     if (!Q.keep) {
         // the panel copy is the only one the step reads: drop the GGUF copy
@@ -585,7 +586,7 @@ int gguf_copy(anehip_ctx *ctx, QMat &Q, uint32_t ggml_type, uint32_t total_rows,
         return set_error(ctx->err, ANEHIP_ENOMEM, "%s: cannot allocate %zu bytes", who, bytes);
     }
     if (Q.p) {
-        TRY(launch_unpack(ctx, ctx->stream, Q.type, Q.p, Q.rows, Q.cols, Q.d));
+        TRY(launch_unpack(ctx, ctx->stream, Q.type, Q.p, Q.rows, Q.cols, Q.d, Q.il));
         ANEHIP_HIP_TRY(ctx->err, hipStreamSynchronize(ctx->stream));
     } else {
         Q.type = ggml_type;
@@ -818,7 +819,12 @@ __attribute__((visibility("hidden"))) int anehip_model_setup(anehip_ctx *ctx, co
     M->types.assign(D.layer_types, D.layer_types + D.n_layers);
     M->desc.layer_types = M->types.data();
     M->layers.resize(D.n_layers);
-    for (uint32_t l = 0; l < D.n_layers; l++) M->layers[l].type = D.layer_types[l];
+    for (uint32_t l = 0; l < D.n_layers; l++) {
+        M->layers[l].type = D.layer_types[l];
+        // the FFN's gate / up products come out in groups of 32 features
+        // (gate sums, then the matching up sums): gu_index()
+        M->layers[l].ffn_gu.il = D.hidden_dim;
+    }
     M->rows_dn = 3 * D.dim + D.dim + 2 * D.ssm_group_count;
     M->rows_attn = has_attn ? 2 * D.n_heads * D.head_dim + 2 * D.n_kv_heads * D.head_dim : 0;
     ctx->model = M;

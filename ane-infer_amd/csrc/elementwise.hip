@@ -170,8 +170,10 @@ __global__ __launch_bounds__(512) void residual_rmsnorm_v4(float *__restrict__ x
     }
 }
 
-// Stacked [gate; up] GEMV output gu[k][b][2F]: h[b][r] = SiLU(gate) * up
-// (scratch.rs:181-186: a = (a / (1 + exp(-a))) * b).
+// Output of the GEMM over the interleaved [gate; up] panel matrix,
+// gu[k][b][2F] with feature r's gate sum at gu_index(r) and its up sum 32
+// positions on: h[b][r] = SiLU(gate) * up (scratch.rs:181-186: a = (a / (1 +
+// exp(-a))) * b).
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restrict__ gu, int ksplit, int rows,
                                                             float *__restrict__ h, int F, Planes xp) {
     __shared__ float wm[kThreads / 64];
@@ -180,10 +182,11 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *__restr
     const bool in = r < F;
     const int rr = in ? r : F - 1;
     const size_t split = (size_t)rows * 2 * F;
-    float g = gu[b * 2 * F + rr], u = gu[b * 2 * F + F + rr];
+    const size_t gi = b * 2 * F + gu_index(rr);
+    float g = gu[gi], u = gu[gi + 32];
     for (int k = 1; k < ksplit; k++) {
-        g += gu[k * split + b * 2 * F + rr];
-        u += gu[k * split + b * 2 * F + F + rr];
+        g += gu[k * split + gi];
+        u += gu[k * split + gi + 32];
     }
     const float v = (g / (1.0f + expf(-g))) * u;
     if (xp.hi) {
@@ -213,13 +216,14 @@ __global__ __launch_bounds__(kThreads) void silu_mul_v4(const float *__restrict_
     const bool in = r < F;
     if (!xp.hi && !in) return;
     const size_t split = (size_t)rows * 2 * F;
-    const float *g0 = gu + (size_t)b * 2 * F + (in ? r : F - 4);
+    // features r .. r + 3 lie in one group of 32 of the interleaved order
+    const float *g0 = gu + (size_t)b * 2 * F + gu_index(in ? r : F - 4);
     float4 gv[KP], uv[KP];
 #pragma unroll
     for (int k = 0; k < KP; k++) {
         const size_t o = (size_t)min(k, ksplit - 1) * split;
         gv[k] = *reinterpret_cast<const float4 *>(g0 + o);
-        uv[k] = *reinterpret_cast<const float4 *>(g0 + F + o);
+        uv[k] = *reinterpret_cast<const float4 *>(g0 + 32 + o);
     }
     float g[4] = {gv[0].x, gv[0].y, gv[0].z, gv[0].w}, u[4] = {uv[0].x, uv[0].y, uv[0].z, uv[0].w};
 #pragma unroll

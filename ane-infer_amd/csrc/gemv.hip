@@ -351,8 +351,9 @@ __device__ __forceinline__ void gemv_prologue(const GemvInput &in, int n, int c0
 #pragma unroll
             for (int i = 0; i < B; i++) {
                 const int j = min(t + NT * (i0 + i), len - 1);
-                g[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)c0 + j);
-                u[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)n + c0 + j);
+                const int gi = gu_index(c0 + j);  // the products' interleaved [gate; up] order
+                g[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)gi);
+                u[i] = sum_parts(in.part, in.kp, in.part_stride, (size_t)gi + 32);
             }
 #pragma unroll
             for (int i = 0; i < B; i++)
@@ -527,10 +528,21 @@ template <> struct Panel<ANEHIP_GGML_Q4_0> {
     static constexpr int kBytes = 9 * 1024;
 };
 
+// The GGUF row behind panel row `row`: the identity, or (il = F > 0, a
+// stacked [gate (F rows); up (F rows)] matrix) gate rows 32 t .. 32 t + 31 in
+// the first half of tile t and the same features' up rows in its second
+// half, so that one 64-row tile of the panel copy holds the gate and the up
+// row of each of its 32 features.
+__host__ __device__ __forceinline__ int src_row(int row, int il) {
+    if (!il) return row;
+    const int t = row >> 6, r = row & 63;
+    return (r < 32 ? 0 : il) + 32 * t + (r & 31);
+}
+
 // One thread per 16-byte destination vector of the panel buffer.
 template <uint32_t T>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
-                                                    int m, int n, size_t nvec) {
+                                                    int m, int n, size_t nvec, int il) {
     const size_t v = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (v >= nvec) return;
     constexpr int BB = QTraits<T>::kBlockBytes;
@@ -541,7 +553,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     const int chunk = within / 64, r = within % 64;  // chunk == kChunks: the scale vector
     const int row = tile * 64 + r;
     uint8_t out[16];
-    const size_t row_off = (size_t)row * (n / 32) * BB;
+    const size_t row_off = (size_t)src_row(row, il) * (n / 32) * BB;
     for (int i = 0; i < 16; i++) {
         uint8_t b = 0;
         if (row < m) {
@@ -568,7 +580,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
 // padding rows of the last tile hold zeros and have no GGUF position).
 template <uint32_t T>
 __global__ __launch_bounds__(256) void unpack_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
-                                                    int m, int n, size_t nvec) {
+                                                    int m, int n, size_t nvec, int il) {
     const size_t v = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (v >= nvec) return;
     constexpr int BB = QTraits<T>::kBlockBytes;
@@ -581,7 +593,7 @@ __global__ __launch_bounds__(256) void unpack_kernel(const uint8_t *__restrict__
     if (row >= m) return;
     const u32x4 w = reinterpret_cast<const u32x4 *>(src)[v];
     const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
-    const size_t row_off = (size_t)row * (n / 32) * BB;
+    const size_t row_off = (size_t)src_row(row, il) * (n / 32) * BB;
     for (int i = 0; i < 16; i++) {
         const uint8_t b = (uint8_t)(w4[i >> 2] >> (8 * (i & 3)));
         if (chunk < Panel<T>::kChunks) {
@@ -855,9 +867,12 @@ __device__ __forceinline__ void prologue_overlapped(const GemvInput &in, int n, 
         __syncthreads();
     } else if constexpr (MODE == GEMV_IN_SILU_MUL) {
         const int e4 = min(t, (len >> 2) - 1);
+        // features c0 + 4 e4 .. + 3: one group of 32 in the products'
+        // interleaved [gate; up] order, their up sums 32 positions on
+        const int gi = gu_index(c0 + 4 * e4);
         float4 g[KP], u[KP];
-        load_parts4<KP>(g, in.part, in.kp, in.part_stride, (size_t)(c0 >> 2) + e4);
-        load_parts4<KP>(u, in.part, in.kp, in.part_stride, (size_t)((n + c0) >> 2) + e4);
+        load_parts4<KP>(g, in.part, in.kp, in.part_stride, (size_t)(gi >> 2));
+        load_parts4<KP>(u, in.part, in.kp, in.part_stride, (size_t)((gi + 32) >> 2));
         issue();
         const float4 gs = sum_parts4<KP>(g, in.kp), us = sum_parts4<KP>(u, in.kp);
         store(make_float4(silu1(gs.x) * us.x, silu1(gs.y) * us.y, silu1(gs.z) * us.z, silu1(gs.w) * us.w), t,
@@ -3213,15 +3228,19 @@ int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, co
 }
 
 int launch_unpack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
-                  void *dst) {
+                  void *dst, uint32_t il) {
+    if (il && (m != 2 * il || il % 32))
+        return set_error(ctx->err, ANEHIP_EINVAL, "unpack: %u rows cannot interleave halves of %u", m, il);
     const size_t nvec = packed_bytes(ggml_type, m, n) / 16;
     const unsigned grid = (unsigned)((nvec + 255) / 256);
     if (ggml_type == ANEHIP_GGML_Q8_0)
         hipLaunchKernelGGL(unpack_kernel<ANEHIP_GGML_Q8_0>, dim3(grid), dim3(256), 0, stream,
-                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec);
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec,
+                           (int)il);
     else
         hipLaunchKernelGGL(unpack_kernel<ANEHIP_GGML_Q4_0>, dim3(grid), dim3(256), 0, stream,
-                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec);
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec,
+                           (int)il);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
@@ -3232,15 +3251,19 @@ size_t packed_bytes(uint32_t ggml_type, uint32_t m, uint32_t n) {
 }
 
 int launch_repack(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *src, uint32_t m, uint32_t n,
-                  void *dst) {
+                  void *dst, uint32_t il) {
+    if (il && (m != 2 * il || il % 32))
+        return set_error(ctx->err, ANEHIP_EINVAL, "repack: %u rows cannot interleave halves of %u", m, il);
     const size_t nvec = packed_bytes(ggml_type, m, n) / 16;
     const unsigned grid = (unsigned)((nvec + 255) / 256);
     if (ggml_type == ANEHIP_GGML_Q8_0)
         hipLaunchKernelGGL(repack_kernel<ANEHIP_GGML_Q8_0>, dim3(grid), dim3(256), 0, stream,
-                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec);
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec,
+                           (int)il);
     else
         hipLaunchKernelGGL(repack_kernel<ANEHIP_GGML_Q4_0>, dim3(grid), dim3(256), 0, stream,
-                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec);
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), (int)m, (int)n, nvec,
+                           (int)il);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
