@@ -386,6 +386,12 @@ int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, co
 // planes needed): launch_gemm_xs_rows writes out[ks][b][r] for its
 // gemm_packed_ksplit splits.
 bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
+// The FFN gate / up product (interleaved [gate; up] panel matrix, m = 2 F)
+// with the SiLU-mul fused: h[b][f] as fp32 rows [batch][F], one launch, no
+// partial sums; covered at batch 17..32 for K = 512, 1024 or 2048.
+bool gemm_gate_up_silu_ok(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
+int launch_gemm_gate_up_silu(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
+                             uint32_t n, const Planes &xp, uint32_t batch, float *h);
 int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
                         uint32_t n, const float *x, uint32_t batch, float *out);
 // x [batch][n] fp32 -> fragment-order hi / lo planes (xf_plane_len(n) halves each).

@@ -495,11 +495,19 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
         const int k3 = gemm_packed_ksplit(ctx, d, cols3, B);
         TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xp, B, M->p0, k3));
         TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, nullptr, eps, xp));
-        const int k4 = gemm_packed_ksplit(ctx, 2 * F, d, B);
-        TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, B, M->p1, k4));
-        TRY(launch_silu_mul_stacked(ctx, s, B, (int)F, M->p1, k4, nullptr, xp));
         const int k5 = gemm_packed_ksplit(ctx, d, F, B);
-        TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xp, B, M->p0, k5));
+        if (gemm_gate_up_silu_ok(ctx, 2 * F, d, B) && gemm_is_xs(ctx, d, F, B)) {
+            // the SiLU-mul in the gate / up product's epilogue (h as fp32
+            // rows in p1), the down product splitting those rows itself:
+            // one launch less per layer
+            TRY(launch_gemm_gate_up_silu(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, B, M->p1));
+            TRY(launch_gemm_xs_rows(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, M->p1, B, M->p0));
+        } else {
+            const int k4 = gemm_packed_ksplit(ctx, 2 * F, d, B);
+            TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, B, M->p1, k4));
+            TRY(launch_silu_mul_stacked(ctx, s, B, (int)F, M->p1, k4, nullptr, xp));
+            TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xp, B, M->p0, k5));
+        }
         const float *next_norm = l + 1 < D.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
         TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k5, next_norm, nullptr, eps, xp));
     }

@@ -2162,8 +2162,11 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
 // (4 quant vectors + 1 scale dword) D deep; a tile's sums are added over the
 // 4 H waves through LDS.  With H = 2 the split's x fragments (up to 8 panels)
 // fit in registers at two waves per SIMD, so lm_head needs no K split and no
-// x loads in its main loop.  Output as gemm_xs.
-template <uint32_t T, int PW, int D, int H, bool XROWS = false>
+// x loads in its main loop.  Output as gemm_xs; with SILU (one K split, the
+// interleaved [gate; up] panel matrix, m = 2 F) the tile's 32 gate sums meet
+// their 32 up sums in the epilogue, which writes h[b][f] = SiLU(gate) * up
+// (scratch.rs:181-186) as fp32 rows [batch][F] instead of the sums.
+template <uint32_t T, int PW, int D, int H, bool XROWS = false, bool SILU = false>
 __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_per_eu(2))) void gemm_xsh(
     const uint8_t *__restrict__ Wp, Planes xp, const float *__restrict__ xrows, float *__restrict__ out, int m, int n,
     int batch, int ksplit, size_t split_stride) {
@@ -2319,11 +2322,28 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
                         const float4 o = mul4(*reinterpret_cast<const float4 *>(&red[w][r][l]), xe_scale(ew[w][b]));
                         sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
                     }
-                    const int row = ct * kWave + 4 * j;
-                    const int off = b < batch && row < m && ct < tiles ? 4 * (ks * (int)split_stride + b * m + row)
-                                                                       : kBadOffset;
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0,
-                                                           kCpolDevice);
+                    if constexpr (SILU) {
+                        // rows 4 j .. + 3 (j < 8): the gate sums of features
+                        // 32 ct + 4 j .. + 3; their up sums are rows 32 + 4 j
+                        // .., held by lane + 8 (same batch row)
+                        const float4 up = make_float4(__shfl_down(sum.x, 8), __shfl_down(sum.y, 8),
+                                                      __shfl_down(sum.z, 8), __shfl_down(sum.w, 8));
+                        const float4 h4 = make_float4((sum.x / (1.0f + expf(-sum.x))) * up.x,
+                                                      (sum.y / (1.0f + expf(-sum.y))) * up.y,
+                                                      (sum.z / (1.0f + expf(-sum.z))) * up.z,
+                                                      (sum.w / (1.0f + expf(-sum.w))) * up.w);
+                        const int f = 32 * ct + 4 * j;
+                        const int off = j < 8 && b < batch && ct < tiles ? 4 * (b * (m >> 1) + f) : kBadOffset;
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, h4), orsrc, off, 0,
+                                                               kCpolDevice);
+                    } else {
+                        const int row = ct * kWave + 4 * j;
+                        const int off = b < batch && row < m && ct < tiles
+                                            ? 4 * (ks * (int)split_stride + b * m + row)
+                                            : kBadOffset;
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), orsrc, off, 0,
+                                                               kCpolDevice);
+                    }
                 }
                 lds_barrier();  // red is free again
                 acc0 = f32x16{};
@@ -3144,6 +3164,44 @@ int launch_gemm_xs_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type,
     else
         launch_gemm_xs_any<ANEHIP_GGML_Q4_0>(ctx, stream, kind, w, m, n, Planes{}, x, batch, out, ksplit,
                                              (size_t)batch * m);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+bool gemm_gate_up_silu_ok(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch) {
+    (void)ctx;
+    const int nsb = (int)(n / 256);
+    return batch > 16 && batch <= 32 && n % 256 == 0 && m % 64 == 0 && (nsb == 2 || nsb == 4 || nsb == 8) &&
+           gemm_kernel(batch, nsb, 1) == GemmKernel::Xsh;
+}
+
+// The FFN's gate / up product in one K split with the SiLU-mul in its
+// epilogue (gemm_xsh<..., SILU>): h[b][f] for the interleaved [gate; up]
+// panel matrix of m = 2 F rows, fp32 rows [batch][F].  Measured on MI355X at
+// batch 32, 12288 x 2048: the unsplit product 11.8 us against 9.7 us in 4
+// splits plus 4.8 us for the SiLU-mul launch that read them.
+int launch_gemm_gate_up_silu(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, const void *wp, uint32_t m,
+                             uint32_t n, const Planes &xp, uint32_t batch, float *h) {
+    if (!gemm_gate_up_silu_ok(ctx, m, n, batch))
+        return set_error(ctx->err, ANEHIP_EINVAL, "gemm_gate_up_silu: %u x %u at batch %u not covered", m, n, batch);
+    const int tiles = (int)(m / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const dim3 grid(max(1, min(tiles, cus)));
+    const uint8_t *w = static_cast<const uint8_t *>(wp);
+    const size_t ss = (size_t)batch * (m / 2);
+#define ANEHIP_GUS(TT, PW, D)                                                                                     \
+    hipLaunchKernelGGL((gemm_xsh<TT, PW, D, 2, false, true>), grid, dim3(512), 0, stream, w, xp, nullptr, h,    \
+                       (int)m, (int)n, (int)batch, 1, ss)
+    const int nsb = (int)(n / 256);
+    if (ggml_type == ANEHIP_GGML_Q8_0) {
+        if (nsb == 2) ANEHIP_GUS(ANEHIP_GGML_Q8_0, 1, 1);
+        else if (nsb == 4) ANEHIP_GUS(ANEHIP_GGML_Q8_0, 2, 2);
+        else ANEHIP_GUS(ANEHIP_GGML_Q8_0, 4, 2);
+    } else {
+        if (nsb == 2) ANEHIP_GUS(ANEHIP_GGML_Q4_0, 1, 1);
+        else if (nsb == 4) ANEHIP_GUS(ANEHIP_GGML_Q4_0, 2, 2);
+        else ANEHIP_GUS(ANEHIP_GGML_Q4_0, 4, 2);
+    }
+#undef ANEHIP_GUS
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }
