@@ -69,10 +69,10 @@ __global__ __launch_bounds__(32 * NQ) void deltanet_step_kernel(
     const float *__restrict__ dt_bias, float *__restrict__ conv_state, float *__restrict__ S, float *__restrict__ out,
     int n_heads, uint32_t *__restrict__ count) {
     constexpr int NT = 32 * NQ, NW = NT / kWave, COLS = 4 * NQ, QK = 2 * kDk / NT;  // q / k channels per thread
-    static_assert(NT % kWave == 0 && QK >= 1 && COLS <= NT, "workgroup shape");
+    static_assert(NQ == 8 && NT % kWave == 0 && QK >= 1 && COLS <= NT, "workgroup shape");
     __shared__ float qn[kDk], kn[kDk], vv[COLS];
     __shared__ float red[NW][2];
-    __shared__ float part[32][COLS];
+    __shared__ __align__(16) float part[NW][COLS];
     __shared__ int last_slice;
 
     const int t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
@@ -175,7 +175,11 @@ __global__ __launch_bounds__(32 * NQ) void deltanet_step_kernel(
     if (count && t == 0)
         last_slice = __hip_atomic_fetch_add(count + (size_t)b * n_heads + h, 1u, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
-    // 2. L2 normalise (deltanet.rs:25-31, 461-467): x *= 1/sqrt(sum x^2 + 1e-12); q *= 1/sqrt(dk)
+    // 2. the L2 norms (deltanet.rs:25-31, 461-467): q *= 1/sqrt(sum q^2 +
+    // 1e-12) / sqrt(dk), k *= 1/sqrt(sum k^2 + 1e-12); qn / kn keep the raw
+    // values and the factors go onto the sums below (no pass and no barrier
+    // of their own)
+    float invq, invk;
     {
         float sq = red[0][0], sk = red[0][1];
 #pragma unroll
@@ -183,18 +187,20 @@ __global__ __launch_bounds__(32 * NQ) void deltanet_step_kernel(
             sq += red[w][0];
             sk += red[w][1];
         }
-        const float invq = 1.0f / sqrtf(sq + 1e-12f), invk = 1.0f / sqrtf(sk + 1e-12f);
-        const float scale = 1.0f / sqrtf((float)kDk);
-#pragma unroll
-        for (int j = 0; j < QK; j++) {
-            const int i = t + NT * j;
-            if (i < kDk) qn[i] = (qn[i] * invq) * scale;
-            else kn[i - kDk] = kn[i - kDk] * invk;
-        }
+        invq = (1.0f / sqrtf(sq + 1e-12f)) * (1.0f / sqrtf((float)kDk));
+        invk = 1.0f / sqrtf(sk + 1e-12f);
     }
-    __syncthreads();
+    // column sums over the 128 rows: thread (row group rg = t / 8, column
+    // quad cq = t % 8) adds its 4 rows, lanes l ^ 8, l ^ 16, l ^ 32 (the
+    // wave's 8 row groups of the same columns) are added by lane exchanges
+    // (DPP row_ror:8, v_permlane16 / 32_swap), the NW waves through LDS
+    const auto wave_cols = [&](float4 v) {
+        return make_float4(lanes_sum4(dpp_add<0x128>(v.x)), lanes_sum4(dpp_add<0x128>(v.y)),
+                           lanes_sum4(dpp_add<0x128>(v.z)), lanes_sum4(dpp_add<0x128>(v.w)));
+    };
 
-    // 3. S' = decay * S, partial recall sum_i S'_ij k_i over this thread's rows
+    // 3. S' = decay S, recall S'^T k over this thread's rows (raw k, the
+    // norm applied to the sum)
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -202,37 +208,41 @@ __global__ __launch_bounds__(32 * NQ) void deltanet_step_kernel(
         s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
         sk.x += s[r].x * ki; sk.y += s[r].y * ki; sk.z += s[r].z * ki; sk.w += s[r].w * ki;
     }
-    *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = sk;
+    sk = wave_cols(sk);
+    if (lane < NQ) *reinterpret_cast<float4 *>(&part[wave][4 * cq]) = sk;
     __syncthreads();
-    // delta_j = beta (v_j - sk_j), every thread for its 4 columns (fixed order)
+    // delta_j = beta (v_j - sk_j), every thread for its 4 columns (waves in order)
     float4 delta;
     {
         float a[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int g = 0; g < 32; g++) {
-            float4 p = *reinterpret_cast<const float4 *>(&part[g][4 * cq]);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float4 p = *reinterpret_cast<const float4 *>(&part[w][4 * cq]);
             a[0] += p.x; a[1] += p.y; a[2] += p.z; a[3] += p.w;
         }
-        delta.x = beta * (vv[4 * cq + 0] - a[0]);
-        delta.y = beta * (vv[4 * cq + 1] - a[1]);
-        delta.z = beta * (vv[4 * cq + 2] - a[2]);
-        delta.w = beta * (vv[4 * cq + 3] - a[3]);
+        delta.x = beta * (vv[4 * cq + 0] - a[0] * invk);
+        delta.y = beta * (vv[4 * cq + 1] - a[1] * invk);
+        delta.z = beta * (vv[4 * cq + 2] - a[2] * invk);
+        delta.w = beta * (vv[4 * cq + 3] - a[3] * invk);
     }
     __syncthreads();  // part[] is reused below
-    // S'' = S' + k delta^T (written back), partial query sum_i S''_ij q_i
+    // S'' = S' + k delta^T (written back), query S''^T q over this thread's rows
     float4 so = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const float ki = kn[4 * rg + r], qi = qn[4 * rg + r];
+        const float ki = kn[4 * rg + r] * invk, qi = qn[4 * rg + r];
         s[r].x += ki * delta.x; s[r].y += ki * delta.y; s[r].z += ki * delta.z; s[r].w += ki * delta.w;
         *reinterpret_cast<float4 *>(Sh + (size_t)(4 * rg + r) * kDk) = s[r];
         so.x += s[r].x * qi; so.y += s[r].y * qi; so.z += s[r].z * qi; so.w += s[r].w * qi;
     }
-    *reinterpret_cast<float4 *>(&part[rg][4 * cq]) = so;
+    so = wave_cols(so);
+    if (lane < NQ) *reinterpret_cast<float4 *>(&part[wave][4 * cq]) = so;
     __syncthreads();
     if (t < COLS) {
         float o = 0.f;
-        for (int g = 0; g < 32; g++) o += part[g][t];
-        out[(size_t)b * chunk + h * kDk + c0 + t] = o;
+#pragma unroll
+        for (int w = 0; w < NW; w++) o += part[w][t];
+        out[(size_t)b * chunk + h * kDk + c0 + t] = o * invq;
     }
     if (count && last_slice) {
         // q / k windows: shift left, append the new input (deltanet_cache.rs:34-42)
