@@ -182,9 +182,9 @@ int anehip_deltanet_step(anehip_ctx *ctx, uint32_t batch, uint32_t n_heads, cons
     if (batch > 1)
         return launch_deltanet_head(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
                                     conv_state, S, out_heads, 0, nullptr, 0.0f, Planes{});
-    // batch 1: one launch, the q / k windows committed in-kernel (per-head
-    // counters); beyond the counters, dn_finish commits them
-    if (n_heads <= (uint32_t)kDnCounters)
+    // batch 1: one launch, the q / k windows committed in-kernel (256
+    // counters per head); beyond the counters, dn_finish commits them
+    if ((size_t)n_heads * 256 <= (size_t)kDnCounters)
         return launch_deltanet_step(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,
                                     conv_state, S, out_heads, ctx->dn_count);
     int rc = launch_deltanet_step(ctx, ctx->stream, (int)batch, (int)n_heads, mq, mb, ma, conv_w, ssm_a, dt_bias,

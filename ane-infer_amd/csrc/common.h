@@ -63,9 +63,10 @@ struct anehip_ctx {
 
 namespace anehip {
 
-// Counters at anehip_ctx::dn_count: the (sequence, head) pairs whose q / k
-// conv windows anehip_deltanet_step commits in its kernel.
-constexpr int kDnCounters = 4096;
+// Counters at anehip_ctx::dn_count for the q / k conv windows that
+// anehip_deltanet_step commits in its kernel: 256 per (sequence, head), one
+// per thread of its workgroups (256 heads at batch 1).
+constexpr int kDnCounters = 65536;
 
 // Ensures the workspace holds at least `floats` floats (grown with
 // hipMalloc; refused while the context stream is being captured).

@@ -49,31 +49,39 @@ __device__ __forceinline__ void head_to_planes(float v, int b, int c0, int n, in
     if (t == 0) xp.xe[xe_index(b, c0, n)] = (int8_t)e;
 }
 
-// grid = (dv / (4 NQ), n_heads, batch), 32 NQ threads: a workgroup takes
-// 4 NQ value columns of one head (NQ = 2: 8 columns and one wave, so a
-// batch-1 step of 16 heads runs 256 workgroups of 4 KiB of state each).
-// mix / mbeta / malpha: the qkv, beta and alpha projections of each sequence
-// ([3 chunk], [n_heads], [n_heads]), read as K-split partial slices
-// (KP >= their number).
+// grid = (dv / 32, n_heads, batch), 256 threads: a workgroup takes 32 value
+// columns of one head (64 workgroups of 16 KiB of state for a batch-1 step of
+// 16 heads).  Thread t holds rows 4 rg .. +3 (rg = t / 8) of columns
+// c0 + 4 cq .. +3 (cq = t % 8) in registers.  mix / mbeta / malpha: the qkv,
+// beta and alpha projections of each sequence ([3 chunk], [n_heads],
+// [n_heads]), read as K-split partial slices (KP >= their number).
 //
-// With `count` (one zeroed counter per (sequence, head)), the q / k windows
-// are committed by this kernel: each workgroup counts itself in once every
-// one of its threads has consumed the windows it read (after the first
-// barrier), and the head's last workgroup to count in -- all others have
-// read the windows by then -- shifts them and appends the new inputs, then
-// sets the counter back to zero.  Without it they are left to dn_finish /
-// the ssm_out GEMV's prologue.
-template <int KP, int NQ>
-__global__ __launch_bounds__(32 * NQ) void deltanet_step_kernel(
+// Each lane convolves one q / k channel, row 4 rg + cq % 4 of q (cq < 4) or
+// of k (cq >= 4), so a group of 8 lanes makes exactly the rows it holds and
+// shares them through LDS within the wave (no barrier).  Column sums over
+// the 128 rows: lanes l ^ 8, l ^ 16, l ^ 32 (the wave's 8 row groups) are
+// added by lane exchanges, the 4 waves through LDS; the q / k L2 norms are
+// applied to those sums (q and k stay raw in registers), and their sums of
+// squares go through the same barrier as the recall.  Two barriers a step.
+//
+// COUNT: the q / k windows are committed by this kernel, with one zeroed
+// counter per (sequence, head, thread): the same thread of every workgroup
+// of a head reads the same window, counts itself in once its convolution
+// has consumed that window, and the last one to count in (all others have
+// read it by then) shifts the window, appends the new input and sets the
+// counter back to zero.  Without COUNT the windows are left to dn_finish /
+// the ssm_out GEMV's prologue.  The v windows (one workgroup each) are
+// committed by their own thread.
+template <int KP, bool COUNT>
+__global__ __launch_bounds__(256) void deltanet_step_kernel(
     MixIn mix, MixIn mbeta, MixIn malpha, const float *__restrict__ conv_w, const float *__restrict__ ssm_a,
     const float *__restrict__ dt_bias, float *__restrict__ conv_state, float *__restrict__ S, float *__restrict__ out,
     int n_heads, uint32_t *__restrict__ count) {
-    constexpr int NT = 32 * NQ, NW = NT / kWave, COLS = 4 * NQ, QK = 2 * kDk / NT;  // q / k channels per thread
-    static_assert(NQ == 8 && NT % kWave == 0 && QK >= 1 && COLS <= NT, "workgroup shape");
-    __shared__ float qn[kDk], kn[kDk], vv[COLS];
-    __shared__ float red[NW][2];
-    __shared__ __align__(16) float part[NW][COLS];
-    __shared__ int last_slice;
+    constexpr int NQ = 8, NT = 32 * NQ, NW = NT / kWave, COLS = 4 * NQ;
+    __shared__ __align__(16) float qn[kDk], kn[kDk];
+    __shared__ float vv[COLS];
+    __shared__ __align__(16) float part[NW][COLS + 4];  // recall sums, then the q / k sums of squares
+    __shared__ __align__(16) float part2[NW][COLS];     // query sums
 
     const int t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
     const int slice = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -81,27 +89,19 @@ __global__ __launch_bounds__(32 * NQ) void deltanet_step_kernel(
     const int C = 3 * chunk;
     const int c0 = slice * COLS;
     float *cs = conv_state + (size_t)b * C * kKsize;
+    const int cq = t % NQ;  // column quad: columns c0 + 4cq .. +3
+    const int rg = t / NQ;  // row group: rows 4rg .. 4rg+3
+    const int row = 4 * rg + (cq & 3);
+    const int ch = (cq < 4 ? 0 : chunk) + h * kDk + row;    // this lane's q / k channel
+    const int chv = 2 * chunk + h * kDk + c0 + (t % COLS);  // v channel (t < COLS)
 
     // Every small input is loaded first and the state slice after it (vector
     // loads complete in order, so the conv and norms wait only for the small
-    // loads while the state is in flight).  Thread t convolves the head's
-    // q / k channels i = t + NT j (i < 128: q channel i, else k channel
-    // i - 128), and t < COLS also v channel c0 + t.
-    int ch[QK];
-#pragma unroll
-    for (int j = 0; j < QK; j++) {
-        const int i = t + NT * j;
-        ch[j] = i < kDk ? h * kDk + i : chunk + h * kDk + (i - kDk);
-    }
-    const int chv = 2 * chunk + h * kDk + c0 + (t % COLS);
-    f32x4 win[QK], wk[QK];
-    float xa[QK][KP];
-#pragma unroll
-    for (int j = 0; j < QK; j++) {
-        win[j] = *reinterpret_cast<const f32x4 *>(cs + (size_t)ch[j] * kKsize);
-        wk[j] = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)ch[j] * kKsize);
-        mix.load<KP>(b, ch[j], xa[j]);
-    }
+    // loads while the state is in flight).
+    f32x4 win = *reinterpret_cast<const f32x4 *>(cs + (size_t)ch * kKsize);
+    f32x4 wk = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)ch * kKsize);
+    float xa[KP];
+    mix.load<KP>(b, ch, xa);
     f32x4 winv = *reinterpret_cast<const f32x4 *>(cs + (size_t)chv * kKsize);
     f32x4 wkv = *reinterpret_cast<const f32x4 *>(conv_w + (size_t)chv * kKsize);
     float xv[KP], xb[KP], xal[KP];
@@ -110,28 +110,19 @@ __global__ __launch_bounds__(32 * NQ) void deltanet_step_kernel(
     malpha.load<KP>(b, h, xal);
     const float sa = ssm_a[h], dtb = dt_bias[h];
     asm volatile("" ::: "memory");  // keeps the state loads behind the small ones
-    // state slice: thread -> 4 columns (cq) x 4 rows (rg)
-    const int cq = t % NQ;         // column quad: columns c0 + 4cq .. +3
-    const int rg = t / NQ;         // row group: rows 4rg .. 4rg+3
     float *Sh = S + (((size_t)b * n_heads + h) * kDk) * kDk + c0 + 4 * cq;
     float4 s[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) s[r] = *reinterpret_cast<const float4 *>(Sh + (size_t)(4 * rg + r) * kDk);
     // the arithmetic on the small inputs starts after the state loads were
     // issued (else it is scheduled above them, with its waits)
-#pragma unroll
-    for (int j = 0; j < QK; j++) asm volatile("" : "+v"(win[j]), "+v"(wk[j])::"memory");
+    asm volatile("" : "+v"(win), "+v"(wk)::"memory");
     asm volatile("" : "+v"(winv), "+v"(wkv)::"memory");
 #pragma unroll
-    for (int q = 0; q < KP; q++) {
-#pragma unroll
-        for (int j = 0; j < QK; j++) asm volatile("" : "+v"(xa[j][q]));
-        asm volatile("" : "+v"(xv[q]), "+v"(xb[q]), "+v"(xal[q]));
-    }
+    for (int q = 0; q < KP; q++) asm volatile("" : "+v"(xa[q]), "+v"(xv[q]), "+v"(xb[q]), "+v"(xal[q]));
 
     // 1. conv + SiLU (conv_shift_and_append + conv_apply, deltanet_cache.rs:
-    // 34-54) of q / k from the old window (committed later by dn_finish / the
-    // ssm_out GEMV) and of v (committed here)
+    // 34-54) from the old window
     const auto conv = [](f32x4 w0, f32x4 k, float x) {
         float sum = 0.0f;
         sum += w0.y * k.x;
@@ -140,116 +131,97 @@ __global__ __launch_bounds__(32 * NQ) void deltanet_step_kernel(
         sum += x * k.w;
         return silu_ref(sum);
     };
-    float xin[QK];  // the new q / k inputs (appended to the windows by the head's last workgroup)
-    {
-        float sq[2] = {0.0f, 0.0f};  // sums of squares of this thread's q and k channels
-#pragma unroll
-        for (int j = 0; j < QK; j++) {
-            const int i = t + NT * j;
-            xin[j] = mix.add<KP>(xa[j]);
-            const float y = conv(win[j], wk[j], xin[j]);
-            if (i < kDk) {
-                qn[i] = y;
-                sq[0] += y * y;
-            } else {
-                kn[i - kDk] = y;
-                sq[1] += y * y;
-            }
-        }
-        const float s0 = wave_sum(sq[0]), s1 = wave_sum(sq[1]);
-        if (lane == 0) {
-            red[wave][0] = s0;
-            red[wave][1] = s1;
-        }
-    }
-    if (t < COLS) {
-        const float x = mix.add<KP>(xv);
-        vv[t] = conv(winv, wkv, x);
-        *reinterpret_cast<float4 *>(cs + (size_t)chv * kKsize) = make_float4(winv.y, winv.z, winv.w, x);
-    }
+    const float xin = mix.add<KP>(xa);
+    const float y = conv(win, wk, xin);
+    (cq < 4 ? qn : kn)[row] = y;
+    // this thread has consumed its window: count it in.  The atomic is issued
+    // by every lane (no branch), so waits for the state loads issued before
+    // it need not wait for it too.
+    asm volatile("" ::"v"(y) : "memory");
+    uint32_t old = 0;
+    uint32_t *cnt = COUNT ? count + ((size_t)b * n_heads + h) * NT + t : nullptr;
+    if (COUNT) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float xvin = mix.add<KP>(xv);
+    if (t < COLS) vv[t] = conv(winv, wkv, xvin);
     // deltanet.rs:474-480, by every thread (no shared copy needed)
     const float beta = 1.0f / (1.0f + expf(-mbeta.add<KP>(xb)));
     const float decay = expf(sa * logf(1.0f + expf(malpha.add<KP>(xal) + dtb)));
-    __syncthreads();
-    // every thread has consumed its window loads: count this workgroup in
-    if (count && t == 0)
-        last_slice = __hip_atomic_fetch_add(count + (size_t)b * n_heads + h, 1u, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     // 2. the L2 norms (deltanet.rs:25-31, 461-467): q *= 1/sqrt(sum q^2 +
-    // 1e-12) / sqrt(dk), k *= 1/sqrt(sum k^2 + 1e-12); qn / kn keep the raw
-    // values and the factors go onto the sums below (no pass and no barrier
-    // of their own)
-    float invq, invk;
-    {
-        float sq = red[0][0], sk = red[0][1];
-#pragma unroll
-        for (int w = 1; w < NW; w++) {
-            sq += red[w][0];
-            sk += red[w][1];
-        }
-        invq = (1.0f / sqrtf(sq + 1e-12f)) * (1.0f / sqrtf((float)kDk));
-        invk = 1.0f / sqrtf(sk + 1e-12f);
-    }
-    // column sums over the 128 rows: thread (row group rg = t / 8, column
-    // quad cq = t % 8) adds its 4 rows, lanes l ^ 8, l ^ 16, l ^ 32 (the
-    // wave's 8 row groups of the same columns) are added by lane exchanges
-    // (DPP row_ror:8, v_permlane16 / 32_swap), the NW waves through LDS
+    // 1e-12) / sqrt(dk), k *= 1/sqrt(sum k^2 + 1e-12), applied to the sums
+    // below.  The wave's sums of squares: its 32 q rows (lanes cq < 4, the
+    // quad by DPP) and its 32 k rows (cq >= 4).
+    float ss = dpp_add<0x4E>(dpp_add<0xB1>(y * y));
+    ss = lanes_sum4(dpp_add<0x128>(ss));
+    // column sums over the wave's 8 row groups (every lane gets its columns')
     const auto wave_cols = [&](float4 v) {
         return make_float4(lanes_sum4(dpp_add<0x128>(v.x)), lanes_sum4(dpp_add<0x128>(v.y)),
                            lanes_sum4(dpp_add<0x128>(v.z)), lanes_sum4(dpp_add<0x128>(v.w)));
     };
+    // rows 4 rg .. +3 were written by this lane's group of 8, in this wave
+    // (LDS accesses of one wave are performed in order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float4 q4 = *reinterpret_cast<const float4 *>(&qn[4 * rg]);
+    const float4 k4 = *reinterpret_cast<const float4 *>(&kn[4 * rg]);
+    const float kr[4] = {k4.x, k4.y, k4.z, k4.w}, qr[4] = {q4.x, q4.y, q4.z, q4.w};
 
-    // 3. S' = decay S, recall S'^T k over this thread's rows (raw k, the
-    // norm applied to the sum)
+    // 3. S' = decay S, recall S'^T k over this thread's rows (raw k)
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const float ki = kn[4 * rg + r];
+        const float ki = kr[r];
         s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
         sk.x += s[r].x * ki; sk.y += s[r].y * ki; sk.z += s[r].z * ki; sk.w += s[r].w * ki;
     }
     sk = wave_cols(sk);
     if (lane < NQ) *reinterpret_cast<float4 *>(&part[wave][4 * cq]) = sk;
+    if (lane == 0) part[wave][COLS] = ss;
+    if (lane == 4) part[wave][COLS + 1] = ss;
     __syncthreads();
     // delta_j = beta (v_j - sk_j), every thread for its 4 columns (waves in order)
     float4 delta;
+    float invq, invk;
     {
-        float a[4] = {0.f, 0.f, 0.f, 0.f};
+        float a[4] = {0.f, 0.f, 0.f, 0.f}, sq = 0.f, skk = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
             const float4 p = *reinterpret_cast<const float4 *>(&part[w][4 * cq]);
             a[0] += p.x; a[1] += p.y; a[2] += p.z; a[3] += p.w;
+            sq += part[w][COLS];
+            skk += part[w][COLS + 1];
         }
+        invq = (1.0f / sqrtf(sq + 1e-12f)) * (1.0f / sqrtf((float)kDk));
+        invk = 1.0f / sqrtf(skk + 1e-12f);
         delta.x = beta * (vv[4 * cq + 0] - a[0] * invk);
         delta.y = beta * (vv[4 * cq + 1] - a[1] * invk);
         delta.z = beta * (vv[4 * cq + 2] - a[2] * invk);
         delta.w = beta * (vv[4 * cq + 3] - a[3] * invk);
     }
-    __syncthreads();  // part[] is reused below
-    // S'' = S' + k delta^T (written back), query S''^T q over this thread's rows
+    // S'' = S' + k delta^T (written back), query S''^T q over this thread's rows (raw q)
     float4 so = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const float ki = kn[4 * rg + r] * invk, qi = qn[4 * rg + r];
+        const float ki = kr[r] * invk, qi = qr[r];
         s[r].x += ki * delta.x; s[r].y += ki * delta.y; s[r].z += ki * delta.z; s[r].w += ki * delta.w;
         *reinterpret_cast<float4 *>(Sh + (size_t)(4 * rg + r) * kDk) = s[r];
         so.x += s[r].x * qi; so.y += s[r].y * qi; so.z += s[r].z * qi; so.w += s[r].w * qi;
     }
     so = wave_cols(so);
-    if (lane < NQ) *reinterpret_cast<float4 *>(&part[wave][4 * cq]) = so;
+    if (lane < NQ) *reinterpret_cast<float4 *>(&part2[wave][4 * cq]) = so;
     __syncthreads();
     if (t < COLS) {
         float o = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; w++) o += part[w][t];
+        for (int w = 0; w < NW; w++) o += part2[w][t];
         out[(size_t)b * chunk + h * kDk + c0 + t] = o * invq;
+        // v window: shift left, append the new input
+        *reinterpret_cast<float4 *>(cs + (size_t)chv * kKsize) = make_float4(winv.y, winv.z, winv.w, xvin);
     }
-    if (count && last_slice) {
-        // q / k windows: shift left, append the new input (deltanet_cache.rs:34-42)
-#pragma unroll
-        for (int j = 0; j < QK; j++)
-            *reinterpret_cast<float4 *>(cs + (size_t)ch[j] * kKsize) = make_float4(win[j].y, win[j].z, win[j].w, xin[j]);
-        if (t == 0) __hip_atomic_store(count + (size_t)b * n_heads + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (COUNT && old == gridDim.x - 1) {
+        // q / k window: shift left, append the new input (deltanet_cache.rs:34-42)
+        *reinterpret_cast<float4 *>(cs + (size_t)ch * kKsize) = make_float4(win.y, win.z, win.w, xin);
+        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -767,19 +739,27 @@ int launch_deltanet_step(anehip_ctx *ctx, hipStream_t stream, int batch, int n_h
                          const float *dt_bias, float *conv_state, float *S, float *out, uint32_t *count) {
     const int kp = max(mix.kp, max(beta.kp, alpha.kp));
     if (kp > 16) return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_step: %d K splits (at most 16)", kp);
-    // 32 value columns per 4-wave workgroup (64 workgroups at batch 1; 16
-    // columns: 6.84 us per step, 8 columns in one wave: 7.29 us, against 6.40)
-    constexpr int NQ = 8;
-    const dim3 grid(kDk / (4 * NQ), n_heads, batch), block(32 * NQ);
-#define DN_STEP(KP)                                                                                                  \
-    hipLaunchKernelGGL((deltanet_step_kernel<KP, NQ>), grid, block, 0, stream, mix, beta, alpha, conv_w, ssm_a,      \
+    if (count && (size_t)batch * n_heads * 256 > (size_t)kDnCounters)
+        return set_error(ctx->err, ANEHIP_EINVAL, "deltanet_step: %d x %d heads exceed the window counters", batch,
+                         n_heads);
+    // 32 value columns per 4-wave workgroup (64 workgroups at batch 1)
+    const dim3 grid(kDk / 32, n_heads, batch), block(256);
+#define DN_STEP(KP, C)                                                                                               \
+    hipLaunchKernelGGL((deltanet_step_kernel<KP, C>), grid, block, 0, stream, mix, beta, alpha, conv_w, ssm_a,       \
                        dt_bias, conv_state, S, out, n_heads, count)
-    if (kp <= 1)
-        DN_STEP(1);
-    else if (kp <= 4)
-        DN_STEP(4);
-    else
-        DN_STEP(16);
+#define DN_STEP_KP(C)                                                                                                \
+    if (kp <= 1)                                                                                                     \
+        DN_STEP(1, C);                                                                                               \
+    else if (kp <= 4)                                                                                                \
+        DN_STEP(4, C);                                                                                               \
+    else                                                                                                             \
+        DN_STEP(16, C)
+    if (count) {
+        DN_STEP_KP(true);
+    } else {
+        DN_STEP_KP(false);
+    }
+#undef DN_STEP_KP
 #undef DN_STEP
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
