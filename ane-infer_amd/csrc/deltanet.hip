@@ -209,19 +209,21 @@ __global__ __launch_bounds__(256) void deltanet_step_kernel(
     }
     so = wave_cols(so);
     if (lane < NQ) *reinterpret_cast<float4 *>(&part2[wave][4 * cq]) = so;
+    // the window stores go out before the last barrier (issued at the end
+    // they would lengthen the tail by their own latency)
+    if (COUNT && old == gridDim.x - 1) {
+        // q / k window: shift left, append the new input (deltanet_cache.rs:34-42)
+        *reinterpret_cast<float4 *>(cs + (size_t)ch * kKsize) = make_float4(win.y, win.z, win.w, xin);
+        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // v window: shift left, append the new input
+    if (t < COLS) *reinterpret_cast<float4 *>(cs + (size_t)chv * kKsize) = make_float4(winv.y, winv.z, winv.w, xvin);
     __syncthreads();
     if (t < COLS) {
         float o = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) o += part2[w][t];
         out[(size_t)b * chunk + h * kDk + c0 + t] = o * invq;
-        // v window: shift left, append the new input
-        *reinterpret_cast<float4 *>(cs + (size_t)chv * kKsize) = make_float4(winv.y, winv.z, winv.w, xvin);
-    }
-    if (COUNT && old == gridDim.x - 1) {
-        // q / k window: shift left, append the new input (deltanet_cache.rs:34-42)
-        *reinterpret_cast<float4 *>(cs + (size_t)ch * kKsize) = make_float4(win.y, win.z, win.w, xin);
-        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
