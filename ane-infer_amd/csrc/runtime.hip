@@ -242,17 +242,18 @@ int anehip_quant_gemm_packed(anehip_ctx *ctx, uint32_t ggml_type, const void *wp
     // batch > 32: one 32-row group of planes per 32 rows (the prefill GEMM)
     const size_t groups = (batch + 31) / 32;
     const size_t count = (size_t)batch * m, xcount = groups * xf_plane_len(n);
-    // Splits of at most 2 panels (512 columns) take the x-stationary kernels
-    // on the fp32 rows, which split them into hi / lo fragments in each
-    // workgroup; wider splits (lm_head: one split of 8 panels) first split x
-    // into planes with one launch, since every workgroup of a wide split would
-    // read and split the whole row.  Measured on MI355X (graphs of
-    // back-to-back calls): lm_head 151936 x 2048 at batch 4 / 16 / 32
-    // 64.8 / 72.4 / 82.5 us on the rows against 61.9 / 66.3 / 75.0 us split
-    // first; 6144 x 2048 and 2048 x 6144 (2-panel splits) 9.2-14.5 us on the
-    // rows against 0.2-1.4 us more split first.
+    // The x-stationary kernels read the fp32 rows themselves and split them
+    // into hi / lo fragments in each workgroup: at batch <= 16 (gemm_xs16)
+    // and for splits of at most 2 panels.  Wider splits at batch 17-32
+    // (lm_head: one split of 8 panels on gemm_xsh, whose 8 waves each split
+    // a quarter of the row) first split x into planes with one launch.
+    // Measured on MI355X (graphs of back-to-back calls, weights rotated):
+    // lm_head 151936 x 2048 at batch 4 / 16 / 32 57.1-57.3 / 63.6-65.7 /
+    // 72.9-74.2 us on the rows against 59.2-62.1 / 64.5-66.4 / 71.4-74.1 us
+    // split first; 6144 x 2048 and 2048 x 6144 (2-panel splits) 9.2-14.5 us on
+    // the rows against 0.2-1.4 us more split first.
     const int nsb = (int)(n / 256);
-    if (batch <= 32 && gemm_is_xs(ctx, m, n, batch) && nsb / ksplit <= 2) {
+    if (batch <= 32 && gemm_is_xs(ctx, m, n, batch) && (batch <= 16 || nsb / ksplit <= 2)) {
         // the x-stationary kernels read the fp32 rows themselves: partials, then their sum
         if (ksplit == 1) return launch_gemm_xs_rows(ctx, ctx->stream, ggml_type, wp, m, n, x, batch, y);
         int rc = ensure_workspace(ctx, (size_t)ksplit * count);

@@ -202,10 +202,11 @@ def test_packed_gemm_tall(gpu_ctx, oracle_lib, t, batch, m, n):
                                          (2, 65600, 1024, 5)])
 def test_packed_gemm_many_tiles(gpu_ctx, oracle_lib, t, m, n, batch):
     """Matrices of at least 4 row tiles per CU: lm_head unsplit on the 16-wide
-    x-stationary kernel with 8 panels per workgroup at batch <= 16, and at
-    batch 32 in two K splits of 4 panels on the 8-wave kernel (gemm_xsh, 2
-    panels per wave); n = 1024 (4 panels, unsplit at batch <= 16) with a
-    ragged last tile.  Checked on the first, a middle and the last batch row."""
+    x-stationary kernel with 8 panels per workgroup at batch <= 16 (splitting
+    the fp32 rows itself), and at batch 17-32 unsplit on the 8-wave kernel
+    (gemm_xsh, 4 panels per wave, after a planes launch); n = 1024 (4
+    panels, unsplit at batch <= 16) with a ragged last tile.  Checked on the
+    first, a middle and the last batch row."""
     w = oracle_lib.gen_quant(t, 6, 6 + m % 7, m, n, std=0.02)
     x = oracle_lib.normal(6, 7 + batch, batch * n).reshape(batch, n)
     dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
@@ -281,6 +282,26 @@ def test_packed_gemm_input_range(gpu_ctx, oracle_lib, t, batch, m, n):
     32 rows on gemm_tall (range-safe planes, per-row scaling over the split)."""
     w = oracle_lib.gen_quant(t, 55, m + n + t, m, n, std=0.02)
     x = extreme_rows(oracle_lib, batch, n, 500 + batch)
+    dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
+    dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(batch * m * 4)
+    gpu_ctx.call("quant_gemm_packed", t, dp, m, n, dx, batch, dy)
+    y = dy.download(np.float32, batch * m).reshape(batch, m)
+    check_extreme(y, x, w, t, m, n, oracle_lib)
+    for b in (dw, dp, dx, dy):
+        b.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("batch", [5, 16, 24])
+def test_packed_gemm_many_tiles_input_range(gpu_ctx, oracle_lib, t, batch):
+    """The extreme rows of the test above on a matrix of at least 4 row tiles
+    per CU (65600 x 2048: one split of 8 panels): at batch <= 16 the 16-wide
+    kernel splits the fp32 rows itself over all 8 panels, at batch 24 the
+    8-wave kernel reads range-safe planes."""
+    m, n = 65600, 2048
+    w = oracle_lib.gen_quant(t, 57, 11 + t, m, n, std=0.02)
+    x = extreme_rows(oracle_lib, batch, n, 700 + batch)
     dw, dp, _ = _pack(gpu_ctx, t, w, m, n)
     dx, dy = gpu_ctx.to_device(x), gpu_ctx.alloc(batch * m * 4)
     gpu_ctx.call("quant_gemm_packed", t, dp, m, n, dx, batch, dy)
