@@ -1208,30 +1208,38 @@ __global__ __launch_bounds__(kWave *kPackedWaves) void dn_ssm_kernel(const uint8
 }
 
 // Batch-1 GEMV of a matrix with few row tiles, in one launch: a workgroup of
-// 16 waves takes R = 64 / H rows of one tile over the whole K range, so the
+// NW waves takes R = 64 / H rows of one tile over the whole K range, so the
 // grid has tiles * H workgroups and no K split (no partial sums, no second
 // launch).  Lane l serves row l % R of the workgroup's rows and slot
-// wave * H + l / R; slot s takes the row's Q8_0 / Q4_0 blocks s, s + 16 H,
-// ... (J of them: 8 n / 256 = 16 H J), whole blocks with their scales, every
+// wave * H + l / R; slot s takes the row's Q8_0 / Q4_0 blocks s, s + NW H,
+// ... (J of them: 8 n / 256 = NW H J), whole blocks with their scales, every
 // load issued before any is used.  x is staged in LDS (its loads issued
 // before the weights', so waiting for them does not wait for the weights) as
 // int8 digits (put_digits).  Per lane: block sums in block order, each scaled
 // (q8_gemv.rs:234-242); then the H slots of a row held by one wave are added
-// by lane exchanges and the 16 waves' sums through LDS in wave order.
-// (8 waves of 8 rows, H = 8, measured 5.06 us against 4.95 at 6144 x 2048.)
+// by lane exchanges and the NW waves' sums through LDS in wave order.
+// Two forms: 16 waves with H = 4 (or 2), and 8 waves with H = 8 for
+// matrices whose tiles x 4 would leave CUs idle.  Measured on MI355X (graphs
+// of back-to-back launches, weights rotated, two boxes): 6144 x 2048 5.07 us
+// (16 waves, H 4, 384 workgroups) against 5.43 (8 waves, H 8); 2048 x 6144
+// 5.81-5.96 (8 waves, H 8, 256 workgroups) against 6.31-7.01 (16 waves, H 4,
+// 128); 2048 x 2048 3.51 against 3.66-3.70; 4 waves of 4 rows (H 16)
+// 8.4-9.0 us.
 constexpr int kRowsWaves = 16;
+constexpr int rows_waves(int H) { return H == 8 ? 8 : kRowsWaves; }
 // blocks per lane slot of gemv_rows for n = 256 nsb columns and row split H
 // (0 if they do not divide evenly)
 inline int rows_blocks_per_slot(int nsb, int H) {
-    const int slots = kRowsWaves * H;
+    const int slots = rows_waves(H) * H;
     return (8 * nsb) % slots ? 0 : 8 * nsb / slots;
 }
 constexpr int kRowsMaxN = 8192;
 
 template <uint32_t T, int H, int J>
-__global__ __launch_bounds__(kWave *kRowsWaves) void gemv_rows(const uint8_t *__restrict__ Wp, const float *__restrict__ x,
-                                                       float *__restrict__ y, int m, int n) {
-    constexpr int NW = kRowsWaves, R = kWave / H, SLOTS = NW * H, NT = kWave * NW;
+__global__ __launch_bounds__(kWave *rows_waves(H)) void gemv_rows(const uint8_t *__restrict__ Wp,
+                                                                 const float *__restrict__ x, float *__restrict__ y,
+                                                                 int m, int n) {
+    constexpr int NW = rows_waves(H), R = kWave / H, SLOTS = NW * H, NT = kWave * NW;
     constexpr int VB = T == ANEHIP_GGML_Q8_0 ? 2 : 1;  // 16-byte quant vectors per block
     constexpr int XV = kRowsMaxN / 4 / NT;              // float4 of x per thread, at most
     __shared__ __align__(16) uint32_t xd[kRowsMaxN / 32 * kXdWords];
@@ -3392,18 +3400,24 @@ int dispatch_packed(anehip_ctx *ctx, hipStream_t s, const void *w, uint32_t m, u
     }
 }
 
-// The row split of gemv_rows for an m x n matrix: H row groups per tile (4,
-// else 2; J = n / (512 H) blocks per slot, 1 <= J <= 4) when the grid gets
-// at least half as many workgroups as CUs; 0 when gemv_rows does not apply
-// (matrices the split GEMV covers with row tiles alone keep it).  Measured on
-// MI355X at batch 1, in graphs of back-to-back launches, against the K split
-// plus its summing launch: 6144 x 2048 5.1 us (H 4) / 5.2 (H 2) against 7.0;
-// 2048 x 2048 3.8 (4) / 4.5 (2) against 6.0; 2048 x 6144 7.5 (4) against 7.9.
+// The row split of gemv_rows for an m x n matrix: H row groups per tile
+// (J = 8 n / 256 / (waves x H) blocks per slot, 1 <= J <= 4): 4 on 16 waves
+// when that fills the CUs, else 8 on 8 waves, else 4 or 2 on 16 waves, when
+// the grid gets at least half as many workgroups as CUs; 0 when gemv_rows
+// does not apply (matrices the split GEMV covers with row tiles alone keep
+// it).  Measured on MI355X at batch 1, in graphs of back-to-back launches,
+// against the K split plus its summing launch: 6144 x 2048 5.1 us (H 4) /
+// 5.2 (H 2) against 7.0; 2048 x 2048 3.8 (4) / 4.5 (2) against 6.0; 2048 x
+// 6144 7.5 (4) against 7.9.
 int gemv_rows_split(const anehip_ctx *ctx, uint32_t m, uint32_t n) {
     if (n % 256 || n > (uint32_t)kRowsMaxN) return 0;
     const int nsb = (int)(n / 256), tiles = (int)((m + kWave - 1) / kWave);
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     if (gemv_packed_ksplit(ctx, m, n) == 1) return 0;
+    for (int H : {4, 8}) {
+        const int J = rows_blocks_per_slot(nsb, H);
+        if (J >= 1 && J <= 4 && tiles * H >= cus) return H;
+    }
     for (int H : {4, 2}) {
         const int J = rows_blocks_per_slot(nsb, H);
         if (J < 1 || J > 4) continue;
@@ -3417,7 +3431,7 @@ int launch_rows_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m
                   float *y, int H) {
     const int tiles = (int)((m + kWave - 1) / kWave), J = rows_blocks_per_slot((int)(n / 256), H);
     const uint8_t *wb = static_cast<const uint8_t *>(w);
-    const dim3 grid(tiles * H), block(kWave * kRowsWaves);
+    const dim3 grid(tiles * H), block(kWave * rows_waves(H));
 #define ANEHIP_ROWS(HH, JJ) hipLaunchKernelGGL((gemv_rows<T, HH, JJ>), grid, block, 0, stream, wb, x, y, (int)m, (int)n)
     if (H == 2) {
         switch (J) {
@@ -3433,6 +3447,14 @@ int launch_rows_t(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m
             case 2: ANEHIP_ROWS(4, 2); break;
             case 3: ANEHIP_ROWS(4, 3); break;
             case 4: ANEHIP_ROWS(4, 4); break;
+            default: return set_error(ctx->err, ANEHIP_EINVAL, "gemv_rows: %d blocks per slot", J);
+        }
+    } else if (H == 8) {
+        switch (J) {
+            case 1: ANEHIP_ROWS(8, 1); break;
+            case 2: ANEHIP_ROWS(8, 2); break;
+            case 3: ANEHIP_ROWS(8, 3); break;
+            case 4: ANEHIP_ROWS(8, 4); break;
             default: return set_error(ctx->err, ANEHIP_EINVAL, "gemv_rows: %d blocks per slot", J);
         }
     } else {
