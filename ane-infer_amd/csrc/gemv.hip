@@ -2883,6 +2883,114 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void quant_gemm_mfma(const uint
             }
 }
 
+// x-stationary form of quant_gemm_mfma for matrices of many row tiles at
+// batch 2..16 (lm_head): 8 waves per workgroup, wave w holds the x fragments
+// (hi + lo, brought to one exponent per batch row over the split's 16
+// groups, as quant_gemm_mfma) of super-block ks * 8 + w in registers, and
+// the workgroup walks the row tiles t = blockIdx.x, + gridDim.x, ...  Per
+// tile each wave stages its 64 rows x 1 super-block of GGUF blocks through
+// its own LDS slice and issues the next tile's loads at once (in flight
+// while this tile is multiplied), then the 8 waves' sums are added through
+// LDS (the staging area, after a barrier).  The x fragments are loaded once
+// per workgroup instead of once per tile (lm_head at batch 16: 2374 tiles x
+// 128 KiB of x from L2 otherwise).  grid = (workgroups per split, K splits
+// of 8 super-blocks); output as quant_gemm_mfma.
+template <uint32_t T>
+__global__ __launch_bounds__(512) void quant_gemm_xs(const uint8_t *__restrict__ W, Planes xp, float *__restrict__ out,
+                                                     int m, int n, int batch, size_t split_stride) {
+    constexpr int V = QTraits<T>::kSbVec;
+    constexpr int NW = 8;
+    constexpr int kSegWords = QTraits<T>::kSbBytes / 4;
+    constexpr int RED = 16;  // sums per lane: [row group rs][element r]
+    static_assert(NW * RED * kWave * 4 <= NW * V * kWave * 16, "the reduction fits the staging area");
+    __shared__ u32x4 lds[NW][V * kWave];
+    __shared__ int xeE[16];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int G = gridDim.x, ks = blockIdx.y;
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
+    const uint32_t row_bytes = (uint32_t)nsb * QTraits<T>::kSbBytes;
+    const int sb = ks * NW + wave;
+    const int li = lane & 15, g = lane >> 4;
+    int t = blockIdx.x;
+    if (t >= tiles) return;  // uniform
+    // chunk c = 64 j + lane of a tile's super-block column: (row c / V, part
+    // c % V), rows past m clamped to the last row (never stored)
+    u32x4 regs[V];
+    auto issue = [&](int tt) {
+        const int rows_left = m - tt * kWave;
+        const uint8_t *base = W + (size_t)tt * kWave * row_bytes + (size_t)sb * QTraits<T>::kSbBytes;
+#pragma unroll
+        for (int j = 0; j < V; j++) {
+            const int c = j * kWave + lane;
+            const uint32_t o = (uint32_t)min(c / V, rows_left - 1) * row_bytes + (uint32_t)(c % V) * 16u;
+            regs[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + o));
+        }
+    };
+    issue(t);
+    // A fragments x[b = li][sb * 256 + 32 blk + 8 g + e] (rows past the batch
+    // read row batch - 1; their outputs are never stored), loaded after the
+    // first tile's weights were issued
+    h8v ah[8], al[8];
+    {
+        const int b = min(li, batch - 1);
+        const int En = xe_max(xp.xe, b, 2 * ks * NW, 2 * NW, n);
+        if (wave == 0 && g == 0) xeE[li] = En;
+        const int8_t *e = xp.xe + (size_t)b * xe_stride(n) + 2 * sb;
+        const _Float16 f0 = xe_factor(e[0], En), f1 = xe_factor(e[1], En);
+#pragma unroll
+        for (int blk = 0; blk < 8; blk++) {
+            const size_t xo = (size_t)b * n + (size_t)sb * 256 + 32 * blk + 8 * g;
+            const _Float16 f = blk < 4 ? f0 : f1;
+            ah[blk] = *reinterpret_cast<const h8v *>(xp.hi + xo) * f;
+            al[blk] = *reinterpret_cast<const h8v *>(xp.lo + xo) * f;
+        }
+    }
+    const uint32_t *lw = reinterpret_cast<const uint32_t *>(lds[wave]);
+    float *red = reinterpret_cast<float *>(&lds[0][0]);  // [wave][RED][lane], after the tile's barrier
+    float *dst = out + (size_t)ks * split_stride;
+    for (; t < tiles; t += G) {
+        stage_tile<T>(regs, lds[wave], lane);
+        if (t + G < tiles) issue(t + G);
+        f32x4 acc[4];
+#pragma unroll
+        for (int rs = 0; rs < 4; rs++) acc[rs] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int blk = 0; blk < 8; blk++) {
+#pragma unroll
+            for (int rs = 0; rs < 4; rs++) {
+                const uint32_t *wl = lw + (rs * 16 + li) * kSegWords;
+                const h8v bw = (blk & 1) ? w_frag<T, 1>(wl, blk, g) : w_frag<T, 0>(wl, blk, g);
+                const float d = blk_scale<T>(wl, blk);
+                f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[blk], bw, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[blk], bw, c, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[rs][r] = fmaf(c[r], d, acc[rs][r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one block's weight fragments live at a time
+        }
+        __syncthreads();  // every wave is done with its slice
+#pragma unroll
+        for (int rs = 0; rs < 4; rs++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[(wave * RED + rs * 4 + r) * kWave + lane] = acc[rs][r];
+        __syncthreads();
+        // outputs (tile row rs * 16 + l % 16, batch row 4 (l / 16) + r), the
+        // 8 waves added in wave order
+#pragma unroll
+        for (int k = 0; k < RED * kWave / 512; k++) {
+            const int o = (int)threadIdx.x + 512 * k;
+            const int idx = o >> 6, l = o & 63;
+            float s = red[idx * kWave + l];
+#pragma unroll
+            for (int w = 1; w < NW; w++) s += red[(w * RED + idx) * kWave + l];
+            const int row = t * kWave + (idx >> 2) * 16 + (l & 15), b = 4 * (l >> 4) + (idx & 3);
+            if (row < m && b < batch) dst[(size_t)b * m + row] = ldexpf(s, xeE[b]);
+        }
+        __syncthreads();  // the staging area is free again
+    }
+}
+
 // y[i] = sum over k of part[k][i], k ascending (deterministic).
 __global__ __launch_bounds__(256) void sum_partials(const float *__restrict__ part, float *__restrict__ y,
                                                    size_t count, int ksplit) {
@@ -2969,7 +3077,19 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
     hipLaunchKernelGGL(split_x_kernel, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0, stream, x, xp, (int)batch,
                        (int)n);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-    if (batch <= 16) return launch_mfma<T, 1>(ctx, stream, w, m, n, xp, batch, out, split_stride, ksplit);
+    if (batch <= 16) {
+        // many row tiles, K splits of 8 super-blocks: the x-stationary form
+        // (lm_head 151936 x 2048 at batch 4 / 16: 75.6-77.2 / 80.1-82.9 us
+        // against 95.8-102.8 / 104.7-113.5 us, graphs of back-to-back launches)
+        const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+        if ((int)(n / 256) == 8 * ksplit && tiles >= 4 * cus) {
+            hipLaunchKernelGGL((quant_gemm_xs<T>), dim3(min(tiles, cus), ksplit), dim3(512), 0, stream,
+                               static_cast<const uint8_t *>(w), xp, out, (int)m, (int)n, (int)batch, split_stride);
+            ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+            return ANEHIP_OK;
+        }
+        return launch_mfma<T, 1>(ctx, stream, w, m, n, xp, batch, out, split_stride, ksplit);
+    }
     // 17..32 rows: a matrix that stays in the 256 MiB MALL takes two 16-row
     // passes (the second reads the weights from the MALL), a larger one the
     // 32-row kernel.  Measured on MI355X (graphs of back-to-back launches):

@@ -85,6 +85,36 @@ def test_small_batch_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
     assert l2 <= TOL and mx <= TOL
 
 
+@pytest.mark.parametrize("t", [8, 2])
+@pytest.mark.parametrize("m,batch", [(151936, 2), (151936, 16), (65570, 9)])
+def test_gguf_gemm_many_tiles(gpu_ctx, oracle_lib, t, m, batch):
+    """GGUF-layout GEMM at batch 2..16 on matrices of at least 4 row tiles per
+    CU: the x-stationary kernel (8 waves, one super-block's x fragments each,
+    the workgroup walking the row tiles); 65570 rows end in a ragged tile of
+    34 rows.  First, middle and last batch rows against the oracle."""
+    n = 2048
+    w = oracle_lib.gen_quant(t, 21, m % 97 + t, m, n, std=0.02)
+    x = oracle_lib.normal(21, 300 + batch, batch * n).reshape(batch, n)
+    y = _run(gpu_ctx, t, w, m, n, x)
+    for b in sorted({0, batch // 2, batch - 1}):
+        l2, mx = rel_errs(y[b], oracle_lib.gemv(t, w, m, n, x[b]))
+        print(f"type={t} m={m} batch={batch} row={b}: rel_l2={l2:.2e} rel_max={mx:.2e}", flush=True)
+        assert l2 <= TOL and mx <= TOL
+
+
+@pytest.mark.parametrize("t", [8, 2])
+def test_gguf_gemm_many_tiles_input_range(gpu_ctx, oracle_lib, t):
+    """The x-stationary GGUF-layout kernel on rows far outside fp16's range
+    (the extreme rows of the panel GEMM's range test), 16 rows."""
+    from test_packed_gpu import check_extreme, extreme_rows
+
+    m, n, batch = 65570, 2048, 16
+    w = oracle_lib.gen_quant(t, 23, 5 + t, m, n, std=0.02)
+    x = extreme_rows(oracle_lib, batch, n, 901)
+    y = _run(gpu_ctx, t, w, m, n, x)
+    check_extreme(y, x, w, t, m, n, oracle_lib)
+
+
 def test_gemm_lm_head_batch32(gpu_ctx, oracle_lib):
     m, n, batch = 151936, 2048, 32
     w = oracle_lib.gen_quant(8, 5, 5, m, n, std=0.02)
