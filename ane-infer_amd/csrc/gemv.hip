@@ -2991,6 +2991,119 @@ __global__ __launch_bounds__(512) void quant_gemm_xs(const uint8_t *__restrict__
     }
 }
 
+// The same for batch 17..32: wave w = 4 h + q holds the x fragments of batch
+// rows 16 h .. + 15 for the two super-blocks ks * 8 + 2 q, + 1 (128
+// registers: 32 rows of one super-block would not fit beside the weights in
+// flight at two waves per SIMD) and loads segment 2 q + h of each tile; the
+// pair's two segments are shared through LDS by waves q and q + 4, and each
+// batch half's 4 waves are added per tile.  The lane's load offsets are
+// recomputed per tile (held across the loop they cost 34 registers and the
+// kernel spilled).  lm_head 151936 x 2048 at batch 17 / 32: 126.8-128.0 /
+// 133.4-133.6 us against 134.3-141.8 / 160.3-166.1 us on quant_gemm_mfma<T,
+// 2> (graphs of back-to-back launches).
+template <uint32_t T>
+__global__ __launch_bounds__(512) void quant_gemm_xs32(const uint8_t *__restrict__ W, Planes xp,
+                                                       float *__restrict__ out, int m, int n, int batch,
+                                                       size_t split_stride) {
+    constexpr int V = QTraits<T>::kSbVec;
+    constexpr int kSegWords = QTraits<T>::kSbBytes / 4;
+    constexpr int RED = 16;  // sums per lane: [row group rs][element r]
+    static_assert(8 * RED * kWave * 4 <= 8 * V * kWave * 16, "the reduction fits the staging area");
+    __shared__ u32x4 lds[4][2][V * kWave];
+    __shared__ int xeE[32];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int hh = wave >> 2, q = wave & 3;
+    const int G = gridDim.x, ks = blockIdx.y;
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
+    const uint32_t row_bytes = (uint32_t)nsb * QTraits<T>::kSbBytes;
+    const int sb0 = ks * 8 + 2 * q;
+    const int li = lane & 15, g = lane >> 4;
+    int t = blockIdx.x;
+    if (t >= tiles) return;  // uniform
+    u32x4 regs[V];
+    auto issue = [&](int tt) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));  // not loop-invariant: the offsets are not kept in registers
+        const int rows_left = m - tt * kWave;
+        const uint8_t *base = W + (size_t)tt * kWave * row_bytes + (size_t)(sb0 + hh) * QTraits<T>::kSbBytes;
+#pragma unroll
+        for (int j = 0; j < V; j++) {
+            const int c = j * kWave + ln;
+            const uint32_t o = (uint32_t)min(c / V, rows_left - 1) * row_bytes + (uint32_t)(c % V) * 16u;
+            regs[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + o));
+        }
+    };
+    issue(t);
+    h8v ah[2][8], al[2][8];
+    {
+        const int b = min(li + 16 * hh, batch - 1);
+        const int En = xe_max(xp.xe, b, 2 * ks * 8, 16, n);
+        if (q == 0 && g == 0) xeE[li + 16 * hh] = En;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int8_t *e = xp.xe + (size_t)b * xe_stride(n) + 2 * (sb0 + s);
+            const _Float16 f0 = xe_factor(e[0], En), f1 = xe_factor(e[1], En);
+#pragma unroll
+            for (int blk = 0; blk < 8; blk++) {
+                const size_t xo = (size_t)b * n + (size_t)(sb0 + s) * 256 + 32 * blk + 8 * g;
+                const _Float16 f = blk < 4 ? f0 : f1;
+                ah[s][blk] = *reinterpret_cast<const h8v *>(xp.hi + xo) * f;
+                al[s][blk] = *reinterpret_cast<const h8v *>(xp.lo + xo) * f;
+            }
+        }
+    }
+    float *red = reinterpret_cast<float *>(&lds[0][0][0]);  // [wave][RED][lane], after the tile's barrier
+    float *dst = out + (size_t)ks * split_stride;
+    for (; t < tiles; t += G) {
+#pragma unroll
+        for (int j = 0; j < V; j++) lds[q][hh][j * kWave + lane] = regs[j];
+        __syncthreads();  // both segments of every pair staged
+        if (t + G < tiles) issue(t + G);
+        f32x4 acc[4];
+#pragma unroll
+        for (int rs = 0; rs < 4; rs++) acc[rs] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const uint32_t *lw = reinterpret_cast<const uint32_t *>(lds[q][s]);
+#pragma unroll
+            for (int blk = 0; blk < 8; blk++) {
+#pragma unroll
+                for (int rs = 0; rs < 4; rs++) {
+                    const uint32_t *wl = lw + (rs * 16 + li) * kSegWords;
+                    const h8v bw = (blk & 1) ? w_frag<T, 1>(wl, blk, g) : w_frag<T, 0>(wl, blk, g);
+                    const float d = blk_scale<T>(wl, blk);
+                    f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[s][blk], bw, f32x4{0.f, 0.f, 0.f, 0.f}, 0,
+                                                                     0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[s][blk], bw, c, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[rs][r] = fmaf(c[r], d, acc[rs][r]);
+                    __builtin_amdgcn_sched_barrier(0);  // one weight fragment live at a time
+                }
+            }
+        }
+        __syncthreads();  // every wave is done with the staged segments
+#pragma unroll
+        for (int rs = 0; rs < 4; rs++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[(wave * RED + rs * 4 + r) * kWave + lane] = acc[rs][r];
+        __syncthreads();
+        // output o: batch half h = o / 1024, then (rs, r, lane); the half's 4
+        // waves added in wave order
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int o = (int)threadIdx.x + 512 * k;
+            const int h = o >> 10, idx = (o >> 6) & 15, l = o & 63;
+            float sum = red[((4 * h) * RED + idx) * kWave + l];
+#pragma unroll
+            for (int w = 1; w < 4; w++) sum += red[((4 * h + w) * RED + idx) * kWave + l];
+            const int row = t * kWave + (idx >> 2) * 16 + (l & 15), b = 16 * h + 4 * (l >> 4) + (idx & 3);
+            if (row < m && b < batch) dst[(size_t)b * m + row] = ldexpf(sum, xeE[b]);
+        }
+        __syncthreads();  // the staging area is free again
+    }
+}
+
 // y[i] = sum over k of part[k][i], k ascending (deterministic).
 __global__ __launch_bounds__(256) void sum_partials(const float *__restrict__ part, float *__restrict__ y,
                                                    size_t count, int ksplit) {
@@ -3077,24 +3190,30 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
     hipLaunchKernelGGL(split_x_kernel, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0, stream, x, xp, (int)batch,
                        (int)n);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-    if (batch <= 16) {
-        // many row tiles, K splits of 8 super-blocks: the x-stationary form
-        // (lm_head 151936 x 2048 at batch 4 / 16: 75.6-77.2 / 80.1-82.9 us
-        // against 95.8-102.8 / 104.7-113.5 us, graphs of back-to-back launches)
-        const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-        if ((int)(n / 256) == 8 * ksplit && tiles >= 4 * cus) {
-            hipLaunchKernelGGL((quant_gemm_xs<T>), dim3(min(tiles, cus), ksplit), dim3(512), 0, stream,
-                               static_cast<const uint8_t *>(w), xp, out, (int)m, (int)n, (int)batch, split_stride);
-            ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-            return ANEHIP_OK;
-        }
-        return launch_mfma<T, 1>(ctx, stream, w, m, n, xp, batch, out, split_stride, ksplit);
+    // many row tiles (at least 4 per CU) with K splits of 8 super-blocks: the
+    // x-stationary kernels, one workgroup per CU walking the row tiles with
+    // the split's x in registers (lm_head 151936 x 2048 at batch 4 / 16 / 32:
+    // 75.6-77.2 / 80.1-82.9 / 133.4-133.6 us against 95.8-102.8 / 104.7-113.5
+    // / 160.3-166.1 us on quant_gemm_mfma, graphs of back-to-back launches)
+    const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    if ((int)(n / 256) == 8 * ksplit && tiles >= 4 * cus) {
+        const dim3 grid(min(tiles, cus), ksplit);
+        const uint8_t *wb = static_cast<const uint8_t *>(w);
+        if (batch <= 16)
+            hipLaunchKernelGGL((quant_gemm_xs<T>), grid, dim3(512), 0, stream, wb, xp, out, (int)m, (int)n,
+                               (int)batch, split_stride);
+        else
+            hipLaunchKernelGGL((quant_gemm_xs32<T>), grid, dim3(512), 0, stream, wb, xp, out, (int)m, (int)n,
+                               (int)batch, split_stride);
+        ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+        return ANEHIP_OK;
     }
+    if (batch <= 16) return launch_mfma<T, 1>(ctx, stream, w, m, n, xp, batch, out, split_stride, ksplit);
     // 17..32 rows: a matrix that stays in the 256 MiB MALL takes two 16-row
     // passes (the second reads the weights from the MALL), a larger one the
     // 32-row kernel.  Measured on MI355X (graphs of back-to-back launches):
     // 6144 x 2048 at 32 rows 24.7 us in one 32-row pass against 9.3 us for
-    // one 16-row pass; lm_head 161 us against 105 per 16-row pass.
+    // one 16-row pass.
     if ((double)m * (n / 32) * QTraits<T>::kBlockBytes <= 128.0 * (1 << 20)) {
         int rc = launch_mfma<T, 1>(ctx, stream, w, m, n, xp, 16, out, split_stride, ksplit);
         if (rc) return rc;

@@ -86,12 +86,14 @@ def test_small_batch_gemm_parity(gpu_ctx, oracle_lib, t, batch, m, n):
 
 
 @pytest.mark.parametrize("t", [8, 2])
-@pytest.mark.parametrize("m,batch", [(151936, 2), (151936, 16), (65570, 9)])
+@pytest.mark.parametrize("m,batch", [(151936, 2), (151936, 16), (65570, 9), (151936, 17), (151936, 32), (65570, 24)])
 def test_gguf_gemm_many_tiles(gpu_ctx, oracle_lib, t, m, batch):
-    """GGUF-layout GEMM at batch 2..16 on matrices of at least 4 row tiles per
-    CU: the x-stationary kernel (8 waves, one super-block's x fragments each,
-    the workgroup walking the row tiles); 65570 rows end in a ragged tile of
-    34 rows.  First, middle and last batch rows against the oracle."""
+    """GGUF-layout GEMM at batch 2..32 on matrices of at least 4 row tiles per
+    CU: the x-stationary kernels (8 waves; up to 16 rows one super-block's x
+    fragments per wave, 17-32 rows two super-blocks' for one 16-row half,
+    the pair's weights shared through LDS), the workgroup walking the row
+    tiles; 65570 rows end in a ragged tile of 34 rows.  First, middle and
+    last batch rows against the oracle."""
     n = 2048
     w = oracle_lib.gen_quant(t, 21, m % 97 + t, m, n, std=0.02)
     x = oracle_lib.normal(21, 300 + batch, batch * n).reshape(batch, n)
@@ -103,12 +105,13 @@ def test_gguf_gemm_many_tiles(gpu_ctx, oracle_lib, t, m, batch):
 
 
 @pytest.mark.parametrize("t", [8, 2])
-def test_gguf_gemm_many_tiles_input_range(gpu_ctx, oracle_lib, t):
-    """The x-stationary GGUF-layout kernel on rows far outside fp16's range
-    (the extreme rows of the panel GEMM's range test), 16 rows."""
+@pytest.mark.parametrize("batch", [16, 24])
+def test_gguf_gemm_many_tiles_input_range(gpu_ctx, oracle_lib, t, batch):
+    """The x-stationary GGUF-layout kernels on rows far outside fp16's range
+    (the extreme rows of the panel GEMM's range test), 16 and 24 rows."""
     from test_packed_gpu import check_extreme, extreme_rows
 
-    m, n, batch = 65570, 2048, 16
+    m, n = 65570, 2048
     w = oracle_lib.gen_quant(t, 23, 5 + t, m, n, std=0.02)
     x = extreme_rows(oracle_lib, batch, n, 901)
     y = _run(gpu_ctx, t, w, m, n, x)
