@@ -504,6 +504,78 @@ __global__ __launch_bounds__(kWave *kWavesPerWg) void gemv_fused(const uint8_t *
     out[(size_t)ks * split_stride + row] = sum;
 }
 
+// x-stationary form of gemv_fused (plain input, matrices of many row tiles,
+// K splits of 8 super-blocks): 8 waves per workgroup, wave w takes
+// super-block ks * 8 + w of every row tile t = blockIdx.x, + gridDim.x, ...
+// (staged through its own LDS slice, the next tile's loads issued at once),
+// with the split's x digitised once per workgroup instead of once per tile;
+// the 8 waves' row sums meet in LDS (two buffers, one barrier per tile).
+// lm_head 151936 x 2048 (GGUF layout): 66.0 us against 72.2-72.7 us
+// (graphs of back-to-back launches).
+template <uint32_t T>
+__global__ __launch_bounds__(512) void gemv_fused_xs(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                                     float *__restrict__ out, int m, int n, size_t split_stride) {
+    constexpr int V = QTraits<T>::kSbVec;
+    constexpr int NT = 512;
+    __shared__ u32x4 lds[8][V * kWave];
+    __shared__ __align__(16) float xs[kMaxSliceSb * 256];  // the split's x, then (in place) its digits
+    __shared__ float red[2][8][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int G = gridDim.x, ks = blockIdx.y;
+    const int nsb = n >> 8, tiles = (m + kWave - 1) / kWave;
+    const uint32_t row_bytes = (uint32_t)nsb * QTraits<T>::kSbBytes;
+    const int sb = ks * 8 + wave;
+    int t = blockIdx.x;
+    if (t >= tiles) return;  // uniform
+    u32x4 regs[V];
+    auto issue = [&](int tt) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));  // not loop-invariant: the offsets are not kept in registers
+        const int rows_left = m - tt * kWave;
+        const uint8_t *base = W + (size_t)tt * kWave * row_bytes + (size_t)sb * QTraits<T>::kSbBytes;
+#pragma unroll
+        for (int j = 0; j < V; j++) {
+            const int c = j * kWave + ln;
+            const uint32_t o = (uint32_t)min(c / V, rows_left - 1) * row_bytes + (uint32_t)(c % V) * 16u;
+            regs[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + o));
+        }
+    };
+    issue(t);
+    {
+        constexpr int IT = kMaxSliceSb * 256 / NT;
+        float v[IT];
+#pragma unroll
+        for (int i = 0; i < IT; i++) v[i] = x[(size_t)ks * 2048 + threadIdx.x + NT * i];
+#pragma unroll
+        for (int i = 0; i < IT; i++) xs[threadIdx.x + NT * i] = v[i];
+    }
+    __syncthreads();
+    digitize_lds_inplace<T, NT, kMaxSliceSb * 256>(xs, kMaxSliceSb * 256);
+    __syncthreads();
+    const uint32_t *xd = reinterpret_cast<const uint32_t *>(xs) + wave * 8 * kXdWords;
+    const uint4 *xq = reinterpret_cast<const uint4 *>(xs + kMaxSliceSb * 8 * kXdWords) + wave * 8;
+    const uint32_t *wl = reinterpret_cast<const uint32_t *>(&lds[wave][lane * V]);  // this lane's row
+    float *dst = out + (size_t)ks * split_stride;
+    for (int p = 0; t < tiles; t += G, p ^= 1) {
+        stage_tile<T>(regs, lds[wave], lane);
+        if (t + G < tiles) issue(t + G);
+        const float acc = sb_dot<T>(wl, xd, xq, 0.0f);
+        wave_sync_lds();  // this tile's reads precede the next tile's writes
+        red[p][wave][lane] = acc;
+        __syncthreads();  // red[p] complete; red[p ^ 1] was read before this barrier
+        if (wave == 0) {
+            const int row = t * kWave + lane;
+            if (row < m) {
+                float sum = red[p][0][lane];
+#pragma unroll
+                for (int w = 1; w < 8; w++) sum += red[p][w][lane];
+                dst[row] = sum;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Panel layout.  The decode step keeps its weights in a GPU-native
 // permutation of the GGUF blocks (same bytes, same values), built once at
@@ -3174,7 +3246,19 @@ template <uint32_t T>
 int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m, uint32_t n, const float *x,
                  uint32_t batch, float *out, int ksplit, _Float16 *xsplit) {
     const size_t split_stride = (size_t)batch * m;
+    const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    // many row tiles (at least 4 per CU) with K splits of 8 super-blocks: the
+    // x-stationary kernels, one workgroup per CU walking the row tiles with
+    // the split's x staged once (batch 1: as digits in LDS; batch 2..32: as
+    // MFMA fragments in registers)
+    const bool xs = (int)(n / 256) == 8 * ksplit && tiles >= 4 * cus;
     if (batch == 1) {
+        if (xs) {
+            hipLaunchKernelGGL((gemv_fused_xs<T>), dim3(min(tiles, cus), ksplit), dim3(512), 0, stream,
+                               static_cast<const uint8_t *>(w), x, out, (int)m, (int)n, split_stride);
+            ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+            return ANEHIP_OK;
+        }
         GemvInput in;
         in.x = x;
         return dispatch_fused<T>(ctx, stream, w, m, n, in, out, ksplit);
@@ -3190,13 +3274,10 @@ int dispatch_raw(anehip_ctx *ctx, hipStream_t stream, const void *w, uint32_t m,
     hipLaunchKernelGGL(split_x_kernel, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0, stream, x, xp, (int)batch,
                        (int)n);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
-    // many row tiles (at least 4 per CU) with K splits of 8 super-blocks: the
-    // x-stationary kernels, one workgroup per CU walking the row tiles with
-    // the split's x in registers (lm_head 151936 x 2048 at batch 4 / 16 / 32:
-    // 75.6-77.2 / 80.1-82.9 / 133.4-133.6 us against 95.8-102.8 / 104.7-113.5
-    // / 160.3-166.1 us on quant_gemm_mfma, graphs of back-to-back launches)
-    const int tiles = (int)((m + kWave - 1) / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    if ((int)(n / 256) == 8 * ksplit && tiles >= 4 * cus) {
+    // (lm_head 151936 x 2048 at batch 4 / 16 / 32: 75.6-77.2 / 80.1-82.9 /
+    // 133.4-133.6 us against 95.8-102.8 / 104.7-113.5 / 160.3-166.1 us on
+    // quant_gemm_mfma, graphs of back-to-back launches)
+    if (xs) {
         const dim3 grid(min(tiles, cus), ksplit);
         const uint8_t *wb = static_cast<const uint8_t *>(w);
         if (batch <= 16)

@@ -118,6 +118,21 @@ def test_gguf_gemm_many_tiles_input_range(gpu_ctx, oracle_lib, t, batch):
     check_extreme(y, x, w, t, m, n, oracle_lib)
 
 
+@pytest.mark.parametrize("t", [8, 2])
+def test_gguf_gemv_many_tiles_input_range(gpu_ctx, oracle_lib, t):
+    """Batch 1 on a GGUF-layout matrix of at least 4 row tiles per CU (the
+    x-stationary GEMV: x as int8 digits with a power-of-two exponent per
+    32-block, digitised once per workgroup): each kind of extreme row as its
+    own call, against the oracle; 65570 rows end in a ragged tile."""
+    from test_packed_gpu import check_extreme, extreme_rows
+
+    m, n = 65570, 2048
+    w = oracle_lib.gen_quant(t, 29, 3 + t, m, n, std=0.02)
+    x = extreme_rows(oracle_lib, 8, n, 903)
+    y = np.stack([_run(gpu_ctx, t, w, m, n, x[b][None])[0] for b in range(x.shape[0])])
+    check_extreme(y, x, w, t, m, n, oracle_lib)
+
+
 def test_gemm_lm_head_batch32(gpu_ctx, oracle_lib):
     m, n, batch = 151936, 2048, 32
     w = oracle_lib.gen_quant(8, 5, 5, m, n, std=0.02)
