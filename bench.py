@@ -27,7 +27,9 @@ step where 18 layers' states stream).
 step (24 layers, fp16 KV cache) at batch 1 and 32 and context 1k / 8k / 32k,
 as tokens/s of greedy decoding with on-device token feedback (one captured
 hipGraph per step); the `_cap32768` points run a 32k-position cache at a live
-length of 1k / 8k (the attention work follows the live length).
+length of 1k / 8k (the attention work follows the live length).  `decode_q4`
+is the same model shape with Q4_0 weights on every linear layer (configs[2]'s
+quantisation) at batch 1 and 32, context 1k.
 
 Timing: HIP events recorded on the library's own stream (anehip_timer_*),
 around exactly `--steps` steps after `--warmup` untimed steps, with a stream
@@ -59,6 +61,7 @@ BLOCK_BYTES = {Q8: 34, Q4: 18}
 # (batch, live context, cache capacity)
 DECODE_POINTS = [(1, 1024, 1024), (1, 8192, 8192), (1, 32768, 32768), (32, 1024, 1024), (32, 8192, 8192),
                  (32, 32768, 32768), (1, 1024, 32768), (1, 8192, 32768), (32, 1024, 32768), (32, 8192, 32768)]
+DECODE_Q4_POINTS = [(1, 1024, 1024), (32, 1024, 1024)]
 # algorithmic bytes of one decode step: every weight once, KV rows read, DeltaNet
 # state read + written (S and the 4-wide conv window), per sequence
 DECODE_WEIGHT_BYTES = 18 * 62_459_904 + 6 * 55_705_600 + 330_612_736
@@ -118,6 +121,7 @@ def parse():
                     help="only run decode points, e.g. '1:1024,32:1024:32768' (batch:ctx[:capacity]), and print "
                          "their line")
     ap.add_argument("--deltanet-only", action="store_true", help="only run the configs[3] DeltaNet leg")
+    ap.add_argument("--q4", action="store_true", help="with --decode-only: Q4_0 weights")
     ap.add_argument("--profile-c0", action="store_true",
                     help="only run the configs[0] GEMV, the streaming-read floor and the empty kernel (for rocprofv3)")
     ap.add_argument("--profile-b1-floors", action="store_true",
@@ -205,12 +209,21 @@ def time_point(ctx, s, batch, launches, gguf=False):
     return ms / launches
 
 
-def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
+def decode_weight_bytes(anehip, spec, ggml_type):
+    """Bytes of every quantised weight of the model (read once per step)."""
+    per_block = BLOCK_BYTES[ggml_type]
+    return sum(rows * cols // 32 * per_block for layer in [-1] + list(range(spec.n_layers))
+               for rows, cols, quant in spec.shapes(layer).values() if quant)
+
+
+def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0, ggml_type=Q8):
     """Greedy decode tok/s of the random-init Qwen3.5-2B shape at each
-    (batch, live context, cache capacity)."""
+    (batch, live context, cache capacity), Q8_0 (or Q4_0) weights."""
     spec = anehip.Spec()
     gm = anehip.Model(spec)
-    gm.randomize(seed=1)
+    gm.randomize(seed=1, ggml_type=ggml_type)
+    weight_bytes = decode_weight_bytes(anehip, spec, ggml_type)
+    assert ggml_type != Q8 or weight_bytes == DECODE_WEIGHT_BYTES
     out = {}
     for batch, ctx_len, cap in points:
         gm.alloc_state(batch, cap)
@@ -234,7 +247,7 @@ def bench_decode(anehip, steps, warmup, points=DECODE_POINTS, prefill_tokens=0):
         gm.generate(toks, steps)
         ms = gm.timer_stop()
         step_ms = ms / steps
-        step_bytes = DECODE_WEIGHT_BYTES + batch * (ctx_len * KV_BYTES_PER_POS + DN_STATE_BYTES)
+        step_bytes = weight_bytes + batch * (ctx_len * KV_BYTES_PER_POS + DN_STATE_BYTES)
         key = f"B{batch}_ctx{ctx_len}" + (f"_cap{cap}" if cap != ctx_len else "")
         out[key] = {
             "tok_s": round(batch * steps / (ms * 1e-3), 1),
@@ -620,7 +633,9 @@ def main():
         for p in args.decode_only.split(","):
             v = [int(t) for t in p.split(":")]
             pts.append((v[0], v[1], v[2] if len(v) > 2 else v[1]))
-        print(json.dumps({"decode": bench_decode(anehip, args.decode_steps, 3, pts)}), flush=True)
+        qt = Q4 if args.q4 else Q8
+        print(json.dumps({"decode_q4" if args.q4 else "decode": bench_decode(anehip, args.decode_steps, 3, pts,
+                                                                             ggml_type=qt)}), flush=True)
         return
     if args.prefill_only:
         print(json.dumps({"decode": bench_decode(anehip, args.decode_steps, 3, [],
@@ -753,6 +768,8 @@ def main():
     out["configs3_deltanet"] = bench_deltanet(anehip, ctx)
     if not args.no_decode:
         out["decode"] = bench_decode(anehip, args.decode_steps, 3, prefill_tokens=(512, 2048))
+        # the same model shape with Q4_0 weights (configs[2]'s quantisation on every linear layer)
+        out["decode_q4"] = bench_decode(anehip, args.decode_steps, 3, DECODE_Q4_POINTS, ggml_type=Q4)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(anehip, ctx, shapes, args.cpu_seconds, decode=not args.no_decode)
     ctx.close()

@@ -442,6 +442,24 @@ def test_qwen35_2b_shape_step(big_host, ctx_len, batch):
     gm.close()
 
 
+@pytest.fixture(scope="module")
+def big_host_q4():
+    return HostModel(anehip.Spec(), seed=12, ggml_type=2)
+
+
+@pytest.mark.parametrize("batch", [1, 32])
+def test_qwen35_2b_shape_q4_0_step(big_host_q4, batch):
+    """The 2B shape with Q4_0 weights on every linear layer (the model the
+    bench's decode_q4 times): one step at pos 1023 (cache capacity 1024) vs
+    the oracle, sequences 0 and batch - 1: logits, then the DeltaNet states
+    and conv windows."""
+    gm = _model(big_host_q4, batch, 1024)
+    _fill_state(gm, big_host_q4.spec, seed=3)
+    _step_vs_oracle(big_host_q4, gm, [1023] * batch, sorted({0, batch - 1}), 15, label=f"2B Q4_0 B={batch}",
+                    dn_state=True)
+    gm.close()
+
+
 @pytest.mark.parametrize("batch,positions,check", [
     (1, [1023], [0]),
     (1, [8191], [0]),
