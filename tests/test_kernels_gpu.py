@@ -68,6 +68,43 @@ def test_deltanet_256_steps_state_parity(gpu_ctx, oracle_lib, batch):
         buf.free()
 
 
+def test_deltanet_many_heads_batch1(gpu_ctx, oracle_lib):
+    """Batch 1 with more heads than the in-kernel window commit has counters
+    for (256 per head, 65536 in all): the step kernel without counters, then
+    the window-commit launch.  260 heads, 4 steps: outputs every step, S and
+    the conv windows (bit-exact) after the last, against the oracle."""
+    h = 260
+    ch = 3 * h * DK
+    seed = 77
+    conv_w = oracle_lib.normal(seed, 1, ch * 4, std=0.5)
+    ssm_a = -oracle_lib.uniform(seed, 2, h)
+    dt_bias = oracle_lib.normal(seed, 3, h)
+    S0 = oracle_lib.normal(seed, 4, h * DK * DK, std=0.01)
+    win0 = oracle_lib.normal(seed, 5, ch * 4)
+    o_S, o_cs = S0.copy(), win0.copy()
+    d_S, d_cs = gpu_ctx.to_device(S0), gpu_ctx.to_device(win0)
+    d_cw, d_a, d_dt = gpu_ctx.to_device(conv_w), gpu_ctx.to_device(ssm_a), gpu_ctx.to_device(dt_bias)
+    d_qkv, d_b, d_al = gpu_ctx.alloc(ch * 4), gpu_ctx.alloc(h * 4), gpu_ctx.alloc(h * 4)
+    d_out = gpu_ctx.alloc(h * DK * 4)
+    worst = 0.0
+    for step in range(4):
+        qkv = oracle_lib.normal(seed, 1000 + step, ch)
+        br = oracle_lib.normal(seed, 2000 + step, h)
+        ar = oracle_lib.normal(seed, 3000 + step, h)
+        d_qkv.upload(qkv)
+        d_b.upload(br)
+        d_al.upload(ar)
+        gpu_ctx.call("deltanet_step", 1, h, d_qkv, d_b, d_al, d_cw, d_a, d_dt, d_cs, d_S, d_out)
+        ref = oracle_lib.deltanet_core(qkv, br, ar, conv_w, ssm_a, dt_bias, o_cs, o_S, h, DK)
+        worst = max(worst, max(rel_errs(d_out.download(np.float32, h * DK), ref)))
+    l2, mx = rel_errs(d_S.download(np.float32, h * DK * DK), o_S)
+    print(f"260 heads: S rel_l2={l2:.2e} rel_max={mx:.2e}; outputs worst {worst:.2e}", flush=True)
+    assert l2 <= 1e-3 and mx <= 1e-3 and worst <= 1e-3
+    assert np.array_equal(d_cs.download(np.float32, ch * 4), o_cs)
+    for buf in (d_S, d_cs, d_cw, d_a, d_dt, d_qkv, d_b, d_al, d_out):
+        buf.free()
+
+
 def test_deltanet_exact_recall_on_gpu(gpu_ctx, oracle_lib):
     """decay = 1 (ssm_a = 0), beta = 1 (beta_raw = 40): after one step S^T k = v."""
     conv_w = np.zeros((CH, 4), np.float32)
