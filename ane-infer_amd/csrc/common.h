@@ -256,15 +256,49 @@ inline size_t xe_bytes(size_t n) { return 32 * (size_t)xe_stride((int)n); }
 struct Planes {
     _Float16 *hi = nullptr, *lo = nullptr;
     int8_t *xe = nullptr;
+    // Deferred RMSNorm scale: when rs is set the planes hold r (.) w and the
+    // GEMM multiplies batch row b's sums by 1 / sqrt(t / n + rs_eps), t the
+    // row's rs_parts sums of squares rs[b * rs_parts + k] added in k order
+    // (n = the GEMM's column count).  Only the x-stationary GEMM of 17..32
+    // rows (gemm_xsh) applies it, and the launchers of the others refuse it;
+    // kernels that write planes ignore it.
+    float *rs = nullptr;
+    int rs_parts = 0;
+    float rs_eps = 0.0f;
     // the planes of rows 32 g .. 32 g + 31 for an n-column input
     __host__ __device__ Planes group(int g, int n) const {
         Planes p;
         p.hi = hi ? hi + (size_t)g * xf_plane_len((size_t)n) : nullptr;
         p.lo = lo ? lo + (size_t)g * xf_plane_len((size_t)n) : nullptr;
         p.xe = xe ? xe + (size_t)g * 32 * xe_stride(n) : nullptr;
+        p.rs = rs ? rs + (size_t)g * 32 * rs_parts : nullptr;
+        p.rs_parts = rs_parts;
+        p.rs_eps = rs_eps;
+        return p;
+    }
+    Planes without_scale() const {
+        Planes p = *this;
+        p.rs = nullptr;
+        p.rs_parts = 0;
         return p;
     }
 };
+// 1 / sqrt(mean square + eps) of batch row b from its deferred-norm sums
+// (the same additions, in the same order, as the full-row norm kernels).
+// In two steps, so that the loads can be issued early and the arithmetic
+// done later: rs_load (branch-free, rs_parts in 1..kMaxRsParts), rs_finish.
+constexpr int kMaxRsParts = 8;
+__device__ __forceinline__ void rs_load(const Planes &xp, int b, float (&v)[kMaxRsParts]) {
+    const float *p = xp.rs + (size_t)b * xp.rs_parts;
+#pragma unroll
+    for (int k = 0; k < kMaxRsParts; k++) v[k] = p[min(k, xp.rs_parts - 1)];
+}
+__device__ __forceinline__ float rs_finish(const Planes &xp, const float (&v)[kMaxRsParts], int n) {
+    float t = v[0];
+#pragma unroll
+    for (int k = 1; k < kMaxRsParts; k++) t = k < xp.rs_parts ? t + v[k] : t;
+    return 1.0f / sqrtf(t / (float)n + xp.rs_eps);
+}
 __host__ __device__ __forceinline__ int xe_index(int b, int c, int n) { return b * xe_stride(n) + c / kXeGroup; }
 // Group exponent from the group's largest |x|.
 __device__ __forceinline__ int group_exp(float amax) {
@@ -387,6 +421,9 @@ int launch_gemm_rows(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, co
 // planes needed): launch_gemm_xs_rows writes out[ks][b][r] for its
 // gemm_packed_ksplit splits.
 bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
+// Whether launch_gemm_packed of this shape applies a deferred norm scale
+// (Planes::rs): the 17..32-row x-stationary kernel, n <= 256 kMaxRsParts.
+bool gemm_takes_norm_scale(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch);
 // The FFN gate / up product (interleaved [gate; up] panel matrix, m = 2 F)
 // with the SiLU-mul fused: h[b][f] as fp32 rows [batch][F], one launch, no
 // partial sums; covered at batch 17..32 for K = 512, 1024 or 2048.
@@ -506,6 +543,10 @@ int launch_embed_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, const 
                          const Planes &xp = Planes{});
 int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
                             int ksplit, const float *w, float *xn, float eps, const Planes &xp = Planes{});
+// x += sum of the ksplit slices; planes of x (.) w with the norm's scale
+// deferred to the consumer (xp.rs: n / 256 sums of squares per row).
+int launch_residual_rmsnorm_parts(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
+                                  int ksplit, const float *w, const Planes &xp);
 // gu: the ksplit partial slices [rows][2F] of a product over the interleaved
 // [gate; up] panel matrix (feature f's gate sum at gu_index(f), up + 32).
 int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit,

@@ -94,6 +94,9 @@ struct Model {
     // pending state updates (kDnPendFloats each, in layer order), committed
     // by one apply launch at the end of the step; null otherwise
     float *dn_pend = nullptr;
+    // batch > 1: the residual norms' per-row sums of squares when their
+    // scale is left to the consuming GEMM (Planes::rs), [32][kMaxRsParts]
+    float *norm_ss = nullptr;
     float *xin = nullptr;        // GEMM input planes (batch > 1): hi then lo, xin_len halves each,
                                  // then the group exponents (xe_cnt bytes)
     size_t xin_len = 0;          // fragment-order plane of the widest GEMM input (32 rows)
@@ -164,7 +167,8 @@ void free_state(Model *M) {
         L.kc = L.vc = nullptr;
     }
     void *bufs[] = {M->d_pos, M->d_tokens, M->d_sampled, M->d_hist,    M->x0,        M->x1,  M->pmix,   M->p0,
-                    M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->xin, M->dn_pend};
+                    M->p1,    M->heads,    M->attn_out,  M->logits, M->attn_part, M->argmax_ws, M->xin, M->dn_pend,
+                    M->norm_ss};
     for (void *p : bufs) free_ptr(p);
     void *pfb[] = {M->pf.x, M->pf.xn, M->pf.pmix, M->pf.p0, M->pf.p1, M->pf.attn_part, M->pf.logits, M->pf.xin,
                    M->pf.d_tokens, M->pf.d_pos};
@@ -178,6 +182,7 @@ void free_state(Model *M) {
     M->x0 = M->x1 = M->pmix = M->p0 = M->p1 = M->heads = M->attn_out = M->logits = M->attn_part = nullptr;
     M->xin = nullptr;
     M->dn_pend = nullptr;
+    M->norm_ss = nullptr;
     M->argmax_ws = nullptr;
     M->batch = M->max_seq = 0;
     M->host_pos.clear();
@@ -467,15 +472,27 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
     const uint32_t qd = D.n_heads * D.head_dim;
     const float eps = D.rms_norm_eps;
     const Planes xp = M->planes();  // GEMM input planes
+    // The residual norms whose consumer is the 17..32-row x-stationary GEMM
+    // write r (.) w planes and leave the scale to it (Planes::rs): one wave
+    // per 256 columns of a row, so that a row's partial slices are read by
+    // 8 CUs instead of one.  Measured on MI355X, batch 32, ctx 1k, the same
+    // box: 1.592-1.597 ms per step against 1.636-1.638 with the full-row
+    // norm kernel (the deferred scale costs the gate / up product a little).
+    Planes xs = xp;
+    xs.rs = M->norm_ss;
+    xs.rs_parts = (int)(d / 256);
+    xs.rs_eps = eps;
+    const bool parts_ok = M->norm_ss && d % 256 == 0 && d / 256 <= (uint32_t)kMaxRsParts;
     float *x = M->x0;
     TRY(launch_embed_rmsnorm(ctx, s, B, (int)d, M->d_tokens, M->embedding, D.vocab_size, x, M->layers[0].attn_norm,
                              nullptr, eps, xp));
+    bool in_scaled = false;  // the planes of the next mixer input carry a deferred scale
     for (uint32_t l = 0; l < D.n_layers; l++) {
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;
         const uint32_t rows_in = dn ? M->rows_dn : M->rows_attn;
         const int k1 = gemm_packed_ksplit(ctx, rows_in, d, B);
-        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, xp, B, M->pmix, k1));
+        TRY(launch_gemm_packed(ctx, s, L.mix_in.type, L.mix_in.p, rows_in, d, in_scaled ? xs : xp, B, M->pmix, k1));
         MixIn mix;
         mix.p = M->pmix;
         mix.kp = k1;
@@ -494,28 +511,42 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
         }
         const int k3 = gemm_packed_ksplit(ctx, d, cols3, B);
         TRY(launch_gemm_packed(ctx, s, L.mix_out.type, L.mix_out.p, d, cols3, xp, B, M->p0, k3));
-        TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, nullptr, eps, xp));
         const int k5 = gemm_packed_ksplit(ctx, d, F, B);
-        if (gemm_gate_up_silu_ok(ctx, 2 * F, d, B) && gemm_is_xs(ctx, d, F, B)) {
+        const bool silu_fused = gemm_gate_up_silu_ok(ctx, 2 * F, d, B) && gemm_is_xs(ctx, d, F, B);
+        const bool ffn_scaled = parts_ok && (silu_fused || gemm_takes_norm_scale(ctx, 2 * F, d, B));
+        if (ffn_scaled)
+            TRY(launch_residual_rmsnorm_parts(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, xs));
+        else
+            TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k3, L.post_attn_norm, nullptr, eps, xp));
+        const Planes &xf = ffn_scaled ? xs : xp;
+        if (silu_fused) {
             // the SiLU-mul in the gate / up product's epilogue (h as fp32
             // rows in p1), the down product splitting those rows itself:
             // one launch less per layer
-            TRY(launch_gemm_gate_up_silu(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, B, M->p1));
+            TRY(launch_gemm_gate_up_silu(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xf, B, M->p1));
             TRY(launch_gemm_xs_rows(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, M->p1, B, M->p0));
         } else {
             const int k4 = gemm_packed_ksplit(ctx, 2 * F, d, B);
-            TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xp, B, M->p1, k4));
+            TRY(launch_gemm_packed(ctx, s, L.ffn_gu.type, L.ffn_gu.p, 2 * F, d, xf, B, M->p1, k4));
             TRY(launch_silu_mul_stacked(ctx, s, B, (int)F, M->p1, k4, nullptr, xp));
             TRY(launch_gemm_packed(ctx, s, L.ffn_down.type, L.ffn_down.p, d, F, xp, B, M->p0, k5));
         }
-        const float *next_norm = l + 1 < D.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
-        TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k5, next_norm, nullptr, eps, xp));
+        const bool last = l + 1 == D.n_layers;
+        const float *next_norm = last ? M->final_norm : M->layers[l + 1].attn_norm;
+        const uint32_t next_rows = last ? D.vocab_size
+                                        : M->layers[l + 1].type == ANEHIP_LAYER_DELTANET ? M->rows_dn : M->rows_attn;
+        in_scaled = parts_ok && gemm_takes_norm_scale(ctx, next_rows, d, B);
+        if (in_scaled)
+            TRY(launch_residual_rmsnorm_parts(ctx, s, B, (int)d, x, M->p0, k5, next_norm, xs));
+        else
+            TRY(launch_residual_rmsnorm(ctx, s, B, (int)d, x, M->p0, k5, next_norm, nullptr, eps, xp));
     }
     const int kf = gemm_packed_ksplit(ctx, D.vocab_size, d, B);
+    const Planes &xl = in_scaled ? xs : xp;
     if (kf == 1) {
-        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xp, B, M->logits, 1));
+        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xl, B, M->logits, 1));
     } else {
-        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xp, B, M->pmix, kf));
+        TRY(launch_gemm_packed(ctx, s, M->lm_head.type, M->lm_head.p, D.vocab_size, d, xl, B, M->pmix, kf));
         TRY(launch_sum_partials(ctx, s, M->pmix, M->logits, (size_t)B * D.vocab_size, kf));
     }
     return ANEHIP_OK;
@@ -1023,6 +1054,7 @@ int anehip_alloc_state(anehip_ctx *ctx, uint32_t batch, uint32_t max_seq) {
     r = r ? r : alloc((void **)&M->xin, M->planes_bytes());
     r = r ? r : alloc((void **)&M->logits, batch * (size_t)D.vocab_size * sizeof(float));
     r = r ? r : alloc(&M->argmax_ws, argmax_workspace_bytes((int)batch));
+    if (batch > 1) r = r ? r : alloc((void **)&M->norm_ss, 32 * kMaxRsParts * sizeof(float));
     if (M->rows_attn) {
         const int G = (int)(D.n_heads / D.n_kv_heads);
         r = r ? r : alloc((void **)&M->attn_part, attn_partial_floats((int)batch, (int)D.n_kv_heads, (int)max_seq, G) * sizeof(float));

@@ -170,6 +170,52 @@ __global__ __launch_bounds__(512) void residual_rmsnorm_v4(float *__restrict__ x
     }
 }
 
+// The same residual add for a consumer that applies the RMSNorm's scale
+// itself (Planes::rs, gemm_xsh): one wave per 256-column slice (grid n / 256
+// x rows), so a row's partial slices are read by n / 256 CUs instead of one.
+// The planes get r (.) w with each 128-column group's exponent from its own
+// largest |r w|, and rs[b * (n / 256) + s] slice s's sum of squares -- the
+// wave sums of residual_rmsnorm_v4, which its consumer adds in slice order
+// as that kernel does; the scale (r * inv_rms) * w of main.rs:1106-1113 is
+// then applied to the consumer's sums (reassociated).
+template <int KP>
+__global__ __launch_bounds__(64) void residual_rmsnorm_parts(float *__restrict__ x, const float *__restrict__ part,
+                                                             int ksplit, int rows, const float *__restrict__ w,
+                                                             int n, Planes xp) {
+    const int t = threadIdx.x, sl = blockIdx.x;
+    const size_t b = blockIdx.y;
+    const int n4 = n >> 2, e4 = sl * 64 + t;
+    float4 *x4 = reinterpret_cast<float4 *>(x) + b * n4;
+    const float4 *p4 = reinterpret_cast<const float4 *>(part) + b * n4;
+    const size_t split4 = (size_t)rows * n4;
+    float4 r = x4[e4];
+    float4 pv[KP];
+#pragma unroll
+    for (int k = 0; k < KP; k++) pv[k] = p4[(size_t)min(k, ksplit - 1) * split4 + e4];
+    const float4 wv = reinterpret_cast<const float4 *>(w)[e4];
+    float4 s = pv[0];
+#pragma unroll
+    for (int k = 1; k < KP; k++) {
+        const bool on = k < ksplit;
+        s.x += on ? pv[k].x : 0.0f;
+        s.y += on ? pv[k].y : 0.0f;
+        s.z += on ? pv[k].z : 0.0f;
+        s.w += on ? pv[k].w : 0.0f;
+    }
+    r = make_float4(r.x + s.x, r.y + s.y, r.z + s.z, r.w + s.w);
+    x4[e4] = r;
+    const float ss = wave_sum(r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w);
+    const float v[4] = {r.x * wv.x, r.y * wv.y, r.z * wv.z, r.w * wv.w};
+    const int e = group_exp(half_max32(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])))));
+    h4v vh, vl;
+    split4_scaled(v, e, vh, vl);
+    const size_t o = xf_index((int)b, 4 * e4, n);
+    *reinterpret_cast<h4v *>(xp.hi + o) = vh;
+    *reinterpret_cast<h4v *>(xp.lo + o) = vl;
+    if ((t & 31) == 0) xp.xe[xe_index((int)b, 4 * e4, n)] = (int8_t)e;
+    if (t == 0) xp.rs[b * (size_t)xp.rs_parts + sl] = ss;
+}
+
 // Output of the GEMM over the interleaved [gate; up] panel matrix,
 // gu[k][b][2F] with feature r's gate sum at gu_index(r) and its up sum 32
 // positions on: h[b][r] = SiLU(gate) * up (scratch.rs:181-186: a = (a / (1 +
@@ -428,6 +474,23 @@ int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, flo
         hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, part, ksplit, rows, w, xn,
                            n, eps, xp);
     }
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_residual_rmsnorm_parts(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
+                                  int ksplit, const float *w, const Planes &xp) {
+    if (int rc = check_planes(ctx, xp, n)) return rc;
+    if (!xp.hi || !xp.rs || !w || n % 256 || xp.rs_parts != n / 256 || xp.rs_parts > kMaxRsParts || ksplit < 1 ||
+        ksplit > 16)
+        return set_error(ctx->err, ANEHIP_EINVAL,
+                         "residual_rmsnorm_parts: n=%d (multiple of 256), %d norm parts, K split %d (1..16)", n,
+                         xp.rs_parts, ksplit);
+    const dim3 grid(n / 256, rows);
+    if (ksplit <= 8)
+        hipLaunchKernelGGL(residual_rmsnorm_parts<8>, grid, dim3(64), 0, s, x, part, ksplit, rows, w, n, xp);
+    else
+        hipLaunchKernelGGL(residual_rmsnorm_parts<16>, grid, dim3(64), 0, s, x, part, ksplit, rows, w, n, xp);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

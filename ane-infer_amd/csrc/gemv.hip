@@ -2246,7 +2246,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_
 // interleaved [gate; up] panel matrix, m = 2 F) the tile's 32 gate sums meet
 // their 32 up sums in the epilogue, which writes h[b][f] = SiLU(gate) * up
 // (scratch.rs:181-186) as fp32 rows [batch][F] instead of the sums.
-template <uint32_t T, int PW, int D, int H, bool XROWS = false, bool SILU = false>
+template <uint32_t T, int PW, int D, int H, bool XROWS = false, bool SILU = false, bool RS = false>
 __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_per_eu(2))) void gemm_xsh(
     const uint8_t *__restrict__ Wp, Planes xp, const float *__restrict__ xrows, float *__restrict__ out, int m, int n,
     int batch, int ksplit, size_t split_stride) {
@@ -2305,6 +2305,11 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
 #pragma unroll
             for (int st = 0; st < 4; st++) load8(xr + xcol(p, st), xv[p][st]);
     }
+    // RS: the norm sums of this thread's epilogue batch row, loaded with x
+    // (ahead of the weight ring) and turned into its scale once E is known
+    static_assert(!RS || !XROWS, "the deferred norm scale comes with planes");
+    float rsv[RS ? kMaxRsParts : 1];
+    if constexpr (RS) rs_load(xp, min((int)(threadIdx.x >> 4), batch - 1), rsv);
     const uint8_t *wpart = Wp + (size_t)panel0 * Panel<T>::kBytes;
     int lt = g0, lp = 0;  // load cursor: tile, panel of the wave's part
     auto load_next = [&](WUnit<T> &u) {
@@ -2365,6 +2370,12 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
             for (int st = 0; st < 4; st++) split8_scaled(xv[p][st], E, xa[p][st], xb[p][st]);
     }
     if (lane < 32) ew[wave][lane] = E;  // lane l holds batch row l (read after the tile's barrier)
+    float rsc = 1.0f;
+    if constexpr (RS) {
+#pragma unroll
+        for (int k = 0; k < kMaxRsParts; k++) asm volatile("" : "+v"(rsv[k]));
+        rsc = rs_finish(xp, rsv, n);
+    }
     static_assert(512 / (kWave * NW) == 1, "one output vector per thread");
     int ct = g0;  // tile being multiplied
     f32x16 acc0 = {}, acc1 = {};
@@ -2402,6 +2413,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves *H) __attribute__((amdgpu_waves_p
                         const float4 o = mul4(*reinterpret_cast<const float4 *>(&red[w][r][l]), xe_scale(ew[w][b]));
                         sum = make_float4(sum.x + o.x, sum.y + o.y, sum.z + o.z, sum.w + o.w);
                     }
+                    if constexpr (RS) sum = mul4(sum, rsc);
                     if constexpr (SILU) {
                         // rows 4 j .. + 3 (j < 8): the gate sums of features
                         // 32 ct + 4 j .. + 3; their up sums are rows 32 + 4 j
@@ -3435,6 +3447,7 @@ void launch_gemm_xs_any(anehip_ctx *ctx, hipStream_t stream, GemmKernel kind, co
 #define ANEHIP_XSH(PW, D)                                                                                          \
     do {                                                                                                           \
         if (xrows) ANEHIP_XS((gemm_xsh<T, PW, D, 2, true>), 512);                                                  \
+        else if (xp.rs) ANEHIP_XS((gemm_xsh<T, PW, D, 2, false, false, true>), 512);                               \
         else ANEHIP_XS((gemm_xsh<T, PW, D, 2, false>), 512);                                                       \
     } while (0)
     if (kind == GemmKernel::Xs16) {
@@ -3463,6 +3476,11 @@ void launch_gemm_xs_any(anehip_ctx *ctx, hipStream_t stream, GemmKernel kind, co
 
 bool gemm_is_xs(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch) {
     return gemm_kernel(batch, (int)(n / 256), gemm_packed_ksplit(ctx, m, n, batch)) != GemmKernel::Persistent;
+}
+
+bool gemm_takes_norm_scale(const anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch) {
+    return n % 256 == 0 && n / 256 <= kMaxRsParts &&
+           gemm_kernel(batch, (int)(n / 256), gemm_packed_ksplit(ctx, m, n, batch)) == GemmKernel::Xsh;
 }
 
 static int check_gemm_args(anehip_ctx *ctx, uint32_t m, uint32_t n, uint32_t batch, int ksplit, size_t ss) {
@@ -3512,13 +3530,21 @@ int launch_gemm_gate_up_silu(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_
                              uint32_t n, const Planes &xp, uint32_t batch, float *h) {
     if (!gemm_gate_up_silu_ok(ctx, m, n, batch))
         return set_error(ctx->err, ANEHIP_EINVAL, "gemm_gate_up_silu: %u x %u at batch %u not covered", m, n, batch);
+    if (xp.rs && (xp.rs_parts < 1 || xp.rs_parts > kMaxRsParts))
+        return set_error(ctx->err, ANEHIP_EINVAL, "gemm_gate_up_silu: %d norm parts", xp.rs_parts);
     const int tiles = (int)(m / kWave), cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     const dim3 grid(max(1, min(tiles, cus)));
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     const size_t ss = (size_t)batch * (m / 2);
 #define ANEHIP_GUS(TT, PW, D)                                                                                     \
-    hipLaunchKernelGGL((gemm_xsh<TT, PW, D, 2, false, true>), grid, dim3(512), 0, stream, w, xp, nullptr, h,    \
-                       (int)m, (int)n, (int)batch, 1, ss)
+    do {                                                                                                          \
+        if (xp.rs)                                                                                                \
+            hipLaunchKernelGGL((gemm_xsh<TT, PW, D, 2, false, true, true>), grid, dim3(512), 0, stream, w, xp,    \
+                               nullptr, h, (int)m, (int)n, (int)batch, 1, ss);                                    \
+        else                                                                                                      \
+            hipLaunchKernelGGL((gemm_xsh<TT, PW, D, 2, false, true>), grid, dim3(512), 0, stream, w, xp, nullptr, \
+                               h, (int)m, (int)n, (int)batch, 1, ss);                                             \
+    } while (0)
     const int nsb = (int)(n / 256);
     if (ggml_type == ANEHIP_GGML_Q8_0) {
         if (nsb == 2) ANEHIP_GUS(ANEHIP_GGML_Q8_0, 1, 1);
@@ -3542,6 +3568,9 @@ int launch_gemm_packed(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, 
     const int per = split_len((int)(n / 256), ksplit);
     const uint8_t *w = static_cast<const uint8_t *>(wp);
     const GemmKernel kind = gemm_kernel(batch, (int)(n / 256), ksplit);
+    if (xp.rs && (kind != GemmKernel::Xsh || xp.rs_parts < 1 || xp.rs_parts > kMaxRsParts))
+        return set_error(ctx->err, ANEHIP_EINVAL,
+                         "gemm: a deferred norm scale (%d parts) needs the 17..32-row x-stationary kernel", xp.rs_parts);
     const bool q8 = ggml_type == ANEHIP_GGML_Q8_0;
     if (kind != GemmKernel::Persistent && q8)
         launch_gemm_xs_any<ANEHIP_GGML_Q8_0>(ctx, stream, kind, w, m, n, xp, nullptr, batch, out, ksplit, ss);
