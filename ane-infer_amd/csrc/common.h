@@ -547,6 +547,9 @@ int launch_residual_rmsnorm(anehip_ctx *ctx, hipStream_t s, int rows, int n, flo
 // deferred to the consumer (xp.rs: n / 256 sums of squares per row).
 int launch_residual_rmsnorm_parts(anehip_ctx *ctx, hipStream_t s, int rows, int n, float *x, const float *part,
                                   int ksplit, const float *w, const Planes &xp);
+// x = embedding rows of the tokens; planes of x (.) w, the scale deferred as above.
+int launch_embed_rmsnorm_parts(anehip_ctx *ctx, hipStream_t s, int rows, int n, const uint32_t *tokens,
+                               const float *emb, uint32_t vocab, float *x, const float *w, const Planes &xp);
 // gu: the ksplit partial slices [rows][2F] of a product over the interleaved
 // [gate; up] panel matrix (feature f's gate sum at gu_index(f), up + 32).
 int launch_silu_mul_stacked(anehip_ctx *ctx, hipStream_t s, int rows, int F, const float *gu, int ksplit,

@@ -484,9 +484,16 @@ int enqueue_step_bn(anehip_ctx *ctx, Model *M, hipStream_t s) {
     xs.rs_eps = eps;
     const bool parts_ok = M->norm_ss && d % 256 == 0 && d / 256 <= (uint32_t)kMaxRsParts;
     float *x = M->x0;
-    TRY(launch_embed_rmsnorm(ctx, s, B, (int)d, M->d_tokens, M->embedding, D.vocab_size, x, M->layers[0].attn_norm,
-                             nullptr, eps, xp));
-    bool in_scaled = false;  // the planes of the next mixer input carry a deferred scale
+    // the planes of the next mixer input carry a deferred scale
+    bool in_scaled = parts_ok && gemm_takes_norm_scale(ctx, M->layers[0].type == ANEHIP_LAYER_DELTANET ? M->rows_dn
+                                                                                                       : M->rows_attn,
+                                                       d, B);
+    if (in_scaled)
+        TRY(launch_embed_rmsnorm_parts(ctx, s, B, (int)d, M->d_tokens, M->embedding, D.vocab_size, x,
+                                       M->layers[0].attn_norm, xs));
+    else
+        TRY(launch_embed_rmsnorm(ctx, s, B, (int)d, M->d_tokens, M->embedding, D.vocab_size, x,
+                                 M->layers[0].attn_norm, nullptr, eps, xp));
     for (uint32_t l = 0; l < D.n_layers; l++) {
         Layer &L = M->layers[l];
         const bool dn = L.type == ANEHIP_LAYER_DELTANET;

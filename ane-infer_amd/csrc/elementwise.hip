@@ -216,6 +216,33 @@ __global__ __launch_bounds__(64) void residual_rmsnorm_parts(float *__restrict__
     if (t == 0) xp.rs[b * (size_t)xp.rs_parts + sl] = ss;
 }
 
+// The embedding gather of embed_rmsnorm_kernel in the same form (grid n /
+// 256 x rows, one wave per slice): x[b] = embedding[token[b]] (zeros if
+// token >= vocab), the planes of x (.) w and the slices' sums of squares.
+__global__ __launch_bounds__(64) void embed_rmsnorm_parts(const uint32_t *__restrict__ tokens,
+                                                          const float *__restrict__ emb, uint32_t vocab,
+                                                          float *__restrict__ x, const float *__restrict__ w, int n,
+                                                          Planes xp) {
+    const int t = threadIdx.x, sl = blockIdx.x;
+    const size_t b = blockIdx.y;
+    const int n4 = n >> 2, e4 = sl * 64 + t;
+    const uint32_t tok = tokens[b];
+    const float4 wv = reinterpret_cast<const float4 *>(w)[e4];
+    const float4 r = tok < vocab ? reinterpret_cast<const float4 *>(emb + (size_t)tok * n)[e4]
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    reinterpret_cast<float4 *>(x)[b * n4 + e4] = r;
+    const float ss = wave_sum(r.x * r.x + r.y * r.y + r.z * r.z + r.w * r.w);
+    const float v[4] = {r.x * wv.x, r.y * wv.y, r.z * wv.z, r.w * wv.w};
+    const int e = group_exp(half_max32(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])))));
+    h4v vh, vl;
+    split4_scaled(v, e, vh, vl);
+    const size_t o = xf_index((int)b, 4 * e4, n);
+    *reinterpret_cast<h4v *>(xp.hi + o) = vh;
+    *reinterpret_cast<h4v *>(xp.lo + o) = vl;
+    if ((t & 31) == 0) xp.xe[xe_index((int)b, 4 * e4, n)] = (int8_t)e;
+    if (t == 0) xp.rs[b * (size_t)xp.rs_parts + sl] = ss;
+}
+
 // Output of the GEMM over the interleaved [gate; up] panel matrix,
 // gu[k][b][2F] with feature r's gate sum at gu_index(r) and its up sum 32
 // positions on: h[b][r] = SiLU(gate) * up (scratch.rs:181-186: a = (a / (1 +
@@ -491,6 +518,17 @@ int launch_residual_rmsnorm_parts(anehip_ctx *ctx, hipStream_t s, int rows, int 
         hipLaunchKernelGGL(residual_rmsnorm_parts<8>, grid, dim3(64), 0, s, x, part, ksplit, rows, w, n, xp);
     else
         hipLaunchKernelGGL(residual_rmsnorm_parts<16>, grid, dim3(64), 0, s, x, part, ksplit, rows, w, n, xp);
+    ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+    return ANEHIP_OK;
+}
+
+int launch_embed_rmsnorm_parts(anehip_ctx *ctx, hipStream_t s, int rows, int n, const uint32_t *tokens,
+                               const float *emb, uint32_t vocab, float *x, const float *w, const Planes &xp) {
+    if (int rc = check_planes(ctx, xp, n)) return rc;
+    if (!xp.hi || !xp.rs || !w || n % 256 || xp.rs_parts != n / 256 || xp.rs_parts > kMaxRsParts)
+        return set_error(ctx->err, ANEHIP_EINVAL, "embed_rmsnorm_parts: n=%d (multiple of 256), %d norm parts", n,
+                         xp.rs_parts);
+    hipLaunchKernelGGL(embed_rmsnorm_parts, dim3(n / 256, rows), dim3(64), 0, s, tokens, emb, vocab, x, w, n, xp);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
     return ANEHIP_OK;
 }

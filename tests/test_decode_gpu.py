@@ -249,6 +249,27 @@ def test_token_beyond_vocab_uses_zero_embedding(small_host):
     gm.close()
 
 
+def test_token_beyond_vocab_batch32(mid_host):
+    """The same at batch 32 on the mid-size model, where the embedding gather
+    runs one wave per 256-column slice and leaves the RMSNorm scale to the
+    first projection: every sequence over 2 steps, tokens past the
+    vocabulary in a few of them."""
+    B = 32
+    V = mid_host.spec.vocab_size
+    gm = _model(mid_host, B, 8)
+    seqs = [mid_host.seq(8) for _ in range(B)]
+    for step in range(2):
+        toks = oracle.randint(77, step, B, V)
+        toks[3 + step] = V + 5
+        toks[31] = V + 1000 * step
+        g = gm.step(toks)
+        for b in range(B):
+            assert max(rel_errs(g[b], seqs[b].forward(int(toks[b])))) <= TOL, (step, b)
+    gm.close()
+    for q in seqs:
+        q.close()
+
+
 def test_generate_feeds_back_on_device(small_host):
     gm = _model(small_host, 2, 40)
     out = gm.generate([1, 2], 12)
