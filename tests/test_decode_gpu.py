@@ -63,11 +63,13 @@ def mid_host():
     return HostModel(anehip.Spec(**MID), seed=5)
 
 
-@pytest.mark.parametrize("B", [2, 7, 32])
+@pytest.mark.parametrize("B", [2, 7, 20, 32])
 def test_mid_model_batched_steps(mid_host, B):
     """Every sequence of a batched step vs the oracle over 4 steps (graph
     replays), on the mid-size model: K-split partial sums of 2 and 4 splits
-    read by the DeltaNet / attention kernels, SiLU-mul and residual RMSNorm."""
+    read by the DeltaNet / attention kernels, SiLU-mul and residual RMSNorm
+    (at 20 and 32 rows sliced per row, the norm's scale applied by the
+    consuming GEMM; batch rows past 20 of its 32-row tiles unused)."""
     steps = 4
     toks = oracle.randint(21, B, steps * B, mid_host.spec.vocab_size).reshape(steps, B)
     gm = _model(mid_host, B, 32)
