@@ -285,6 +285,15 @@ struct Planes {
 };
 // 1 / sqrt(mean square + eps) of batch row b from its deferred-norm sums
 // (the same additions, in the same order, as the full-row norm kernels).
+// Non-temporal 16-byte load / store of 4 floats, for data streamed once per
+// step that the caches cannot keep (the DeltaNet states).
+typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_nt4(const float *p) {
+    return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4 *>(p)));
+}
+__device__ __forceinline__ void st_nt4(float *p, float4 v) {
+    __builtin_nontemporal_store(__builtin_bit_cast(nt_f32x4, v), reinterpret_cast<nt_f32x4 *>(p));
+}
 // In two steps, so that the loads can be issued early and the arithmetic
 // done later: rs_load (branch-free, rs_parts in 1..kMaxRsParts), rs_finish.
 constexpr int kMaxRsParts = 8;
