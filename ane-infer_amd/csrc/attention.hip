@@ -71,12 +71,15 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWord3 = 0x00020000;  // raw buffer resource word 3 (gfx9 family)
 constexpr float kPScale = 16384.0f;  // 2^14: probabilities in the PV MFMA operands
-// Cache-policy bit nt of the K / V cache loads: each cached row is read once
-// per step and the caches of a batch exceed the L2s and the MALL.  Measured
-// on MI355X (caches rotated past the MALL): batch 32 ctx 1k / 8k / 32k 19.1 /
-// 94-98 / 364-369 -> 17.1 / 82.3 / 307.3 us, batch 1 ctx 32k 18.6 -> 17.4,
-// batch 1 ctx 1k 6.8 -> 7.0.
+// Cache-policy bit nt of the K / V cache loads, for launches whose caches
+// (capacity) reach kNtKvBytes: each cached row is read once per step and the
+// caches of a batch exceed the L2s and the MALL.  Measured on MI355X (caches
+// rotated past the MALL): batch 32 ctx 1k / 8k / 32k 19.1 / 94-98 / 364-369
+// -> 17.1 / 82.3 / 307.3 us, batch 1 ctx 32k 18.6 -> 17.4, batch 1 ctx 1k
+// 6.8 -> 7.0; batch-1 decode ctx 1k / 8k / 32k with the bit on every launch
+// 1248 / 1241 / 1166 tok/s against 1254 / 1245 / 1130 with it on none.
 constexpr int kCpolNt = 2;
+constexpr size_t kNtKvBytes = (size_t)32 << 20;
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -119,7 +122,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // (decode: every row its own sequence; prefill: row_stride 0, every row a
 // token of one sequence whose K / V rows the prefill append kernel wrote
 // before this launch -- then `append` is false and no row is written here).
-template <int G>
+template <int G, bool NT>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
     MixIn mix, const float *__restrict__ q_norm, const float *__restrict__ k_norm,
     const float *__restrict__ inv_freq, const uint32_t *__restrict__ pos_arr, __half *__restrict__ k_cache,
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
 #pragma unroll
         for (int s = 0; s < 8; s++) {
             const int off = ((row0 + 16 * wave + li) * kHd + 32 * s + 8 * lg) * 2;
-            kr[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, kCpolNt));
+            kr[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, NT ? kCpolNt : 0));
         }
     };
     // V rows row0 + 16 wave + 4 lg + r, dims 64 q + 4 li .. + 3 in vr[4 q + r]
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int off = ((row0 + 16 * wave + 4 * lg + r) * kHd + 64 * q + 4 * li) * 2;
-                vr[4 * q + r] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, off, 0, kCpolNt));
+                vr[4 * q + r] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, off, 0, NT ? kCpolNt : 0));
             }
     };
     auto row_of = [&](int ti) { return ti < te ? ti * kCh : kFar; };
@@ -547,11 +550,18 @@ int attention_impl(anehip_ctx *ctx, hipStream_t stream, int batch, int n_heads, 
     float *part_o = part;
     float *part_ml = part + (size_t)batch * n_kv * nch * G * kHd;
     dim3 g1(nch, n_kv, batch), g2(n_heads, batch);
+    // the caches this launch can read (prefill rows share one sequence's)
+    const bool nt = (size_t)(row_stride ? batch : 1) * n_kv * max_seq * 2 * kHd * sizeof(__half) >= kNtKvBytes;
 #define ANEHIP_ATTN_CASE(GG)                                                                                   \
     case GG:                                                                                                   \
-        hipLaunchKernelGGL(attn_partial_kernel<GG>, g1, dim3(kThreads), 0, stream, mix, q_norm, k_norm,        \
-                           inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, part_o, part_ml,          \
-                           cache_off, row_stride, append);                                                    \
+        if (nt)                                                                                                \
+            hipLaunchKernelGGL((attn_partial_kernel<GG, true>), g1, dim3(kThreads), 0, stream, mix, q_norm,    \
+                               k_norm, inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, part_o,       \
+                               part_ml, cache_off, row_stride, append);                                       \
+        else                                                                                                   \
+            hipLaunchKernelGGL((attn_partial_kernel<GG, false>), g1, dim3(kThreads), 0, stream, mix, q_norm,   \
+                               k_norm, inv_freq, pos, k_cache, v_cache, max_seq, n_heads, n_kv, part_o,       \
+                               part_ml, cache_off, row_stride, append);                                       \
         ANEHIP_HIP_TRY(ctx->err, hipGetLastError());                                                           \
         if (!out && !xp.hi) return ANEHIP_OK; /* partials only */                                              \
         hipLaunchKernelGGL(attn_combine_kernel<GG>, g2, dim3(kThreads), 0, stream, mix, pos, part_o, part_ml,  \
