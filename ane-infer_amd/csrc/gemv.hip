@@ -3201,6 +3201,28 @@ __global__ __launch_bounds__(256) void sum_partials(const float *__restrict__ pa
     for (int k = 1; k < ksplit; k++) s += part[(size_t)k * count + i];
     y[i] = s;
 }
+// The same, 4 consecutive values per thread (count % 4 == 0) with every slice
+// loaded before the first add (slices past ksplit re-read the last one and are
+// not added), so a thread waits for one round trip instead of ksplit.
+template <int KP>
+__global__ __launch_bounds__(256) void sum_partials4(const float4 *__restrict__ part, float4 *__restrict__ y,
+                                                     size_t count4, int ksplit) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= count4) return;
+    float4 v[KP];
+#pragma unroll
+    for (int k = 0; k < KP; k++) v[k] = part[(size_t)min(k, ksplit - 1) * count4 + i];
+    float4 s = v[0];
+#pragma unroll
+    for (int k = 1; k < KP; k++) {
+        const bool on = k < ksplit;
+        s.x = on ? s.x + v[k].x : s.x;
+        s.y = on ? s.y + v[k].y : s.y;
+        s.z = on ? s.z + v[k].z : s.z;
+        s.w = on ? s.w + v[k].w : s.w;
+    }
+    y[i] = s;
+}
 
 // K splits: the smallest divisor k of the super-block count with at most 8
 // super-blocks per workgroup, and at most one per wave (4) unless the row
@@ -3901,6 +3923,20 @@ int launch_gemm_raw(anehip_ctx *ctx, hipStream_t stream, uint32_t ggml_type, con
 }
 
 int launch_sum_partials(anehip_ctx *ctx, hipStream_t stream, const float *part, float *y, size_t count, int ksplit) {
+    const bool v4 = count % 4 == 0 && ksplit >= 1 && ksplit <= 16 && reinterpret_cast<uintptr_t>(part) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    if (v4) {
+        const size_t c4 = count / 4;
+        const dim3 grid((unsigned)((c4 + 255) / 256));
+        const float4 *p4 = reinterpret_cast<const float4 *>(part);
+        float4 *y4 = reinterpret_cast<float4 *>(y);
+        if (ksplit <= 2) hipLaunchKernelGGL(sum_partials4<2>, grid, dim3(256), 0, stream, p4, y4, c4, ksplit);
+        else if (ksplit <= 4) hipLaunchKernelGGL(sum_partials4<4>, grid, dim3(256), 0, stream, p4, y4, c4, ksplit);
+        else if (ksplit <= 8) hipLaunchKernelGGL(sum_partials4<8>, grid, dim3(256), 0, stream, p4, y4, c4, ksplit);
+        else hipLaunchKernelGGL(sum_partials4<16>, grid, dim3(256), 0, stream, p4, y4, c4, ksplit);
+        ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
+        return ANEHIP_OK;
+    }
     hipLaunchKernelGGL(sum_partials, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, part, y, count,
                        ksplit);
     ANEHIP_HIP_TRY(ctx->err, hipGetLastError());
