@@ -446,18 +446,55 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(MixIn mix, const
     const int len = (int)pos_arr[b] + 1;
     const int nc = active_chunks(len, nch);
     const size_t base = ((size_t)b * n_kv + kvh) * nch;
-    const float4 gate = mix.at4(b, h * 2 * kHd + kHd + 4 * l);  // independent of the partials
-    // maximum over the chunks
+    // the gate's K-split slices (independent of the partials) and this
+    // group's first 4 chunks (g, g + 4, g + 8, g + 12; the only ones at batch
+    // 32) are loaded together, before the maximum is known
+    float4 gq[8];
+    {
+        const float *g0 = mix.p + (size_t)b * mix.stride + h * 2 * kHd + kHd + 4 * l;
+#pragma unroll
+        for (int q = 0; q < 8; q++) gq[q] = *reinterpret_cast<const float4 *>(g0 + (size_t)min(q, mix.kp - 1) * mix.split);
+    }
+    float4 p4[4];
+    float pm[4], pl[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const size_t slot = (base + min(g + 4 * i, nc - 1)) * G + hh;
+        p4[i] = *reinterpret_cast<const float4 *>(part_o + slot * kHd + 4 * l);
+        pm[i] = part_ml[slot * 2];
+        pl[i] = part_ml[slot * 2 + 1];
+    }
+    float4 gate = gq[0];
+#pragma unroll
+    for (int q = 1; q < 8; q++)
+        if (q < mix.kp) gate = make_float4(gate.x + gq[q].x, gate.y + gq[q].y, gate.z + gq[q].z, gate.w + gq[q].w);
+    for (int q = 8; q < mix.kp; q++) {
+        const float4 v = *reinterpret_cast<const float4 *>(mix.p + (size_t)b * mix.stride + h * 2 * kHd + kHd + 4 * l +
+                                                           (size_t)q * mix.split);
+        gate = make_float4(gate.x + v.x, gate.y + v.y, gate.z + v.z, gate.w + v.w);
+    }
+    // maximum over the chunks: each group's (the same in all its lanes), then
+    // over the 4 groups
     float mx = -INFINITY;
-    for (int cc = t; cc < nc; cc += kThreads) mx = fmaxf(mx, part_ml[((base + cc) * G + hh) * 2]);
-    mx = wave_max64(mx);
+#pragma unroll
+    for (int i = 0; i < 4; i++) mx = g + 4 * i < nc ? fmaxf(mx, pm[i]) : mx;
+    for (int c2 = g + 16; c2 < nc; c2 += 4) mx = fmaxf(mx, part_ml[((base + c2) * G + hh) * 2]);
     if (l == 0) red[g] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    // this group's chunks, 4 per trip with their loads issued together
+    // this group's chunks in order: the 4 loaded above, then 4 per trip with
+    // their loads issued together
     float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
     float den = 0.f;
-    int cc = g;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (g + 4 * i < nc) {
+            const float w = expf(pm[i] - M);
+            num = make_float4(num.x + w * p4[i].x, num.y + w * p4[i].y, num.z + w * p4[i].z, num.w + w * p4[i].w);
+            den += w * pl[i];
+        }
+    }
+    int cc = g + 16;
     for (; cc + 12 < nc; cc += 16) {
         float4 o4[4];
         float m4[4], l4[4];
