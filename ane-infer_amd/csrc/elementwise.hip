@@ -417,14 +417,27 @@ __global__ __launch_bounds__(kThreads) void argmax_stage1(const float *__restric
     int32_t k = INT32_MIN;
     uint32_t idx = 0;
     bool any = false;
-    for (uint32_t j = blockIdx.x * kThreads + threadIdx.x; j < n; j += kArgBlocks * kThreads) {
-        int32_t kk = total_key(row[j]);
-        if (!any) {
-            k = kk;
-            idx = j;
-            any = true;
-        } else {
-            arg_better(k, idx, kk, j);
+    // 8 strided values per trip, loaded before any is compared (the order of
+    // the comparisons does not matter: arg_better is a total order on (key,
+    // index)), so a 151936-entry row costs 2 round trips instead of 10
+    constexpr uint32_t kStride = kArgBlocks * kThreads;
+    for (uint32_t j0 = blockIdx.x * kThreads + threadIdx.x; j0 < n; j0 += 8 * kStride) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = row[min(j0 + u * kStride, n - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t j = j0 + u * kStride;
+            if (j < n) {
+                const int32_t kk = total_key(v[u]);
+                if (!any) {
+                    k = kk;
+                    idx = j;
+                    any = true;
+                } else {
+                    arg_better(k, idx, kk, j);
+                }
+            }
         }
     }
     if (!any) {

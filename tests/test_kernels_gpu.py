@@ -245,6 +245,24 @@ def test_argmax_total_cmp(gpu_ctx, oracle_lib):
     assert exp[1] == 151935 and exp[2] == 1234 and exp[3] == n - 1
 
 
+@pytest.mark.parametrize("n", [1000, 131072, 131073])
+def test_argmax_row_lengths(gpu_ctx, oracle_lib, n):
+    """Rows shorter than one strided pass of the 64 x 256 threads (8 values
+    each) and rows ending exactly at, or one past, a pass: the maximum at the
+    last index, a tie with it earlier, and a row whose maximum sits in the
+    second pass's only value."""
+    rows = 3
+    lg = oracle_lib.normal(13, n, rows * n).reshape(rows, n)
+    lg[0, n - 1] = 40.0
+    lg[1, 7] = lg[1, n - 1] = 40.0
+    lg[2, :] = -1.0
+    lg[2, n - 1] = 2.0
+    d_out = gpu_ctx.alloc(rows * 4)
+    gpu_ctx.call("argmax", gpu_ctx.to_device(lg), rows, n, d_out)
+    got = d_out.download(np.uint32, rows)
+    assert list(got) == [oracle_lib.argmax(lg[r]) for r in range(rows)] == [n - 1] * rows
+
+
 # ------------------------------------------------------------ utilities ---
 
 @pytest.mark.parametrize("t", [8, 2])
